@@ -1,0 +1,54 @@
+"""Builds the EXL3 HIP library (ijah_amd/_lib/libijah_exl3.so) for gfx950 with hipcc; no CMake, no JIT cache.
+
+    python -m ijah_amd.build          # or: from ijah_amd.build import build; build()
+"""
+import os
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+SRC = PKG / "csrc"
+OUT = PKG / "_lib"
+LIB = OUT / "libijah_exl3.so"
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ARCH = os.environ.get("IJAH_ARCH", "gfx950")
+
+SOURCES = ["exl3_kernels.hip", "exl3_host.cpp", "capi.cpp", "json.cpp"]
+# -ffp-contract=off: the prepared input must round exactly as the reference's f32 arithmetic (no fused x*suh + y).
+# -packed-fp32-ops off: packed FP32 VALU forms are not used on this pool.
+COMMON = ["-O3", "-std=c++17", "-fPIC", "-ffp-contract=off", "-fvisibility=hidden", "-Wall", "-Wno-unused-function",
+          f"-I{PKG.parent / 'include'}"]
+DEVICE = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+          "-munsafe-fp-atomics"]
+
+
+def _compile(src):
+    obj = OUT / (Path(src).stem + ".o")
+    cmd = [HIPCC, *COMMON, *DEVICE, "-x", "hip", "-c", str(SRC / src), "-o", str(obj)]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc failed on {src}:\n{r.stderr[-6000:]}")
+    return obj, r.stderr
+
+
+def build(verbose=False):
+    """Compiles every source and links the shared library. Returns its path."""
+    OUT.mkdir(exist_ok=True)
+    with ThreadPoolExecutor(max_workers=min(4, os.cpu_count() or 1)) as ex:
+        results = list(ex.map(_compile, SOURCES))
+    objs = [str(o) for o, _ in results]
+    if verbose:
+        for _, err in results:
+            if err.strip():
+                print(err, file=sys.stderr)
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(LIB), *objs]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"link failed:\n{r.stderr[-4000:]}")
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

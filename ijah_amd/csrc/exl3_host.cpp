@@ -1,0 +1,674 @@
+// Hot-path entry points (include/ijah_exl3.h): EXL3 linears and the fused MoE layer, resident in HBM.
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <functional>
+#include <set>
+
+#include "kernels.h"
+#include "pack.h"
+
+using namespace ijah;
+
+namespace {
+
+int had_size(int d) {  // reference tools/convert_trunk_enc.py:59-63
+  for (int n : {128, 64, 32, 16})
+    if (d % n == 0) return n;
+  throw Error(strfmt("no Hadamard size for %d", d));
+}
+float had_scale(int n) { return (float)(1.0 / std::sqrt((double)n)); }
+
+template <typename T>
+T *dev_alloc(size_t count) {
+  void *p = nullptr;
+  if (count) IJ_HIP(hipMalloc(&p, count * sizeof(T)));
+  return (T *)p;
+}
+void dev_free(void *p) {
+  if (p) (void)hipFree(p);
+}
+
+// Copies the tiles of a trellis [IT][OT][16K] (pack layout) into the re-laid order [OT/2][IT][2] at dst (host).
+void relay_tiles(const uint16_t *src, int IT, int OT, int K, uint8_t *dst) {
+  const size_t tb = 32u * (size_t)K;
+  const int OTp = OT + (OT & 1);
+  for (int tk = 0; tk < IT; tk++)
+    for (int tn = 0; tn < OTp; tn++) {
+      uint8_t *d = dst + relaid_tile(IT, tk, tn) * tb;
+      if (tn < OT) memcpy(d, (const uint8_t *)src + ((size_t)tk * OT + tn) * tb, tb);
+      else memset(d, 0, tb);
+    }
+}
+
+void check_dims(int in, int out, int K) {
+  IJ_CHECK(in > 0 && out > 0 && in % 16 == 0 && out % 16 == 0, "EXL3 dims %d x %d must be multiples of 16", in, out);
+  IJ_CHECK(K >= 2 && K <= 8, "EXL3 K=%d not instantiated (2..8)", K);
+  had_size(in);
+  had_size(out);
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------------------------------- linear
+struct ne_exl3_lin {
+  int in = 0, out = 0, K = 0, IT = 0, OT = 0, OTp = 0, had_in = 0, had_out = 0;
+  uint32_t *tiles = nullptr;
+  uint16_t *suh = nullptr, *svh = nullptr;
+  uint16_t *xh = nullptr;  // [8][in]
+  float *part = nullptr;   // [S][8][OTp*16]
+  int part_S = 0;
+  ~ne_exl3_lin() {
+    dev_free(tiles);
+    dev_free(suh);
+    dev_free(svh);
+    dev_free(xh);
+    dev_free(part);
+  }
+  // k splits: smallest S (dividing IT, >= 8 k tiles per split) that gives >= 1024 workgroups, then enough to keep
+  // the staged input within 32 KiB of LDS at R rows
+  int splits(int R) const {
+    const int NP = OTp / 2;
+    int S = 1;
+    while (NP * S < 1024 && IT % (2 * S) == 0 && IT / (2 * S) >= 8) S *= 2;
+    const int RT = R <= 1 ? 1 : R <= 2 ? 2 : R <= 4 ? 4 : 8;
+    while ((size_t)RT * (IT / S) * 32 > 32768 && IT % (2 * S) == 0) S *= 2;
+    return S;
+  }
+};
+
+static ne_exl3_lin *lin_create(const uint16_t *trellis, const uint16_t *suh, const uint16_t *svh, int in, int out,
+                               int K) {
+  check_dims(in, out, K);
+  IJ_CHECK(trellis && suh && svh, "null array");
+  ensure_device();
+  auto l = std::make_unique<ne_exl3_lin>();
+  l->in = in;
+  l->out = out;
+  l->K = K;
+  l->IT = in / 16;
+  l->OT = out / 16;
+  l->OTp = l->OT + (l->OT & 1);
+  l->had_in = had_size(in);
+  l->had_out = had_size(out);
+  const size_t tbytes = (size_t)l->IT * l->OTp * 32 * K;
+  std::vector<uint8_t> host(tbytes);
+  relay_tiles(trellis, l->IT, l->OT, K, host.data());
+  l->tiles = (uint32_t *)dev_alloc<uint8_t>(tbytes);
+  IJ_HIP(hipMemcpy(l->tiles, host.data(), tbytes, hipMemcpyHostToDevice));
+  l->suh = dev_alloc<uint16_t>(in);
+  l->svh = dev_alloc<uint16_t>(out);
+  IJ_HIP(hipMemcpy(l->suh, suh, 2u * in, hipMemcpyHostToDevice));
+  IJ_HIP(hipMemcpy(l->svh, svh, 2u * out, hipMemcpyHostToDevice));
+  l->xh = dev_alloc<uint16_t>((size_t)8 * in);
+  return l.release();
+}
+
+extern "C" {
+
+NE_API ne_exl3_lin *ne_exl3_lin_create(const uint16_t *trellis, const uint16_t *suh, const uint16_t *svh, int in,
+                                       int out, int K) {
+  ne_exl3_lin *r = nullptr;
+  c_call([&] { r = lin_create(trellis, suh, svh, in, out, K); });
+  return r;
+}
+
+NE_API ne_exl3_lin *ne_exl3_lin_load(const ne_pack *p, const char *prefix) {
+  ne_exl3_lin *r = nullptr;
+  c_call([&] {
+    IJ_CHECK(p && prefix, "null argument");
+    const std::string pre = prefix;
+    const TensorInfo &t = p->pack->need(pre + ".trellis", NE_U16, {-1, -1, -1});
+    const int in = (int)t.shape[0] * 16, out = (int)t.shape[1] * 16;
+    IJ_CHECK(t.shape[2] % 16 == 0, "%s.trellis: last dim %lld not 16 K", prefix, (long long)t.shape[2]);
+    const int K = (int)t.shape[2] / 16;
+    const TensorInfo &su = p->pack->need(pre + ".suh", NE_F16, {in});
+    const TensorInfo &sv = p->pack->need(pre + ".svh", NE_F16, {out});
+    r = lin_create((const uint16_t *)t.host, (const uint16_t *)su.host, (const uint16_t *)sv.host, in, out, K);
+  });
+  return r;
+}
+
+NE_API void ne_exl3_lin_free(ne_exl3_lin *l) {
+  if (l) {
+    (void)hipStreamSynchronize(stream());
+    delete l;
+  }
+}
+
+NE_API int ne_exl3_lin_info(const ne_exl3_lin *l, int *in, int *out, int *K) {
+  return c_call([&] {
+    IJ_CHECK(l, "null linear");
+    if (in) *in = l->in;
+    if (out) *out = l->out;
+    if (K) *K = l->K;
+  });
+}
+
+static void timed(hipStream_t s, double *gpu_ms, const std::function<void()> &work) {
+  if (!gpu_ms) {
+    work();
+    return;
+  }
+  hipEvent_t e0, e1;
+  IJ_HIP(hipEventCreate(&e0));
+  IJ_HIP(hipEventCreate(&e1));
+  IJ_HIP(hipEventRecord(e0, s));
+  work();
+  IJ_HIP(hipEventRecord(e1, s));
+  IJ_HIP(hipEventSynchronize(e1));
+  float ms = 0.f;
+  IJ_HIP(hipEventElapsedTime(&ms, e0, e1));
+  *gpu_ms = ms;
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+}
+
+NE_API int ne_exl3_lin_run(ne_exl3_lin *l, int R, const ne_buf *x, uint64_t x_off, ne_buf *y, uint64_t y_off,
+                           double *gpu_ms) {
+  return c_call([&] {
+    IJ_CHECK(l && x && y, "null argument");
+    IJ_CHECK(R >= 1 && R <= 8, "rows %d (1..8)", R);
+    IJ_CHECK(x_off % 4 == 0 && y_off % 4 == 0, "offsets must be 4-byte aligned");
+    IJ_CHECK(x_off + (uint64_t)R * l->in * 4 <= x->size, "x buffer too small for [%d][%d] f32", R, l->in);
+    IJ_CHECK(y_off + (uint64_t)R * l->out * 4 <= y->size, "y buffer too small for [%d][%d] f32", R, l->out);
+    const int S = l->splits(R);
+    if (S > l->part_S) {
+      dev_free(l->part);
+      l->part = dev_alloc<float>((size_t)S * 8 * l->OTp * 16);
+      l->part_S = S;
+    }
+    LinArgs a;
+    a.tiles = l->tiles;
+    a.suh = l->suh;
+    a.svh = l->svh;
+    a.in = l->in;
+    a.out = l->out;
+    a.K = l->K;
+    a.IT = l->IT;
+    a.OT = l->OT;
+    a.had_in = l->had_in;
+    a.had_out = l->had_out;
+    a.sc_in = had_scale(l->had_in);
+    a.sc_out = had_scale(l->had_out);
+    a.R = R;
+    a.S = S;
+    a.x = (const float *)((const char *)x->dev + x_off);
+    a.y = (float *)((char *)y->dev + y_off);
+    a.xh = l->xh;
+    a.part = l->part;
+    timed(stream(), gpu_ms, [&] { launch_lin(a, stream()); });
+  });
+}
+
+NE_API int ne_exl3_lin_decode(ne_exl3_lin *l, ne_buf *w, double *gpu_ms) {
+  return c_call([&] {
+    IJ_CHECK(l && w, "null argument");
+    IJ_CHECK(w->size >= (uint64_t)l->in * l->out * 2, "w buffer too small for [%d][%d] fp16", l->in, l->out);
+    timed(stream(), gpu_ms, [&] { launch_decode(l->tiles, l->IT, l->OT, l->K, (uint16_t *)w->dev, stream()); });
+  });
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------------------------------- MoE layer
+struct ne_moe {
+  int hid = 0, inter = 0, ne = 0, topk = 0, K = 0, Ks = 0, has_shared = 0, has_sgate = 0, ksplit = 2;
+  ExpertLayout lay, slay;
+  uint8_t *experts = nullptr, *shared = nullptr;
+  uint16_t *router = nullptr;  // [ne + has_sgate][hid]
+  int Rcap = 0;
+  float *logits = nullptr, *sgv = nullptr, *guo = nullptr, *dn = nullptr;
+  uint32_t *route = nullptr, *ctr = nullptr;
+  int last_R = 0;
+  float *last_y = nullptr;
+  ~ne_moe() {
+    for (void *p : std::initializer_list<void *>{experts, shared, router, logits, sgv, guo, dn, route, ctr})
+      dev_free(p);
+  }
+  int nslot() const { return topk + has_shared; }
+  void ensure_scratch(int R) {
+    if (R <= Rcap) return;
+    for (void *p : std::initializer_list<void *>{logits, sgv, guo, dn, route}) dev_free(p);
+    const size_t S = (size_t)R * nslot();
+    logits = dev_alloc<float>((size_t)R * (ne + 1));
+    sgv = dev_alloc<float>(R);
+    guo = dev_alloc<float>(S * 2 * ksplit * inter);
+    dn = dev_alloc<float>(S * hid);
+    route = dev_alloc<uint32_t>((size_t)R * 2 * topk);
+    IJ_HIP(hipMemset(route, 0, sizeof(uint32_t) * R * 2 * topk));
+    Rcap = R;
+  }
+  MoeArgs args(int R, const float *x, float *y) const {
+    MoeArgs a;
+    a.x = x;
+    a.y = y;
+    a.R = R;
+    a.hid = hid;
+    a.inter = inter;
+    a.ne = ne;
+    a.topk = topk;
+    a.nslot = nslot();
+    a.router = router;
+    a.has_sgate = has_sgate;
+    a.experts = experts;
+    a.shared = shared;
+    a.lay = lay;
+    a.slay = slay;
+    a.had_hid = had_size(hid);
+    a.had_inter = had_size(inter);
+    a.sc_hid = had_scale(a.had_hid);
+    a.sc_inter = had_scale(a.had_inter);
+    a.ksplit = ksplit;
+    a.logits = logits;
+    a.route = route;
+    a.sgv = sgv;
+    a.guo = guo;
+    a.dn = dn;
+    a.ctr = ctr;
+    return a;
+  }
+  void launch(int R, const float *x, float *y, hipStream_t s) const {
+    const MoeArgs a = args(R, x, y);
+    launch_moe_router(a, s);
+    launch_moe_gateup(a, s);
+    launch_moe_down(a, s);
+    launch_moe_combine(a, s);
+  }
+};
+
+namespace {
+
+void moe_check_dims(int hid, int inter, int ne, int topk) {
+  IJ_CHECK(hid % 128 == 0 && inter % 32 == 0, "MoE hid %d must be a multiple of 128, inter %d of 32", hid, inter);
+  IJ_CHECK(hid % 8 == 0 && hid / 2 <= 4096 && inter <= 4096, "MoE dims too large for one workgroup's LDS");
+  IJ_CHECK(ne >= 1 && ne <= 1024 && topk >= 1 && topk <= 32 && topk <= ne, "MoE ne %d / topk %d out of range", ne,
+           topk);
+  had_size(hid);
+  had_size(inter);
+}
+
+// one expert's (or the shared expert's) block in the re-laid layout, built on the host
+void build_block(const ExpertLayout &L, int hid, int inter, const uint16_t *tr[3], const uint16_t *su[3],
+                 const uint16_t *sv[3], uint8_t *dst) {
+  memset(dst, 0, L.bytes);
+  const int dims[3][2] = {{hid, inter}, {hid, inter}, {inter, hid}};
+  for (int p = 0; p < 3; p++) {
+    relay_tiles(tr[p], dims[p][0] / 16, dims[p][1] / 16, L.K, dst + L.tr[p]);
+    memcpy(dst + L.su[p], su[p], 2u * dims[p][0]);
+    memcpy(dst + L.sv[p], sv[p], 2u * dims[p][1]);
+  }
+}
+
+ne_moe *moe_create(const ne_moe_desc &d) {
+  moe_check_dims(d.hid, d.inter, d.ne, d.topk);
+  IJ_CHECK(d.K >= 2 && d.K <= 8, "routed K %d (2..8)", d.K);
+  IJ_CHECK(d.router && d.gt && d.ut && d.dt && d.gsu && d.gsv && d.usu && d.usv && d.dsu && d.dsv,
+           "missing routed expert or router arrays");
+  const bool sh = d.sgt != nullptr;
+  IJ_CHECK(!sh || (d.sut && d.sdt && d.sgsu && d.sgsv && d.susu && d.susv && d.sdsu && d.sdsv),
+           "shared expert arrays incomplete");
+  IJ_CHECK(!sh || (d.Ks >= 2 && d.Ks <= 8), "shared K %d (2..8)", d.Ks);
+  ensure_device();
+  auto m = std::make_unique<ne_moe>();
+  m->hid = d.hid;
+  m->inter = d.inter;
+  m->ne = d.ne;
+  m->topk = d.topk;
+  m->K = d.K;
+  m->Ks = sh ? d.Ks : 0;
+  m->has_shared = sh;
+  m->has_sgate = d.sgate != nullptr;
+  m->lay = expert_layout(d.hid, d.inter, d.K);
+  const size_t tsz[3] = {(size_t)d.hid * d.inter * d.K / 16, (size_t)d.hid * d.inter * d.K / 16,
+                         (size_t)d.inter * d.hid * d.K / 16};
+  m->experts = dev_alloc<uint8_t>((size_t)d.ne * m->lay.bytes);
+  const int chunk = 16;
+  std::vector<uint8_t> host((size_t)chunk * m->lay.bytes);
+  for (int e0 = 0; e0 < d.ne; e0 += chunk) {
+    const int n = std::min(chunk, d.ne - e0);
+    for (int i = 0; i < n; i++) {
+      const size_t e = (size_t)(e0 + i);
+      const uint16_t *tr[3] = {d.gt + e * tsz[0], d.ut + e * tsz[1], d.dt + e * tsz[2]};
+      const uint16_t *su[3] = {d.gsu + e * d.hid, d.usu + e * d.hid, d.dsu + e * d.inter};
+      const uint16_t *sv[3] = {d.gsv + e * d.inter, d.usv + e * d.inter, d.dsv + e * d.hid};
+      build_block(m->lay, d.hid, d.inter, tr, su, sv, host.data() + (size_t)i * m->lay.bytes);
+    }
+    IJ_HIP(hipMemcpy(m->experts + (size_t)e0 * m->lay.bytes, host.data(), (size_t)n * m->lay.bytes,
+                     hipMemcpyHostToDevice));
+  }
+  if (sh) {
+    m->slay = expert_layout(d.hid, d.inter, d.Ks);
+    std::vector<uint8_t> sb(m->slay.bytes);
+    const uint16_t *tr[3] = {d.sgt, d.sut, d.sdt};
+    const uint16_t *su[3] = {d.sgsu, d.susu, d.sdsu};
+    const uint16_t *sv[3] = {d.sgsv, d.susv, d.sdsv};
+    build_block(m->slay, d.hid, d.inter, tr, su, sv, sb.data());
+    m->shared = dev_alloc<uint8_t>(m->slay.bytes);
+    IJ_HIP(hipMemcpy(m->shared, sb.data(), sb.size(), hipMemcpyHostToDevice));
+  }
+  const size_t rrows = (size_t)d.ne + m->has_sgate;
+  m->router = dev_alloc<uint16_t>(rrows * d.hid);
+  IJ_HIP(hipMemcpy(m->router, d.router, 2u * d.ne * d.hid, hipMemcpyHostToDevice));
+  if (m->has_sgate) IJ_HIP(hipMemcpy(m->router + (size_t)d.ne * d.hid, d.sgate, 2u * d.hid, hipMemcpyHostToDevice));
+  m->ctr = dev_alloc<uint32_t>(1);
+  IJ_HIP(hipMemset(m->ctr, 0, 4));
+  if (const char *e = getenv("IJAH_MOE_KSPLIT")) m->ksplit = std::max(1, atoi(e));
+  IJ_CHECK((d.hid / 16) % m->ksplit == 0 && ((d.hid / 16) / m->ksplit) % 8 == 0, "ksplit %d does not divide hid %d",
+           m->ksplit, d.hid);
+  m->ensure_scratch(1);
+  return m.release();
+}
+
+}  // namespace
+
+extern "C" {
+
+NE_API ne_moe *ne_moe_create(const ne_moe_desc *d) {
+  ne_moe *r = nullptr;
+  c_call([&] {
+    IJ_CHECK(d, "null descriptor");
+    r = moe_create(*d);
+  });
+  return r;
+}
+
+NE_API ne_moe *ne_moe_load(const ne_pack *p, const char *prefix, int topk) {
+  ne_moe *r = nullptr;
+  c_call([&] {
+    IJ_CHECK(p && prefix, "null argument");
+    const Pack &P = *p->pack;
+    const std::string mp = prefix;
+    const TensorInfo &rw = P.need(mp + "gate.weight", NE_BF16, {-1, -1});
+    ne_moe_desc d;
+    memset(&d, 0, sizeof d);
+    d.ne = (int)rw.shape[0];
+    d.hid = (int)rw.shape[1];
+    d.topk = topk;
+    d.router = (const uint16_t *)rw.host;
+    if (P.has(mp + "shared_expert_gate.weight"))
+      d.sgate = (const uint16_t *)P.need(mp + "shared_expert_gate.weight", NE_BF16, {}).host;
+    const TensorInfo &gt = P.need(mp + "switch_mlp.gate_proj.trellis", NE_U16, {d.ne, d.hid / 16, -1, -1});
+    d.inter = (int)gt.shape[2] * 16;
+    IJ_CHECK(gt.shape[3] % 16 == 0, "switch_mlp.gate_proj.trellis: last dim not 16 K");
+    d.K = (int)gt.shape[3] / 16;
+    const int64_t tl = 16 * d.K;
+    auto T = [&](const char *n, std::initializer_list<int64_t> s) {
+      return (const uint16_t *)P.need(mp + n, -1, s).host;
+    };
+    d.gt = (const uint16_t *)gt.host;
+    d.ut = T("switch_mlp.up_proj.trellis", {d.ne, d.hid / 16, d.inter / 16, tl});
+    d.dt = T("switch_mlp.down_proj.trellis", {d.ne, d.inter / 16, d.hid / 16, tl});
+    d.gsu = T("switch_mlp.gate_proj.suh", {d.ne, d.hid});
+    d.gsv = T("switch_mlp.gate_proj.svh", {d.ne, d.inter});
+    d.usu = T("switch_mlp.up_proj.suh", {d.ne, d.hid});
+    d.usv = T("switch_mlp.up_proj.svh", {d.ne, d.inter});
+    d.dsu = T("switch_mlp.down_proj.suh", {d.ne, d.inter});
+    d.dsv = T("switch_mlp.down_proj.svh", {d.ne, d.hid});
+    for (const char *n : {"gate_proj", "up_proj", "down_proj"})
+      for (const char *s : {"suh", "svh"})
+        IJ_CHECK(P.need(mp + "switch_mlp." + n + "." + s, -1, {}).dtype == NE_F16, "%s: suh/svh must be F16", n);
+    if (P.has(mp + "shared_expert.gate_proj.trellis")) {
+      const TensorInfo &sg = P.need(mp + "shared_expert.gate_proj.trellis", NE_U16, {d.hid / 16, d.inter / 16, -1});
+      d.Ks = (int)sg.shape[2] / 16;
+      const int64_t ts = 16 * d.Ks;
+      d.sgt = (const uint16_t *)sg.host;
+      d.sut = T("shared_expert.up_proj.trellis", {d.hid / 16, d.inter / 16, ts});
+      d.sdt = T("shared_expert.down_proj.trellis", {d.inter / 16, d.hid / 16, ts});
+      d.sgsu = T("shared_expert.gate_proj.suh", {d.hid});
+      d.sgsv = T("shared_expert.gate_proj.svh", {d.inter});
+      d.susu = T("shared_expert.up_proj.suh", {d.hid});
+      d.susv = T("shared_expert.up_proj.svh", {d.inter});
+      d.sdsu = T("shared_expert.down_proj.suh", {d.inter});
+      d.sdsv = T("shared_expert.down_proj.svh", {d.hid});
+    }
+    r = moe_create(d);
+  });
+  return r;
+}
+
+NE_API ne_moe *ne_moe_synth(int hid, int inter, int ne, int topk, int K, int has_shared, int Ks, uint64_t seed) {
+  ne_moe *r = nullptr;
+  c_call([&] {
+    moe_check_dims(hid, inter, ne, topk);
+    IJ_CHECK(K >= 2 && K <= 8 && (!has_shared || (Ks >= 2 && Ks <= 8)), "K out of range");
+    ensure_device();
+    auto m = std::make_unique<ne_moe>();
+    m->hid = hid;
+    m->inter = inter;
+    m->ne = ne;
+    m->topk = topk;
+    m->K = K;
+    m->Ks = has_shared ? Ks : 0;
+    m->has_shared = has_shared != 0;
+    m->lay = expert_layout(hid, inter, K);
+    hipStream_t s = stream();
+    m->experts = dev_alloc<uint8_t>((size_t)ne * m->lay.bytes);
+    launch_fill_u32((uint32_t *)m->experts, (size_t)ne * m->lay.bytes / 4, seed * 7 + 1, s);
+    auto scales = [&](uint8_t *blk, const ExpertLayout &L, uint64_t sd) {
+      const int dims[3][2] = {{hid, inter}, {hid, inter}, {inter, hid}};
+      for (int p = 0; p < 3; p++) {
+        launch_fill_scale_f16((uint16_t *)(blk + L.su[p]), dims[p][0], sd * 131 + 2 * p, s);
+        launch_fill_scale_f16((uint16_t *)(blk + L.sv[p]), dims[p][1], sd * 131 + 2 * p + 1, s);
+      }
+    };
+    for (int e = 0; e < ne; e++) scales(m->experts + (size_t)e * m->lay.bytes, m->lay, seed * 100003 + e);
+    if (has_shared) {
+      m->slay = expert_layout(hid, inter, Ks);
+      m->shared = dev_alloc<uint8_t>(m->slay.bytes);
+      launch_fill_u32((uint32_t *)m->shared, m->slay.bytes / 4, seed * 7 + 3, s);
+      scales(m->shared, m->slay, seed * 100003 + 999983);
+    }
+    m->router = dev_alloc<uint16_t>((size_t)ne * hid);
+    launch_fill_normal_bf16(m->router, (size_t)ne * hid, seed * 7 + 5, (float)(1.0 / std::sqrt((double)hid)), s);
+    m->ctr = dev_alloc<uint32_t>(1);
+    IJ_HIP(hipMemsetAsync(m->ctr, 0, 4, s));
+    if (const char *e = getenv("IJAH_MOE_KSPLIT")) m->ksplit = std::max(1, atoi(e));
+    IJ_CHECK((hid / 16) % m->ksplit == 0 && ((hid / 16) / m->ksplit) % 8 == 0, "ksplit %d does not divide hid %d",
+             m->ksplit, hid);
+    m->ensure_scratch(1);
+    IJ_HIP(hipStreamSynchronize(s));
+    r = m.release();
+  });
+  return r;
+}
+
+NE_API void ne_moe_free(ne_moe *m) {
+  if (m) {
+    (void)hipStreamSynchronize(stream());
+    delete m;
+  }
+}
+
+NE_API int ne_moe_info(const ne_moe *m, int *hid, int *inter, int *ne, int *topk, int *K, int *slots) {
+  return c_call([&] {
+    IJ_CHECK(m, "null layer");
+    if (hid) *hid = m->hid;
+    if (inter) *inter = m->inter;
+    if (ne) *ne = m->ne;
+    if (topk) *topk = m->topk;
+    if (K) *K = m->K;
+    if (slots) *slots = m->nslot();
+  });
+}
+
+NE_API int ne_moe_run(ne_moe *m, int R, const ne_buf *x, uint64_t x_off, ne_buf *y, uint64_t y_off, double *gpu_ms) {
+  return c_call([&] {
+    IJ_CHECK(m && x && y, "null argument");
+    IJ_CHECK(R >= 1 && R <= 4096, "rows %d (1..4096)", R);
+    IJ_CHECK(x_off % 16 == 0 && y_off % 4 == 0, "x offset must be 16-byte aligned, y offset 4-byte aligned");
+    IJ_CHECK(x_off + (uint64_t)R * m->hid * 4 <= x->size, "x buffer too small for [%d][%d] f32", R, m->hid);
+    IJ_CHECK(y_off + (uint64_t)R * m->hid * 4 <= y->size, "y buffer too small for [%d][%d] f32", R, m->hid);
+    m->ensure_scratch(R);
+    const float *xp = (const float *)((const char *)x->dev + x_off);
+    float *yp = (float *)((char *)y->dev + y_off);
+    timed(stream(), gpu_ms, [&] { m->launch(R, xp, yp, stream()); });
+    m->last_R = R;
+    m->last_y = yp;
+  });
+}
+
+NE_API int ne_moe_read(ne_moe *m, const char *name, void *dst, uint64_t nbytes) {
+  return c_call([&] {
+    IJ_CHECK(m && name && (dst || nbytes == 0), "null argument");
+    IJ_CHECK(m->last_R > 0, "no run yet");
+    IJ_HIP(hipStreamSynchronize(stream()));
+    const int R = m->last_R, S = R * m->nslot();
+    const std::string n = name;
+    std::vector<uint8_t> out;
+    auto fetch = [&](const void *src, size_t bytes) {
+      out.resize(bytes);
+      IJ_HIP(hipMemcpy(out.data(), src, bytes, hipMemcpyDeviceToHost));
+    };
+    if (n == "logits") {
+      std::vector<float> all((size_t)R * (m->ne + 1));
+      IJ_HIP(hipMemcpy(all.data(), m->logits, all.size() * 4, hipMemcpyDeviceToHost));
+      out.resize((size_t)R * m->ne * 4);
+      for (int r = 0; r < R; r++) memcpy(out.data() + (size_t)r * m->ne * 4, &all[(size_t)r * (m->ne + 1)], 4u * m->ne);
+    } else if (n == "route") {
+      fetch(m->route, (size_t)R * 2 * m->topk * 4);
+    } else if (n == "shared_gate") {
+      fetch(m->sgv, (size_t)R * 4);
+    } else if (n == "experts_gu") {
+      std::vector<float> g((size_t)S * 2 * m->ksplit * m->inter);
+      IJ_HIP(hipMemcpy(g.data(), m->guo, g.size() * 4, hipMemcpyDeviceToHost));
+      std::vector<float> o((size_t)S * 2 * m->inter, 0.f);
+      for (int sp = 0; sp < S * 2; sp++)
+        for (int k = 0; k < m->ksplit; k++)
+          for (int j = 0; j < m->inter; j++)
+            o[(size_t)sp * m->inter + j] += g[((size_t)sp * m->ksplit + k) * m->inter + j];
+      out.resize(o.size() * 4);
+      memcpy(out.data(), o.data(), out.size());
+    } else if (n == "experts_dn") {
+      fetch(m->dn, (size_t)S * m->hid * 4);
+    } else if (n == "mlp_out") {
+      fetch(m->last_y, (size_t)R * m->hid * 4);
+    } else {
+      throw Error(strfmt("unknown intermediate %s", name));
+    }
+    memcpy(dst, out.data(), std::min<uint64_t>(nbytes, out.size()));
+  });
+}
+
+NE_API int ne_moe_decode(ne_moe *m, int e, int proj, ne_buf *w, double *gpu_ms) {
+  return c_call([&] {
+    IJ_CHECK(m && w, "null argument");
+    IJ_CHECK(proj >= 0 && proj <= 2, "proj %d (0 gate, 1 up, 2 down)", proj);
+    IJ_CHECK(e >= 0 && (e < m->ne || (e == m->ne && m->has_shared)), "expert %d out of range", e);
+    const bool sh = e == m->ne;
+    const ExpertLayout &L = sh ? m->slay : m->lay;
+    const uint8_t *blk = sh ? m->shared : m->experts + (size_t)e * m->lay.bytes;
+    const int in = proj == 2 ? m->inter : m->hid, out = proj == 2 ? m->hid : m->inter;
+    IJ_CHECK(w->size >= (uint64_t)in * out * 2, "w buffer too small");
+    timed(stream(), gpu_ms, [&] {
+      launch_decode((const uint32_t *)(blk + L.tr[proj]), in / 16, out / 16, L.K, (uint16_t *)w->dev, stream());
+    });
+  });
+}
+
+NE_API int ne_moe_bytes(const ne_moe *m, int R, uint64_t *bytes) {
+  return c_call([&] {
+    IJ_CHECK(m && bytes, "null argument");
+    IJ_CHECK(m->last_R >= R && R >= 1, "run the layer at R rows first");
+    IJ_HIP(hipStreamSynchronize(stream()));
+    std::vector<uint32_t> rt((size_t)R * 2 * m->topk);
+    IJ_HIP(hipMemcpy(rt.data(), m->route, rt.size() * 4, hipMemcpyDeviceToHost));
+    std::set<uint32_t> uniq;
+    for (int r = 0; r < R; r++)
+      for (int k = 0; k < m->topk; k++) uniq.insert(rt[(size_t)r * 2 * m->topk + k]);
+    auto per_expert = [&](int K) {
+      const uint64_t w = (uint64_t)m->hid * m->inter;
+      return 3 * w * K / 8 + 2u * (uint64_t)(3 * (m->hid + m->inter));
+    };
+    uint64_t b = uniq.size() * per_expert(m->K);
+    if (m->has_shared) b += per_expert(m->Ks);
+    b += 2u * (uint64_t)(m->ne + m->has_sgate) * m->hid;
+    *bytes = b;
+  });
+}
+
+NE_API int ne_moe_time(ne_moe *const *layers, int n, int R, const ne_buf *x, int warmup, int reps,
+                       double *us_per_layer) {
+  return c_call([&] {
+    IJ_CHECK(layers && n >= 1 && x && us_per_layer && reps >= 1, "bad arguments");
+    for (int i = 0; i < n; i++) {
+      IJ_CHECK(layers[i], "null layer %d", i);
+      IJ_CHECK(layers[i]->hid == layers[0]->hid, "layers differ in hid");
+      layers[i]->ensure_scratch(R);
+    }
+    const int hid = layers[0]->hid;
+    IJ_CHECK((uint64_t)R * hid * 4 <= x->size, "x buffer too small");
+    hipStream_t s = stream();
+    float *ys = dev_alloc<float>((size_t)n * R * hid);
+    const float *xp = (const float *)x->dev;
+    hipGraph_t g = nullptr;
+    hipGraphExec_t ge = nullptr;
+    auto cleanup = [&] {
+      if (ge) (void)hipGraphExecDestroy(ge);
+      if (g) (void)hipGraphDestroy(g);
+      dev_free(ys);
+    };
+    try {
+      IJ_HIP(hipStreamSynchronize(s));
+      IJ_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+      for (int i = 0; i < n; i++) layers[i]->launch(R, xp, ys + (size_t)i * R * hid, s);
+      IJ_HIP(hipStreamEndCapture(s, &g));
+      IJ_HIP(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0));
+      for (int i = 0; i < warmup; i++) IJ_HIP(hipGraphLaunch(ge, s));
+      double ms = 0;
+      timed(s, &ms, [&] {
+        for (int i = 0; i < reps; i++) IJ_HIP(hipGraphLaunch(ge, s));
+      });
+      *us_per_layer = ms * 1000.0 / ((double)reps * n);
+      for (int i = 0; i < n; i++) {
+        layers[i]->last_R = R;
+        layers[i]->last_y = nullptr;
+      }
+    } catch (...) {
+      cleanup();
+      throw;
+    }
+    cleanup();
+  });
+}
+
+NE_API int ne_moe_time_kernels(ne_moe *const *layers, int n, int R, const ne_buf *x, int reps, char names[][16],
+                               double *us, int *n_kinds) {
+  return c_call([&] {
+    IJ_CHECK(layers && n >= 1 && x && us && n_kinds && names && reps >= 1, "bad arguments");
+    IJ_CHECK(*n_kinds >= 4, "need room for 4 kernel kinds");
+    const int hid = layers[0]->hid;
+    IJ_CHECK((uint64_t)R * hid * 4 <= x->size, "x buffer too small");
+    hipStream_t s = stream();
+    float *ys = dev_alloc<float>((size_t)n * R * hid);
+    const float *xp = (const float *)x->dev;
+    std::vector<MoeArgs> a;
+    for (int i = 0; i < n; i++) {
+      layers[i]->ensure_scratch(R);
+      a.push_back(layers[i]->args(R, xp, ys + (size_t)i * R * hid));
+      layers[i]->launch(R, xp, ys + (size_t)i * R * hid, s);
+    }
+    void (*fns[4])(const MoeArgs &, hipStream_t) = {launch_moe_router, launch_moe_gateup, launch_moe_down,
+                                                    launch_moe_combine};
+    const char *nm[4] = {"router", "gateup", "down", "combine"};
+    try {
+      for (int k = 0; k < 4; k++) {
+        double ms = 0;
+        timed(s, &ms, [&] {
+          for (int r = 0; r < reps; r++)
+            for (int i = 0; i < n; i++) fns[k](a[i], s);
+        });
+        snprintf(names[k], 16, "%s", nm[k]);
+        us[k] = ms * 1000.0 / ((double)reps * n);
+      }
+    } catch (...) {
+      dev_free(ys);
+      throw;
+    }
+    IJ_HIP(hipStreamSynchronize(s));
+    dev_free(ys);
+    *n_kinds = 4;
+  });
+}
+
+}  // extern "C"

@@ -1,0 +1,77 @@
+// Host-side view of the HIP kernels: registry for ne_run_kernel and the launch wrappers the entry points use.
+#pragma once
+#include <string>
+#include <vector>
+
+#include "common.h"
+
+namespace ijah {
+
+struct KernelEntry {
+  std::string name;
+  const void *fn;
+  std::vector<uint32_t> arg_sizes;
+  int K;  // function constant 10 (-1: not specialised on it)
+  int R;  // function constant 16
+};
+// name + optional function constants (index 10 = K, 16 = R) -> entry, or nullptr
+const KernelEntry *find_kernel(const char *name, const ne_fconst *fc, int nfc);
+
+// Byte offsets of one expert's (or one linear's) regions inside its HBM block. Tiles of a projection are re-laid as
+// [n-pair p][k-tile tk][2], so a workgroup working on output tiles (2p, 2p+1) streams one contiguous span.
+struct ExpertLayout {
+  int K = 0;
+  uint64_t tr[3] = {0, 0, 0};  // gate, up, down trellis
+  uint64_t su[3] = {0, 0, 0};  // F16 input scales
+  uint64_t sv[3] = {0, 0, 0};  // F16 output scales
+  uint64_t bytes = 0;          // block stride (256-byte multiple)
+};
+ExpertLayout expert_layout(int hid, int inter, int K);
+// halfword index of tile (tk, tn) of a [IT][OT] matrix in the re-laid order (OT padded to even)
+inline uint64_t relaid_tile(int IT, int tk, int tn) { return ((uint64_t)(tn >> 1) * IT + tk) * 2 + (tn & 1); }
+
+struct MoeArgs {
+  const float *x;
+  float *y;
+  int R, hid, inter, ne, topk, nslot;  // nslot = topk + (shared expert ? 1 : 0)
+  const uint16_t *router;              // BF16 [ne + has_sgate][hid]
+  int has_sgate;
+  const uint8_t *experts;              // ne blocks of stride lay.bytes
+  const uint8_t *shared;               // shared block (layout slay) or null
+  ExpertLayout lay, slay;
+  int had_hid, had_inter;
+  float sc_hid, sc_inter;              // f32(1/sqrt(had))
+  int ksplit;                          // gate/up k splits
+  float *logits;                       // [R][ne + 1]
+  uint32_t *route;                     // [R][2 topk]
+  float *sgv;                          // [R]
+  float *guo;                          // [R nslot][2][ksplit][inter]
+  float *dn;                           // [R nslot][hid]
+  uint32_t *ctr;                       // router arrival counter (self-resetting)
+};
+void launch_moe_router(const MoeArgs &a, hipStream_t s);
+void launch_moe_gateup(const MoeArgs &a, hipStream_t s);
+void launch_moe_down(const MoeArgs &a, hipStream_t s);
+void launch_moe_combine(const MoeArgs &a, hipStream_t s);
+
+struct LinArgs {
+  const uint32_t *tiles;  // re-laid trellis
+  const uint16_t *suh, *svh;
+  int in, out, K, IT, OT, had_in, had_out;
+  float sc_in, sc_out;
+  int R, S;               // rows, k splits
+  const float *x;
+  float *y;
+  uint16_t *xh;           // [R][in] prepared fp16 input (scratch)
+  float *part;            // [S][R][OTp * 16] (scratch)
+};
+void launch_lin(const LinArgs &a, hipStream_t s);
+// W' fp16 bits [IT*16][OT*16] from re-laid tiles
+void launch_decode(const uint32_t *tiles, int IT, int OT, int K, uint16_t *w, hipStream_t s);
+
+// device-side seeded fills (synthetic packs)
+void launch_fill_u32(uint32_t *p, uint64_t n, uint64_t seed, hipStream_t s);
+void launch_fill_scale_f16(uint16_t *p, uint64_t n, uint64_t seed, hipStream_t s);        // +-|N(1, 0.1)|
+void launch_fill_normal_bf16(uint16_t *p, uint64_t n, uint64_t seed, float stddev, hipStream_t s);
+
+}  // namespace ijah

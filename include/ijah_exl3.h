@@ -1,0 +1,95 @@
+/* EXL3 hot path on MI355X: trellis-decode fused into the MoE expert linears and the trunk linears.
+ *
+ * These entry points are the hot path's own C ABI. The reference adds such entry points in their own headers
+ * (reference include/engine.h:11-12); each function cites the reference interface whose job it takes over. All
+ * tensors are device buffers (ne_buf from engine.h); activations are f32 row-major, as in the reference kernels.
+ * Errors: 0 / -1 (NULL) + ne_last_error(), as engine.h. Every function that takes gpu_ms (may be NULL) waits for
+ * its GPU work and reports the GPU time of it; the others enqueue on the library stream and return.
+ */
+#ifndef IJAH_EXL3_H
+#define IJAH_EXL3_H
+#include "engine.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- buffers on a discrete GPU ---- */
+/* Writes the host mirror returned by ne_buf_contents back to the device. No reference counterpart: the reference's
+ * buffers are unified memory (reference include/engine.h:6-7), where this is a no-op. */
+NE_API int ne_buf_flush(ne_buf *b);
+/* Waits for all queued GPU work of the library (the reference's Recorder::wait, core/recorder.h:76). */
+NE_API int ne_sync(void);
+
+/* ---- one EXL3 linear: y[R][out] = x[R][in] @ W, W = diag(suh) H_in W' H_out diag(svh) ----
+ * trellis U16 [in/16][out/16][16K] (tile (tk, tn) = W'[16tk.., 16tn..] in the reference's slot order), suh F16 [in],
+ * svh F16 [out]; K 1..8; in, out multiples of 16 and of their Hadamard sizes (128, 64, 32 or 16). */
+typedef struct ne_exl3_lin ne_exl3_lin;
+/* reference kernels/trunk6/trunk6.mm:39-66 (t6::load of "<prefix>.trellis/.suh/.svh"); the tiles are re-laid in HBM
+ * for the GEMV's streaming order (pairs of output tiles, k-major inside a pair). */
+NE_API ne_exl3_lin *ne_exl3_lin_load(const ne_pack *p, const char *prefix);
+/* same from host arrays in the pack's layout */
+NE_API ne_exl3_lin *ne_exl3_lin_create(const uint16_t *trellis, const uint16_t *suh, const uint16_t *svh, int in,
+                                       int out, int K);
+NE_API void ne_exl3_lin_free(ne_exl3_lin *l);
+NE_API int ne_exl3_lin_info(const ne_exl3_lin *l, int *in, int *out, int *K);
+/* reference kernels/trunk6/trunk6.mm:232-249 (t6::record, SIMD path R 1..8): x f32 [R][in] at x_off, y f32 [R][out]
+ * at y_off; R 1..8. */
+NE_API int ne_exl3_lin_run(ne_exl3_lin *l, int R, const ne_buf *x, uint64_t x_off, ne_buf *y, uint64_t y_off,
+                           double *gpu_ms);
+/* W' decoded on the GPU from the re-laid tiles: fp16 bits [in][out] into w (at least in*out*2 bytes). Replaces the
+ * reference's decoded-weight check through exl3_codec.decode_inner (tests/trunk6/check_kernels.py:86). */
+NE_API int ne_exl3_lin_decode(ne_exl3_lin *l, ne_buf *w, double *gpu_ms);
+
+/* ---- fused MoE layer (router + softmax/top-k + routed and shared EXL3 experts + weighted combine) ---- */
+typedef struct ne_moe ne_moe;
+/* Host arrays in the pack's layout (reference models/flash_next/layer.mm:180-196):
+ *   router BF16 [ne][hid]; sgate BF16 [hid] or NULL (no shared_expert_gate: the shared expert is added with weight 1);
+ *   routed gate/up/down: trellis U16 [ne][in/16][out/16][16K], suh F16 [ne][in], svh F16 [ne][out];
+ *   shared gate/up/down (all NULL = no shared expert): trellis U16 [in/16][out/16][16 Ks], suh, svh. */
+typedef struct {
+  int hid, inter, ne, topk, K, Ks;
+  const uint16_t *router, *sgate;
+  const uint16_t *gt, *ut, *dt, *gsu, *gsv, *usu, *usv, *dsu, *dsv;
+  const uint16_t *sgt, *sut, *sdt, *sgsu, *sgsv, *susu, *susv, *sdsu, *sdsv;
+} ne_moe_desc;
+NE_API ne_moe *ne_moe_create(const ne_moe_desc *d);
+/* reference models/flash_next/layer.mm:180-196 (MoeW from "<prefix>gate.weight", "switch_mlp.*", "shared_expert.*",
+ * "shared_expert_gate.weight"); prefix like "language_model.model.layers.0.mlp." The pack's expert tensors are
+ * re-laid so each expert's trellis tiles, suh and svh are one contiguous 256-byte-aligned block in HBM. */
+NE_API ne_moe *ne_moe_load(const ne_pack *p, const char *prefix, int topk);
+/* Seeded synthetic layer generated on the device (no host copy): trellis uniform u16, suh / svh = +-|N(1, 0.1)|,
+ * router BF16 N(0, 1/hid) (logits ~ N(0,1) for N(0,1) inputs). has_shared: 1 = a shared expert of Ks bits.
+ * No reference counterpart (the reference benchmarks real packs); it feeds the benchmark at full size. */
+NE_API ne_moe *ne_moe_synth(int hid, int inter, int ne, int topk, int K, int has_shared, int Ks, uint64_t seed);
+NE_API void ne_moe_free(ne_moe *m);
+/* reference models/flash_next/layer.h:244-263 (ne_fn_layer_run_stage(l, 5): moe_router, moe_gateup, moe_down):
+ * x f32 [R][hid] -> y f32 [R][hid] = sum over the top-k slots in slot order of w_k expert_k(x) + g * shared(x). */
+NE_API int ne_moe_run(ne_moe *m, int R, const ne_buf *x, uint64_t x_off, ne_buf *y, uint64_t y_off,
+                      double *gpu_ms);
+/* reference models/flash_next/layer.h:258-262 (ne_fn_layer_read) for the MoE intermediates of the last run:
+ * "logits" f32 [R][ne], "route" u32 [R][2 topk] (ids, f32 weight bits), "shared_gate" f32 [R],
+ * "experts_gu" f32 [R][slots][2][inter] (gate / up inner outputs before H_out), "experts_dn" f32 [R][slots][hid]
+ * (down inner outputs before H_out), "mlp_out" f32 [R][hid]. Copies at most nbytes; returns 0. */
+NE_API int ne_moe_read(ne_moe *m, const char *name, void *dst, uint64_t nbytes);
+/* Expert e's projection proj (0 gate, 1 up, 2 down; e == ne: the shared expert) decoded from the re-laid HBM block:
+ * fp16 bits [in][out] into w. */
+NE_API int ne_moe_decode(ne_moe *m, int e, int proj, ne_buf *w, double *gpu_ms);
+NE_API int ne_moe_info(const ne_moe *m, int *hid, int *inter, int *ne, int *topk, int *K, int *slots);
+/* Bytes one layer step at R rows reads from HBM by algorithm: the touched experts' trellis + suh + svh (distinct
+ * experts of the last run's route), the shared expert and the router. */
+NE_API int ne_moe_bytes(const ne_moe *m, int R, uint64_t *bytes);
+/* Chain of n layers (layer i's output feeds layer i+1; layers may repeat), captured once in a HIP graph and replayed
+ * reps times after warmup replays: us_per_layer = GPU time per layer (HIP events on the library stream). Replaces the
+ * reference's differential timing (ne_fn_layer_time, models/flash_next/layer.h:266-267; core/bench.h:21-24). */
+NE_API int ne_moe_time(ne_moe *const *layers, int n, int R, const ne_buf *x, int warmup, int reps,
+                       double *us_per_layer);
+/* Per-kernel timing of the same chain: launches each kernel kind of the layer step alone, reps times per layer, and
+ * returns the mean duration in microseconds of each (names: "router", "gateup", "down", "combine"); n_kinds in/out. */
+NE_API int ne_moe_time_kernels(ne_moe *const *layers, int n, int R, const ne_buf *x, int reps, char names[][16],
+                               double *us, int *n_kinds);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* IJAH_EXL3_H */

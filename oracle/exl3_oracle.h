@@ -1,0 +1,86 @@
+/* CPU oracle for the EXL3 trellis decode + MoE / trunk linear path.
+ *
+ * TEST INFRASTRUCTURE ONLY. Nothing in the product (ijah_amd/) links, loads or calls this code; only tests/,
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg do, and there only as the checker / the timed CPU baseline.
+ *
+ * Every function restates the reference algorithm (publicExcess/ijah) in plain C. Citations are file:line in the
+ * reference tree. Pinning status of each function is listed in oracle/README.md.
+ */
+#ifndef IJAH_EXL3_ORACLE_H
+#define IJAH_EXL3_ORACLE_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- number formats ---- */
+uint16_t orc_f32_to_f16(float f); /* IEEE binary16, round to nearest even */
+float orc_f16_to_f32(uint16_t h);
+float orc_bf16r(float x);          /* round to bf16 (RNE) and back to f32: kernels/ne_common.h:23-26 */
+float orc_bf16_to_f32(uint16_t b);
+
+/* ---- EXL3 codebook and trellis readers ---- */
+uint16_t orc_mcg(uint32_t cw);     /* window-15 MCG codeword -> fp16 bits: kernels/ne_common.h:139-144 */
+/* slot s (0..255) -> row, col inside a 16x16 tile: kernels/ne_common.h:105-108, kernels/trunk6/trunk6.metal:611-629 */
+void orc_slot_rc(int s, int *row, int *col);
+/* codeword (16 bits; the decoder uses the low 15) of every slot of one tile (16K u16 halfwords).
+ * ring: brute force over the tail-biting ring of 256K bits (the definition).
+ * lane: kernels/ne_common.h:109-157 lane_load/lane_funnel/cw_at, K 4..6.
+ * t6:   kernels/trunk6/trunk6.metal:91-127 t6_lane/t6_load/t6_dec, K 1..8. */
+void orc_tile_cw_ring(const uint16_t *tile, int K, uint16_t cw[256]);
+int orc_tile_cw_lane(const uint16_t *tile, int K, uint16_t cw[256]);
+int orc_tile_cw_t6(const uint16_t *tile, int K, uint16_t cw[256]);
+/* W' [in][out] as fp16 bits from trellis U16 [in/16][out/16][16K] */
+void orc_decode(const uint16_t *trellis, int in, int out, int K, uint16_t *w);
+
+/* ---- Hadamard ---- */
+int orc_had_size(int d);                       /* tools/convert_trunk_enc.py:59-63 */
+float orc_had_scale(int n);                    /* f32(1/sqrt(n)) */
+void orc_fwht_f32(float *v, int n, int had);   /* blocks of `had`, butterfly bits 0,1,..; then * 1/sqrt(had) */
+void orc_fwht_f64(double *v, int n, int had);
+
+/* ---- EXL3 linear: y[R][out] = x[R][in] @ W, W = diag(suh) H_hi W' H_ho diag(svh) ---- */
+/* kernel arithmetic: f32 x*suh, f32 FWHT, fp16 prep, f64 dot with exact fp16 W', f32 H_ho, * svh
+ * (tests/trunk6/check_kernels.py:96-98, kernels/trunk6/trunk6.metal:68-85,199-214) */
+void orc_exl3_linear(const float *x, int R, const uint16_t *trellis, const uint16_t *suh, const uint16_t *svh,
+                     int in, int out, int K, float *y);
+/* exact: everything in f64, no fp16 rounding of the input (tools/convert_trunk_enc.py:125-128) */
+void orc_exl3_linear_exact(const float *x, int R, const uint16_t *trellis, const uint16_t *suh, const uint16_t *svh,
+                           int in, int out, int K, double *y);
+
+/* ---- router (kernels/fn_moe.metal:50-131) ---- */
+/* logits[ne] = bf16r(f32(x . rw[e])) when round_bf16 (the reference's default rounding, FC 0 on) */
+void orc_router_logits(const float *x, const uint16_t *rw, int ne, int hid, int round_bf16, float *logits);
+/* top-k by logit (ties -> lower index), weights exp(l - l_max) / sum over the top k, f32 */
+void orc_route(const float *logits, int ne, int topk, uint32_t *ids, float *w);
+
+/* ---- fused MoE layer at R rows (kernels/fn_moe.metal D1-D3, tools/opref.py:417-435) ---- */
+typedef struct {
+  int hid, inter, ne, topk, K;   /* K = routed expert bits */
+  const uint16_t *router;        /* BF16 [ne][hid] */
+  const uint16_t *sgate;         /* BF16 [hid] shared-expert gate row, or NULL (shared weight 1) */
+  /* routed: trellis [ne][in/16][out/16][16K], suh [ne][in], svh [ne][out] */
+  const uint16_t *gt, *ut, *dt, *gsu, *gsv, *usu, *usv, *dsu, *dsv;
+  /* shared expert (NULL = none): same per-projection layout without the expert dim; bits Ks */
+  int Ks;
+  const uint16_t *sgt, *sut, *sdt, *sgsu, *sgsv, *susu, *susv, *sdsu, *sdsv;
+} orc_moe;
+/* kernel arithmetic; y [R][hid] f32; logits [R][ne] (may be NULL); route [R][2 topk] u32 (ids, f32 weight bits,
+ * may be NULL). Returns 0. */
+int orc_moe_layer(const orc_moe *m, const float *x, int R, float *y, float *logits, uint32_t *route);
+/* Same layer given a route (ids + f32 weights [R][2 topk]) and shared gate value per row (sg may be NULL -> 1):
+ * separates the routing decision from the expert math in tests. */
+int orc_moe_experts(const orc_moe *m, const float *x, int R, const uint32_t *route, const float *sg, float *y);
+/* f64 "exact" layer from the same route: no fp16 rounding anywhere, f64 math throughout */
+int orc_moe_experts_exact(const orc_moe *m, const float *x, int R, const uint32_t *route, const float *sg, double *y);
+
+/* ---- CPU baseline (timed in bench.py): the same layer math, OpenMP over slots and column tiles,
+ * a 2^15-entry MCG table instead of the multiply. Returns the number of threads used. ---- */
+int orc_moe_experts_fast(const orc_moe *m, const float *x, int R, const uint32_t *route, const float *sg, float *y,
+                         int nthreads);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

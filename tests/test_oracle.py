@@ -1,0 +1,278 @@
+"""Pins the CPU oracle (oracle/exl3_oracle.c) before it is trusted as the parity reference.
+
+The reference ships no golden vectors for this path and its CPU decoder (exl3_codec) is external. Each oracle
+function is checked here against something it does not share code with: numpy's IEEE fp16 arithmetic, the textbook
+Sylvester Hadamard matrix, a pure-Python walk over the tail-biting ring, the reference's two other trellis readers
+(restated in the oracle from kernels/ne_common.h and kernels/trunk6/trunk6.metal), hand-computed known answers,
+numpy's stable argsort, and an explicit-matrix numpy restatement of the EXL3 linear and the MoE layer.
+"""
+import numpy as np
+import pytest
+
+from ijah_amd import synth
+
+
+# ------------------------------------------------------------------------------------------------ number formats
+def test_f16_conversion_matches_numpy(oracle):
+    L = oracle.lib()
+    rng = np.random.default_rng(1)
+    vals = np.concatenate([rng.standard_normal(4000).astype(np.float32) * 10.0 ** rng.integers(-9, 6, 4000),
+                           np.array([0.0, -0.0, 65504.0, 65519.99, 65520.0, 1e-8, 5.96e-8, 2.98e-8, 6.1e-5, -7.0],
+                                    np.float32)])
+    vals = vals.astype(np.float32)
+    got = np.array([L.orc_f32_to_f16(float(v)) for v in vals], np.uint16)
+    with np.errstate(over="ignore"):
+        want = vals.astype(np.float16).view(np.uint16)
+    assert np.array_equal(got, want)
+    back = np.array([L.orc_f16_to_f32(int(h)) for h in want], np.float32)
+    assert np.array_equal(back, want.view(np.float16).astype(np.float32))
+
+
+def test_bf16_round_known_answers(oracle):
+    L = oracle.lib()
+    # 1 + 2^-8 is a tie between 1 and 1 + 2^-7: even -> 1.0; 1 + 3*2^-8 ties up to 1 + 2^-6 (even mantissa)
+    assert L.orc_bf16r(1.0 + 2 ** -8) == 1.0
+    assert L.orc_bf16r(1.0 + 3 * 2 ** -8) == 1.0 + 2 ** -6
+    assert L.orc_bf16r(1.0 + 2 ** -8 + 2 ** -20) == 1.0 + 2 ** -7
+    assert L.orc_bf16r(-3.0) == -3.0
+
+
+# ------------------------------------------------------------------------------------------------ codebook
+def test_mcg_known_answers(oracle):
+    # cw 0: r = 0x3B603B60, both halves 0x3B60 = 0.921875 -> 1.84375 = fp16 0x3F60
+    assert oracle.mcg(0) == 0x3F60
+    # bit 15 is ignored (window 15)
+    assert oracle.mcg(0x8000) == oracle.mcg(0)
+    # cw 1: r = 0xCBAC1FED & 0x8FFF8FFF ^ 0x3B603B60 = 0xB0CC348D -> fp16(0x348D) + fp16(0xB0CC)
+    r = (0xCBAC1FED & 0x8FFF8FFF) ^ 0x3B603B60
+    assert r == 0xB0CC348D
+    lo = np.array([0x348D], np.uint16).view(np.float16)[0]
+    hi = np.array([0xB0CC], np.uint16).view(np.float16)[0]
+    assert oracle.mcg(1) == np.array([np.float16(lo + hi)]).view(np.uint16)[0]
+
+
+def test_mcg_table_vs_numpy(oracle):
+    """All 2^15 codewords against numpy's uint32 wrap-around multiply and fp16 add."""
+    cw = np.arange(1 << 15, dtype=np.uint32)
+    r = ((cw * np.uint32(0xCBAC1FED)) & np.uint32(0x8FFF8FFF)) ^ np.uint32(0x3B603B60)
+    h = r.view(np.uint16).reshape(-1, 2).view(np.float16)
+    want = (h[:, 0] + h[:, 1]).astype(np.float16).view(np.uint16)
+    got = oracle.mcg_table()
+    assert np.array_equal(got, want)
+    v = got.view(np.float16).astype(np.float64)
+    # both halves lie in +-[2^-3, 2^1): every value is finite and below 4 in magnitude
+    assert np.isfinite(v).all() and np.abs(v).max() < 4.0
+    # the codebook is a zero-mean, unit-scale Gaussian proxy
+    assert abs(v.mean()) < 0.05 and 0.8 < v.std() < 1.3
+
+
+# ------------------------------------------------------------------------------------------------ trellis readers
+def py_ring_codewords(tile, K):
+    """Pure-Python walk over the ring (the definition, independent of the C code)."""
+    words = [int(tile[2 * w]) | (int(tile[2 * w + 1]) << 16) for w in range(8 * K)]
+    bits = []
+    for w in words:
+        bits.extend((w >> (31 - b)) & 1 for b in range(32))
+    tot = 256 * K
+    out = []
+    for i in range(256):
+        end = (i + 1) * K
+        v = 0
+        for p in range(end - 15, end):
+            v = (v << 1) | bits[p % tot]
+        out.append(v)
+    return np.array(out, np.uint16)
+
+
+@pytest.mark.parametrize("K", range(1, 9))
+def test_readers_agree(oracle, K):
+    rng = np.random.default_rng(100 + K)
+    for t in range(25):
+        tile = rng.integers(0, 1 << 16, 16 * K, dtype=np.uint16)
+        ring = oracle.tile_cw(tile, K, "ring") & 0x7FFF
+        assert np.array_equal(ring, oracle.tile_cw(tile, K, "t6") & 0x7FFF)
+        if 4 <= K <= 6:
+            assert np.array_equal(ring, oracle.tile_cw(tile, K, "lane") & 0x7FFF)
+        if t < 2:
+            assert np.array_equal(ring, py_ring_codewords(tile, K))
+
+
+@pytest.mark.parametrize("K", [4, 5, 8])
+def test_constant_tiles(oracle, K):
+    zeros = np.zeros(16 * K, np.uint16)
+    ones = np.full(16 * K, 0xFFFF, np.uint16)
+    assert (oracle.tile_cw(zeros, K) & 0x7FFF == 0).all()
+    assert (oracle.tile_cw(ones, K) & 0x7FFF == 0x7FFF).all()
+    w = oracle.decode(zeros.reshape(1, 1, -1))
+    assert (w.view(np.uint16) == 0x3F60).all()
+
+
+def test_single_bit_moves_expected_codewords(oracle):
+    """A single set bit at ring position p appears in exactly the codewords whose 15-bit window covers p."""
+    K = 5
+    for p in (0, 7, 31, 32, 639, 1279):
+        tile = np.zeros(16 * K, np.uint16)
+        w, b = divmod(p, 32)
+        word = 1 << (31 - b)
+        tile[2 * w] = word & 0xFFFF
+        tile[2 * w + 1] = word >> 16
+        cw = oracle.tile_cw(tile, K) & 0x7FFF
+        for i in range(256):
+            end = (i + 1) * K
+            covered = [(end - 15 + t) % (256 * K) for t in range(15)]
+            want = (1 << (14 - covered.index(p))) if p in covered else 0
+            assert cw[i] == want, (p, i)
+
+
+def test_slot_map_is_a_bijection_with_reference_rows(oracle):
+    seen = set()
+    for s in range(256):
+        r, c = oracle.slot_rc(s)
+        l, j = s >> 3, s & 7
+        q = l & 3
+        assert r == [2 * q, 2 * q + 1, 2 * q + 8, 2 * q + 9][j & 3]
+        assert c == (l >> 2) + 8 * (j >> 2)
+        seen.add((r, c))
+    assert len(seen) == 256
+
+
+def test_decode_matrix_tiles(oracle):
+    rng = np.random.default_rng(3)
+    K = 6
+    t = rng.integers(0, 1 << 16, (3, 2, 16 * K), dtype=np.uint16)
+    w = oracle.decode(t).view(np.uint16)
+    table = oracle.mcg_table()
+    for tk in range(3):
+        for tn in range(2):
+            cw = py_ring_codewords(t[tk, tn], K)
+            for s in range(0, 256, 37):
+                r, c = oracle.slot_rc(s)
+                assert w[16 * tk + r, 16 * tn + c] == table[cw[s]]
+
+
+# ------------------------------------------------------------------------------------------------ Hadamard
+def sylvester(n):
+    i = np.arange(n)
+    x = i[:, None] & i[None, :]
+    pc = np.zeros((n, n), np.int64)
+    while x.any():
+        pc += x & 1
+        x = x >> 1
+    return np.where(pc % 2 == 0, 1.0, -1.0) / np.sqrt(n)
+
+
+@pytest.mark.parametrize("n,had", [(128, 128), (512, 128), (320, 64), (48, 16), (96, 32)])
+def test_fwht_matches_sylvester(oracle, n, had):
+    assert oracle.had_size(n) == had
+    rng = np.random.default_rng(n)
+    v = rng.standard_normal(n)
+    H = sylvester(had)
+    want = (v.reshape(-1, had) @ H).reshape(-1)
+    assert np.allclose(oracle.fwht(v, had, f64=True), want, rtol=0, atol=1e-12)
+    assert np.allclose(oracle.fwht(v.astype(np.float32), had), want, rtol=0, atol=1e-5)
+
+
+# ------------------------------------------------------------------------------------------------ linear
+def np_linear_exact(oracle, x, t, suh, svh):
+    """x @ (diag(suh) H_in W' H_out diag(svh)) with explicit matrices (tools/convert_trunk_enc.py:125-128)."""
+    w = oracle.decode(t).astype(np.float64)
+    k, m = w.shape
+    hk, hm = oracle.had_size(k), oracle.had_size(m)
+    Hk = np.kron(np.eye(k // hk), sylvester(hk))
+    Hm = np.kron(np.eye(m // hm), sylvester(hm))
+    W = np.diag(suh.astype(np.float64)) @ Hk @ w @ Hm @ np.diag(svh.astype(np.float64))
+    return x.astype(np.float64) @ W
+
+
+@pytest.mark.parametrize("inp,out,K", [(256, 128, 5), (128, 320, 6), (512, 256, 8), (128, 128, 4)])
+def test_linear_vs_explicit_matrices(oracle, inp, out, K):
+    rng = np.random.default_rng(inp + out + K)
+    t, su, sv = synth.linear(rng, inp, out, K)
+    x = synth.bf16_values(rng, 3, inp)
+    want = np_linear_exact(oracle, x, t, su, sv)
+    exact = oracle.exl3_linear(x, t, su, sv, exact=True)
+    assert np.allclose(exact, want, rtol=1e-12, atol=1e-9)
+    emul = oracle.exl3_linear(x, t, su, sv)
+    rel = np.linalg.norm(emul - want) / np.linalg.norm(want)
+    assert rel < 2e-3  # the fp16 input preparation (reference docs/trunk6.md:74-84: ~3e-4)
+
+
+# ------------------------------------------------------------------------------------------------ router
+def test_route_ties_and_order(oracle):
+    rng = np.random.default_rng(5)
+    for trial in range(50):
+        lg = (np.round(rng.standard_normal(64) * 4) / 4).astype(np.float32)  # many ties
+        ids, w = oracle.route(lg, 10)
+        want = np.argsort(-lg, kind="stable")[:10]
+        assert np.array_equal(ids, want)
+        top = lg[want]
+        e = np.exp((top - top[0]).astype(np.float32))
+        assert np.allclose(w, e / e.sum(), rtol=1e-6)
+        assert abs(w.sum() - 1) < 1e-5
+
+
+def test_router_logits(oracle):
+    rng = np.random.default_rng(6)
+    x = synth.bf16_values(rng, 256)
+    rw = synth.bf16(rng.standard_normal((32, 256)).astype(np.float32) / 16)
+    lg = oracle.router_logits(x, rw)
+    want = x.astype(np.float64) @ ((rw.astype(np.uint32) << 16).view(np.float32).astype(np.float64)).T
+    assert np.allclose(lg, want, rtol=1e-2, atol=1e-6)
+    assert np.array_equal(synth.bf16(lg), (lg.view(np.uint32) >> 16).astype(np.uint16))  # bf16-representable
+
+
+# ------------------------------------------------------------------------------------------------ MoE layer
+def np_moe_exact(oracle, W, x, route, sg):
+    """Explicit-matrix restatement of one MoE row set: tools/opref.py:417-435 (+ the shared expert)."""
+    hid, inter, topk = W.d["hid"], W.d["inter"], W.d["topk"]
+
+    def mat(t, su, sv):
+        w = oracle.decode(t).astype(np.float64)
+        k, m = w.shape
+        Hk = np.kron(np.eye(k // oracle.had_size(k)), sylvester(oracle.had_size(k)))
+        Hm = np.kron(np.eye(m // oracle.had_size(m)), sylvester(oracle.had_size(m)))
+        return np.diag(su.astype(np.float64)) @ Hk @ w @ Hm @ np.diag(sv.astype(np.float64))
+
+    def expert(mats, xr):
+        g, u = xr @ mats[0], xr @ mats[1]
+        return (g / (1 + np.exp(-g)) * u) @ mats[2]
+
+    d = W.d
+    y = np.zeros((x.shape[0], hid))
+    for r in range(x.shape[0]):
+        xr = x[r].astype(np.float64)
+        for k in range(topk):
+            e = int(route[r, k])
+            wk = route[r, topk + k:topk + k + 1].view(np.float32)[0]
+            mats = [mat(d[f"{p}.trellis"][e], d[f"{p}.suh"][e], d[f"{p}.svh"][e]) for p in ("gate", "up", "down")]
+            y[r] += wk * expert(mats, xr)
+        if "sgate_proj.trellis" in d:
+            mats = [mat(d[f"{p}.trellis"], d[f"{p}.suh"], d[f"{p}.svh"]) for p in ("sgate_proj", "sup_proj",
+                                                                                    "sdown_proj")]
+            y[r] += (1.0 if sg is None else sg[r]) * expert(mats, xr)
+    return y
+
+
+@pytest.mark.parametrize("shared,sgate", [(True, False), (False, False), (True, True)])
+def test_moe_layer_vs_explicit(oracle, shared, sgate):
+    w = synth.moe_layer(11, hid=256, inter=128, ne=16, topk=4, K=5, shared=shared, Ks=6, sgate=sgate)
+    W = oracle.MoeWeights(w)
+    rng = np.random.default_rng(12)
+    x = synth.bf16_values(rng, 2, 256)
+    y, lg, rt = oracle.moe_layer(W, x)
+    for r in range(2):
+        ids, wt = oracle.route(lg[r], 4)
+        assert np.array_equal(rt[r, :4], ids)
+        assert np.array_equal(rt[r, 4:].view(np.float32), wt)
+    sg = None
+    if sgate:
+        l = np.array([oracle.router_logits(x[r], w["sgate"][None]) for r in range(2)]).reshape(-1)
+        sg = 1 / (1 + np.exp(-l.astype(np.float32)))
+    want = np_moe_exact(oracle, W, x, rt, sg)
+    exact = oracle.moe_experts(W, x, rt, sg=sg, exact=True)
+    assert np.allclose(exact, want, rtol=1e-9, atol=1e-9 * np.abs(want).max())
+    rel = np.linalg.norm(y - want) / np.linalg.norm(want)
+    assert rel < 5e-3
+    fast, used = oracle.moe_experts(W, x, rt, sg=sg, fast_threads=2)
+    assert used >= 1
+    assert np.linalg.norm(fast - y) / np.linalg.norm(y) < 1e-5
