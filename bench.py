@@ -88,8 +88,9 @@ def main():
     from ijah_amd import synth
     x = synth.bf16_values(np.random.default_rng(a.seed), 1, HID)
     xb = eng.from_numpy(x)
-    for m in layers:  # eager pass: routes resident, byte counts
-        m.run_bufs(1, xb, eng.alloc(HID * 4))
+    ybufs = [eng.alloc(HID * 4) for _ in layers]
+    for m, yb in zip(layers, ybufs):  # eager pass: routes resident, byte counts
+        m.run_bufs(1, xb, yb)
     eng.sync()
     layer_bytes = [m.bytes(1) for m in layers]
     bytes_per_layer = float(np.mean(layer_bytes))

@@ -297,6 +297,7 @@ class MoeLayer:
         xb, yb = self.eng.from_numpy(x), self.eng.alloc(R * self.hid * 4)
         self.run_bufs(R, xb, yb)
         self._R = R
+        self._io = (xb, yb)  # "mlp_out" reads the last output buffer: keep it alive
         return yb.download(np.float32, (R, self.hid))
 
     def read(self, name, R=None):
