@@ -213,23 +213,24 @@ NE_API int ne_exl3_lin_decode(ne_exl3_lin *l, ne_buf *w, double *gpu_ms) {
 
 // ---------------------------------------------------------------------------------------------------- MoE layer
 struct ne_moe {
-  int hid = 0, inter = 0, ne = 0, topk = 0, K = 0, Ks = 0, has_shared = 0, has_sgate = 0, ksplit = 2;
+  int hid = 0, inter = 0, ne = 0, topk = 0, K = 0, Ks = 0, has_shared = 0, has_sgate = 0, ksplit = 4;
   ExpertLayout lay, slay;
   uint8_t *experts = nullptr, *shared = nullptr;
   uint16_t *router = nullptr;  // [ne + has_sgate][hid]
   int Rcap = 0;
   float *logits = nullptr, *sgv = nullptr, *guo = nullptr, *dn = nullptr;
-  uint32_t *route = nullptr, *ctr = nullptr;
+  uint32_t *route = nullptr, *sync = nullptr;
+  bool fused = true;  // one persistent launch per step (IJAH_MOE_PATH=staged: four launches)
   int last_R = 0;
   float *last_y = nullptr;
   ~ne_moe() {
-    for (void *p : std::initializer_list<void *>{experts, shared, router, logits, sgv, guo, dn, route, ctr})
+    for (void *p : std::initializer_list<void *>{experts, shared, router, logits, sgv, guo, dn, route, sync})
       dev_free(p);
   }
   int nslot() const { return topk + has_shared; }
   void ensure_scratch(int R) {
     if (R <= Rcap) return;
-    for (void *p : std::initializer_list<void *>{logits, sgv, guo, dn, route}) dev_free(p);
+    for (void *p : std::initializer_list<void *>{logits, sgv, guo, dn, route, sync}) dev_free(p);
     const size_t S = (size_t)R * nslot();
     logits = dev_alloc<float>((size_t)R * (ne + 1));
     sgv = dev_alloc<float>(R);
@@ -237,6 +238,8 @@ struct ne_moe {
     dn = dev_alloc<float>(S * hid);
     route = dev_alloc<uint32_t>((size_t)R * 2 * topk);
     IJ_HIP(hipMemset(route, 0, sizeof(uint32_t) * R * 2 * topk));
+    sync = dev_alloc<uint32_t>(sync_words(R, nslot(), hid));
+    IJ_HIP(hipMemset(sync, 0, 4 * sync_words(R, nslot(), hid)));
     Rcap = R;
   }
   MoeArgs args(int R, const float *x, float *y) const {
@@ -265,11 +268,26 @@ struct ne_moe {
     a.sgv = sgv;
     a.guo = guo;
     a.dn = dn;
-    a.ctr = ctr;
+    a.sync = sync;
     return a;
+  }
+  // a failed cross-workgroup wait leaves the error word set: report it and clear the counters
+  void check_sync(hipStream_t s) {
+    uint32_t err = 0;
+    IJ_HIP(hipMemcpyAsync(&err, sync + kSyncErrWord, 4, hipMemcpyDeviceToHost, s));
+    IJ_HIP(hipStreamSynchronize(s));
+    if (err) {
+      IJ_HIP(hipMemsetAsync(sync, 0, 4 * sync_words(Rcap, nslot(), hid), s));
+      IJ_HIP(hipStreamSynchronize(s));
+      throw Error("moe: a cross-workgroup wait timed out (layer output invalid)");
+    }
   }
   void launch(int R, const float *x, float *y, hipStream_t s) const {
     const MoeArgs a = args(R, x, y);
+    if (fused && moe_fused_supported(K, has_shared ? Ks : K)) {
+      launch_moe_fused(a, 0, s);
+      return;
+    }
     launch_moe_router(a, s);
     launch_moe_gateup(a, s);
     launch_moe_down(a, s);
@@ -351,8 +369,7 @@ ne_moe *moe_create(const ne_moe_desc &d) {
   m->router = dev_alloc<uint16_t>(rrows * d.hid);
   IJ_HIP(hipMemcpy(m->router, d.router, 2u * d.ne * d.hid, hipMemcpyHostToDevice));
   if (m->has_sgate) IJ_HIP(hipMemcpy(m->router + (size_t)d.ne * d.hid, d.sgate, 2u * d.hid, hipMemcpyHostToDevice));
-  m->ctr = dev_alloc<uint32_t>(1);
-  IJ_HIP(hipMemset(m->ctr, 0, 4));
+  if (const char *e = getenv("IJAH_MOE_PATH")) m->fused = strcmp(e, "staged") != 0;
   if (const char *e = getenv("IJAH_MOE_KSPLIT")) m->ksplit = std::max(1, atoi(e));
   IJ_CHECK((d.hid / 16) % m->ksplit == 0 && ((d.hid / 16) / m->ksplit) % 8 == 0, "ksplit %d does not divide hid %d",
            m->ksplit, d.hid);
@@ -461,8 +478,7 @@ NE_API ne_moe *ne_moe_synth(int hid, int inter, int ne, int topk, int K, int has
     }
     m->router = dev_alloc<uint16_t>((size_t)ne * hid);
     launch_fill_normal_bf16(m->router, (size_t)ne * hid, seed * 7 + 5, (float)(1.0 / std::sqrt((double)hid)), s);
-    m->ctr = dev_alloc<uint32_t>(1);
-    IJ_HIP(hipMemsetAsync(m->ctr, 0, 4, s));
+    if (const char *e = getenv("IJAH_MOE_PATH")) m->fused = strcmp(e, "staged") != 0;
     if (const char *e = getenv("IJAH_MOE_KSPLIT")) m->ksplit = std::max(1, atoi(e));
     IJ_CHECK((hid / 16) % m->ksplit == 0 && ((hid / 16) / m->ksplit) % 8 == 0, "ksplit %d does not divide hid %d",
              m->ksplit, hid);
@@ -505,6 +521,7 @@ NE_API int ne_moe_run(ne_moe *m, int R, const ne_buf *x, uint64_t x_off, ne_buf 
     timed(stream(), gpu_ms, [&] { m->launch(R, xp, yp, stream()); });
     m->last_R = R;
     m->last_y = yp;
+    if (gpu_ms) m->check_sync(stream());
   });
 }
 
@@ -620,6 +637,7 @@ NE_API int ne_moe_time(ne_moe *const *layers, int n, int R, const ne_buf *x, int
         for (int i = 0; i < reps; i++) IJ_HIP(hipGraphLaunch(ge, s));
       });
       *us_per_layer = ms * 1000.0 / ((double)reps * n);
+      for (int i = 0; i < n; i++) layers[i]->check_sync(s);
       for (int i = 0; i < n; i++) {
         layers[i]->last_R = R;
         layers[i]->last_y = nullptr;
@@ -636,7 +654,7 @@ NE_API int ne_moe_time_kernels(ne_moe *const *layers, int n, int R, const ne_buf
                                double *us, int *n_kinds) {
   return c_call([&] {
     IJ_CHECK(layers && n >= 1 && x && us && n_kinds && names && reps >= 1, "bad arguments");
-    IJ_CHECK(*n_kinds >= 4, "need room for 4 kernel kinds");
+    IJ_CHECK(*n_kinds >= 5, "need room for 5 kernel kinds");
     const int hid = layers[0]->hid;
     IJ_CHECK((uint64_t)R * hid * 4 <= x->size, "x buffer too small");
     hipStream_t s = stream();
@@ -648,11 +666,14 @@ NE_API int ne_moe_time_kernels(ne_moe *const *layers, int n, int R, const ne_buf
       a.push_back(layers[i]->args(R, xp, ys + (size_t)i * R * hid));
       layers[i]->launch(R, xp, ys + (size_t)i * R * hid, s);
     }
-    void (*fns[4])(const MoeArgs &, hipStream_t) = {launch_moe_router, launch_moe_gateup, launch_moe_down,
-                                                    launch_moe_combine};
-    const char *nm[4] = {"router", "gateup", "down", "combine"};
+    auto fused = [](const MoeArgs &x, hipStream_t st) { launch_moe_fused(x, 0, st); };
+    void (*fns[5])(const MoeArgs &, hipStream_t) = {launch_moe_router, launch_moe_gateup, launch_moe_down,
+                                                    launch_moe_combine, fused};
+    const char *nm[5] = {"router", "gateup", "down", "combine", "fused"};
+    const int KS = layers[0]->has_shared ? layers[0]->Ks : layers[0]->K;
+    const int kinds = moe_fused_supported(layers[0]->K, KS) ? 5 : 4;
     try {
-      for (int k = 0; k < 4; k++) {
+      for (int k = 0; k < kinds; k++) {
         double ms = 0;
         timed(s, &ms, [&] {
           for (int r = 0; r < reps; r++)
@@ -667,7 +688,8 @@ NE_API int ne_moe_time_kernels(ne_moe *const *layers, int n, int R, const ne_buf
     }
     IJ_HIP(hipStreamSynchronize(s));
     dev_free(ys);
-    *n_kinds = 4;
+    for (int i = 0; i < n; i++) layers[i]->check_sync(s);
+    *n_kinds = kinds;
   });
 }
 

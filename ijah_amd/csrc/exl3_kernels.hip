@@ -19,6 +19,7 @@
 // bit-identical to the reference arithmetic. The library is compiled with -ffp-contract=off for that reason.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 
@@ -105,11 +106,30 @@ __device__ __forceinline__ TileWords load_tile(const uint32_t *__restrict__ T, c
   return w;
 }
 
-// MCG window-15 codebook (reference kernels/ne_common.h:139-144); half + half rounds once (RNE) like the reference.
-__device__ __forceinline__ _Float16 mcg(uint32_t cw) {
-  const uint32_t r = ((cw * 0xCBAC1FEDu) & 0x8FFF8FFFu) ^ 0x3B603B60u;
-  const f16x2 h = __builtin_bit_cast(f16x2, r);
-  return h.x + h.y;
+// MCG window-15 codebook (reference kernels/ne_common.h:139-144): r = cw * 0xCBAC1FED mod 2^32, masked, xored;
+// value = fp16(r_lo) + fp16(r_hi) rounded once (RNE), as the reference's half + half.
+// The 32-bit multiply is quarter rate on CDNA; cw < 2^15 lets two full-rate 24-bit multiplies form it:
+// v_mul_u32_u24 (SDWA, dst WORD_1) writes lo16(cw * 0xCBAC) << 16, v_mad_u32_u24 adds cw * 0x1FED.
+__device__ __forceinline__ uint32_t mcg_bits(uint32_t cw) {
+  uint32_t t, r;
+  asm("v_mul_u32_u24_sdwa %0, %1, %2 dst_sel:WORD_1 dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:DWORD"
+      : "=v"(t)
+      : "v"(cw), "s"(0xCBACu));
+  asm("v_mad_u32_u24 %0, %1, %2, %3" : "=v"(r) : "v"(cw), "s"(0x1FEDu), "v"(t));
+  return (r & 0x8FFF8FFFu) ^ 0x3B603B60u;
+}
+// two codewords -> their fp16 values packed (c0 low, c1 high): each v_add_f16 (SDWA) adds the two halves of one r
+// and writes one half of the result, so no pack instruction is needed.
+__device__ __forceinline__ f16x2 mcg_pair(uint32_t c0, uint32_t c1) {
+  const uint32_t r0 = mcg_bits(c0), r1 = mcg_bits(c1);
+  uint32_t d;
+  asm("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1"
+      : "=v"(d)
+      : "v"(r0));
+  asm("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0 src1_sel:WORD_1"
+      : "+v"(d)
+      : "v"(r1));
+  return __builtin_bit_cast(f16x2, d);
 }
 
 // The lane's four weights: a = rows (2q, 2q+1), b = rows (2q+8, 2q+9) of its column.
@@ -128,8 +148,8 @@ __device__ __forceinline__ void decode4(const TileWords &w, uint32_t sh, f16x2 &
       c[i] = (s >= 32 ? (hi >> (s - 32)) : __builtin_amdgcn_alignbit(hi, lo, (uint32_t)s)) & 0x7FFFu;
     }
   }
-  a = f16x2{mcg(c[0]), mcg(c[1])};
-  b = f16x2{mcg(c[2]), mcg(c[3])};
+  a = mcg_pair(c[0], c[1]);
+  b = mcg_pair(c[2], c[3]);
 }
 
 __device__ __forceinline__ float dot4(f16x2 a, f16x2 b, f16x4 x, float acc) {
@@ -162,34 +182,66 @@ ExpertLayout expert_layout(int hid, int inter, int K) {
 }
 
 // ------------------------------------------------------------------------------------------------ shared GEMV core
-// One workgroup (4 waves) multiplies the LDS-staged prepared input span (fp16, kp order, `xs` = rows [16*tk0, ...))
-// with output tiles (2p, 2p+1) over k tiles [k0, k1) of a re-laid matrix; waves stride k by 4. Returns per lane the
-// partial sums of its column for the two tiles, reduced over the four lanes sharing the column.
+// A workgroup (4 waves) multiplies the LDS-staged prepared input (fp16, kp order; xs[0] = input row 16*k0) with
+// output tiles (2p, 2p+1) over k tiles [k0, k1) of a re-laid matrix; wave w takes k tiles k0 + w + 4j. The tile words
+// of up to kPrefetch iterations are loaded into registers in one batch (pair_load) so that their HBM latency overlaps
+// the caller's input preparation; pair_dot then decodes and accumulates. Per lane: partial sums of its column for the
+// two tiles, reduced over the four lanes sharing the column.
+constexpr int kPrefetch = 8;
 template <int K>
-__device__ __forceinline__ void pair_gemv(const uint32_t *__restrict__ tiles, int IT, int p, int k0, int k1,
-                                          const _Float16 *xs, float &acc0, float &acc1) {
+struct PairBuf {
+  TileWords w[kPrefetch][2];
+};
+template <int K>
+__device__ __forceinline__ void pair_load(PairBuf<K> &b, const uint32_t *__restrict__ pair_base, const TileLane<K> &L,
+                                          int tk0, int k1) {
   constexpr int TW = 8 * K;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const TileLane<K> L = tile_lane<K>((uint32_t)lane);
-  const int q = (lane >> 1) & 3;
-  acc0 = 0.f;
-  acc1 = 0.f;
-  const uint32_t *base = tiles + (uint64_t)p * IT * 2 * TW;
-#pragma unroll 4
-  for (int tk = k0 + wave; tk < k1; tk += 4) {
-    const uint32_t *T0 = base + (uint64_t)tk * 2 * TW;
-    const TileWords wa = load_tile<K>(T0, L), wb = load_tile<K>(T0 + TW, L);
-    const f16x4 xv = *(const f16x4 *)(xs + (tk - k0) * 16 + 4 * q);
-    f16x2 a0, b0, a1, b1;
-    decode4<K>(wa, L.sh, a0, b0);
-    decode4<K>(wb, L.sh, a1, b1);
-    acc0 = dot4(a0, b0, xv, acc0);
-    acc1 = dot4(a1, b1, xv, acc1);
+#pragma unroll
+  for (int j = 0; j < kPrefetch; j++) {
+    const int tk = tk0 + 4 * j;
+    if (tk < k1) {
+      const uint32_t *T0 = pair_base + (uint64_t)tk * 2 * TW;
+      b.w[j][0] = load_tile<K>(T0, L);
+      b.w[j][1] = load_tile<K>(T0 + TW, L);
+    }
   }
+}
+template <int K>
+__device__ __forceinline__ void pair_dot(const PairBuf<K> &b, const TileLane<K> &L, int tk0, int k0, int k1,
+                                         const _Float16 *xs, float &acc0, float &acc1) {
+  const int q = ((threadIdx.x & 63) >> 1) & 3;
+#pragma unroll
+  for (int j = 0; j < kPrefetch; j++) {
+    const int tk = tk0 + 4 * j;
+    if (tk < k1) {
+      const f16x4 xv = *(const f16x4 *)(xs + (tk - k0) * 16 + 4 * q);
+      f16x2 a0, b0, a1, b1;
+      decode4<K>(b.w[j][0], L.sh, a0, b0);
+      decode4<K>(b.w[j][1], L.sh, a1, b1);
+      acc0 = dot4(a0, b0, xv, acc0);
+      acc1 = dot4(a1, b1, xv, acc1);
+    }
+  }
+}
+__device__ __forceinline__ void lane_col_reduce(float &acc0, float &acc1) {
   acc0 += __shfl_xor(acc0, 2, 64);
   acc0 += __shfl_xor(acc0, 4, 64);
   acc1 += __shfl_xor(acc1, 2, 64);
   acc1 += __shfl_xor(acc1, 4, 64);
+}
+// The whole pair GEMV for spans beyond one prefetch batch; `b` already holds the first batch (loaded by the caller
+// before its prologue).
+template <int K>
+__device__ __forceinline__ void pair_gemv(PairBuf<K> &b, const uint32_t *__restrict__ pair_base, const TileLane<K> &L,
+                                          int k0, int k1, const _Float16 *xs, float &acc0, float &acc1) {
+  const int tkw = k0 + (int)(threadIdx.x >> 6);
+  acc0 = 0.f;
+  acc1 = 0.f;
+  for (int tk0 = tkw; tk0 < k1; tk0 += 4 * kPrefetch) {
+    if (tk0 != tkw) pair_load<K>(b, pair_base, L, tk0, k1);
+    pair_dot<K>(b, L, tk0, k0, k1, xs, acc0, acc1);
+  }
+  lane_col_reduce(acc0, acc1);
 }
 
 // sums the 4 waves' column partials in a fixed order; result on threads 0..31 (column 32p + tid)
@@ -227,87 +279,55 @@ __device__ __forceinline__ float pair_reduce(float acc0, float acc1, float *red)
 constexpr int kMaxExperts = 1024;
 constexpr int kMaxTopk = 32;
 
-__global__ __launch_bounds__(256) void moe_router(MoeArgs a) {
-  __shared__ float lv[kMaxExperts];
-  __shared__ uint32_t sid[kMaxTopk];
-  __shared__ float sval[kMaxTopk];
-  __shared__ int last;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int nrows = a.ne + a.has_sgate;
-  const int row = blockIdx.x * 4 + wave;
-  const int ld = a.ne + 1;
-  if (row < nrows) {
-    const uint16_t *w = a.router + (uint64_t)row * a.hid;
-    for (int r = 0; r < a.R; r++) {
-      const float *x = a.x + (uint64_t)r * a.hid;
-      float acc = 0.f;
-      for (int c = lane; c * 8 < a.hid; c += 64) {
-        const uint4 wv = *(const uint4 *)(w + c * 8);
-        const float4 x0 = *(const float4 *)(x + c * 8), x1 = *(const float4 *)(x + c * 8 + 4);
-        acc = fmaf(x0.x, bf16_f32(wv.x & 0xFFFFu), acc);
-        acc = fmaf(x0.y, bf16_f32(wv.x >> 16), acc);
-        acc = fmaf(x0.z, bf16_f32(wv.y & 0xFFFFu), acc);
-        acc = fmaf(x0.w, bf16_f32(wv.y >> 16), acc);
-        acc = fmaf(x1.x, bf16_f32(wv.z & 0xFFFFu), acc);
-        acc = fmaf(x1.y, bf16_f32(wv.z >> 16), acc);
-        acc = fmaf(x1.z, bf16_f32(wv.w & 0xFFFFu), acc);
-        acc = fmaf(x1.w, bf16_f32(wv.w >> 16), acc);
-      }
-#pragma unroll
-      for (int o = 32; o >= 1; o >>= 1) acc += __shfl_xor(acc, o, 64);
-      if (lane == 0) a.logits[(uint64_t)r * ld + row] = bf16_round(acc);
-    }
-  }
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) last = (atomicAdd(a.ctr, 1u) == gridDim.x - 1u) ? 1 : 0;
-  __syncthreads();
-  if (!last) return;
-  __threadfence();
-  for (int r = 0; r < a.R; r++) {
-    for (int i = threadIdx.x; i < a.ne; i += blockDim.x) {
-      const float v = __hip_atomic_load(a.logits + (uint64_t)r * ld + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      lv[i] = (v != v) ? -INFINITY : v;
-    }
-    __syncthreads();
-    for (int i = threadIdx.x; i < a.ne; i += blockDim.x) {
-      const float v = lv[i];
-      int rank = 0;
-      for (int j = 0; j < a.ne; j++) {
-        const float u = lv[j];
-        rank += (u > v) || (u == v && j < i);
-      }
-      if (rank < a.topk) {
-        sid[rank] = (uint32_t)i;
-        sval[rank] = v;
-      }
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      float pr[kMaxTopk];
-      const float top = sval[0];
-      float s = 0.f;
-      for (int k = 0; k < a.topk; k++) {
-        pr[k] = expf(sval[k] - top);
-        s += pr[k];
-      }
-      uint32_t *rt = a.route + (uint64_t)r * 2 * a.topk;
-      for (int k = 0; k < a.topk; k++) {
-        rt[k] = sid[k];
-        rt[a.topk + k] = __float_as_uint(pr[k] / s);
-      }
-      float g = 1.f;
-      if (a.has_sgate) {
-        const float l = __hip_atomic_load(a.logits + (uint64_t)r * ld + a.ne, __ATOMIC_RELAXED,
-                                          __HIP_MEMORY_SCOPE_AGENT);
-        g = 1.f / (1.f + expf(-l));
-      }
-      a.sgv[r] = g;
-    }
-    __syncthreads();
-  }
-  if (threadIdx.x == 0) atomicExch(a.ctr, 0u);
+// ------------------------------------------------------------------------------------------------ top-k
+// Wave-wide max of a u32 (DPP within rows of 16, then the 4 rows' maxima through readlane): uniform result.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));   // quad_perm 1,0,3,2
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));   // quad_perm 2,3,0,1
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false));  // row_half_mirror
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false));  // row_mirror
+  const uint32_t a = __builtin_amdgcn_readlane(v, 0), b = __builtin_amdgcn_readlane(v, 16);
+  const uint32_t c = __builtin_amdgcn_readlane(v, 32), d = __builtin_amdgcn_readlane(v, 48);
+  return max(max(a, b), max(c, d));
 }
+// Order key of a bf16-valued logit and its index: a larger key is a larger logit, equal logits order the lower index
+// first (the reference's tie rule, kernels/fn_moe.metal:84,105). NaN ranks as -inf, -0 as +0. Zero is below every key.
+__device__ __forceinline__ uint32_t topk_key(float v, int i) {
+  if (v != v) v = -INFINITY;
+  if (v == 0.f) v = 0.f;
+  uint32_t u = __float_as_uint(v);
+  u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return (u & 0xFFFF0000u) | (0xFFFFu - (uint32_t)i);
+}
+// Top-k of lv[0..ne) (bf16-valued, ne <= 1024, k <= 32) by a 256-thread block: each wave takes the top k of its
+// quarter by k rounds of wave max; wave 0 merges the 4 k candidates the same way. ids land in sid[0..k) in order.
+__device__ void block_topk(const float *lv, int ne, int k, uint32_t *cand, uint32_t *sid) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  uint32_t key[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const int i = (wave * 4 + j) * 64 + lane;
+    key[j] = i < ne ? topk_key(lv[i], i) : 0u;
+  }
+  for (int t = 0; t < k; t++) {
+    const uint32_t m = wave_max_u32(max(max(key[0], key[1]), max(key[2], key[3])));
+    if (lane == 0) cand[wave * k + t] = m;
+#pragma unroll
+    for (int j = 0; j < 4; j++) key[j] = key[j] == m ? 0u : key[j];
+  }
+  __syncthreads();
+  if (wave == 0) {
+    uint32_t c0 = lane < 4 * k ? cand[lane] : 0u, c1 = lane + 64 < 4 * k ? cand[lane + 64] : 0u;
+    for (int t = 0; t < k; t++) {
+      const uint32_t m = wave_max_u32(max(c0, c1));
+      if (lane == 0) sid[t] = 0xFFFFu - (m & 0xFFFFu);
+      c0 = c0 == m ? 0u : c0;
+      c1 = c1 == m ? 0u : c1;
+    }
+  }
+  __syncthreads();
+}
+
 
 // slot (row r, k): routed expert route[r][k] (ids past ne clamp to 0, as the reference masks with NE - 1) or the
 // shared expert (k == topk). Offsets are picked as scalars so no layout struct is copied to scratch.
@@ -334,16 +354,138 @@ __device__ __forceinline__ uint64_t off_tr(const MoeArgs &a, int sh, int p) { re
 __device__ __forceinline__ uint64_t off_su(const MoeArgs &a, int sh, int p) { return sh ? a.slay.su[p] : a.lay.su[p]; }
 __device__ __forceinline__ uint64_t off_sv(const MoeArgs &a, int sh, int p) { return sh ? a.slay.sv[p] : a.lay.sv[p]; }
 
+// ------------------------------------------------------------------------------------------------ cross-workgroup sync
+// Counters live in a per-layer u32 block (MoeArgs::sync). Producers write their data, fence (agent-scope release)
+// and add to a counter; consumers spin on a relaxed agent-scope load (thread 0, s_sleep between polls), then fence
+// (acquire) before reading. Every spin is bounded: past the limit, or once any workgroup has flagged an error, it
+// gives up and the unit is skipped, so every wave reaches the kernel's end whatever happens.
+constexpr uint32_t kSpinLimit = 1u << 22;  // polls of ~0.1-1 us each: seconds, far beyond any real wait
+enum { kSyncHead = 0, kSyncRouterDone = 1, kSyncRouteReady = 2, kSyncErr = kSyncErrWord, kSyncSlots = 8 };
+
+__device__ __forceinline__ uint32_t ld_acq(const uint32_t *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// thread 0 waits for *p >= v and fences (acquire: this CU's caches drop stale lines); all threads return whether it
+// was reached (uniform). One fence per workgroup: an agent-scope fence is an L2 write-back / invalidate on CDNA.
+__device__ bool block_wait_geq(uint32_t *sync, const uint32_t *p, uint32_t v, int *flag) {
+  if (threadIdx.x == 0) {
+    int ok = 0;
+    for (uint32_t it = 0; it < kSpinLimit; it++) {
+      if (ld_acq(p) >= v) {
+        ok = 1;
+        break;
+      }
+      if (ld_acq(sync + kSyncErr)) break;
+      __builtin_amdgcn_s_sleep(2);
+    }
+    if (!ok) atomicOr(sync + kSyncErr, 1u);
+    __threadfence();
+    *flag = ok;
+  }
+  __syncthreads();
+  return *flag != 0;
+}
+// acquire for the whole workgroup after a signal seen by thread 0
+__device__ __forceinline__ void block_acquire() {
+  if (threadIdx.x == 0) __threadfence();
+  __syncthreads();
+}
+// the workgroup's prior global writes (made visible to thread 0 by the barrier) released by thread 0's fence, then
+// thread 0 adds 1 to *p; returns the old value on every thread
+__device__ uint32_t block_signal(uint32_t *p, int *flag) {
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    __threadfence();
+    *flag = (int)atomicAdd(p, 1u);
+  }
+  __syncthreads();
+  const uint32_t old = (uint32_t)*flag;
+  __syncthreads();
+  return old;
+}
+
+// ------------------------------------------------------------------------------------------------ MoE: D1 router
+// Router GEMV (reference kernels/fn_moe.metal:50-67): one wave per router row (ne experts, then the shared-expert gate
+// row when present), every weight chunk of the row loaded before the dot; logits rounded to bf16 (the reference
+// rounding).
+constexpr int kRouterChunks = 8;  // hid <= 8 * 512
+__device__ void router_rows(const MoeArgs &a, int unit) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int row = unit * 4 + wave;
+  if (row >= a.ne + a.has_sgate) return;
+  const uint16_t *w = a.router + (uint64_t)row * a.hid;
+  uint4 wv[kRouterChunks];
+#pragma unroll
+  for (int j = 0; j < kRouterChunks; j++) {
+    const int e = j * 512 + lane * 8;
+    wv[j] = e < a.hid ? *(const uint4 *)(w + e) : make_uint4(0, 0, 0, 0);
+  }
+  for (int r = 0; r < a.R; r++) {
+    const float *x = a.x + (uint64_t)r * a.hid;
+    float acc = 0.f;
+#pragma unroll
+    for (int j = 0; j < kRouterChunks; j++) {
+      const int e = j * 512 + lane * 8;
+      if (e < a.hid) {
+        const float4 x0 = *(const float4 *)(x + e), x1 = *(const float4 *)(x + e + 4);
+        acc = fmaf(x0.x, bf16_f32(wv[j].x & 0xFFFFu), acc);
+        acc = fmaf(x0.y, bf16_f32(wv[j].x >> 16), acc);
+        acc = fmaf(x0.z, bf16_f32(wv[j].y & 0xFFFFu), acc);
+        acc = fmaf(x0.w, bf16_f32(wv[j].y >> 16), acc);
+        acc = fmaf(x1.x, bf16_f32(wv[j].z & 0xFFFFu), acc);
+        acc = fmaf(x1.y, bf16_f32(wv[j].z >> 16), acc);
+        acc = fmaf(x1.z, bf16_f32(wv[j].w & 0xFFFFu), acc);
+        acc = fmaf(x1.w, bf16_f32(wv[j].w >> 16), acc);
+      }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) acc += __shfl_xor(acc, o, 64);
+    if (lane == 0) a.logits[(uint64_t)r * (a.ne + 1) + row] = bf16_round(acc);
+  }
+}
+
+// Route of every row from the logits (reference kernels/fn_moe.metal:76-131): top-k by logit, the lower index first
+// on ties, weights exp(l - l_max) / sum over the top k in f32 (summed in slot order), shared gate sigmoid(logit).
+// Called by one workgroup after every router row is written.
+__device__ void route_rows(const MoeArgs &a, float *lv, uint32_t *cand, uint32_t *sid) {
+  const int ld = a.ne + 1;
+  for (int r = 0; r < a.R; r++) {
+    for (int i = threadIdx.x; i < a.ne; i += blockDim.x) lv[i] = a.logits[(uint64_t)r * ld + i];
+    __syncthreads();
+    block_topk(lv, a.ne, a.topk, cand, sid);
+    if (threadIdx.x == 0) {
+      float pr[kMaxTopk];
+      const float top = lv[sid[0]];
+      float s = 0.f;
+      for (int k = 0; k < a.topk; k++) {
+        pr[k] = expf(lv[sid[k]] - top);
+        s += pr[k];
+      }
+      uint32_t *rt = a.route + (uint64_t)r * 2 * a.topk;
+      for (int k = 0; k < a.topk; k++) {
+        rt[k] = sid[k];
+        rt[a.topk + k] = __float_as_uint(pr[k] / s);
+      }
+      a.sgv[r] = a.has_sgate ? 1.f / (1.f + expf(-a.logits[(uint64_t)r * ld + a.ne])) : 1.f;
+    }
+    __syncthreads();
+  }
+}
+
 // ------------------------------------------------------------------------------------------------ MoE: D2 gate/up
-// grid = R nslot x 2 (gate, up) x inter/32 (output tile pairs) x ksplit; 256 threads. Prep x * suh -> H -> fp16 into
-// LDS for the workgroup's k span (reference kernels/fn_moe.metal:304-312), then the pair GEMV; guo holds the raw
-// inner outputs per k split (summed in order by D3).
+// One unit = (slot, gate|up, output tile pair p, k split ks): prefetch the unit's tiles, prep x * suh -> H -> fp16
+// into LDS for the k span (reference kernels/fn_moe.metal:304-312), pair GEMV; guo holds the raw inner outputs per
+// k split (summed in order by the down unit).
 template <int K>
-__device__ void gateup_body(const MoeArgs &a, const SlotRef &sr, int slot, int proj, int p, int ks, _Float16 *prep,
+__device__ void gateup_unit(const MoeArgs &a, const SlotRef &sr, int slot, int proj, int p, int ks, _Float16 *prep,
                             float *red) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = slot / a.nslot;
   const int IT = a.hid >> 4, ktn = IT / a.ksplit, k0 = ks * ktn, n = ktn * 16;
+  const TileLane<K> L = tile_lane<K>((uint32_t)lane);
+  const uint32_t *pb = (const uint32_t *)(sr.blk + off_tr(a, sr.sh, proj)) + (uint64_t)p * IT * 2 * 8 * K;
+  PairBuf<K> buf;
+  pair_load<K>(buf, pb, L, k0 + wave, k0 + ktn);
   const float *x = a.x + (uint64_t)r * a.hid + k0 * 16;
   const uint16_t *su = (const uint16_t *)(sr.blk + off_su(a, sr.sh, proj)) + k0 * 16;
   for (int c = wave; c * 128 < n; c += 4) {
@@ -356,36 +498,29 @@ __device__ void gateup_body(const MoeArgs &a, const SlotRef &sr, int slot, int p
   }
   __syncthreads();
   float acc0, acc1;
-  pair_gemv<K>((const uint32_t *)(sr.blk + off_tr(a, sr.sh, proj)), IT, p, k0, k0 + ktn, prep, acc0, acc1);
+  pair_gemv<K>(buf, pb, L, k0, k0 + ktn, prep, acc0, acc1);
   const float s = pair_reduce(acc0, acc1, red);
   const int o = p * 32 + (int)threadIdx.x;
   if (threadIdx.x < 32 && o < a.inter) a.guo[(((uint64_t)slot * 2 + proj) * a.ksplit + ks) * a.inter + o] = s;
-}
-
-constexpr int kMaxPrep = 4096;  // halves of prepared input per workgroup
-
-__global__ __launch_bounds__(256) void moe_gateup(MoeArgs a) {
-  __shared__ _Float16 prep[kMaxPrep];
-  __shared__ float red[128];
-  int b = blockIdx.x;
-  const int NP = (a.inter / 16 + 1) / 2;
-  const int ks = b % a.ksplit;
-  b /= a.ksplit;
-  const int p = b % NP;
-  b /= NP;
-  const int proj = b & 1, slot = b >> 1;
-  const SlotRef sr = slot_ref(a, slot / a.nslot, slot % a.nslot);
-  IJ_DISPATCH_K(sr.K, gateup_body<KK>(a, sr, slot, proj, p, ks, prep, red));
+  __syncthreads();
 }
 
 // ------------------------------------------------------------------------------------------------ MoE: D3 down
-// grid = R nslot x hid/32 (output tile pairs); 256 threads. Prologue (reference kernels/fn_moe.metal:370-384):
-// g = H(guo_g) * svh_g, u = H(guo_u) * svh_u, h = H(silu(g) u * suh_d) -> fp16 LDS; then the down pair GEMV over all
-// inter k tiles; dn holds the raw down outputs (H_out, svh and the route weight are applied by the combine).
+// One unit = (slot, output tile pair p). The down tiles are prefetched first; then (fused kernel) the unit waits for
+// its slot's gate/up outputs; prologue (reference kernels/fn_moe.metal:370-384): g = H(guo_g) * svh_g,
+// u = H(guo_u) * svh_u, h = H(silu(g) u * suh_d) -> fp16 LDS; then the pair GEMV over all inter k tiles. dn holds the
+// raw down outputs (H_out, svh and the route weight are applied by the combine). Returns false if the wait failed.
 template <int K>
-__device__ void down_body(const MoeArgs &a, const SlotRef &sr, int slot, int p, _Float16 *prep, float *red) {
+__device__ bool down_unit(const MoeArgs &a, const SlotRef &sr, int slot, int p, _Float16 *prep, float *red,
+                          const uint32_t *wait_ctr, uint32_t wait_val, int *flag) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int inter = a.inter;
+  const int IT = inter >> 4;
+  const TileLane<K> L = tile_lane<K>((uint32_t)lane);
+  const uint32_t *pb = (const uint32_t *)(sr.blk + off_tr(a, sr.sh, 2)) + (uint64_t)p * IT * 2 * 8 * K;
+  PairBuf<K> buf;
+  pair_load<K>(buf, pb, L, wave, IT);
+  if (wait_ctr && !block_wait_geq(a.sync, wait_ctr, wait_val, flag)) return false;
   const float *gp = a.guo + (uint64_t)slot * 2 * a.ksplit * inter;
   const float *up = gp + (uint64_t)a.ksplit * inter;
   const uint16_t *gsv = (const uint16_t *)(sr.blk + off_sv(a, sr.sh, 0));
@@ -424,43 +559,208 @@ __device__ void down_body(const MoeArgs &a, const SlotRef &sr, int slot, int p, 
   }
   __syncthreads();
   float acc0, acc1;
-  pair_gemv<K>((const uint32_t *)(sr.blk + off_tr(a, sr.sh, 2)), inter >> 4, p, 0, inter >> 4, prep, acc0, acc1);
+  pair_gemv<K>(buf, pb, L, 0, IT, prep, acc0, acc1);
   const float s = pair_reduce(acc0, acc1, red);
   const int o = p * 32 + (int)threadIdx.x;
   if (threadIdx.x < 32 && o < a.hid) a.dn[(uint64_t)slot * a.hid + o] = s;
+  __syncthreads();
+  return true;
+}
+
+// ------------------------------------------------------------------------------------------------ MoE: combine
+// y[r][128 c ..] = sum over slots in slot order of H(dn) * svh_d * w_k, the shared slot last with its gate
+// (reference kernels/fn_moe.metal:412-447); 4 waves take the slots round-robin, the sum runs in slot order from LDS.
+constexpr int kMaxSlots = kMaxTopk + 1;
+__device__ void combine_block(const MoeArgs &a, int r, int c, float (*vs)[128]) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int i0 = c * 128 + lane, i1 = i0 + 64;
+  const bool m0 = i0 < a.hid, m1 = i1 < a.hid;
+  for (int k = wave; k < a.nslot; k += 4) {
+    const int slot = r * a.nslot + k;
+    const SlotRef sr = slot_ref(a, r, k);
+    const float w = k < a.topk ? __uint_as_float(a.route[(uint64_t)r * 2 * a.topk + a.topk + k]) : a.sgv[r];
+    const float *d = a.dn + (uint64_t)slot * a.hid;
+    const uint16_t *sv = (const uint16_t *)(sr.blk + off_sv(a, sr.sh, 2));
+    float v0 = m0 ? d[i0] : 0.f, v1 = m1 ? d[i1] : 0.f;
+    const float s0 = m0 ? h2f(sv[i0]) : 0.f, s1 = m1 ? h2f(sv[i1]) : 0.f;
+    fwht2(v0, v1, lane, a.had_hid, a.sc_hid);
+    vs[k][lane] = v0 * s0 * w;
+    vs[k][lane + 64] = v1 * s1 * w;
+  }
+  __syncthreads();
+  if (threadIdx.x < 128) {
+    const int i = c * 128 + threadIdx.x;
+    float y = 0.f;
+    for (int k = 0; k < a.nslot; k++) y += vs[k][threadIdx.x];
+    if (i < a.hid) a.y[(uint64_t)r * a.hid + i] = y;
+  }
+  __syncthreads();
+}
+
+// ------------------------------------------------------------------------------------------------ staged kernels
+// D1..D3 + combine as four launches (the reference's dispatch structure, kernels/fn_moe.metal). The router's last
+// workgroup to arrive (atomic counter, reset by it) computes the route.
+__global__ __launch_bounds__(256) void moe_router(MoeArgs a) {
+  __shared__ float lv[kMaxExperts];
+  __shared__ uint32_t sid[kMaxTopk];
+  __shared__ uint32_t cand[4 * kMaxTopk];
+  __shared__ int flag;
+  router_rows(a, blockIdx.x);
+  if (block_signal(a.sync + kSyncRouterDone, &flag) != gridDim.x - 1u) return;
+  block_acquire();
+  route_rows(a, lv, cand, sid);
+  if (threadIdx.x == 0) atomicExch(a.sync + kSyncRouterDone, 0u);
+}
+
+constexpr int kMaxPrep = 4096;  // halves of prepared input per workgroup
+
+__global__ __launch_bounds__(256) void moe_gateup(MoeArgs a) {
+  __shared__ _Float16 prep[kMaxPrep];
+  __shared__ float red[128];
+  int b = blockIdx.x;
+  const int NP = (a.inter / 16 + 1) / 2;
+  const int ks = b % a.ksplit;
+  b /= a.ksplit;
+  const int p = b % NP;
+  b /= NP;
+  const int proj = b & 1, slot = b >> 1;
+  const SlotRef sr = slot_ref(a, slot / a.nslot, slot % a.nslot);
+  IJ_DISPATCH_K(sr.K, gateup_unit<KK>(a, sr, slot, proj, p, ks, prep, red));
 }
 
 __global__ __launch_bounds__(256) void moe_down(MoeArgs a) {
   __shared__ _Float16 prep[kMaxPrep];
   __shared__ float red[128];
+  __shared__ int flag;
   const int NP = (a.hid / 16 + 1) / 2;
   const int p = blockIdx.x % NP, slot = blockIdx.x / NP;
   const SlotRef sr = slot_ref(a, slot / a.nslot, slot % a.nslot);
-  IJ_DISPATCH_K(sr.K, down_body<KK>(a, sr, slot, p, prep, red));
+  IJ_DISPATCH_K(sr.K, down_unit<KK>(a, sr, slot, p, prep, red, nullptr, 0u, &flag));
 }
 
-// ------------------------------------------------------------------------------------------------ MoE: combine
-// y[r] = sum over slots in slot order of H(dn) * svh_d * w_k, the shared slot last with its gate
-// (reference kernels/fn_moe.metal:412-447). grid = R x ceil(hid/128), one wave.
-__global__ __launch_bounds__(64) void moe_combine(MoeArgs a) {
+__global__ __launch_bounds__(256) void moe_combine(MoeArgs a) {
+  __shared__ float vs[kMaxSlots][128];
   const int nch = (a.hid + 127) / 128;
-  const int r = blockIdx.x / nch, c = blockIdx.x % nch, lane = threadIdx.x;
-  const int i0 = c * 128 + lane, i1 = i0 + 64;
-  const bool m0 = i0 < a.hid, m1 = i1 < a.hid;
-  float y0 = 0.f, y1 = 0.f;
-  for (int k = 0; k < a.nslot; k++) {
+  combine_block(a, blockIdx.x / nch, blockIdx.x % nch, vs);
+}
+
+// ------------------------------------------------------------------------------------------------ fused layer kernel
+// The whole layer step in one launch. Workgroups take units from an ordered queue (atomic head):
+//   [router rows] [shared-expert gate/up] [routed gate/up, slot-major] [down: shared slot first, then routed]
+// A unit only ever waits on units before it in the queue (route ready <- all router units; a slot's down units <-
+// its gate/up units), and a workgroup takes a new unit only after finishing the previous one, so the units waited on
+// are already held by running workgroups: the queue makes progress whatever number of workgroups is resident.
+// The last router unit to finish computes the route; the last down unit of each (row, 128-column block) runs the
+// combine for that block (fixed slot order: deterministic). The workgroup whose final (empty) take is the last one
+// of the grid resets every counter for the next launch / graph replay.
+struct FusedShape {
+  int NPg, NPd, nblk, n0, n1, n2, n3, total, per_slot;
+};
+__device__ __forceinline__ FusedShape fused_shape(const MoeArgs &a) {
+  FusedShape f;
+  f.NPg = (a.inter / 16 + 1) / 2;
+  f.NPd = (a.hid / 16 + 1) / 2;
+  f.nblk = (a.hid + 127) / 128;
+  f.per_slot = 2 * f.NPg * a.ksplit;
+  f.n0 = (a.ne + a.has_sgate + 3) / 4;
+  f.n1 = (a.nslot > a.topk) ? a.R * f.per_slot : 0;
+  f.n2 = a.R * a.topk * f.per_slot;
+  f.n3 = a.R * a.nslot * f.NPd;
+  f.total = f.n0 + f.n1 + f.n2 + f.n3;
+  return f;
+}
+
+__device__ __forceinline__ int grab_unit(uint32_t *sync, int *s_unit) {
+  if (threadIdx.x == 0) *s_unit = (int)atomicAdd(sync + kSyncHead, 1u);
+  __syncthreads();
+  const int u = *s_unit;
+  __syncthreads();
+  return u;
+}
+
+// The queue is walked in three loops, one per unit kind, so each loop keeps only its own values live. Instantiated per
+// (routed K, shared K): one decoder per expert kind keeps the register budget at 3 workgroups per CU.
+#define IJ_FUSED_K(CALL)          \
+  if (sr.sh) {                    \
+    constexpr int KK = KS;        \
+    CALL;                         \
+  } else {                        \
+    constexpr int KK = K;         \
+    CALL;                         \
+  }
+template <int K, int KS>
+__global__ __launch_bounds__(256, 3) void moe_fused(MoeArgs a) {
+  __shared__ _Float16 prep[kMaxPrep];
+  __shared__ float red[128];
+  __shared__ float lv[kMaxExperts];
+  __shared__ uint32_t sid[kMaxTopk];
+  __shared__ uint32_t cand[4 * kMaxTopk];
+  __shared__ float vs[kMaxSlots][128];
+  __shared__ int flag, s_unit;
+  const FusedShape f = fused_shape(a);
+  uint32_t *sync = a.sync;
+  uint32_t *gu_done = sync + kSyncSlots;
+  uint32_t *blk_cnt = gu_done + a.R * a.nslot;
+  int u = grab_unit(sync, &s_unit);
+  // router rows; the last to finish computes the route
+  for (; u < f.n0; u = grab_unit(sync, &s_unit)) {
+    if (ld_acq(sync + kSyncErr)) continue;
+    router_rows(a, u);
+    if (block_signal(sync + kSyncRouterDone, &flag) == (uint32_t)f.n0 - 1u) {
+      block_acquire();
+      route_rows(a, lv, cand, sid);
+      block_signal(sync + kSyncRouteReady, &flag);
+    }
+  }
+  // gate/up: shared slots (one per row) first, then routed slots (row-major, k order)
+  for (; u < f.n0 + f.n1 + f.n2; u = grab_unit(sync, &s_unit)) {
+    if (ld_acq(sync + kSyncErr)) continue;
+    int v = u - f.n0, r, k;
+    if (v < f.n1) {
+      r = v / f.per_slot;
+      k = a.topk;
+    } else {
+      v -= f.n1;
+      const int sidx = v / f.per_slot;
+      r = sidx / a.topk;
+      k = sidx % a.topk;
+    }
+    const int w = v % f.per_slot;
+    const int ks = w % a.ksplit, p = (w / a.ksplit) % f.NPg, proj = w / (a.ksplit * f.NPg);
+    if (k < a.topk && !block_wait_geq(sync, sync + kSyncRouteReady, 1u, &flag)) continue;
     const int slot = r * a.nslot + k;
     const SlotRef sr = slot_ref(a, r, k);
-    const float w = k < a.topk ? __uint_as_float(a.route[(uint64_t)r * 2 * a.topk + a.topk + k]) : a.sgv[r];
-    const float *d = a.dn + (uint64_t)slot * a.hid;
-    float v0 = m0 ? d[i0] : 0.f, v1 = m1 ? d[i1] : 0.f;
-    fwht2(v0, v1, lane, a.had_hid, a.sc_hid);
-    const uint16_t *sv = (const uint16_t *)(sr.blk + off_sv(a, sr.sh, 2));
-    if (m0) y0 += v0 * h2f(sv[i0]) * w;
-    if (m1) y1 += v1 * h2f(sv[i1]) * w;
+    IJ_FUSED_K(gateup_unit<KK>(a, sr, slot, proj, p, ks, prep, red));
+    block_signal(gu_done + slot, &flag);
   }
-  if (m0) a.y[(uint64_t)r * a.hid + i0] = y0;
-  if (m1) a.y[(uint64_t)r * a.hid + i1] = y1;
+  // down: per row, the shared slot first, then the routed slots; the last unit of each 128-column block combines it
+  for (; u < f.total; u = grab_unit(sync, &s_unit)) {
+    if (ld_acq(sync + kSyncErr)) continue;
+    const int v = u - f.n0 - f.n1 - f.n2;
+    const int p = v % f.NPd, q = v / f.NPd, r = q / a.nslot, j = q % a.nslot;
+    const int k = (a.nslot > a.topk) ? (j == 0 ? a.topk : j - 1) : j;
+    if (k < a.topk && !block_wait_geq(sync, sync + kSyncRouteReady, 1u, &flag)) continue;
+    const int slot = r * a.nslot + k;
+    const SlotRef sr = slot_ref(a, r, k);
+    bool ok = false;
+    IJ_FUSED_K(ok = down_unit<KK>(a, sr, slot, p, prep, red, gu_done + slot, (uint32_t)f.per_slot, &flag));
+    if (!ok) continue;
+    const int c = (p * 32) / 128;
+    const uint32_t arrivals = (uint32_t)a.nslot * (uint32_t)min(4, f.NPd - c * 4);
+    if (block_signal(blk_cnt + r * f.nblk + c, &flag) == arrivals - 1u) {
+      block_acquire();
+      combine_block(a, r, c, vs);
+    }
+  }
+  // the grid's last (empty) take resets the counters for the next launch
+  if (threadIdx.x == 0 && u == f.total + (int)gridDim.x - 1) {
+    for (int i = 0; i < a.R * a.nslot; i++) gu_done[i] = 0u;
+    for (int i = 0; i < a.R * f.nblk; i++) blk_cnt[i] = 0u;
+    sync[kSyncRouterDone] = 0u;
+    sync[kSyncRouteReady] = 0u;
+    __threadfence();
+    atomicExch(sync + kSyncHead, 0u);
+  }
 }
 
 // ------------------------------------------------------------------------------------------------ trunk linear
@@ -482,10 +782,14 @@ __global__ __launch_bounds__(64) void lin_prep(LinArgs a) {
 template <int K, int RT>
 __global__ __launch_bounds__(256) void lin_gemv(LinArgs a) {
   extern __shared__ _Float16 xs[];
-  constexpr int TW = 8 * K;
   const int NP = (a.OT + 1) / 2, OTp = 2 * NP;
   const int p = blockIdx.x % NP, s = blockIdx.x / NP;
-  const int span = a.IT / a.S, k0 = s * span, n = span * 16;
+  const int span = a.IT / a.S, k0 = s * span, k1 = k0 + span, n = span * 16;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const TileLane<K> L = tile_lane<K>((uint32_t)lane);
+  const uint32_t *pb = a.tiles + (uint64_t)p * a.IT * 2 * 8 * K;
+  PairBuf<K> buf;
+  pair_load<K>(buf, pb, L, k0 + wave, k1);
   for (int i = threadIdx.x; i < RT * n / 8; i += blockDim.x) {
     const int r = (i * 8) / n, o = (i * 8) % n;
     uint4 v = make_uint4(0, 0, 0, 0);
@@ -493,25 +797,26 @@ __global__ __launch_bounds__(256) void lin_gemv(LinArgs a) {
     *(uint4 *)(xs + r * n + o) = v;
   }
   __syncthreads();
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const TileLane<K> L = tile_lane<K>((uint32_t)lane);
   const int q = (lane >> 1) & 3;
   float acc0[RT], acc1[RT];
 #pragma unroll
   for (int r = 0; r < RT; r++) acc0[r] = acc1[r] = 0.f;
-  const uint32_t *base = a.tiles + (uint64_t)p * a.IT * 2 * TW;
-#pragma unroll 2
-  for (int tk = k0 + wave; tk < k0 + span; tk += 4) {
-    const uint32_t *T0 = base + (uint64_t)tk * 2 * TW;
-    const TileWords wa = load_tile<K>(T0, L), wb = load_tile<K>(T0 + TW, L);
-    f16x2 a0, b0, a1, b1;
-    decode4<K>(wa, L.sh, a0, b0);
-    decode4<K>(wb, L.sh, a1, b1);
+  for (int tk0 = k0 + wave; tk0 < k1; tk0 += 4 * kPrefetch) {
+    if (tk0 != k0 + wave) pair_load<K>(buf, pb, L, tk0, k1);
 #pragma unroll
-    for (int r = 0; r < RT; r++) {
-      const f16x4 xv = *(const f16x4 *)(xs + r * n + (tk - k0) * 16 + 4 * q);
-      acc0[r] = dot4(a0, b0, xv, acc0[r]);
-      acc1[r] = dot4(a1, b1, xv, acc1[r]);
+    for (int j = 0; j < kPrefetch; j++) {
+      const int tk = tk0 + 4 * j;
+      if (tk < k1) {
+        f16x2 a0, b0, a1, b1;
+        decode4<K>(buf.w[j][0], L.sh, a0, b0);
+        decode4<K>(buf.w[j][1], L.sh, a1, b1);
+#pragma unroll
+        for (int r = 0; r < RT; r++) {
+          const f16x4 xv = *(const f16x4 *)(xs + r * n + (tk - k0) * 16 + 4 * q);
+          acc0[r] = dot4(a0, b0, xv, acc0[r]);
+          acc1[r] = dot4(a1, b1, xv, acc1[r]);
+        }
+      }
     }
   }
   __shared__ float red[4 * 32 * RT];
@@ -638,7 +943,32 @@ void launch_moe_down(const MoeArgs &a, hipStream_t s) {
   hipLaunchKernelGGL(moe_down, dim3(a.R * a.nslot * NP), dim3(256), 0, s, a);
 }
 void launch_moe_combine(const MoeArgs &a, hipStream_t s) {
-  hipLaunchKernelGGL(moe_combine, dim3(a.R * ((a.hid + 127) / 128)), dim3(64), 0, s, a);
+  hipLaunchKernelGGL(moe_combine, dim3(a.R * ((a.hid + 127) / 128)), dim3(256), 0, s, a);
+}
+static const void *fused_fn(int K, int KS) {
+#define IJ_FUSED_CASE(k, ks) \
+  if (K == k && KS == ks) return (const void *)&moe_fused<k, ks>;
+  IJ_FUSED_CASE(4, 4) IJ_FUSED_CASE(5, 5) IJ_FUSED_CASE(6, 6) IJ_FUSED_CASE(4, 6) IJ_FUSED_CASE(5, 6)
+  IJ_FUSED_CASE(4, 8) IJ_FUSED_CASE(5, 8) IJ_FUSED_CASE(6, 8)
+#undef IJ_FUSED_CASE
+  return nullptr;
+}
+bool moe_fused_supported(int K, int KS) { return fused_fn(K, KS) != nullptr; }
+int moe_fused_grid(int K, int KS) {
+  const void *f = fused_fn(K, KS);
+  IJ_CHECK(f, "fused MoE kernel not instantiated for K%d / shared K%d", K, KS);
+  int dev = 0, cus = 0, per = 0;
+  IJ_HIP(hipGetDevice(&dev));
+  IJ_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+  IJ_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, f, 256, 0));
+  return cus * std::max(1, std::min(per, 4));
+}
+void launch_moe_fused(const MoeArgs &a, int grid, hipStream_t s) {
+  const int KS = a.nslot > a.topk ? a.slay.K : a.lay.K;
+  const void *f = fused_fn(a.lay.K, KS);
+  IJ_CHECK(f, "fused MoE kernel not instantiated for K%d / shared K%d", a.lay.K, KS);
+  void *args[] = {const_cast<MoeArgs *>(&a)};
+  IJ_HIP(hipLaunchKernel(f, dim3(grid > 0 ? grid : moe_fused_grid(a.lay.K, KS)), dim3(256), args, 0, s));
 }
 
 template <int K>
@@ -694,6 +1024,9 @@ static std::vector<KernelEntry> build_registry() {
   v.push_back({"moe_gateup", (const void *)&moe_gateup, {(uint32_t)sizeof(MoeArgs)}, -1, -1});
   v.push_back({"moe_down", (const void *)&moe_down, {(uint32_t)sizeof(MoeArgs)}, -1, -1});
   v.push_back({"moe_combine", (const void *)&moe_combine, {(uint32_t)sizeof(MoeArgs)}, -1, -1});
+  for (int K = 4; K <= 6; K++)
+    for (int KS : {4, 5, 6, 8})
+      if (fused_fn(K, KS)) v.push_back({"moe_fused_ks" + std::to_string(KS), fused_fn(K, KS), {(uint32_t)sizeof(MoeArgs)}, K, -1});
   v.push_back({"fill_u32", (const void *)&fill_u32, {P, 8, 8}, -1, -1});
   return v;
 }

@@ -84,8 +84,9 @@ NE_API int ne_moe_bytes(const ne_moe *m, int R, uint64_t *bytes);
  * reference's differential timing (ne_fn_layer_time, models/flash_next/layer.h:266-267; core/bench.h:21-24). */
 NE_API int ne_moe_time(ne_moe *const *layers, int n, int R, const ne_buf *x, int warmup, int reps,
                        double *us_per_layer);
-/* Per-kernel timing of the same chain: launches each kernel kind of the layer step alone, reps times per layer, and
- * returns the mean duration in microseconds of each (names: "router", "gateup", "down", "combine"); n_kinds in/out. */
+/* Per-kernel timing of the same chain: launches each kernel kind alone, reps times per layer, and returns the mean
+ * duration in microseconds of each: the staged path's "router", "gateup", "down", "combine", and "fused" (the whole
+ * step in one persistent launch) when instantiated for the layer's bit widths. n_kinds: capacity in (>= 5), count out. */
 NE_API int ne_moe_time_kernels(ne_moe *const *layers, int n, int R, const ne_buf *x, int reps, char names[][16],
                                double *us, int *n_kinds);
 

@@ -128,3 +128,18 @@ def test_moe_synth_full_properties(eng):
     assert np.array_equal(y, m.run(x))
     per_expert = 3 * 2048 * 512 * 5 // 8 + 2 * 3 * (2048 + 512)
     assert m.bytes(1) == 11 * per_expert + 512 * 2048 * 2
+
+
+def test_moe_fused_and_staged_paths_agree(eng, oracle, monkeypatch):
+    """The persistent fused launch and the four staged launches run the same unit code: bit-identical outputs."""
+    w = synth.moe_layer(61, hid=2048, inter=512, ne=64, topk=10, K=5, shared=True, Ks=6, sgate=True)
+    x = synth.bf16_values(np.random.default_rng(62), 2, 2048)
+    monkeypatch.setenv("IJAH_MOE_PATH", "staged")
+    ys = eng.moe_create(w).run(x)
+    monkeypatch.setenv("IJAH_MOE_PATH", "fused")
+    m = eng.moe_create(w)
+    yf = m.run(x)
+    assert np.array_equal(ys, yf)
+    for _ in range(3):  # counters reset between launches
+        assert np.array_equal(m.run(x), yf)
+    check_layer(eng, oracle, m, oracle.MoeWeights(w), x)
