@@ -219,27 +219,35 @@ struct ne_moe {
   uint16_t *router = nullptr;  // [ne + has_sgate][hid]
   int Rcap = 0;
   float *logits = nullptr, *sgv = nullptr, *guo = nullptr, *dn = nullptr;
+  uint16_t *hprep = nullptr;
   uint32_t *route = nullptr, *sync = nullptr;
+  uint64_t *trace = nullptr;  // IJAH_MOE_TRACE=1: per-unit timestamps of the fused kernel (debug)
   bool fused = true;  // one persistent launch per step (IJAH_MOE_PATH=staged: four launches)
   int last_R = 0;
   float *last_y = nullptr;
   ~ne_moe() {
-    for (void *p : std::initializer_list<void *>{experts, shared, router, logits, sgv, guo, dn, route, sync})
+    for (void *p : std::initializer_list<void *>{experts, shared, router, logits, sgv, guo, dn, route, sync, trace, hprep})
       dev_free(p);
   }
   int nslot() const { return topk + has_shared; }
   void ensure_scratch(int R) {
     if (R <= Rcap) return;
-    for (void *p : std::initializer_list<void *>{logits, sgv, guo, dn, route, sync}) dev_free(p);
+    for (void *p : std::initializer_list<void *>{logits, sgv, guo, dn, route, sync, hprep}) dev_free(p);
     const size_t S = (size_t)R * nslot();
     logits = dev_alloc<float>((size_t)R * (ne + 1));
     sgv = dev_alloc<float>(R);
     guo = dev_alloc<float>(S * 2 * ksplit * inter);
     dn = dev_alloc<float>(S * hid);
+    hprep = dev_alloc<uint16_t>(S * inter);
     route = dev_alloc<uint32_t>((size_t)R * 2 * topk);
     IJ_HIP(hipMemset(route, 0, sizeof(uint32_t) * R * 2 * topk));
-    sync = dev_alloc<uint32_t>(sync_words(R, nslot(), hid));
-    IJ_HIP(hipMemset(sync, 0, 4 * sync_words(R, nslot(), hid)));
+    sync = dev_alloc<uint32_t>(sync_words(R, nslot(), hid, inter));
+    if (getenv("IJAH_MOE_TRACE")) {
+      dev_free(trace);
+      trace = dev_alloc<uint64_t>((size_t)8 * 65536);
+      IJ_HIP(hipMemset(trace, 0, 8 * 8 * 65536));
+    }
+    IJ_HIP(hipMemset(sync, 0, 4 * sync_words(R, nslot(), hid, inter)));
     Rcap = R;
   }
   MoeArgs args(int R, const float *x, float *y) const {
@@ -269,6 +277,8 @@ struct ne_moe {
     a.guo = guo;
     a.dn = dn;
     a.sync = sync;
+    a.trace = trace;
+    a.hprep = hprep;
     return a;
   }
   // a failed cross-workgroup wait leaves the error word set: report it and clear the counters
@@ -277,14 +287,14 @@ struct ne_moe {
     IJ_HIP(hipMemcpyAsync(&err, sync + kSyncErrWord, 4, hipMemcpyDeviceToHost, s));
     IJ_HIP(hipStreamSynchronize(s));
     if (err) {
-      IJ_HIP(hipMemsetAsync(sync, 0, 4 * sync_words(Rcap, nslot(), hid), s));
+      IJ_HIP(hipMemsetAsync(sync, 0, 4 * sync_words(Rcap, nslot(), hid, inter), s));
       IJ_HIP(hipStreamSynchronize(s));
       throw Error("moe: a cross-workgroup wait timed out (layer output invalid)");
     }
   }
   void launch(int R, const float *x, float *y, hipStream_t s) const {
     const MoeArgs a = args(R, x, y);
-    if (fused && moe_fused_supported(K, has_shared ? Ks : K)) {
+    if (fused && moe_fused_supported(K, has_shared ? Ks : K, R, hid, inter, ksplit)) {
       launch_moe_fused(a, 0, s);
       return;
     }
@@ -558,6 +568,9 @@ NE_API int ne_moe_read(ne_moe *m, const char *name, void *dst, uint64_t nbytes) 
       memcpy(out.data(), o.data(), out.size());
     } else if (n == "experts_dn") {
       fetch(m->dn, (size_t)S * m->hid * 4);
+    } else if (n == "trace") {
+      IJ_CHECK(m->trace, "no trace (set IJAH_MOE_TRACE=1 before creating the layer)");
+      fetch(m->trace, (size_t)8 * 8 * 65536);
     } else if (n == "mlp_out") {
       fetch(m->last_y, (size_t)R * m->hid * 4);
     } else {
@@ -671,7 +684,7 @@ NE_API int ne_moe_time_kernels(ne_moe *const *layers, int n, int R, const ne_buf
                                                     launch_moe_combine, fused};
     const char *nm[5] = {"router", "gateup", "down", "combine", "fused"};
     const int KS = layers[0]->has_shared ? layers[0]->Ks : layers[0]->K;
-    const int kinds = moe_fused_supported(layers[0]->K, KS) ? 5 : 4;
+    const int kinds = moe_fused_supported(layers[0]->K, KS, R, hid, layers[0]->inter, layers[0]->ksplit) ? 5 : 4;
     try {
       for (int k = 0; k < kinds; k++) {
         double ms = 0;

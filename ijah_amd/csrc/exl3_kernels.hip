@@ -50,6 +50,18 @@ __device__ __forceinline__ uint32_t kp(uint32_t p) {
   return (p & ~15u) | (((p & 7u) >> 1) << 2) | (p & 1u) | (((p >> 3) & 1u) << 1);
 }
 
+// Data handed between workgroups (logits, route, gate/up and down partials) moves with device-coherent accesses
+// (agent-scope relaxed atomics: sc1 loads / stores, which bypass the per-XCD L2's non-coherent lines), so ordering
+// needs only s_waitcnt + barriers: no agent-scope fence, which on CDNA writes back or invalidates the whole L2.
+template <typename T>
+__device__ __forceinline__ T ld_cg(const T *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <typename T>
+__device__ __forceinline__ void st_cg(T *p, T v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // ------------------------------------------------------------------------------------------------ Hadamard
 // normalised Sylvester H_N (N = 16..128) on a 128-chunk held as (lane, lane + 64); blocks of N are contiguous.
 __device__ __forceinline__ void fwht2(float &v0, float &v1, int lane, int N, float sc) {
@@ -286,9 +298,10 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
   v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));   // quad_perm 2,3,0,1
   v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false));  // row_half_mirror
   v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false));  // row_mirror
-  const uint32_t a = __builtin_amdgcn_readlane(v, 0), b = __builtin_amdgcn_readlane(v, 16);
-  const uint32_t c = __builtin_amdgcn_readlane(v, 32), d = __builtin_amdgcn_readlane(v, 48);
-  return max(max(a, b), max(c, d));
+  // every lane of a row holds the row max; row_bcast:15 / :31 carry it to the next row(s); lane 63 ends with all
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xA, 0xF, false));  // row_bcast:15
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xC, 0xF, false));  // row_bcast:31
+  return __builtin_amdgcn_readlane(v, 63);
 }
 // Order key of a bf16-valued logit and its index: a larger key is a larger logit, equal logits order the lower index
 // first (the reference's tie rule, kernels/fn_moe.metal:84,105). NaN ranks as -inf, -0 as +0. Zero is below every key.
@@ -299,35 +312,30 @@ __device__ __forceinline__ uint32_t topk_key(float v, int i) {
   u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
   return (u & 0xFFFF0000u) | (0xFFFFu - (uint32_t)i);
 }
-// Top-k of lv[0..ne) (bf16-valued, ne <= 1024, k <= 32) by a 256-thread block: each wave takes the top k of its
-// quarter by k rounds of wave max; wave 0 merges the 4 k candidates the same way. ids land in sid[0..k) in order.
+// Top-k of lv[0..ne) (bf16-valued, ne <= 1024, k <= 32): wave 0 holds 16 keys per lane and runs k rounds of
+// wave max + clear; ids land in sid[0..k) in order. All threads of the block call it (barrier at the end).
 __device__ void block_topk(const float *lv, int ne, int k, uint32_t *cand, uint32_t *sid) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  uint32_t key[4];
-#pragma unroll
-  for (int j = 0; j < 4; j++) {
-    const int i = (wave * 4 + j) * 64 + lane;
-    key[j] = i < ne ? topk_key(lv[i], i) : 0u;
-  }
-  for (int t = 0; t < k; t++) {
-    const uint32_t m = wave_max_u32(max(max(key[0], key[1]), max(key[2], key[3])));
-    if (lane == 0) cand[wave * k + t] = m;
-#pragma unroll
-    for (int j = 0; j < 4; j++) key[j] = key[j] == m ? 0u : key[j];
-  }
-  __syncthreads();
+  (void)cand;
   if (wave == 0) {
-    uint32_t c0 = lane < 4 * k ? cand[lane] : 0u, c1 = lane + 64 < 4 * k ? cand[lane + 64] : 0u;
+    uint32_t key[16];
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+      const int i = j * 64 + lane;
+      key[j] = i < ne ? topk_key(lv[i], i) : 0u;
+    }
     for (int t = 0; t < k; t++) {
-      const uint32_t m = wave_max_u32(max(c0, c1));
+      uint32_t m = 0u;
+#pragma unroll
+      for (int j = 0; j < 16; j += 2) m = max(m, max(key[j], key[j + 1]));
+      m = wave_max_u32(m);
       if (lane == 0) sid[t] = 0xFFFFu - (m & 0xFFFFu);
-      c0 = c0 == m ? 0u : c0;
-      c1 = c1 == m ? 0u : c1;
+#pragma unroll
+      for (int j = 0; j < 16; j++) key[j] = key[j] == m ? 0u : key[j];
     }
   }
   __syncthreads();
 }
-
 
 // slot (row r, k): routed expert route[r][k] (ids past ne clamp to 0, as the reference masks with NE - 1) or the
 // shared expert (k == topk). Offsets are picked as scalars so no layout struct is copied to scratch.
@@ -338,7 +346,7 @@ struct SlotRef {
 __device__ __forceinline__ SlotRef slot_ref(const MoeArgs &a, int r, int k) {
   SlotRef s;
   if (k < a.topk) {
-    uint32_t e = a.route[(uint64_t)r * 2 * a.topk + k];
+    uint32_t e = ld_cg(a.route + (uint64_t)r * 2 * a.topk + k);
     e = e < (uint32_t)a.ne ? e : 0u;
     s.blk = a.experts + (uint64_t)e * a.lay.bytes;
     s.K = a.lay.K;
@@ -360,13 +368,19 @@ __device__ __forceinline__ uint64_t off_sv(const MoeArgs &a, int sh, int p) { re
 // (acquire) before reading. Every spin is bounded: past the limit, or once any workgroup has flagged an error, it
 // gives up and the unit is skipped, so every wave reaches the kernel's end whatever happens.
 constexpr uint32_t kSpinLimit = 1u << 22;  // polls of ~0.1-1 us each: seconds, far beyond any real wait
-enum { kSyncHead = 0, kSyncRouterDone = 1, kSyncRouteReady = 2, kSyncErr = kSyncErrWord, kSyncSlots = 8 };
+enum {
+  kSyncHead = 0,
+  kSyncRouterDone = kSyncStride,
+  kSyncRouteReady = 2 * kSyncStride,
+  kSyncErr = kSyncErrWord,
+  kSyncSlots = 8 * kSyncStride
+};
 
 __device__ __forceinline__ uint32_t ld_acq(const uint32_t *p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-// thread 0 waits for *p >= v and fences (acquire: this CU's caches drop stale lines); all threads return whether it
-// was reached (uniform). One fence per workgroup: an agent-scope fence is an L2 write-back / invalidate on CDNA.
+// thread 0 waits for *p >= v; all threads return whether it was reached (uniform). The data the counter guards is
+// read with ld_cg afterwards.
 __device__ bool block_wait_geq(uint32_t *sync, const uint32_t *p, uint32_t v, int *flag) {
   if (threadIdx.x == 0) {
     int ok = 0;
@@ -375,29 +389,21 @@ __device__ bool block_wait_geq(uint32_t *sync, const uint32_t *p, uint32_t v, in
         ok = 1;
         break;
       }
-      if (ld_acq(sync + kSyncErr)) break;
+      if ((it & 63u) == 63u && ld_acq(sync + kSyncErr)) break;
       __builtin_amdgcn_s_sleep(2);
     }
     if (!ok) atomicOr(sync + kSyncErr, 1u);
-    __threadfence();
     *flag = ok;
   }
   __syncthreads();
   return *flag != 0;
 }
-// acquire for the whole workgroup after a signal seen by thread 0
-__device__ __forceinline__ void block_acquire() {
-  if (threadIdx.x == 0) __threadfence();
-  __syncthreads();
-}
-// the workgroup's prior global writes (made visible to thread 0 by the barrier) released by thread 0's fence, then
-// thread 0 adds 1 to *p; returns the old value on every thread
+// every wave's st_cg stores completed (s_waitcnt 0, then the barrier), then thread 0 adds 1 to *p; returns the old
+// value on every thread
 __device__ uint32_t block_signal(uint32_t *p, int *flag) {
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  if (threadIdx.x == 0) {
-    __threadfence();
-    *flag = (int)atomicAdd(p, 1u);
-  }
+  if (threadIdx.x == 0) *flag = (int)atomicAdd(p, 1u);
   __syncthreads();
   const uint32_t old = (uint32_t)*flag;
   __syncthreads();
@@ -409,25 +415,30 @@ __device__ uint32_t block_signal(uint32_t *p, int *flag) {
 // row when present), every weight chunk of the row loaded before the dot; logits rounded to bf16 (the reference
 // rounding).
 constexpr int kRouterChunks = 8;  // hid <= 8 * 512
-__device__ void router_rows(const MoeArgs &a, int unit) {
+// xs: LDS staging for one input row (hid floats); every thread of the workgroup calls this (barriers inside)
+__device__ void router_rows(const MoeArgs &a, int unit, float *xs) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int row = unit * 4 + wave;
-  if (row >= a.ne + a.has_sgate) return;
-  const uint16_t *w = a.router + (uint64_t)row * a.hid;
+  const int row = unit * (int)(blockDim.x >> 6) + wave;
+  const bool active = row < a.ne + a.has_sgate;
+  const uint16_t *w = a.router + (uint64_t)(active ? row : 0) * a.hid;
   uint4 wv[kRouterChunks];
 #pragma unroll
   for (int j = 0; j < kRouterChunks; j++) {
     const int e = j * 512 + lane * 8;
-    wv[j] = e < a.hid ? *(const uint4 *)(w + e) : make_uint4(0, 0, 0, 0);
+    wv[j] = (active && e < a.hid) ? *(const uint4 *)(w + e) : make_uint4(0, 0, 0, 0);
   }
   for (int r = 0; r < a.R; r++) {
-    const float *x = a.x + (uint64_t)r * a.hid;
+    __syncthreads();
+    for (int i = threadIdx.x; i < a.hid / 4; i += blockDim.x)
+      ((float4 *)xs)[i] = ((const float4 *)(a.x + (uint64_t)r * a.hid))[i];
+    __syncthreads();
+    if (!active) continue;
     float acc = 0.f;
 #pragma unroll
     for (int j = 0; j < kRouterChunks; j++) {
       const int e = j * 512 + lane * 8;
       if (e < a.hid) {
-        const float4 x0 = *(const float4 *)(x + e), x1 = *(const float4 *)(x + e + 4);
+        const float4 x0 = *(const float4 *)(xs + e), x1 = *(const float4 *)(xs + e + 4);
         acc = fmaf(x0.x, bf16_f32(wv[j].x & 0xFFFFu), acc);
         acc = fmaf(x0.y, bf16_f32(wv[j].x >> 16), acc);
         acc = fmaf(x0.z, bf16_f32(wv[j].y & 0xFFFFu), acc);
@@ -440,7 +451,7 @@ __device__ void router_rows(const MoeArgs &a, int unit) {
     }
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) acc += __shfl_xor(acc, o, 64);
-    if (lane == 0) a.logits[(uint64_t)r * (a.ne + 1) + row] = bf16_round(acc);
+    if (lane == 0) st_cg(a.logits + (uint64_t)r * (a.ne + 1) + row, bf16_round(acc));
   }
 }
 
@@ -450,7 +461,7 @@ __device__ void router_rows(const MoeArgs &a, int unit) {
 __device__ void route_rows(const MoeArgs &a, float *lv, uint32_t *cand, uint32_t *sid) {
   const int ld = a.ne + 1;
   for (int r = 0; r < a.R; r++) {
-    for (int i = threadIdx.x; i < a.ne; i += blockDim.x) lv[i] = a.logits[(uint64_t)r * ld + i];
+    for (int i = threadIdx.x; i < a.ne; i += blockDim.x) lv[i] = ld_cg(a.logits + (uint64_t)r * ld + i);
     __syncthreads();
     block_topk(lv, a.ne, a.topk, cand, sid);
     if (threadIdx.x == 0) {
@@ -463,12 +474,21 @@ __device__ void route_rows(const MoeArgs &a, float *lv, uint32_t *cand, uint32_t
       }
       uint32_t *rt = a.route + (uint64_t)r * 2 * a.topk;
       for (int k = 0; k < a.topk; k++) {
-        rt[k] = sid[k];
-        rt[a.topk + k] = __float_as_uint(pr[k] / s);
+        st_cg(rt + k, sid[k]);
+        st_cg(rt + a.topk + k, __float_as_uint(pr[k] / s));
       }
-      a.sgv[r] = a.has_sgate ? 1.f / (1.f + expf(-a.logits[(uint64_t)r * ld + a.ne])) : 1.f;
+      st_cg(a.sgv + r, a.has_sgate ? 1.f / (1.f + expf(-ld_cg(a.logits + (uint64_t)r * ld + a.ne))) : 1.f);
     }
     __syncthreads();
+  }
+}
+
+// optional unit trace (MoeArgs::trace): [u][0] = wall clock at the take, [1] = after the unit's waits, [2] = done,
+// [3] = workgroup id
+__device__ __forceinline__ void trace_mark(const MoeArgs &a, int u, int total, int field) {
+  if (a.trace && threadIdx.x == 0 && u < total) {
+    a.trace[(uint64_t)u * 8 + field] = wall_clock64();
+    if (field == 0) a.trace[(uint64_t)u * 8 + 7] = blockIdx.x;
   }
 }
 
@@ -478,7 +498,7 @@ __device__ void route_rows(const MoeArgs &a, float *lv, uint32_t *cand, uint32_t
 // k split (summed in order by the down unit).
 template <int K>
 __device__ void gateup_unit(const MoeArgs &a, const SlotRef &sr, int slot, int proj, int p, int ks, _Float16 *prep,
-                            float *red) {
+                            float *red, int tu = 1 << 30, int ttot = 0) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = slot / a.nslot;
   const int IT = a.hid >> 4, ktn = IT / a.ksplit, k0 = ks * ktn, n = ktn * 16;
@@ -497,11 +517,13 @@ __device__ void gateup_unit(const MoeArgs &a, const SlotRef &sr, int slot, int p
     if (i1 < n) prep[kp(i1)] = to_f16(v1);
   }
   __syncthreads();
+  trace_mark(a, tu, ttot, 3);
   float acc0, acc1;
   pair_gemv<K>(buf, pb, L, k0, k0 + ktn, prep, acc0, acc1);
   const float s = pair_reduce(acc0, acc1, red);
+  trace_mark(a, tu, ttot, 4);
   const int o = p * 32 + (int)threadIdx.x;
-  if (threadIdx.x < 32 && o < a.inter) a.guo[(((uint64_t)slot * 2 + proj) * a.ksplit + ks) * a.inter + o] = s;
+  if (threadIdx.x < 32 && o < a.inter) st_cg(a.guo + (((uint64_t)slot * 2 + proj) * a.ksplit + ks) * a.inter + o, s);
   __syncthreads();
 }
 
@@ -529,15 +551,16 @@ __device__ bool down_unit(const MoeArgs &a, const SlotRef &sr, int slot, int p, 
   for (int c = wave; c * 128 < inter; c += 4) {
     const int i0 = c * 128 + lane, i1 = i0 + 64;
     const bool m0 = i0 < inter, m1 = i1 < inter;
-    float g0 = m0 ? gp[i0] : 0.f, g1 = m1 ? gp[i1] : 0.f, u0 = m0 ? up[i0] : 0.f, u1 = m1 ? up[i1] : 0.f;
+    float g0 = m0 ? ld_cg(gp + i0) : 0.f, g1 = m1 ? ld_cg(gp + i1) : 0.f;
+    float u0 = m0 ? ld_cg(up + i0) : 0.f, u1 = m1 ? ld_cg(up + i1) : 0.f;
     for (int s = 1; s < a.ksplit; s++) {
       if (m0) {
-        g0 += gp[s * inter + i0];
-        u0 += up[s * inter + i0];
+        g0 += ld_cg(gp + s * inter + i0);
+        u0 += ld_cg(up + s * inter + i0);
       }
       if (m1) {
-        g1 += gp[s * inter + i1];
-        u1 += up[s * inter + i1];
+        g1 += ld_cg(gp + s * inter + i1);
+        u1 += ld_cg(up + s * inter + i1);
       }
     }
     fwht2(g0, g1, lane, a.had_inter, a.sc_inter);
@@ -562,7 +585,7 @@ __device__ bool down_unit(const MoeArgs &a, const SlotRef &sr, int slot, int p, 
   pair_gemv<K>(buf, pb, L, 0, IT, prep, acc0, acc1);
   const float s = pair_reduce(acc0, acc1, red);
   const int o = p * 32 + (int)threadIdx.x;
-  if (threadIdx.x < 32 && o < a.hid) a.dn[(uint64_t)slot * a.hid + o] = s;
+  if (threadIdx.x < 32 && o < a.hid) st_cg(a.dn + (uint64_t)slot * a.hid + o, s);
   __syncthreads();
   return true;
 }
@@ -575,13 +598,15 @@ __device__ void combine_block(const MoeArgs &a, int r, int c, float (*vs)[128]) 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int i0 = c * 128 + lane, i1 = i0 + 64;
   const bool m0 = i0 < a.hid, m1 = i1 < a.hid;
-  for (int k = wave; k < a.nslot; k += 4) {
+  const int nw = (int)(blockDim.x >> 6);
+  for (int k = wave; k < a.nslot; k += nw) {
     const int slot = r * a.nslot + k;
     const SlotRef sr = slot_ref(a, r, k);
-    const float w = k < a.topk ? __uint_as_float(a.route[(uint64_t)r * 2 * a.topk + a.topk + k]) : a.sgv[r];
+    const float w = k < a.topk ? __uint_as_float(ld_cg(a.route + (uint64_t)r * 2 * a.topk + a.topk + k))
+                               : ld_cg(a.sgv + r);
     const float *d = a.dn + (uint64_t)slot * a.hid;
     const uint16_t *sv = (const uint16_t *)(sr.blk + off_sv(a, sr.sh, 2));
-    float v0 = m0 ? d[i0] : 0.f, v1 = m1 ? d[i1] : 0.f;
+    float v0 = m0 ? ld_cg(d + i0) : 0.f, v1 = m1 ? ld_cg(d + i1) : 0.f;
     const float s0 = m0 ? h2f(sv[i0]) : 0.f, s1 = m1 ? h2f(sv[i1]) : 0.f;
     fwht2(v0, v1, lane, a.had_hid, a.sc_hid);
     vs[k][lane] = v0 * s0 * w;
@@ -605,9 +630,9 @@ __global__ __launch_bounds__(256) void moe_router(MoeArgs a) {
   __shared__ uint32_t sid[kMaxTopk];
   __shared__ uint32_t cand[4 * kMaxTopk];
   __shared__ int flag;
-  router_rows(a, blockIdx.x);
+  __shared__ float xs[kRouterChunks * 512];
+  router_rows(a, blockIdx.x, xs);
   if (block_signal(a.sync + kSyncRouterDone, &flag) != gridDim.x - 1u) return;
-  block_acquire();
   route_rows(a, lv, cand, sid);
   if (threadIdx.x == 0) atomicExch(a.sync + kSyncRouterDone, 0u);
 }
@@ -645,123 +670,500 @@ __global__ __launch_bounds__(256) void moe_combine(MoeArgs a) {
 }
 
 // ------------------------------------------------------------------------------------------------ fused layer kernel
-// The whole layer step in one launch. Workgroups take units from an ordered queue (atomic head):
-//   [router rows] [shared-expert gate/up] [routed gate/up, slot-major] [down: shared slot first, then routed]
-// A unit only ever waits on units before it in the queue (route ready <- all router units; a slot's down units <-
-// its gate/up units), and a workgroup takes a new unit only after finishing the previous one, so the units waited on
-// are already held by running workgroups: the queue makes progress whatever number of workgroups is resident.
-// The last router unit to finish computes the route; the last down unit of each (row, 128-column block) runs the
-// combine for that block (fixed slot order: deterministic). The workgroup whose final (empty) take is the last one
-// of the grid resets every counter for the next launch / graph replay.
-struct FusedShape {
-  int NPg, NPd, nblk, n0, n1, n2, n3, total, per_slot;
+// The whole layer step in one launch, one 8-wave workgroup per CU. Work comes from three ordered queues (atomic heads):
+//   A: router units (one router row per wave); the last to finish computes the route and publishes it;
+//   G: gate/up wave units (slot, gate|up, k split, output tile pair): [shared slots][routed slots, slot-major];
+//   D: down wave units (slot, output tile pair), per row the shared slot first.
+// A wave unit is one output tile pair over 32 k tiles (64 tiles: 10 KB at K5), the work of one wave. Each round a
+// workgroup takes NG gate/up and ND down units and streams all their tiles straight into LDS (global_load_lds_dwordx4)
+// before computing, so the chip has nearly the whole layer's expert weights in flight once the route is known, and
+// every CU takes part in both the gate/up and the down phase. A round's gate/up units are computed and signalled
+// before its down units wait, so a round never waits on itself; units only wait on units earlier in the queues,
+// which running workgroups hold, so progress does not depend on how many workgroups are resident. The last down unit
+// of each (row, 128-column block) combines it (fixed slot order). The last workgroup to leave resets every counter
+// for the next launch.
+constexpr int kF2Waves = 16;
+constexpr int kF2KT = 32;    // k tiles per wave unit
+constexpr int kMaxRows = 4;  // rows (tokens) of one fused step
+constexpr uint32_t kF2UnitBytesK = 2 * kF2KT * 32;  // LDS bytes of one wave unit's tiles per unit of K (x K)
+enum {
+  kSyncHeadG = 4 * kSyncStride,
+  kSyncHeadD = 5 * kSyncStride,
+  kSyncRouteReady2 = 6 * kSyncStride,
+  kSyncExit = 7 * kSyncStride
 };
-__device__ __forceinline__ FusedShape fused_shape(const MoeArgs &a) {
-  FusedShape f;
-  f.NPg = (a.inter / 16 + 1) / 2;
-  f.NPd = (a.hid / 16 + 1) / 2;
-  f.nblk = (a.hid + 127) / 128;
-  f.per_slot = 2 * f.NPg * a.ksplit;
-  f.n0 = (a.ne + a.has_sgate + 3) / 4;
-  f.n1 = (a.nslot > a.topk) ? a.R * f.per_slot : 0;
-  f.n2 = a.R * a.topk * f.per_slot;
-  f.n3 = a.R * a.nslot * f.NPd;
-  f.total = f.n0 + f.n1 + f.n2 + f.n3;
+// units per round (gate/up, down) by the widest bit width: the LDS holds NG + ND wave units
+template <int KM>
+struct F2Take {
+  static constexpr int NG = KM <= 6 ? 6 : 5;
+  static constexpr int ND = KM <= 6 ? 3 : 2;
+};
+
+struct F2Shape {
+  int nA, NPg, NPd, gu_slot, nsh, nG, nD, nblk, IT, ITd;
+};
+__device__ __forceinline__ F2Shape f2_shape(const MoeArgs &a) {
+  F2Shape f;
+  f.nA = (a.ne + a.has_sgate + kF2Waves - 1) / kF2Waves;  // one router row per wave
+  f.NPg = a.inter / 32;
+  f.NPd = a.hid / 32;
+  f.gu_slot = 2 * a.ksplit * f.NPg;
+  f.nsh = (a.nslot > a.topk) ? a.R * f.gu_slot : 0;
+  f.nG = f.nsh + a.R * a.topk * f.gu_slot;
+  f.nD = a.R * a.nslot * f.NPd;
+  f.nblk = a.hid / 128;
+  f.IT = a.hid / 16;
+  f.ITd = a.inter / 16;
   return f;
 }
 
-__device__ __forceinline__ int grab_unit(uint32_t *sync, int *s_unit) {
-  if (threadIdx.x == 0) *s_unit = (int)atomicAdd(sync + kSyncHead, 1u);
-  __syncthreads();
-  const int u = *s_unit;
-  __syncthreads();
+struct F2Route {  // the workgroup's copy of the route
+  uint32_t id[kMaxRows][kMaxTopk];
+  float w[kMaxRows][kMaxTopk];
+  float sg[kMaxRows];
+  int ready;
+};
+
+struct F2Unit {
+  int valid, r, k, slot, proj, ks, p, sh;
+};
+__device__ __forceinline__ F2Unit f2_gu_unit(const MoeArgs &a, const F2Shape &f, int v) {
+  F2Unit u;
+  u.valid = v < f.nG;
+  int w;
+  if (v < f.nsh) {
+    u.r = v / f.gu_slot;
+    u.k = a.topk;
+    w = v % f.gu_slot;
+  } else {
+    const int v2 = v - f.nsh, sidx = v2 / f.gu_slot;
+    u.r = sidx / a.topk;
+    u.k = sidx % a.topk;
+    w = v2 % f.gu_slot;
+  }
+  u.proj = w / (a.ksplit * f.NPg);
+  u.ks = (w / f.NPg) % a.ksplit;
+  u.p = w % f.NPg;
+  u.slot = u.r * a.nslot + u.k;
+  u.sh = u.k >= a.topk;
+  return u;
+}
+__device__ __forceinline__ F2Unit f2_dn_unit(const MoeArgs &a, const F2Shape &f, int v) {
+  F2Unit u;
+  u.valid = v < f.nD;
+  const int q = v / f.NPd, j = q % a.nslot;
+  u.p = v % f.NPd;
+  u.r = q / a.nslot;
+  u.k = (a.nslot > a.topk) ? (j == 0 ? a.topk : j - 1) : j;
+  u.slot = u.r * a.nslot + u.k;
+  u.sh = u.k >= a.topk;
+  u.proj = 2;
+  u.ks = 0;
   return u;
 }
 
-// The queue is walked in three loops, one per unit kind, so each loop keeps only its own values live. Instantiated per
-// (routed K, shared K): one decoder per expert kind keeps the register budget at 3 workgroups per CU.
-#define IJ_FUSED_K(CALL)          \
-  if (sr.sh) {                    \
-    constexpr int KK = KS;        \
-    CALL;                         \
-  } else {                        \
-    constexpr int KK = K;         \
-    CALL;                         \
-  }
-template <int K, int KS>
-__global__ __launch_bounds__(256, 3) void moe_fused(MoeArgs a) {
-  __shared__ _Float16 prep[kMaxPrep];
-  __shared__ float red[128];
-  __shared__ float lv[kMaxExperts];
-  __shared__ uint32_t sid[kMaxTopk];
-  __shared__ uint32_t cand[4 * kMaxTopk];
-  __shared__ float vs[kMaxSlots][128];
-  __shared__ int flag, s_unit;
-  const FusedShape f = fused_shape(a);
-  uint32_t *sync = a.sync;
-  uint32_t *gu_done = sync + kSyncSlots;
-  uint32_t *blk_cnt = gu_done + a.R * a.nslot;
-  int u = grab_unit(sync, &s_unit);
-  // router rows; the last to finish computes the route
-  for (; u < f.n0; u = grab_unit(sync, &s_unit)) {
-    if (ld_acq(sync + kSyncErr)) continue;
-    router_rows(a, u);
-    if (block_signal(sync + kSyncRouterDone, &flag) == (uint32_t)f.n0 - 1u) {
-      block_acquire();
-      route_rows(a, lv, cand, sid);
-      block_signal(sync + kSyncRouteReady, &flag);
+// Route of every row from the logits, by the last router workgroup, published to the route / shared-gate buffers.
+__device__ void f2_route_publish(const MoeArgs &a, float *lv, uint32_t *cand, uint32_t *sid, int tu) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, ld = a.ne + 1;
+  for (int r = 0; r < a.R; r++) {
+    for (int i = threadIdx.x; i < a.ne; i += blockDim.x) lv[i] = ld_cg(a.logits + (uint64_t)r * ld + i);
+    __syncthreads();
+    trace_mark(a, tu, 1 << 30, 3);
+    block_topk(lv, a.ne, a.topk, cand, sid);
+    trace_mark(a, tu, 1 << 30, 4);
+    if (wave == 0) {
+      const uint32_t id = lane < a.topk ? sid[lane] : 0u;
+      const float top = lv[sid[0]];
+      const float pk = lane < a.topk ? expf(lv[id] - top) : 0.f;
+      float s = 0.f;
+      for (int k = 0; k < a.topk; k++) s += __shfl(pk, k, 64);  // slot order, as the reference's finisher
+      if (lane < a.topk) {
+        st_cg(a.route + (uint64_t)r * 2 * a.topk + lane, id);
+        st_cg(a.route + (uint64_t)r * 2 * a.topk + a.topk + lane, __float_as_uint(pk / s));
+      }
+      if (lane == 0)
+        st_cg(a.sgv + r, a.has_sgate ? 1.f / (1.f + expf(-ld_cg(a.logits + (uint64_t)r * ld + a.ne))) : 1.f);
     }
-  }
-  // gate/up: shared slots (one per row) first, then routed slots (row-major, k order)
-  for (; u < f.n0 + f.n1 + f.n2; u = grab_unit(sync, &s_unit)) {
-    if (ld_acq(sync + kSyncErr)) continue;
-    int v = u - f.n0, r, k;
-    if (v < f.n1) {
-      r = v / f.per_slot;
-      k = a.topk;
-    } else {
-      v -= f.n1;
-      const int sidx = v / f.per_slot;
-      r = sidx / a.topk;
-      k = sidx % a.topk;
-    }
-    const int w = v % f.per_slot;
-    const int ks = w % a.ksplit, p = (w / a.ksplit) % f.NPg, proj = w / (a.ksplit * f.NPg);
-    if (k < a.topk && !block_wait_geq(sync, sync + kSyncRouteReady, 1u, &flag)) continue;
-    const int slot = r * a.nslot + k;
-    const SlotRef sr = slot_ref(a, r, k);
-    IJ_FUSED_K(gateup_unit<KK>(a, sr, slot, proj, p, ks, prep, red));
-    block_signal(gu_done + slot, &flag);
-  }
-  // down: per row, the shared slot first, then the routed slots; the last unit of each 128-column block combines it
-  for (; u < f.total; u = grab_unit(sync, &s_unit)) {
-    if (ld_acq(sync + kSyncErr)) continue;
-    const int v = u - f.n0 - f.n1 - f.n2;
-    const int p = v % f.NPd, q = v / f.NPd, r = q / a.nslot, j = q % a.nslot;
-    const int k = (a.nslot > a.topk) ? (j == 0 ? a.topk : j - 1) : j;
-    if (k < a.topk && !block_wait_geq(sync, sync + kSyncRouteReady, 1u, &flag)) continue;
-    const int slot = r * a.nslot + k;
-    const SlotRef sr = slot_ref(a, r, k);
-    bool ok = false;
-    IJ_FUSED_K(ok = down_unit<KK>(a, sr, slot, p, prep, red, gu_done + slot, (uint32_t)f.per_slot, &flag));
-    if (!ok) continue;
-    const int c = (p * 32) / 128;
-    const uint32_t arrivals = (uint32_t)a.nslot * (uint32_t)min(4, f.NPd - c * 4);
-    if (block_signal(blk_cnt + r * f.nblk + c, &flag) == arrivals - 1u) {
-      block_acquire();
-      combine_block(a, r, c, vs);
-    }
-  }
-  // the grid's last (empty) take resets the counters for the next launch
-  if (threadIdx.x == 0 && u == f.total + (int)gridDim.x - 1) {
-    for (int i = 0; i < a.R * a.nslot; i++) gu_done[i] = 0u;
-    for (int i = 0; i < a.R * f.nblk; i++) blk_cnt[i] = 0u;
-    sync[kSyncRouterDone] = 0u;
-    sync[kSyncRouteReady] = 0u;
-    __threadfence();
-    atomicExch(sync + kSyncHead, 0u);
+    __syncthreads();
   }
 }
+// the workgroup's copy of the published route (waits for it)
+__device__ bool f2_route_fetch(const MoeArgs &a, F2Route *rt, int *flag) {
+  if (!block_wait_geq(a.sync, a.sync + kSyncRouteReady2, 1u, flag)) return false;
+  for (int i = threadIdx.x; i < a.R * a.topk; i += blockDim.x) {
+    const int r = i / a.topk, k = i % a.topk;
+    rt->id[r][k] = ld_cg(a.route + (uint64_t)r * 2 * a.topk + k);
+    rt->w[r][k] = __uint_as_float(ld_cg(a.route + (uint64_t)r * 2 * a.topk + a.topk + k));
+  }
+  if (threadIdx.x < a.R) rt->sg[threadIdx.x] = ld_cg(a.sgv + threadIdx.x);
+  if (threadIdx.x == 0) rt->ready = 1;
+  __syncthreads();
+  return true;
+}
+
+__device__ __forceinline__ const uint8_t *f2_block(const MoeArgs &a, const F2Route *rt, int r, int k) {
+  if (k >= a.topk) return a.shared;
+  uint32_t e = rt->id[r][k];
+  e = e < (uint32_t)a.ne ? e : 0u;
+  return a.experts + (uint64_t)e * a.lay.bytes;
+}
+
+// stream a wave unit's tiles (pair p, k tiles [k0, k0 + nkt) of a re-laid matrix) into this wave's LDS buffer
+__device__ __forceinline__ void f2_stream(const uint8_t *tr, int IT, int p, int k0, int nkt, uint32_t tb,
+                                          uint8_t *dst) {
+  const int lane = threadIdx.x & 63;
+  const uint8_t *src = tr + ((uint64_t)p * IT + k0) * 2 * tb;
+  const uint32_t bytes = (uint32_t)nkt * 2 * tb;
+  for (uint32_t o = 0; o < bytes; o += 1024)
+    if (o + (uint32_t)lane * 16 < bytes)
+      __builtin_amdgcn_global_load_lds((const void *)(src + o + lane * 16),
+                                       (__attribute__((address_space(3))) void *)(dst + o), 16, 0, 0);
+}
+
+// one wave: its unit's output tile pair over nkt k tiles from the LDS-staged tiles; returns the two column sums on
+// the lanes with (lane & 6) == 0 (column (lane >> 3) + 8 (lane & 1) of each tile)
+template <int K>
+__device__ __forceinline__ void f2_pair_dot(const uint8_t *tl, const _Float16 *xs, int nkt, float &acc0, float &acc1) {
+  constexpr int TW = 8 * K;
+  const int lane = threadIdx.x & 63;
+  const TileLane<K> L = tile_lane<K>((uint32_t)lane);
+  const int q = (lane >> 1) & 3;
+  acc0 = 0.f;
+  acc1 = 0.f;
+  const uint32_t *T = (const uint32_t *)tl;
+#pragma unroll 4
+  for (int kt = 0; kt < nkt; kt++) {
+    const uint32_t *T0 = T + kt * 2 * TW;
+    TileWords wa, wb;
+    wa.w0 = T0[L.i0];
+    wa.w1 = T0[L.i1];
+    wa.w2 = kThreeWords<K> ? T0[L.i2] : 0u;
+    wb.w0 = T0[TW + L.i0];
+    wb.w1 = T0[TW + L.i1];
+    wb.w2 = kThreeWords<K> ? T0[TW + L.i2] : 0u;
+    const f16x4 xv = *(const f16x4 *)(xs + kt * 16 + 4 * q);
+    f16x2 a0, b0, a1, b1;
+    decode4<K>(wa, L.sh, a0, b0);
+    decode4<K>(wb, L.sh, a1, b1);
+    acc0 = dot4(a0, b0, xv, acc0);
+    acc1 = dot4(a1, b1, xv, acc1);
+  }
+  lane_col_reduce(acc0, acc1);
+}
+
+// combine for (row r, 128-column block c) from the workgroup's route copy (the arithmetic of combine_block)
+__device__ void f2_combine(const MoeArgs &a, const F2Route *rt, int r, int c, float (*vs)[128]) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = (int)(blockDim.x >> 6);
+  const int i0 = c * 128 + lane, i1 = i0 + 64;
+  for (int k = wave; k < a.nslot; k += nw) {
+    const int slot = r * a.nslot + k;
+    const uint8_t *blk = f2_block(a, rt, r, k);
+    const int sh = k >= a.topk;
+    const float w = sh ? rt->sg[r] : rt->w[r][k];
+    const float *d = a.dn + (uint64_t)slot * a.hid;
+    const uint16_t *sv = (const uint16_t *)(blk + off_sv(a, sh, 2));
+    float v0 = ld_cg(d + i0), v1 = ld_cg(d + i1);
+    const float s0 = h2f(sv[i0]), s1 = h2f(sv[i1]);
+    fwht2(v0, v1, lane, a.had_hid, a.sc_hid);
+    vs[k][lane] = v0 * s0 * w;
+    vs[k][lane + 64] = v1 * s1 * w;
+  }
+  __syncthreads();
+  if (threadIdx.x < 128) {
+    float y = 0.f;
+    for (int k = 0; k < a.nslot; k++) y += vs[k][threadIdx.x];
+    a.y[(uint64_t)r * a.hid + c * 128 + threadIdx.x] = y;
+  }
+  __syncthreads();
+}
+
+// Gate/up block finisher: the last gate/up unit of (slot, 128-column block cb of inter) sums the k splits in order and
+// applies the down unit's prologue (reference kernels/fn_moe.metal:370-384): g = H(inner_g) * svh_g,
+// u = H(inner_u) * svh_u, h = H(silu(g) u * suh_d), rounded to fp16 and stored in the k-permuted order the down units
+// stage (hprep). One wave; `stage` = 128 halves of this wave's LDS.
+constexpr int kMaxKsplit = 8;
+__device__ void f2_gu_finish(const MoeArgs &a, const uint8_t *blk, int sh, int slot, int cb, _Float16 *stage) {
+  const int lane = threadIdx.x & 63, inter = a.inter;
+  const float *gp = a.guo + (uint64_t)slot * 2 * a.ksplit * inter;
+  const float *up = gp + (uint64_t)a.ksplit * inter;
+  const int i0 = cb * 128 + lane, i1 = i0 + 64;
+  float gv[kMaxKsplit][2], uv[kMaxKsplit][2];
+#pragma unroll
+  for (int s2 = 0; s2 < kMaxKsplit; s2++) {  // every partial requested before the first is used
+    if (s2 < a.ksplit) {
+      gv[s2][0] = ld_cg(gp + s2 * inter + i0);
+      gv[s2][1] = ld_cg(gp + s2 * inter + i1);
+      uv[s2][0] = ld_cg(up + s2 * inter + i0);
+      uv[s2][1] = ld_cg(up + s2 * inter + i1);
+    }
+  }
+  const float sg0 = h2f(((const uint16_t *)(blk + off_sv(a, sh, 0)))[i0]);
+  const float sg1 = h2f(((const uint16_t *)(blk + off_sv(a, sh, 0)))[i1]);
+  const float su0 = h2f(((const uint16_t *)(blk + off_sv(a, sh, 1)))[i0]);
+  const float su1 = h2f(((const uint16_t *)(blk + off_sv(a, sh, 1)))[i1]);
+  const float sd0 = h2f(((const uint16_t *)(blk + off_su(a, sh, 2)))[i0]);
+  const float sd1 = h2f(((const uint16_t *)(blk + off_su(a, sh, 2)))[i1]);
+  float g0 = gv[0][0], g1 = gv[0][1], u0 = uv[0][0], u1 = uv[0][1];
+#pragma unroll
+  for (int s2 = 1; s2 < kMaxKsplit; s2++) {
+    if (s2 < a.ksplit) {
+      g0 += gv[s2][0];
+      g1 += gv[s2][1];
+      u0 += uv[s2][0];
+      u1 += uv[s2][1];
+    }
+  }
+  fwht2(g0, g1, lane, a.had_inter, a.sc_inter);
+  fwht2(u0, u1, lane, a.had_inter, a.sc_inter);
+  g0 = g0 * sg0;
+  u0 = u0 * su0;
+  g1 = g1 * sg1;
+  u1 = u1 * su1;
+  float h0 = g0 / (1.f + expf(-g0)) * u0 * sd0;
+  float h1 = g1 / (1.f + expf(-g1)) * u1 * sd1;
+  fwht2(h0, h1, lane, a.had_inter, a.sc_inter);
+  stage[kp(lane)] = to_f16(h0);
+  stage[kp(lane + 64)] = to_f16(h1);
+  __builtin_amdgcn_wave_barrier();
+  const uint32_t word = ((const uint32_t *)stage)[lane];  // 128 halves = 64 words, one per lane
+  st_cg((uint32_t *)(a.hprep + (uint64_t)slot * inter + cb * 128) + lane, word);
+}
+
+#define IJ_F2_K(SH, CALL)   \
+  if (SH) {                 \
+    constexpr int KK = KS;  \
+    CALL;                   \
+  } else {                  \
+    constexpr int KK = K;   \
+    CALL;                   \
+  }
+
+template <int K, int KS>
+__global__ __launch_bounds__(1024, 1) void moe_fused(MoeArgs a) {
+  constexpr int KM = K > KS ? K : KS;
+  constexpr int NG = F2Take<KM>::NG, ND = F2Take<KM>::ND;
+  constexpr uint32_t UB = kF2UnitBytesK * KM;  // LDS bytes per wave unit buffer
+  extern __shared__ __attribute__((aligned(16))) uint8_t f2_tiles[];  // (NG + ND) x UB
+  __shared__ _Float16 prep_g[NG][512];
+  __shared__ _Float16 prep_d[ND][512];
+  __shared__ float red[kF2Waves][32];
+  __shared__ float lv[kMaxExperts];
+  __shared__ uint32_t sid[kMaxTopk];
+  __shared__ float vs[kMaxSlots][128];
+  __shared__ F2Route rt;
+  __shared__ int flag, s_g, s_d, s_last[ND], s_fin[NG];
+  const F2Shape f = f2_shape(a);
+  uint32_t *sync = a.sync;
+  uint32_t *gu_done = sync + kSyncSlots;                        // [slot * kSyncStride]: finished 128-blocks
+  uint32_t *blk_cnt = gu_done + a.R * a.nslot * kSyncStride;    // [(r * nblk + c) * kSyncStride]
+  uint32_t *fin_cnt = blk_cnt + a.R * f.nblk * kSyncStride;     // [(slot * nbi + cb) * kSyncStride]
+  const int nbi = a.inter / 128;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int G = (int)gridDim.x;
+  if (threadIdx.x == 0) rt.ready = 0;
+
+  // ---- queue A: router rows (the first G statically, one per workgroup); the last to finish publishes the route
+  for (int u = blockIdx.x;;) {
+    if (u >= f.nA) break;
+    trace_mark(a, u, 1 << 30, 0);
+    router_rows(a, u, &vs[0][0]);
+    trace_mark(a, u, 1 << 30, 1);
+    if (block_signal(sync + kSyncRouterDone, &flag) == (uint32_t)f.nA - 1u) {
+      f2_route_publish(a, lv, nullptr, sid, u);
+      trace_mark(a, u, 1 << 30, 5);
+      block_signal(sync + kSyncRouteReady2, &flag);
+    }
+    trace_mark(a, u, 1 << 30, 2);
+    if (threadIdx.x == 0) s_g = G + (int)atomicAdd(sync + kSyncHead, 1u);
+    __syncthreads();
+    u = s_g;
+    __syncthreads();
+  }
+
+  // ---- rounds of NG gate/up + ND down wave units; the first round is static, later ones come from the heads.
+  // Waves: gate/up task w < 2 NG = unit w / 2, k half w % 2; down task w < 4 ND = unit w / 4, k quarter w % 4;
+  // stream: wave w < NG + ND loads unit buffer w (gate/up units first).
+  for (int round = 0;; round++) {
+    if (round > 0) {
+      if (threadIdx.x == 0) {
+        s_g = G * NG + (int)atomicAdd(sync + kSyncHeadG, (uint32_t)NG);
+        s_d = G * ND + (int)atomicAdd(sync + kSyncHeadD, (uint32_t)ND);
+      }
+      __syncthreads();
+    }
+    const int g0 = round > 0 ? s_g : (int)blockIdx.x * NG, d0 = round > 0 ? s_d : (int)blockIdx.x * ND;
+    __syncthreads();
+    if (g0 >= f.nG && d0 >= f.nD) break;
+    const int tu = f.nA + g0 / NG;
+    trace_mark(a, tu, 1 << 30, 0);
+    bool routed = false;
+#pragma unroll
+    for (int i = 0; i < NG; i++) routed |= (g0 + i < f.nG) && (g0 + i >= f.nsh);
+    routed |= d0 < f.nD;
+    if (routed && !rt.ready && !f2_route_fetch(a, &rt, &flag)) continue;
+    trace_mark(a, tu, 1 << 30, 1);
+
+    const int gi = wave >> 1, gh = wave & 1, dj = wave >> 2, dq = wave & 3;
+    const F2Unit Gt = f2_gu_unit(a, f, g0 + gi);                 // this wave's gate/up task unit
+    const bool hasG = wave < 2 * NG && Gt.valid;
+    const uint8_t *gblk = hasG ? f2_block(a, &rt, Gt.r, Gt.k) : nullptr;
+    // gate/up prep inputs (this wave's two 128-chunks of its unit's 512) first, then the tile stream
+    float xv[4], sv[4];
+    if (hasG) {
+      const float *x = a.x + (uint64_t)Gt.r * a.hid + Gt.ks * kF2KT * 16 + gh * 256;
+      const uint16_t *su = (const uint16_t *)(gblk + off_su(a, Gt.sh, Gt.proj)) + Gt.ks * kF2KT * 16 + gh * 256;
+#pragma unroll
+      for (int h = 0; h < 4; h++) {
+        xv[h] = x[h * 64 + lane];
+        sv[h] = h2f(su[h * 64 + lane]);
+      }
+    }
+    if (wave < NG + ND) {  // stream one unit's tiles
+      const bool isg = wave < NG;
+      const F2Unit S = isg ? f2_gu_unit(a, f, g0 + wave) : f2_dn_unit(a, f, d0 + wave - NG);
+      if (S.valid) {
+        const uint8_t *sblk = f2_block(a, &rt, S.r, S.k);
+        const uint32_t tb = 32u * (uint32_t)(S.sh ? KS : K);
+        if (isg)
+          f2_stream(sblk + off_tr(a, S.sh, S.proj), f.IT, S.p, S.ks * kF2KT, kF2KT, tb, f2_tiles + (uint32_t)wave * UB);
+        else
+          f2_stream(sblk + off_tr(a, S.sh, 2), f.ITd, S.p, 0, f.ITd, tb, f2_tiles + (uint32_t)wave * UB);
+      }
+    }
+    if (hasG) {
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        float v0 = xv[2 * h] * sv[2 * h], v1 = xv[2 * h + 1] * sv[2 * h + 1];
+        fwht2(v0, v1, lane, a.had_hid, a.sc_hid);
+        const int e = gh * 256 + h * 128 + lane;
+        prep_g[gi][kp(e)] = to_f16(v0);
+        prep_g[gi][kp(e + 64)] = to_f16(v1);
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    trace_mark(a, tu, 1 << 30, 2);
+
+    // gate/up: each wave half the unit's k tiles; the second half's sums meet the first's in LDS (fixed order)
+    float g_acc0 = 0.f, g_acc1 = 0.f;
+    if (hasG) {
+      const uint8_t *tl = f2_tiles + (uint32_t)gi * UB + (uint32_t)gh * (kF2KT / 2) * 2 * 32u * (Gt.sh ? KS : K);
+      IJ_F2_K(Gt.sh, f2_pair_dot<KK>(tl, prep_g[gi] + gh * (kF2KT / 2) * 16, kF2KT / 2, g_acc0, g_acc1));
+      if (gh == 1 && (lane & 6) == 0) {
+        const int col = (lane >> 3) + 8 * (lane & 1);
+        red[wave][col] = g_acc0;
+        red[wave][16 + col] = g_acc1;
+      }
+    }
+    __syncthreads();
+    if (hasG && gh == 0 && (lane & 6) == 0) {
+      const int col = (lane >> 3) + 8 * (lane & 1);
+      float *g = a.guo + (((uint64_t)Gt.slot * 2 + Gt.proj) * a.ksplit + Gt.ks) * a.inter + Gt.p * 32;
+      st_cg(g + col, g_acc0 + red[wave + 1][col]);
+      st_cg(g + 16 + col, g_acc1 + red[wave + 1][16 + col]);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    // count the units per (slot, 128-column block); the last one of a block finishes it (one wave per block)
+    if (threadIdx.x == 0) {
+#pragma unroll
+      for (int i = 0; i < NG; i++) {
+        s_fin[i] = -1;
+        const F2Unit Gi = f2_gu_unit(a, f, g0 + i);
+        if (!Gi.valid) continue;
+        const int cb = Gi.p / 4;
+        const uint32_t old = atomicAdd(fin_cnt + (Gi.slot * nbi + cb) * kSyncStride, 1u);
+        if (old == 8u * (uint32_t)a.ksplit - 1u) s_fin[i] = Gi.slot * nbi + cb;  // 2 proj x ksplit x 4 pairs
+      }
+    }
+    __syncthreads();
+    if (wave < NG && s_fin[wave] >= 0) {
+      const int fs = s_fin[wave] / nbi, cb = s_fin[wave] % nbi;
+      f2_gu_finish(a, f2_block(a, &rt, fs / a.nslot, fs % a.nslot), (fs % a.nslot) >= a.topk, fs, cb,
+                   prep_g[wave]);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+#pragma unroll
+      for (int i = 0; i < NG; i++)
+        if (s_fin[i] >= 0) atomicAdd(gu_done + (s_fin[i] / nbi) * kSyncStride, 1u);
+    }
+    trace_mark(a, tu, 1 << 30, 3);
+    if (d0 >= f.nD) continue;
+
+    // down: wait for each unit's slot, stage its finished input, each wave a quarter of the k tiles, sums in LDS
+    bool ok = true;
+#pragma unroll
+    for (int i = 0; i < ND; i++) {
+      const F2Unit Di = f2_dn_unit(a, f, d0 + i);
+      if (Di.valid && ok) ok = block_wait_geq(sync, gu_done + Di.slot * kSyncStride, (uint32_t)nbi, &flag);
+    }
+    if (!ok) continue;
+    trace_mark(a, tu, 1 << 30, 4);
+    const F2Unit Dt = f2_dn_unit(a, f, d0 + dj);
+    const bool hasD = wave < 4 * ND && Dt.valid;
+    if (hasD) {  // wave q of the unit stages words [64 q, 64 q + 64) of the slot's inter / 2 words
+      const uint32_t *hp = (const uint32_t *)(a.hprep + (uint64_t)Dt.slot * a.inter);
+      const int wi = dq * 64 + lane;
+      if (wi * 2 < a.inter) ((uint32_t *)prep_d[dj])[wi] = ld_cg(hp + wi);
+    }
+    __syncthreads();
+    float d_acc0 = 0.f, d_acc1 = 0.f;
+    const int qkt = f.ITd / 4;  // k tiles per quarter
+    if (hasD) {
+      const uint8_t *tl = f2_tiles + (uint32_t)(NG + dj) * UB + (uint32_t)dq * qkt * 2 * 32u * (Dt.sh ? KS : K);
+      IJ_F2_K(Dt.sh, f2_pair_dot<KK>(tl, prep_d[dj] + dq * qkt * 16, qkt, d_acc0, d_acc1));
+      if (dq > 0 && (lane & 6) == 0) {
+        const int col = (lane >> 3) + 8 * (lane & 1);
+        red[wave][col] = d_acc0;
+        red[wave][16 + col] = d_acc1;
+      }
+    }
+    __syncthreads();
+    if (hasD && dq == 0 && (lane & 6) == 0) {
+      const int col = (lane >> 3) + 8 * (lane & 1);
+      float *d = a.dn + (uint64_t)Dt.slot * a.hid + Dt.p * 32;
+      st_cg(d + col, ((d_acc0 + red[wave + 1][col]) + red[wave + 2][col]) + red[wave + 3][col]);
+      st_cg(d + 16 + col, ((d_acc1 + red[wave + 1][16 + col]) + red[wave + 2][16 + col]) + red[wave + 3][16 + col]);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    trace_mark(a, tu, 1 << 30, 5);
+    if (threadIdx.x == 0) {
+#pragma unroll
+      for (int i = 0; i < ND; i++) {
+        s_last[i] = -1;
+        const F2Unit Di = f2_dn_unit(a, f, d0 + i);
+        if (!Di.valid) continue;
+        const int c = Di.p / 4;  // 128-column block of the pair's 32 columns
+        const uint32_t old = atomicAdd(blk_cnt + (Di.r * f.nblk + c) * kSyncStride, 1u);
+        if (old == 4u * (uint32_t)a.nslot - 1u) s_last[i] = Di.r * f.nblk + c;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < ND; i++) {
+      const int rb = s_last[i];
+      if (rb >= 0) f2_combine(a, &rt, rb / f.nblk, rb % f.nblk, vs);
+    }
+    trace_mark(a, tu, 1 << 30, 6);
+  }
+  // the last workgroup to leave resets the counters for the next launch
+  if (threadIdx.x == 0 && atomicAdd(sync + kSyncExit, 1u) == gridDim.x - 1u) {
+    for (int i = 0; i < a.R * a.nslot; i++) st_cg(gu_done + i * kSyncStride, 0u);
+    for (int i = 0; i < a.R * f.nblk; i++) st_cg(blk_cnt + i * kSyncStride, 0u);
+    for (int i = 0; i < a.R * a.nslot * nbi; i++) st_cg(fin_cnt + i * kSyncStride, 0u);
+    st_cg(sync + kSyncRouterDone, 0u);
+    st_cg(sync + kSyncRouteReady2, 0u);
+    st_cg(sync + kSyncHead, 0u);
+    st_cg(sync + kSyncHeadG, 0u);
+    st_cg(sync + kSyncHeadD, 0u);
+    __builtin_amdgcn_s_waitcnt(0);
+    atomicExch(sync + kSyncExit, 0u);
+  }
+}
+#undef IJ_F2_K
 
 // ------------------------------------------------------------------------------------------------ trunk linear
 // lin_prep: xh[r][kp(i)] = fp16(H_in(x * suh)) (reference kernels/trunk6/trunk6.metal:68-85), grid R x ceil(in/128).
@@ -953,22 +1355,35 @@ static const void *fused_fn(int K, int KS) {
 #undef IJ_FUSED_CASE
   return nullptr;
 }
-bool moe_fused_supported(int K, int KS) { return fused_fn(K, KS) != nullptr; }
+static size_t fused_lds(int K, int KS) {
+  const int KM = std::max(K, KS);
+  return (size_t)(KM <= 6 ? F2Take<6>::NG + F2Take<6>::ND : F2Take<8>::NG + F2Take<8>::ND) * kF2UnitBytesK * KM;
+}
+// shapes the fused kernel serves: units of 2 output tile pairs x 32 k tiles, at most kMaxRows rows
+bool moe_fused_supported(int K, int KS, int R, int hid, int inter, int ksplit) {
+  return fused_fn(K, KS) != nullptr && R <= kMaxRows && hid % 512 == 0 && hid / 16 == ksplit * kF2KT &&
+         inter % 128 == 0 && inter / 16 <= kF2KT && inter <= 512;
+}
 int moe_fused_grid(int K, int KS) {
   const void *f = fused_fn(K, KS);
   IJ_CHECK(f, "fused MoE kernel not instantiated for K%d / shared K%d", K, KS);
-  int dev = 0, cus = 0, per = 0;
+  int dev = 0, cus = 0;
   IJ_HIP(hipGetDevice(&dev));
   IJ_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-  IJ_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, f, 256, 0));
-  return cus * std::max(1, std::min(per, 4));
+  return cus;
 }
 void launch_moe_fused(const MoeArgs &a, int grid, hipStream_t s) {
   const int KS = a.nslot > a.topk ? a.slay.K : a.lay.K;
   const void *f = fused_fn(a.lay.K, KS);
   IJ_CHECK(f, "fused MoE kernel not instantiated for K%d / shared K%d", a.lay.K, KS);
+  const size_t lds = fused_lds(a.lay.K, KS);
+  static bool attr_set[9][9] = {};
+  if (!attr_set[a.lay.K][KS]) {
+    IJ_HIP(hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    attr_set[a.lay.K][KS] = true;
+  }
   void *args[] = {const_cast<MoeArgs *>(&a)};
-  IJ_HIP(hipLaunchKernel(f, dim3(grid > 0 ? grid : moe_fused_grid(a.lay.K, KS)), dim3(256), args, 0, s));
+  IJ_HIP(hipLaunchKernel(f, dim3(grid > 0 ? grid : moe_fused_grid(a.lay.K, KS)), dim3(64 * kF2Waves), args, lds, s));
 }
 
 template <int K>

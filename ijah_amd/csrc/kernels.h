@@ -48,6 +48,8 @@ struct MoeArgs {
   float *guo;                          // [R nslot][2][ksplit][inter]
   float *dn;                           // [R nslot][hid]
   uint32_t *sync;                      // counters: see sync_words(); zero between launches (kernels reset them)
+  uint64_t *trace;                     // fused kernel: per unit {grab, ready, done} wall-clock ticks, or null
+  uint16_t *hprep;                     // fused kernel: [R nslot][inter] fp16 down inputs (kp order)
 };
 void launch_moe_router(const MoeArgs &a, hipStream_t s);
 void launch_moe_gateup(const MoeArgs &a, hipStream_t s);
@@ -56,10 +58,15 @@ void launch_moe_combine(const MoeArgs &a, hipStream_t s);
 // the whole layer step in one persistent launch (grid = workgroups; 0 = one per CU times the occupancy limit)
 void launch_moe_fused(const MoeArgs &a, int grid, hipStream_t s);
 int moe_fused_grid(int K, int KS);
-bool moe_fused_supported(int K, int KS);  // instantiated for this (routed K, shared K)
-// u32 words of the sync block for R rows: header, per-slot gate/up counters, per-(row, 128-column block) counters
-inline size_t sync_words(int R, int nslot, int hid) { return 8 + (size_t)R * nslot + (size_t)R * ((hid + 127) / 128); }
-enum { kSyncErrWord = 3 };
+bool moe_fused_supported(int K, int KS, int R, int hid, int inter, int ksplit);
+// The sync block for R rows: header counters, per-slot gate/up counters, per-(row, 128-column block) counters; every
+// counter sits alone in a 256-byte line so that polling workgroups do not contend on one line.
+constexpr int kSyncStride = 64;  // u32 words between counters
+inline size_t sync_words(int R, int nslot, int hid, int inter) {
+  return kSyncStride * (8 + (size_t)R * nslot + (size_t)R * ((hid + 127) / 128) +
+                        (size_t)R * nslot * ((inter + 127) / 128));
+}
+enum { kSyncErrWord = 3 * kSyncStride };
 
 struct LinArgs {
   const uint32_t *tiles;  // re-laid trellis
