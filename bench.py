@@ -38,7 +38,19 @@ def kernel_bytes(hid=HID, inter=INTER, ne=NE, topk=TOPK, k=K, shared=1):
             "combine": ns * hid * 2}
 
 
-def cpu_baseline(seconds=12.0):
+def profiled_traffic(kernel):
+    """HBM bytes per launch of the dominant kernel from the committed rocprofv3 PMC summary (FETCH_SIZE and
+    WRITE_SIZE, each scaled by the copy-probe factor), or None when no summary covers it."""
+    f = ROOT / "profiles" / "moe_fused_k5_config2.md"
+    if kernel != "fused" or not f.exists():
+        return None
+    for line in f.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(line.split(":")[1])
+    return None
+
+
+def cpu_baseline(seconds=10.0):
     """The oracle's OpenMP layer (router over 512 experts + top-10 + 10 routed and 1 shared K5 expert) on the
     host's cores; per-layer time from a bounded sample. Returns a dict for the JSON line."""
     from ijah_amd import synth
@@ -58,7 +70,7 @@ def cpu_baseline(seconds=12.0):
         _, used = O.moe_experts(W, x, rt, fast_threads=threads)
         n += 1
         el = time.perf_counter() - t0
-        if el > seconds or n >= 200:
+        if el > seconds or n >= 5000:
             break
     us = el / n * 1e6
     total = sum(kernel_bytes().values())
@@ -75,6 +87,10 @@ def main():
     ap.add_argument("--layers", type=int, default=32)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--eager-only", action="store_true",
+                    help="run the layer chain eagerly --steps times and exit (for rocprofv3 --pmc passes)")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MB",
+                    help="only run the plain copy kernel over MB MiB 5 times (scales --pmc byte counters) and exit")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {a.gpus}); the MoE layer shards by "
@@ -83,6 +99,13 @@ def main():
 
     import ijah_amd
     eng = ijah_amd.load_engine()
+    if a.copy_probe:
+        n = a.copy_probe << 20
+        src, dst = eng.alloc(n), eng.alloc(n)
+        for _ in range(5):
+            eng.run_kernel("copy_u128", [src, dst, np.uint64(n // 16)], (2048, 1, 1), (256, 1, 1))
+        print(json.dumps({"copy_probe_bytes": n, "launches": 5}), flush=True)
+        return
     t_setup = time.perf_counter()
     layers = [eng.moe_synth(HID, INTER, NE, TOPK, K, True, K, seed=a.seed * 1000 + i) for i in range(a.layers)]
     from ijah_amd import synth
@@ -96,6 +119,14 @@ def main():
     bytes_per_layer = float(np.mean(layer_bytes))
     print(f"setup {time.perf_counter() - t_setup:.1f}s, {a.layers} layers, {bytes_per_layer / 1e6:.2f} MB/layer",
           file=sys.stderr, flush=True)
+
+    if a.eager_only:
+        for _ in range(a.steps):
+            for m, yb in zip(layers, ybufs):
+                m.run_bufs(1, xb, yb)
+        eng.sync()
+        print(json.dumps({"eager_layers": a.steps * a.layers, "bytes_per_layer": int(bytes_per_layer)}), flush=True)
+        return
 
     eng.sync()
     wall0 = time.perf_counter()
@@ -128,7 +159,7 @@ def main():
         "wall_s_timed": round(wall, 3),
         "kernels_us": {k: round(v, 3) for k, v in kus.items()},
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": profiled_traffic(dom),
                      "bytes_per_launch": kb[dom]},
         "cpu_baseline": cpu,
     }

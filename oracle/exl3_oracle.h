@@ -4,7 +4,20 @@
  * __graft_entry__.smoke() and bench.py's cpu_baseline leg do, and there only as the checker / the timed CPU baseline.
  *
  * Every function restates the reference algorithm (publicExcess/ijah) in plain C. Citations are file:line in the
- * reference tree. Pinning status of each function is listed in oracle/README.md.
+ * reference tree. The reference ships no golden vectors for this path and its CPU decoder (the external exl3_codec
+ * module, no pinned version) cannot run here, so each function is pinned by tests/test_oracle.py against something
+ * it shares no code with:
+ *   orc_f32_to_f16 / orc_f16_to_f32 / orc_bf16r: numpy IEEE fp16 on 4,000 values + edge cases; bf16 tie known answers.
+ *   orc_mcg:              known answers (cw 0 -> 0x3F60, cw 1) and all 2^15 codewords against numpy uint32 arithmetic.
+ *   orc_tile_cw_ring/lane/t6: the three readers agree on random tiles (K 1..8), a pure-Python ring walk, constant
+ *                         tiles, and single-bit placement (each bit lands in exactly the windows that cover it).
+ *   orc_slot_rc / orc_decode: bijection + the reference row/column formula; decode vs per-tile codeword lookups.
+ *   orc_fwht_*:           the textbook Sylvester matrix (parity of popcount(i & j)), blocks of 16..128.
+ *   orc_exl3_linear*:     explicit-matrix numpy restatement diag(suh) H W' H diag(svh).
+ *   orc_router_logits / orc_route: numpy dot + bf16 rounding; ties to the lower index vs numpy stable argsort.
+ *   orc_moe_*:            explicit numpy restatement of SwiGLU experts and the slot-order combine.
+ * Parity versus upstream exllamav3's codec itself stays unpinned (the module is absent); the restatement follows
+ * the reference's Metal kernels, which the reference checks against that codec (docs/trunk6.md:74-84).
  */
 #ifndef IJAH_EXL3_ORACLE_H
 #define IJAH_EXL3_ORACLE_H
