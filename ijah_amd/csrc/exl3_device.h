@@ -1,0 +1,225 @@
+// EXL3 trellis decode fused into GEMV / MoE expert kernels for CDNA4 (gfx950), wave64.
+//
+// Format (reference kernels/ne_common.h:105-161, kernels/trunk6/trunk6.metal:87-127): a 16x16 tile of W' is a
+// tail-biting ring of 256 K bits held as 16 K u16 halfwords read as little-endian u32 words, bits consumed MSB
+// first. The codeword of slot i is the 15 ring bits ending at bit (i+1) K; its value is the MCG codebook entry
+// fp16(fp16(r_lo) + fp16(r_hi)), r = (cw * 0xCBAC1FED) & 0x8FFF8FFF ^ 0x3B603B60. Slot s = 8l + j of the reference's
+// 32-lane order holds row (2q, 2q+1, 2q+8, 2q+9)[j & 3] (q = l & 3) at column (l >> 2) + 8 (j >> 2).
+//
+// Wave64 mapping (this build's own): lane m of a wave owns slots 4m .. 4m+3 of a tile, i.e. rows 2q, 2q+1, 2q+8,
+// 2q+9 (q = (m >> 1) & 3) of column (m >> 3) + 8 (m & 1). Its four codewords span 15 + 3K ring bits starting at
+// (4m + 1) K - 15: one funnel shift (v_alignbit) of two words for K <= 5, two funnels of three words above. The input
+// is staged in LDS as fp16 in the reference's k-permuted order (kp), so a lane's four rows are one 8-byte read, and the
+// four weights meet it in two v_dot2_f32_f16. Lanes sharing a column differ in lane bits 1-2: two xor-shuffles reduce.
+//
+// Hadamard transforms hold 128 elements as (lane, lane + 64) and run the butterflies over index bits 0..6 in order
+// (lane shuffles for bits 0-5, the register pair for bit 6) with lo + hi / lo - hi in f32, then one multiply by
+// f32(1/sqrt n): the same operations, in the same order, as the reference's fwht128 / t6_fwht
+// (kernels/ne_common.h:93-103, kernels/trunk6/trunk6.metal:42-51), so the fp16-rounded prepared input is
+// bit-identical to the reference arithmetic. The library is compiled with -ffp-contract=off for that reason.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace ijah {
+
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+
+// ------------------------------------------------------------------------------------------------ scalar helpers
+__device__ __forceinline__ float bf16_f32(uint32_t b16) { return __uint_as_float(b16 << 16); }
+__device__ __forceinline__ float bf16_round(float x) {  // reference kernels/ne_common.h:23-26
+  uint32_t u = __float_as_uint(x);
+  u = (u + 0x7FFFu + ((u >> 16) & 1u)) & 0xFFFF0000u;
+  return __uint_as_float(u);
+}
+__device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+// f32 -> fp16 (RNE) of a value already rounded to f32: the empty asm keeps the compiler from folding a preceding
+// multiply into the conversion (v_fma_mix*), which would round once from the exact product instead of twice.
+__device__ __forceinline__ _Float16 to_f16(float f) {
+  asm("" : "+v"(f));
+  return (_Float16)f;
+}
+__device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, to_f16(f)); }
+// position of input p inside its 16-block in the lane order (2q, 2q+1, 2q+8, 2q+9): reference kernels/ne_common.h:158-161
+__device__ __forceinline__ uint32_t kp(uint32_t p) {
+  return (p & ~15u) | (((p & 7u) >> 1) << 2) | (p & 1u) | (((p >> 3) & 1u) << 1);
+}
+
+// Data handed between workgroups (logits, route, gate/up and down partials) moves with device-coherent accesses
+// (agent-scope relaxed atomics: sc1 loads / stores, which bypass the per-XCD L2's non-coherent lines), so ordering
+// needs only s_waitcnt + barriers: no agent-scope fence, which on CDNA writes back or invalidates the whole L2.
+template <typename T>
+__device__ __forceinline__ T ld_cg(const T *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <typename T>
+__device__ __forceinline__ void st_cg(T *p, T v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ------------------------------------------------------------------------------------------------ Hadamard
+// The value of lane (lane ^ bit) for bit = 1 .. 32, all in VALU: DPP inside rows of 16 (xor 4 = half-mirror then
+// quad reverse, xor 8 = mirror then half-mirror), the gfx950 row / half swaps (v_permlane16/32_swap) across rows.
+template <int BIT>
+__device__ __forceinline__ float xor_lane(float v, int lane) {
+  const int x = __float_as_int(v);
+  if constexpr (BIT == 1) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, false));  // quad_perm 1,0,3,2
+  } else if constexpr (BIT == 2) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, false));  // quad_perm 2,3,0,1
+  } else if constexpr (BIT == 4) {
+    const int t = __builtin_amdgcn_mov_dpp(x, 0x141, 0xF, 0xF, false);            // row_half_mirror: i ^ 7
+    return __int_as_float(__builtin_amdgcn_mov_dpp(t, 0x1B, 0xF, 0xF, false));    // quad_perm 3,2,1,0: ^ 3
+  } else if constexpr (BIT == 8) {
+    const int t = __builtin_amdgcn_mov_dpp(x, 0x140, 0xF, 0xF, false);            // row_mirror: i ^ 15
+    return __int_as_float(__builtin_amdgcn_mov_dpp(t, 0x141, 0xF, 0xF, false));   // row_half_mirror: ^ 7
+  } else if constexpr (BIT == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap((unsigned)x, (unsigned)x, false, false);
+    return __uint_as_float((lane & 16) ? r[0] : r[1]);
+  } else {
+    const auto r = __builtin_amdgcn_permlane32_swap((unsigned)x, (unsigned)x, false, false);
+    return __uint_as_float((lane & 32) ? r[0] : r[1]);
+  }
+}
+template <int BIT>
+__device__ __forceinline__ void fwht_stage(float &v0, float &v1, int lane) {
+  const float p0 = xor_lane<BIT>(v0, lane), p1 = xor_lane<BIT>(v1, lane);
+  const bool up = (lane & BIT) != 0;
+  v0 = up ? p0 - v0 : v0 + p0;
+  v1 = up ? p1 - v1 : v1 + p1;
+}
+// normalised Sylvester H_N (N = 16..128) on a 128-chunk held as (lane, lane + 64); blocks of N are contiguous.
+__device__ __forceinline__ void fwht2(float &v0, float &v1, int lane, int N, float sc) {
+  fwht_stage<1>(v0, v1, lane);
+  fwht_stage<2>(v0, v1, lane);
+  fwht_stage<4>(v0, v1, lane);
+  fwht_stage<8>(v0, v1, lane);
+  if (N > 16) fwht_stage<16>(v0, v1, lane);
+  if (N > 32) fwht_stage<32>(v0, v1, lane);
+  if (N >= 128) {
+    const float a = v0 + v1, b = v0 - v1;
+    v0 = a;
+    v1 = b;
+  }
+  v0 *= sc;
+  v1 *= sc;
+}
+
+// ------------------------------------------------------------------------------------------------ trellis reader
+template <int K>
+struct TileLane {
+  uint32_t i0, i1, i2, sh;  // word indices inside the tile; funnel shift
+};
+// Lane m's window starts at ring bit S = (4m + 1) K - 15 (mod 256 K). Taking i0 = floor((S - 1) / 32) puts the
+// window's first bit at a' = S - 32 i0 in [1, 32] of words (i0, i0+1), so v_alignbit(w0, w1, 32 - a') yields the
+// window's first 32 bits with no special case for a' = 32.
+template <int K>
+__device__ __forceinline__ TileLane<K> tile_lane(uint32_t m) {
+  constexpr uint32_t NW = 8u * K, TOT = 256u * K;
+  const uint32_t S = ((4u * m + 1u) * K + TOT - 15u) % TOT;
+  const uint32_t Sm1 = (S + TOT - 1u) % TOT;
+  TileLane<K> t;
+  t.i0 = Sm1 >> 5;
+  t.i1 = (t.i0 + 1u) % NW;
+  t.i2 = (t.i0 + 2u) % NW;
+  t.sh = 31u - (Sm1 & 31u);
+  return t;
+}
+template <int K>
+constexpr bool kThreeWords = (15 + 3 * K > 32);
+
+struct TileWords {
+  uint32_t w0, w1, w2;
+};
+template <int K>
+__device__ __forceinline__ TileWords load_tile(const uint32_t *__restrict__ T, const TileLane<K> &L) {
+  TileWords w;
+  w.w0 = __builtin_nontemporal_load(T + L.i0);
+  w.w1 = __builtin_nontemporal_load(T + L.i1);
+  w.w2 = kThreeWords<K> ? __builtin_nontemporal_load(T + L.i2) : 0u;
+  return w;
+}
+
+// MCG window-15 codebook (reference kernels/ne_common.h:139-144): r = cw * 0xCBAC1FED mod 2^32, masked, xored;
+// value = fp16(r_lo) + fp16(r_hi) rounded once (RNE), as the reference's half + half.
+// The 32-bit multiply is quarter rate on CDNA; cw < 2^15 lets two full-rate 24-bit multiplies form it:
+// v_mul_u32_u24 (SDWA, dst WORD_1) writes lo16(cw * 0xCBAC) << 16, v_mad_u32_u24 adds cw * 0x1FED.
+__device__ __forceinline__ uint32_t mcg_bits(uint32_t cw) {
+  uint32_t t, r;
+  asm("v_mul_u32_u24_sdwa %0, %1, %2 dst_sel:WORD_1 dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:DWORD"
+      : "=v"(t)
+      : "v"(cw), "s"(0xCBACu));
+  asm("v_mad_u32_u24 %0, %1, %2, %3" : "=v"(r) : "v"(cw), "s"(0x1FEDu), "v"(t));
+  return (r & 0x8FFF8FFFu) ^ 0x3B603B60u;
+}
+// two codewords -> their fp16 values packed (c0 low, c1 high): each v_add_f16 (SDWA) adds the two halves of one r
+// and writes one half of the result, so no pack instruction is needed.
+__device__ __forceinline__ f16x2 mcg_pair(uint32_t c0, uint32_t c1) {
+  const uint32_t r0 = mcg_bits(c0), r1 = mcg_bits(c1);
+  uint32_t d;
+  asm("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1"
+      : "=v"(d)
+      : "v"(r0));
+  asm("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0 src1_sel:WORD_1"
+      : "+v"(d)
+      : "v"(r1));
+  return __builtin_bit_cast(f16x2, d);
+}
+
+// The lane's four weights: a = rows (2q, 2q+1), b = rows (2q+8, 2q+9) of its column.
+template <int K>
+__device__ __forceinline__ void decode4(const TileWords &w, uint32_t sh, f16x2 &a, f16x2 &b) {
+  uint32_t c[4];
+  const uint32_t hi = __builtin_amdgcn_alignbit(w.w0, w.w1, sh);
+  if constexpr (!kThreeWords<K>) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) c[i] = (hi >> (17 - i * K)) & 0x7FFFu;
+  } else {
+    const uint32_t lo = __builtin_amdgcn_alignbit(w.w1, w.w2, sh);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int s = 49 - i * K;
+      c[i] = (s >= 32 ? (hi >> (s - 32)) : __builtin_amdgcn_alignbit(hi, lo, (uint32_t)s)) & 0x7FFFu;
+    }
+  }
+  a = mcg_pair(c[0], c[1]);
+  b = mcg_pair(c[2], c[3]);
+}
+
+__device__ __forceinline__ float dot4(f16x2 a, f16x2 b, f16x4 x, float acc) {
+  acc = __builtin_amdgcn_fdot2(a, f16x2{x.x, x.y}, acc, false);
+  return __builtin_amdgcn_fdot2(b, f16x2{x.z, x.w}, acc, false);
+}
+
+// ------------------------------------------------------------------------------------------------ reductions
+// column sums of a lane pair-tile product: lanes sharing a column differ in lane bits 1-2
+__device__ __forceinline__ void lane_col_reduce(float &acc0, float &acc1) {
+  acc0 += __shfl_xor(acc0, 2, 64);
+  acc0 += __shfl_xor(acc0, 4, 64);
+  acc1 += __shfl_xor(acc1, 2, 64);
+  acc1 += __shfl_xor(acc1, 4, 64);
+}
+// Wave-wide max of a u32 (DPP within rows of 16, then the 4 rows' maxima through readlane): uniform result.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));   // quad_perm 1,0,3,2
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));   // quad_perm 2,3,0,1
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false));  // row_half_mirror
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false));  // row_mirror
+  // every lane of a row holds the row max; row_bcast:15 / :31 carry it to the next row(s); lane 63 ends with all
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xA, 0xF, false));  // row_bcast:15
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xC, 0xF, false));  // row_bcast:31
+  return __builtin_amdgcn_readlane(v, 63);
+}
+// Order key of a bf16-valued logit and its index: a larger key is a larger logit, equal logits order the lower index
+// first (the reference's tie rule, kernels/fn_moe.metal:84,105). NaN ranks as -inf, -0 as +0. Zero is below every key.
+__device__ __forceinline__ uint32_t topk_key(float v, int i) {
+  if (v != v) v = -INFINITY;
+  if (v == 0.f) v = 0.f;
+  uint32_t u = __float_as_uint(v);
+  u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return (u & 0xFFFF0000u) | (0xFFFFu - (uint32_t)i);
+}
+
+}  // namespace ijah

@@ -220,25 +220,40 @@ struct ne_moe {
   int Rcap = 0;
   float *logits = nullptr, *sgv = nullptr, *guo = nullptr, *dn = nullptr;
   uint16_t *hprep = nullptr;
-  uint32_t *route = nullptr, *sync = nullptr;
+  uint32_t *route = nullptr, *sync = nullptr, *plan = nullptr;
+  float *part = nullptr;
+  int plan_grid = 0;  // fused step: its grid (0: no plan, the staged path runs)
   uint64_t *trace = nullptr;  // IJAH_MOE_TRACE=1: per-unit timestamps of the fused kernel (debug)
   bool fused = true;  // one persistent launch per step (IJAH_MOE_PATH=staged: four launches)
   int last_R = 0;
   float *last_y = nullptr;
   ~ne_moe() {
-    for (void *p : std::initializer_list<void *>{experts, shared, router, logits, sgv, guo, dn, route, sync, trace, hprep})
+    for (void *p : std::initializer_list<void *>{experts, shared, router, logits, sgv, guo, dn, route, sync, trace, hprep, plan, part})
       dev_free(p);
   }
   int nslot() const { return topk + has_shared; }
+  size_t logit_floats(int R) const {
+    return std::max<size_t>((size_t)R * (ne + 1), (size_t)kLogitReplicas * moe_logit_stride(ne));
+  }
   void ensure_scratch(int R) {
     if (R <= Rcap) return;
     for (void *p : std::initializer_list<void *>{logits, sgv, guo, dn, route, sync, hprep}) dev_free(p);
     const size_t S = (size_t)R * nslot();
-    logits = dev_alloc<float>((size_t)R * (ne + 1));
+    logits = dev_alloc<float>(logit_floats(R));
+    IJ_HIP(hipMemset(logits, 0, sizeof(float) * logit_floats(R)));  // the fused kernel's launch tags start at 1
     sgv = dev_alloc<float>(R);
     guo = dev_alloc<float>(S * 2 * ksplit * inter);
     dn = dev_alloc<float>(S * hid);
     hprep = dev_alloc<uint16_t>(S * inter);
+    if (!plan && fused && moe_fused_supported(K, has_shared ? Ks : K, 1, hid, inter, ne, topk)) {
+      const MoePlan pl = moe_fused_plan(hid, inter, topk, nslot(), moe_fused_grid());
+      if (pl.ok) {
+        plan = dev_alloc<uint32_t>(pl.words.size());
+        IJ_HIP(hipMemcpy(plan, pl.words.data(), pl.words.size() * 4, hipMemcpyHostToDevice));
+        part = dev_alloc<float>(pl.part_floats);
+        plan_grid = pl.grid;
+      }
+    }
     route = dev_alloc<uint32_t>((size_t)R * 2 * topk);
     IJ_HIP(hipMemset(route, 0, sizeof(uint32_t) * R * 2 * topk));
     sync = dev_alloc<uint32_t>(sync_words(R, nslot(), hid, inter));
@@ -279,6 +294,8 @@ struct ne_moe {
     a.sync = sync;
     a.trace = trace;
     a.hprep = hprep;
+    a.units = plan;
+    a.part = part;
     return a;
   }
   // a failed cross-workgroup wait leaves the error word set: report it and clear the counters
@@ -288,14 +305,16 @@ struct ne_moe {
     IJ_HIP(hipStreamSynchronize(s));
     if (err) {
       IJ_HIP(hipMemsetAsync(sync, 0, 4 * sync_words(Rcap, nslot(), hid, inter), s));
+      IJ_HIP(hipMemsetAsync(logits, 0, sizeof(float) * logit_floats(Rcap), s));  // launch tags restart with the epoch
       IJ_HIP(hipStreamSynchronize(s));
       throw Error("moe: a cross-workgroup wait timed out (layer output invalid)");
     }
   }
+  bool fused_ok(int R) const { return fused && plan_grid > 0 && R == 1; }
   void launch(int R, const float *x, float *y, hipStream_t s) const {
     const MoeArgs a = args(R, x, y);
-    if (fused && moe_fused_supported(K, has_shared ? Ks : K, R, hid, inter, ksplit)) {
-      launch_moe_fused(a, 0, s);
+    if (fused_ok(R)) {
+      launch_moe_fused(a, plan_grid, s);
       return;
     }
     launch_moe_router(a, s);
@@ -539,7 +558,7 @@ NE_API int ne_moe_read(ne_moe *m, const char *name, void *dst, uint64_t nbytes) 
   return c_call([&] {
     IJ_CHECK(m && name && (dst || nbytes == 0), "null argument");
     IJ_CHECK(m->last_R > 0, "no run yet");
-    IJ_HIP(hipStreamSynchronize(stream()));
+    m->check_sync(stream());
     const int R = m->last_R, S = R * m->nslot();
     const std::string n = name;
     std::vector<uint8_t> out;
@@ -551,11 +570,15 @@ NE_API int ne_moe_read(ne_moe *m, const char *name, void *dst, uint64_t nbytes) 
       std::vector<float> all((size_t)R * (m->ne + 1));
       IJ_HIP(hipMemcpy(all.data(), m->logits, all.size() * 4, hipMemcpyDeviceToHost));
       out.resize((size_t)R * m->ne * 4);
+      // the fused kernel keeps its launch tag in the low 16 bits of each (bf16-valued) logit
+      for (float &v : all) v = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, v) & 0xFFFF0000u);
       for (int r = 0; r < R; r++) memcpy(out.data() + (size_t)r * m->ne * 4, &all[(size_t)r * (m->ne + 1)], 4u * m->ne);
     } else if (n == "route") {
       fetch(m->route, (size_t)R * 2 * m->topk * 4);
     } else if (n == "shared_gate") {
       fetch(m->sgv, (size_t)R * 4);
+    } else if (n == "experts_gu" && m->fused_ok(R)) {  // the fused step stores the summed inner outputs
+      fetch(m->guo, (size_t)S * 2 * m->inter * 4);
     } else if (n == "experts_gu") {
       std::vector<float> g((size_t)S * 2 * m->ksplit * m->inter);
       IJ_HIP(hipMemcpy(g.data(), m->guo, g.size() * 4, hipMemcpyDeviceToHost));
@@ -683,8 +706,9 @@ NE_API int ne_moe_time_kernels(ne_moe *const *layers, int n, int R, const ne_buf
     void (*fns[5])(const MoeArgs &, hipStream_t) = {launch_moe_router, launch_moe_gateup, launch_moe_down,
                                                     launch_moe_combine, fused};
     const char *nm[5] = {"router", "gateup", "down", "combine", "fused"};
-    const int KS = layers[0]->has_shared ? layers[0]->Ks : layers[0]->K;
-    const int kinds = moe_fused_supported(layers[0]->K, KS, R, hid, layers[0]->inter, layers[0]->ksplit) ? 5 : 4;
+    bool all_fused = true;
+    for (int i = 0; i < n; i++) all_fused = all_fused && layers[i]->fused_ok(R);
+    const int kinds = all_fused ? 5 : 4;
     try {
       for (int k = 0; k < kinds; k++) {
         double ms = 0;

@@ -50,15 +50,30 @@ struct MoeArgs {
   uint32_t *sync;                      // counters: see sync_words(); zero between launches (kernels reset them)
   uint64_t *trace;                     // fused kernel: per unit {grab, ready, done} wall-clock ticks, or null
   uint16_t *hprep;                     // fused kernel: [R nslot][inter] fp16 down inputs (kp order)
+  const uint32_t *units;               // fused kernel: the plan words (MoePlan::words) in device memory
+  float *part;                         // fused kernel: column partial sums (MoePlan::part_floats)
 };
 void launch_moe_router(const MoeArgs &a, hipStream_t s);
 void launch_moe_gateup(const MoeArgs &a, hipStream_t s);
 void launch_moe_down(const MoeArgs &a, hipStream_t s);
 void launch_moe_combine(const MoeArgs &a, hipStream_t s);
-// the whole layer step in one persistent launch (grid = workgroups; 0 = one per CU times the occupancy limit)
+// The whole layer step of one row in one persistent launch (moe_fused.hip): grid = moe_fused_grid() workgroups, all
+// resident together. The plan splits the gate/up and down work evenly over every wave of that grid.
+struct MoePlan {
+  bool ok = false;
+  int grid = 0;
+  std::vector<uint32_t> words;  // per wave 4 segment words, then per-column segment counts and counter targets
+  size_t part_floats = 0;
+};
+int moe_fused_grid();
+MoePlan moe_fused_plan(int hid, int inter, int topk, int nslot, int grid);
+bool moe_fused_supported(int K, int KS, int R, int hid, int inter, int ne, int topk);
 void launch_moe_fused(const MoeArgs &a, int grid, hipStream_t s);
-int moe_fused_grid(int K, int KS);
-bool moe_fused_supported(int K, int KS, int R, int hid, int inter, int ksplit);
+const void *moe_fused_kernel(int K, int KS, int hid, int inter);  // nullptr if not instantiated
+// Fused step logits: kLogitReplicas copies of [ne + 1] floats, moe_logit_stride(ne) floats apart (replica 0 is the
+// [R = 1][ne + 1] logits buffer the staged path uses); the copies spread the workgroups' polling over memory channels.
+constexpr int kLogitReplicas = 8;
+__host__ __device__ inline int moe_logit_stride(int ne) { return (ne + 1 + 63) / 64 * 64 + 1024; }
 // The sync block for R rows: header counters, per-slot gate/up counters, per-(row, 128-column block) counters; every
 // counter sits alone in a 256-byte line so that polling workgroups do not contend on one line.
 constexpr int kSyncStride = 64;  // u32 words between counters

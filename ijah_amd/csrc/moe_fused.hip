@@ -1,0 +1,783 @@
+// The fused MoE decode step (one input row) in one persistent launch on CDNA4: router, top-k, the routed and shared
+// experts' gate/up and down EXL3 GEMVs with SwiGLU, and the weighted combine (reference kernels/fn_moe.metal:26-452,
+// driven by models/flash_next/layer.mm:532-568).
+//
+// One 16-wave workgroup per CU. Every wave of the grid gets, from a host-built plan, an equal slice of the layer's
+// gate/up work and of its down work: consecutive k tiles of output tile pairs ("columns"), at most two segments each.
+// The step:
+//   1. router: wave w of workgroup b computes router row b + G w and stores its bf16 logit with this launch's tag in
+//      the (always zero) low 16 bits; waves whose gate/up slice belongs to the shared expert request its tiles.
+//   2. route: one wave of every workgroup waits until all logits carry the tag and ranks them itself (no exchange).
+//   3. gate/up: each wave streams its slice's tiles into its own LDS area (global_load_lds), prepares the input
+//      chunks it needs (x * suh, Hadamard, fp16), decodes and multiplies, and stores one partial per column segment.
+//      Per (slot, 128-column block) a counter collects the partials; the workgroup that completes it sums them in
+//      segment order and applies the down prologue (H, svh, SwiGLU, suh_d, H) into fp16 `hprep`.
+//   4. down: each wave streams and decodes its down slice into registers while the gate/up blocks finish, waits for
+//      its slot's blocks, multiplies, and stores its partials; the workgroup completing a 128-column block of the
+//      output combines it: per slot the partials in segment order, H, svh and the route weight, slots in slot order.
+// Cross-workgroup data moves through coherent (sc1) stores and loads; counters are single atomics per workgroup and
+// target; every wait is bounded and raises the error word. The last workgroup out resets the counters and advances
+// the launch epoch. All workgroups must be resident together (grid = CU count, one workgroup per CU).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <vector>
+
+#include "exl3_device.h"
+#include "kernels.h"
+
+namespace ijah {
+
+namespace {
+
+constexpr int kWaves = 16;
+// Control wave: the route and the counting run on the last wave, which requests no tiles before the route. Vector
+// memory waits are in order, so a wave with tile streams in flight would wait for them before any load or atomic
+// result of its control duty.
+constexpr int kCtl = kWaves - 1;
+constexpr int kMaxGu = 12;                 // gate/up k tiles per wave (its LDS area)
+constexpr int kMaxDn = 8;                  // down k tiles per wave (held decoded in registers)
+constexpr int kMaxSeg = 16;                // partial sums per column
+constexpr int kPrepHalves = 2 * 3 * 128;   // two segments of up to three 128-chunks of prepared input
+constexpr int kMaxExpertsV = 1024;
+constexpr int kMaxTopkV = 32;
+constexpr uint32_t kSpin = 1u << 22;       // bounded waits: polls of ~0.1-1 us each, far beyond any real wait
+enum {  // words 0-2 belong to the staged kernels' counters
+  kWordExit = 5 * kSyncStride,
+  kWordEpoch = 4 * kSyncStride,            // launches so far (mod 2^32); tags this launch's logits
+  kWordErr = kSyncErrWord,
+  kWordGuDone = 8 * kSyncStride            // then: gu_done[nslot], blk[nblk], fin[nslot * nbi], one line each
+};
+
+__device__ __forceinline__ uint32_t ld_relaxed(const uint32_t *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void mark(const MoeArgs &a, int field) {
+  if (a.trace && threadIdx.x == 0) a.trace[(uint64_t)blockIdx.x * 8 + field] = wall_clock64();
+}
+// second trace row of the workgroup, written by lane 0 of the calling wave
+__device__ __forceinline__ void mark2(const MoeArgs &a, int field) {
+  if (a.trace && (threadIdx.x & 63) == 0) a.trace[(uint64_t)(256 + blockIdx.x) * 8 + field] = wall_clock64();
+}
+// Workgroup barrier ordering LDS (ds_*) and scalar traffic only. Outstanding vector memory operations, including the
+// wave's LDS-DMA tile streams, stay in flight: __syncthreads() would wait for them (its release fence covers the LDS
+// the DMA writes). Every use here exchanges only ds_write data; each wave waits for its own DMA itself.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+// s_waitcnt vmcnt(n) for a run-time n: at most n vector memory operations of this wave still outstanding (n above 15
+// waits as for 15, which only waits longer). Operation completion is counted in issue order.
+__device__ __forceinline__ void wait_vm(int n) {
+  switch (n < 15 ? n : 15) {
+#define IJ_VM(k) \
+  case k: __builtin_amdgcn_s_waitcnt(0x0F70 | k); break;
+    IJ_VM(0) IJ_VM(1) IJ_VM(2) IJ_VM(3) IJ_VM(4) IJ_VM(5) IJ_VM(6) IJ_VM(7)
+    IJ_VM(8) IJ_VM(9) IJ_VM(10) IJ_VM(11) IJ_VM(12) IJ_VM(13) IJ_VM(14) IJ_VM(15)
+#undef IJ_VM
+  }
+}
+// global_load_lds instructions a stream of `bytes` issues (one per 1 KB)
+__device__ __forceinline__ int dma_ops(uint32_t bytes) { return (int)((bytes + 1023u) >> 10); }
+constexpr int had_of(int d) { return d % 128 == 0 ? 128 : d % 64 == 0 ? 64 : d % 32 == 0 ? 32 : 16; }
+
+struct Seg {  // a segment of a wave's slice: k tiles [k0, k0 + n) of column col; partial jj of that column
+  int col, k0, n, jj;
+};
+__device__ __forceinline__ Seg seg_of(uint32_t d) {
+  return {(int)(d & 0xFFFu), (int)((d >> 12) & 0xFFu), (int)((d >> 20) & 0x7Fu), (int)(d >> 27)};
+}
+
+struct Route {  // the workgroup's copy of the route of the row
+  uint32_t id[kMaxTopkV];
+  float w[kMaxTopkV];
+  float sg;
+};
+
+// slot order in the plan (ls): the shared expert first (its work needs no route), then the routed slots k = 0..topk-1.
+// Slot index j as the reference numbers it: routed k -> k, shared -> topk.
+__device__ __forceinline__ int slot_j(const MoeArgs &a, int ls) {
+  return a.nslot > a.topk ? (ls == 0 ? a.topk : ls - 1) : ls;
+}
+__device__ __forceinline__ bool slot_shared(const MoeArgs &a, int ls) { return a.nslot > a.topk && ls == 0; }
+__device__ __forceinline__ const uint8_t *slot_block(const MoeArgs &a, const Route &rt, int ls) {
+  if (slot_shared(a, ls)) return a.shared;
+  uint32_t e = rt.id[slot_j(a, ls)];
+  e = e < (uint32_t)a.ne ? e : 0u;  // out-of-range ids clamp to expert 0, as the reference masks with NE - 1
+  return a.experts + (uint64_t)e * a.lay.bytes;
+}
+// region offsets of a slot's block, picked with constant member indices (a dynamic index into the kernel-argument
+// struct would become a vector load, and its wait would also wait for the wave's outstanding tile streams)
+__device__ __forceinline__ uint64_t tr_off(const MoeArgs &a, int ls, int proj) {
+  const ExpertLayout &L = slot_shared(a, ls) ? a.slay : a.lay;
+  return proj == 0 ? L.tr[0] : proj == 1 ? L.tr[1] : L.tr[2];
+}
+__device__ __forceinline__ uint64_t su_off(const MoeArgs &a, int ls, int proj) {
+  const ExpertLayout &L = slot_shared(a, ls) ? a.slay : a.lay;
+  return proj == 0 ? L.su[0] : proj == 1 ? L.su[1] : L.su[2];
+}
+__device__ __forceinline__ uint64_t sv_off(const MoeArgs &a, int ls, int proj) {
+  const ExpertLayout &L = slot_shared(a, ls) ? a.slay : a.lay;
+  return proj == 0 ? L.sv[0] : proj == 1 ? L.sv[1] : L.sv[2];
+}
+
+// ---------------------------------------------------------------------------------------------------- router
+// Router row b + G w on wave w (reference kernels/fn_moe.metal:50-67): the bf16 row and x are loaded straight into
+// registers; the logit is rounded to bf16 (the reference rounding), so its low 16 bits are zero and carry the tag.
+// It goes to kLogitReplicas copies (a few KB apart), so that the workgroups polling for the logits spread over as many
+// memory channels instead of all reading the same lines.
+template <int HID>
+__device__ __forceinline__ void router_row(const MoeArgs &a, const uint32_t *tag_lds) {
+  constexpr int NC = HID / 512;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int row = (int)blockIdx.x + (int)gridDim.x * wave;
+  const bool active = row < a.ne + a.has_sgate;
+  uint4 wv[NC];
+  float4 x0[NC], x1[NC];
+  if (active) {
+    const uint16_t *w = a.router + (uint64_t)row * HID;
+#pragma unroll
+    for (int j = 0; j < NC; j++) {
+      wv[j] = *(const uint4 *)(w + j * 512 + lane * 8);
+      x0[j] = *(const float4 *)(a.x + j * 512 + lane * 8);
+      x1[j] = *(const float4 *)(a.x + j * 512 + lane * 8 + 4);
+    }
+  }
+  lds_barrier();  // the tag (thread 0) is visible after this
+  if (!active) return;
+  float acc = 0.f;
+#pragma unroll
+  for (int j = 0; j < NC; j++) {
+    acc = fmaf(x0[j].x, bf16_f32(wv[j].x & 0xFFFFu), acc);
+    acc = fmaf(x0[j].y, bf16_f32(wv[j].x >> 16), acc);
+    acc = fmaf(x0[j].z, bf16_f32(wv[j].y & 0xFFFFu), acc);
+    acc = fmaf(x0[j].w, bf16_f32(wv[j].y >> 16), acc);
+    acc = fmaf(x1[j].x, bf16_f32(wv[j].z & 0xFFFFu), acc);
+    acc = fmaf(x1[j].y, bf16_f32(wv[j].z >> 16), acc);
+    acc = fmaf(x1[j].z, bf16_f32(wv[j].w & 0xFFFFu), acc);
+    acc = fmaf(x1[j].w, bf16_f32(wv[j].w >> 16), acc);
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) acc += __shfl_xor(acc, o, 64);
+  const uint32_t v = (__float_as_uint(bf16_round(acc)) & 0xFFFF0000u) | *tag_lds;
+  const int stride = moe_logit_stride(a.ne);
+  if (lane < kLogitReplicas) st_cg((uint32_t *)a.logits + lane * stride + row, v);
+}
+
+// bf16-valued logit back from its order key (the inverse of topk_key on the top 16 bits)
+__device__ __forceinline__ float key_value(uint32_t key) {
+  const uint32_t h = key >> 16;
+  return __uint_as_float((h & 0x8000u) ? (h & 0x7FFFu) << 16 : (~h & 0xFFFFu) << 16);
+}
+// descending bitonic sort of J keys held in registers (J a power of two; compile-time indices)
+template <int J>
+__device__ __forceinline__ void sort_desc(uint32_t (&k)[J]) {
+#pragma unroll
+  for (int s = 2; s <= J; s <<= 1)
+#pragma unroll
+    for (int d = s >> 1; d > 0; d >>= 1)
+#pragma unroll
+      for (int i = 0; i < J; i++) {
+        const int l = i ^ d;
+        if (l > i) {
+          const uint32_t hi = max(k[i], k[l]), lo = min(k[i], k[l]);
+          if ((i & s) == 0) {
+            k[i] = hi;
+            k[l] = lo;
+          } else {
+            k[i] = lo;
+            k[l] = hi;
+          }
+        }
+      }
+}
+// The route, by one wave of every workgroup (reference kernels/fn_moe.metal:76-131): waits until every logit carries
+// this launch's tag (bounded), then top-k by logit with ties to the lower index, weights exp(l - l_max) / sum over the
+// top k in f32 summed in slot order, and the shared gate sigmoid(logit). Each lane sorts its J keys once; a round
+// takes the wave max of the lanes' heads and the winning lane shifts its list. A NaN logit ranks as -inf (weight 0).
+// Workgroup 0 also writes the route to the route / shared-gate buffers for the host.
+template <int J>
+__device__ bool route_wave(const MoeArgs &a, Route *rt, uint32_t tag) {
+  const int lane = threadIdx.x & 63, n = a.ne + a.has_sgate;
+  const uint32_t *lg = (const uint32_t *)a.logits + (blockIdx.x % kLogitReplicas) * moe_logit_stride(a.ne);
+  uint32_t v[J + 1];
+  bool ok = false;
+  for (uint32_t it = 0; it < kSpin; it++) {
+    bool mine = true;
+#pragma unroll
+    for (int j = 0; j <= J; j++) {
+      const int i = j * 64 + lane;
+      v[j] = i < n ? ld_cg(lg + i) : tag;
+      mine = mine && ((v[j] & 0xFFFFu) == tag);
+    }
+    if (__all(mine)) {
+      ok = true;
+      if (a.trace && lane == 0) {
+        a.trace[(uint64_t)(5000 + blockIdx.x) * 8] = wall_clock64();
+        a.trace[(uint64_t)(5000 + blockIdx.x) * 8 + 2] = it;
+      }
+      break;
+    }
+    if ((it & 63u) == 63u && ld_relaxed(a.sync + kWordErr)) break;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  if (!ok) {
+    if (lane == 0) atomicOr(a.sync + kWordErr, 1u);
+    return false;
+  }
+  uint32_t key[J];
+  float sgl = 0.f;
+#pragma unroll
+  for (int j = 0; j <= J; j++) {
+    const int i = j * 64 + lane;
+    const float val = __uint_as_float(v[j] & 0xFFFF0000u);
+    if (j < J) key[j] = i < a.ne ? topk_key(val, i) : 0u;
+    if (i == a.ne) sgl = val;
+  }
+  sgl = __shfl(sgl, a.ne & 63, 64);
+  sort_desc<J>(key);
+  uint32_t mykey = 0u;  // lane t < topk: the t-th largest key
+  for (int t = 0; t < a.topk; t++) {
+    const uint32_t m = wave_max_u32(key[0]);
+    mykey = lane == t ? m : mykey;
+    const bool win = key[0] == m;
+#pragma unroll
+    for (int j = 0; j < J - 1; j++) key[j] = win ? key[j + 1] : key[j];
+    key[J - 1] = win ? 0u : key[J - 1];
+  }
+  const uint32_t id = 0xFFFFu - (mykey & 0xFFFFu);
+  if (a.trace && lane == 0) a.trace[(uint64_t)(5000 + blockIdx.x) * 8 + 1] = wall_clock64();
+  const float top = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(key_value(mykey)), 0));
+  const float pk = lane < a.topk ? expf(key_value(mykey) - top) : 0.f;
+  float sum = 0.f;
+  for (int k = 0; k < a.topk; k++) sum += __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(pk), k));
+  const float wk = pk / sum;
+  const float sg = a.has_sgate ? 1.f / (1.f + expf(-sgl)) : 1.f;
+  if (lane < a.topk) {
+    rt->id[lane] = id;
+    rt->w[lane] = wk;
+    if (blockIdx.x == 0) {
+      st_cg(a.route + lane, id);
+      st_cg(a.route + a.topk + lane, __float_as_uint(wk));
+    }
+  }
+  if (lane == 0) {
+    rt->sg = sg;
+    if (blockIdx.x == 0) st_cg(a.sgv, sg);
+  }
+  return true;
+}
+
+// ---------------------------------------------------------------------------------------------------- streaming
+// n k tiles of pair p starting at k0 of a re-laid matrix with IT k tiles (tile bytes tb) into LDS at dst
+__device__ __forceinline__ void stream_tiles(const uint8_t *tr, int IT, int p, int k0, int n, uint32_t tb, uint8_t *dst) {
+  const int lane = threadIdx.x & 63;
+  const uint8_t *src = tr + ((uint64_t)p * IT + k0) * 2 * tb;
+  const uint32_t bytes = (uint32_t)n * 2 * tb;
+  for (uint32_t o = 0; o < bytes; o += 1024)
+    if (o + (uint32_t)lane * 16 < bytes)
+      __builtin_amdgcn_global_load_lds((const void *)(src + o + lane * 16),
+                                       (__attribute__((address_space(3))) void *)(dst + o), 16, 0, 0);
+}
+// one wave: output tile pair over k tiles [kt0, kt1) staged in LDS, accumulated per lane (lane_col_reduce gives the
+// column sums on lanes with (lane & 6) == 0)
+template <int K>
+__device__ __forceinline__ void pair_dot_range(const uint8_t *tl, const _Float16 *xs, int kt0, int kt1, float &acc0,
+                                               float &acc1) {
+  constexpr int TW = 8 * K;
+  const int lane = threadIdx.x & 63;
+  const TileLane<K> L = tile_lane<K>((uint32_t)lane);
+  const int q = (lane >> 1) & 3;
+  const uint32_t *T = (const uint32_t *)tl;
+#pragma unroll 4
+  for (int kt = kt0; kt < kt1; kt++) {
+    const uint32_t *T0 = T + kt * 2 * TW;
+    TileWords wa, wb;
+    wa.w0 = T0[L.i0];
+    wa.w1 = T0[L.i1];
+    wa.w2 = kThreeWords<K> ? T0[L.i2] : 0u;
+    wb.w0 = T0[TW + L.i0];
+    wb.w1 = T0[TW + L.i1];
+    wb.w2 = kThreeWords<K> ? T0[TW + L.i2] : 0u;
+    const f16x4 xv = *(const f16x4 *)(xs + kt * 16 + 4 * q);
+    f16x2 a0, b0, a1, b1;
+    decode4<K>(wa, L.sh, a0, b0);
+    decode4<K>(wb, L.sh, a1, b1);
+    acc0 = dot4(a0, b0, xv, acc0);
+    acc1 = dot4(a1, b1, xv, acc1);
+  }
+}
+// decode k tiles [t0, t0 + n) of the staged pair tiles into w[kt] (kt = t0 .. t0 + n - 1 of the wave's down slice):
+// w[kt][0..1] = tile 2p (rows a, b), w[kt][2..3] = tile 2p + 1
+template <int K>
+__device__ __forceinline__ void decode_pairs(const uint8_t *tl, int t0, int n, f16x2 (&w)[kMaxDn][4]) {
+  constexpr int TW = 8 * K;
+  const int lane = threadIdx.x & 63;
+  const TileLane<K> L = tile_lane<K>((uint32_t)lane);
+  const uint32_t *T = (const uint32_t *)tl;
+#pragma unroll
+  for (int kt = 0; kt < kMaxDn; kt++) {
+    if (kt >= t0 && kt < t0 + n) {
+      const uint32_t *T0 = T + (kt - t0) * 2 * TW;
+      TileWords wa, wb;
+      wa.w0 = T0[L.i0];
+      wa.w1 = T0[L.i1];
+      wa.w2 = kThreeWords<K> ? T0[L.i2] : 0u;
+      wb.w0 = T0[TW + L.i0];
+      wb.w1 = T0[TW + L.i1];
+      wb.w2 = kThreeWords<K> ? T0[TW + L.i2] : 0u;
+      decode4<K>(wa, L.sh, w[kt][0], w[kt][1]);
+      decode4<K>(wb, L.sh, w[kt][2], w[kt][3]);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------- counting
+// Each wave posts up to two counter indices (or ~0u) in ids[2 wave + s]; wave kCtl merges runs of equal neighbours and
+// adds each run with one atomic; fin[i] = the counter index this workgroup completed (target[idx] reached), else -1.
+// All threads call it (barriers inside).
+__device__ void count_runs(uint32_t *ctr, const uint32_t *target, const uint32_t *ids, int *fin, uint64_t *trace) {
+  const int lane = threadIdx.x & 63;
+  lds_barrier();
+  if ((int)(threadIdx.x >> 6) == kCtl) {
+    const bool in = lane < 2 * kWaves;
+    const uint32_t id = in ? ids[lane] : ~0u;
+    const uint32_t nxt = __shfl_down(id, 1, 64);
+    const uint32_t prv = __shfl_up(id, 1, 64);
+    const bool valid = id != ~0u;
+    const bool head = valid && (lane == 0 || prv != id);
+    const bool tail = valid && (lane == 2 * kWaves - 1 || nxt != id);
+    const uint64_t tails = __ballot(tail);
+    int res = -1;
+    if (head) {
+      const uint32_t cnt = (uint32_t)__builtin_ctzll(tails >> lane) + 1u;
+      const uint32_t old = atomicAdd(ctr + (uint64_t)id * kSyncStride, cnt);
+      if (old + cnt == target[id]) res = (int)id;
+      if (trace) trace[(uint64_t)(256 + blockIdx.x) * 8 + 5] = wall_clock64();
+    }
+    if (in) fin[lane] = res;
+  }
+  lds_barrier();
+}
+
+// The partials of one output column c32 of a gate/up column, [column][kMaxSeg][32] floats: every segment slot is loaded
+// (lanes of a wave read 32 consecutive floats per load; the slots past ns hold stale data and are not added), then the
+// ns valid ones are summed in segment order.
+struct Partials {
+  float v[kMaxSeg];
+};
+__device__ __forceinline__ Partials load_partials(const float *p) {
+  Partials r;
+#pragma unroll
+  for (int jj = 0; jj < kMaxSeg; jj++) r.v[jj] = ld_cg(p + jj * 32);
+  return r;
+}
+__device__ __forceinline__ float sum_partials(const Partials &r, int ns) {
+  float s = r.v[0];
+#pragma unroll
+  for (int jj = 1; jj < kMaxSeg; jj++) s = jj < ns ? s + r.v[jj] : s;
+  return s;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------------------------------- the kernel
+template <int K, int KS, int HID, int INTER>
+__global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
+  constexpr int KM = K > KS ? K : KS;
+  constexpr int IT = HID / 16, ITd = INTER / 16, NPg = INTER / 32, NBI = INTER / 128,
+                NBLK = HID / 128, HH = had_of(HID), HI = had_of(INTER);
+  constexpr uint32_t GUB = kMaxGu * 64 * KM, AREA = GUB + kMaxDn * 64 * KM;  // a wave's gate/up + down tile bytes
+  extern __shared__ __attribute__((aligned(16))) uint8_t tiles[];  // kWaves x AREA
+  __shared__ _Float16 prep[kWaves][kPrepHalves];  // per segment: suh chunks (DMA), then fp16(H(x suh)) in place
+  __shared__ __attribute__((aligned(16))) float xl[HID];  // the input row
+  __shared__ Route rt;
+  __shared__ uint32_t s_tag, s_ok, ids[2 * kWaves];
+  __shared__ int fin[64];
+  const float sch = a.sc_hid, sci = a.sc_inter;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, G = (int)gridDim.x;
+  const int NW = G * kWaves, CG = a.nslot * 2 * NPg;
+  const uint32_t *plan = a.units;
+  uint2 pw = *(const uint2 *)(plan + 2 * (blockIdx.x * kWaves + wave));  // gate/up segments s0, s1
+  pw.x = __builtin_amdgcn_readfirstlane(pw.x);  // wave-uniform: scalar registers and branches
+  pw.y = __builtin_amdgcn_readfirstlane(pw.y);
+  const uint32_t *gu_nseg = plan + 2 * NW, *fin_tgt = gu_nseg + CG;
+  uint32_t *sync = a.sync;
+  uint32_t *gu_done = sync + kWordGuDone;               // [ls]: finished 128-column blocks of slot ls
+  uint32_t *blk_cnt = gu_done + a.nslot * kSyncStride;   // [c]: slots stored of output block c
+  uint32_t *fin_cnt = blk_cnt + NBLK * kSyncStride;      // [ls * NBI + cb]: gate/up partials of a block
+  float *part_gu = a.part, *part_dn = a.part + (size_t)CG * kMaxSeg * 32;  // gate/up partials; weighted slot outputs
+  uint8_t *area = tiles + wave * AREA;
+  mark(a, 0);
+  if (threadIdx.x == 0) s_tag = ld_cg(sync + kWordEpoch) % 65535u + 1u;  // 1..65535, never the initial 0
+
+  const Seg g0 = seg_of(pw.x), g1 = seg_of(pw.y);
+  // gate/up column c = (ls * 2 + proj) * NPg + p; down column c = ls * NPd + p
+  auto gu_ls = [&](const Seg &s) { return s.col / (2 * NPg); };
+  auto gu_proj = [&](const Seg &s) { return (s.col / NPg) & 1; };
+  auto gu_p = [&](const Seg &s) { return s.col % NPg; };
+  auto tbytes = [&](int ls) { return 32u * (uint32_t)(slot_shared(a, ls) ? KS : K); };
+  const uint32_t off1 = (uint32_t)g0.n * 2 * (g0.n ? tbytes(gu_ls(g0)) : 0u);  // second segment's LDS offset
+  auto issue_gu = [&](const Seg &s, uint32_t off) {
+    const int ls = gu_ls(s);
+    stream_tiles(slot_block(a, rt, ls) + tr_off(a, ls, gu_proj(s)), IT, gu_p(s), s.k0, s.n, tbytes(ls), area + off);
+  };
+
+  // ---- 1. router; the control wave stages x in LDS; the shared expert's gate/up tiles need no route
+  if (wave == kCtl) {
+#pragma unroll
+    for (int o = 0; o < HID * 4; o += 1024)
+      __builtin_amdgcn_global_load_lds((const void *)((const uint8_t *)a.x + o + lane * 16),
+                                       (__attribute__((address_space(3))) void *)((uint8_t *)xl + o), 16, 0, 0);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): x is in LDS before the next barrier
+  }
+  router_row<HID>(a, &s_tag);
+  mark(a, 1);
+  const bool pre0 = wave != kCtl && g0.n && slot_shared(a, gu_ls(g0));
+  const bool pre1 = wave != kCtl && g1.n && slot_shared(a, gu_ls(g1));
+  if (pre0) issue_gu(g0, 0);
+  if (pre1) issue_gu(g1, off1);
+
+  // ---- 2. route
+  if (threadIdx.x == 0) s_ok = 1;
+  lds_barrier();
+  if (wave == kCtl) {
+    const bool ok = a.ne <= 512 ? route_wave<8>(a, &rt, s_tag) : route_wave<16>(a, &rt, s_tag);
+    if (!ok && lane == 0) s_ok = 0;
+  }
+  lds_barrier();
+  mark(a, 2);
+  const bool ok = s_ok != 0;
+
+  // ---- 3. gate/up. Requests, in order: each segment's suh chunks (into its prep area), its gate/up tiles (unless
+  // already requested), the down tiles. Then waits step by step: suh -> prep; each 1 KB of gate/up tiles -> the k
+  // tiles it completes.
+  // down: workgroup b < nslot * NBLK owns slot ls_d's 128-column output block bd; wave w takes pair 4 bd + w / 4,
+  // k quarter w % 4 (QK k tiles)
+  constexpr int QK = ITd / 4;
+  const bool has_dn = ok && (int)blockIdx.x < a.nslot * NBLK;
+  const int ls_d = (int)blockIdx.x / NBLK, bd = (int)blockIdx.x % NBLK, dpair = bd * 4 + (wave >> 2), dq = wave & 3;
+  const uint32_t gb0 = g0.n ? (uint32_t)g0.n * 2 * tbytes(gu_ls(g0)) : 0u, gb1 = g1.n ? (uint32_t)g1.n * 2 * tbytes(gu_ls(g1)) : 0u;
+  const int n_g0 = (ok && !pre0) ? dma_ops(gb0) : 0, n_g1 = (ok && !pre1) ? dma_ops(gb1) : 0;
+  const int n_dn = has_dn ? dma_ops((uint32_t)QK * 2 * tbytes(ls_d)) : 0;
+  auto issue_suh = [&](const Seg &s, _Float16 *dst) {
+    const int ls = gu_ls(s), c0 = s.k0 / 8, c1 = (s.k0 + s.n - 1) / 8;
+    const uint8_t *src = slot_block(a, rt, ls) + su_off(a, ls, gu_proj(s)) + c0 * 256;
+    const uint32_t bytes = (uint32_t)(c1 - c0 + 1) * 256;  // <= 768: one request
+    if ((uint32_t)lane * 16 < bytes)
+      __builtin_amdgcn_global_load_lds((const void *)(src + lane * 16), (__attribute__((address_space(3))) void *)dst,
+                                       16, 0, 0);
+  };
+  if (ok && g0.n) issue_suh(g0, prep[wave]);
+  if (ok && g1.n) issue_suh(g1, prep[wave] + 384);
+  if (ok && g0.n && !pre0) issue_gu(g0, 0);
+  if (ok && g1.n && !pre1) issue_gu(g1, off1);
+  if (has_dn) stream_tiles(slot_block(a, rt, ls_d) + tr_off(a, ls_d, 2), ITd, dpair, dq * QK, QK, tbytes(ls_d), area + GUB);
+  // fp16(H(x * suh)) of each 128-chunk of the segment, in kp order, over its suh chunks
+  auto prep_seg = [&](const Seg &s, _Float16 *dst) {
+    const int c0 = s.k0 / 8, nc = (s.k0 + s.n - 1) / 8 - c0 + 1;
+    float su[3][2];
+#pragma unroll
+    for (int c = 0; c < 3; c++)
+      if (c < nc) {
+        su[c][0] = (float)dst[c * 128 + lane];
+        su[c][1] = (float)dst[c * 128 + lane + 64];
+      }
+#pragma unroll
+    for (int c = 0; c < 3; c++)
+      if (c < nc) {
+        float v0 = xl[(c0 + c) * 128 + lane] * su[c][0], v1 = xl[(c0 + c) * 128 + lane + 64] * su[c][1];
+        fwht2(v0, v1, lane, HH, sch);
+        dst[c * 128 + kp(lane)] = to_f16(v0);
+        dst[c * 128 + kp(lane + 64)] = to_f16(v1);
+      }
+  };
+  wait_vm(n_g0 + n_g1 + n_dn);  // suh chunks are in
+  if (ok && g0.n) prep_seg(g0, prep[wave]);
+  if (ok && g1.n) prep_seg(g1, prep[wave] + 384);
+  mark(a, 3);
+  // a segment's dot, k tiles taken as each 1 KB request lands (n_after: requests issued after the segment's; stores
+  // come only after both segments, so they are never counted as "after": a wait may be stricter, never looser)
+  auto gu_dot = [&](const Seg &s, uint32_t off, const _Float16 *pr, int n_seg, int n_after, float &acc0, float &acc1) {
+    const _Float16 *xs = pr + (s.k0 - 8 * (s.k0 / 8)) * 16;
+    const bool sh = slot_shared(a, gu_ls(s));
+    const uint32_t pb = 2 * tbytes(gu_ls(s));  // bytes of one k tile pair
+    int kt0 = 0;
+    const int steps = n_seg > 0 ? n_seg : 1;
+    for (int j = 0; j < steps; j++) {
+      if (n_seg > 0) wait_vm(n_after + n_seg - 1 - j);
+      const int kt1 = j == steps - 1 ? s.n : (int)((uint32_t)(j + 1) * 1024u / pb);
+      if (kt1 > kt0) {
+        if (sh)
+          pair_dot_range<KS>(area + off, xs, kt0, kt1, acc0, acc1);
+        else
+          pair_dot_range<K>(area + off, xs, kt0, kt1, acc0, acc1);
+        kt0 = kt1;
+      }
+    }
+    lane_col_reduce(acc0, acc1);
+  };
+  auto gu_store = [&](const Seg &s, float acc0, float acc1) {
+    if ((lane & 6) == 0) {
+      const int col = (lane >> 3) + 8 * (lane & 1);
+      float *d = part_gu + ((size_t)s.col * kMaxSeg + s.jj) * 32;  // [column][kMaxSeg][32]
+      st_cg(d + col, acc0);
+      st_cg(d + 16 + col, acc1);
+    }
+  };
+  float ga0 = 0.f, ga1 = 0.f, gb0s = 0.f, gb1s = 0.f;
+  if (ok && g0.n) gu_dot(g0, 0, prep[wave], n_g0, n_g1 + n_dn, ga0, ga1);
+  if (ok && g1.n) gu_dot(g1, off1, prep[wave] + 384, n_g1, n_dn, gb0s, gb1s);
+  if (ok && g0.n) gu_store(g0, ga0, ga1);
+  if (ok && g1.n) gu_store(g1, gb0s, gb1s);
+  if (wave == 0) mark2(a, 0);
+  __builtin_amdgcn_s_waitcnt(0);  // partials stored before they are counted
+  if (wave == 0) mark2(a, 1);
+  if (a.trace && lane == 0) a.trace[(uint64_t)(512 + blockIdx.x * kWaves + wave) * 8] = wall_clock64();
+  if (lane == 0) {
+    ids[2 * wave] = (ok && g0.n) ? (uint32_t)(gu_ls(g0) * NBI + gu_p(g0) / 4) : ~0u;
+    ids[2 * wave + 1] = (ok && g1.n) ? (uint32_t)(gu_ls(g1) * NBI + gu_p(g1) / 4) : ~0u;
+  }
+  if (a.trace && threadIdx.x == 0) a.trace[(uint64_t)(256 + blockIdx.x) * 8 + 6] = wall_clock64();
+  count_runs(fin_cnt, fin_tgt, ids, fin, a.trace);
+  mark(a, 4);
+  // gate/up block finisher (one wave per completed block): sums the partials in segment order, then the down
+  // prologue (reference kernels/fn_moe.metal:370-384): g = H(inner_g) svh_g, u = H(inner_u) svh_u,
+  // h = H(silu(g) u suh_d) -> fp16 in kp order
+  for (int fi = wave; fi < 2 * kWaves; fi += kWaves) {
+    const int id = fin[fi];
+    if (id < 0) continue;
+    const int ls = id / NBI, cb = id % NBI;
+    mark2(a, 2);
+    const uint8_t *blk = slot_block(a, rt, ls);
+    const int i0 = cb * 128 + lane, i1 = i0 + 64;
+    Partials pp[2][2];
+    int ns[2][2];
+#pragma unroll
+    for (int proj = 0; proj < 2; proj++)
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        const int i = cb * 128 + h * 64 + lane, c = (ls * 2 + proj) * NPg + i / 32;
+        pp[proj][h] = load_partials(part_gu + (size_t)c * kMaxSeg * 32 + (i & 31));
+        ns[proj][h] = (int)gu_nseg[c];
+      }
+    const uint16_t *svg = (const uint16_t *)(blk + sv_off(a, ls, 0)), *svu = (const uint16_t *)(blk + sv_off(a, ls, 1));
+    const uint16_t *sud = (const uint16_t *)(blk + su_off(a, ls, 2));
+    const float sg0 = h2f(svg[i0]), sg1 = h2f(svg[i1]), su0 = h2f(svu[i0]), su1 = h2f(svu[i1]);
+    const float sd0 = h2f(sud[i0]), sd1 = h2f(sud[i1]);
+    float gu[2][2];
+#pragma unroll
+    for (int proj = 0; proj < 2; proj++)
+#pragma unroll
+      for (int h = 0; h < 2; h++) gu[proj][h] = sum_partials(pp[proj][h], ns[proj][h]);
+    mark2(a, 3);
+    float *gsum = a.guo + (size_t)slot_j(a, ls) * 2 * INTER;  // inner gate / up outputs, for reads
+    st_cg(gsum + i0, gu[0][0]);
+    st_cg(gsum + i1, gu[0][1]);
+    st_cg(gsum + INTER + i0, gu[1][0]);
+    st_cg(gsum + INTER + i1, gu[1][1]);
+    float g0v = gu[0][0], g1v = gu[0][1], u0v = gu[1][0], u1v = gu[1][1];
+    fwht2(g0v, g1v, lane, HI, sci);
+    fwht2(u0v, u1v, lane, HI, sci);
+    g0v = g0v * sg0;
+    u0v = u0v * su0;
+    g1v = g1v * sg1;
+    u1v = u1v * su1;
+    float h0 = g0v / (1.f + expf(-g0v)) * u0v * sd0;
+    float h1 = g1v / (1.f + expf(-g1v)) * u1v * sd1;
+    fwht2(h0, h1, lane, HI, sci);
+    uint16_t *hp = a.hprep + (size_t)ls * INTER + cb * 128;
+    st_cg(hp + kp(lane), f2h(h0));
+    st_cg(hp + kp(lane + 64), f2h(h1));
+    __builtin_amdgcn_s_waitcnt(0);
+    mark2(a, 4);
+    if (lane == 0) atomicAdd(gu_done + ls * kSyncStride, 1u);
+  }
+
+  // ---- 4. down: decode the slice into registers, wait for the slot's gate/up blocks, multiply; the workgroup then has
+  // the slot's block: k quarters summed in LDS (fixed order), H, svh_d and the route weight, stored per slot; the last
+  // slot to arrive sums the slots in slot order (reference kernels/fn_moe.metal:412-450)
+  f16x2 dw[kMaxDn][4];
+  if (has_dn) {
+    if (slot_shared(a, ls_d)) decode_pairs<KS>(area + GUB, 0, QK, dw);
+    else decode_pairs<K>(area + GUB, 0, QK, dw);
+  }
+  mark(a, 5);
+  bool dok = has_dn;
+  if (dok && lane == 0) {
+    bool got = false;
+    for (uint32_t it = 0; it < kSpin; it++) {
+      if (ld_relaxed(gu_done + ls_d * kSyncStride) >= (uint32_t)NBI) {
+        got = true;
+        break;
+      }
+      if ((it & 63u) == 63u && ld_relaxed(sync + kWordErr)) break;
+      __builtin_amdgcn_s_sleep(2);
+    }
+    if (!got) atomicOr(sync + kWordErr, 1u);
+    dok = got;
+  }
+  dok = __shfl(dok ? 1 : 0, 0, 64) != 0;
+  mark(a, 6);
+  float(*red)[32] = (float(*)[32])tiles;  // [wave][32] column sums: the tile areas are no longer read
+  if (dok) {
+    const int q = (lane >> 1) & 3;
+    f16x4 hv[kMaxDn];
+    const uint16_t *hp = a.hprep + (size_t)ls_d * INTER + dq * QK * 16 + 4 * q;
+#pragma unroll
+    for (int kt = 0; kt < QK; kt++) hv[kt] = __builtin_bit_cast(f16x4, ld_cg((const uint64_t *)(hp + kt * 16)));
+    float acc0 = 0.f, acc1 = 0.f;
+#pragma unroll
+    for (int kt = 0; kt < QK; kt++) {
+      acc0 = dot4(dw[kt][0], dw[kt][1], hv[kt], acc0);
+      acc1 = dot4(dw[kt][2], dw[kt][3], hv[kt], acc1);
+    }
+    lane_col_reduce(acc0, acc1);
+    if ((lane & 6) == 0) {
+      const int col = (lane >> 3) + 8 * (lane & 1);
+      red[wave][col] = acc0;
+      red[wave][16 + col] = acc1;
+    }
+  }
+  lds_barrier();
+  mark(a, 7);
+  if (dok && wave == 0) {
+    const int j = slot_j(a, ls_d), i0 = bd * 128 + lane, i1 = i0 + 64;
+    const uint16_t *sv = (const uint16_t *)(slot_block(a, rt, ls_d) + sv_off(a, ls_d, 2));
+    const float s0 = h2f(sv[i0]), s1 = h2f(sv[i1]);
+    float v[2];
+#pragma unroll
+    for (int h = 0; h < 2; h++) {  // column 64 h + lane of the block: pair (64 h + lane) / 32, quarters in order
+      const int w4 = ((h * 64 + lane) >> 5) * 4, c = lane & 31;
+      v[h] = ((red[w4][c] + red[w4 + 1][c]) + red[w4 + 2][c]) + red[w4 + 3][c];
+    }
+    st_cg(a.dn + (size_t)j * HID + i0, v[0]);  // inner down outputs, for reads
+    st_cg(a.dn + (size_t)j * HID + i1, v[1]);
+    fwht2(v[0], v[1], lane, HH, sch);
+    const float w = slot_shared(a, ls_d) ? rt.sg : rt.w[j];
+    float *ys = part_dn + (size_t)j * HID;  // per-slot weighted outputs
+    st_cg(ys + i0, v[0] * s0 * w);
+    st_cg(ys + i1, v[1] * s1 * w);
+    __builtin_amdgcn_s_waitcnt(0);
+    uint32_t old = 0;
+    if (lane == 0) old = atomicAdd(blk_cnt + bd * kSyncStride, 1u);
+    old = __shfl(old, 0, 64);
+    if (old == (uint32_t)a.nslot - 1u) {  // every slot of the block is stored: y = sum over slots in slot order
+      constexpr int U = 12;  // slots loaded in one batch
+      float yv[2] = {0.f, 0.f};
+      for (int j0 = 0; j0 < a.nslot; j0 += U) {
+        float t[U][2];
+#pragma unroll
+        for (int u = 0; u < U; u++)
+          if (j0 + u < a.nslot) {
+            t[u][0] = ld_cg(part_dn + (size_t)(j0 + u) * HID + i0);
+            t[u][1] = ld_cg(part_dn + (size_t)(j0 + u) * HID + i1);
+          }
+#pragma unroll
+        for (int u = 0; u < U; u++)
+          if (j0 + u < a.nslot) {
+            yv[0] += t[u][0];
+            yv[1] += t[u][1];
+          }
+      }
+      a.y[i0] = yv[0];
+      a.y[i1] = yv[1];
+    }
+  }
+
+  // ---- the last workgroup out resets the counters and advances the epoch
+  if (threadIdx.x == 0 && atomicAdd(sync + kWordExit, 1u) == gridDim.x - 1u) {
+    for (int i = 0; i < a.nslot; i++) st_cg(gu_done + i * kSyncStride, 0u);
+    for (int i = 0; i < NBLK; i++) st_cg(blk_cnt + i * kSyncStride, 0u);
+    for (int i = 0; i < a.nslot * NBI; i++) st_cg(fin_cnt + i * kSyncStride, 0u);
+    st_cg(sync + kWordEpoch, ld_cg(sync + kWordEpoch) + 1u);
+    __builtin_amdgcn_s_waitcnt(0);
+    atomicExch(sync + kWordExit, 0u);
+    if (a.trace) a.trace[(uint64_t)6000 * 8] = wall_clock64();
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------- host side
+namespace {
+using StepFn = const void *;
+template <int HID, int INTER>
+StepFn step_for_k(int K, int KS) {
+#define IJ_STEP(k, ks) \
+  if (K == k && KS == ks) return (StepFn)&moe_step<k, ks, HID, INTER>;
+  IJ_STEP(4, 4) IJ_STEP(5, 5) IJ_STEP(6, 6) IJ_STEP(4, 6) IJ_STEP(5, 6) IJ_STEP(4, 5)
+#undef IJ_STEP
+  return nullptr;
+}
+StepFn step_fn(int K, int KS, int hid, int inter) {
+  if (hid == 2048 && inter == 512) return step_for_k<2048, 512>(K, KS);
+  if (hid == 1024 && inter == 256) return step_for_k<1024, 256>(K, KS);
+  if (hid == 2560 && inter == 640) return step_for_k<2560, 640>(K, KS);
+  return nullptr;
+}
+size_t step_lds(int K, int KS) { return (size_t)kWaves * (kMaxGu + kMaxDn) * 64 * std::max(K, KS); }  // = kWaves AREA
+}  // namespace
+
+int moe_fused_grid() {
+  static int cus = 0;
+  if (!cus) {
+    int dev = 0;
+    IJ_HIP(hipGetDevice(&dev));
+    IJ_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+  }
+  return cus;
+}
+
+MoePlan moe_fused_plan(int hid, int inter, int topk, int nslot, int G) {
+  MoePlan pl;
+  const int NW = G * kWaves, IT = hid / 16, ITd = inter / 16, NPg = inter / 32, NBI = inter / 128, NBLK = hid / 128;
+  const int CG = nslot * 2 * NPg;
+  const long TG = (long)CG * IT;
+  // per-wave gate/up slice: even split, at least so long that a column has at most kMaxSeg segments
+  const int wg = (int)std::max<long>((TG + NW - 1) / NW, (IT + kMaxSeg - 2) / (kMaxSeg - 1));
+  // down: one (slot, 128-column block) per workgroup, a k quarter of one tile pair per wave
+  pl.ok = wg <= kMaxGu && wg <= IT && CG < 4096 && IT < 256 && ITd % 4 == 0 && ITd / 4 <= kMaxDn &&
+          nslot * NBLK <= G;
+  if (!pl.ok) return pl;
+  std::vector<uint32_t> slices((size_t)NW * 2, 0u), gnseg(CG, 0u);
+  for (int g = 0; g < NW; g++) {
+    long u = (long)g * wg, end = std::min<long>(u + wg, TG);
+    for (int s = 0; u < end; s++) {
+      const int col = (int)(u / IT), k0 = (int)(u % IT);
+      const int n = (int)std::min<long>(end - u, IT - k0);
+      slices[(size_t)g * 2 + s] = (uint32_t)col | (uint32_t)k0 << 12 | (uint32_t)n << 20 | gnseg[col] << 27;
+      gnseg[col]++;
+      u += n;
+    }
+  }
+  std::vector<uint32_t> fin_t((size_t)nslot * NBI, 0u);
+  for (int c = 0; c < CG; c++) fin_t[(c / (2 * NPg)) * NBI + (c % NPg) / 4] += gnseg[c];
+  pl.words = slices;
+  pl.words.insert(pl.words.end(), gnseg.begin(), gnseg.end());
+  pl.words.insert(pl.words.end(), fin_t.begin(), fin_t.end());
+  pl.part_floats = (size_t)CG * kMaxSeg * 32 + (size_t)nslot * hid;
+  pl.grid = G;
+  return pl;
+}
+
+bool moe_fused_supported(int K, int KS, int R, int hid, int inter, int ne, int topk) {
+  return R == 1 && step_fn(K, KS, hid, inter) != nullptr && ne <= kMaxExpertsV && topk <= kMaxTopkV &&
+         topk <= 64;
+}
+
+void launch_moe_fused(const MoeArgs &a, int grid, hipStream_t s) {
+  const int KS = a.nslot > a.topk ? a.slay.K : a.lay.K;
+  const StepFn f = step_fn(a.lay.K, KS, a.hid, a.inter);
+  IJ_CHECK(f && a.R == 1, "fused MoE step not instantiated for K%d / shared K%d at %d x %d, R %d", a.lay.K, KS, a.hid,
+           a.inter, a.R);
+  if (grid <= 0) grid = moe_fused_grid();
+  IJ_CHECK(grid * kWaves >= a.ne + a.has_sgate, "fused MoE: %d router rows on %d workgroups", a.ne + a.has_sgate, grid);
+  const size_t lds = step_lds(a.lay.K, KS);
+  static std::vector<StepFn> attr_set;  // functions whose dynamic LDS limit is raised already
+  if (std::find(attr_set.begin(), attr_set.end(), f) == attr_set.end()) {
+    IJ_HIP(hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    attr_set.push_back(f);
+  }
+  void *args[] = {const_cast<MoeArgs *>(&a)};
+  IJ_HIP(hipLaunchKernel(f, dim3(grid), dim3(64 * kWaves), args, lds, s));
+}
+
+const void *moe_fused_kernel(int K, int KS, int hid, int inter) { return step_fn(K, KS, hid, inter); }
+
+}  // namespace ijah

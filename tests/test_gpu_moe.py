@@ -132,15 +132,18 @@ def test_moe_synth_full_properties(eng):
 
 def test_moe_fused_and_staged_paths_agree(eng, oracle, monkeypatch):
     """The persistent fused launch and the four staged launches compute the same layer (same decode, prep and combine
-    arithmetic; the f32 k-accumulation order differs: one wave per column pair vs four), and each is deterministic."""
+    arithmetic; the f32 k-accumulation order differs), and each is deterministic; the inner outputs agree too."""
     w = synth.moe_layer(61, hid=2048, inter=512, ne=64, topk=10, K=5, shared=True, Ks=6, sgate=True)
-    x = synth.bf16_values(np.random.default_rng(62), 2, 2048)
+    x = synth.bf16_values(np.random.default_rng(62), 1, 2048)  # the fused step serves one row
     monkeypatch.setenv("IJAH_MOE_PATH", "staged")
-    ys = eng.moe_create(w).run(x)
+    st = eng.moe_create(w)
+    ys = st.run(x)
     monkeypatch.setenv("IJAH_MOE_PATH", "fused")
     m = eng.moe_create(w)
     yf = m.run(x)
     assert rel(yf, ys) < 1e-5
+    for name in ("experts_gu", "experts_dn"):
+        assert rel(m.read(name), st.read(name)) < 1e-5, name
     for _ in range(3):  # counters reset between launches
         assert np.array_equal(m.run(x), yf)
     check_layer(eng, oracle, m, oracle.MoeWeights(w), x)
