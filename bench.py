@@ -41,7 +41,7 @@ def kernel_bytes(hid=HID, inter=INTER, ne=NE, topk=TOPK, k=K, shared=1):
 def profiled_traffic(kernel):
     """HBM bytes per launch of the dominant kernel from the committed rocprofv3 PMC summary (FETCH_SIZE and
     WRITE_SIZE, each scaled by the copy-probe factor), or None when no summary covers it."""
-    f = ROOT / "profiles" / "moe_fused_k5_config2.md"
+    f = ROOT / "profiles" / "moe_step_k5_config2.md"
     if kernel != "fused" or not f.exists():
         return None
     for line in f.read_text().splitlines():

@@ -222,13 +222,14 @@ struct ne_moe {
   uint16_t *hprep = nullptr;
   uint32_t *route = nullptr, *sync = nullptr, *plan = nullptr;
   float *part = nullptr;
+  uint32_t *fsync = nullptr;  // the fused step's counters
   int plan_grid = 0;  // fused step: its grid (0: no plan, the staged path runs)
   uint64_t *trace = nullptr;  // IJAH_MOE_TRACE=1: per-unit timestamps of the fused kernel (debug)
   bool fused = true;  // one persistent launch per step (IJAH_MOE_PATH=staged: four launches)
   int last_R = 0;
   float *last_y = nullptr;
   ~ne_moe() {
-    for (void *p : std::initializer_list<void *>{experts, shared, router, logits, sgv, guo, dn, route, sync, trace, hprep, plan, part})
+    for (void *p : std::initializer_list<void *>{experts, shared, router, logits, sgv, guo, dn, route, sync, trace, hprep, plan, part, fsync})
       dev_free(p);
   }
   int nslot() const { return topk + has_shared; }
@@ -251,6 +252,8 @@ struct ne_moe {
         plan = dev_alloc<uint32_t>(pl.words.size());
         IJ_HIP(hipMemcpy(plan, pl.words.data(), pl.words.size() * 4, hipMemcpyHostToDevice));
         part = dev_alloc<float>(pl.part_floats);
+        fsync = dev_alloc<uint32_t>(moe_fused_sync_words(nslot(), hid, inter));
+        IJ_HIP(hipMemset(fsync, 0, 4 * moe_fused_sync_words(nslot(), hid, inter)));
         plan_grid = pl.grid;
       }
     }
@@ -296,6 +299,7 @@ struct ne_moe {
     a.hprep = hprep;
     a.units = plan;
     a.part = part;
+    a.fsync = fsync;
     return a;
   }
   // a failed cross-workgroup wait leaves the error word set: report it and clear the counters
@@ -306,6 +310,7 @@ struct ne_moe {
     if (err) {
       IJ_HIP(hipMemsetAsync(sync, 0, 4 * sync_words(Rcap, nslot(), hid, inter), s));
       IJ_HIP(hipMemsetAsync(logits, 0, sizeof(float) * logit_floats(Rcap), s));  // launch tags restart with the epoch
+      if (fsync) IJ_HIP(hipMemsetAsync(fsync, 0, 4 * moe_fused_sync_words(nslot(), hid, inter), s));
       IJ_HIP(hipStreamSynchronize(s));
       throw Error("moe: a cross-workgroup wait timed out (layer output invalid)");
     }

@@ -52,6 +52,7 @@ struct MoeArgs {
   uint16_t *hprep;                     // fused kernel: [R nslot][inter] fp16 down inputs (kp order)
   const uint32_t *units;               // fused kernel: the plan words (MoePlan::words) in device memory
   float *part;                         // fused kernel: column partial sums (MoePlan::part_floats)
+  uint32_t *fsync;                     // fused kernel: its counters (moe_fused_sync_words), zero when created
 };
 void launch_moe_router(const MoeArgs &a, hipStream_t s);
 void launch_moe_gateup(const MoeArgs &a, hipStream_t s);
@@ -68,6 +69,9 @@ struct MoePlan {
 int moe_fused_grid();
 MoePlan moe_fused_plan(int hid, int inter, int topk, int nslot, int grid);
 bool moe_fused_supported(int K, int KS, int R, int hid, int inter, int ne, int topk);
+inline size_t moe_fused_sync_words(int nslot, int hid, int inter) {
+  return 64 * (1 + (size_t)nslot * (inter / 128) + hid / 128);
+}
 void launch_moe_fused(const MoeArgs &a, int grid, hipStream_t s);
 const void *moe_fused_kernel(int K, int KS, int hid, int inter);  // nullptr if not instantiated
 // Fused step logits: kLogitReplicas copies of [ne + 1] floats, moe_logit_stride(ne) floats apart (replica 0 is the

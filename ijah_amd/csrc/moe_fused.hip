@@ -42,12 +42,11 @@ constexpr int kPrepHalves = 2 * 3 * 128;   // two segments of up to three 128-ch
 constexpr int kMaxExpertsV = 1024;
 constexpr int kMaxTopkV = 32;
 constexpr uint32_t kSpin = 1u << 22;       // bounded waits: polls of ~0.1-1 us each, far beyond any real wait
-enum {  // words 0-2 belong to the staged kernels' counters
-  kWordExit = 5 * kSyncStride,
-  kWordEpoch = 4 * kSyncStride,            // launches so far (mod 2^32); tags this launch's logits
-  kWordErr = kSyncErrWord,
-  kWordGuDone = 8 * kSyncStride            // then: gu_done[nslot], blk[nblk], fin[nslot * nbi], one line each
-};
+enum { kWordErr = kSyncErrWord };  // the error word of the layer's sync block (shared with the staged kernels)
+// The fused step's own counters (MoeArgs::fsync), one per 256-byte line, never reset: line 0 holds a u64 count of
+// finished workgroups over all launches, so a launch's epoch e = count / grid; then fin[nslot * NBI] (gate/up
+// partials per (slot, 128-column block)) and blk[NBLK] (slots stored per output block), which grow by the same
+// amount T every launch and are compared as (value - e T) mod 2^32. No workgroup has to reset anything at the end.
 
 __device__ __forceinline__ uint32_t ld_relaxed(const uint32_t *p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -330,10 +329,9 @@ __device__ __forceinline__ void decode_pairs(const uint8_t *tl, int t0, int n, f
 }
 
 // ---------------------------------------------------------------------------------------------------- counting
-// Each wave posts up to two counter indices (or ~0u) in ids[2 wave + s]; wave kCtl merges runs of equal neighbours and
-// adds each run with one atomic; fin[i] = the counter index this workgroup completed (target[idx] reached), else -1.
-// All threads call it (barriers inside).
-__device__ void count_runs(uint32_t *ctr, const uint32_t *target, const uint32_t *ids, int *fin, uint64_t *trace) {
+// Each wave posts up to two counter indices (or ~0u) in ids[2 wave + s]; wave kCtl merges runs of equal neighbours
+// and adds each run to its counter with one atomic. All threads call it (barriers inside).
+__device__ void add_runs(uint32_t *ctr, const uint32_t *ids) {
   const int lane = threadIdx.x & 63;
   lds_barrier();
   if ((int)(threadIdx.x >> 6) == kCtl) {
@@ -345,14 +343,7 @@ __device__ void count_runs(uint32_t *ctr, const uint32_t *target, const uint32_t
     const bool head = valid && (lane == 0 || prv != id);
     const bool tail = valid && (lane == 2 * kWaves - 1 || nxt != id);
     const uint64_t tails = __ballot(tail);
-    int res = -1;
-    if (head) {
-      const uint32_t cnt = (uint32_t)__builtin_ctzll(tails >> lane) + 1u;
-      const uint32_t old = atomicAdd(ctr + (uint64_t)id * kSyncStride, cnt);
-      if (old + cnt == target[id]) res = (int)id;
-      if (trace) trace[(uint64_t)(256 + blockIdx.x) * 8 + 5] = wall_clock64();
-    }
-    if (in) fin[lane] = res;
+    if (head) atomicAdd(ctr + (uint64_t)id * kSyncStride, (uint32_t)__builtin_ctzll(tails >> lane) + 1u);
   }
   lds_barrier();
 }
@@ -389,8 +380,7 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
   __shared__ _Float16 prep[kWaves][kPrepHalves];  // per segment: suh chunks (DMA), then fp16(H(x suh)) in place
   __shared__ __attribute__((aligned(16))) float xl[HID];  // the input row
   __shared__ Route rt;
-  __shared__ uint32_t s_tag, s_ok, ids[2 * kWaves];
-  __shared__ int fin[64];
+  __shared__ uint32_t s_tag, s_ok, s_ep, ids[2 * kWaves];
   const float sch = a.sc_hid, sci = a.sc_inter;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, G = (int)gridDim.x;
   const int NW = G * kWaves, CG = a.nslot * 2 * NPg;
@@ -400,13 +390,16 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
   pw.y = __builtin_amdgcn_readfirstlane(pw.y);
   const uint32_t *gu_nseg = plan + 2 * NW, *fin_tgt = gu_nseg + CG;
   uint32_t *sync = a.sync;
-  uint32_t *gu_done = sync + kWordGuDone;               // [ls]: finished 128-column blocks of slot ls
-  uint32_t *blk_cnt = gu_done + a.nslot * kSyncStride;   // [c]: slots stored of output block c
-  uint32_t *fin_cnt = blk_cnt + NBLK * kSyncStride;      // [ls * NBI + cb]: gate/up partials of a block
+  uint32_t *fin_cnt = a.fsync + kSyncStride;                  // [ls * NBI + cb]: gate/up partials of a block
+  uint32_t *blk_cnt = fin_cnt + a.nslot * NBI * kSyncStride;  // [c]: slots stored of output block c
   float *part_gu = a.part, *part_dn = a.part + (size_t)CG * kMaxSeg * 32;  // gate/up partials; weighted slot outputs
   uint8_t *area = tiles + wave * AREA;
   mark(a, 0);
-  if (threadIdx.x == 0) s_tag = ld_cg(sync + kWordEpoch) % 65535u + 1u;  // 1..65535, never the initial 0
+  if (threadIdx.x == 0) {
+    const uint64_t e = ld_cg((const uint64_t *)a.fsync) / (uint64_t)G;
+    s_tag = (uint32_t)(e % 65535u) + 1u;  // 1..65535, never the initial 0
+    s_ep = (uint32_t)e;
+  }
 
   const Seg g0 = seg_of(pw.x), g1 = seg_of(pw.y);
   // gate/up column c = (ls * 2 + proj) * NPg + p; down column c = ls * NPd + p
@@ -489,7 +482,9 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
         dst[c * 128 + kp(lane + 64)] = to_f16(v1);
       }
   };
+  if (a.trace && lane == 0) a.trace[(uint64_t)(512 + blockIdx.x * kWaves + wave) * 8 + 3] = wall_clock64();
   wait_vm(n_g0 + n_g1 + n_dn);  // suh chunks are in
+  if (a.trace && lane == 0) a.trace[(uint64_t)(512 + blockIdx.x * kWaves + wave) * 8 + 4] = wall_clock64();
   if (ok && g0.n) prep_seg(g0, prep[wave]);
   if (ok && g1.n) prep_seg(g1, prep[wave] + 384);
   mark(a, 3);
@@ -503,6 +498,8 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
     const int steps = n_seg > 0 ? n_seg : 1;
     for (int j = 0; j < steps; j++) {
       if (n_seg > 0) wait_vm(n_after + n_seg - 1 - j);
+      if (a.trace && lane == 0 && j == steps - 1) a.trace[(uint64_t)(512 + blockIdx.x * kWaves + wave) * 8 + 1] = wall_clock64();
+      if (a.trace && lane == 0 && j == 0 && n_seg > 0) a.trace[(uint64_t)(512 + blockIdx.x * kWaves + wave) * 8 + 5] = wall_clock64();
       const int kt1 = j == steps - 1 ? s.n : (int)((uint32_t)(j + 1) * 1024u / pb);
       if (kt1 > kt0) {
         if (sh)
@@ -525,6 +522,7 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
   float ga0 = 0.f, ga1 = 0.f, gb0s = 0.f, gb1s = 0.f;
   if (ok && g0.n) gu_dot(g0, 0, prep[wave], n_g0, n_g1 + n_dn, ga0, ga1);
   if (ok && g1.n) gu_dot(g1, off1, prep[wave] + 384, n_g1, n_dn, gb0s, gb1s);
+  if (a.trace && lane == 0) a.trace[(uint64_t)(512 + blockIdx.x * kWaves + wave) * 8 + 2] = wall_clock64();
   if (ok && g0.n) gu_store(g0, ga0, ga1);
   if (ok && g1.n) gu_store(g1, gb0s, gb1s);
   if (wave == 0) mark2(a, 0);
@@ -536,93 +534,89 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
     ids[2 * wave + 1] = (ok && g1.n) ? (uint32_t)(gu_ls(g1) * NBI + gu_p(g1) / 4) : ~0u;
   }
   if (a.trace && threadIdx.x == 0) a.trace[(uint64_t)(256 + blockIdx.x) * 8 + 6] = wall_clock64();
-  count_runs(fin_cnt, fin_tgt, ids, fin, a.trace);
+  add_runs(fin_cnt, ids);
   mark(a, 4);
-  // gate/up block finisher (one wave per completed block): sums the partials in segment order, then the down
+  // ---- 4. down. The workgroup of (slot ls_d, output block bd) first finishes the slot's gate/up blocks itself:
+  // wave cb < NBI waits until every partial of block cb is stored, sums them in segment order and applies the down
   // prologue (reference kernels/fn_moe.metal:370-384): g = H(inner_g) svh_g, u = H(inner_u) svh_u,
-  // h = H(silu(g) u suh_d) -> fp16 in kp order
-  for (int fi = wave; fi < 2 * kWaves; fi += kWaves) {
-    const int id = fin[fi];
-    if (id < 0) continue;
-    const int ls = id / NBI, cb = id % NBI;
-    mark2(a, 2);
-    const uint8_t *blk = slot_block(a, rt, ls);
-    const int i0 = cb * 128 + lane, i1 = i0 + 64;
-    Partials pp[2][2];
-    int ns[2][2];
-#pragma unroll
-    for (int proj = 0; proj < 2; proj++)
-#pragma unroll
-      for (int h = 0; h < 2; h++) {
-        const int i = cb * 128 + h * 64 + lane, c = (ls * 2 + proj) * NPg + i / 32;
-        pp[proj][h] = load_partials(part_gu + (size_t)c * kMaxSeg * 32 + (i & 31));
-        ns[proj][h] = (int)gu_nseg[c];
-      }
-    const uint16_t *svg = (const uint16_t *)(blk + sv_off(a, ls, 0)), *svu = (const uint16_t *)(blk + sv_off(a, ls, 1));
-    const uint16_t *sud = (const uint16_t *)(blk + su_off(a, ls, 2));
-    const float sg0 = h2f(svg[i0]), sg1 = h2f(svg[i1]), su0 = h2f(svu[i0]), su1 = h2f(svu[i1]);
-    const float sd0 = h2f(sud[i0]), sd1 = h2f(sud[i1]);
-    float gu[2][2];
-#pragma unroll
-    for (int proj = 0; proj < 2; proj++)
-#pragma unroll
-      for (int h = 0; h < 2; h++) gu[proj][h] = sum_partials(pp[proj][h], ns[proj][h]);
-    mark2(a, 3);
-    float *gsum = a.guo + (size_t)slot_j(a, ls) * 2 * INTER;  // inner gate / up outputs, for reads
-    st_cg(gsum + i0, gu[0][0]);
-    st_cg(gsum + i1, gu[0][1]);
-    st_cg(gsum + INTER + i0, gu[1][0]);
-    st_cg(gsum + INTER + i1, gu[1][1]);
-    float g0v = gu[0][0], g1v = gu[0][1], u0v = gu[1][0], u1v = gu[1][1];
-    fwht2(g0v, g1v, lane, HI, sci);
-    fwht2(u0v, u1v, lane, HI, sci);
-    g0v = g0v * sg0;
-    u0v = u0v * su0;
-    g1v = g1v * sg1;
-    u1v = u1v * su1;
-    float h0 = g0v / (1.f + expf(-g0v)) * u0v * sd0;
-    float h1 = g1v / (1.f + expf(-g1v)) * u1v * sd1;
-    fwht2(h0, h1, lane, HI, sci);
-    uint16_t *hp = a.hprep + (size_t)ls * INTER + cb * 128;
-    st_cg(hp + kp(lane), f2h(h0));
-    st_cg(hp + kp(lane + 64), f2h(h1));
-    __builtin_amdgcn_s_waitcnt(0);
-    mark2(a, 4);
-    if (lane == 0) atomicAdd(gu_done + ls * kSyncStride, 1u);
-  }
-
-  // ---- 4. down: decode the slice into registers, wait for the slot's gate/up blocks, multiply; the workgroup then has
-  // the slot's block: k quarters summed in LDS (fixed order), H, svh_d and the route weight, stored per slot; the last
-  // slot to arrive sums the slots in slot order (reference kernels/fn_moe.metal:412-450)
+  // h = H(silu(g) u suh_d) -> fp16 in kp order, into LDS. Its down slice is decoded into registers meanwhile.
   f16x2 dw[kMaxDn][4];
   if (has_dn) {
     if (slot_shared(a, ls_d)) decode_pairs<KS>(area + GUB, 0, QK, dw);
     else decode_pairs<K>(area + GUB, 0, QK, dw);
   }
   mark(a, 5);
-  bool dok = has_dn;
-  if (dok && lane == 0) {
+  _Float16 *hl = prep[0];  // the slot's down input, INTER halves (the prep areas are no longer read)
+  if (has_dn && wave < NBI) {
+    const int cb = wave, ls = ls_d, id = ls * NBI + cb;
     bool got = false;
-    for (uint32_t it = 0; it < kSpin; it++) {
-      if (ld_relaxed(gu_done + ls_d * kSyncStride) >= (uint32_t)NBI) {
-        got = true;
-        break;
+    if (lane == 0) {
+      for (uint32_t it = 0; it < kSpin; it++) {
+        if (ld_relaxed(fin_cnt + id * kSyncStride) - s_ep * fin_tgt[id] >= fin_tgt[id]) {
+          got = true;
+          break;
+        }
+        if ((it & 63u) == 63u && ld_relaxed(sync + kWordErr)) break;
+        __builtin_amdgcn_s_sleep(1);
       }
-      if ((it & 63u) == 63u && ld_relaxed(sync + kWordErr)) break;
-      __builtin_amdgcn_s_sleep(2);
+      if (!got) atomicOr(sync + kWordErr, 1u);
     }
-    if (!got) atomicOr(sync + kWordErr, 1u);
-    dok = got;
+    if (__shfl(got ? 1 : 0, 0, 64)) {
+      mark2(a, 2);
+      const uint8_t *blk = slot_block(a, rt, ls);
+      const int i0 = cb * 128 + lane, i1 = i0 + 64;
+      Partials pp[2][2];
+      int ns[2][2];
+#pragma unroll
+      for (int proj = 0; proj < 2; proj++)
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+          const int i = cb * 128 + h * 64 + lane, c = (ls * 2 + proj) * NPg + i / 32;
+          pp[proj][h] = load_partials(part_gu + (size_t)c * kMaxSeg * 32 + (i & 31));
+          ns[proj][h] = (int)gu_nseg[c];
+        }
+      const uint16_t *svg = (const uint16_t *)(blk + sv_off(a, ls, 0)), *svu = (const uint16_t *)(blk + sv_off(a, ls, 1));
+      const uint16_t *sud = (const uint16_t *)(blk + su_off(a, ls, 2));
+      const float sg0 = h2f(svg[i0]), sg1 = h2f(svg[i1]), su0 = h2f(svu[i0]), su1 = h2f(svu[i1]);
+      const float sd0 = h2f(sud[i0]), sd1 = h2f(sud[i1]);
+      float gu[2][2];
+#pragma unroll
+      for (int proj = 0; proj < 2; proj++)
+#pragma unroll
+        for (int h = 0; h < 2; h++) gu[proj][h] = sum_partials(pp[proj][h], ns[proj][h]);
+      mark2(a, 3);
+      float g0v = gu[0][0], g1v = gu[0][1], u0v = gu[1][0], u1v = gu[1][1];
+      fwht2(g0v, g1v, lane, HI, sci);
+      fwht2(u0v, u1v, lane, HI, sci);
+      g0v = g0v * sg0;
+      u0v = u0v * su0;
+      g1v = g1v * sg1;
+      u1v = u1v * su1;
+      float h0 = g0v / (1.f + expf(-g0v)) * u0v * sd0;
+      float h1 = g1v / (1.f + expf(-g1v)) * u1v * sd1;
+      fwht2(h0, h1, lane, HI, sci);
+      hl[cb * 128 + kp(lane)] = to_f16(h0);
+      hl[cb * 128 + kp(lane + 64)] = to_f16(h1);
+      if (bd == 0) {  // inner gate / up outputs, for reads (one workgroup per slot; nothing waits for them)
+        float *gsum = a.guo + (size_t)slot_j(a, ls) * 2 * INTER;
+        st_cg(gsum + i0, gu[0][0]);
+        st_cg(gsum + i1, gu[0][1]);
+        st_cg(gsum + INTER + i0, gu[1][0]);
+        st_cg(gsum + INTER + i1, gu[1][1]);
+      }
+      mark2(a, 4);
+    }
   }
-  dok = __shfl(dok ? 1 : 0, 0, 64) != 0;
+  bool dok = has_dn;
+  lds_barrier();
   mark(a, 6);
   float(*red)[32] = (float(*)[32])tiles;  // [wave][32] column sums: the tile areas are no longer read
   if (dok) {
     const int q = (lane >> 1) & 3;
     f16x4 hv[kMaxDn];
-    const uint16_t *hp = a.hprep + (size_t)ls_d * INTER + dq * QK * 16 + 4 * q;
+    const _Float16 *hp = hl + dq * QK * 16 + 4 * q;
 #pragma unroll
-    for (int kt = 0; kt < QK; kt++) hv[kt] = __builtin_bit_cast(f16x4, ld_cg((const uint64_t *)(hp + kt * 16)));
+    for (int kt = 0; kt < QK; kt++) hv[kt] = *(const f16x4 *)(hp + kt * 16);
     float acc0 = 0.f, acc1 = 0.f;
 #pragma unroll
     for (int kt = 0; kt < QK; kt++) {
@@ -659,7 +653,9 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
     uint32_t old = 0;
     if (lane == 0) old = atomicAdd(blk_cnt + bd * kSyncStride, 1u);
     old = __shfl(old, 0, 64);
-    if (old == (uint32_t)a.nslot - 1u) {  // every slot of the block is stored: y = sum over slots in slot order
+    if (a.trace && lane == 0) a.trace[(uint64_t)(6001 + blockIdx.x) * 8 + 3] = wall_clock64();
+    if (old - s_ep * (uint32_t)a.nslot == (uint32_t)a.nslot - 1u) {  // every slot of the block is stored: y = the sum
+                                                                     // over the slots in slot order
       constexpr int U = 12;  // slots loaded in one batch
       float yv[2] = {0.f, 0.f};
       for (int j0 = 0; j0 < a.nslot; j0 += U) {
@@ -679,19 +675,12 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
       }
       a.y[i0] = yv[0];
       a.y[i1] = yv[1];
+      if (a.trace && lane == 0) a.trace[(uint64_t)(6001 + blockIdx.x) * 8 + 4] = wall_clock64();
     }
   }
 
-  // ---- the last workgroup out resets the counters and advances the epoch
-  if (threadIdx.x == 0 && atomicAdd(sync + kWordExit, 1u) == gridDim.x - 1u) {
-    for (int i = 0; i < a.nslot; i++) st_cg(gu_done + i * kSyncStride, 0u);
-    for (int i = 0; i < NBLK; i++) st_cg(blk_cnt + i * kSyncStride, 0u);
-    for (int i = 0; i < a.nslot * NBI; i++) st_cg(fin_cnt + i * kSyncStride, 0u);
-    st_cg(sync + kWordEpoch, ld_cg(sync + kWordEpoch) + 1u);
-    __builtin_amdgcn_s_waitcnt(0);
-    atomicExch(sync + kWordExit, 0u);
-    if (a.trace) a.trace[(uint64_t)6000 * 8] = wall_clock64();
-  }
+  // ---- done: count this workgroup (the next launch derives its epoch from the count)
+  if (threadIdx.x == 0) atomicAdd((unsigned long long *)a.fsync, 1ull);
 }
 
 // ---------------------------------------------------------------------------------------------------- host side
