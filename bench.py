@@ -79,6 +79,35 @@ def cpu_baseline(seconds=10.0):
             "sample": f"{n} M=1 layers (router 512x2048 + top-10 + 11 K5 experts of 2048x512x3) in {el:.1f}s"}
 
 
+def moe_flops(R, hid=HID, inter=INTER, topk=TOPK, shared=1):
+    """Algorithmic flops of the layer's expert GEMMs at R rows (gate, up, down per slot; router excluded)."""
+    return 2.0 * 3 * hid * inter * R * (topk + shared)
+
+
+def measure_batch(eng, R, n_layers, steps, seed):
+    """The layer at R rows (BASELINE.json config 4 at R = 16, config 5 at R = 4096) on the grouped matrix-core path:
+    a chain of n_layers distinct synthetic layers in one HIP graph. Returns a dict for the JSON line."""
+    from ijah_amd import synth
+    layers = [eng.moe_synth(HID, INTER, NE, TOPK, K, True, K, seed=seed + 7919 * i) for i in range(n_layers)]
+    x = synth.bf16_values(np.random.default_rng(seed), R, HID)
+    xb = eng.from_numpy(x)
+    yb = eng.alloc(R * HID * 4)
+    for m in layers:
+        m.run_bufs(R, xb, yb)
+    eng.sync()
+    byts = float(np.mean([m.bytes(R) for m in layers]))
+    us = eng.moe_time(layers, R, xb, warmup=2, reps=steps)
+    fl = moe_flops(R)
+    out = {"rows": R, "layers_per_step": n_layers, "us_per_layer": round(us, 2),
+           "tokens_per_s_per_layer": round(R * 1e6 / us, 1),
+           "weight_bytes_per_layer": int(byts), "weight_GBps": round(byts / (us * 1e-6) / 1e9, 1),
+           "expert_gemm_TFLOPs": round(fl / (us * 1e-6) / 1e12, 2),
+           "pct_bf16_mfma_peak": round(100 * fl / (us * 1e-6) / 2.5e15, 2)}
+    for m in layers:
+        m.free()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -87,6 +116,7 @@ def main():
     ap.add_argument("--layers", type=int, default=32)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-batch", action="store_true", help="skip the verify (R=16) and prefill (R=4096) lines")
     ap.add_argument("--eager-only", action="store_true",
                     help="run the layer chain eagerly --steps times and exit (for rocprofv3 --pmc passes)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MB",
@@ -145,6 +175,14 @@ def main():
     print("kernels (us per launch): " + ", ".join(f"{k} {v:.2f} ({kb[k] / (v * 1e-6) / 1e9:.0f} GB/s)"
                                                  for k, v in kus.items()), file=sys.stderr, flush=True)
 
+    extra = {}
+    if not a.no_batch:
+        for m in layers:  # the M=1 layers' memory is no longer needed
+            m.free()
+        extra["verify_r16"] = measure_batch(eng, 16, 32, max(5, a.steps // 5), a.seed + 16)
+        print(f"verify R=16: {extra['verify_r16']}", file=sys.stderr, flush=True)
+        extra["prefill_r4096"] = measure_batch(eng, 4096, 4, 3, a.seed + 4096)
+        print(f"prefill R=4096: {extra['prefill_r4096']}", file=sys.stderr, flush=True)
     cpu = None if a.no_cpu else cpu_baseline()
     line = {
         "metric": "MoE layer us + effective packed-weight GB/s (% HBM peak), 5-bit EXL3, M=1",
@@ -162,6 +200,7 @@ def main():
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": profiled_traffic(dom),
                      "bytes_per_launch": kb[dom]},
         "cpu_baseline": cpu,
+        **extra,
     }
     print(json.dumps(line), flush=True)
 

@@ -224,6 +224,9 @@ struct ne_moe {
   float *part = nullptr;
   uint32_t *fsync = nullptr;  // the fused step's counters
   int plan_grid = 0;  // fused step: its grid (0: no plan, the staged path runs)
+  MoeBatchBufs bat;   // batched path (R >= 2)
+  int bat_R = 0;      // rows the batched buffers hold
+  bool batch = true;  // R >= 2 on the grouped matrix-core path (IJAH_MOE_PATH=staged: the staged kernels)
   uint64_t *trace = nullptr;  // IJAH_MOE_TRACE=1: per-unit timestamps of the fused kernel (debug)
   bool fused = true;  // one persistent launch per step (IJAH_MOE_PATH=staged: four launches)
   int last_R = 0;
@@ -231,8 +234,30 @@ struct ne_moe {
   ~ne_moe() {
     for (void *p : std::initializer_list<void *>{experts, shared, router, logits, sgv, guo, dn, route, sync, trace, hprep, plan, part, fsync})
       dev_free(p);
+    free_batch();
   }
   int nslot() const { return topk + has_shared; }
+  void free_batch() {
+    for (void *p : std::initializer_list<void *>{bat.bk, bat.chunks, bat.rows, bat.xh, bat.hh, bat.dnw}) dev_free(p);
+    bat = MoeBatchBufs();
+    bat_R = 0;
+  }
+  bool batch_ok(int R) const {
+    return batch && R >= 2 && moe_batch_supported(K, has_shared ? Ks : K, hid, inter, ne, topk);
+  }
+  void ensure_batch(int R) {
+    if (R <= bat_R || !batch_ok(R)) return;
+    free_batch();
+    const size_t S = (size_t)R * nslot();
+    bat.max_chunks = moe_batch_max_chunks(R, ne, topk, has_shared);
+    bat.bk = dev_alloc<uint32_t>(3 * (size_t)(ne + 1) + 1);
+    bat.chunks = dev_alloc<uint32_t>(3 * (size_t)bat.max_chunks);
+    bat.rows = dev_alloc<uint32_t>(S);
+    bat.xh = dev_alloc<uint16_t>(S * 2 * hid);
+    bat.hh = dev_alloc<uint16_t>(S * inter);
+    bat.dnw = dev_alloc<float>(S * hid);
+    bat_R = R;
+  }
   size_t logit_floats(int R) const {
     return std::max<size_t>((size_t)R * (ne + 1), (size_t)kLogitReplicas * moe_logit_stride(ne));
   }
@@ -267,6 +292,7 @@ struct ne_moe {
     }
     IJ_HIP(hipMemset(sync, 0, 4 * sync_words(R, nslot(), hid, inter)));
     Rcap = R;
+    ensure_batch(R);
   }
   MoeArgs args(int R, const float *x, float *y) const {
     MoeArgs a;
@@ -318,6 +344,10 @@ struct ne_moe {
   bool fused_ok(int R) const { return fused && plan_grid > 0 && R == 1; }
   void launch(int R, const float *x, float *y, hipStream_t s) const {
     const MoeArgs a = args(R, x, y);
+    if (batch_ok(R) && R <= bat_R) {
+      launch_moe_batch(a, bat, s);
+      return;
+    }
     if (fused_ok(R)) {
       launch_moe_fused(a, plan_grid, s);
       return;
@@ -403,7 +433,7 @@ ne_moe *moe_create(const ne_moe_desc &d) {
   m->router = dev_alloc<uint16_t>(rrows * d.hid);
   IJ_HIP(hipMemcpy(m->router, d.router, 2u * d.ne * d.hid, hipMemcpyHostToDevice));
   if (m->has_sgate) IJ_HIP(hipMemcpy(m->router + (size_t)d.ne * d.hid, d.sgate, 2u * d.hid, hipMemcpyHostToDevice));
-  if (const char *e = getenv("IJAH_MOE_PATH")) m->fused = strcmp(e, "staged") != 0;
+  if (const char *e = getenv("IJAH_MOE_PATH")) m->fused = m->batch = strcmp(e, "staged") != 0;
   if (const char *e = getenv("IJAH_MOE_KSPLIT")) m->ksplit = std::max(1, atoi(e));
   IJ_CHECK((d.hid / 16) % m->ksplit == 0 && ((d.hid / 16) / m->ksplit) % 8 == 0, "ksplit %d does not divide hid %d",
            m->ksplit, d.hid);
@@ -512,7 +542,7 @@ NE_API ne_moe *ne_moe_synth(int hid, int inter, int ne, int topk, int K, int has
     }
     m->router = dev_alloc<uint16_t>((size_t)ne * hid);
     launch_fill_normal_bf16(m->router, (size_t)ne * hid, seed * 7 + 5, (float)(1.0 / std::sqrt((double)hid)), s);
-    if (const char *e = getenv("IJAH_MOE_PATH")) m->fused = strcmp(e, "staged") != 0;
+    if (const char *e = getenv("IJAH_MOE_PATH")) m->fused = m->batch = strcmp(e, "staged") != 0;
     if (const char *e = getenv("IJAH_MOE_KSPLIT")) m->ksplit = std::max(1, atoi(e));
     IJ_CHECK((hid / 16) % m->ksplit == 0 && ((hid / 16) / m->ksplit) % 8 == 0, "ksplit %d does not divide hid %d",
              m->ksplit, hid);
@@ -582,6 +612,8 @@ NE_API int ne_moe_read(ne_moe *m, const char *name, void *dst, uint64_t nbytes) 
       fetch(m->route, (size_t)R * 2 * m->topk * 4);
     } else if (n == "shared_gate") {
       fetch(m->sgv, (size_t)R * 4);
+    } else if ((n == "experts_gu" || n == "experts_dn") && m->batch_ok(R)) {
+      IJ_CHECK(false, "\"%s\" is not kept by the batched path (R >= 2); IJAH_MOE_PATH=staged keeps it", name);
     } else if (n == "experts_gu" && m->fused_ok(R)) {  // the fused step stores the summed inner outputs
       fetch(m->guo, (size_t)S * 2 * m->inter * 4);
     } else if (n == "experts_gu") {

@@ -74,6 +74,19 @@ inline size_t moe_fused_sync_words(int nslot, int hid, int inter) {
 }
 void launch_moe_fused(const MoeArgs &a, int grid, hipStream_t s);
 const void *moe_fused_kernel(int K, int KS, int hid, int inter);  // nullptr if not instantiated
+// The batched layer (moe_batch.hip) for R >= 2 rows: device buffers sized by the host for R rows.
+struct MoeBatchBufs {
+  uint32_t *bk = nullptr;      // [ne + 1] counts, [ne + 1] offsets, [ne + 1] cursors, 1 chunk count
+  uint32_t *chunks = nullptr;  // [max_chunks][3] (expert, first sorted row, rows)
+  uint32_t *rows = nullptr;    // [R nslot] sorted row -> slot r * nslot + k
+  uint16_t *xh = nullptr;      // [R nslot][2][hid] prepared gate / up inputs, fp16, kp order
+  uint16_t *hh = nullptr;      // [R nslot][inter] prepared down inputs
+  float *dnw = nullptr;        // [R][nslot][hid] weighted slot outputs
+  int max_chunks = 0;
+};
+bool moe_batch_supported(int K, int KS, int hid, int inter, int ne, int topk);
+int moe_batch_max_chunks(int R, int ne, int topk, bool shared);
+void launch_moe_batch(const MoeArgs &a, const MoeBatchBufs &b, hipStream_t s);
 // Fused step logits: kLogitReplicas copies of [ne + 1] floats, moe_logit_stride(ne) floats apart (replica 0 is the
 // [R = 1][ne + 1] logits buffer the staged path uses); the copies spread the workgroups' polling over memory channels.
 constexpr int kLogitReplicas = 8;

@@ -1,0 +1,498 @@
+// The MoE layer for a batch of rows (speculative verify, prefill): router GEMM, per-row top-k, slots sorted by
+// expert, and grouped expert GEMMs on the matrix cores that decode each expert's EXL3 tiles once per 128-row chunk
+// and feed them to v_mfma_f32_32x32x16_f16 (reference kernels/prefill/pf_moe.metal:26-338 and
+// kernels/fn_moe.metal:677-884, driven by prefill.mm:235-276).
+//
+// Launches, in order:
+//   bat_router   logits[R][ne (+ shared gate)] = bf16(x . router) in f32 (reference kernels/fn_moe.metal:50-67)
+//   bat_route    per row: top-k, ties to the lower index, weights exp(l - l_max) / sum (kernels/fn_moe.metal:76-131);
+//                counts the routed slots per expert
+//   bat_scan     per-expert offsets of the expert-sorted slot list (the shared expert's rows last) and the list of
+//                128-row chunks (expert, first row, rows) the GEMMs run over (kernels/prefill/pf_moe.metal:26-83)
+//   bat_place    each slot's place in its expert's rows (row order inside an expert does not change any result:
+//                every row is computed independently)
+//   bat_prep     xh[row][proj] = fp16(H(x[token] * suh_e,proj)) in kp order for the gate and the up projection (each
+//                linear has its own suh), per sorted row (kernels/prefill/pf_moe.metal:85-110)
+//   bat_gateup   per (chunk, 128-column block ib of inter): gate and up GEMMs on the matrix cores, then the down
+//                prologue on the block: hh[row][ib] = fp16(H(silu(H(g) svh_g) H(u) svh_u suh_d)) (:111-140)
+//   bat_down     per (chunk, 128-column block of hid): the down GEMM, then H, svh_d and the slot's route weight,
+//                stored per (token, slot) (:141-161)
+//   bat_combine  y[token] = sum over the token's slots in slot order
+//
+// Matrix-core operands (this build's layout): a 16-row k tile of A is held in the reference's kp order, so lane
+// (m, h) of v_mfma_f32_32x32x16_f16 reads rows m, k positions [8h, 8h + 8) as one 16-byte LDS read. The decoder's
+// lane for (column c, quad q) writes its four weights (rows 2q, 2q+1, 2q+8, 2q+9 = kp positions 4q..4q+3) of both
+// tiles of a pair to LDS at [tile][c][q]; matrix-core lane (n, h) then reads quads 2h and 2h+1 of column n as one
+// 16-byte read: the same k permutation on both operands.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+
+#include "exl3_device.h"
+#include "kernels.h"
+
+namespace ijah {
+
+namespace {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kChunkRows = 128;   // rows of one GEMM chunk (4 matrix-core row blocks of 32)
+constexpr int kRowBlocks = kChunkRows / 32;
+constexpr int kAhead = 6;         // k tiles requested ahead of the one being multiplied
+constexpr int kRing = kAhead + 2; // LDS ring slots per stream
+
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+__device__ __forceinline__ void wait_vm(int n) {
+  switch (n < 15 ? n : 15) {
+#define IJ_VM(k) \
+  case k: __builtin_amdgcn_s_waitcnt(0x0F70 | k); break;
+    IJ_VM(0) IJ_VM(1) IJ_VM(2) IJ_VM(3) IJ_VM(4) IJ_VM(5) IJ_VM(6) IJ_VM(7)
+    IJ_VM(8) IJ_VM(9) IJ_VM(10) IJ_VM(11) IJ_VM(12) IJ_VM(13) IJ_VM(14) IJ_VM(15)
+#undef IJ_VM
+  }
+}
+__device__ __forceinline__ void dma16(const void *src, void *lds_dst) {
+  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)lds_dst, 16, 0, 0);
+}
+
+// the expert block and layout of expert e (e == ne: the shared expert)
+__device__ __forceinline__ const uint8_t *expert_block(const MoeArgs &a, int e) {
+  return e >= a.ne ? a.shared : a.experts + (uint64_t)e * a.lay.bytes;
+}
+__device__ __forceinline__ uint64_t tr_of(const MoeArgs &a, int e, int proj) {
+  const ExpertLayout &L = e >= a.ne ? a.slay : a.lay;
+  return proj == 0 ? L.tr[0] : proj == 1 ? L.tr[1] : L.tr[2];
+}
+__device__ __forceinline__ uint64_t su_of(const MoeArgs &a, int e, int proj) {
+  const ExpertLayout &L = e >= a.ne ? a.slay : a.lay;
+  return proj == 0 ? L.su[0] : proj == 1 ? L.su[1] : L.su[2];
+}
+__device__ __forceinline__ uint64_t sv_of(const MoeArgs &a, int e, int proj) {
+  const ExpertLayout &L = e >= a.ne ? a.slay : a.lay;
+  return proj == 0 ? L.sv[0] : proj == 1 ? L.sv[1] : L.sv[2];
+}
+
+}  // namespace
+
+__global__ __launch_bounds__(1024) void bat_zero(uint32_t *p, int n) {
+  for (int i = threadIdx.x; i < n; i += 1024) p[i] = 0u;
+}
+
+// ---------------------------------------------------------------------------------------------------- router
+// logits[r][c] for c < ne + has_sgate, 64 x 64 output tiles, 256 threads (4 x 4 outputs each), k chunks of 32
+__global__ __launch_bounds__(256) void bat_router(MoeArgs a) {
+  __shared__ float xs[64][33], ws[64][33];
+  const int tid = threadIdx.x, r0 = blockIdx.x * 64, c0 = blockIdx.y * 64, ncol = a.ne + a.has_sgate;
+  const int tr = tid / 16, tc = tid % 16;  // rows tr + 16 i, columns tc + 16 j
+  float acc[4][4] = {};
+  for (int k0 = 0; k0 < a.hid; k0 += 32) {
+    for (int i = tid; i < 64 * 32; i += 256) {
+      const int rr = i / 32, kk = i % 32, row = r0 + rr, col = c0 + rr;
+      xs[rr][kk] = row < a.R ? a.x[(uint64_t)row * a.hid + k0 + kk] : 0.f;
+      ws[rr][kk] = col < ncol ? bf16_f32(a.router[(uint64_t)col * a.hid + k0 + kk]) : 0.f;
+    }
+    __syncthreads();
+#pragma unroll 8
+    for (int kk = 0; kk < 32; kk++)
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = fmaf(xs[tr + 16 * i][kk], ws[tc + 16 * j][kk], acc[i][j]);
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int row = r0 + tr + 16 * i, col = c0 + tc + 16 * j;
+      if (row < a.R && col < ncol) a.logits[(uint64_t)row * (a.ne + 1) + col] = bf16_round(acc[i][j]);
+    }
+}
+
+// ---------------------------------------------------------------------------------------------------- route
+// one wave per row; also counts each routed slot in counts[expert]
+template <int J>
+__device__ void route_one(const MoeArgs &a, int r, uint32_t *counts) {
+  const int lane = threadIdx.x & 63;
+  const float *lg = a.logits + (uint64_t)r * (a.ne + 1);
+  uint32_t key[J];
+#pragma unroll
+  for (int j = 0; j < J; j++) {
+    const int i = j * 64 + lane;
+    key[j] = i < a.ne ? topk_key(lg[i], i) : 0u;
+  }
+#pragma unroll
+  for (int s = 2; s <= J; s <<= 1)
+#pragma unroll
+    for (int d = s >> 1; d > 0; d >>= 1)
+#pragma unroll
+      for (int i = 0; i < J; i++) {
+        const int l = i ^ d;
+        if (l > i) {
+          const uint32_t hi = max(key[i], key[l]), lo = min(key[i], key[l]);
+          key[i] = (i & s) == 0 ? hi : lo;
+          key[l] = (i & s) == 0 ? lo : hi;
+        }
+      }
+  uint32_t mykey = 0u;
+  for (int t = 0; t < a.topk; t++) {
+    const uint32_t m = wave_max_u32(key[0]);
+    mykey = lane == t ? m : mykey;
+    const bool win = key[0] == m;
+#pragma unroll
+    for (int j = 0; j < J - 1; j++) key[j] = win ? key[j + 1] : key[j];
+    key[J - 1] = win ? 0u : key[J - 1];
+  }
+  const uint32_t id = lane < a.topk ? 0xFFFFu - (mykey & 0xFFFFu) : 0u;  // lanes past topk read logit 0
+  const float top = lg[__builtin_amdgcn_readlane((int)id, 0)];
+  const float pk = lane < a.topk ? expf(lg[id] - top) : 0.f;
+  float sum = 0.f;
+  for (int k = 0; k < a.topk; k++) sum += __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(pk), k));
+  if (lane < a.topk) {
+    a.route[(uint64_t)r * 2 * a.topk + lane] = id;
+    a.route[(uint64_t)r * 2 * a.topk + a.topk + lane] = __float_as_uint(pk / sum);
+    atomicAdd(counts + id, 1u);
+  }
+  if (lane == 0) a.sgv[r] = a.has_sgate ? 1.f / (1.f + expf(-lg[a.ne])) : 1.f;
+}
+__global__ __launch_bounds__(256) void bat_route(MoeArgs a, uint32_t *counts) {
+  const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= a.R) return;
+  if (a.ne <= 512)
+    route_one<8>(a, r, counts);
+  else
+    route_one<16>(a, r, counts);
+}
+
+// ---------------------------------------------------------------------------------------------------- sort
+// One workgroup: offsets (exclusive scan over experts; the shared expert's R rows last), the chunk list and the
+// placement cursors. bk: [ne + 1] counts (in), [ne + 1] offsets, [ne + 1] cursors, then 1 chunk count; chunks: u32x3.
+__global__ __launch_bounds__(1024) void bat_scan(MoeArgs a, uint32_t *bk, uint32_t *chunks, int max_chunks) {
+  __shared__ uint32_t sc[1024 + 1], cc[1024 + 1];
+  const int tid = threadIdx.x, n = a.ne + (a.nslot > a.topk ? 1 : 0);
+  uint32_t *counts = bk, *offs = bk + (a.ne + 1), *cursor = offs + (a.ne + 1), *nchunks = cursor + (a.ne + 1);
+  if (a.nslot > a.topk && tid == 0) counts[a.ne] = (uint32_t)a.R;
+  __syncthreads();
+  const uint32_t c = tid < n ? counts[tid] : 0u;
+  sc[tid] = c;
+  cc[tid] = (c + kChunkRows - 1) / kChunkRows;
+  __syncthreads();
+  for (int d = 1; d < 1024; d <<= 1) {  // inclusive Hillis-Steele scans of rows and chunks
+    const uint32_t v = tid >= d ? sc[tid - d] : 0u, w = tid >= d ? cc[tid - d] : 0u;
+    __syncthreads();
+    sc[tid] += v;
+    cc[tid] += w;
+    __syncthreads();
+  }
+  if (tid < n) {
+    const uint32_t off = sc[tid] - c, ch0 = cc[tid] - (c + kChunkRows - 1) / kChunkRows;
+    offs[tid] = off;
+    cursor[tid] = 0u;
+    for (uint32_t r = 0, q = ch0; r < c; r += kChunkRows, q++)
+      if ((int)q < max_chunks) {
+        chunks[3 * q] = (uint32_t)tid;
+        chunks[3 * q + 1] = off + r;
+        chunks[3 * q + 2] = min(c - r, (uint32_t)kChunkRows);
+      }
+  }
+  if (tid == 0) *nchunks = min(cc[n > 0 ? n - 1 : 0], (uint32_t)max_chunks);
+}
+// slot (r, k) -> its row in its expert's list; rows[row] = r * nslot + k (k == topk: the shared expert)
+__global__ __launch_bounds__(256) void bat_place(MoeArgs a, uint32_t *bk, uint32_t *rows) {
+  const int s = blockIdx.x * 256 + threadIdx.x;
+  if (s >= a.R * a.nslot) return;
+  const int r = s / a.nslot, k = s % a.nslot;
+  const uint32_t *offs = bk + (a.ne + 1);
+  uint32_t *cursor = bk + 2 * (a.ne + 1);
+  uint32_t row;
+  if (k >= a.topk) {
+    row = offs[a.ne] + (uint32_t)r;
+  } else {
+    uint32_t e = a.route[(uint64_t)r * 2 * a.topk + k];
+    e = e < (uint32_t)a.ne ? e : 0u;
+    row = offs[e] + atomicAdd(cursor + e, 1u);
+  }
+  rows[row] = (uint32_t)s;
+}
+
+// ---------------------------------------------------------------------------------------------------- prep
+// xh[row] = fp16(H(x[token] * suh_e)) in kp order (one wave per 128-chunk, 4 waves per row)
+__global__ __launch_bounds__(256) void bat_prep(MoeArgs a, const uint32_t *rows, const uint32_t *bk, uint16_t *xh) {
+  const int row = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint32_t s = rows[row];
+  const int r = s / a.nslot, k = s % a.nslot;
+  int e = a.ne;
+  if (k < a.topk) {
+    e = (int)a.route[(uint64_t)r * 2 * a.topk + k];
+    e = e < a.ne ? e : 0;
+  }
+  const uint16_t *sug = (const uint16_t *)(expert_block(a, e) + su_of(a, e, 0));
+  const uint16_t *suu = (const uint16_t *)(expert_block(a, e) + su_of(a, e, 1));
+  const float *x = a.x + (uint64_t)r * a.hid;
+  uint16_t *out = xh + (uint64_t)row * 2 * a.hid;
+  for (int c = wave; c < a.hid / 128; c += 4) {
+    const int e0 = c * 128 + lane, e1 = e0 + 64;
+    const float x0 = x[e0], x1 = x[e1];
+    float g0 = x0 * h2f(sug[e0]), g1 = x1 * h2f(sug[e1]), u0 = x0 * h2f(suu[e0]), u1 = x1 * h2f(suu[e1]);
+    fwht2(g0, g1, lane, a.had_hid, a.sc_hid);
+    fwht2(u0, u1, lane, a.had_hid, a.sc_hid);
+    out[c * 128 + kp(lane)] = f2h(g0);
+    out[c * 128 + kp(lane + 64)] = f2h(g1);
+    out[a.hid + c * 128 + kp(lane)] = f2h(u0);
+    out[a.hid + c * 128 + kp(lane + 64)] = f2h(u1);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------- grouped GEMM
+// One workgroup (4 waves) multiplies a chunk of up to 128 expert-sorted rows of A by NP tile pairs per wave of the
+// expert's re-laid matrix (IT k tiles), streaming both through LDS rings kAhead k tiles ahead. There are NA A
+// operands (fp16, kp order, row stride lda halves, the second at A + ahalf): wave w multiplies operand aidx.
+// acc[rb][p] = rows 32 rb.., columns of pair p of this wave, in the matrix-core layout.
+template <int K, int NP, int NA>
+struct GemmIo {
+  static constexpr uint32_t TB = 32u * K;                  // bytes of one 16x16 tile
+  static constexpr uint32_t PB = 2 * TB * NP;              // a wave's B bytes per k tile
+  static constexpr uint32_t AB = NA * kChunkRows * 32;     // A bytes per k tile (NA x 128 rows x 16 halves)
+  static constexpr uint32_t WAVE_B = kRing * PB + NP * 1024;  // B ring + decoded fragments
+  static constexpr uint32_t LDS = kRing * AB + 4 * WAVE_B;
+};
+
+template <int K, int NP, int NA>
+__device__ void chunk_gemm(const uint16_t *A, int lda, int ahalf, int aidx, int nrows, const uint8_t *tr, int IT,
+                           int p0, uint8_t *lds, f32x16 (&acc)[kRowBlocks][NP]) {
+  using Io = GemmIo<K, NP, NA>;
+  constexpr int TW = 8 * K;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  uint8_t *ring_a = lds;
+  uint8_t *ring_b = lds + kRing * Io::AB + wave * Io::WAVE_B;
+  uint8_t *frag = ring_b + kRing * Io::PB;
+  const TileLane<K> L = tile_lane<K>((uint32_t)lane);
+  const int c = (lane >> 3) + 8 * (lane & 1), q = (lane >> 1) & 3;
+  const int nrb = (nrows + 31) / 32;
+#pragma unroll
+  for (int rb = 0; rb < kRowBlocks; rb++)
+#pragma unroll
+    for (int p = 0; p < NP; p++)
+#pragma unroll
+      for (int i = 0; i < 16; i++) acc[rb][p][i] = 0.f;
+  // k tile kt: this wave's quarter of each A operand (32 rows x 32 B = 1 KB, lane -> row w * 32 + lane / 2, half
+  // lane % 2), then this wave's NP pairs (contiguous tile pair bytes per pair)
+  auto issue = [&](int kt) {
+    const int slot = kt % kRing;
+    const int rr = min(wave * 32 + (lane >> 1), nrows - 1);
+#pragma unroll
+    for (int o = 0; o < NA; o++)
+      dma16(A + o * ahalf + (uint64_t)rr * lda + kt * 16 + (lane & 1) * 8,
+            ring_a + slot * Io::AB + o * kChunkRows * 32 + wave * 1024);
+#pragma unroll
+    for (int p = 0; p < NP; p++) {
+      const uint8_t *src = tr + ((uint64_t)(p0 + p) * IT + kt) * 2 * Io::TB;
+      uint8_t *dst = ring_b + slot * Io::PB + p * 2 * Io::TB;
+      for (uint32_t o = 0; o < 2 * Io::TB; o += 1024)
+        if (o + (uint32_t)lane * 16 < 2 * Io::TB) dma16(src + o + lane * 16, dst + o);
+    }
+  };
+  constexpr int OPS = NA + NP * ((2 * Io::TB + 1023) / 1024);  // requests per k tile
+  for (int kt = 0; kt < kAhead && kt < IT; kt++) issue(kt);
+  for (int kt = 0; kt < IT; kt++) {
+    const int ahead = min(kAhead, IT - kt) - 1;  // k tiles requested after kt
+    wait_vm(ahead * OPS);
+    lds_barrier();  // every wave's quarter of A tile kt is in; every wave is done with ring slot (kt - 2) % kRing
+    if (kt + kAhead < IT) issue(kt + kAhead);
+    const int slot = kt % kRing;
+    // decode this wave's pairs into the matrix-core B layout
+#pragma unroll
+    for (int p = 0; p < NP; p++) {
+      const uint32_t *T0 = (const uint32_t *)(ring_b + slot * Io::PB + p * 2 * Io::TB);
+      TileWords wa, wb;
+      wa.w0 = T0[L.i0];
+      wa.w1 = T0[L.i1];
+      wa.w2 = kThreeWords<K> ? T0[L.i2] : 0u;
+      wb.w0 = T0[TW + L.i0];
+      wb.w1 = T0[TW + L.i1];
+      wb.w2 = kThreeWords<K> ? T0[TW + L.i2] : 0u;
+      f16x2 a0, b0, a1, b1;
+      decode4<K>(wa, L.sh, a0, b0);
+      decode4<K>(wb, L.sh, a1, b1);
+      uint8_t *fp = frag + p * 1024;
+      *(f16x4 *)(fp + ((0 * 16 + c) * 4 + q) * 8) = f16x4{a0.x, a0.y, b0.x, b0.y};
+      *(f16x4 *)(fp + ((1 * 16 + c) * 4 + q) * 8) = f16x4{a1.x, a1.y, b1.x, b1.y};
+    }
+    f16x8 bf[NP];
+#pragma unroll
+    for (int p = 0; p < NP; p++) bf[p] = *(const f16x8 *)(frag + p * 1024 + ((lane & 31) * 4 + 2 * (lane >> 5)) * 8);
+    const uint8_t *at = ring_a + slot * Io::AB + aidx * kChunkRows * 32;
+#pragma unroll
+    for (int rb = 0; rb < kRowBlocks; rb++) {
+      if (rb < nrb) {
+        const f16x8 af = *(const f16x8 *)(at + (rb * 32 + (lane & 31)) * 32 + (lane >> 5) * 16);
+#pragma unroll
+        for (int p = 0; p < NP; p++) acc[rb][p] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf[p], acc[rb][p], 0, 0, 0);
+      }
+    }
+  }
+}
+
+// gate/up: chunk ch, 128-column block ib of inter; waves 0-1 gate pairs 4 ib + 2 w + {0, 1}, waves 2-3 up
+template <int K, int KS>
+__global__ __launch_bounds__(256, 1) void bat_gateup(MoeArgs a, const uint32_t *bk, const uint32_t *chunks,
+                                                     const uint32_t *rows, const uint16_t *xh, uint16_t *hh) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const uint32_t nch = bk[3 * (a.ne + 1)];
+  const int ch = blockIdx.x, ib = blockIdx.y;
+  if ((uint32_t)ch >= nch) return;
+  const int e = (int)chunks[3 * ch], row0 = (int)chunks[3 * ch + 1], nrows = (int)chunks[3 * ch + 2];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, proj = wave >> 1;
+  const uint8_t *blk = expert_block(a, e);
+  f32x16 acc[kRowBlocks][2];
+  const uint16_t *A = xh + (uint64_t)row0 * 2 * a.hid;  // [row][gate | up][hid]
+  const int p0 = ib * 4 + 2 * (wave & 1);
+  if (e >= a.ne)
+    chunk_gemm<KS, 2, 2>(A, 2 * a.hid, a.hid, proj, nrows, blk + tr_of(a, e, proj), a.hid / 16, p0, lds, acc);
+  else
+    chunk_gemm<K, 2, 2>(A, 2 * a.hid, a.hid, proj, nrows, blk + tr_of(a, e, proj), a.hid / 16, p0, lds, acc);
+  // epilogue per 32-row block: columns to LDS as [32][256] f32 (gate 0..127, up 128..255), then one wave per row
+  float *ot = (float *)lds;
+  const uint16_t *svg = (const uint16_t *)(blk + sv_of(a, e, 0)) + ib * 128;
+  const uint16_t *svu = (const uint16_t *)(blk + sv_of(a, e, 1)) + ib * 128;
+  const uint16_t *sud = (const uint16_t *)(blk + su_of(a, e, 2)) + ib * 128;
+  const float sg0 = h2f(svg[lane]), sg1 = h2f(svg[lane + 64]), su0 = h2f(svu[lane]), su1 = h2f(svu[lane + 64]);
+  const float sd0 = h2f(sud[lane]), sd1 = h2f(sud[lane + 64]);
+  const int nrb = (nrows + 31) / 32;
+#pragma unroll
+  for (int rb = 0; rb < kRowBlocks; rb++) {  // compile-time rb: acc stays in registers
+    if (rb >= nrb) break;
+    __syncthreads();
+#pragma unroll
+    for (int p = 0; p < 2; p++)
+#pragma unroll
+      for (int i = 0; i < 16; i++) {
+        const int rr = 4 * (lane >> 5) + (i & 3) + 8 * (i >> 2), col = proj * 128 + (2 * (wave & 1) + p) * 32 + (lane & 31);
+        ot[rr * 256 + col] = acc[rb][p][i];
+      }
+    __syncthreads();
+    for (int rr = wave; rr < 32 && rb * 32 + rr < nrows; rr += 4) {
+      float g0 = ot[rr * 256 + lane], g1 = ot[rr * 256 + 64 + lane];
+      float u0 = ot[rr * 256 + 128 + lane], u1 = ot[rr * 256 + 192 + lane];
+      fwht2(g0, g1, lane, a.had_inter, a.sc_inter);
+      fwht2(u0, u1, lane, a.had_inter, a.sc_inter);
+      g0 = g0 * sg0;
+      u0 = u0 * su0;
+      g1 = g1 * sg1;
+      u1 = u1 * su1;
+      float h0 = g0 / (1.f + expf(-g0)) * u0 * sd0;
+      float h1 = g1 / (1.f + expf(-g1)) * u1 * sd1;
+      fwht2(h0, h1, lane, a.had_inter, a.sc_inter);
+      uint16_t *out = hh + (uint64_t)(row0 + rb * 32 + rr) * a.inter + ib * 128;
+      out[kp(lane)] = f2h(h0);
+      out[kp(lane + 64)] = f2h(h1);
+    }
+  }
+}
+
+// down: chunk ch, 128-column block ob of hid; wave w: pair 4 ob + w. Output per (token, slot): H, svh_d, weight.
+template <int K, int KS>
+__global__ __launch_bounds__(256, 1) void bat_down(MoeArgs a, const uint32_t *bk, const uint32_t *chunks,
+                                                   const uint32_t *rows, const uint16_t *hh, float *dnw) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const uint32_t nch = bk[3 * (a.ne + 1)];
+  const int ch = blockIdx.x, ob = blockIdx.y;
+  if ((uint32_t)ch >= nch) return;
+  const int e = (int)chunks[3 * ch], row0 = (int)chunks[3 * ch + 1], nrows = (int)chunks[3 * ch + 2];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint8_t *blk = expert_block(a, e);
+  f32x16 acc[kRowBlocks][1];
+  const uint16_t *A = hh + (uint64_t)row0 * a.inter;
+  if (e >= a.ne)
+    chunk_gemm<KS, 1, 1>(A, a.inter, 0, 0, nrows, blk + tr_of(a, e, 2), a.inter / 16, ob * 4 + wave, lds, acc);
+  else
+    chunk_gemm<K, 1, 1>(A, a.inter, 0, 0, nrows, blk + tr_of(a, e, 2), a.inter / 16, ob * 4 + wave, lds, acc);
+  float *ot = (float *)lds;
+  const uint16_t *sv = (const uint16_t *)(blk + sv_of(a, e, 2)) + ob * 128;
+  const float s0 = h2f(sv[lane]), s1 = h2f(sv[lane + 64]);
+  const int nrb = (nrows + 31) / 32;
+#pragma unroll
+  for (int rb = 0; rb < kRowBlocks; rb++) {
+    if (rb >= nrb) break;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      const int rr = 4 * (lane >> 5) + (i & 3) + 8 * (i >> 2), col = wave * 32 + (lane & 31);
+      ot[rr * 128 + col] = acc[rb][0][i];
+    }
+    __syncthreads();
+    for (int rr = wave; rr < 32 && rb * 32 + rr < nrows; rr += 4) {
+      float v0 = ot[rr * 128 + lane], v1 = ot[rr * 128 + 64 + lane];
+      fwht2(v0, v1, lane, a.had_hid, a.sc_hid);
+      const uint32_t s = rows[row0 + rb * 32 + rr];
+      const int r = s / a.nslot, k = s % a.nslot;
+      const float w = k >= a.topk ? a.sgv[r] : __uint_as_float(a.route[(uint64_t)r * 2 * a.topk + a.topk + k]);
+      float *out = dnw + ((uint64_t)r * a.nslot + k) * a.hid + ob * 128;
+      out[lane] = v0 * s0 * w;
+      out[lane + 64] = v1 * s1 * w;
+    }
+  }
+}
+
+// y[r] = sum over the row's slots in slot order (routed k = 0..topk-1, then the shared expert)
+__global__ __launch_bounds__(256) void bat_combine(MoeArgs a, const float *dnw) {
+  const int r = blockIdx.x, i = blockIdx.y * 256 + threadIdx.x;
+  if (i >= a.hid) return;
+  float y = 0.f;
+  for (int k = 0; k < a.nslot; k++) y += dnw[((uint64_t)r * a.nslot + k) * a.hid + i];
+  a.y[(uint64_t)r * a.hid + i] = y;
+}
+
+// ---------------------------------------------------------------------------------------------------- host side
+namespace {
+template <int K, int KS>
+void launch_gemms(const MoeArgs &a, const MoeBatchBufs &b, hipStream_t s) {
+  const size_t lg = GemmIo<(K > KS ? K : KS), 2, 2>::LDS, ld = GemmIo<(K > KS ? K : KS), 1, 1>::LDS;
+  static bool attr = false;
+  if (!attr) {
+    IJ_HIP(hipFuncSetAttribute((const void *)&bat_gateup<K, KS>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lg));
+    IJ_HIP(hipFuncSetAttribute((const void *)&bat_down<K, KS>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)ld));
+    attr = true;
+  }
+  // epilogue staging reuses the rings: [32][256] f32 = 32 KB must fit
+  static_assert(GemmIo<4, 1, 1>::LDS >= 32 * 128 * 4 && GemmIo<4, 2, 2>::LDS >= 32 * 256 * 4,
+                "LDS too small for the epilogue staging");
+  hipLaunchKernelGGL((bat_gateup<K, KS>), dim3(b.max_chunks, a.inter / 128), dim3(256), lg, s, a, b.bk, b.chunks,
+                     b.rows, b.xh, b.hh);
+  hipLaunchKernelGGL((bat_down<K, KS>), dim3(b.max_chunks, a.hid / 128), dim3(256), ld, s, a, b.bk, b.chunks,
+                     b.rows, b.hh, b.dnw);
+}
+}  // namespace
+
+bool moe_batch_supported(int K, int KS, int hid, int inter, int ne, int topk) {
+  const bool ks = (K >= 4 && K <= 6) && (KS >= 4 && KS <= 6);
+  return ks && hid % 128 == 0 && inter % 128 == 0 && hid <= 8192 && inter <= 4096 && ne < 1024 && topk <= 32;
+}
+int moe_batch_max_chunks(int R, int ne, int topk, bool shared) {
+  return (R * topk + kChunkRows - 1) / kChunkRows + ne + (shared ? (R + kChunkRows - 1) / kChunkRows : 0) + 1;
+}
+
+void launch_moe_batch(const MoeArgs &a, const MoeBatchBufs &b, hipStream_t s) {
+  const int ncol = a.ne + a.has_sgate, S = a.R * a.nslot;
+  hipLaunchKernelGGL(bat_zero, dim3(1), dim3(1024), 0, s, b.bk, a.ne + 1);  // a kernel, not a memset node
+  hipLaunchKernelGGL(bat_router, dim3((a.R + 63) / 64, (ncol + 63) / 64), dim3(256), 0, s, a);
+  hipLaunchKernelGGL(bat_route, dim3((a.R + 3) / 4), dim3(256), 0, s, a, b.bk);
+  hipLaunchKernelGGL(bat_scan, dim3(1), dim3(1024), 0, s, a, b.bk, b.chunks, b.max_chunks);
+  hipLaunchKernelGGL(bat_place, dim3((S + 255) / 256), dim3(256), 0, s, a, b.bk, b.rows);
+  hipLaunchKernelGGL(bat_prep, dim3(S), dim3(256), 0, s, a, b.rows, b.bk, b.xh);
+  const int KS = a.nslot > a.topk ? a.slay.K : a.lay.K;
+  bool done = false;
+#define IJ_BAT(k, ks)                        \
+  if (!done && a.lay.K == k && KS == ks) {   \
+    launch_gemms<k, ks>(a, b, s);            \
+    done = true;                             \
+  }
+  IJ_BAT(4, 4) IJ_BAT(5, 5) IJ_BAT(6, 6) IJ_BAT(4, 5) IJ_BAT(4, 6) IJ_BAT(5, 6) IJ_BAT(5, 4) IJ_BAT(6, 4) IJ_BAT(6, 5)
+#undef IJ_BAT
+  IJ_CHECK(done, "batched MoE: K%d / shared K%d not instantiated", a.lay.K, KS);
+  hipLaunchKernelGGL(bat_combine, dim3(a.R, (a.hid + 255) / 256), dim3(256), 0, s, a, b.dnw);
+}
+
+}  // namespace ijah
