@@ -81,34 +81,56 @@ __global__ __launch_bounds__(1024) void bat_zero(uint32_t *p, int n) {
 }
 
 // ---------------------------------------------------------------------------------------------------- router
-// logits[r][c] for c < ne + has_sgate, 64 x 64 output tiles, 256 threads (4 x 4 outputs each), k chunks of 32
+// logits[r][c] = bf16(x[r] . router[c]) for c < ne + has_sgate on the matrix cores: one wave per 32 x 32 tile
+// (rows x router rows), k steps of 16. x is split into bf16 hi + lo (x - hi rounded again), two MFMAs per step, so the
+// product carries about 16 mantissa bits of x: within f32 rounding of the reference's f32 dot for these logits.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 __global__ __launch_bounds__(256) void bat_router(MoeArgs a) {
-  __shared__ float xs[64][33], ws[64][33];
-  const int tid = threadIdx.x, r0 = blockIdx.x * 64, c0 = blockIdx.y * 64, ncol = a.ne + a.has_sgate;
-  const int tr = tid / 16, tc = tid % 16;  // rows tr + 16 i, columns tc + 16 j
-  float acc[4][4] = {};
-  for (int k0 = 0; k0 < a.hid; k0 += 32) {
-    for (int i = tid; i < 64 * 32; i += 256) {
-      const int rr = i / 32, kk = i % 32, row = r0 + rr, col = c0 + rr;
-      xs[rr][kk] = row < a.R ? a.x[(uint64_t)row * a.hid + k0 + kk] : 0.f;
-      ws[rr][kk] = col < ncol ? bf16_f32(a.router[(uint64_t)col * a.hid + k0 + kk]) : 0.f;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, ncol = a.ne + a.has_sgate;
+  const int rt = blockIdx.x, ct = blockIdx.y * 4 + wave;  // 32-row tile, 32-column tile
+  if (ct * 32 >= ncol) return;
+  const int m = lane & 31, h = lane >> 5;
+  const int row = min(rt * 32 + m, a.R - 1), col = min(ct * 32 + m, ncol - 1);
+  const float *xp = a.x + (uint64_t)row * a.hid + 8 * h;
+  const uint16_t *wp = a.router + (uint64_t)col * a.hid + 8 * h;
+  f32x16 acc;
+#pragma unroll
+  for (int i = 0; i < 16; i++) acc[i] = 0.f;
+  constexpr int U = 8;  // k steps per batch of loads
+  for (int k0 = 0; k0 < a.hid; k0 += 16 * U) {
+    float4 xv[U][2];
+    uint4 wv[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int k = k0 + 16 * u;
+      if (k < a.hid) {
+        xv[u][0] = *(const float4 *)(xp + k);
+        xv[u][1] = *(const float4 *)(xp + k + 4);
+        wv[u] = *(const uint4 *)(wp + k);
+      }
     }
-    __syncthreads();
-#pragma unroll 8
-    for (int kk = 0; kk < 32; kk++)
 #pragma unroll
-      for (int i = 0; i < 4; i++)
+    for (int u = 0; u < U; u++) {
+      if (k0 + 16 * u < a.hid) {
+        const float xs[8] = {xv[u][0].x, xv[u][0].y, xv[u][0].z, xv[u][0].w,
+                             xv[u][1].x, xv[u][1].y, xv[u][1].z, xv[u][1].w};
+        bf16x8 hi, lo;
 #pragma unroll
-        for (int j = 0; j < 4; j++) acc[i][j] = fmaf(xs[tr + 16 * i][kk], ws[tc + 16 * j][kk], acc[i][j]);
-    __syncthreads();
+        for (int e = 0; e < 8; e++) {
+          hi[e] = (__bf16)xs[e];
+          lo[e] = (__bf16)(xs[e] - (float)hi[e]);
+        }
+        const bf16x8 wb = __builtin_bit_cast(bf16x8, wv[u]);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(hi, wb, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(lo, wb, acc, 0, 0, 0);
+      }
+    }
   }
 #pragma unroll
-  for (int i = 0; i < 4; i++)
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const int row = r0 + tr + 16 * i, col = c0 + tc + 16 * j;
-      if (row < a.R && col < ncol) a.logits[(uint64_t)row * (a.ne + 1) + col] = bf16_round(acc[i][j]);
-    }
+  for (int i = 0; i < 16; i++) {
+    const int r = rt * 32 + 4 * h + (i & 3) + 8 * (i >> 2), c = ct * 32 + m;
+    if (r < a.R && c < ncol) a.logits[(uint64_t)r * (a.ne + 1) + c] = bf16_round(acc[i]);
+  }
 }
 
 // ---------------------------------------------------------------------------------------------------- route
@@ -246,66 +268,90 @@ __global__ __launch_bounds__(256) void bat_prep(MoeArgs a, const uint32_t *rows,
 }
 
 // ---------------------------------------------------------------------------------------------------- grouped GEMM
-// One workgroup (4 waves) multiplies a chunk of up to 128 expert-sorted rows of A by NP tile pairs per wave of the
-// expert's re-laid matrix (IT k tiles), streaming both through LDS rings kAhead k tiles ahead. There are NA A
-// operands (fp16, kp order, row stride lda halves, the second at A + ahalf): wave w multiplies operand aidx.
-// acc[rb][p] = rows 32 rb.., columns of pair p of this wave, in the matrix-core layout.
-template <int K, int NP, int NA>
+// One workgroup (8 waves, two per SIMD) multiplies a chunk of up to 128 expert-sorted rows of A by one tile pair (32
+// columns) per wave of the expert's re-laid matrix (IT k tiles, IT even), two k tiles per step. There are NA A
+// operands (fp16, kp order, row stride lda halves, the second at A + ahalf): wave w multiplies operand aidx. Both
+// stream through LDS rings: A (shared; each wave requests 16 of its rows) kDA steps ahead, and each wave's own B
+// tiles kDB steps ahead, so that enough weight bytes are in flight per CU to cover the memory latency.
+// acc[rb] = rows 32 rb.., the wave's 32 columns, in the matrix-core layout.
+constexpr int kWavesG = 8;
+constexpr int kDA = 3, kDB = 8;  // steps (of 2 k tiles) requested ahead: A, B
+template <int K, int NA>
 struct GemmIo {
   static constexpr uint32_t TB = 32u * K;                  // bytes of one 16x16 tile
-  static constexpr uint32_t PB = 2 * TB * NP;              // a wave's B bytes per k tile
-  static constexpr uint32_t AB = NA * kChunkRows * 32;     // A bytes per k tile (NA x 128 rows x 16 halves)
-  static constexpr uint32_t WAVE_B = kRing * PB + NP * 1024;  // B ring + decoded fragments
-  static constexpr uint32_t LDS = kRing * AB + 4 * WAVE_B;
+  static constexpr uint32_t PB = 2 * 2 * TB;               // a wave's B bytes per step (a pair x 2 k tiles)
+  static constexpr uint32_t AB = NA * kChunkRows * 64;     // A bytes per step (NA x 128 rows x 32 halves)
+  static constexpr int RA = kDA + 1, RB = kDB + 1;         // ring slots
+  static constexpr uint32_t WAVE_B = RB * PB + 2 * 1024;   // B ring + decoded fragments of the step
+  static constexpr uint32_t LDS = RA * AB + kWavesG * WAVE_B;
+  static constexpr int OA = NA, OB = (PB + 1023) / 1024;   // requests per A / B step
 };
+// Issue order: prologue A(0) B(0) A(1) B(1) .. A(kDA-1) B(kDA-1) B(kDA) .. B(kDB-1); step j then issues
+// A(j + kDA) and B(j + kDB) (while < NS). Returns how many requests were issued after A(t) and B(t), counted at
+// step t before it issues: the s_waitcnt vmcnt that makes both complete (completion is in issue order).
+template <int OA, int OB>
+__device__ __forceinline__ int after_step(int t, int NS) {
+  auto sum_ops = [&](int n) { return OA * min(n, max(NS - kDA, 0)) + OB * min(n, max(NS - kDB, 0)); };
+  const int pa = min(kDA, NS), pb = min(kDB, NS);
+  const int prologue = OA * pa + OB * pb;
+  const int total = prologue + sum_ops(t);
+  int last;  // one past the position of the later of A(t), B(t)
+  if (t < kDA) {
+    last = (OA + OB) * (t + 1);
+  } else if (t < kDB) {
+    last = max(prologue + sum_ops(t - kDA) + OA, (OA + OB) * pa + OB * (t - pa) + OB);
+  } else {
+    last = max(prologue + sum_ops(t - kDA) + OA, prologue + sum_ops(t - kDB) + ((t - kDB) + kDA < NS ? OA : 0) + OB);
+  }
+  return total - last;
+}
 
-template <int K, int NP, int NA>
+template <int K, int NA>
 __device__ void chunk_gemm(const uint16_t *A, int lda, int ahalf, int aidx, int nrows, const uint8_t *tr, int IT,
-                           int p0, uint8_t *lds, f32x16 (&acc)[kRowBlocks][NP]) {
-  using Io = GemmIo<K, NP, NA>;
+                           int pair, uint8_t *lds, f32x16 (&acc)[kRowBlocks]) {
+  using Io = GemmIo<K, NA>;
   constexpr int TW = 8 * K;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, NS = IT / 2;
   uint8_t *ring_a = lds;
-  uint8_t *ring_b = lds + kRing * Io::AB + wave * Io::WAVE_B;
-  uint8_t *frag = ring_b + kRing * Io::PB;
+  uint8_t *ring_b = lds + Io::RA * Io::AB + wave * Io::WAVE_B;
+  uint8_t *frag = ring_b + Io::RB * Io::PB;
   const TileLane<K> L = tile_lane<K>((uint32_t)lane);
   const int c = (lane >> 3) + 8 * (lane & 1), q = (lane >> 1) & 3;
   const int nrb = (nrows + 31) / 32;
 #pragma unroll
   for (int rb = 0; rb < kRowBlocks; rb++)
 #pragma unroll
-    for (int p = 0; p < NP; p++)
-#pragma unroll
-      for (int i = 0; i < 16; i++) acc[rb][p][i] = 0.f;
-  // k tile kt: this wave's quarter of each A operand (32 rows x 32 B = 1 KB, lane -> row w * 32 + lane / 2, half
-  // lane % 2), then this wave's NP pairs (contiguous tile pair bytes per pair)
-  auto issue = [&](int kt) {
-    const int slot = kt % kRing;
-    const int rr = min(wave * 32 + (lane >> 1), nrows - 1);
+    for (int i = 0; i < 16; i++) acc[rb][i] = 0.f;
+  // A(t): 16 rows of this wave per operand (row 16 w + lane / 4, 16-byte quarter lane % 4 of its 64 bytes)
+  const int rr = min(wave * 16 + (lane >> 2), nrows - 1);
+  auto issue_a = [&](int t) {
+    const int slot = t % Io::RA;
 #pragma unroll
     for (int o = 0; o < NA; o++)
-      dma16(A + o * ahalf + (uint64_t)rr * lda + kt * 16 + (lane & 1) * 8,
-            ring_a + slot * Io::AB + o * kChunkRows * 32 + wave * 1024);
-#pragma unroll
-    for (int p = 0; p < NP; p++) {
-      const uint8_t *src = tr + ((uint64_t)(p0 + p) * IT + kt) * 2 * Io::TB;
-      uint8_t *dst = ring_b + slot * Io::PB + p * 2 * Io::TB;
-      for (uint32_t o = 0; o < 2 * Io::TB; o += 1024)
-        if (o + (uint32_t)lane * 16 < 2 * Io::TB) dma16(src + o + lane * 16, dst + o);
-    }
+      dma16(A + o * ahalf + (uint64_t)rr * lda + t * 32 + (lane & 3) * 8,
+            ring_a + slot * Io::AB + o * kChunkRows * 64 + wave * 1024);
   };
-  constexpr int OPS = NA + NP * ((2 * Io::TB + 1023) / 1024);  // requests per k tile
-  for (int kt = 0; kt < kAhead && kt < IT; kt++) issue(kt);
-  for (int kt = 0; kt < IT; kt++) {
-    const int ahead = min(kAhead, IT - kt) - 1;  // k tiles requested after kt
-    wait_vm(ahead * OPS);
-    lds_barrier();  // every wave's quarter of A tile kt is in; every wave is done with ring slot (kt - 2) % kRing
-    if (kt + kAhead < IT) issue(kt + kAhead);
-    const int slot = kt % kRing;
-    // decode this wave's pairs into the matrix-core B layout
+  // B(t): the wave's pair at k tiles 2t, 2t + 1 (contiguous)
+  const uint8_t *bsrc = tr + (uint64_t)pair * IT * 2 * Io::TB;
+  auto issue_b = [&](int t) {
+    const int slot = t % Io::RB;
 #pragma unroll
-    for (int p = 0; p < NP; p++) {
-      const uint32_t *T0 = (const uint32_t *)(ring_b + slot * Io::PB + p * 2 * Io::TB);
+    for (uint32_t o = 0; o < Io::PB; o += 1024)
+      if (o + (uint32_t)lane * 16 < Io::PB) dma16(bsrc + (uint64_t)t * Io::PB + o + lane * 16, ring_b + slot * Io::PB + o);
+  };
+  for (int j = 0; j < kDB && j < NS; j++) {
+    if (j < kDA) issue_a(j);
+    issue_b(j);
+  }
+  for (int t = 0; t < NS; t++) {
+    wait_vm(after_step<Io::OA, Io::OB>(t, NS));
+    lds_barrier();  // every wave's rows of A(t) are in; every wave is done with A slot (t - 1) % RA
+    if (t + kDA < NS) issue_a(t + kDA);
+    if (t + kDB < NS) issue_b(t + kDB);
+    // decode both k tiles of the pair into the matrix-core B layout
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+      const uint32_t *T0 = (const uint32_t *)(ring_b + (t % Io::RB) * Io::PB + u * 2 * Io::TB);
       TileWords wa, wb;
       wa.w0 = T0[L.i0];
       wa.w1 = T0[L.i1];
@@ -316,43 +362,43 @@ __device__ void chunk_gemm(const uint16_t *A, int lda, int ahalf, int aidx, int 
       f16x2 a0, b0, a1, b1;
       decode4<K>(wa, L.sh, a0, b0);
       decode4<K>(wb, L.sh, a1, b1);
-      uint8_t *fp = frag + p * 1024;
+      uint8_t *fp = frag + u * 1024;
       *(f16x4 *)(fp + ((0 * 16 + c) * 4 + q) * 8) = f16x4{a0.x, a0.y, b0.x, b0.y};
       *(f16x4 *)(fp + ((1 * 16 + c) * 4 + q) * 8) = f16x4{a1.x, a1.y, b1.x, b1.y};
     }
-    f16x8 bf[NP];
-#pragma unroll
-    for (int p = 0; p < NP; p++) bf[p] = *(const f16x8 *)(frag + p * 1024 + ((lane & 31) * 4 + 2 * (lane >> 5)) * 8);
-    const uint8_t *at = ring_a + slot * Io::AB + aidx * kChunkRows * 32;
+    const f16x8 bf0 = *(const f16x8 *)(frag + ((lane & 31) * 4 + 2 * (lane >> 5)) * 8);
+    const f16x8 bf1 = *(const f16x8 *)(frag + 1024 + ((lane & 31) * 4 + 2 * (lane >> 5)) * 8);
+    const uint8_t *at = ring_a + (t % Io::RA) * Io::AB + aidx * kChunkRows * 64;
 #pragma unroll
     for (int rb = 0; rb < kRowBlocks; rb++) {
       if (rb < nrb) {
-        const f16x8 af = *(const f16x8 *)(at + (rb * 32 + (lane & 31)) * 32 + (lane >> 5) * 16);
-#pragma unroll
-        for (int p = 0; p < NP; p++) acc[rb][p] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf[p], acc[rb][p], 0, 0, 0);
+        const uint8_t *ar = at + (rb * 32 + (lane & 31)) * 64 + (lane >> 5) * 16;
+        const f16x8 a0 = *(const f16x8 *)ar, a1 = *(const f16x8 *)(ar + 32);
+        acc[rb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, bf0, acc[rb], 0, 0, 0);
+        acc[rb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, bf1, acc[rb], 0, 0, 0);
       }
     }
   }
 }
 
-// gate/up: chunk ch, 128-column block ib of inter; waves 0-1 gate pairs 4 ib + 2 w + {0, 1}, waves 2-3 up
+// gate/up: chunk ch, 128-column block ib of inter; wave w: projection w / 4 (gate, up), pair 4 ib + w % 4
 template <int K, int KS>
-__global__ __launch_bounds__(256, 1) void bat_gateup(MoeArgs a, const uint32_t *bk, const uint32_t *chunks,
+__global__ __launch_bounds__(512, 1) void bat_gateup(MoeArgs a, const uint32_t *bk, const uint32_t *chunks,
                                                      const uint32_t *rows, const uint16_t *xh, uint16_t *hh) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const uint32_t nch = bk[3 * (a.ne + 1)];
   const int ch = blockIdx.x, ib = blockIdx.y;
   if ((uint32_t)ch >= nch) return;
   const int e = (int)chunks[3 * ch], row0 = (int)chunks[3 * ch + 1], nrows = (int)chunks[3 * ch + 2];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, proj = wave >> 1;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, proj = wave >> 2;
   const uint8_t *blk = expert_block(a, e);
-  f32x16 acc[kRowBlocks][2];
+  f32x16 acc[kRowBlocks];
   const uint16_t *A = xh + (uint64_t)row0 * 2 * a.hid;  // [row][gate | up][hid]
-  const int p0 = ib * 4 + 2 * (wave & 1);
+  const int pair = ib * 4 + (wave & 3);
   if (e >= a.ne)
-    chunk_gemm<KS, 2, 2>(A, 2 * a.hid, a.hid, proj, nrows, blk + tr_of(a, e, proj), a.hid / 16, p0, lds, acc);
+    chunk_gemm<KS, 2>(A, 2 * a.hid, a.hid, proj, nrows, blk + tr_of(a, e, proj), a.hid / 16, pair, lds, acc);
   else
-    chunk_gemm<K, 2, 2>(A, 2 * a.hid, a.hid, proj, nrows, blk + tr_of(a, e, proj), a.hid / 16, p0, lds, acc);
+    chunk_gemm<K, 2>(A, 2 * a.hid, a.hid, proj, nrows, blk + tr_of(a, e, proj), a.hid / 16, pair, lds, acc);
   // epilogue per 32-row block: columns to LDS as [32][256] f32 (gate 0..127, up 128..255), then one wave per row
   float *ot = (float *)lds;
   const uint16_t *svg = (const uint16_t *)(blk + sv_of(a, e, 0)) + ib * 128;
@@ -366,16 +412,14 @@ __global__ __launch_bounds__(256, 1) void bat_gateup(MoeArgs a, const uint32_t *
     if (rb >= nrb) break;
     __syncthreads();
 #pragma unroll
-    for (int p = 0; p < 2; p++)
-#pragma unroll
-      for (int i = 0; i < 16; i++) {
-        const int rr = 4 * (lane >> 5) + (i & 3) + 8 * (i >> 2), col = proj * 128 + (2 * (wave & 1) + p) * 32 + (lane & 31);
-        ot[rr * 256 + col] = acc[rb][p][i];
-      }
+    for (int i = 0; i < 16; i++) {
+      const int r = 4 * (lane >> 5) + (i & 3) + 8 * (i >> 2), col = proj * 128 + (wave & 3) * 32 + (lane & 31);
+      ot[r * 256 + col] = acc[rb][i];
+    }
     __syncthreads();
-    for (int rr = wave; rr < 32 && rb * 32 + rr < nrows; rr += 4) {
-      float g0 = ot[rr * 256 + lane], g1 = ot[rr * 256 + 64 + lane];
-      float u0 = ot[rr * 256 + 128 + lane], u1 = ot[rr * 256 + 192 + lane];
+    for (int r = wave; r < 32 && rb * 32 + r < nrows; r += kWavesG) {
+      float g0 = ot[r * 256 + lane], g1 = ot[r * 256 + 64 + lane];
+      float u0 = ot[r * 256 + 128 + lane], u1 = ot[r * 256 + 192 + lane];
       fwht2(g0, g1, lane, a.had_inter, a.sc_inter);
       fwht2(u0, u1, lane, a.had_inter, a.sc_inter);
       g0 = g0 * sg0;
@@ -385,33 +429,39 @@ __global__ __launch_bounds__(256, 1) void bat_gateup(MoeArgs a, const uint32_t *
       float h0 = g0 / (1.f + expf(-g0)) * u0 * sd0;
       float h1 = g1 / (1.f + expf(-g1)) * u1 * sd1;
       fwht2(h0, h1, lane, a.had_inter, a.sc_inter);
-      uint16_t *out = hh + (uint64_t)(row0 + rb * 32 + rr) * a.inter + ib * 128;
+      uint16_t *out = hh + (uint64_t)(row0 + rb * 32 + r) * a.inter + ib * 128;
       out[kp(lane)] = f2h(h0);
       out[kp(lane + 64)] = f2h(h1);
     }
   }
 }
 
-// down: chunk ch, 128-column block ob of hid; wave w: pair 4 ob + w. Output per (token, slot): H, svh_d, weight.
+// down: chunk ch, 256 columns of hid (output blocks 2 ob2, 2 ob2 + 1); wave w: pair 8 ob2 + w. Output per
+// (token, slot): H over each 128-column block, svh_d, the slot's route weight.
 template <int K, int KS>
-__global__ __launch_bounds__(256, 1) void bat_down(MoeArgs a, const uint32_t *bk, const uint32_t *chunks,
+__global__ __launch_bounds__(512, 1) void bat_down(MoeArgs a, const uint32_t *bk, const uint32_t *chunks,
                                                    const uint32_t *rows, const uint16_t *hh, float *dnw) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const uint32_t nch = bk[3 * (a.ne + 1)];
-  const int ch = blockIdx.x, ob = blockIdx.y;
+  const int ch = blockIdx.x, ob2 = blockIdx.y;
   if ((uint32_t)ch >= nch) return;
   const int e = (int)chunks[3 * ch], row0 = (int)chunks[3 * ch + 1], nrows = (int)chunks[3 * ch + 2];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const uint8_t *blk = expert_block(a, e);
-  f32x16 acc[kRowBlocks][1];
+  f32x16 acc[kRowBlocks];
   const uint16_t *A = hh + (uint64_t)row0 * a.inter;
   if (e >= a.ne)
-    chunk_gemm<KS, 1, 1>(A, a.inter, 0, 0, nrows, blk + tr_of(a, e, 2), a.inter / 16, ob * 4 + wave, lds, acc);
+    chunk_gemm<KS, 1>(A, a.inter, 0, 0, nrows, blk + tr_of(a, e, 2), a.inter / 16, ob2 * 8 + wave, lds, acc);
   else
-    chunk_gemm<K, 1, 1>(A, a.inter, 0, 0, nrows, blk + tr_of(a, e, 2), a.inter / 16, ob * 4 + wave, lds, acc);
-  float *ot = (float *)lds;
-  const uint16_t *sv = (const uint16_t *)(blk + sv_of(a, e, 2)) + ob * 128;
-  const float s0 = h2f(sv[lane]), s1 = h2f(sv[lane + 64]);
+    chunk_gemm<K, 1>(A, a.inter, 0, 0, nrows, blk + tr_of(a, e, 2), a.inter / 16, ob2 * 8 + wave, lds, acc);
+  float *ot = (float *)lds;  // [32][256]
+  const uint16_t *sv = (const uint16_t *)(blk + sv_of(a, e, 2)) + ob2 * 256;
+  float s[2][2];
+#pragma unroll
+  for (int bb = 0; bb < 2; bb++) {
+    s[bb][0] = h2f(sv[bb * 128 + lane]);
+    s[bb][1] = h2f(sv[bb * 128 + lane + 64]);
+  }
   const int nrb = (nrows + 31) / 32;
 #pragma unroll
   for (int rb = 0; rb < kRowBlocks; rb++) {
@@ -419,19 +469,22 @@ __global__ __launch_bounds__(256, 1) void bat_down(MoeArgs a, const uint32_t *bk
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < 16; i++) {
-      const int rr = 4 * (lane >> 5) + (i & 3) + 8 * (i >> 2), col = wave * 32 + (lane & 31);
-      ot[rr * 128 + col] = acc[rb][0][i];
+      const int r = 4 * (lane >> 5) + (i & 3) + 8 * (i >> 2), col = wave * 32 + (lane & 31);
+      ot[r * 256 + col] = acc[rb][i];
     }
     __syncthreads();
-    for (int rr = wave; rr < 32 && rb * 32 + rr < nrows; rr += 4) {
-      float v0 = ot[rr * 128 + lane], v1 = ot[rr * 128 + 64 + lane];
-      fwht2(v0, v1, lane, a.had_hid, a.sc_hid);
-      const uint32_t s = rows[row0 + rb * 32 + rr];
-      const int r = s / a.nslot, k = s % a.nslot;
-      const float w = k >= a.topk ? a.sgv[r] : __uint_as_float(a.route[(uint64_t)r * 2 * a.topk + a.topk + k]);
-      float *out = dnw + ((uint64_t)r * a.nslot + k) * a.hid + ob * 128;
-      out[lane] = v0 * s0 * w;
-      out[lane + 64] = v1 * s1 * w;
+    for (int r = wave; r < 32 && rb * 32 + r < nrows; r += kWavesG) {
+      const uint32_t sl = rows[row0 + rb * 32 + r];
+      const int tok = sl / a.nslot, k = sl % a.nslot;
+      const float w = k >= a.topk ? a.sgv[tok] : __uint_as_float(a.route[(uint64_t)tok * 2 * a.topk + a.topk + k]);
+      float *out = dnw + ((uint64_t)tok * a.nslot + k) * a.hid + ob2 * 256;
+#pragma unroll
+      for (int bb = 0; bb < 2; bb++) {
+        float v0 = ot[r * 256 + bb * 128 + lane], v1 = ot[r * 256 + bb * 128 + 64 + lane];
+        fwht2(v0, v1, lane, a.had_hid, a.sc_hid);
+        out[bb * 128 + lane] = v0 * s[bb][0] * w;
+        out[bb * 128 + lane + 64] = v1 * s[bb][1] * w;
+      }
     }
   }
 }
@@ -449,26 +502,25 @@ __global__ __launch_bounds__(256) void bat_combine(MoeArgs a, const float *dnw) 
 namespace {
 template <int K, int KS>
 void launch_gemms(const MoeArgs &a, const MoeBatchBufs &b, hipStream_t s) {
-  const size_t lg = GemmIo<(K > KS ? K : KS), 2, 2>::LDS, ld = GemmIo<(K > KS ? K : KS), 1, 1>::LDS;
+  constexpr int KM = K > KS ? K : KS;
+  const size_t lg = GemmIo<KM, 2>::LDS, ld = GemmIo<KM, 1>::LDS;
+  static_assert(GemmIo<4, 1>::LDS >= 32 * 256 * 4, "LDS too small for the epilogue staging");
   static bool attr = false;
   if (!attr) {
     IJ_HIP(hipFuncSetAttribute((const void *)&bat_gateup<K, KS>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lg));
     IJ_HIP(hipFuncSetAttribute((const void *)&bat_down<K, KS>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)ld));
     attr = true;
   }
-  // epilogue staging reuses the rings: [32][256] f32 = 32 KB must fit
-  static_assert(GemmIo<4, 1, 1>::LDS >= 32 * 128 * 4 && GemmIo<4, 2, 2>::LDS >= 32 * 256 * 4,
-                "LDS too small for the epilogue staging");
-  hipLaunchKernelGGL((bat_gateup<K, KS>), dim3(b.max_chunks, a.inter / 128), dim3(256), lg, s, a, b.bk, b.chunks,
-                     b.rows, b.xh, b.hh);
-  hipLaunchKernelGGL((bat_down<K, KS>), dim3(b.max_chunks, a.hid / 128), dim3(256), ld, s, a, b.bk, b.chunks,
+  hipLaunchKernelGGL((bat_gateup<K, KS>), dim3(b.max_chunks, a.inter / 128), dim3(64 * kWavesG), lg, s, a, b.bk,
+                     b.chunks, b.rows, b.xh, b.hh);
+  hipLaunchKernelGGL((bat_down<K, KS>), dim3(b.max_chunks, a.hid / 256), dim3(64 * kWavesG), ld, s, a, b.bk, b.chunks,
                      b.rows, b.hh, b.dnw);
 }
 }  // namespace
 
 bool moe_batch_supported(int K, int KS, int hid, int inter, int ne, int topk) {
   const bool ks = (K >= 4 && K <= 6) && (KS >= 4 && KS <= 6);
-  return ks && hid % 128 == 0 && inter % 128 == 0 && hid <= 8192 && inter <= 4096 && ne < 1024 && topk <= 32;
+  return ks && hid % 256 == 0 && inter % 128 == 0 && hid <= 8192 && inter <= 4096 && ne < 1024 && topk <= 32;
 }
 int moe_batch_max_chunks(int R, int ne, int topk, bool shared) {
   return (R * topk + kChunkRows - 1) / kChunkRows + ne + (shared ? (R + kChunkRows - 1) / kChunkRows : 0) + 1;
@@ -477,7 +529,7 @@ int moe_batch_max_chunks(int R, int ne, int topk, bool shared) {
 void launch_moe_batch(const MoeArgs &a, const MoeBatchBufs &b, hipStream_t s) {
   const int ncol = a.ne + a.has_sgate, S = a.R * a.nslot;
   hipLaunchKernelGGL(bat_zero, dim3(1), dim3(1024), 0, s, b.bk, a.ne + 1);  // a kernel, not a memset node
-  hipLaunchKernelGGL(bat_router, dim3((a.R + 63) / 64, (ncol + 63) / 64), dim3(256), 0, s, a);
+  hipLaunchKernelGGL(bat_router, dim3((a.R + 31) / 32, (ncol + 127) / 128), dim3(256), 0, s, a);
   hipLaunchKernelGGL(bat_route, dim3((a.R + 3) / 4), dim3(256), 0, s, a, b.bk);
   hipLaunchKernelGGL(bat_scan, dim3(1), dim3(1024), 0, s, a, b.bk, b.chunks, b.max_chunks);
   hipLaunchKernelGGL(bat_place, dim3((S + 255) / 256), dim3(256), 0, s, a, b.bk, b.rows);
