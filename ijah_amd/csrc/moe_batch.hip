@@ -275,48 +275,126 @@ __global__ __launch_bounds__(256) void bat_prep(MoeArgs a, const uint32_t *rows,
 // tiles kDB steps ahead, so that enough weight bytes are in flight per CU to cover the memory latency.
 // acc[rb] = rows 32 rb.., the wave's 32 columns, in the matrix-core layout.
 constexpr int kWavesG = 8;
-constexpr int kDA = 3, kDB = 8;  // steps (of 2 k tiles) requested ahead: A, B
+// Work item of this workgroup for a 1-D grid over nitems items (grid a multiple of 8): consecutive workgroups go to
+// the 8 XCDs in turn, so each XCD takes a contiguous eighth of the items; items that share an operand (the column
+// blocks of one chunk) then run together on one XCD and share its L2. False for workgroups past the work.
+__device__ __forceinline__ bool xcd_item(int nitems, int &item) {
+  const int b = blockIdx.x, xcd = b & 7, idx = b >> 3, q = nitems >> 3, r = nitems & 7;
+  if (idx >= q + (xcd < r ? 1 : 0)) return false;
+  item = xcd * q + min(xcd, r) + idx;
+  return true;
+}
+// Two workgroups share a CU (so four waves per SIMD hide each other's latency): each keeps under 80 KB of LDS.
+constexpr int kDA = 2;  // steps (of 2 k tiles) of A requested ahead
+template <int K>
+constexpr int kDB = K >= 6 ? 4 : 5;  // steps of B requested ahead
 template <int K, int NA>
 struct GemmIo {
   static constexpr uint32_t TB = 32u * K;                  // bytes of one 16x16 tile
   static constexpr uint32_t PB = 2 * 2 * TB;               // a wave's B bytes per step (a pair x 2 k tiles)
   static constexpr uint32_t AB = NA * kChunkRows * 64;     // A bytes per step (NA x 128 rows x 32 halves)
-  static constexpr int RA = kDA + 1, RB = kDB + 1;         // ring slots
-  static constexpr uint32_t WAVE_B = RB * PB + 2 * 1024;   // B ring + decoded fragments of the step
-  static constexpr uint32_t LDS = RA * AB + kWavesG * WAVE_B;
+  static constexpr int DB = kDB<K>;
+  static constexpr int RA = kDA + 1, RB = DB + 1;          // ring slots
+  static constexpr uint32_t LDS_RING = RA * AB + kWavesG * RB * PB;
+  static constexpr uint32_t LDS = LDS_RING > 32768 ? LDS_RING : 32768;  // the epilogue stages 32 x 256 floats
   static constexpr int OA = NA, OB = (PB + 1023) / 1024;   // requests per A / B step
+  static_assert(LDS <= 81920, "two workgroups per CU");
 };
-// Issue order: prologue A(0) B(0) A(1) B(1) .. A(kDA-1) B(kDA-1) B(kDA) .. B(kDB-1); step j then issues
-// A(j + kDA) and B(j + kDB) (while < NS). Returns how many requests were issued after A(t) and B(t), counted at
+// Issue order: prologue A(0) B(0) A(1) B(1) .. A(kDA-1) B(kDA-1) B(kDA) .. B(DB-1); step j then issues
+// A(j + kDA) and B(j + DB) (while < NS). Returns how many requests were issued after A(t) and B(t), counted at
 // step t before it issues: the s_waitcnt vmcnt that makes both complete (completion is in issue order).
-template <int OA, int OB>
-__device__ __forceinline__ int after_step(int t, int NS) {
-  auto sum_ops = [&](int n) { return OA * min(n, max(NS - kDA, 0)) + OB * min(n, max(NS - kDB, 0)); };
-  const int pa = min(kDA, NS), pb = min(kDB, NS);
+template <int OA, int OB, int DB>
+__host__ __device__ constexpr int after_step(int t, int NS) {
+  auto mn = [](int x, int y) { return x < y ? x : y; };
+  auto mx = [](int x, int y) { return x > y ? x : y; };
+  auto sum_ops = [&](int n) { return OA * mn(n, mx(NS - kDA, 0)) + OB * mn(n, mx(NS - DB, 0)); };
+  const int pa = mn(kDA, NS), pb = mn(DB, NS);
   const int prologue = OA * pa + OB * pb;
   const int total = prologue + sum_ops(t);
   int last;  // one past the position of the later of A(t), B(t)
   if (t < kDA) {
     last = (OA + OB) * (t + 1);
-  } else if (t < kDB) {
-    last = max(prologue + sum_ops(t - kDA) + OA, (OA + OB) * pa + OB * (t - pa) + OB);
+  } else if (t < DB) {
+    last = mx(prologue + sum_ops(t - kDA) + OA, (OA + OB) * pa + OB * (t - pa) + OB);
   } else {
-    last = max(prologue + sum_ops(t - kDA) + OA, prologue + sum_ops(t - kDB) + ((t - kDB) + kDA < NS ? OA : 0) + OB);
+    last = mx(prologue + sum_ops(t - kDA) + OA, prologue + sum_ops(t - DB) + ((t - DB) + kDA < NS ? OA : 0) + OB);
   }
   return total - last;
+}
+// the count of steps t with DB <= t and t + DB < NS (both streams still issuing): A(t) is the later request,
+// followed by B(t - kDA + DB) and kDA - 1 full steps
+template <int OA, int OB>
+constexpr int kAfterSteady = OB + (kDA - 1) * (OA + OB);
+static_assert(after_step<2, 1, 5>(5, 1000) == kAfterSteady<2, 1> && after_step<1, 1, 4>(9, 1000) == kAfterSteady<1, 1>,
+              "steady-state wait count");
+template <int OA, int OB, int DB>
+__device__ __forceinline__ void wait_step(int t, int NS) {
+  static_assert(kAfterSteady<OA, OB> <= 15, "vmcnt immediate");
+  if (t >= DB && t + DB < NS)
+    __builtin_amdgcn_s_waitcnt(0x0F70 | kAfterSteady<OA, OB>);
+  else
+    wait_vm(after_step<OA, OB, DB>(t, NS));
+}
+
+// The matrix-core B operand of lane l is column n = l % 32 of the pair (tile n / 16, column c = n % 16), k values
+// 8 (l / 32) .. + 8: the trellis groups (c, q) with q = 2 (l / 32) and q + 1, four consecutive k each. Group m of a
+// tile (weights 4m .. 4m + 3 of the bitstream) holds column c = (m >> 3) + 8 (m & 1), k quarter q = (m >> 1) & 3.
+__device__ __forceinline__ uint32_t group_of(uint32_t c, uint32_t q) { return ((c & 7u) << 3) | (q << 1) | (c >> 3); }
+template <int K>
+struct BLane {
+  TileLane<K> g0, g1;  // the lane's two groups
+  uint32_t tile;       // 0 or 1: which tile of the pair
+};
+template <int K>
+__device__ __forceinline__ BLane<K> b_lane(uint32_t lane) {
+  const uint32_t n = lane & 31u, q = 2u * (lane >> 5);
+  BLane<K> b;
+  b.g0 = tile_lane<K>(group_of(n & 15u, q));
+  b.g1 = tile_lane<K>(group_of(n & 15u, q + 1u));
+  b.tile = n >> 4;
+  return b;
+}
+// decodes the lane's B operand for both k tiles of one step straight from the ring bytes src
+template <int K>
+__device__ __forceinline__ void decode_step(const uint8_t *src, const BLane<K> &B, f16x8 (&bf)[2]) {
+  constexpr int TW = 8 * K;
+  const uint32_t *T = (const uint32_t *)src + B.tile * TW;
+  TileWords w[4];
+#pragma unroll
+  for (int u = 0; u < 2; u++) {
+    const uint32_t *Tu = T + u * 2 * TW;
+    w[2 * u].w0 = Tu[B.g0.i0];
+    w[2 * u].w1 = Tu[B.g0.i1];
+    w[2 * u].w2 = kThreeWords<K> ? Tu[B.g0.i2] : 0u;
+    w[2 * u + 1].w0 = Tu[B.g1.i0];
+    w[2 * u + 1].w1 = Tu[B.g1.i1];
+    w[2 * u + 1].w2 = kThreeWords<K> ? Tu[B.g1.i2] : 0u;
+  }
+#pragma unroll
+  for (int u = 0; u < 2; u++) {
+    f16x2 l0, h0, l1, h1;
+    decode4<K>(w[2 * u], B.g0.sh, l0, h0);
+    decode4<K>(w[2 * u + 1], B.g1.sh, l1, h1);
+    bf[u] = f16x8{l0.x, l0.y, h0.x, h0.y, l1.x, l1.y, h1.x, h1.y};
+  }
 }
 
 template <int K, int NA>
 __device__ void chunk_gemm(const uint16_t *A, int lda, int ahalf, int aidx, int nrows, const uint8_t *tr, int IT,
-                           int pair, uint8_t *lds, f32x16 (&acc)[kRowBlocks]) {
+                           int pair, uint8_t *lds, f32x16 (&acc)[kRowBlocks], uint64_t *dbg) {
   using Io = GemmIo<K, NA>;
-  constexpr int TW = 8 * K;
+  constexpr int DB = Io::DB;
+#ifdef IJ_BATCH_TRACE  // debug builds only: shader-clock stamps of step 20 per (workgroup, wave)
+  uint64_t *drow = dbg ? dbg + ((uint64_t)8192 + blockIdx.x * 8 + (threadIdx.x >> 6)) * 8 : nullptr;
+#define IJ_STAMP(t_, f_) \
+  if (drow && (t_) && (threadIdx.x & 63) == 0) drow[f_] = __builtin_amdgcn_s_memtime();
+#else
+#define IJ_STAMP(t_, f_)
+#endif
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, NS = IT / 2;
   uint8_t *ring_a = lds;
-  uint8_t *ring_b = lds + Io::RA * Io::AB + wave * Io::WAVE_B;
-  uint8_t *frag = ring_b + Io::RB * Io::PB;
-  const TileLane<K> L = tile_lane<K>((uint32_t)lane);
-  const int c = (lane >> 3) + 8 * (lane & 1), q = (lane >> 1) & 3;
+  uint8_t *ring_b = lds + Io::RA * Io::AB + wave * Io::RB * Io::PB;
+  const BLane<K> BL = b_lane<K>((uint32_t)lane);
   const int nrb = (nrows + 31) / 32;
 #pragma unroll
   for (int rb = 0; rb < kRowBlocks; rb++)
@@ -339,56 +417,59 @@ __device__ void chunk_gemm(const uint16_t *A, int lda, int ahalf, int aidx, int 
     for (uint32_t o = 0; o < Io::PB; o += 1024)
       if (o + (uint32_t)lane * 16 < Io::PB) dma16(bsrc + (uint64_t)t * Io::PB + o + lane * 16, ring_b + slot * Io::PB + o);
   };
-  for (int j = 0; j < kDB && j < NS; j++) {
+  // step s begins when A(s) and B(s) are in: every wave's rows of A(s) landed (barrier), and every wave has read
+  // its fragments of A(s - 1), whose ring slot the step's A request then reuses
+  f16x8 bf[2];
+  auto begin_step = [&](int s) {
+    wait_step<Io::OA, Io::OB, DB>(s, NS);
+    lds_barrier();
+    if (s + kDA < NS) issue_a(s + kDA);
+    if (s + DB < NS) issue_b(s + DB);
+    decode_step<K>(ring_b + (s % Io::RB) * Io::PB, BL, bf);
+  };
+  for (int j = 0; j < DB && j < NS; j++) {
     if (j < kDA) issue_a(j);
     issue_b(j);
   }
+  begin_step(0);
   for (int t = 0; t < NS; t++) {
-    wait_vm(after_step<Io::OA, Io::OB>(t, NS));
-    lds_barrier();  // every wave's rows of A(t) are in; every wave is done with A slot (t - 1) % RA
-    if (t + kDA < NS) issue_a(t + kDA);
-    if (t + kDB < NS) issue_b(t + kDB);
-    // decode both k tiles of the pair into the matrix-core B layout
+    IJ_STAMP(t == 20, 0)
+    const uint8_t *at = ring_a + (t % Io::RA) * Io::AB + aidx * kChunkRows * 64 + (lane & 31) * 64 + (lane >> 5) * 16;
+    const f16x8 b0 = bf[0], b1 = bf[1];
 #pragma unroll
-    for (int u = 0; u < 2; u++) {
-      const uint32_t *T0 = (const uint32_t *)(ring_b + (t % Io::RB) * Io::PB + u * 2 * Io::TB);
-      TileWords wa, wb;
-      wa.w0 = T0[L.i0];
-      wa.w1 = T0[L.i1];
-      wa.w2 = kThreeWords<K> ? T0[L.i2] : 0u;
-      wb.w0 = T0[TW + L.i0];
-      wb.w1 = T0[TW + L.i1];
-      wb.w2 = kThreeWords<K> ? T0[TW + L.i2] : 0u;
-      f16x2 a0, b0, a1, b1;
-      decode4<K>(wa, L.sh, a0, b0);
-      decode4<K>(wb, L.sh, a1, b1);
-      uint8_t *fp = frag + u * 1024;
-      *(f16x4 *)(fp + ((0 * 16 + c) * 4 + q) * 8) = f16x4{a0.x, a0.y, b0.x, b0.y};
-      *(f16x4 *)(fp + ((1 * 16 + c) * 4 + q) * 8) = f16x4{a1.x, a1.y, b1.x, b1.y};
-    }
-    const f16x8 bf0 = *(const f16x8 *)(frag + ((lane & 31) * 4 + 2 * (lane >> 5)) * 8);
-    const f16x8 bf1 = *(const f16x8 *)(frag + 1024 + ((lane & 31) * 4 + 2 * (lane >> 5)) * 8);
-    const uint8_t *at = ring_a + (t % Io::RA) * Io::AB + aidx * kChunkRows * 64;
+    for (int r2 = 0; r2 < kRowBlocks; r2 += 2) {  // two row blocks' A fragments in flight at a time
+      f16x8 af[2][2];
 #pragma unroll
-    for (int rb = 0; rb < kRowBlocks; rb++) {
-      if (rb < nrb) {
-        const uint8_t *ar = at + (rb * 32 + (lane & 31)) * 64 + (lane >> 5) * 16;
-        const f16x8 a0 = *(const f16x8 *)ar, a1 = *(const f16x8 *)(ar + 32);
-        acc[rb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, bf0, acc[rb], 0, 0, 0);
-        acc[rb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, bf1, acc[rb], 0, 0, 0);
+      for (int i = 0; i < 2; i++) {
+        af[i][0] = *(const f16x8 *)(at + (r2 + i) * 2048);
+        af[i][1] = *(const f16x8 *)(at + (r2 + i) * 2048 + 32);
+      }
+#pragma unroll
+      for (int i = 0; i < 2; i++) {
+        if (r2 + i < nrb) {
+          acc[r2 + i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i][0], b0, acc[r2 + i], 0, 0, 0);
+          acc[r2 + i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i][1], b1, acc[r2 + i], 0, 0, 0);
+        }
       }
     }
+    IJ_STAMP(t == 20, 1)
+    // the matrix cores run while the next step's tiles decode
+    if (t + 1 < NS) begin_step(t + 1);
+    IJ_STAMP(t == 20, 2)
   }
+  IJ_STAMP(true, 5)
+#undef IJ_STAMP
 }
 
 // gate/up: chunk ch, 128-column block ib of inter; wave w: projection w / 4 (gate, up), pair 4 ib + w % 4
 template <int K, int KS>
-__global__ __launch_bounds__(512, 1) void bat_gateup(MoeArgs a, const uint32_t *bk, const uint32_t *chunks,
+__global__ __launch_bounds__(512, 4) void bat_gateup(MoeArgs a, const uint32_t *bk, const uint32_t *chunks,
                                                      const uint32_t *rows, const uint16_t *xh, uint16_t *hh) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-  const uint32_t nch = bk[3 * (a.ne + 1)];
-  const int ch = blockIdx.x, ib = blockIdx.y;
-  if ((uint32_t)ch >= nch) return;
+  const int nib = a.inter / 128;
+  int item;
+  if (!xcd_item((int)bk[3 * (a.ne + 1)] * nib, item)) return;
+  const int ch = item / nib, ib = item % nib;
   const int e = (int)chunks[3 * ch], row0 = (int)chunks[3 * ch + 1], nrows = (int)chunks[3 * ch + 2];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, proj = wave >> 2;
   const uint8_t *blk = expert_block(a, e);
@@ -396,9 +477,9 @@ __global__ __launch_bounds__(512, 1) void bat_gateup(MoeArgs a, const uint32_t *
   const uint16_t *A = xh + (uint64_t)row0 * 2 * a.hid;  // [row][gate | up][hid]
   const int pair = ib * 4 + (wave & 3);
   if (e >= a.ne)
-    chunk_gemm<KS, 2>(A, 2 * a.hid, a.hid, proj, nrows, blk + tr_of(a, e, proj), a.hid / 16, pair, lds, acc);
+    chunk_gemm<KS, 2>(A, 2 * a.hid, a.hid, proj, nrows, blk + tr_of(a, e, proj), a.hid / 16, pair, lds, acc, a.trace);
   else
-    chunk_gemm<K, 2>(A, 2 * a.hid, a.hid, proj, nrows, blk + tr_of(a, e, proj), a.hid / 16, pair, lds, acc);
+    chunk_gemm<K, 2>(A, 2 * a.hid, a.hid, proj, nrows, blk + tr_of(a, e, proj), a.hid / 16, pair, lds, acc, a.trace);
   // epilogue per 32-row block: columns to LDS as [32][256] f32 (gate 0..127, up 128..255), then one wave per row
   float *ot = (float *)lds;
   const uint16_t *svg = (const uint16_t *)(blk + sv_of(a, e, 0)) + ib * 128;
@@ -439,21 +520,22 @@ __global__ __launch_bounds__(512, 1) void bat_gateup(MoeArgs a, const uint32_t *
 // down: chunk ch, 256 columns of hid (output blocks 2 ob2, 2 ob2 + 1); wave w: pair 8 ob2 + w. Output per
 // (token, slot): H over each 128-column block, svh_d, the slot's route weight.
 template <int K, int KS>
-__global__ __launch_bounds__(512, 1) void bat_down(MoeArgs a, const uint32_t *bk, const uint32_t *chunks,
+__global__ __launch_bounds__(512, 4) void bat_down(MoeArgs a, const uint32_t *bk, const uint32_t *chunks,
                                                    const uint32_t *rows, const uint16_t *hh, float *dnw) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-  const uint32_t nch = bk[3 * (a.ne + 1)];
-  const int ch = blockIdx.x, ob2 = blockIdx.y;
-  if ((uint32_t)ch >= nch) return;
+  const int nob = a.hid / 256;
+  int item;
+  if (!xcd_item((int)bk[3 * (a.ne + 1)] * nob, item)) return;
+  const int ch = item / nob, ob2 = item % nob;
   const int e = (int)chunks[3 * ch], row0 = (int)chunks[3 * ch + 1], nrows = (int)chunks[3 * ch + 2];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const uint8_t *blk = expert_block(a, e);
   f32x16 acc[kRowBlocks];
   const uint16_t *A = hh + (uint64_t)row0 * a.inter;
   if (e >= a.ne)
-    chunk_gemm<KS, 1>(A, a.inter, 0, 0, nrows, blk + tr_of(a, e, 2), a.inter / 16, ob2 * 8 + wave, lds, acc);
+    chunk_gemm<KS, 1>(A, a.inter, 0, 0, nrows, blk + tr_of(a, e, 2), a.inter / 16, ob2 * 8 + wave, lds, acc, nullptr);
   else
-    chunk_gemm<K, 1>(A, a.inter, 0, 0, nrows, blk + tr_of(a, e, 2), a.inter / 16, ob2 * 8 + wave, lds, acc);
+    chunk_gemm<K, 1>(A, a.inter, 0, 0, nrows, blk + tr_of(a, e, 2), a.inter / 16, ob2 * 8 + wave, lds, acc, nullptr);
   float *ot = (float *)lds;  // [32][256]
   const uint16_t *sv = (const uint16_t *)(blk + sv_of(a, e, 2)) + ob2 * 256;
   float s[2][2];
@@ -504,16 +586,15 @@ template <int K, int KS>
 void launch_gemms(const MoeArgs &a, const MoeBatchBufs &b, hipStream_t s) {
   constexpr int KM = K > KS ? K : KS;
   const size_t lg = GemmIo<KM, 2>::LDS, ld = GemmIo<KM, 1>::LDS;
-  static_assert(GemmIo<4, 1>::LDS >= 32 * 256 * 4, "LDS too small for the epilogue staging");
   static bool attr = false;
   if (!attr) {
     IJ_HIP(hipFuncSetAttribute((const void *)&bat_gateup<K, KS>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lg));
     IJ_HIP(hipFuncSetAttribute((const void *)&bat_down<K, KS>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)ld));
     attr = true;
   }
-  hipLaunchKernelGGL((bat_gateup<K, KS>), dim3(b.max_chunks, a.inter / 128), dim3(64 * kWavesG), lg, s, a, b.bk,
+  hipLaunchKernelGGL((bat_gateup<K, KS>), dim3((b.max_chunks * (a.inter / 128) + 7) & ~7), dim3(64 * kWavesG), lg, s, a, b.bk,
                      b.chunks, b.rows, b.xh, b.hh);
-  hipLaunchKernelGGL((bat_down<K, KS>), dim3(b.max_chunks, a.hid / 256), dim3(64 * kWavesG), ld, s, a, b.bk, b.chunks,
+  hipLaunchKernelGGL((bat_down<K, KS>), dim3((b.max_chunks * (a.hid / 256) + 7) & ~7), dim3(64 * kWavesG), ld, s, a, b.bk, b.chunks,
                      b.rows, b.hh, b.dnw);
 }
 }  // namespace
