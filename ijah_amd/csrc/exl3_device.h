@@ -86,9 +86,10 @@ __device__ __forceinline__ float xor_lane(float v, int lane) {
 template <int BIT>
 __device__ __forceinline__ void fwht_stage(float &v0, float &v1, int lane) {
   const float p0 = xor_lane<BIT>(v0, lane), p1 = xor_lane<BIT>(v1, lane);
-  const bool up = (lane & BIT) != 0;
-  v0 = up ? p0 - v0 : v0 + p0;
-  v1 = up ? p1 - v1 : v1 + p1;
+  // partner + (-1 or +1) v: one fused op, rounded once, so exactly p - v on the upper lanes and v + p on the others
+  const float sg = (lane & BIT) ? -1.f : 1.f;
+  v0 = __builtin_fmaf(sg, v0, p0);
+  v1 = __builtin_fmaf(sg, v1, p1);
 }
 // normalised Sylvester H_N (N = 16..128) on a 128-chunk held as (lane, lane + 64); blocks of N are contiguous.
 __device__ __forceinline__ void fwht2(float &v0, float &v1, int lane, int N, float sc) {

@@ -81,29 +81,33 @@ __global__ __launch_bounds__(1024) void bat_zero(uint32_t *p, int n) {
 }
 
 // ---------------------------------------------------------------------------------------------------- router
-// logits[r][c] = bf16(x[r] . router[c]) for c < ne + has_sgate on the matrix cores: one wave per 32 x 32 tile
-// (rows x router rows), k steps of 16. x is split into bf16 hi + lo (x - hi rounded again), two MFMAs per step, so the
-// product carries about 16 mantissa bits of x: within f32 rounding of the reference's f32 dot for these logits.
+// logits[r][c] = bf16(x[r] . router[c]) for c < ne + has_sgate on the matrix cores: one workgroup per 32 x 32 tile
+// (rows x router rows), its 8 waves splitting k into eighths (so that even a few rows keep the chip busy) and
+// summing in LDS in wave order. k steps of 16: x is split into bf16 hi + lo (x - hi rounded again), two MFMAs per
+// step, so the product carries about 16 mantissa bits of x: within f32 rounding of the reference's f32 dot for
+// these logits.
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-__global__ __launch_bounds__(256) void bat_router(MoeArgs a) {
+constexpr int kRouterWaves = 8;
+__global__ __launch_bounds__(512) void bat_router(MoeArgs a) {
+  __shared__ float red[kRouterWaves][16][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, ncol = a.ne + a.has_sgate;
-  const int rt = blockIdx.x, ct = blockIdx.y * 4 + wave;  // 32-row tile, 32-column tile
-  if (ct * 32 >= ncol) return;
+  const int rt = blockIdx.x, ct = blockIdx.y;  // 32-row tile, 32-column tile
   const int m = lane & 31, h = lane >> 5;
   const int row = min(rt * 32 + m, a.R - 1), col = min(ct * 32 + m, ncol - 1);
-  const float *xp = a.x + (uint64_t)row * a.hid + 8 * h;
-  const uint16_t *wp = a.router + (uint64_t)col * a.hid + 8 * h;
+  const int kn = a.hid / kRouterWaves, kb = wave * kn;  // this wave's k range (a multiple of 32 long)
+  const float *xp = a.x + (uint64_t)row * a.hid + kb + 8 * h;
+  const uint16_t *wp = a.router + (uint64_t)col * a.hid + kb + 8 * h;
   f32x16 acc;
 #pragma unroll
   for (int i = 0; i < 16; i++) acc[i] = 0.f;
-  constexpr int U = 8;  // k steps per batch of loads
-  for (int k0 = 0; k0 < a.hid; k0 += 16 * U) {
+  constexpr int U = 4;  // k steps per batch of loads
+  for (int k0 = 0; k0 < kn; k0 += 16 * U) {
     float4 xv[U][2];
     uint4 wv[U];
 #pragma unroll
     for (int u = 0; u < U; u++) {
       const int k = k0 + 16 * u;
-      if (k < a.hid) {
+      if (k < kn) {
         xv[u][0] = *(const float4 *)(xp + k);
         xv[u][1] = *(const float4 *)(xp + k + 4);
         wv[u] = *(const uint4 *)(wp + k);
@@ -111,7 +115,7 @@ __global__ __launch_bounds__(256) void bat_router(MoeArgs a) {
     }
 #pragma unroll
     for (int u = 0; u < U; u++) {
-      if (k0 + 16 * u < a.hid) {
+      if (k0 + 16 * u < kn) {
         const float xs[8] = {xv[u][0].x, xv[u][0].y, xv[u][0].z, xv[u][0].w,
                              xv[u][1].x, xv[u][1].y, xv[u][1].z, xv[u][1].w};
         bf16x8 hi, lo;
@@ -127,9 +131,15 @@ __global__ __launch_bounds__(256) void bat_router(MoeArgs a) {
     }
   }
 #pragma unroll
-  for (int i = 0; i < 16; i++) {
-    const int r = rt * 32 + 4 * h + (i & 3) + 8 * (i >> 2), c = ct * 32 + m;
-    if (r < a.R && c < ncol) a.logits[(uint64_t)r * (a.ne + 1) + c] = bf16_round(acc[i]);
+  for (int i = 0; i < 16; i++) red[wave][i][lane] = acc[i];
+  __syncthreads();
+  for (int o = threadIdx.x; o < 16 * 64; o += kRouterWaves * 64) {
+    const int i = o >> 6, l = o & 63;
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < kRouterWaves; w++) v += red[w][i][l];
+    const int r = rt * 32 + 4 * (l >> 5) + (i & 3) + 8 * (i >> 2), c = ct * 32 + (l & 31);
+    if (r < a.R && c < ncol) a.logits[(uint64_t)r * (a.ne + 1) + c] = bf16_round(v);
   }
 }
 
@@ -254,16 +264,33 @@ __global__ __launch_bounds__(256) void bat_prep(MoeArgs a, const uint32_t *rows,
   const uint16_t *suu = (const uint16_t *)(expert_block(a, e) + su_of(a, e, 1));
   const float *x = a.x + (uint64_t)r * a.hid;
   uint16_t *out = xh + (uint64_t)row * 2 * a.hid;
-  for (int c = wave; c < a.hid / 128; c += 4) {
-    const int e0 = c * 128 + lane, e1 = e0 + 64;
-    const float x0 = x[e0], x1 = x[e1];
-    float g0 = x0 * h2f(sug[e0]), g1 = x1 * h2f(sug[e1]), u0 = x0 * h2f(suu[e0]), u1 = x1 * h2f(suu[e1]);
-    fwht2(g0, g1, lane, a.had_hid, a.sc_hid);
-    fwht2(u0, u1, lane, a.had_hid, a.sc_hid);
-    out[c * 128 + kp(lane)] = f2h(g0);
-    out[c * 128 + kp(lane + 64)] = f2h(g1);
-    out[a.hid + c * 128 + kp(lane)] = f2h(u0);
-    out[a.hid + c * 128 + kp(lane + 64)] = f2h(u1);
+  constexpr int U = 4;  // blocks per wave whose loads are all issued before the first store
+  for (int c0 = wave; c0 < a.hid / 128; c0 += 4 * U) {
+    float g[U][2], u[U][2];
+#pragma unroll
+    for (int j = 0; j < U; j++) {
+      const int c = c0 + 4 * j;
+      if (c < a.hid / 128) {
+        const int e0 = c * 128 + lane, e1 = e0 + 64;
+        const float x0 = x[e0], x1 = x[e1];
+        g[j][0] = x0 * h2f(sug[e0]);
+        g[j][1] = x1 * h2f(sug[e1]);
+        u[j][0] = x0 * h2f(suu[e0]);
+        u[j][1] = x1 * h2f(suu[e1]);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < U; j++) {
+      const int c = c0 + 4 * j;
+      if (c < a.hid / 128) {
+        fwht2(g[j][0], g[j][1], lane, a.had_hid, a.sc_hid);
+        fwht2(u[j][0], u[j][1], lane, a.had_hid, a.sc_hid);
+        out[c * 128 + kp(lane)] = f2h(g[j][0]);
+        out[c * 128 + kp(lane + 64)] = f2h(g[j][1]);
+        out[a.hid + c * 128 + kp(lane)] = f2h(u[j][0]);
+        out[a.hid + c * 128 + kp(lane + 64)] = f2h(u[j][1]);
+      }
+    }
   }
 }
 
@@ -572,12 +599,18 @@ __global__ __launch_bounds__(512, 4) void bat_down(MoeArgs a, const uint32_t *bk
 }
 
 // y[r] = sum over the row's slots in slot order (routed k = 0..topk-1, then the shared expert)
-__global__ __launch_bounds__(256) void bat_combine(MoeArgs a, const float *dnw) {
-  const int r = blockIdx.x, i = blockIdx.y * 256 + threadIdx.x;
+__global__ __launch_bounds__(256) void bat_combine(MoeArgs a, const float *__restrict__ dnw) {
+  const int r = blockIdx.x, i = (blockIdx.y * 256 + threadIdx.x) * 4;
   if (i >= a.hid) return;
-  float y = 0.f;
-  for (int k = 0; k < a.nslot; k++) y += dnw[((uint64_t)r * a.nslot + k) * a.hid + i];
-  a.y[(uint64_t)r * a.hid + i] = y;
+  float4 y = {0.f, 0.f, 0.f, 0.f};
+  for (int k = 0; k < a.nslot; k++) {
+    const float4 v = *(const float4 *)(dnw + ((uint64_t)r * a.nslot + k) * a.hid + i);
+    y.x += v.x;
+    y.y += v.y;
+    y.z += v.z;
+    y.w += v.w;
+  }
+  *(float4 *)(a.y + (uint64_t)r * a.hid + i) = y;
 }
 
 // ---------------------------------------------------------------------------------------------------- host side
@@ -610,7 +643,7 @@ int moe_batch_max_chunks(int R, int ne, int topk, bool shared) {
 void launch_moe_batch(const MoeArgs &a, const MoeBatchBufs &b, hipStream_t s) {
   const int ncol = a.ne + a.has_sgate, S = a.R * a.nslot;
   hipLaunchKernelGGL(bat_zero, dim3(1), dim3(1024), 0, s, b.bk, a.ne + 1);  // a kernel, not a memset node
-  hipLaunchKernelGGL(bat_router, dim3((a.R + 31) / 32, (ncol + 127) / 128), dim3(256), 0, s, a);
+  hipLaunchKernelGGL(bat_router, dim3((a.R + 31) / 32, (ncol + 31) / 32), dim3(64 * kRouterWaves), 0, s, a);
   hipLaunchKernelGGL(bat_route, dim3((a.R + 3) / 4), dim3(256), 0, s, a, b.bk);
   hipLaunchKernelGGL(bat_scan, dim3(1), dim3(1024), 0, s, a, b.bk, b.chunks, b.max_chunks);
   hipLaunchKernelGGL(bat_place, dim3((S + 255) / 256), dim3(256), 0, s, a, b.bk, b.rows);
@@ -625,7 +658,7 @@ void launch_moe_batch(const MoeArgs &a, const MoeBatchBufs &b, hipStream_t s) {
   IJ_BAT(4, 4) IJ_BAT(5, 5) IJ_BAT(6, 6) IJ_BAT(4, 5) IJ_BAT(4, 6) IJ_BAT(5, 6) IJ_BAT(5, 4) IJ_BAT(6, 4) IJ_BAT(6, 5)
 #undef IJ_BAT
   IJ_CHECK(done, "batched MoE: K%d / shared K%d not instantiated", a.lay.K, KS);
-  hipLaunchKernelGGL(bat_combine, dim3(a.R, (a.hid + 255) / 256), dim3(256), 0, s, a, b.dnw);
+  hipLaunchKernelGGL(bat_combine, dim3(a.R, (a.hid + 1023) / 1024), dim3(256), 0, s, a, b.dnw);
 }
 
 }  // namespace ijah
