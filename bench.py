@@ -102,9 +102,41 @@ def measure_batch(eng, R, n_layers, steps, seed):
            "tokens_per_s_per_layer": round(R * 1e6 / us, 1),
            "weight_bytes_per_layer": int(byts), "weight_GBps": round(byts / (us * 1e-6) / 1e9, 1),
            "expert_gemm_TFLOPs": round(fl / (us * 1e-6) / 1e12, 2),
-           "pct_bf16_mfma_peak": round(100 * fl / (us * 1e-6) / 2.5e15, 2)}
+           "pct_f16_mfma_peak": round(100 * fl / (us * 1e-6) / 2.5e15, 2)}
     for m in layers:
         m.free()
+    return out
+
+
+TRUNK = [("q", 2048, 4096, 6), ("k", 2048, 512, 6), ("v", 2048, 512, 6), ("o", 4096, 2048, 6),
+         ("lm_head", 2048, 151936, 8)]
+
+
+def measure_trunk(eng, R, steps, seed, min_bytes=300e6):
+    """the trunk linears at R rows, each shape timed over a graph of distinct copies whose
+    weights total >= min_bytes (beyond the 256 MB last-level cache, so every replay streams from HBM). Returns
+    {name: {us, bytes, GBps, pct_hbm_peak}} plus the q+k+v+o sum."""
+    from ijah_amd import synth
+    out = {}
+    x = synth.bf16_values(np.random.default_rng(seed), R, 4096)
+    xb = eng.from_numpy(x)
+    for name, inp, o, K in TRUNK:
+        rng = np.random.default_rng(seed + inp + o + K)
+        t, su, sv = synth.linear(rng, inp, o, K)
+        nbytes = t.nbytes + su.nbytes + sv.nbytes
+        copies = int(min(64, max(2, np.ceil(min_bytes / nbytes))))
+        lins = [eng.exl3_linear(t, su, sv) for _ in range(copies)]
+        del t
+        us = eng.lin_time(lins, R, xb, warmup=2, reps=max(3, steps))
+        for m in lins:
+            m.free()
+        gbs = nbytes / (us * 1e-6) / 1e9
+        out[name] = {"in": inp, "out": o, "K": K, "us": round(us, 3), "bytes": int(nbytes), "GBps": round(gbs, 1),
+                     "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2)}
+        print(f"trunk {name} R={R}: {out[name]}", file=sys.stderr, flush=True)
+    qkvo = sum(out[n]["us"] for n in ("q", "k", "v", "o"))
+    qkvo_b = sum(out[n]["bytes"] for n in ("q", "k", "v", "o"))
+    out["qkvo_sum"] = {"us": round(qkvo, 3), "GBps": round(qkvo_b / (qkvo * 1e-6) / 1e9, 1)}
     return out
 
 
@@ -119,6 +151,10 @@ def main():
     ap.add_argument("--no-batch", action="store_true", help="skip the verify (R=16) and prefill (R=4096) lines")
     ap.add_argument("--eager-only", action="store_true",
                     help="run the layer chain eagerly --steps times and exit (for rocprofv3 --pmc passes)")
+    ap.add_argument("--no-trunk", action="store_true", help="skip the trunk (config 3) lines")
+    ap.add_argument("--trunk-only", action="store_true", help="only measure the trunk linears (config 3) and exit")
+    ap.add_argument("--batch-rows", type=int, default=0, metavar="R",
+                    help="only measure the grouped matrix-core layer at R rows (a 4-layer graph) and exit")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MB",
                     help="only run the plain copy kernel over MB MiB 5 times (scales --pmc byte counters) and exit")
     a = ap.parse_args()
@@ -135,6 +171,12 @@ def main():
         for _ in range(5):
             eng.run_kernel("copy_u128", [src, dst, np.uint64(n // 16)], (2048, 1, 1), (256, 1, 1))
         print(json.dumps({"copy_probe_bytes": n, "launches": 5}), flush=True)
+        return
+    if a.trunk_only:
+        print(json.dumps(measure_trunk(eng, 1, a.steps, a.seed)), flush=True)
+        return
+    if a.batch_rows:
+        print(json.dumps(measure_batch(eng, a.batch_rows, 4, a.steps, a.seed + a.batch_rows)), flush=True)
         return
     t_setup = time.perf_counter()
     layers = [eng.moe_synth(HID, INTER, NE, TOPK, K, True, K, seed=a.seed * 1000 + i) for i in range(a.layers)]
@@ -183,6 +225,8 @@ def main():
         print(f"verify R=16: {extra['verify_r16']}", file=sys.stderr, flush=True)
         extra["prefill_r4096"] = measure_batch(eng, 4096, 4, 3, a.seed + 4096)
         print(f"prefill R=4096: {extra['prefill_r4096']}", file=sys.stderr, flush=True)
+    if not a.no_trunk:
+        extra["trunk_m1"] = measure_trunk(eng, 1, max(5, a.steps // 5), a.seed + 3)
     cpu = None if a.no_cpu else cpu_baseline()
     line = {
         "metric": "MoE layer us + effective packed-weight GB/s (% HBM peak), 5-bit EXL3, M=1",

@@ -143,6 +143,27 @@ __device__ __forceinline__ TileWords load_tile(const uint32_t *__restrict__ T, c
   return w;
 }
 
+// ------------------------------------------------------------------------------------------------ matrix cores
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+// The matrix-core B operand of lane l is column n = l % 32 of the pair (tile n / 16, column c = n % 16), k values
+// 8 (l / 32) .. + 8: the trellis groups (c, q) with q = 2 (l / 32) and q + 1, four consecutive k each. Group m of a
+// tile (weights 4m .. 4m + 3 of the bitstream) holds column c = (m >> 3) + 8 (m & 1), k quarter q = (m >> 1) & 3.
+__device__ __forceinline__ uint32_t group_of(uint32_t c, uint32_t q) { return ((c & 7u) << 3) | (q << 1) | (c >> 3); }
+template <int K>
+struct BLane {
+  TileLane<K> g0, g1;  // the lane's two groups
+  uint32_t tile;       // 0 or 1: which tile of the pair
+};
+template <int K>
+__device__ __forceinline__ BLane<K> b_lane(uint32_t lane) {
+  const uint32_t n = lane & 31u, q = 2u * (lane >> 5);
+  BLane<K> b;
+  b.g0 = tile_lane<K>(group_of(n & 15u, q));
+  b.g1 = tile_lane<K>(group_of(n & 15u, q + 1u));
+  b.tile = n >> 4;
+  return b;
+}
 // MCG window-15 codebook (reference kernels/ne_common.h:139-144): r = cw * 0xCBAC1FED mod 2^32, masked, xored;
 // value = fp16(r_lo) + fp16(r_hi) rounded once (RNE), as the reference's half + half.
 // The 32-bit multiply is quarter rate on CDNA; cw < 2^15 lets two full-rate 24-bit multiplies form it:

@@ -55,8 +55,8 @@ struct ne_exl3_lin {
   int in = 0, out = 0, K = 0, IT = 0, OT = 0, OTp = 0, had_in = 0, had_out = 0;
   uint32_t *tiles = nullptr;
   uint16_t *suh = nullptr, *svh = nullptr;
-  uint16_t *xh = nullptr;  // [8][in]
-  float *part = nullptr;   // [S][8][OTp*16]
+  uint16_t *xh = nullptr;  // [kLinMaxRows][in]
+  float *part = nullptr;   // [S][kLinMaxRows][OTp*16]
   int part_S = 0;
   ~ne_exl3_lin() {
     dev_free(tiles);
@@ -70,6 +70,10 @@ struct ne_exl3_lin {
   int splits(int R) const {
     const int NP = OTp / 2;
     int S = 1;
+    if (R > kLinSimdRows) {  // matrix cores: one wave per (pair, split), >= 2048 waves, >= 8 k tiles per split
+      while (NP * S < 2048 && IT % (2 * S) == 0 && IT / (2 * S) >= 8) S *= 2;
+      return S;
+    }
     while (NP * S < 1024 && IT % (2 * S) == 0 && IT / (2 * S) >= 8) S *= 2;
     const int RT = R <= 1 ? 1 : R <= 2 ? 2 : R <= 4 ? 4 : 8;
     while ((size_t)RT * (IT / S) * 32 > 32768 && IT % (2 * S) == 0) S *= 2;
@@ -100,7 +104,7 @@ static ne_exl3_lin *lin_create(const uint16_t *trellis, const uint16_t *suh, con
   l->svh = dev_alloc<uint16_t>(out);
   IJ_HIP(hipMemcpy(l->suh, suh, 2u * in, hipMemcpyHostToDevice));
   IJ_HIP(hipMemcpy(l->svh, svh, 2u * out, hipMemcpyHostToDevice));
-  l->xh = dev_alloc<uint16_t>((size_t)8 * in);
+  l->xh = dev_alloc<uint16_t>((size_t)kLinMaxRows * in);
   return l.release();
 }
 
@@ -164,40 +168,95 @@ static void timed(hipStream_t s, double *gpu_ms, const std::function<void()> &wo
   (void)hipEventDestroy(e1);
 }
 
+}  // extern "C"
+
+// LinArgs of one run at R rows (the k-split scratch grown as needed)
+static LinArgs lin_args(ne_exl3_lin *l, int R, const float *x, float *y) {
+  const int S = l->splits(R);
+  if (S > l->part_S) {
+    dev_free(l->part);
+    l->part = dev_alloc<float>((size_t)S * kLinMaxRows * l->OTp * 16);
+    l->part_S = S;
+  }
+  LinArgs a;
+  a.tiles = l->tiles;
+  a.suh = l->suh;
+  a.svh = l->svh;
+  a.in = l->in;
+  a.out = l->out;
+  a.K = l->K;
+  a.IT = l->IT;
+  a.OT = l->OT;
+  a.had_in = l->had_in;
+  a.had_out = l->had_out;
+  a.sc_in = had_scale(l->had_in);
+  a.sc_out = had_scale(l->had_out);
+  a.R = R;
+  a.S = S;
+  a.x = x;
+  a.y = y;
+  a.xh = l->xh;
+  a.part = l->part;
+  return a;
+}
+
+extern "C" {
+
 NE_API int ne_exl3_lin_run(ne_exl3_lin *l, int R, const ne_buf *x, uint64_t x_off, ne_buf *y, uint64_t y_off,
                            double *gpu_ms) {
   return c_call([&] {
     IJ_CHECK(l && x && y, "null argument");
-    IJ_CHECK(R >= 1 && R <= 8, "rows %d (1..8)", R);
+    IJ_CHECK(R >= 1 && R <= kLinMaxRows, "rows %d (1..%d)", R, kLinMaxRows);
     IJ_CHECK(x_off % 4 == 0 && y_off % 4 == 0, "offsets must be 4-byte aligned");
     IJ_CHECK(x_off + (uint64_t)R * l->in * 4 <= x->size, "x buffer too small for [%d][%d] f32", R, l->in);
     IJ_CHECK(y_off + (uint64_t)R * l->out * 4 <= y->size, "y buffer too small for [%d][%d] f32", R, l->out);
-    const int S = l->splits(R);
-    if (S > l->part_S) {
-      dev_free(l->part);
-      l->part = dev_alloc<float>((size_t)S * 8 * l->OTp * 16);
-      l->part_S = S;
-    }
-    LinArgs a;
-    a.tiles = l->tiles;
-    a.suh = l->suh;
-    a.svh = l->svh;
-    a.in = l->in;
-    a.out = l->out;
-    a.K = l->K;
-    a.IT = l->IT;
-    a.OT = l->OT;
-    a.had_in = l->had_in;
-    a.had_out = l->had_out;
-    a.sc_in = had_scale(l->had_in);
-    a.sc_out = had_scale(l->had_out);
-    a.R = R;
-    a.S = S;
-    a.x = (const float *)((const char *)x->dev + x_off);
-    a.y = (float *)((char *)y->dev + y_off);
-    a.xh = l->xh;
-    a.part = l->part;
+    const LinArgs a = lin_args(l, R, (const float *)((const char *)x->dev + x_off), (float *)((char *)y->dev + y_off));
     timed(stream(), gpu_ms, [&] { launch_lin(a, stream()); });
+  });
+}
+
+NE_API int ne_exl3_lin_time(ne_exl3_lin *const *lins, int n, int R, const ne_buf *x, int warmup, int reps,
+                            double *us_per_lin) {
+  return c_call([&] {
+    IJ_CHECK(lins && n >= 1 && x && us_per_lin && reps >= 1 && R >= 1 && R <= kLinMaxRows, "bad arguments");
+    size_t ytot = 0;
+    for (int i = 0; i < n; i++) {
+      IJ_CHECK(lins[i], "null linear %d", i);
+      IJ_CHECK((uint64_t)R * lins[i]->in * 4 <= x->size, "x buffer too small for linear %d", i);
+      ytot += (size_t)R * lins[i]->out;
+    }
+    hipStream_t s = stream();
+    float *ys = dev_alloc<float>(ytot);
+    hipGraph_t g = nullptr;
+    hipGraphExec_t ge = nullptr;
+    auto cleanup = [&] {
+      if (ge) (void)hipGraphExecDestroy(ge);
+      if (g) (void)hipGraphDestroy(g);
+      dev_free(ys);
+    };
+    try {
+      std::vector<LinArgs> args;
+      size_t yo = 0;
+      for (int i = 0; i < n; i++) {
+        args.push_back(lin_args(lins[i], R, (const float *)x->dev, ys + yo));
+        yo += (size_t)R * lins[i]->out;
+      }
+      IJ_HIP(hipStreamSynchronize(s));
+      IJ_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+      for (const LinArgs &a : args) launch_lin(a, s);
+      IJ_HIP(hipStreamEndCapture(s, &g));
+      IJ_HIP(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0));
+      for (int i = 0; i < warmup; i++) IJ_HIP(hipGraphLaunch(ge, s));
+      double ms = 0;
+      timed(s, &ms, [&] {
+        for (int i = 0; i < reps; i++) IJ_HIP(hipGraphLaunch(ge, s));
+      });
+      *us_per_lin = ms * 1000.0 / ((double)reps * n);
+    } catch (...) {
+      cleanup();
+      throw;
+    }
+    cleanup();
   });
 }
 

@@ -111,6 +111,8 @@ struct LinArgs {
   uint16_t *xh;           // [R][in] prepared fp16 input (scratch)
   float *part;            // [S][R][OTp * 16] (scratch)
 };
+// rows up to kLinSimdRows take the VALU GEMV (lin_gemv), more rows (up to kLinMaxRows) the matrix cores (lin_mfma)
+constexpr int kLinSimdRows = 8, kLinMaxRows = 32;
 void launch_lin(const LinArgs &a, hipStream_t s);
 // W' fp16 bits [IT*16][OT*16] from re-laid tiles
 void launch_decode(const uint32_t *tiles, int IT, int OT, int K, uint16_t *w, hipStream_t s);

@@ -35,8 +35,6 @@ namespace ijah {
 
 namespace {
 
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kChunkRows = 128;   // rows of one GEMM chunk (4 matrix-core row blocks of 32)
 constexpr int kRowBlocks = kChunkRows / 32;
@@ -363,24 +361,6 @@ __device__ __forceinline__ void wait_step(int t, int NS) {
     wait_vm(after_step<OA, OB, DB>(t, NS));
 }
 
-// The matrix-core B operand of lane l is column n = l % 32 of the pair (tile n / 16, column c = n % 16), k values
-// 8 (l / 32) .. + 8: the trellis groups (c, q) with q = 2 (l / 32) and q + 1, four consecutive k each. Group m of a
-// tile (weights 4m .. 4m + 3 of the bitstream) holds column c = (m >> 3) + 8 (m & 1), k quarter q = (m >> 1) & 3.
-__device__ __forceinline__ uint32_t group_of(uint32_t c, uint32_t q) { return ((c & 7u) << 3) | (q << 1) | (c >> 3); }
-template <int K>
-struct BLane {
-  TileLane<K> g0, g1;  // the lane's two groups
-  uint32_t tile;       // 0 or 1: which tile of the pair
-};
-template <int K>
-__device__ __forceinline__ BLane<K> b_lane(uint32_t lane) {
-  const uint32_t n = lane & 31u, q = 2u * (lane >> 5);
-  BLane<K> b;
-  b.g0 = tile_lane<K>(group_of(n & 15u, q));
-  b.g1 = tile_lane<K>(group_of(n & 15u, q + 1u));
-  b.tile = n >> 4;
-  return b;
-}
 // decodes the lane's B operand for both k tiles of one step straight from the ring bytes src
 template <int K>
 __device__ __forceinline__ void decode_step(const uint8_t *src, const BLane<K> &B, f16x8 (&bf)[2]) {
@@ -406,6 +386,9 @@ __device__ __forceinline__ void decode_step(const uint8_t *src, const BLane<K> &
   }
 }
 
+// quarter swizzle of A row r: distinct 16-byte bank groups for rows r .. r + 7 (eight lanes of a 128-byte read phase)
+// and for rows r .. r + 15 (sixteen lanes of a 256-byte phase), rows aligned to 8
+__device__ __forceinline__ int a_swz(int r) { return ((r >> 1) ^ ((r >> 3) & 1)) & 3; }
 template <int K, int NA>
 __device__ void chunk_gemm(const uint16_t *A, int lda, int ahalf, int aidx, int nrows, const uint8_t *tr, int IT,
                            int pair, uint8_t *lds, f32x16 (&acc)[kRowBlocks], uint64_t *dbg) {
@@ -427,13 +410,17 @@ __device__ void chunk_gemm(const uint16_t *A, int lda, int ahalf, int aidx, int 
   for (int rb = 0; rb < kRowBlocks; rb++)
 #pragma unroll
     for (int i = 0; i < 16; i++) acc[rb][i] = 0.f;
-  // A(t): 16 rows of this wave per operand (row 16 w + lane / 4, 16-byte quarter lane % 4 of its 64 bytes)
+  // A(t): 16 rows of this wave per operand. Row r's 64 bytes (four 16-byte quarters q: k 8q .. 8q + 7) sit at
+  // r * 64 with quarter q in position q ^ a_swz(r), so that a read of one quarter of consecutive rows is free of bank
+  // conflicts. DMA lane l fills position l % 4 of row
+  // 16 w + l / 4.
   const int rr = min(wave * 16 + (lane >> 2), nrows - 1);
+  const int aq = (lane & 3) ^ a_swz(lane >> 2);
   auto issue_a = [&](int t) {
     const int slot = t % Io::RA;
 #pragma unroll
     for (int o = 0; o < NA; o++)
-      dma16(A + o * ahalf + (uint64_t)rr * lda + t * 32 + (lane & 3) * 8,
+      dma16(A + o * ahalf + (uint64_t)rr * lda + t * 32 + aq * 8,
             ring_a + slot * Io::AB + o * kChunkRows * 64 + wave * 1024);
   };
   // B(t): the wave's pair at k tiles 2t, 2t + 1 (contiguous)
@@ -461,15 +448,16 @@ __device__ void chunk_gemm(const uint16_t *A, int lda, int ahalf, int aidx, int 
   begin_step(0);
   for (int t = 0; t < NS; t++) {
     IJ_STAMP(t == 20, 0)
-    const uint8_t *at = ring_a + (t % Io::RA) * Io::AB + aidx * kChunkRows * 64 + (lane & 31) * 64 + (lane >> 5) * 16;
+    const uint8_t *at = ring_a + (t % Io::RA) * Io::AB + aidx * kChunkRows * 64 + (lane & 31) * 64;
+    const int q0 = ((lane >> 5) ^ a_swz(lane & 31)) * 16, q1 = ((2 + (lane >> 5)) ^ a_swz(lane & 31)) * 16;
     const f16x8 b0 = bf[0], b1 = bf[1];
 #pragma unroll
     for (int r2 = 0; r2 < kRowBlocks; r2 += 2) {  // two row blocks' A fragments in flight at a time
       f16x8 af[2][2];
 #pragma unroll
       for (int i = 0; i < 2; i++) {
-        af[i][0] = *(const f16x8 *)(at + (r2 + i) * 2048);
-        af[i][1] = *(const f16x8 *)(at + (r2 + i) * 2048 + 32);
+        af[i][0] = *(const f16x8 *)(at + (r2 + i) * 2048 + q0);
+        af[i][1] = *(const f16x8 *)(at + (r2 + i) * 2048 + q1);
       }
 #pragma unroll
       for (int i = 0; i < 2; i++) {

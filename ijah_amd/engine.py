@@ -94,6 +94,7 @@ SIGNATURES = {
     "ne_moe_info": (_i, [_vp] + [C.POINTER(_i)] * 6),
     "ne_moe_bytes": (_i, [_vp, _i, C.POINTER(_u64)]),
     "ne_moe_time": (_i, [C.POINTER(_vp), _i, _i, _vp, _i, _i, _dp]),
+    "ne_exl3_lin_time": (_i, [C.POINTER(_vp), _i, _i, _vp, _i, _i, _dp]),
     "ne_moe_time_kernels": (_i, [C.POINTER(_vp), _i, _i, _vp, _i, C.c_void_p, _dp, C.POINTER(_i)]),
 }
 
@@ -494,6 +495,13 @@ class Engine:
         arr = (C.c_void_p * len(layers))(*[m.ptr for m in layers])
         us = C.c_double(0)
         self._ok(self.lib.ne_moe_time(arr, len(layers), R, x.ptr, warmup, reps, C.byref(us)), "ne_moe_time")
+        return us.value
+
+    def lin_time(self, lins, R, x, warmup=3, reps=20):
+        """GPU microseconds per linear over a graph of the given linears at R rows (ne_exl3_lin_time)."""
+        arr = (C.c_void_p * len(lins))(*[m.ptr for m in lins])
+        us = C.c_double(0)
+        self._ok(self.lib.ne_exl3_lin_time(arr, len(lins), R, x.ptr, warmup, reps, C.byref(us)), "ne_exl3_lin_time")
         return us.value
 
     def moe_time_kernels(self, layers, R, x, reps=5):

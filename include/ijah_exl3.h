@@ -33,10 +33,15 @@ NE_API ne_exl3_lin *ne_exl3_lin_create(const uint16_t *trellis, const uint16_t *
                                        int out, int K);
 NE_API void ne_exl3_lin_free(ne_exl3_lin *l);
 NE_API int ne_exl3_lin_info(const ne_exl3_lin *l, int *in, int *out, int *K);
-/* reference kernels/trunk6/trunk6.mm:232-249 (t6::record, SIMD path R 1..8): x f32 [R][in] at x_off, y f32 [R][out]
- * at y_off; R 1..8. */
+/* reference kernels/trunk6/trunk6.mm:232-249 (t6::record: SIMD path R 1..8, matrix-op path t6_nax above that):
+ * x f32 [R][in] at x_off, y f32 [R][out] at y_off; R 1..32 (1..8 on the VALU GEMV, 9..32 on the matrix cores). */
 NE_API int ne_exl3_lin_run(ne_exl3_lin *l, int R, const ne_buf *x, uint64_t x_off, ne_buf *y, uint64_t y_off,
                            double *gpu_ms);
+/* n linears at R rows, all reading x (f32 [R][in_i]) and writing scratch outputs, captured once in a HIP graph and
+ * replayed reps times after warmup replays: us_per_lin = GPU time per linear (HIP events). Replaces the reference's
+ * differential timing of the trunk stages (kernels/trunk6/trunk6.mm:232-249 replays, core/bench.h:21-24). */
+NE_API int ne_exl3_lin_time(ne_exl3_lin *const *lins, int n, int R, const ne_buf *x, int warmup, int reps,
+                            double *us_per_lin);
 /* W' decoded on the GPU from the re-laid tiles: fp16 bits [in][out] into w (at least in*out*2 bytes). Replaces the
  * reference's decoded-weight check through exl3_codec.decode_inner (tests/trunk6/check_kernels.py:86). */
 NE_API int ne_exl3_lin_decode(ne_exl3_lin *l, ne_buf *w, double *gpu_ms);

@@ -62,6 +62,24 @@ def test_linear_trunk_shapes(eng, oracle, inp, out, K, R):
     assert rel(y, oracle.exl3_linear(x, t, su, sv, exact=True)) < 1e-2
 
 
+@pytest.mark.parametrize("inp,out,K,R", [(2048, 512, 5, 9), (2048, 512, 5, 16), (2048, 512, 5, 32),
+                                         (2048, 4096, 6, 16), (4096, 2048, 6, 16), (320, 640, 7, 12), (96, 48, 4, 12),
+                                         (2048, 1024, 8, 16)])
+def test_linear_matrix_cores(eng, oracle, inp, out, K, R):
+    """9..32 rows take the matrix-core kernel (lin_mfma): same tolerances as the GEMV rows."""
+    print(f"linear mfma {inp}x{out} K{K} R{R}", flush=True)
+    rng = np.random.default_rng(inp * 5 + out + K + R)
+    t, su, sv = synth.linear(rng, inp, out, K)
+    x = synth.bf16_values(rng, R, inp)
+    lin = eng.exl3_linear(t, su, sv)
+    y = lin.run(x)
+    assert rel(y, oracle.exl3_linear(x, t, su, sv)) < 5e-5
+    assert rel(y, oracle.exl3_linear(x, t, su, sv, exact=True)) < 1e-2
+    assert np.array_equal(y, lin.run(x))  # deterministic
+    y1 = lin.run(x[:1])  # the GEMV path on the first row agrees with the matrix-core row
+    assert rel(y1, y[:1]) < 5e-5
+
+
 def test_lm_head_k8_column_blocks(eng, oracle):
     """Config 3's lm_head 2048 -> 151936 at K8 (311 MB of trellis). H_out is block-diagonal over 128 columns, so
     any 128-column block of y equals the oracle run on that block's trellis columns alone."""
