@@ -57,6 +57,8 @@ struct ne_exl3_lin {
   uint16_t *suh = nullptr, *svh = nullptr;
   uint16_t *xh = nullptr;  // [kLinMaxRows][in]
   float *part = nullptr;   // [S][kLinMaxRows][OTp*16]
+  uint32_t *cnt = nullptr; // per 128-column output block (the one-launch path's completion counters)
+  bool one_launch = true;  // IJAH_LIN_PATH=staged at creation: prep, GEMV and finish as three launches
   int part_S = 0;
   ~ne_exl3_lin() {
     dev_free(tiles);
@@ -64,6 +66,7 @@ struct ne_exl3_lin {
     dev_free(svh);
     dev_free(xh);
     dev_free(part);
+    dev_free(cnt);
   }
   // k splits: smallest S (dividing IT, >= 8 k tiles per split) that gives >= 1024 workgroups, then enough to keep
   // the staged input within 32 KiB of LDS at R rows
@@ -105,6 +108,11 @@ static ne_exl3_lin *lin_create(const uint16_t *trellis, const uint16_t *suh, con
   IJ_HIP(hipMemcpy(l->suh, suh, 2u * in, hipMemcpyHostToDevice));
   IJ_HIP(hipMemcpy(l->svh, svh, 2u * out, hipMemcpyHostToDevice));
   l->xh = dev_alloc<uint16_t>((size_t)kLinMaxRows * in);
+  const size_t nc = (size_t)((out + 127) / 128) * kSyncStride;
+  l->cnt = dev_alloc<uint32_t>(nc);
+  IJ_HIP(hipMemset(l->cnt, 0, nc * 4));
+  const char *path = getenv("IJAH_LIN_PATH");
+  l->one_launch = !(path && std::string(path) == "staged");
   return l.release();
 }
 
@@ -197,6 +205,10 @@ static LinArgs lin_args(ne_exl3_lin *l, int R, const float *x, float *y) {
   a.y = y;
   a.xh = l->xh;
   a.part = l->part;
+  // one launch unless its per-workgroup input preparation (each workgroup prepares the 128-blocks of its own k span)
+  // adds up to more than ~8K block preparations (large outputs with few splits, e.g. a vocabulary head)
+  const long prep_blocks = (long)(l->OTp / 2) * S * ((l->IT / S * 16 + 127) / 128 + 1);
+  a.cnt = (l->one_launch && R <= kLinSimdRows && prep_blocks <= 8192) ? l->cnt : nullptr;
   return a;
 }
 

@@ -564,6 +564,104 @@ __global__ __launch_bounds__(256) void lin_gemv(LinArgs a) {
   }
 }
 
+// lin_step: the whole linear at R <= 8 rows in one launch (reference kernels/trunk6/trunk6.metal: t6_prep :68-85,
+// t6_simd, t6_finish :199-214). Grid and GEMV as lin_gemv. Each workgroup first requests its weights, then prepares
+// the fp16(H_in(x * suh)) input of its own k span in LDS (the 128-element blocks overlapping the span; workgroups of
+// other pairs redo the same few blocks), runs the pair GEMV and stores its partials coherently. The last workgroup to
+// store into a 128-column output block (a counter per block, reset to 0 by that workgroup for the next launch) sums
+// the block's splits in split order and applies H_out and svh.
+template <int K, int RT>
+__global__ __launch_bounds__(256) void lin_step(LinArgs a) {
+  extern __shared__ _Float16 xs[];
+  __shared__ float red[4 * 32 * RT];
+  __shared__ int flag;
+  const int NP = (a.OT + 1) / 2, OTp = 2 * NP;
+  const int p = blockIdx.x % NP, s = blockIdx.x / NP;
+  const int span = a.IT / a.S, k0 = s * span, k1 = k0 + span, n = span * 16;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const TileLane<K> L = tile_lane<K>((uint32_t)lane);
+  const uint32_t *pb = a.tiles + (uint64_t)p * a.IT * 2 * 8 * K;
+  PairBuf<K> buf;
+  pair_load<K>(buf, pb, L, k0 + wave, k1);
+  // prepared input of the span: block b covers elements [128 b, 128 b + 128), lanes hold (lane, lane + 64)
+  const int e0 = k0 * 16, e1 = k1 * 16, b0 = e0 / 128, nb = (e1 + 127) / 128 - b0;
+  for (int it = wave; it < RT * nb; it += 4) {
+    const int r = it / nb, b = b0 + it % nb;
+    const int i0 = b * 128 + lane, i1 = i0 + 64;
+    float v0 = 0.f, v1 = 0.f;
+    if (r < a.R) {
+      const float *x = a.x + (uint64_t)r * a.in;
+      v0 = i0 < a.in ? x[i0] * h2f(a.suh[i0]) : 0.f;
+      v1 = i1 < a.in ? x[i1] * h2f(a.suh[i1]) : 0.f;
+      fwht2(v0, v1, lane, a.had_in, a.sc_in);
+    }
+    const int j0 = (int)kp((uint32_t)i0), j1 = (int)kp((uint32_t)i1);  // kp keeps an element in its 16-block
+    if (j0 >= e0 && j0 < e1) xs[r * n + j0 - e0] = to_f16(v0);
+    if (j1 >= e0 && j1 < e1) xs[r * n + j1 - e0] = to_f16(v1);
+  }
+  __syncthreads();
+  const int q = (lane >> 1) & 3;
+  float acc0[RT], acc1[RT];
+#pragma unroll
+  for (int r = 0; r < RT; r++) acc0[r] = acc1[r] = 0.f;
+  for (int tk0 = k0 + wave; tk0 < k1; tk0 += 4 * kPrefetch) {
+    if (tk0 != k0 + wave) pair_load<K>(buf, pb, L, tk0, k1);
+#pragma unroll
+    for (int j = 0; j < kPrefetch; j++) {
+      const int tk = tk0 + 4 * j;
+      if (tk < k1) {
+        f16x2 a0, b0v, a1, b1v;
+        decode4<K>(buf.w[j][0], L.sh, a0, b0v);
+        decode4<K>(buf.w[j][1], L.sh, a1, b1v);
+#pragma unroll
+        for (int r = 0; r < RT; r++) {
+          const f16x4 xv = *(const f16x4 *)(xs + r * n + (tk - k0) * 16 + 4 * q);
+          acc0[r] = dot4(a0, b0v, xv, acc0[r]);
+          acc1[r] = dot4(a1, b1v, xv, acc1[r]);
+        }
+      }
+    }
+  }
+  const int col = (lane >> 3) + 8 * (lane & 1);
+#pragma unroll
+  for (int r = 0; r < RT; r++) {
+    float v0 = acc0[r], v1 = acc1[r];
+    v0 += __shfl_xor(v0, 2, 64);
+    v0 += __shfl_xor(v0, 4, 64);
+    v1 += __shfl_xor(v1, 2, 64);
+    v1 += __shfl_xor(v1, 4, 64);
+    if ((lane & 6) == 0) {
+      red[(r * 4 + wave) * 32 + col] = v0;
+      red[(r * 4 + wave) * 32 + 16 + col] = v1;
+    }
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < a.R * 32; i += blockDim.x) {
+    const int r = i / 32, t = i % 32;
+    const float v = (red[(r * 4 + 0) * 32 + t] + red[(r * 4 + 1) * 32 + t]) +
+                    (red[(r * 4 + 2) * 32 + t] + red[(r * 4 + 3) * 32 + t]);
+    st_cg(a.part + ((uint64_t)s * a.R + r) * OTp * 16 + p * 32 + t, v);
+  }
+  // completion of the 128-column output block cb (pairs 4 cb .. 4 cb + 3)
+  const int cb = p / 4, npb = min(4, NP - 4 * cb);
+  uint32_t *ctr = a.cnt + (uint64_t)cb * kSyncStride;
+  if (block_signal(ctr, &flag) != (uint32_t)(npb * a.S - 1)) return;
+  if (threadIdx.x == 0) st_cg(ctr, 0u);
+  for (int r = wave; r < a.R; r += 4) {
+    const int i0 = cb * 128 + lane, i1 = i0 + 64;
+    const bool m0 = i0 < a.out, m1 = i1 < a.out;
+    float v0 = 0.f, v1 = 0.f;
+    for (int ss = 0; ss < a.S; ss++) {
+      const float *pp = a.part + ((uint64_t)ss * a.R + r) * OTp * 16;
+      if (m0) v0 += ld_cg(pp + i0);
+      if (m1) v1 += ld_cg(pp + i1);
+    }
+    fwht2(v0, v1, lane, a.had_out, a.sc_out);
+    if (m0) a.y[(uint64_t)r * a.out + i0] = v0 * h2f(a.svh[i0]);
+    if (m1) a.y[(uint64_t)r * a.out + i1] = v1 * h2f(a.svh[i1]);
+  }
+}
+
 // lin_mfma: 9..32 rows on the matrix cores, the weights decoded straight into the B operand of
 // v_mfma_f32_32x32x16_f16 (reference kernels/trunk6/trunk6.metal:431-539, t6_nax). One wave per (tile pair p, k split
 // s), four waves per workgroup. A = rows of xh (fp16, kp order, L2-resident): lane l reads row l % 32, k 8 (l / 32)
@@ -742,6 +840,20 @@ static const void *lin_gemv_any(int K, int RT) {
   IJ_DISPATCH_K(K, f = lin_gemv_fn<KK>(RT));
   return f;
 }
+template <int K>
+static const void *lin_step_fn(int RT) {
+  switch (RT) {
+    case 1: return (const void *)&lin_step<K, 1>;
+    case 2: return (const void *)&lin_step<K, 2>;
+    case 4: return (const void *)&lin_step<K, 4>;
+    default: return (const void *)&lin_step<K, 8>;
+  }
+}
+static const void *lin_step_any(int K, int RT) {
+  const void *f = nullptr;
+  IJ_DISPATCH_K(K, f = lin_step_fn<KK>(RT));
+  return f;
+}
 static int rows_tier(int R) { return R <= 1 ? 1 : R <= 2 ? 2 : R <= 4 ? 4 : 8; }
 
 static const void *lin_mfma_any(int K) {
@@ -751,8 +863,8 @@ static const void *lin_mfma_any(int K) {
 }
 
 void launch_lin(const LinArgs &a, hipStream_t s) {
-  hipLaunchKernelGGL(lin_prep, dim3(a.R * ((a.in + 127) / 128)), dim3(64), 0, s, a);
   const int NP = (a.OT + 1) / 2;
+  if (a.R > kLinSimdRows || !a.cnt) hipLaunchKernelGGL(lin_prep, dim3(a.R * ((a.in + 127) / 128)), dim3(64), 0, s, a);
   if (a.R > kLinSimdRows) {
     void *args[] = {const_cast<LinArgs *>(&a)};
     IJ_HIP(hipLaunchKernel(lin_mfma_any(a.K), dim3((NP * a.S + 3) / 4), dim3(256), args, 0, s));
@@ -762,6 +874,10 @@ void launch_lin(const LinArgs &a, hipStream_t s) {
   const int RT = rows_tier(a.R);
   const size_t lds = (size_t)RT * (a.IT / a.S) * 16 * sizeof(uint16_t);
   void *args[] = {const_cast<LinArgs *>(&a)};
+  if (a.cnt) {  // one launch
+    IJ_HIP(hipLaunchKernel(lin_step_any(a.K, RT), dim3(NP * a.S), dim3(256), args, lds, s));
+    return;
+  }
   IJ_HIP(hipLaunchKernel(lin_gemv_any(a.K, RT), dim3(NP * a.S), dim3(256), args, lds, s));
   hipLaunchKernelGGL(lin_finish, dim3(a.R * ((a.out + 127) / 128)), dim3(64), 0, s, a);
 }
@@ -787,6 +903,7 @@ static std::vector<KernelEntry> build_registry() {
     v.push_back({"exl3_decode", decode_fn(K), {P, I, I, P}, K, -1});
     for (int RT : {1, 2, 4, 8}) v.push_back({"lin_gemv", lin_gemv_any(K, RT), {(uint32_t)sizeof(LinArgs)}, K, RT});
     v.push_back({"lin_mfma", lin_mfma_any(K), {(uint32_t)sizeof(LinArgs)}, K, -1});
+    for (int RT : {1, 2, 4, 8}) v.push_back({"lin_step", lin_step_any(K, RT), {(uint32_t)sizeof(LinArgs)}, K, RT});
   }
   v.push_back({"lin_prep", (const void *)&lin_prep, {(uint32_t)sizeof(LinArgs)}, -1, -1});
   v.push_back({"lin_finish", (const void *)&lin_finish, {(uint32_t)sizeof(LinArgs)}, -1, -1});

@@ -110,6 +110,8 @@ struct LinArgs {
   float *y;
   uint16_t *xh;           // [R][in] prepared fp16 input (scratch)
   float *part;            // [S][R][OTp * 16] (scratch)
+  uint32_t *cnt;          // per 128-column output block, kSyncStride apart, zero between launches; null: the staged
+                          // three-kernel path (prep, GEMV, finish)
 };
 // rows up to kLinSimdRows take the VALU GEMV (lin_gemv), more rows (up to kLinMaxRows) the matrix cores (lin_mfma)
 constexpr int kLinSimdRows = 8, kLinMaxRows = 32;

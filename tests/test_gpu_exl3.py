@@ -80,6 +80,23 @@ def test_linear_matrix_cores(eng, oracle, inp, out, K, R):
     assert rel(y1, y[:1]) < 5e-5
 
 
+@pytest.mark.parametrize("inp,out,K,R", [(2048, 512, 5, 1), (2048, 4096, 6, 3), (320, 640, 7, 8), (96, 48, 4, 2)])
+def test_linear_one_launch_matches_staged(eng, oracle, inp, out, K, R, monkeypatch):
+    """The one-launch linear (in-workgroup prep, last-arriver finish) against the three-launch path: bit-identical
+    (same per-element arithmetic and split order), over repeated runs (the block counters reset themselves)."""
+    print(f"linear one-launch vs staged {inp}x{out} K{K} R{R}", flush=True)
+    rng = np.random.default_rng(inp + out + K + R)
+    t, su, sv = synth.linear(rng, inp, out, K)
+    x = synth.bf16_values(rng, R, inp)
+    one = eng.exl3_linear(t, su, sv)
+    monkeypatch.setenv("IJAH_LIN_PATH", "staged")
+    staged = eng.exl3_linear(t, su, sv)
+    want = staged.run(x)
+    for _ in range(3):
+        assert np.array_equal(one.run(x), want)
+    assert rel(want, oracle.exl3_linear(x, t, su, sv)) < 5e-5
+
+
 def test_lm_head_k8_column_blocks(eng, oracle):
     """Config 3's lm_head 2048 -> 151936 at K8 (311 MB of trellis). H_out is block-diagonal over 128 columns, so
     any 128-column block of y equals the oracle run on that block's trellis columns alone."""
