@@ -38,7 +38,7 @@ constexpr int kCtl = kWaves - 1;
 constexpr int kMaxGu = 12;                 // gate/up k tiles per wave (its LDS area)
 constexpr int kMaxDn = 8;                  // down k tiles per wave (held decoded in registers)
 constexpr int kMaxSeg = 16;                // partial sums per column
-constexpr int kPrepHalves = 2 * 3 * 128;   // two segments of up to three 128-chunks of prepared input
+constexpr int kMaxPrep = 8;                 // prepared 128-chunks of input per workgroup (shared by its waves)
 constexpr int kMaxExpertsV = 1024;
 constexpr int kMaxTopkV = 32;
 constexpr uint32_t kSpin = 1u << 22;       // bounded waits: polls of ~0.1-1 us each, far beyond any real wait
@@ -377,7 +377,9 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
                 NBLK = HID / 128, HH = had_of(HID), HI = had_of(INTER);
   constexpr uint32_t GUB = kMaxGu * 64 * KM, AREA = GUB + kMaxDn * 64 * KM;  // a wave's gate/up + down tile bytes
   extern __shared__ __attribute__((aligned(16))) uint8_t tiles[];  // kWaves x AREA
-  __shared__ _Float16 prep[kWaves][kPrepHalves];  // per segment: suh chunks (DMA), then fp16(H(x suh)) in place
+  // the workgroup's prepared input chunks (suh by DMA, then fp16(H(x suh)) in place); later the slot's down input
+  constexpr int PW = kMaxPrep * 128 > INTER ? kMaxPrep * 128 : INTER;
+  __shared__ __attribute__((aligned(16))) _Float16 prepw[PW];
   __shared__ __attribute__((aligned(16))) float xl[HID];  // the input row
   __shared__ Route rt;
   __shared__ uint32_t s_tag, s_ok, s_ep, ids[2 * kWaves];
@@ -385,10 +387,19 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, G = (int)gridDim.x;
   const int NW = G * kWaves, CG = a.nslot * 2 * NPg;
   const uint32_t *plan = a.units;
-  uint2 pw = *(const uint2 *)(plan + 2 * (blockIdx.x * kWaves + wave));  // gate/up segments s0, s1
+  // per wave: gate/up segments s0, s1 and the index of each one's first chunk in the workgroup's prepared input;
+  // per workgroup: the count of its prepared chunks and each one's (matrix << 8 | chunk)
+  const uint32_t *pwp = plan + 3 * (blockIdx.x * kWaves + wave);
+  const uint32_t *wpl = plan + 3 * NW + blockIdx.x * (1 + kMaxPrep);
+  uint2 pw = *(const uint2 *)pwp;
+  uint32_t pidx = pwp[2], np = wpl[0], pe = wpl[1 + (wave < kMaxPrep ? wave : 0)];
   pw.x = __builtin_amdgcn_readfirstlane(pw.x);  // wave-uniform: scalar registers and branches
   pw.y = __builtin_amdgcn_readfirstlane(pw.y);
-  const uint32_t *gu_nseg = plan + 2 * NW, *fin_tgt = gu_nseg + CG;
+  pidx = __builtin_amdgcn_readfirstlane(pidx);
+  np = __builtin_amdgcn_readfirstlane(np);
+  pe = __builtin_amdgcn_readfirstlane(pe);
+  const bool preps = wave < (int)np;  // this wave prepares chunk `wave` of the workgroup's list
+  const uint32_t *gu_nseg = plan + 3 * NW + G * (1 + kMaxPrep), *fin_tgt = gu_nseg + CG;
   uint32_t *sync = a.sync;
   uint32_t *fin_cnt = a.fsync + kSyncStride;                  // [ls * NBI + cb]: gate/up partials of a block
   uint32_t *blk_cnt = fin_cnt + a.nslot * NBI * kSyncStride;  // [c]: slots stored of output block c
@@ -439,9 +450,9 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
   mark(a, 2);
   const bool ok = s_ok != 0;
 
-  // ---- 3. gate/up. Requests, in order: each segment's suh chunks (into its prep area), its gate/up tiles (unless
-  // already requested), the down tiles. Then waits step by step: suh -> prep; each 1 KB of gate/up tiles -> the k
-  // tiles it completes.
+  // ---- 3. gate/up. Requests, in order: the suh of the chunk the wave prepares (waves below the workgroup's chunk
+  // count), its gate/up tiles (unless already requested), the down tiles. Then: suh -> the prepared chunk -> a
+  // barrier; each 1 KB of gate/up tiles -> the k tiles it completes.
   // down: workgroup b < nslot * NBLK owns slot ls_d's 128-column output block bd; wave w takes pair 4 bd + w / 4,
   // k quarter w % 4 (QK k tiles)
   constexpr int QK = ITd / 4;
@@ -450,43 +461,27 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
   const uint32_t gb0 = g0.n ? (uint32_t)g0.n * 2 * tbytes(gu_ls(g0)) : 0u, gb1 = g1.n ? (uint32_t)g1.n * 2 * tbytes(gu_ls(g1)) : 0u;
   const int n_g0 = (ok && !pre0) ? dma_ops(gb0) : 0, n_g1 = (ok && !pre1) ? dma_ops(gb1) : 0;
   const int n_dn = has_dn ? dma_ops((uint32_t)QK * 2 * tbytes(ls_d)) : 0;
-  auto issue_suh = [&](const Seg &s, _Float16 *dst) {
-    const int ls = gu_ls(s), c0 = s.k0 / 8, c1 = (s.k0 + s.n - 1) / 8;
-    const uint8_t *src = slot_block(a, rt, ls) + su_off(a, ls, gu_proj(s)) + c0 * 256;
-    const uint32_t bytes = (uint32_t)(c1 - c0 + 1) * 256;  // <= 768: one request
-    if ((uint32_t)lane * 16 < bytes)
-      __builtin_amdgcn_global_load_lds((const void *)(src + lane * 16), (__attribute__((address_space(3))) void *)dst,
-                                       16, 0, 0);
-  };
-  if (ok && g0.n) issue_suh(g0, prep[wave]);
-  if (ok && g1.n) issue_suh(g1, prep[wave] + 384);
+  const int pm = (int)(pe >> 8), pc = (int)(pe & 0xFFu);  // the chunk this wave prepares: matrix, 128-chunk
+  if (ok && preps && lane < 16) {  // its suh chunk (256 bytes)
+    const uint8_t *src = slot_block(a, rt, pm >> 1) + su_off(a, pm >> 1, pm & 1) + pc * 256;
+    __builtin_amdgcn_global_load_lds((const void *)(src + lane * 16),
+                                     (__attribute__((address_space(3))) void *)(prepw + wave * 128), 16, 0, 0);
+  }
   if (ok && g0.n && !pre0) issue_gu(g0, 0);
   if (ok && g1.n && !pre1) issue_gu(g1, off1);
   if (has_dn) stream_tiles(slot_block(a, rt, ls_d) + tr_off(a, ls_d, 2), ITd, dpair, dq * QK, QK, tbytes(ls_d), area + GUB);
-  // fp16(H(x * suh)) of each 128-chunk of the segment, in kp order, over its suh chunks
-  auto prep_seg = [&](const Seg &s, _Float16 *dst) {
-    const int c0 = s.k0 / 8, nc = (s.k0 + s.n - 1) / 8 - c0 + 1;
-    float su[3][2];
-#pragma unroll
-    for (int c = 0; c < 3; c++)
-      if (c < nc) {
-        su[c][0] = (float)dst[c * 128 + lane];
-        su[c][1] = (float)dst[c * 128 + lane + 64];
-      }
-#pragma unroll
-    for (int c = 0; c < 3; c++)
-      if (c < nc) {
-        float v0 = xl[(c0 + c) * 128 + lane] * su[c][0], v1 = xl[(c0 + c) * 128 + lane + 64] * su[c][1];
-        fwht2(v0, v1, lane, HH, sch);
-        dst[c * 128 + kp(lane)] = to_f16(v0);
-        dst[c * 128 + kp(lane + 64)] = to_f16(v1);
-      }
-  };
   if (a.trace && lane == 0) a.trace[(uint64_t)(512 + blockIdx.x * kWaves + wave) * 8 + 3] = wall_clock64();
-  wait_vm(n_g0 + n_g1 + n_dn);  // suh chunks are in
+  if (ok && preps) {  // fp16(H(x * suh)) of the chunk, in kp order, in place of its suh
+    wait_vm(n_g0 + n_g1 + n_dn);  // the suh chunk is in
+    _Float16 *dst = prepw + wave * 128;
+    const float s0 = (float)dst[lane], s1 = (float)dst[lane + 64];
+    float v0 = xl[pc * 128 + lane] * s0, v1 = xl[pc * 128 + lane + 64] * s1;
+    fwht2(v0, v1, lane, HH, sch);
+    dst[kp(lane)] = to_f16(v0);
+    dst[kp(lane + 64)] = to_f16(v1);
+  }
+  lds_barrier();  // every chunk of the workgroup is prepared
   if (a.trace && lane == 0) a.trace[(uint64_t)(512 + blockIdx.x * kWaves + wave) * 8 + 4] = wall_clock64();
-  if (ok && g0.n) prep_seg(g0, prep[wave]);
-  if (ok && g1.n) prep_seg(g1, prep[wave] + 384);
   mark(a, 3);
   // a segment's dot, k tiles taken as each 1 KB request lands (n_after: requests issued after the segment's; stores
   // come only after both segments, so they are never counted as "after": a wait may be stricter, never looser)
@@ -520,8 +515,8 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
     }
   };
   float ga0 = 0.f, ga1 = 0.f, gb0s = 0.f, gb1s = 0.f;
-  if (ok && g0.n) gu_dot(g0, 0, prep[wave], n_g0, n_g1 + n_dn, ga0, ga1);
-  if (ok && g1.n) gu_dot(g1, off1, prep[wave] + 384, n_g1, n_dn, gb0s, gb1s);
+  if (ok && g0.n) gu_dot(g0, 0, prepw + (pidx & 0xFu) * 128, n_g0, n_g1 + n_dn, ga0, ga1);
+  if (ok && g1.n) gu_dot(g1, off1, prepw + ((pidx >> 4) & 0xFu) * 128, n_g1, n_dn, gb0s, gb1s);
   if (a.trace && lane == 0) a.trace[(uint64_t)(512 + blockIdx.x * kWaves + wave) * 8 + 2] = wall_clock64();
   if (ok && g0.n) gu_store(g0, ga0, ga1);
   if (ok && g1.n) gu_store(g1, gb0s, gb1s);
@@ -546,7 +541,7 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
     else decode_pairs<K>(area + GUB, 0, QK, dw);
   }
   mark(a, 5);
-  _Float16 *hl = prep[0];  // the slot's down input, INTER halves (the prep areas are no longer read)
+  _Float16 *hl = prepw;  // the slot's down input, INTER halves (the prepared chunks are no longer read)
   if (has_dn && wave < NBI) {
     const int cb = wave, ls = ls_d, id = ls * NBI + cb;
     bool got = false;
@@ -713,31 +708,63 @@ int moe_fused_grid() {
   return cus;
 }
 
+// Gate/up work plan. The 2 nslot gate/up matrices (m = 2 ls + proj, NPg tile-pair columns x IT k tiles each) are
+// cut by k rows: workgroup b takes an equal run of the nslot * 2 * IT (matrix, k tile) rows, all NPg columns of
+// them. Its kWaves / NPg waves per column split the run's k range; a run that crosses into the next matrix gives each
+// wave a second segment. So a workgroup needs the prepared input of only the 128-chunks its k rows cover (one or two
+// per matrix), which it computes once and shares in LDS.
 MoePlan moe_fused_plan(int hid, int inter, int topk, int nslot, int G) {
   MoePlan pl;
-  const int NW = G * kWaves, IT = hid / 16, ITd = inter / 16, NPg = inter / 32, NBI = inter / 128, NBLK = hid / 128;
-  const int CG = nslot * 2 * NPg;
-  const long TG = (long)CG * IT;
-  // per-wave gate/up slice: even split, at least so long that a column has at most kMaxSeg segments
-  const int wg = (int)std::max<long>((TG + NW - 1) / NW, (IT + kMaxSeg - 2) / (kMaxSeg - 1));
-  // down: one (slot, 128-column block) per workgroup, a k quarter of one tile pair per wave
-  pl.ok = wg <= kMaxGu && wg <= IT && CG < 4096 && IT < 256 && ITd % 4 == 0 && ITd / 4 <= kMaxDn &&
-          nslot * NBLK <= G;
+  const int IT = hid / 16, ITd = inter / 16, NPg = inter / 32, NBI = inter / 128, NBLK = hid / 128;
+  const int NW = G * kWaves, CG = nslot * 2 * NPg, NM = nslot * 2;
+  const long TR = (long)NM * IT;  // k rows
+  const int W = NPg > 0 && kWaves % NPg == 0 ? kWaves / NPg : 0;  // waves per column
+  const long rows = (TR + G - 1) / G;
+  pl.ok = W > 0 && rows <= IT && (rows + W - 1) / W <= kMaxGu && CG < 4096 && IT < 256 && ITd % 4 == 0 &&
+          ITd / 4 <= kMaxDn && nslot * NBLK <= G;
   if (!pl.ok) return pl;
-  std::vector<uint32_t> slices((size_t)NW * 2, 0u), gnseg(CG, 0u);
-  for (int g = 0; g < NW; g++) {
-    long u = (long)g * wg, end = std::min<long>(u + wg, TG);
-    for (int s = 0; u < end; s++) {
-      const int col = (int)(u / IT), k0 = (int)(u % IT);
-      const int n = (int)std::min<long>(end - u, IT - k0);
-      slices[(size_t)g * 2 + s] = (uint32_t)col | (uint32_t)k0 << 12 | (uint32_t)n << 20 | gnseg[col] << 27;
-      gnseg[col]++;
-      u += n;
+  std::vector<uint32_t> wv((size_t)NW * 3, 0u), prep((size_t)G * (1 + kMaxPrep), 0u), gnseg(CG, 0u);
+  for (int b = 0; b < G; b++) {
+    const long r0 = std::min<long>((long)b * rows, TR), r1 = std::min<long>(r0 + rows, TR);
+    std::vector<uint32_t> chunks;  // (m << 8 | c), sorted
+    int nseg = 0;
+    for (long r = r0; r < r1;) {  // parts of the run inside one matrix
+      const int m = (int)(r / IT), k0 = (int)(r % IT), kn = (int)std::min<long>(r1 - r, IT - k0);
+      for (int c = k0 / 8; c <= (k0 + kn - 1) / 8; c++) chunks.push_back((uint32_t)m << 8 | (uint32_t)c);
+      for (int w = 0; w < kWaves; w++) {
+        const int col = m * NPg + w % NPg, sub = w / NPg;
+        const int a0 = k0 + (int)((long)kn * sub / W), a1 = k0 + (int)((long)kn * (sub + 1) / W);
+        if (a1 <= a0) continue;
+        uint32_t *seg = &wv[((size_t)b * kWaves + w) * 3];
+        const int si = seg[0] ? 1 : 0;
+        if (si == 1 && seg[1]) { pl.ok = false; return pl; }
+        seg[si] = (uint32_t)col | (uint32_t)a0 << 12 | (uint32_t)(a1 - a0) << 20 | gnseg[col] << 27;
+        gnseg[col]++;
+      }
+      nseg++;
+      r += kn;
     }
+    if ((int)chunks.size() > kMaxPrep) { pl.ok = false; return pl; }
+    prep[(size_t)b * (1 + kMaxPrep)] = (uint32_t)chunks.size();
+    for (size_t i = 0; i < chunks.size(); i++) prep[(size_t)b * (1 + kMaxPrep) + 1 + i] = chunks[i];
+    for (int w = 0; w < kWaves; w++) {  // each segment's first chunk in the workgroup's list
+      uint32_t *seg = &wv[((size_t)b * kWaves + w) * 3];
+      for (int si = 0; si < 2; si++) {
+        if (!seg[si]) continue;
+        const int col = (int)(seg[si] & 0xFFFu), k0 = (int)((seg[si] >> 12) & 0xFFu);
+        const uint32_t key = (uint32_t)(col / NPg) << 8 | (uint32_t)(k0 / 8);
+        const size_t idx = (size_t)(std::find(chunks.begin(), chunks.end(), key) - chunks.begin());
+        seg[2] |= (uint32_t)idx << (4 * si);
+      }
+    }
+    (void)nseg;
   }
+  for (int c = 0; c < CG; c++)
+    if (gnseg[c] > (uint32_t)kMaxSeg) { pl.ok = false; return pl; }
   std::vector<uint32_t> fin_t((size_t)nslot * NBI, 0u);
   for (int c = 0; c < CG; c++) fin_t[(c / (2 * NPg)) * NBI + (c % NPg) / 4] += gnseg[c];
-  pl.words = slices;
+  pl.words = wv;
+  pl.words.insert(pl.words.end(), prep.begin(), prep.end());
   pl.words.insert(pl.words.end(), gnseg.begin(), gnseg.end());
   pl.words.insert(pl.words.end(), fin_t.begin(), fin_t.end());
   pl.part_floats = (size_t)CG * kMaxSeg * 32 + (size_t)nslot * hid;
