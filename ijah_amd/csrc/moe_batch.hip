@@ -39,7 +39,6 @@ namespace {
 constexpr int kChunkRows = 128;   // rows of one GEMM chunk (4 matrix-core row blocks of 32)
 constexpr int kRowBlocks = kChunkRows / 32;
 constexpr int kAhead = 6;         // k tiles requested ahead of the one being multiplied
-constexpr int kRing = kAhead + 2; // LDS ring slots per stream
 
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 __device__ __forceinline__ void wait_vm(int n) {

@@ -275,59 +275,59 @@ __device__ __forceinline__ void stream_tiles(const uint8_t *tr, int IT, int p, i
       __builtin_amdgcn_global_load_lds((const void *)(src + o + lane * 16),
                                        (__attribute__((address_space(3))) void *)(dst + o), 16, 0, 0);
 }
-// one wave: output tile pair over k tiles [kt0, kt1) staged in LDS, accumulated per lane (lane_col_reduce gives the
-// column sums on lanes with (lane & 6) == 0)
+// one wave: output tile pair over k tiles [kt0, kt1) staged in LDS, on the matrix cores: the weights are decoded
+// straight into the B operand of v_mfma_f32_32x32x16_f16 and A repeats the prepared input row (xs, kp order) in all
+// 32 rows, so every row of the product holds the pair's 32 column sums: lanes 0-31 read them from acc[0].
 template <int K>
-__device__ __forceinline__ void pair_dot_range(const uint8_t *tl, const _Float16 *xs, int kt0, int kt1, float &acc0,
-                                               float &acc1) {
+__device__ __forceinline__ void pair_mfma_range(const uint8_t *tl, const _Float16 *xs, int kt0, int kt1, f32x16 &acc) {
   constexpr int TW = 8 * K;
   const int lane = threadIdx.x & 63;
-  const TileLane<K> L = tile_lane<K>((uint32_t)lane);
-  const int q = (lane >> 1) & 3;
-  const uint32_t *T = (const uint32_t *)tl;
+  const BLane<K> B = b_lane<K>((uint32_t)lane);
+  const uint32_t *T = (const uint32_t *)tl + B.tile * TW;
+  const _Float16 *xa = xs + 8 * (lane >> 5);
 #pragma unroll 4
   for (int kt = kt0; kt < kt1; kt++) {
     const uint32_t *T0 = T + kt * 2 * TW;
-    TileWords wa, wb;
-    wa.w0 = T0[L.i0];
-    wa.w1 = T0[L.i1];
-    wa.w2 = kThreeWords<K> ? T0[L.i2] : 0u;
-    wb.w0 = T0[TW + L.i0];
-    wb.w1 = T0[TW + L.i1];
-    wb.w2 = kThreeWords<K> ? T0[TW + L.i2] : 0u;
-    const f16x4 xv = *(const f16x4 *)(xs + kt * 16 + 4 * q);
-    f16x2 a0, b0, a1, b1;
-    decode4<K>(wa, L.sh, a0, b0);
-    decode4<K>(wb, L.sh, a1, b1);
-    acc0 = dot4(a0, b0, xv, acc0);
-    acc1 = dot4(a1, b1, xv, acc1);
+    TileWords w0, w1;
+    w0.w0 = T0[B.g0.i0];
+    w0.w1 = T0[B.g0.i1];
+    w0.w2 = kThreeWords<K> ? T0[B.g0.i2] : 0u;
+    w1.w0 = T0[B.g1.i0];
+    w1.w1 = T0[B.g1.i1];
+    w1.w2 = kThreeWords<K> ? T0[B.g1.i2] : 0u;
+    const f16x8 av = *(const f16x8 *)(xa + kt * 16);
+    f16x2 l0, h0, l1, h1;
+    decode4<K>(w0, B.g0.sh, l0, h0);
+    decode4<K>(w1, B.g1.sh, l1, h1);
+    const f16x8 bv = {l0.x, l0.y, h0.x, h0.y, l1.x, l1.y, h1.x, h1.y};
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bv, acc, 0, 0, 0);
   }
 }
-// decode k tiles [t0, t0 + n) of the staged pair tiles into w[kt] (kt = t0 .. t0 + n - 1 of the wave's down slice):
-// w[kt][0..1] = tile 2p (rows a, b), w[kt][2..3] = tile 2p + 1
+// decode k tiles [0, n) of the staged pair tiles into the lane's B operands w[kt] (the wave's down slice)
 template <int K>
-__device__ __forceinline__ void decode_pairs(const uint8_t *tl, int t0, int n, f16x2 (&w)[kMaxDn][4]) {
+__device__ __forceinline__ void decode_b(const uint8_t *tl, int n, f16x8 (&w)[kMaxDn]) {
   constexpr int TW = 8 * K;
   const int lane = threadIdx.x & 63;
-  const TileLane<K> L = tile_lane<K>((uint32_t)lane);
-  const uint32_t *T = (const uint32_t *)tl;
+  const BLane<K> B = b_lane<K>((uint32_t)lane);
+  const uint32_t *T = (const uint32_t *)tl + B.tile * TW;
 #pragma unroll
   for (int kt = 0; kt < kMaxDn; kt++) {
-    if (kt >= t0 && kt < t0 + n) {
-      const uint32_t *T0 = T + (kt - t0) * 2 * TW;
-      TileWords wa, wb;
-      wa.w0 = T0[L.i0];
-      wa.w1 = T0[L.i1];
-      wa.w2 = kThreeWords<K> ? T0[L.i2] : 0u;
-      wb.w0 = T0[TW + L.i0];
-      wb.w1 = T0[TW + L.i1];
-      wb.w2 = kThreeWords<K> ? T0[TW + L.i2] : 0u;
-      decode4<K>(wa, L.sh, w[kt][0], w[kt][1]);
-      decode4<K>(wb, L.sh, w[kt][2], w[kt][3]);
+    if (kt < n) {
+      const uint32_t *T0 = T + kt * 2 * TW;
+      TileWords w0, w1;
+      w0.w0 = T0[B.g0.i0];
+      w0.w1 = T0[B.g0.i1];
+      w0.w2 = kThreeWords<K> ? T0[B.g0.i2] : 0u;
+      w1.w0 = T0[B.g1.i0];
+      w1.w1 = T0[B.g1.i1];
+      w1.w2 = kThreeWords<K> ? T0[B.g1.i2] : 0u;
+      f16x2 l0, h0, l1, h1;
+      decode4<K>(w0, B.g0.sh, l0, h0);
+      decode4<K>(w1, B.g1.sh, l1, h1);
+      w[kt] = f16x8{l0.x, l0.y, h0.x, h0.y, l1.x, l1.y, h1.x, h1.y};
     }
   }
 }
-
 // ---------------------------------------------------------------------------------------------------- counting
 // Each wave posts up to two counter indices (or ~0u) in ids[2 wave + s]; wave kCtl merges runs of equal neighbours
 // and adds each run to its counter with one atomic. All threads call it (barriers inside).
@@ -485,7 +485,7 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
   mark(a, 3);
   // a segment's dot, k tiles taken as each 1 KB request lands (n_after: requests issued after the segment's; stores
   // come only after both segments, so they are never counted as "after": a wait may be stricter, never looser)
-  auto gu_dot = [&](const Seg &s, uint32_t off, const _Float16 *pr, int n_seg, int n_after, float &acc0, float &acc1) {
+  auto gu_dot = [&](const Seg &s, uint32_t off, const _Float16 *pr, int n_seg, int n_after, f32x16 &acc) {
     const _Float16 *xs = pr + (s.k0 - 8 * (s.k0 / 8)) * 16;
     const bool sh = slot_shared(a, gu_ls(s));
     const uint32_t pb = 2 * tbytes(gu_ls(s));  // bytes of one k tile pair
@@ -498,28 +498,24 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
       const int kt1 = j == steps - 1 ? s.n : (int)((uint32_t)(j + 1) * 1024u / pb);
       if (kt1 > kt0) {
         if (sh)
-          pair_dot_range<KS>(area + off, xs, kt0, kt1, acc0, acc1);
+          pair_mfma_range<KS>(area + off, xs, kt0, kt1, acc);
         else
-          pair_dot_range<K>(area + off, xs, kt0, kt1, acc0, acc1);
+          pair_mfma_range<K>(area + off, xs, kt0, kt1, acc);
         kt0 = kt1;
       }
     }
-    lane_col_reduce(acc0, acc1);
   };
-  auto gu_store = [&](const Seg &s, float acc0, float acc1) {
-    if ((lane & 6) == 0) {
-      const int col = (lane >> 3) + 8 * (lane & 1);
-      float *d = part_gu + ((size_t)s.col * kMaxSeg + s.jj) * 32;  // [column][kMaxSeg][32]
-      st_cg(d + col, acc0);
-      st_cg(d + 16 + col, acc1);
-    }
+  auto gu_store = [&](const Seg &s, const f32x16 &acc) {
+    if (lane < 32) st_cg(part_gu + ((size_t)s.col * kMaxSeg + s.jj) * 32 + lane, acc[0]);  // [column][kMaxSeg][32]
   };
-  float ga0 = 0.f, ga1 = 0.f, gb0s = 0.f, gb1s = 0.f;
-  if (ok && g0.n) gu_dot(g0, 0, prepw + (pidx & 0xFu) * 128, n_g0, n_g1 + n_dn, ga0, ga1);
-  if (ok && g1.n) gu_dot(g1, off1, prepw + ((pidx >> 4) & 0xFu) * 128, n_g1, n_dn, gb0s, gb1s);
+  f32x16 ga, gb;
+#pragma unroll
+  for (int i = 0; i < 16; i++) ga[i] = gb[i] = 0.f;
+  if (ok && g0.n) gu_dot(g0, 0, prepw + (pidx & 0xFu) * 128, n_g0, n_g1 + n_dn, ga);
+  if (ok && g1.n) gu_dot(g1, off1, prepw + ((pidx >> 4) & 0xFu) * 128, n_g1, n_dn, gb);
   if (a.trace && lane == 0) a.trace[(uint64_t)(512 + blockIdx.x * kWaves + wave) * 8 + 2] = wall_clock64();
-  if (ok && g0.n) gu_store(g0, ga0, ga1);
-  if (ok && g1.n) gu_store(g1, gb0s, gb1s);
+  if (ok && g0.n) gu_store(g0, ga);
+  if (ok && g1.n) gu_store(g1, gb);
   if (wave == 0) mark2(a, 0);
   __builtin_amdgcn_s_waitcnt(0);  // partials stored before they are counted
   if (wave == 0) mark2(a, 1);
@@ -535,10 +531,10 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
   // wave cb < NBI waits until every partial of block cb is stored, sums them in segment order and applies the down
   // prologue (reference kernels/fn_moe.metal:370-384): g = H(inner_g) svh_g, u = H(inner_u) svh_u,
   // h = H(silu(g) u suh_d) -> fp16 in kp order, into LDS. Its down slice is decoded into registers meanwhile.
-  f16x2 dw[kMaxDn][4];
+  f16x8 dw[kMaxDn];
   if (has_dn) {
-    if (slot_shared(a, ls_d)) decode_pairs<KS>(area + GUB, 0, QK, dw);
-    else decode_pairs<K>(area + GUB, 0, QK, dw);
+    if (slot_shared(a, ls_d)) decode_b<KS>(area + GUB, QK, dw);
+    else decode_b<K>(area + GUB, QK, dw);
   }
   mark(a, 5);
   _Float16 *hl = prepw;  // the slot's down input, INTER halves (the prepared chunks are no longer read)
@@ -606,24 +602,17 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
   lds_barrier();
   mark(a, 6);
   float(*red)[32] = (float(*)[32])tiles;  // [wave][32] column sums: the tile areas are no longer read
-  if (dok) {
-    const int q = (lane >> 1) & 3;
-    f16x4 hv[kMaxDn];
-    const _Float16 *hp = hl + dq * QK * 16 + 4 * q;
+  if (dok) {  // on the matrix cores, A = the down input repeated in all rows (as the gate/up dot)
+    const _Float16 *hp = hl + dq * QK * 16 + 8 * (lane >> 5);
+    f16x8 hv[kMaxDn];
 #pragma unroll
-    for (int kt = 0; kt < QK; kt++) hv[kt] = *(const f16x4 *)(hp + kt * 16);
-    float acc0 = 0.f, acc1 = 0.f;
+    for (int kt = 0; kt < QK; kt++) hv[kt] = *(const f16x8 *)(hp + kt * 16);
+    f32x16 acc;
 #pragma unroll
-    for (int kt = 0; kt < QK; kt++) {
-      acc0 = dot4(dw[kt][0], dw[kt][1], hv[kt], acc0);
-      acc1 = dot4(dw[kt][2], dw[kt][3], hv[kt], acc1);
-    }
-    lane_col_reduce(acc0, acc1);
-    if ((lane & 6) == 0) {
-      const int col = (lane >> 3) + 8 * (lane & 1);
-      red[wave][col] = acc0;
-      red[wave][16 + col] = acc1;
-    }
+    for (int i = 0; i < 16; i++) acc[i] = 0.f;
+#pragma unroll
+    for (int kt = 0; kt < QK; kt++) acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(hv[kt], dw[kt], acc, 0, 0, 0);
+    if (lane < 32) red[wave][lane] = acc[0];
   }
   lds_barrier();
   mark(a, 7);
