@@ -38,7 +38,6 @@ namespace {
 
 constexpr int kChunkRows = 128;   // rows of one GEMM chunk (4 matrix-core row blocks of 32)
 constexpr int kRowBlocks = kChunkRows / 32;
-constexpr int kAhead = 6;         // k tiles requested ahead of the one being multiplied
 
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 __device__ __forceinline__ void wait_vm(int n) {
@@ -451,20 +450,13 @@ __device__ void chunk_gemm(const uint16_t *A, int lda, int ahalf, int aidx, int 
     const int q0 = ((lane >> 5) ^ a_swz(lane & 31)) * 16, q1 = ((2 + (lane >> 5)) ^ a_swz(lane & 31)) * 16;
     const f16x8 b0 = bf[0], b1 = bf[1];
 #pragma unroll
-    for (int r2 = 0; r2 < kRowBlocks; r2 += 2) {  // two row blocks' A fragments in flight at a time
-      f16x8 af[2][2];
+    for (int u = 0; u < 2; u++) {  // k tile u of the step for every row block: no two dependent MFMAs adjacent
+      f16x8 af[kRowBlocks];
 #pragma unroll
-      for (int i = 0; i < 2; i++) {
-        af[i][0] = *(const f16x8 *)(at + (r2 + i) * 2048 + q0);
-        af[i][1] = *(const f16x8 *)(at + (r2 + i) * 2048 + q1);
-      }
+      for (int rb = 0; rb < kRowBlocks; rb++) af[rb] = *(const f16x8 *)(at + rb * 2048 + (u ? q1 : q0));
 #pragma unroll
-      for (int i = 0; i < 2; i++) {
-        if (r2 + i < nrb) {
-          acc[r2 + i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i][0], b0, acc[r2 + i], 0, 0, 0);
-          acc[r2 + i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i][1], b1, acc[r2 + i], 0, 0, 0);
-        }
-      }
+      for (int rb = 0; rb < kRowBlocks; rb++)
+        if (rb < nrb) acc[rb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[rb], u ? b1 : b0, acc[rb], 0, 0, 0);
     }
     IJ_STAMP(t == 20, 1)
     // the matrix cores run while the next step's tiles decode
