@@ -52,6 +52,19 @@ __device__ __forceinline__ void wait_vm(int n) {
 __device__ __forceinline__ void dma16(const void *src, void *lds_dst) {
   __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)lds_dst, 16, 0, 0);
 }
+// The same through a buffer resource: wave-uniform base in the descriptor, per-lane byte offset voff, uniform byte
+// offset soff (a scalar register): the streams of the k loop then cost no vector address arithmetic.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t stream_rsrc(const void *base) {
+  const uint64_t b = (uint64_t)base;  // wave-uniform by construction; readfirstlane tells the compiler so
+  // (readfirstlane returns int: widen through uint32_t, or a low word with bit 31 set would sign-extend)
+  const uint64_t u = (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b) |
+                     (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32)) << 32;
+  return __builtin_amdgcn_make_buffer_rsrc((void *)u, (short)0, 0x7FFFFFFF, 0x00020000);
+}
+__device__ __forceinline__ void dma16_buf(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, void *lds_dst) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)lds_dst, 16, voff,
+                                          __builtin_amdgcn_readfirstlane(soff), 0, 0);
+}
 
 // the expert block and layout of expert e (e == ne: the shared expert)
 __device__ __forceinline__ const uint8_t *expert_block(const MoeArgs &a, int e) {
@@ -308,55 +321,61 @@ __device__ __forceinline__ bool xcd_item(int nitems, int &item) {
   return true;
 }
 // Two workgroups share a CU (so four waves per SIMD hide each other's latency): each keeps under 80 KB of LDS.
-constexpr int kDA = 2;  // steps (of 2 k tiles) of A requested ahead
+// Steps (of 2 k tiles) requested ahead: A kDA, B kDB; the B ring's slot count is a multiple of the A ring's, so that
+// the k loop, unrolled by the B ring's length, addresses every ring slot with compile-time offsets.
 template <int K>
-constexpr int kDB = K >= 6 ? 4 : 5;  // steps of B requested ahead
+constexpr int kDA = K >= 6 ? 1 : 2;
+template <int K>
+constexpr int kDB = K >= 6 ? 3 : 5;
 template <int K, int NA>
 struct GemmIo {
   static constexpr uint32_t TB = 32u * K;                  // bytes of one 16x16 tile
   static constexpr uint32_t PB = 2 * 2 * TB;               // a wave's B bytes per step (a pair x 2 k tiles)
   static constexpr uint32_t AB = NA * kChunkRows * 64;     // A bytes per step (NA x 128 rows x 32 halves)
-  static constexpr int DB = kDB<K>;
-  static constexpr int RA = kDA + 1, RB = DB + 1;          // ring slots
+  static constexpr int DA = kDA<K>, DB = kDB<K>;
+  static constexpr int RA = DA + 1, RB = DB + 1;           // ring slots
   static constexpr uint32_t LDS_RING = RA * AB + kWavesG * RB * PB;
   static constexpr uint32_t LDS = LDS_RING > 32768 ? LDS_RING : 32768;  // the epilogue stages 32 x 256 floats
   static constexpr int OA = NA, OB = (PB + 1023) / 1024;   // requests per A / B step
   static_assert(LDS <= 81920, "two workgroups per CU");
+  static_assert(RB % RA == 0 && DB > DA, "ring shapes");
 };
-// Issue order: prologue A(0) B(0) A(1) B(1) .. A(kDA-1) B(kDA-1) B(kDA) .. B(DB-1); step j then issues
-// A(j + kDA) and B(j + DB) (while < NS). Returns how many requests were issued after A(t) and B(t), counted at
-// step t before it issues: the s_waitcnt vmcnt that makes both complete (completion is in issue order).
-template <int OA, int OB, int DB>
+// Issue order: prologue A(0) B(0) A(1) B(1) .. A(DA-1) B(DA-1) B(DA) .. B(DB-1); step j then issues A(j + DA) and
+// B(j + DB) (while < NS). Returns how many requests were issued after A(t) and B(t), counted at step t before it
+// issues: the s_waitcnt vmcnt that makes both complete (completion is in issue order).
+template <int OA, int OB, int DA, int DB>
 __host__ __device__ constexpr int after_step(int t, int NS) {
   auto mn = [](int x, int y) { return x < y ? x : y; };
   auto mx = [](int x, int y) { return x > y ? x : y; };
-  auto sum_ops = [&](int n) { return OA * mn(n, mx(NS - kDA, 0)) + OB * mn(n, mx(NS - DB, 0)); };
-  const int pa = mn(kDA, NS), pb = mn(DB, NS);
+  auto sum_ops = [&](int n) { return OA * mn(n, mx(NS - DA, 0)) + OB * mn(n, mx(NS - DB, 0)); };
+  const int pa = mn(DA, NS), pb = mn(DB, NS);
   const int prologue = OA * pa + OB * pb;
   const int total = prologue + sum_ops(t);
   int last;  // one past the position of the later of A(t), B(t)
-  if (t < kDA) {
+  if (t < DA) {
     last = (OA + OB) * (t + 1);
   } else if (t < DB) {
-    last = mx(prologue + sum_ops(t - kDA) + OA, (OA + OB) * pa + OB * (t - pa) + OB);
+    last = mx(prologue + sum_ops(t - DA) + OA, (OA + OB) * pa + OB * (t - pa) + OB);
   } else {
-    last = mx(prologue + sum_ops(t - kDA) + OA, prologue + sum_ops(t - DB) + ((t - DB) + kDA < NS ? OA : 0) + OB);
+    last = mx(prologue + sum_ops(t - DA) + OA, prologue + sum_ops(t - DB) + ((t - DB) + DA < NS ? OA : 0) + OB);
   }
   return total - last;
 }
 // the count of steps t with DB <= t and t + DB < NS (both streams still issuing): A(t) is the later request,
-// followed by B(t - kDA + DB) and kDA - 1 full steps
-template <int OA, int OB>
-constexpr int kAfterSteady = OB + (kDA - 1) * (OA + OB);
-static_assert(after_step<2, 1, 5>(5, 1000) == kAfterSteady<2, 1> && after_step<1, 1, 4>(9, 1000) == kAfterSteady<1, 1>,
+// followed by B(t - DA + DB) and DA - 1 full steps
+template <int OA, int OB, int DA>
+constexpr int kAfterSteady = OB + (DA - 1) * (OA + OB);
+static_assert(after_step<2, 1, 2, 5>(5, 1000) == kAfterSteady<2, 1, 2> &&
+                  after_step<1, 1, 2, 5>(9, 1000) == kAfterSteady<1, 1, 2> &&
+                  after_step<2, 1, 1, 3>(7, 1000) == kAfterSteady<2, 1, 1>,
               "steady-state wait count");
-template <int OA, int OB, int DB>
+template <int OA, int OB, int DA, int DB>
 __device__ __forceinline__ void wait_step(int t, int NS) {
-  static_assert(kAfterSteady<OA, OB> <= 15, "vmcnt immediate");
+  static_assert(kAfterSteady<OA, OB, DA> <= 15, "vmcnt immediate");
   if (t >= DB && t + DB < NS)
-    __builtin_amdgcn_s_waitcnt(0x0F70 | kAfterSteady<OA, OB>);
+    __builtin_amdgcn_s_waitcnt(0x0F70 | kAfterSteady<OA, OB, DA>);
   else
-    wait_vm(after_step<OA, OB, DB>(t, NS));
+    wait_vm(after_step<OA, OB, DA, DB>(t, NS));
 }
 
 // decodes the lane's B operand for both k tiles of one step straight from the ring bytes src
@@ -391,7 +410,6 @@ template <int K, int NA>
 __device__ void chunk_gemm(const uint16_t *A, int lda, int ahalf, int aidx, int nrows, const uint8_t *tr, int IT,
                            int pair, uint8_t *lds, f32x16 (&acc)[kRowBlocks], uint64_t *dbg) {
   using Io = GemmIo<K, NA>;
-  constexpr int DB = Io::DB;
 #ifdef IJ_BATCH_TRACE  // debug builds only: shader-clock stamps of step 20 per (workgroup, wave)
   uint64_t *drow = dbg ? dbg + ((uint64_t)8192 + blockIdx.x * 8 + (threadIdx.x >> 6)) * 8 : nullptr;
 #define IJ_STAMP(t_, f_) \
@@ -399,7 +417,9 @@ __device__ void chunk_gemm(const uint16_t *A, int lda, int ahalf, int aidx, int 
 #else
 #define IJ_STAMP(t_, f_)
 #endif
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, NS = IT / 2;
+  constexpr int DA = Io::DA, U = Io::RB;  // the k loop is unrolled by the B ring's length
+  const int lane = threadIdx.x & 63, NS = IT / 2;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   uint8_t *ring_a = lds;
   uint8_t *ring_b = lds + Io::RA * Io::AB + wave * Io::RB * Io::PB;
   const BLane<K> BL = b_lane<K>((uint32_t)lane);
@@ -410,58 +430,63 @@ __device__ void chunk_gemm(const uint16_t *A, int lda, int ahalf, int aidx, int 
     for (int i = 0; i < 16; i++) acc[rb][i] = 0.f;
   // A(t): 16 rows of this wave per operand. Row r's 64 bytes (four 16-byte quarters q: k 8q .. 8q + 7) sit at
   // r * 64 with quarter q in position q ^ a_swz(r), so that a read of one quarter of consecutive rows is free of bank
-  // conflicts. DMA lane l fills position l % 4 of row
-  // 16 w + l / 4.
+  // conflicts. DMA lane l fills position l % 4 of row 16 w + l / 4. Stream addresses are a wave-uniform base plus a
+  // fixed per-lane offset.
   const int rr = min(wave * 16 + (lane >> 2), nrows - 1);
-  const int aq = (lane & 3) ^ a_swz(lane >> 2);
-  auto issue_a = [&](int t) {
-    const int slot = t % Io::RA;
+  const uint32_t a_off = (uint32_t)(rr * lda + ((lane & 3) ^ a_swz(lane >> 2)) * 8) * 2;
+  const __amdgpu_buffer_rsrc_t ra = stream_rsrc(A);
+  auto issue_a = [&](int t, int slot) {
 #pragma unroll
     for (int o = 0; o < NA; o++)
-      dma16(A + o * ahalf + (uint64_t)rr * lda + t * 32 + aq * 8,
-            ring_a + slot * Io::AB + o * kChunkRows * 64 + wave * 1024);
+      dma16_buf(ra, a_off, (uint32_t)(o * ahalf * 2 + t * 64), ring_a + slot * Io::AB + o * kChunkRows * 64 + wave * 1024);
   };
   // B(t): the wave's pair at k tiles 2t, 2t + 1 (contiguous)
-  const uint8_t *bsrc = tr + (uint64_t)pair * IT * 2 * Io::TB;
-  auto issue_b = [&](int t) {
-    const int slot = t % Io::RB;
+  const __amdgpu_buffer_rsrc_t rb = stream_rsrc(tr + (uint64_t)__builtin_amdgcn_readfirstlane(pair) * IT * 2 * Io::TB);
+  auto issue_b = [&](int t, int slot) {
 #pragma unroll
     for (uint32_t o = 0; o < Io::PB; o += 1024)
-      if (o + (uint32_t)lane * 16 < Io::PB) dma16(bsrc + (uint64_t)t * Io::PB + o + lane * 16, ring_b + slot * Io::PB + o);
+      if (o + (uint32_t)lane * 16 < Io::PB)
+        dma16_buf(rb, o + (uint32_t)lane * 16, (uint32_t)t * Io::PB, ring_b + slot * Io::PB + o);
   };
   // step s begins when A(s) and B(s) are in: every wave's rows of A(s) landed (barrier), and every wave has read
-  // its fragments of A(s - 1), whose ring slot the step's A request then reuses
+  // its fragments of A(s - 1), whose ring slot the step's A request then reuses. sb = s mod RB (compile-time).
   f16x8 bf[2];
-  auto begin_step = [&](int s) {
-    wait_step<Io::OA, Io::OB, DB>(s, NS);
+  auto begin_step = [&](int s, int sb) {
+    wait_step<Io::OA, Io::OB, DA, Io::DB>(s, NS);
     lds_barrier();
-    if (s + kDA < NS) issue_a(s + kDA);
-    if (s + DB < NS) issue_b(s + DB);
-    decode_step<K>(ring_b + (s % Io::RB) * Io::PB, BL, bf);
+    if (s + DA < NS) issue_a(s + DA, (sb + DA) % Io::RA);
+    if (s + Io::DB < NS) issue_b(s + Io::DB, (sb + Io::DB) % Io::RB);
+    decode_step<K>(ring_b + sb * Io::PB, BL, bf);
   };
-  for (int j = 0; j < DB && j < NS; j++) {
-    if (j < kDA) issue_a(j);
-    issue_b(j);
+  for (int j = 0; j < Io::DB && j < NS; j++) {
+    if (j < DA) issue_a(j, j % Io::RA);
+    issue_b(j, j);
   }
-  begin_step(0);
-  for (int t = 0; t < NS; t++) {
-    IJ_STAMP(t == 20, 0)
-    const uint8_t *at = ring_a + (t % Io::RA) * Io::AB + aidx * kChunkRows * 64 + (lane & 31) * 64;
-    const int q0 = ((lane >> 5) ^ a_swz(lane & 31)) * 16, q1 = ((2 + (lane >> 5)) ^ a_swz(lane & 31)) * 16;
-    const f16x8 b0 = bf[0], b1 = bf[1];
+  begin_step(0, 0);
+  const uint8_t *a_lane = ring_a + aidx * kChunkRows * 64 + (lane & 31) * 64;
+  const int q0 = ((lane >> 5) ^ a_swz(lane & 31)) * 16, q1 = ((2 + (lane >> 5)) ^ a_swz(lane & 31)) * 16;
+  for (int t0 = 0; t0 < NS; t0 += U) {
 #pragma unroll
-    for (int u = 0; u < 2; u++) {  // k tile u of the step for every row block: no two dependent MFMAs adjacent
-      f16x8 af[kRowBlocks];
+    for (int u = 0; u < U; u++) {
+      const int t = t0 + u;
+      if (t >= NS) break;
+      IJ_STAMP(t == 20, 0)
+      const uint8_t *at = a_lane + (u % Io::RA) * Io::AB;
+      const f16x8 b0 = bf[0], b1 = bf[1];
 #pragma unroll
-      for (int rb = 0; rb < kRowBlocks; rb++) af[rb] = *(const f16x8 *)(at + rb * 2048 + (u ? q1 : q0));
+      for (int h = 0; h < 2; h++) {  // k tile h of the step for every row block: no two dependent MFMAs adjacent
+        f16x8 af[kRowBlocks];
 #pragma unroll
-      for (int rb = 0; rb < kRowBlocks; rb++)
-        if (rb < nrb) acc[rb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[rb], u ? b1 : b0, acc[rb], 0, 0, 0);
+        for (int rb = 0; rb < kRowBlocks; rb++) af[rb] = *(const f16x8 *)(at + rb * 2048 + (h ? q1 : q0));
+#pragma unroll
+        for (int rb = 0; rb < kRowBlocks; rb++)
+          if (rb < nrb) acc[rb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[rb], h ? b1 : b0, acc[rb], 0, 0, 0);
+      }
+      IJ_STAMP(t == 20, 1)
+      // the matrix cores run while the next step's tiles decode
+      if (t + 1 < NS) begin_step(t + 1, (u + 1) % U);
+      IJ_STAMP(t == 20, 2)
     }
-    IJ_STAMP(t == 20, 1)
-    // the matrix cores run while the next step's tiles decode
-    if (t + 1 < NS) begin_step(t + 1);
-    IJ_STAMP(t == 20, 2)
   }
   IJ_STAMP(true, 5)
 #undef IJ_STAMP
@@ -596,8 +621,8 @@ __global__ __launch_bounds__(256) void bat_combine(MoeArgs a, const float *__res
 namespace {
 template <int K, int KS>
 void launch_gemms(const MoeArgs &a, const MoeBatchBufs &b, hipStream_t s) {
-  constexpr int KM = K > KS ? K : KS;
-  const size_t lg = GemmIo<KM, 2>::LDS, ld = GemmIo<KM, 1>::LDS;
+  // the routed (K) and shared (KS) chunks use ring layouts of their own widths: room for the larger of each
+  const size_t lg = std::max(GemmIo<K, 2>::LDS, GemmIo<KS, 2>::LDS), ld = std::max(GemmIo<K, 1>::LDS, GemmIo<KS, 1>::LDS);
   static bool attr = false;
   if (!attr) {
     IJ_HIP(hipFuncSetAttribute((const void *)&bat_gateup<K, KS>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lg));
