@@ -562,12 +562,22 @@ __global__ __launch_bounds__(512, 4) void bat_down(MoeArgs a, const uint32_t *bk
   const int e = (int)chunks[3 * ch], row0 = (int)chunks[3 * ch + 1], nrows = (int)chunks[3 * ch + 2];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const uint8_t *blk = expert_block(a, e);
+  // each row's slot (token, k) and route weight, gathered once into LDS (the slot ids requested before the GEMM)
+  __shared__ uint32_t m_dst[kChunkRows];
+  __shared__ float m_w[kChunkRows];
+  const int mt = threadIdx.x;
+  const uint32_t sl = mt < nrows ? rows[row0 + mt] : 0u;
   f32x16 acc[kRowBlocks];
   const uint16_t *A = hh + (uint64_t)row0 * a.inter;
   if (e >= a.ne)
     chunk_gemm<KS, 1>(A, a.inter, 0, 0, nrows, blk + tr_of(a, e, 2), a.inter / 16, ob2 * 8 + wave, lds, acc, nullptr);
   else
     chunk_gemm<K, 1>(A, a.inter, 0, 0, nrows, blk + tr_of(a, e, 2), a.inter / 16, ob2 * 8 + wave, lds, acc, nullptr);
+  if (mt < nrows) {
+    const int tok = sl / a.nslot, k = sl % a.nslot;
+    m_dst[mt] = sl;
+    m_w[mt] = k >= a.topk ? a.sgv[tok] : __uint_as_float(a.route[(uint64_t)tok * 2 * a.topk + a.topk + k]);
+  }
   float *ot = (float *)lds;  // [32][256]
   const uint16_t *sv = (const uint16_t *)(blk + sv_of(a, e, 2)) + ob2 * 256;
   float s[2][2];
@@ -588,10 +598,8 @@ __global__ __launch_bounds__(512, 4) void bat_down(MoeArgs a, const uint32_t *bk
     }
     __syncthreads();
     for (int r = wave; r < 32 && rb * 32 + r < nrows; r += kWavesG) {
-      const uint32_t sl = rows[row0 + rb * 32 + r];
-      const int tok = sl / a.nslot, k = sl % a.nslot;
-      const float w = k >= a.topk ? a.sgv[tok] : __uint_as_float(a.route[(uint64_t)tok * 2 * a.topk + a.topk + k]);
-      float *out = dnw + ((uint64_t)tok * a.nslot + k) * a.hid + ob2 * 256;
+      const float w = m_w[rb * 32 + r];
+      float *out = dnw + (uint64_t)m_dst[rb * 32 + r] * a.hid + ob2 * 256;  // slot sl = token * nslot + k
 #pragma unroll
       for (int bb = 0; bb < 2; bb++) {
         float v0 = ot[r * 256 + bb * 128 + lane], v1 = ot[r * 256 + bb * 128 + 64 + lane];
