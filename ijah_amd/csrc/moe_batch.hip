@@ -90,27 +90,31 @@ __global__ __launch_bounds__(1024) void bat_zero(uint32_t *p, int n) {
 }
 
 // ---------------------------------------------------------------------------------------------------- router
-// logits[r][c] = bf16(x[r] . router[c]) for c < ne + has_sgate on the matrix cores: one workgroup per 32 x 32 tile
-// (rows x router rows), its 8 waves splitting k into eighths (so that even a few rows keep the chip busy) and
-// summing in LDS in wave order. k steps of 16: x is split into bf16 hi + lo (x - hi rounded again), two MFMAs per
+// logits[r][c] = bf16(x[r] . router[c]) for c < ne + has_sgate on the matrix cores. A workgroup covers 32 rows and
+// CT 32-column tiles; its 8 waves are CT column tiles x KSP k splits, summed in LDS in split order. Few rows take
+// CT = 1, KSP = 8 (the k split keeps the chip busy); many rows take CT = 4, KSP = 2, so that each row of x is read
+// by a quarter as many workgroups. k steps of 16: x is split into bf16 hi + lo (x - hi rounded again), two MFMAs per
 // step, so the product carries about 16 mantissa bits of x: within f32 rounding of the reference's f32 dot for
 // these logits.
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 constexpr int kRouterWaves = 8;
+template <int CT>
 __global__ __launch_bounds__(512) void bat_router(MoeArgs a) {
+  constexpr int KSP = kRouterWaves / CT;
   __shared__ float red[kRouterWaves][16][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, ncol = a.ne + a.has_sgate;
-  const int rt = blockIdx.x, ct = blockIdx.y;  // 32-row tile, 32-column tile
+  const int rt = blockIdx.x, ct = blockIdx.y * CT + wave % CT, ks = wave / CT;  // 32-row tile, 32-column tile
+  const bool live = ct * 32 < ncol;
   const int m = lane & 31, h = lane >> 5;
   const int row = min(rt * 32 + m, a.R - 1), col = min(ct * 32 + m, ncol - 1);
-  const int kn = a.hid / kRouterWaves, kb = wave * kn;  // this wave's k range (a multiple of 32 long)
+  const int kn = a.hid / KSP, kb = ks * kn;  // this wave's k range (a multiple of 32 long)
   const float *xp = a.x + (uint64_t)row * a.hid + kb + 8 * h;
   const uint16_t *wp = a.router + (uint64_t)col * a.hid + kb + 8 * h;
   f32x16 acc;
 #pragma unroll
   for (int i = 0; i < 16; i++) acc[i] = 0.f;
   constexpr int U = 4;  // k steps per batch of loads
-  for (int k0 = 0; k0 < kn; k0 += 16 * U) {
+  for (int k0 = 0; live && k0 < kn; k0 += 16 * U) {
     float4 xv[U][2];
     uint4 wv[U];
 #pragma unroll
@@ -142,13 +146,13 @@ __global__ __launch_bounds__(512) void bat_router(MoeArgs a) {
 #pragma unroll
   for (int i = 0; i < 16; i++) red[wave][i][lane] = acc[i];
   __syncthreads();
-  for (int o = threadIdx.x; o < 16 * 64; o += kRouterWaves * 64) {
-    const int i = o >> 6, l = o & 63;
+  for (int o = threadIdx.x; o < CT * 16 * 64; o += kRouterWaves * 64) {
+    const int c = o / (16 * 64), i = (o >> 6) & 15, l = o & 63;
     float v = 0.f;
 #pragma unroll
-    for (int w = 0; w < kRouterWaves; w++) v += red[w][i][l];
-    const int r = rt * 32 + 4 * (l >> 5) + (i & 3) + 8 * (i >> 2), c = ct * 32 + (l & 31);
-    if (r < a.R && c < ncol) a.logits[(uint64_t)r * (a.ne + 1) + c] = bf16_round(v);
+    for (int k = 0; k < KSP; k++) v += red[k * CT + c][i][l];
+    const int r = rt * 32 + 4 * (l >> 5) + (i & 3) + 8 * (i >> 2), cc = (blockIdx.y * CT + c) * 32 + (l & 31);
+    if (r < a.R && cc < ncol) a.logits[(uint64_t)r * (a.ne + 1) + cc] = bf16_round(v);
   }
 }
 
@@ -656,7 +660,10 @@ int moe_batch_max_chunks(int R, int ne, int topk, bool shared) {
 void launch_moe_batch(const MoeArgs &a, const MoeBatchBufs &b, hipStream_t s) {
   const int ncol = a.ne + a.has_sgate, S = a.R * a.nslot;
   hipLaunchKernelGGL(bat_zero, dim3(1), dim3(1024), 0, s, b.bk, a.ne + 1);  // a kernel, not a memset node
-  hipLaunchKernelGGL(bat_router, dim3((a.R + 31) / 32, (ncol + 31) / 32), dim3(64 * kRouterWaves), 0, s, a);
+  if (a.R >= 512)
+    hipLaunchKernelGGL(bat_router<4>, dim3((a.R + 31) / 32, (ncol + 127) / 128), dim3(64 * kRouterWaves), 0, s, a);
+  else
+    hipLaunchKernelGGL(bat_router<1>, dim3((a.R + 31) / 32, (ncol + 31) / 32), dim3(64 * kRouterWaves), 0, s, a);
   hipLaunchKernelGGL(bat_route, dim3((a.R + 3) / 4), dim3(256), 0, s, a, b.bk);
   hipLaunchKernelGGL(bat_scan, dim3(1), dim3(1024), 0, s, a, b.bk, b.chunks, b.max_chunks);
   hipLaunchKernelGGL(bat_place, dim3((S + 255) / 256), dim3(256), 0, s, a, b.bk, b.rows);

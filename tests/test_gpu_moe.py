@@ -150,7 +150,7 @@ def test_moe_fused_and_staged_paths_agree(eng, oracle, monkeypatch):
 
 
 # ---------------------------------------------------------------------------------------------- batched path (R >= 2)
-@pytest.mark.parametrize("R", [16, 200])
+@pytest.mark.parametrize("R", [16, 200, 640])
 def test_moe_batch_chunks(eng, oracle, R):
     """R rows through the grouped matrix-core path: experts with more than one 128-row chunk (the shared expert at
     R = 200, ~50 rows per routed expert), ties and order checked against the oracle on the GPU's route."""
