@@ -108,39 +108,48 @@ __global__ __launch_bounds__(512) void bat_router(MoeArgs a) {
   const int m = lane & 31, h = lane >> 5;
   const int row = min(rt * 32 + m, a.R - 1), col = min(ct * 32 + m, ncol - 1);
   const int kn = a.hid / KSP, kb = ks * kn;  // this wave's k range (a multiple of 32 long)
+  static_assert(kRouterWaves % CT == 0, "waves per tile");
   const float *xp = a.x + (uint64_t)row * a.hid + kb + 8 * h;
   const uint16_t *wp = a.router + (uint64_t)col * a.hid + kb + 8 * h;
   f32x16 acc;
 #pragma unroll
   for (int i = 0; i < 16; i++) acc[i] = 0.f;
-  constexpr int U = 4;  // k steps per batch of loads
-  for (int k0 = 0; live && k0 < kn; k0 += 16 * U) {
-    float4 xv[U][2];
-    uint4 wv[U];
+  // k steps in batches of U, the next batch's loads in flight while this one multiplies (kn is a multiple of 32,
+  // so batches are whole: kn / 16 steps, U = 2)
+  constexpr int U = 2;
+  float4 xv[2][U][2];
+  uint4 wv[2][U];
+  auto load = [&](int b, int k0) {
 #pragma unroll
     for (int u = 0; u < U; u++) {
-      const int k = k0 + 16 * u;
-      if (k < kn) {
-        xv[u][0] = *(const float4 *)(xp + k);
-        xv[u][1] = *(const float4 *)(xp + k + 4);
-        wv[u] = *(const uint4 *)(wp + k);
-      }
+      xv[b][u][0] = *(const float4 *)(xp + k0 + 16 * u);
+      xv[b][u][1] = *(const float4 *)(xp + k0 + 16 * u + 4);
+      wv[b][u] = *(const uint4 *)(wp + k0 + 16 * u);
     }
+  };
+  auto mul = [&](int b) {
 #pragma unroll
     for (int u = 0; u < U; u++) {
-      if (k0 + 16 * u < kn) {
-        const float xs[8] = {xv[u][0].x, xv[u][0].y, xv[u][0].z, xv[u][0].w,
-                             xv[u][1].x, xv[u][1].y, xv[u][1].z, xv[u][1].w};
-        bf16x8 hi, lo;
+      const float xs[8] = {xv[b][u][0].x, xv[b][u][0].y, xv[b][u][0].z, xv[b][u][0].w,
+                           xv[b][u][1].x, xv[b][u][1].y, xv[b][u][1].z, xv[b][u][1].w};
+      bf16x8 hi, lo;
 #pragma unroll
-        for (int e = 0; e < 8; e++) {
-          hi[e] = (__bf16)xs[e];
-          lo[e] = (__bf16)(xs[e] - (float)hi[e]);
-        }
-        const bf16x8 wb = __builtin_bit_cast(bf16x8, wv[u]);
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(hi, wb, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(lo, wb, acc, 0, 0, 0);
+      for (int e = 0; e < 8; e++) {
+        hi[e] = (__bf16)xs[e];
+        lo[e] = (__bf16)(xs[e] - (float)hi[e]);
       }
+      const bf16x8 wb = __builtin_bit_cast(bf16x8, wv[b][u]);
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(hi, wb, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(lo, wb, acc, 0, 0, 0);
+    }
+  };
+  if (live) {
+    load(0, 0);
+    for (int k0 = 0; k0 < kn; k0 += 32 * U) {  // two batches per trip, so the buffer index stays compile-time
+      if (k0 + 16 * U < kn) load(1, k0 + 16 * U);
+      mul(0);
+      if (k0 + 32 * U < kn) load(0, k0 + 32 * U);
+      if (k0 + 16 * U < kn) mul(1);
     }
   }
 #pragma unroll
