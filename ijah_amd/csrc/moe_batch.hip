@@ -9,21 +9,20 @@
 //                counts the routed slots per expert
 //   bat_scan     per-expert offsets of the expert-sorted slot list (the shared expert's rows last) and the list of
 //                128-row chunks (expert, first row, rows) the GEMMs run over (kernels/prefill/pf_moe.metal:26-83)
-//   bat_place    each slot's place in its expert's rows (row order inside an expert does not change any result:
-//                every row is computed independently)
-//   bat_prep     xh[row][proj] = fp16(H(x[token] * suh_e,proj)) in kp order for the gate and the up projection (each
-//                linear has its own suh), per sorted row (kernels/prefill/pf_moe.metal:85-110)
+//   bat_place_prep  one wave per slot: its place in its expert's rows (row order inside an expert does not change
+//                any result: every row is computed independently) and that row of the A operand,
+//                xh[row][proj] = fp16(H(x[token] * suh_e,proj)) in kp order for the gate and the up projection (each
+//                linear has its own suh) (kernels/prefill/pf_moe.metal:85-110)
 //   bat_gateup   per (chunk, 128-column block ib of inter): gate and up GEMMs on the matrix cores, then the down
 //                prologue on the block: hh[row][ib] = fp16(H(silu(H(g) svh_g) H(u) svh_u suh_d)) (:111-140)
-//   bat_down     per (chunk, 128-column block of hid): the down GEMM, then H, svh_d and the slot's route weight,
-//                stored per (token, slot) (:141-161)
+//   bat_down     per (chunk, 256 columns of hid): the down GEMM, then H, svh_d and the slot's route weight, stored
+//                per (token, slot) (:141-161)
 //   bat_combine  y[token] = sum over the token's slots in slot order
 //
 // Matrix-core operands (this build's layout): a 16-row k tile of A is held in the reference's kp order, so lane
-// (m, h) of v_mfma_f32_32x32x16_f16 reads rows m, k positions [8h, 8h + 8) as one 16-byte LDS read. The decoder's
-// lane for (column c, quad q) writes its four weights (rows 2q, 2q+1, 2q+8, 2q+9 = kp positions 4q..4q+3) of both
-// tiles of a pair to LDS at [tile][c][q]; matrix-core lane (n, h) then reads quads 2h and 2h+1 of column n as one
-// 16-byte read: the same k permutation on both operands.
+// (m, h) of v_mfma_f32_32x32x16_f16 reads row m, k positions [8h, 8h + 8) as one 16-byte LDS read. Matrix-core lane
+// (n, h) decodes its B operand itself: the trellis groups (column n % 16, quads 2h and 2h + 1) of tile n / 16 of the
+// pair, i.e. kp positions 8h .. 8h + 7: the same k permutation on both operands.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -253,46 +252,47 @@ __global__ __launch_bounds__(1024) void bat_scan(MoeArgs a, uint32_t *bk, uint32
   }
   if (tid == 0) *nchunks = min(cc[n > 0 ? n - 1 : 0], (uint32_t)max_chunks);
 }
-// slot (r, k) -> its row in its expert's list; rows[row] = r * nslot + k (k == topk: the shared expert)
-__global__ __launch_bounds__(256) void bat_place(MoeArgs a, uint32_t *bk, uint32_t *rows) {
-  const int s = blockIdx.x * 256 + threadIdx.x;
-  if (s >= a.R * a.nslot) return;
+// One wave per slot (r, k): takes the slot's row in its expert's list (rows[row] = r * nslot + k; k == topk: the
+// shared expert, whose list is every token in order) and writes that row of the A operand:
+// xh[row] = [gate | up] fp16(H(x[r] * suh_e)) in kp order (the two projections have their own suh).
+// WPS waves per slot (1 for many rows; 4 for few, so that they still fill the chip), each a quarter of the blocks.
+template <int WPS>
+__global__ __launch_bounds__(256) void bat_place_prep(MoeArgs a, uint32_t *bk, uint32_t *rows, uint16_t *xh) {
+  __shared__ uint32_t s_row;
+  const int lane = threadIdx.x & 63, wq = (int)(threadIdx.x >> 6) % WPS;
+  const int s = blockIdx.x * (4 / WPS) + (int)(threadIdx.x >> 6) / WPS;
+  if (WPS == 1 && s >= a.R * a.nslot) return;
   const int r = s / a.nslot, k = s % a.nslot;
   const uint32_t *offs = bk + (a.ne + 1);
   uint32_t *cursor = bk + 2 * (a.ne + 1);
-  uint32_t row;
-  if (k >= a.topk) {
-    row = offs[a.ne] + (uint32_t)r;
-  } else {
-    uint32_t e = a.route[(uint64_t)r * 2 * a.topk + k];
-    e = e < (uint32_t)a.ne ? e : 0u;
-    row = offs[e] + atomicAdd(cursor + e, 1u);
-  }
-  rows[row] = (uint32_t)s;
-}
-
-// ---------------------------------------------------------------------------------------------------- prep
-// xh[row] = fp16(H(x[token] * suh_e)) in kp order (one wave per 128-chunk, 4 waves per row)
-__global__ __launch_bounds__(256) void bat_prep(MoeArgs a, const uint32_t *rows, const uint32_t *bk, uint16_t *xh) {
-  const int row = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const uint32_t s = rows[row];
-  const int r = s / a.nslot, k = s % a.nslot;
   int e = a.ne;
   if (k < a.topk) {
     e = (int)a.route[(uint64_t)r * 2 * a.topk + k];
     e = e < a.ne ? e : 0;
   }
+  uint32_t row = 0u;
+  if (lane == 0 && wq == 0) {
+    row = k >= a.topk ? offs[a.ne] + (uint32_t)r : offs[e] + atomicAdd(cursor + e, 1u);
+    rows[row] = (uint32_t)s;
+    if (WPS > 1) s_row = row;
+  }
+  if (WPS > 1) {
+    __syncthreads();
+    row = s_row;
+  }
+  row = (uint32_t)__builtin_amdgcn_readfirstlane(row);
   const uint16_t *sug = (const uint16_t *)(expert_block(a, e) + su_of(a, e, 0));
   const uint16_t *suu = (const uint16_t *)(expert_block(a, e) + su_of(a, e, 1));
   const float *x = a.x + (uint64_t)r * a.hid;
   uint16_t *out = xh + (uint64_t)row * 2 * a.hid;
-  constexpr int U = 4;  // blocks per wave whose loads are all issued before the first store
-  for (int c0 = wave; c0 < a.hid / 128; c0 += 4 * U) {
+  constexpr int U = 4;  // blocks whose loads are all issued before the first store
+  const int nb = a.hid / 128;
+  for (int c0 = wq; c0 < nb; c0 += U * WPS) {
     float g[U][2], u[U][2];
 #pragma unroll
     for (int j = 0; j < U; j++) {
-      const int c = c0 + 4 * j;
-      if (c < a.hid / 128) {
+      const int c = c0 + j * WPS;
+      if (c < nb) {
         const int e0 = c * 128 + lane, e1 = e0 + 64;
         const float x0 = x[e0], x1 = x[e1];
         g[j][0] = x0 * h2f(sug[e0]);
@@ -303,8 +303,8 @@ __global__ __launch_bounds__(256) void bat_prep(MoeArgs a, const uint32_t *rows,
     }
 #pragma unroll
     for (int j = 0; j < U; j++) {
-      const int c = c0 + 4 * j;
-      if (c < a.hid / 128) {
+      const int c = c0 + j * WPS;
+      if (c < nb) {
         fwht2(g[j][0], g[j][1], lane, a.had_hid, a.sc_hid);
         fwht2(u[j][0], u[j][1], lane, a.had_hid, a.sc_hid);
         out[c * 128 + kp(lane)] = f2h(g[j][0]);
@@ -675,8 +675,10 @@ void launch_moe_batch(const MoeArgs &a, const MoeBatchBufs &b, hipStream_t s) {
     hipLaunchKernelGGL(bat_router<1>, dim3((a.R + 31) / 32, (ncol + 31) / 32), dim3(64 * kRouterWaves), 0, s, a);
   hipLaunchKernelGGL(bat_route, dim3((a.R + 3) / 4), dim3(256), 0, s, a, b.bk);
   hipLaunchKernelGGL(bat_scan, dim3(1), dim3(1024), 0, s, a, b.bk, b.chunks, b.max_chunks);
-  hipLaunchKernelGGL(bat_place, dim3((S + 255) / 256), dim3(256), 0, s, a, b.bk, b.rows);
-  hipLaunchKernelGGL(bat_prep, dim3(S), dim3(256), 0, s, a, b.rows, b.bk, b.xh);
+  if (S >= 8192)
+    hipLaunchKernelGGL(bat_place_prep<1>, dim3((S + 3) / 4), dim3(256), 0, s, a, b.bk, b.rows, b.xh);
+  else
+    hipLaunchKernelGGL(bat_place_prep<4>, dim3(S), dim3(256), 0, s, a, b.bk, b.rows, b.xh);
   const int KS = a.nslot > a.topk ? a.slay.K : a.lay.K;
   bool done = false;
 #define IJ_BAT(k, ks)                        \
