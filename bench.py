@@ -84,11 +84,12 @@ def moe_flops(R, hid=HID, inter=INTER, topk=TOPK, shared=1):
     return 2.0 * 3 * hid * inter * R * (topk + shared)
 
 
-def measure_batch(eng, R, n_layers, steps, seed):
+def measure_batch(eng, R, n_layers, steps, seed, k=K):
     """The layer at R rows (BASELINE.json config 4 at R = 16, config 5 at R = 4096) on the grouped matrix-core path:
-    a chain of n_layers distinct synthetic layers in one HIP graph. Returns a dict for the JSON line."""
+    a chain of n_layers distinct synthetic layers in one HIP graph, experts and shared expert at k bits. Returns a
+    dict for the JSON line."""
     from ijah_amd import synth
-    layers = [eng.moe_synth(HID, INTER, NE, TOPK, K, True, K, seed=seed + 7919 * i) for i in range(n_layers)]
+    layers = [eng.moe_synth(HID, INTER, NE, TOPK, k, True, k, seed=seed + 7919 * i) for i in range(n_layers)]
     x = synth.bf16_values(np.random.default_rng(seed), R, HID)
     xb = eng.from_numpy(x)
     yb = eng.alloc(R * HID * 4)
@@ -98,7 +99,7 @@ def measure_batch(eng, R, n_layers, steps, seed):
     byts = float(np.mean([m.bytes(R) for m in layers]))
     us = eng.moe_time(layers, R, xb, warmup=2, reps=steps)
     fl = moe_flops(R)
-    out = {"rows": R, "layers_per_step": n_layers, "us_per_layer": round(us, 2),
+    out = {"rows": R, "K": k, "layers_per_step": n_layers, "us_per_layer": round(us, 2),
            "tokens_per_s_per_layer": round(R * 1e6 / us, 1),
            "weight_bytes_per_layer": int(byts), "weight_GBps": round(byts / (us * 1e-6) / 1e9, 1),
            "expert_gemm_TFLOPs": round(fl / (us * 1e-6) / 1e12, 2),
@@ -134,6 +135,7 @@ def measure_trunk(eng, R, steps, seed, min_bytes=300e6):
         out[name] = {"in": inp, "out": o, "K": K, "us": round(us, 3), "bytes": int(nbytes), "GBps": round(gbs, 1),
                      "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2)}
         print(f"trunk {name} R={R}: {out[name]}", file=sys.stderr, flush=True)
+    # at R rows the weights are read once for all rows: "GBps" is weight bytes over time
     qkvo = sum(out[n]["us"] for n in ("q", "k", "v", "o"))
     qkvo_b = sum(out[n]["bytes"] for n in ("q", "k", "v", "o"))
     out["qkvo_sum"] = {"us": round(qkvo, 3), "GBps": round(qkvo_b / (qkvo * 1e-6) / 1e9, 1)}
@@ -173,7 +175,8 @@ def main():
         print(json.dumps({"copy_probe_bytes": n, "launches": 5}), flush=True)
         return
     if a.trunk_only:
-        print(json.dumps(measure_trunk(eng, 1, a.steps, a.seed)), flush=True)
+        print(json.dumps({"m1": measure_trunk(eng, 1, a.steps, a.seed), "m16": measure_trunk(eng, 16, a.steps, a.seed)}),
+              flush=True)
         return
     if a.batch_rows:
         print(json.dumps(measure_batch(eng, a.batch_rows, 4, a.steps, a.seed + a.batch_rows)), flush=True)
@@ -223,10 +226,13 @@ def main():
             m.free()
         extra["verify_r16"] = measure_batch(eng, 16, 32, max(5, a.steps // 5), a.seed + 16)
         print(f"verify R=16: {extra['verify_r16']}", file=sys.stderr, flush=True)
+        extra["verify_r16_k4"] = measure_batch(eng, 16, 32, max(5, a.steps // 5), a.seed + 17, k=4)
+        print(f"verify R=16 K4: {extra['verify_r16_k4']}", file=sys.stderr, flush=True)
         extra["prefill_r4096"] = measure_batch(eng, 4096, 4, 3, a.seed + 4096)
         print(f"prefill R=4096: {extra['prefill_r4096']}", file=sys.stderr, flush=True)
     if not a.no_trunk:
         extra["trunk_m1"] = measure_trunk(eng, 1, max(5, a.steps // 5), a.seed + 3)
+        extra["trunk_m16"] = measure_trunk(eng, 16, max(5, a.steps // 5), a.seed + 4)
     cpu = None if a.no_cpu else cpu_baseline()
     line = {
         "metric": "MoE layer us + effective packed-weight GB/s (% HBM peak), 5-bit EXL3, M=1",

@@ -73,8 +73,8 @@ struct ne_exl3_lin {
   int splits(int R) const {
     const int NP = OTp / 2;
     int S = 1;
-    if (R > kLinSimdRows) {  // matrix cores: one wave per (pair, split), >= 2048 waves, >= 8 k tiles per split
-      while (NP * S < 2048 && IT % (2 * S) == 0 && IT / (2 * S) >= 8) S *= 2;
+    if (R > kLinSimdRows) {  // matrix cores: 8 pairs per workgroup, >= 512 workgroups, >= 16 k tiles per split
+      while ((NP + 7) / 8 * S < 512 && IT % (2 * S) == 0 && IT / (2 * S) >= 16) S *= 2;
       return S;
     }
     while (NP * S < 1024 && IT % (2 * S) == 0 && IT / (2 * S) >= 8) S *= 2;
@@ -212,6 +212,19 @@ static LinArgs lin_args(ne_exl3_lin *l, int R, const float *x, float *y) {
   return a;
 }
 
+// The launches of one run: rows beyond the GEMV's 8 take the matrix-core GEMM when the k tiles pair up (IT even);
+// otherwise they run as groups of 8 rows through the GEMV path.
+static void lin_launch(ne_exl3_lin *l, int R, const float *x, float *y, hipStream_t s) {
+  if (R <= kLinSimdRows || l->IT % 2 == 0) {
+    launch_lin(lin_args(l, R, x, y), s);
+    return;
+  }
+  for (int r0 = 0; r0 < R; r0 += kLinSimdRows) {
+    const int n = std::min(kLinSimdRows, R - r0);
+    launch_lin(lin_args(l, n, x + (size_t)r0 * l->in, y + (size_t)r0 * l->out), s);
+  }
+}
+
 extern "C" {
 
 NE_API int ne_exl3_lin_run(ne_exl3_lin *l, int R, const ne_buf *x, uint64_t x_off, ne_buf *y, uint64_t y_off,
@@ -222,8 +235,9 @@ NE_API int ne_exl3_lin_run(ne_exl3_lin *l, int R, const ne_buf *x, uint64_t x_of
     IJ_CHECK(x_off % 4 == 0 && y_off % 4 == 0, "offsets must be 4-byte aligned");
     IJ_CHECK(x_off + (uint64_t)R * l->in * 4 <= x->size, "x buffer too small for [%d][%d] f32", R, l->in);
     IJ_CHECK(y_off + (uint64_t)R * l->out * 4 <= y->size, "y buffer too small for [%d][%d] f32", R, l->out);
-    const LinArgs a = lin_args(l, R, (const float *)((const char *)x->dev + x_off), (float *)((char *)y->dev + y_off));
-    timed(stream(), gpu_ms, [&] { launch_lin(a, stream()); });
+    const float *xp = (const float *)((const char *)x->dev + x_off);
+    float *yp = (float *)((char *)y->dev + y_off);
+    timed(stream(), gpu_ms, [&] { lin_launch(l, R, xp, yp, stream()); });
   });
 }
 
@@ -247,15 +261,17 @@ NE_API int ne_exl3_lin_time(ne_exl3_lin *const *lins, int n, int R, const ne_buf
       dev_free(ys);
     };
     try {
-      std::vector<LinArgs> args;
-      size_t yo = 0;
-      for (int i = 0; i < n; i++) {
-        args.push_back(lin_args(lins[i], R, (const float *)x->dev, ys + yo));
-        yo += (size_t)R * lins[i]->out;
+      for (int i = 0; i < n; i++) {  // grow the split scratch before capture (both row paths lin_launch may take)
+        lin_args(lins[i], R, nullptr, nullptr);
+        lin_args(lins[i], std::min(R, kLinSimdRows), nullptr, nullptr);
       }
       IJ_HIP(hipStreamSynchronize(s));
       IJ_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
-      for (const LinArgs &a : args) launch_lin(a, s);
+      size_t yo = 0;
+      for (int i = 0; i < n; i++) {
+        lin_launch(lins[i], R, (const float *)x->dev, ys + yo, s);
+        yo += (size_t)R * lins[i]->out;
+      }
       IJ_HIP(hipStreamEndCapture(s, &g));
       IJ_HIP(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0));
       for (int i = 0; i < warmup; i++) IJ_HIP(hipGraphLaunch(ge, s));

@@ -662,61 +662,6 @@ __global__ __launch_bounds__(256) void lin_step(LinArgs a) {
   }
 }
 
-// lin_mfma: 9..32 rows on the matrix cores, the weights decoded straight into the B operand of
-// v_mfma_f32_32x32x16_f16 (reference kernels/trunk6/trunk6.metal:431-539, t6_nax). One wave per (tile pair p, k split
-// s), four waves per workgroup. A = rows of xh (fp16, kp order, L2-resident): lane l reads row l % 32, k 8 (l / 32)
-// .. + 8 of each k tile, which is exactly the k range of the lane's two trellis groups. part[s][r][OTp * 16] as
-// lin_gemv; rows past R are computed on a clamped row and dropped.
-template <int K>
-__global__ __launch_bounds__(256) void lin_mfma(LinArgs a) {
-  constexpr int TW = 8 * K, U = 4;
-  const int lane = threadIdx.x & 63;
-  const int NP = (a.OT + 1) / 2, OTp = 2 * NP;
-  const int w = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (w >= NP * a.S) return;
-  const int p = w % NP, s = w / NP;
-  const int span = a.IT / a.S, k0 = s * span, k1 = k0 + span;
-  const BLane<K> B = b_lane<K>((uint32_t)lane);
-  const uint32_t *pb = a.tiles + (uint64_t)p * a.IT * 2 * TW + B.tile * TW;
-  const uint16_t *xr = a.xh + (uint64_t)min(lane & 31, a.R - 1) * a.in + 8 * (lane >> 5);
-  f32x16 acc;
-#pragma unroll
-  for (int i = 0; i < 16; i++) acc[i] = 0.f;
-  for (int tk0 = k0; tk0 < k1; tk0 += U) {
-    TileWords w0[U], w1[U];
-    f16x8 av[U];
-#pragma unroll
-    for (int u = 0; u < U; u++) {
-      const int tk = tk0 + u;
-      if (tk < k1) {
-        const uint32_t *T = pb + (uint64_t)tk * 2 * TW;
-        w0[u].w0 = __builtin_nontemporal_load(T + B.g0.i0);
-        w0[u].w1 = __builtin_nontemporal_load(T + B.g0.i1);
-        w0[u].w2 = kThreeWords<K> ? __builtin_nontemporal_load(T + B.g0.i2) : 0u;
-        w1[u].w0 = __builtin_nontemporal_load(T + B.g1.i0);
-        w1[u].w1 = __builtin_nontemporal_load(T + B.g1.i1);
-        w1[u].w2 = kThreeWords<K> ? __builtin_nontemporal_load(T + B.g1.i2) : 0u;
-        av[u] = *(const f16x8 *)(xr + tk * 16);
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < U; u++) {
-      if (tk0 + u < k1) {
-        f16x2 l0, h0, l1, h1;
-        decode4<K>(w0[u], B.g0.sh, l0, h0);
-        decode4<K>(w1[u], B.g1.sh, l1, h1);
-        const f16x8 bv = {l0.x, l0.y, h0.x, h0.y, l1.x, l1.y, h1.x, h1.y};
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[u], bv, acc, 0, 0, 0);
-      }
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < 16; i++) {
-    const int r = 4 * (lane >> 5) + (i & 3) + 8 * (i >> 2);
-    if (r < a.R) a.part[((uint64_t)s * a.R + r) * OTp * 16 + p * 32 + (lane & 31)] = acc[i];
-  }
-}
-
 // lin_finish: y = H_out(sum over splits in order) * svh (reference kernels/trunk6/trunk6.metal:199-214),
 // grid R x ceil(out/128).
 __global__ __launch_bounds__(64) void lin_finish(LinArgs a) {
@@ -856,18 +801,12 @@ static const void *lin_step_any(int K, int RT) {
 }
 static int rows_tier(int R) { return R <= 1 ? 1 : R <= 2 ? 2 : R <= 4 ? 4 : 8; }
 
-static const void *lin_mfma_any(int K) {
-  const void *f = nullptr;
-  IJ_DISPATCH_K(K, f = (const void *)&lin_mfma<KK>);
-  return f;
-}
 
 void launch_lin(const LinArgs &a, hipStream_t s) {
   const int NP = (a.OT + 1) / 2;
   if (a.R > kLinSimdRows || !a.cnt) hipLaunchKernelGGL(lin_prep, dim3(a.R * ((a.in + 127) / 128)), dim3(64), 0, s, a);
   if (a.R > kLinSimdRows) {
-    void *args[] = {const_cast<LinArgs *>(&a)};
-    IJ_HIP(hipLaunchKernel(lin_mfma_any(a.K), dim3((NP * a.S + 3) / 4), dim3(256), args, 0, s));
+    launch_lin_mm(a, s);
     hipLaunchKernelGGL(lin_finish, dim3(a.R * ((a.out + 127) / 128)), dim3(64), 0, s, a);
     return;
   }
@@ -902,7 +841,6 @@ static std::vector<KernelEntry> build_registry() {
   for (int K = 2; K <= 8; K++) {
     v.push_back({"exl3_decode", decode_fn(K), {P, I, I, P}, K, -1});
     for (int RT : {1, 2, 4, 8}) v.push_back({"lin_gemv", lin_gemv_any(K, RT), {(uint32_t)sizeof(LinArgs)}, K, RT});
-    v.push_back({"lin_mfma", lin_mfma_any(K), {(uint32_t)sizeof(LinArgs)}, K, -1});
     for (int RT : {1, 2, 4, 8}) v.push_back({"lin_step", lin_step_any(K, RT), {(uint32_t)sizeof(LinArgs)}, K, RT});
   }
   v.push_back({"lin_prep", (const void *)&lin_prep, {(uint32_t)sizeof(LinArgs)}, -1, -1});

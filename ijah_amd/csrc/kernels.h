@@ -113,9 +113,10 @@ struct LinArgs {
   uint32_t *cnt;          // per 128-column output block, kSyncStride apart, zero between launches; null: the staged
                           // three-kernel path (prep, GEMV, finish)
 };
-// rows up to kLinSimdRows take the VALU GEMV (lin_gemv), more rows (up to kLinMaxRows) the matrix cores (lin_mfma)
+// rows up to kLinSimdRows take the VALU GEMV (lin_gemv), more rows (up to kLinMaxRows) the matrix cores (lin_mm)
 constexpr int kLinSimdRows = 8, kLinMaxRows = 32;
 void launch_lin(const LinArgs &a, hipStream_t s);
+void launch_lin_mm(const LinArgs &a, hipStream_t s);  // rows kLinSimdRows+1 .. kLinMaxRows (matrix cores)
 // W' fp16 bits [IT*16][OT*16] from re-laid tiles
 void launch_decode(const uint32_t *tiles, int IT, int OT, int K, uint16_t *w, hipStream_t s);
 

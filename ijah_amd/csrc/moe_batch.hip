@@ -421,7 +421,7 @@ __device__ __forceinline__ void decode_step(const uint8_t *src, const BLane<K> &
 __device__ __forceinline__ int a_swz(int r) { return ((r >> 1) ^ ((r >> 3) & 1)) & 3; }
 template <int K, int NA>
 __device__ void chunk_gemm(const uint16_t *A, int lda, int ahalf, int aidx, int nrows, const uint8_t *tr, int IT,
-                           int pair, uint8_t *lds, f32x16 (&acc)[kRowBlocks], uint64_t *dbg) {
+                           int pair, uint8_t *lds, f32x16 (&acc)[kRowBlocks], uint64_t *dbg, int kt0, int nkt) {
   using Io = GemmIo<K, NA>;
 #ifdef IJ_BATCH_TRACE  // debug builds only: shader-clock stamps of step 20 per (workgroup, wave)
   uint64_t *drow = dbg ? dbg + ((uint64_t)8192 + blockIdx.x * 8 + (threadIdx.x >> 6)) * 8 : nullptr;
@@ -431,7 +431,7 @@ __device__ void chunk_gemm(const uint16_t *A, int lda, int ahalf, int aidx, int 
 #define IJ_STAMP(t_, f_)
 #endif
   constexpr int DA = Io::DA, U = Io::RB;  // the k loop is unrolled by the B ring's length
-  const int lane = threadIdx.x & 63, NS = IT / 2;
+  const int lane = threadIdx.x & 63, NS = nkt / 2;  // k tiles [kt0, kt0 + nkt) of IT (nkt even)
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   uint8_t *ring_a = lds;
   uint8_t *ring_b = lds + Io::RA * Io::AB + wave * Io::RB * Io::PB;
@@ -447,14 +447,15 @@ __device__ void chunk_gemm(const uint16_t *A, int lda, int ahalf, int aidx, int 
   // fixed per-lane offset.
   const int rr = min(wave * 16 + (lane >> 2), nrows - 1);
   const uint32_t a_off = (uint32_t)(rr * lda + ((lane & 3) ^ a_swz(lane >> 2)) * 8) * 2;
-  const __amdgpu_buffer_rsrc_t ra = stream_rsrc(A);
+  const __amdgpu_buffer_rsrc_t ra = stream_rsrc(A + kt0 * 16);
   auto issue_a = [&](int t, int slot) {
 #pragma unroll
     for (int o = 0; o < NA; o++)
       dma16_buf(ra, a_off, (uint32_t)(o * ahalf * 2 + t * 64), ring_a + slot * Io::AB + o * kChunkRows * 64 + wave * 1024);
   };
   // B(t): the wave's pair at k tiles 2t, 2t + 1 (contiguous)
-  const __amdgpu_buffer_rsrc_t rb = stream_rsrc(tr + (uint64_t)__builtin_amdgcn_readfirstlane(pair) * IT * 2 * Io::TB);
+  const __amdgpu_buffer_rsrc_t rb =
+      stream_rsrc(tr + ((uint64_t)__builtin_amdgcn_readfirstlane(pair) * IT + kt0) * 2 * Io::TB);
   auto issue_b = [&](int t, int slot) {
 #pragma unroll
     for (uint32_t o = 0; o < Io::PB; o += 1024)
@@ -521,9 +522,9 @@ __global__ __launch_bounds__(512, 4) void bat_gateup(MoeArgs a, const uint32_t *
   const uint16_t *A = xh + (uint64_t)row0 * 2 * a.hid;  // [row][gate | up][hid]
   const int pair = ib * 4 + (wave & 3);
   if (e >= a.ne)
-    chunk_gemm<KS, 2>(A, 2 * a.hid, a.hid, proj, nrows, blk + tr_of(a, e, proj), a.hid / 16, pair, lds, acc, a.trace);
+    chunk_gemm<KS, 2>(A, 2 * a.hid, a.hid, proj, nrows, blk + tr_of(a, e, proj), a.hid / 16, pair, lds, acc, a.trace, 0, a.hid / 16);
   else
-    chunk_gemm<K, 2>(A, 2 * a.hid, a.hid, proj, nrows, blk + tr_of(a, e, proj), a.hid / 16, pair, lds, acc, a.trace);
+    chunk_gemm<K, 2>(A, 2 * a.hid, a.hid, proj, nrows, blk + tr_of(a, e, proj), a.hid / 16, pair, lds, acc, a.trace, 0, a.hid / 16);
   // epilogue per 32-row block: columns to LDS as [32][256] f32 (gate 0..127, up 128..255), then one wave per row
   float *ot = (float *)lds;
   const uint16_t *svg = (const uint16_t *)(blk + sv_of(a, e, 0)) + ib * 128;
@@ -583,9 +584,9 @@ __global__ __launch_bounds__(512, 4) void bat_down(MoeArgs a, const uint32_t *bk
   f32x16 acc[kRowBlocks];
   const uint16_t *A = hh + (uint64_t)row0 * a.inter;
   if (e >= a.ne)
-    chunk_gemm<KS, 1>(A, a.inter, 0, 0, nrows, blk + tr_of(a, e, 2), a.inter / 16, ob2 * 8 + wave, lds, acc, nullptr);
+    chunk_gemm<KS, 1>(A, a.inter, 0, 0, nrows, blk + tr_of(a, e, 2), a.inter / 16, ob2 * 8 + wave, lds, acc, nullptr, 0, a.inter / 16);
   else
-    chunk_gemm<K, 1>(A, a.inter, 0, 0, nrows, blk + tr_of(a, e, 2), a.inter / 16, ob2 * 8 + wave, lds, acc, nullptr);
+    chunk_gemm<K, 1>(A, a.inter, 0, 0, nrows, blk + tr_of(a, e, 2), a.inter / 16, ob2 * 8 + wave, lds, acc, nullptr, 0, a.inter / 16);
   if (mt < nrows) {
     const int tok = sl / a.nslot, k = sl % a.nslot;
     m_dst[mt] = sl;
@@ -637,6 +638,49 @@ __global__ __launch_bounds__(256) void bat_combine(MoeArgs a, const float *__res
     y.w += v.w;
   }
   *(float4 *)(a.y + (uint64_t)r * a.hid + i) = y;
+}
+
+// ---------------------------------------------------------------------------------------------------- trunk
+// A trunk linear at 9..32 rows on the same grouped GEMM (reference kernels/trunk6/trunk6.metal:431-539, t6_nax):
+// workgroup (g, s) multiplies the prepared rows xh (fp16, kp order) by tile pairs 8g .. 8g + 7 (one per wave) over k
+// split s; part[s][r][OTp * 16] as the GEMV path, summed and rotated by lin_finish.
+template <int K>
+__global__ __launch_bounds__(512, 4) void lin_mm(LinArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const int NP = (a.OT + 1) / 2, OTp = 2 * NP, NG = (NP + kWavesG - 1) / kWavesG;
+  const int g = blockIdx.x % NG, s = blockIdx.x / NG, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int p = g * kWavesG + wave, span = a.IT / a.S;
+  f32x16 acc[kRowBlocks];
+  chunk_gemm<K, 1>(a.xh, a.in, 0, 0, a.R, (const uint8_t *)a.tiles, a.IT, min(p, NP - 1), lds, acc, nullptr, s * span,
+                   span);
+  if (p >= NP) return;
+#pragma unroll
+  for (int i = 0; i < 16; i++) {
+    const int r = 4 * (lane >> 5) + (i & 3) + 8 * (i >> 2);
+    if (r < a.R) a.part[((uint64_t)s * a.R + r) * OTp * 16 + p * 32 + (lane & 31)] = acc[0][i];
+  }
+}
+template <int K>
+static void lin_mm_launch(const LinArgs &a, hipStream_t s) {
+  const size_t lds = GemmIo<K, 1>::LDS;
+  static bool attr = false;
+  if (!attr) {
+    IJ_HIP(hipFuncSetAttribute((const void *)&lin_mm<K>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    attr = true;
+  }
+  const int NG = ((a.OT + 1) / 2 + kWavesG - 1) / kWavesG;
+  hipLaunchKernelGGL(lin_mm<K>, dim3(NG * a.S), dim3(64 * kWavesG), lds, s, a);
+}
+void launch_lin_mm(const LinArgs &a, hipStream_t s) {
+  switch (a.K) {
+    case 2: lin_mm_launch<2>(a, s); break;
+    case 3: lin_mm_launch<3>(a, s); break;
+    case 4: lin_mm_launch<4>(a, s); break;
+    case 5: lin_mm_launch<5>(a, s); break;
+    case 6: lin_mm_launch<6>(a, s); break;
+    case 7: lin_mm_launch<7>(a, s); break;
+    default: lin_mm_launch<8>(a, s); break;
+  }
 }
 
 // ---------------------------------------------------------------------------------------------------- host side
