@@ -84,10 +84,6 @@ __device__ __forceinline__ uint64_t sv_of(const MoeArgs &a, int e, int proj) {
 
 }  // namespace
 
-__global__ __launch_bounds__(1024) void bat_zero(uint32_t *p, int n) {
-  for (int i = threadIdx.x; i < n; i += 1024) p[i] = 0u;
-}
-
 // ---------------------------------------------------------------------------------------------------- router
 // logits[r][c] = bf16(x[r] . router[c]) for c < ne + has_sgate on the matrix cores. A workgroup covers 32 rows and
 // CT 32-column tiles; its 8 waves are CT column tiles x KSP k splits, summed in LDS in split order. Few rows take
@@ -232,6 +228,7 @@ __global__ __launch_bounds__(1024) void bat_scan(MoeArgs a, uint32_t *bk, uint32
   sc[tid] = c;
   cc[tid] = (c + kChunkRows - 1) / kChunkRows;
   __syncthreads();
+  if (tid <= a.ne) counts[tid] = 0u;  // zero for the next launch's bat_route (zero at allocation for the first)
   for (int d = 1; d < 1024; d <<= 1) {  // inclusive Hillis-Steele scans of rows and chunks
     const uint32_t v = tid >= d ? sc[tid - d] : 0u, w = tid >= d ? cc[tid - d] : 0u;
     __syncthreads();
@@ -712,7 +709,6 @@ int moe_batch_max_chunks(int R, int ne, int topk, bool shared) {
 
 void launch_moe_batch(const MoeArgs &a, const MoeBatchBufs &b, hipStream_t s) {
   const int ncol = a.ne + a.has_sgate, S = a.R * a.nslot;
-  hipLaunchKernelGGL(bat_zero, dim3(1), dim3(1024), 0, s, b.bk, a.ne + 1);  // a kernel, not a memset node
   if (a.R >= 512)
     hipLaunchKernelGGL(bat_router<4>, dim3((a.R + 31) / 32, (ncol + 127) / 128), dim3(64 * kRouterWaves), 0, s, a);
   else
