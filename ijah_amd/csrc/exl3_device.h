@@ -243,5 +243,10 @@ __device__ __forceinline__ uint32_t topk_key(float v, int i) {
   u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
   return (u & 0xFFFF0000u) | (0xFFFFu - (uint32_t)i);
 }
+// bf16-valued logit back from its order key (the inverse of topk_key on the top 16 bits)
+__device__ __forceinline__ float key_value(uint32_t key) {
+  const uint32_t h = key >> 16;
+  return __uint_as_float((h & 0x8000u) ? (h & 0x7FFFu) << 16 : (~h & 0xFFFFu) << 16);
+}
 
 }  // namespace ijah

@@ -5,10 +5,10 @@
 //
 // Launches, in order:
 //   bat_router   logits[R][ne (+ shared gate)] = bf16(x . router) in f32 (reference kernels/fn_moe.metal:50-67)
-//   bat_route    per row: top-k, ties to the lower index, weights exp(l - l_max) / sum (kernels/fn_moe.metal:76-131);
-//                counts the routed slots per expert
-//   bat_scan     per-expert offsets of the expert-sorted slot list (the shared expert's rows last) and the list of
-//                128-row chunks (expert, first row, rows) the GEMMs run over (kernels/prefill/pf_moe.metal:26-83)
+//   bat_route    per row: top-k, ties to the lower index, weights exp(l - l_max) / sum (kernels/fn_moe.metal:76-131)
+//   bat_scan     one workgroup: slots per expert (a histogram of the route in LDS), per-expert offsets of the
+//                expert-sorted slot list (the shared expert's rows last) and the list of 128-row chunks (expert,
+//                first row, rows) the GEMMs run over (kernels/prefill/pf_moe.metal:26-83)
 //   bat_place_prep  one wave per slot: its place in its expert's rows (row order inside an expert does not change
 //                any result: every row is computed independently) and that row of the A operand,
 //                xh[row][proj] = fp16(H(x[token] * suh_e,proj)) in kp order for the gate and the up projection (each
@@ -161,11 +161,12 @@ __global__ __launch_bounds__(512) void bat_router(MoeArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------------------- route
-// one wave per row; also counts each routed slot in counts[expert]
+// one wave per row
 template <int J>
-__device__ void route_one(const MoeArgs &a, int r, uint32_t *counts) {
+__device__ void route_one(const MoeArgs &a, int r) {
   const int lane = threadIdx.x & 63;
   const float *lg = a.logits + (uint64_t)r * (a.ne + 1);
+  const float sgl = a.has_sgate ? lg[a.ne] : 0.f;  // the shared-expert gate logit, requested with the others
   uint32_t key[J];
 #pragma unroll
   for (int j = 0; j < J; j++) {
@@ -194,25 +195,25 @@ __device__ void route_one(const MoeArgs &a, int r, uint32_t *counts) {
     for (int j = 0; j < J - 1; j++) key[j] = win ? key[j + 1] : key[j];
     key[J - 1] = win ? 0u : key[J - 1];
   }
-  const uint32_t id = lane < a.topk ? 0xFFFFu - (mykey & 0xFFFFu) : 0u;  // lanes past topk read logit 0
-  const float top = lg[__builtin_amdgcn_readlane((int)id, 0)];
-  const float pk = lane < a.topk ? expf(lg[id] - top) : 0.f;
+  const uint32_t id = lane < a.topk ? 0xFFFFu - (mykey & 0xFFFFu) : 0u;  // lanes past topk: expert 0, unused
+  // the selected logits come back out of their keys (no second load), as in the fused step
+  const float top = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(key_value(mykey)), 0));
+  const float pk = lane < a.topk ? expf(key_value(mykey) - top) : 0.f;
   float sum = 0.f;
   for (int k = 0; k < a.topk; k++) sum += __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(pk), k));
   if (lane < a.topk) {
     a.route[(uint64_t)r * 2 * a.topk + lane] = id;
     a.route[(uint64_t)r * 2 * a.topk + a.topk + lane] = __float_as_uint(pk / sum);
-    atomicAdd(counts + id, 1u);
   }
-  if (lane == 0) a.sgv[r] = a.has_sgate ? 1.f / (1.f + expf(-lg[a.ne])) : 1.f;
+  if (lane == 0) a.sgv[r] = a.has_sgate ? 1.f / (1.f + expf(-sgl)) : 1.f;
 }
-__global__ __launch_bounds__(256) void bat_route(MoeArgs a, uint32_t *counts) {
+__global__ __launch_bounds__(256) void bat_route(MoeArgs a) {
   const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (r >= a.R) return;
   if (a.ne <= 512)
-    route_one<8>(a, r, counts);
+    route_one<8>(a, r);
   else
-    route_one<16>(a, r, counts);
+    route_one<16>(a, r);
 }
 
 // ---------------------------------------------------------------------------------------------------- sort
@@ -222,13 +223,51 @@ __global__ __launch_bounds__(1024) void bat_scan(MoeArgs a, uint32_t *bk, uint32
   __shared__ uint32_t sc[1024 + 1], cc[1024 + 1];
   const int tid = threadIdx.x, n = a.ne + (a.nslot > a.topk ? 1 : 0);
   uint32_t *counts = bk, *offs = bk + (a.ne + 1), *cursor = offs + (a.ne + 1), *nchunks = cursor + (a.ne + 1);
-  if (a.nslot > a.topk && tid == 0) counts[a.ne] = (uint32_t)a.R;
+  // routed slots per expert: a histogram of the route ids in LDS (one workgroup: no global atomics to contend)
+  // The route is [R][2 topk] words (ids, then weights): each thread takes a contiguous run of whole 16-byte groups,
+  // loaded together, and adds the ids among them.
+  sc[tid] = 0u;
   __syncthreads();
-  const uint32_t c = tid < n ? counts[tid] : 0u;
+  {
+    const int stride = 2 * a.topk, total = a.R * stride, groups = (total + 3) / 4;
+    const int per = (groups + 1023) / 1024, g0 = tid * per, g1 = min(g0 + per, groups);
+    constexpr int B = 8;  // groups requested at once
+    int col = (g0 * 4) % stride;  // column of the next word inside its row (ids below topk)
+    for (int g = g0; g < g1; g += B) {
+      uint4 v[B];
+#pragma unroll
+      for (int j = 0; j < B; j++)
+        if (g + j < g1) {
+          if ((g + j) * 4 + 4 <= total) {
+            v[j] = *(const uint4 *)(a.route + (size_t)(g + j) * 4);
+          } else {  // the last, partial group
+            const uint32_t *w = a.route + (size_t)(g + j) * 4;
+            const int left = total - (g + j) * 4;
+            v[j] = make_uint4(w[0], left > 1 ? w[1] : 0u, left > 2 ? w[2] : 0u, 0u);
+          }
+        }
+#pragma unroll
+      for (int j = 0; j < B; j++)
+        if (g + j < g1) {
+          const uint32_t w4[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+#pragma unroll
+          for (int q = 0; q < 4; q++) {
+            if ((g + j) * 4 + q < total && col < a.topk) {
+              const uint32_t e = w4[q];
+              atomicAdd(&sc[e < (uint32_t)a.ne ? e : 0u], 1u);
+            }
+            col = col + 1 == stride ? 0 : col + 1;
+          }
+        }
+    }
+  }
+  __syncthreads();
+  const uint32_t c = tid < a.ne ? sc[tid] : (tid < n ? (uint32_t)a.R : 0u);  // the shared expert takes every row
+  __syncthreads();
+  if (tid < n) counts[tid] = c;
   sc[tid] = c;
   cc[tid] = (c + kChunkRows - 1) / kChunkRows;
   __syncthreads();
-  if (tid <= a.ne) counts[tid] = 0u;  // zero for the next launch's bat_route (zero at allocation for the first)
   for (int d = 1; d < 1024; d <<= 1) {  // inclusive Hillis-Steele scans of rows and chunks
     const uint32_t v = tid >= d ? sc[tid - d] : 0u, w = tid >= d ? cc[tid - d] : 0u;
     __syncthreads();
@@ -361,7 +400,7 @@ __host__ __device__ constexpr int after_step(int t, int NS) {
   const int pa = mn(DA, NS), pb = mn(DB, NS);
   const int prologue = OA * pa + OB * pb;
   const int total = prologue + sum_ops(t);
-  int last;  // one past the position of the later of A(t), B(t)
+  int last = 0;  // one past the position of the later of A(t), B(t)
   if (t < DA) {
     last = (OA + OB) * (t + 1);
   } else if (t < DB) {
@@ -713,7 +752,7 @@ void launch_moe_batch(const MoeArgs &a, const MoeBatchBufs &b, hipStream_t s) {
     hipLaunchKernelGGL(bat_router<4>, dim3((a.R + 31) / 32, (ncol + 127) / 128), dim3(64 * kRouterWaves), 0, s, a);
   else
     hipLaunchKernelGGL(bat_router<1>, dim3((a.R + 31) / 32, (ncol + 31) / 32), dim3(64 * kRouterWaves), 0, s, a);
-  hipLaunchKernelGGL(bat_route, dim3((a.R + 3) / 4), dim3(256), 0, s, a, b.bk);
+  hipLaunchKernelGGL(bat_route, dim3((a.R + 3) / 4), dim3(256), 0, s, a);
   hipLaunchKernelGGL(bat_scan, dim3(1), dim3(1024), 0, s, a, b.bk, b.chunks, b.max_chunks);
   if (S >= 8192)
     hipLaunchKernelGGL(bat_place_prep<1>, dim3((S + 3) / 4), dim3(256), 0, s, a, b.bk, b.rows, b.xh);

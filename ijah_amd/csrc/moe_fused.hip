@@ -160,11 +160,6 @@ __device__ __forceinline__ void router_row(const MoeArgs &a, const uint32_t *tag
   if (lane < kLogitReplicas) st_cg((uint32_t *)a.logits + lane * stride + row, v);
 }
 
-// bf16-valued logit back from its order key (the inverse of topk_key on the top 16 bits)
-__device__ __forceinline__ float key_value(uint32_t key) {
-  const uint32_t h = key >> 16;
-  return __uint_as_float((h & 0x8000u) ? (h & 0x7FFFu) << 16 : (~h & 0xFFFFu) << 16);
-}
 // descending bitonic sort of J keys held in registers (J a power of two; compile-time indices)
 template <int J>
 __device__ __forceinline__ void sort_desc(uint32_t (&k)[J]) {
