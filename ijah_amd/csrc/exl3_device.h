@@ -146,6 +146,7 @@ __device__ __forceinline__ TileWords load_tile(const uint32_t *__restrict__ T, c
 // ------------------------------------------------------------------------------------------------ matrix cores
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 // The matrix-core B operand of lane l is column n = l % 32 of the pair (tile n / 16, column c = n % 16), k values
 // 8 (l / 32) .. + 8: the trellis groups (c, q) with q = 2 (l / 32) and q + 1, four consecutive k each. Group m of a
 // tile (weights 4m .. 4m + 3 of the bitstream) holds column c = (m >> 3) + 8 (m & 1), k quarter q = (m >> 1) & 3.

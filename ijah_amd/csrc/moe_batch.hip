@@ -82,6 +82,15 @@ __device__ __forceinline__ uint64_t sv_of(const MoeArgs &a, int e, int proj) {
   return proj == 0 ? L.sv[0] : proj == 1 ? L.sv[1] : L.sv[2];
 }
 
+// Work item of this workgroup for a 1-D grid over nitems items (grid a multiple of 8): consecutive workgroups go to
+// the 8 XCDs in turn, so each XCD takes a contiguous eighth of the items; items that share an operand (the column
+// blocks of one chunk) then run together on one XCD and share its L2. False for workgroups past the work.
+__device__ __forceinline__ bool xcd_item(int nitems, int &item) {
+  const int b = blockIdx.x, xcd = b & 7, idx = b >> 3, q = nitems >> 3, r = nitems & 7;
+  if (idx >= q + (xcd < r ? 1 : 0)) return false;
+  item = xcd * q + min(xcd, r) + idx;
+  return true;
+}
 }  // namespace
 
 // ---------------------------------------------------------------------------------------------------- router
@@ -157,6 +166,90 @@ __global__ __launch_bounds__(512) void bat_router(MoeArgs a) {
     for (int k = 0; k < KSP; k++) v += red[k * CT + c][i][l];
     const int r = rt * 32 + 4 * (l >> 5) + (i & 3) + 8 * (i >> 2), cc = (blockIdx.y * CT + c) * 32 + (l & 31);
     if (r < a.R && cc < ncol) a.logits[(uint64_t)r * (a.ne + 1) + cc] = bf16_round(v);
+  }
+}
+
+// Many rows: a workgroup covers 64 rows x 128 columns over the whole k range, wave (rb, ct) = wave (rb = wave / 4,
+// ct = wave % 4) one 32 x 32 tile. The x rows are shared by the four column waves, so the workgroup stages each
+// 64-wide k chunk of them once through LDS, already split into bf16 hi and lo (the conversion runs once per element
+// per workgroup, and the rows cross from L2 once); each wave streams its own router columns from memory one chunk
+// ahead. Same arithmetic as bat_router (hi and lo products summed in f32), one k order.
+constexpr int kRtKc = 64, kRtRows = 64, kRtPitch = kRtKc + 8;  // k chunk, rows, LDS row pitch in bf16 (conflict-free)
+__global__ __launch_bounds__(512, 2) void bat_router_rows(MoeArgs a, int ngroups) {
+  __shared__ __attribute__((aligned(16))) __bf16 xs[2][2][kRtRows * kRtPitch];  // [buffer][hi, lo]
+  int item;
+  if (!xcd_item(ngroups * ((a.ne + a.has_sgate + 127) / 128), item)) return;
+  const int ncol = a.ne + a.has_sgate, ncg = (ncol + 127) / 128, rg = item / ncg, cg = item % ncg;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, rb = wave >> 2, ct = cg * 4 + (wave & 3);
+  const int m = lane & 31, h = lane >> 5;
+  const bool live = ct * 32 < ncol;
+  // staging: thread t converts row t / 8, k [8 (t % 8), +8) of the chunk
+  const int srow = threadIdx.x >> 3, sk = (threadIdx.x & 7) * 8;
+  const float *xp = a.x + (uint64_t)min(rg * kRtRows + srow, a.R - 1) * a.hid + sk;
+  const uint16_t *wp = a.router + (uint64_t)min(ct * 32 + m, ncol - 1) * a.hid + 8 * h;
+  const int nch = a.hid / kRtKc;
+  float4 xr[2];
+  uint4 wv[2][kRtKc / 16];
+  auto load_x = [&](int c) {
+    xr[0] = *(const float4 *)(xp + c * kRtKc);
+    xr[1] = *(const float4 *)(xp + c * kRtKc + 4);
+  };
+  auto load_w = [&](int b, int c) {
+#pragma unroll
+    for (int u = 0; u < kRtKc / 16; u++) wv[b][u] = *(const uint4 *)(wp + c * kRtKc + 16 * u);
+  };
+  auto stage = [&](int b) {
+    const float v[8] = {xr[0].x, xr[0].y, xr[0].z, xr[0].w, xr[1].x, xr[1].y, xr[1].z, xr[1].w};
+    bf16x8 hi, lo;
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      hi[e] = (__bf16)v[e];
+      lo[e] = (__bf16)(v[e] - (float)hi[e]);
+    }
+    *(bf16x8 *)&xs[b][0][srow * kRtPitch + sk] = hi;
+    *(bf16x8 *)&xs[b][1][srow * kRtPitch + sk] = lo;
+  };
+  f32x16 acc;
+#pragma unroll
+  for (int i = 0; i < 16; i++) acc[i] = 0.f;
+  auto mul = [&](int b) {
+    const __bf16 *ph = &xs[b][0][(rb * 32 + m) * kRtPitch + 8 * h], *pl = &xs[b][1][(rb * 32 + m) * kRtPitch + 8 * h];
+#pragma unroll
+    for (int u = 0; u < kRtKc / 16; u++) {
+      const bf16x8 hi = *(const bf16x8 *)(ph + 16 * u), lo = *(const bf16x8 *)(pl + 16 * u);
+      const bf16x8 wb = __builtin_bit_cast(bf16x8, wv[b][u]);
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(hi, wb, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(lo, wb, acc, 0, 0, 0);
+    }
+  };
+  // chunk c: stage it (its x already in registers), request chunk c + 1, one barrier, multiply. The buffer written
+  // at chunk c + 1 was last read at chunk c - 1, before every wave passed chunk c's barrier.
+  load_x(0);
+  if (live) load_w(0, 0);
+  for (int c = 0; c < nch; c += 2) {
+    stage(0);
+    if (c + 1 < nch) {
+      load_x(c + 1);
+      if (live) load_w(1, c + 1);
+    }
+    __syncthreads();
+    if (live) mul(0);
+    if (c + 1 < nch) {
+      stage(1);
+      if (c + 2 < nch) {
+        load_x(c + 2);
+        if (live) load_w(0, c + 2);
+      }
+      __syncthreads();
+      if (live) mul(1);
+    }
+  }
+  if (!live) return;
+  const int cc = ct * 32 + m;
+#pragma unroll
+  for (int i = 0; i < 16; i++) {
+    const int r = rg * kRtRows + rb * 32 + 4 * h + (i & 3) + 8 * (i >> 2);
+    if (r < a.R && cc < ncol) a.logits[(uint64_t)r * (a.ne + 1) + cc] = bf16_round(acc[i]);
   }
 }
 
@@ -291,14 +384,51 @@ __global__ __launch_bounds__(1024) void bat_scan(MoeArgs a, uint32_t *bk, uint32
 // One wave per slot (r, k): takes the slot's row in its expert's list (rows[row] = r * nslot + k; k == topk: the
 // shared expert, whose list is every token in order) and writes that row of the A operand:
 // xh[row] = [gate | up] fp16(H(x[r] * suh_e)) in kp order (the two projections have their own suh).
-// WPS waves per slot (1 for many rows; 4 for few, so that they still fill the chip), each a quarter of the blocks.
-template <int WPS>
-__global__ __launch_bounds__(256) void bat_place_prep(MoeArgs a, uint32_t *bk, uint32_t *rows, uint16_t *xh) {
-  __shared__ uint32_t s_row;
-  const int lane = threadIdx.x & 63, wq = (int)(threadIdx.x >> 6) % WPS;
-  const int s = blockIdx.x * (4 / WPS) + (int)(threadIdx.x >> 6) / WPS;
-  if (WPS == 1 && s >= a.R * a.nslot) return;
+// The 128-wide Hadamard runs on the matrix cores. H_128 = H_4 (x) H_32 in the split i = 32 q + j, so for the 32
+// vectors of a tile (gate and up of 16 blocks) the wave multiplies each 32-chunk q' by H_32
+// (v_mfma_f32_32x32x16_f16, H as the A operand, the vectors as B), then combines the four chunk products with H_4 in
+// registers. The rows of H_32 are permuted so that output row m lands where the matrix-core layout lets one lane
+// hold 16 consecutive kp positions (16 h + i, i = 0..15, of each 32-chunk): every lane then stores 32 contiguous
+// bytes per chunk. Each vector is scaled by a power of two (its largest element to [2^14, 2^15)) and split into f16
+// hi + lo, both rounded to nearest (about 23 bits reach the products, summed in f32): a result differs from a
+// butterfly transform's by f32 rounding only.
+__device__ __forceinline__ uint32_t kp_inv32(uint32_t u) {  // kp restricted to 0..31, inverted
+  return (u & 16u) | (((u >> 1) & 1u) << 3) | (((u >> 2) & 3u) << 1) | (u & 1u);
+}
+// LDS per wave (16-byte units; a pad unit after every 64, so a direct-to-LDS load of 64 lanes fills one run):
+//   x part:  block b of the tile (128 f32 = 32 units) in run b / 2; an odd block is rotated by 8 units:
+//            unit u of block b at 65 (b / 2) + 32 (b % 2) + ((u + 8 (b % 2)) % 32)
+//   su part: projection p, block b (128 f16 = 16 units) at 260 p + 65 (b / 4) + 16 (b % 4) + ((u + 4 (b % 4)) % 16)
+//   output (reuses the x part): vector v (32 = gate blocks, then up blocks; 16 units) at
+//            65 (v / 4) + 16 (v % 4) + ((c + 4 (v % 4)) % 16)
+// With these, every matrix-core fragment read and every output write of 8 consecutive lanes hits 8 distinct 4-bank
+// groups, each lane's unit offsets differ from one per-lane base by compile-time amounts, and each load lane's
+// source offset is the same for all runs (the loads are 1 KB contiguous each: loading the fragments straight into
+// registers, 16 scattered bytes per lane, is slower).
+constexpr int kPrepUnits = 1040;  // x / output part 520 units, su part 520
+constexpr int kPrepWaves = 4;
+constexpr size_t kPrepLds = (size_t)kPrepWaves * kPrepUnits * 16;
+__global__ __launch_bounds__(64 * kPrepWaves, 2) void bat_place_prep(MoeArgs a, uint32_t *bk, uint32_t *rows,
+                                                                      uint16_t *xh) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int s = blockIdx.x * kPrepWaves + wave;  // wave-uniform, so the row's buffer descriptors are too
+  if (s >= a.R * a.nslot) return;
+  uint8_t *lx = lds + (size_t)wave * kPrepUnits * 16, *lsu = lx + 520 * 16;
   const int r = s / a.nslot, k = s % a.nslot;
+  const int n = lane & 31, h = lane >> 5, proj = n >> 4, bl = n & 15, nb = a.hid / 128;
+  const float *x = a.x + (uint64_t)r * a.hid;
+  // load lanes: source byte offsets inside a run (x: two blocks of 512 B; su: four blocks of 256 B)
+  const uint32_t vx = lane < 32 ? 16u * lane : 512u + 16u * ((lane - 40) & 31);
+  const uint32_t vs = 256u * (lane >> 4) + 16u * (((lane & 15) - 4 * (lane >> 4)) & 15);
+  // the tile's x (blocks past the row's end read zeros); the first tile's is requested before the route is read
+  auto load_x = [&](int t0) {
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void *)(x + t0 * 128), (short)0,
+                                                                        (a.hid - t0 * 128) * 4, 0x00020000);
+#pragma unroll
+    for (int j = 0; j < 8; j++) dma16_buf(rx, vx, 1024u * j, lx + 65 * 16 * j);
+  };
+  load_x(0);
   const uint32_t *offs = bk + (a.ne + 1);
   uint32_t *cursor = bk + 2 * (a.ne + 1);
   int e = a.ne;
@@ -306,50 +436,126 @@ __global__ __launch_bounds__(256) void bat_place_prep(MoeArgs a, uint32_t *bk, u
     e = (int)a.route[(uint64_t)r * 2 * a.topk + k];
     e = e < a.ne ? e : 0;
   }
-  uint32_t row = 0u;
-  if (lane == 0 && wq == 0) {
-    row = k >= a.topk ? offs[a.ne] + (uint32_t)r : offs[e] + atomicAdd(cursor + e, 1u);
-    rows[row] = (uint32_t)s;
-    if (WPS > 1) s_row = row;
-  }
-  if (WPS > 1) {
-    __syncthreads();
-    row = s_row;
-  }
-  row = (uint32_t)__builtin_amdgcn_readfirstlane(row);
-  const uint16_t *sug = (const uint16_t *)(expert_block(a, e) + su_of(a, e, 0));
-  const uint16_t *suu = (const uint16_t *)(expert_block(a, e) + su_of(a, e, 1));
-  const float *x = a.x + (uint64_t)r * a.hid;
-  uint16_t *out = xh + (uint64_t)row * 2 * a.hid;
-  constexpr int U = 4;  // blocks whose loads are all issued before the first store
-  const int nb = a.hid / 128;
-  for (int c0 = wq; c0 < nb; c0 += U * WPS) {
-    float g[U][2], u[U][2];
+  e = __builtin_amdgcn_readfirstlane(e);  // one slot per wave: the expert's layout then stays in scalar registers
+  // the slot's row, first needed by the stores: both requests are issued by hand and waited for with the tile's loads
+  // (the compiler would wait for the atomic's result right here, and sink the offset's load to its use)
+  uint32_t pos = (uint32_t)r, base;  // the shared expert's list is every token in order
+  asm volatile("global_load_dword %0, %1, off" : "=v"(base) : "v"(offs + e) : "memory");
+  if (lane == 0 && k < a.topk)
+    asm volatile("global_atomic_add %0, %1, %2, off sc0" : "=v"(pos) : "v"(cursor + e), "v"(1u) : "memory");
+  // A operand: lane (m = n, h) holds H_32[j(m)][16 st + 8 h + t] for k steps st = 0, 1, where output row m is kp
+  // position d = 16 ((m >> 2) & 1) + 4 (m >> 3) + (m & 3) of the chunk, i.e. element j(m) = kp^-1(d)
+  f16x8 hA[2];
+  {
+    const uint32_t j = kp_inv32(16u * ((n >> 2) & 1) + 4u * (n >> 3) + (n & 3));
 #pragma unroll
-    for (int j = 0; j < U; j++) {
-      const int c = c0 + j * WPS;
-      if (c < nb) {
-        const int e0 = c * 128 + lane, e1 = e0 + 64;
-        const float x0 = x[e0], x1 = x[e1];
-        g[j][0] = x0 * h2f(sug[e0]);
-        g[j][1] = x1 * h2f(sug[e1]);
-        u[j][0] = x0 * h2f(suu[e0]);
-        u[j][1] = x1 * h2f(suu[e1]);
+    for (int st = 0; st < 2; st++)
+#pragma unroll
+      for (int t = 0; t < 8; t++)
+        hA[st][t] = (__builtin_popcount(j & (uint32_t)(16 * st + 8 * h + t)) & 1) ? (_Float16)-1.f : (_Float16)1.f;
+  }
+  // fragment bases (bytes) per chunk q: x units 8 q + 4 st + 2 h + w, su units 4 q + 2 st + h, output units 4 q + 2 h + w
+  uint32_t xb[4], sb[4], ob[4];
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    const int odd = bl & 1, m4 = bl & 3, v4 = n & 3;
+    xb[q] = 16u * (65 * (bl >> 1) + 32 * odd + 8 * ((q + odd) & 3) + 2 * h);
+    sb[q] = 16u * (260 * proj + 65 * (bl >> 2) + 16 * m4 + 4 * ((q + m4) & 3) + h);
+    ob[q] = 16u * (65 * (n >> 2) + 16 * v4 + 4 * ((q + v4) & 3) + 2 * h);
+  }
+  // store lanes: unit c = lane % 16 of vector 4 j + lane / 16 (store j); its global offset is 16 lane bytes
+  const uint32_t rb = 16u * (16 * (lane >> 4) + (((lane & 15) + 4 * (lane >> 4)) & 15));
+  const uint8_t *eb = expert_block(a, e);
+  const uint16_t *sug = (const uint16_t *)(eb + su_of(a, e, 0)), *suu = (const uint16_t *)(eb + su_of(a, e, 1));
+  uint16_t *orow_p = nullptr;
+  for (int t0 = 0; t0 < nb; t0 += 16) {
+    const int nbl = min(nb - t0, 16);  // blocks of this tile; loads past the row's end read zeros
+    {
+      if (t0 > 0) load_x(t0);
+      const __amdgpu_buffer_rsrc_t rg = __builtin_amdgcn_make_buffer_rsrc((void *)(sug + t0 * 128), (short)0,
+                                                                          (a.hid - t0 * 128) * 2, 0x00020000);
+      const __amdgpu_buffer_rsrc_t ru = __builtin_amdgcn_make_buffer_rsrc((void *)(suu + t0 * 128), (short)0,
+                                                                          (a.hid - t0 * 128) * 2, 0x00020000);
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        dma16_buf(rg, vs, 1024u * j, lsu + 65 * 16 * j);
+        dma16_buf(ru, vs, 1024u * j, lsu + (260 + 65 * j) * 16);
       }
     }
+    asm volatile("s_waitcnt vmcnt(0)" : "+v"(base), "+v"(pos) : : "memory");  // the tile, base and pos arrived
+    // v = x * suh for this lane's 64 elements of vector n, and the vector's largest |v| (lanes n and n + 32)
+    float v[4][2][8];
+    float mx = 0.f;
 #pragma unroll
-    for (int j = 0; j < U; j++) {
-      const int c = c0 + j * WPS;
-      if (c < nb) {
-        fwht2(g[j][0], g[j][1], lane, a.had_hid, a.sc_hid);
-        fwht2(u[j][0], u[j][1], lane, a.had_hid, a.sc_hid);
-        out[c * 128 + kp(lane)] = f2h(g[j][0]);
-        out[c * 128 + kp(lane + 64)] = f2h(g[j][1]);
-        out[a.hid + c * 128 + kp(lane)] = f2h(u[j][0]);
-        out[a.hid + c * 128 + kp(lane + 64)] = f2h(u[j][1]);
+    for (int q = 0; q < 4; q++)
+#pragma unroll
+      for (int st = 0; st < 2; st++) {
+        const float4 x0 = *(const float4 *)(lx + xb[q] + 16 * (4 * st));
+        const float4 x1 = *(const float4 *)(lx + xb[q] + 16 * (4 * st + 1));
+        const f16x8 sh = *(const f16x8 *)(lsu + sb[q] + 16 * (2 * st));
+        const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+          v[q][st][t] = __builtin_fmaf(xv[t], (float)sh[t], 0.f);
+          mx = fmaxf(mx, fabsf(v[q][st][t]));
+        }
       }
+    mx = fmaxf(mx, xor_lane<32>(mx, lane));
+    // exact power-of-two scale putting the largest |v| in [2^14, 2^15): the split then stays clear of both the f16
+    // overflow and its subnormals; the output takes the inverse scale with 1/sqrt(128)
+    const int ex = min(max(141 - (int)((__float_as_uint(mx) >> 23) & 0xFFu), -126), 127);
+    const float osc = __builtin_ldexpf(a.sc_hid, -ex);
+    f32x16 acc[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++)
+#pragma unroll
+      for (int i = 0; i < 16; i++) acc[q][i] = 0.f;
+#pragma unroll
+    for (int q = 0; q < 4; q++)
+#pragma unroll
+      for (int st = 0; st < 2; st++) {
+        f16x8 hi, lo;
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+          const float w = __builtin_ldexpf(v[q][st][t], ex);  // hi, lo rounded to nearest: v - hi exact in f32
+          hi[t] = (_Float16)w;
+          lo[t] = (_Float16)(w - (float)hi[t]);
+        }
+        acc[q] = __builtin_amdgcn_mfma_f32_32x32x16_f16(hA[st], hi, acc[q], 0, 0, 0);
+        acc[q] = __builtin_amdgcn_mfma_f32_32x32x16_f16(hA[st], lo, acc[q], 0, 0, 0);
+      }
+    // H_4 over the chunk products: out_q = sum_q' (-1)^popcount(q & q') T_q', scaled, to f16 in the output part
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      const float a0 = acc[0][i] + acc[1][i], a1 = acc[0][i] - acc[1][i];
+      const float a2 = acc[2][i] + acc[3][i], a3 = acc[2][i] - acc[3][i];
+      acc[0][i] = (a0 + a2) * osc;
+      acc[1][i] = (a1 + a3) * osc;
+      acc[2][i] = (a0 - a2) * osc;
+      acc[3][i] = (a1 - a3) * osc;
     }
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      uint32_t w[8];
+#pragma unroll
+      for (int i = 0; i < 8; i++)
+        w[i] = __builtin_bit_cast(uint32_t, f16x2{(_Float16)acc[q][2 * i], (_Float16)acc[q][2 * i + 1]});
+      *(uint4 *)(lx + ob[q]) = make_uint4(w[0], w[1], w[2], w[3]);
+      *(uint4 *)(lx + ob[q] + 16) = make_uint4(w[4], w[5], w[6], w[7]);
+    }
+    __builtin_amdgcn_wave_barrier();  // one wave's LDS accesses run in order: its writes are seen by its reads
+    // the row: gate at [0, hid), up at [hid, 2 hid); store j covers vectors 4 j .. 4 j + 3, 1 KB contiguous
+    orow_p = xh + (uint64_t)((uint32_t)__builtin_amdgcn_readfirstlane(base) +
+                             (uint32_t)__builtin_amdgcn_readfirstlane(pos)) * 2 * a.hid;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const uint4 w = *(const uint4 *)(lx + rb + 65 * 16 * j);
+      const int vb = 4 * (j & 3) + (lane >> 4);
+      if (vb < nbl) *(uint4 *)((uint8_t *)(orow_p + (j >> 2) * a.hid + (t0 + 4 * (j & 3)) * 128) + 16 * lane) = w;
+    }
+    __builtin_amdgcn_wave_barrier();  // the next tile's loads into LDS come after these reads
   }
+  if (lane == 0) rows[(orow_p - xh) / (2 * a.hid)] = (uint32_t)s;
 }
 
 // ---------------------------------------------------------------------------------------------------- grouped GEMM
@@ -360,15 +566,6 @@ __global__ __launch_bounds__(256) void bat_place_prep(MoeArgs a, uint32_t *bk, u
 // tiles kDB steps ahead, so that enough weight bytes are in flight per CU to cover the memory latency.
 // acc[rb] = rows 32 rb.., the wave's 32 columns, in the matrix-core layout.
 constexpr int kWavesG = 8;
-// Work item of this workgroup for a 1-D grid over nitems items (grid a multiple of 8): consecutive workgroups go to
-// the 8 XCDs in turn, so each XCD takes a contiguous eighth of the items; items that share an operand (the column
-// blocks of one chunk) then run together on one XCD and share its L2. False for workgroups past the work.
-__device__ __forceinline__ bool xcd_item(int nitems, int &item) {
-  const int b = blockIdx.x, xcd = b & 7, idx = b >> 3, q = nitems >> 3, r = nitems & 7;
-  if (idx >= q + (xcd < r ? 1 : 0)) return false;
-  item = xcd * q + min(xcd, r) + idx;
-  return true;
-}
 // Two workgroups share a CU (so four waves per SIMD hide each other's latency): each keeps under 80 KB of LDS.
 // Steps (of 2 k tiles) requested ahead: A kDA, B kDB; the B ring's slot count is a multiple of the A ring's, so that
 // the k loop, unrolled by the B ring's length, addresses every ring slot with compile-time offsets.
@@ -666,12 +863,21 @@ __global__ __launch_bounds__(256) void bat_combine(MoeArgs a, const float *__res
   const int r = blockIdx.x, i = (blockIdx.y * 256 + threadIdx.x) * 4;
   if (i >= a.hid) return;
   float4 y = {0.f, 0.f, 0.f, 0.f};
-  for (int k = 0; k < a.nslot; k++) {
-    const float4 v = *(const float4 *)(dnw + ((uint64_t)r * a.nslot + k) * a.hid + i);
-    y.x += v.x;
-    y.y += v.y;
-    y.z += v.z;
-    y.w += v.w;
+  const float *p = dnw + (uint64_t)r * a.nslot * a.hid + i;
+  constexpr int B = 6;  // slots requested together; summed in slot order
+  for (int k0 = 0; k0 < a.nslot; k0 += B) {
+    f32x4 v[B];
+#pragma unroll
+    for (int j = 0; j < B; j++)
+      if (k0 + j < a.nslot) v[j] = __builtin_nontemporal_load((const f32x4 *)(p + (uint64_t)(k0 + j) * a.hid));
+#pragma unroll
+    for (int j = 0; j < B; j++)
+      if (k0 + j < a.nslot) {
+        y.x += v[j][0];
+        y.y += v[j][1];
+        y.z += v[j][2];
+        y.w += v[j][3];
+      }
   }
   *(float4 *)(a.y + (uint64_t)r * a.hid + i) = y;
 }
@@ -748,16 +954,21 @@ int moe_batch_max_chunks(int R, int ne, int topk, bool shared) {
 
 void launch_moe_batch(const MoeArgs &a, const MoeBatchBufs &b, hipStream_t s) {
   const int ncol = a.ne + a.has_sgate, S = a.R * a.nslot;
-  if (a.R >= 512)
-    hipLaunchKernelGGL(bat_router<4>, dim3((a.R + 31) / 32, (ncol + 127) / 128), dim3(64 * kRouterWaves), 0, s, a);
-  else
+  if (a.R >= 512) {
+    const int ng = (a.R + kRtRows - 1) / kRtRows;
+    hipLaunchKernelGGL(bat_router_rows, dim3((ng * ((ncol + 127) / 128) + 7) & ~7), dim3(512), 0, s, a, ng);
+  } else
     hipLaunchKernelGGL(bat_router<1>, dim3((a.R + 31) / 32, (ncol + 31) / 32), dim3(64 * kRouterWaves), 0, s, a);
   hipLaunchKernelGGL(bat_route, dim3((a.R + 3) / 4), dim3(256), 0, s, a);
   hipLaunchKernelGGL(bat_scan, dim3(1), dim3(1024), 0, s, a, b.bk, b.chunks, b.max_chunks);
-  if (S >= 8192)
-    hipLaunchKernelGGL(bat_place_prep<1>, dim3((S + 3) / 4), dim3(256), 0, s, a, b.bk, b.rows, b.xh);
-  else
-    hipLaunchKernelGGL(bat_place_prep<4>, dim3(S), dim3(256), 0, s, a, b.bk, b.rows, b.xh);
+  IJ_CHECK(a.had_hid == 128, "batched MoE: hidden size %d needs a 128-wide Hadamard", a.hid);
+  static bool prep_attr = false;
+  if (!prep_attr) {
+    IJ_HIP(hipFuncSetAttribute((const void *)&bat_place_prep, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPrepLds));
+    prep_attr = true;
+  }
+  hipLaunchKernelGGL(bat_place_prep, dim3((S + kPrepWaves - 1) / kPrepWaves), dim3(64 * kPrepWaves), kPrepLds, s, a,
+                     b.bk, b.rows, b.xh);
   const int KS = a.nslot > a.topk ? a.slay.K : a.lay.K;
   bool done = false;
 #define IJ_BAT(k, ks)                        \

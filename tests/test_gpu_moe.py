@@ -31,7 +31,8 @@ def check_layer(eng, oracle, moe, W, x, tol=1e-4, exact=True):
     if W.d.get("sgate") is not None:
         for r in range(R):
             l = oracle.router_logits(x[r], W.d["sgate"][None])[0]
-            assert abs(sg[r] - 1 / (1 + np.exp(-np.float64(l)))) < 1e-6
+            # the gate logit, like the others, may round to the neighbouring bf16 value (sigmoid' <= 1/4)
+            assert abs(sg[r] - 1 / (1 + np.exp(-np.float64(l)))) < 0.25 * abs(l) * 2 ** -7 + 1e-6
     else:
         assert np.all(sg == 1.0)
     sgv = sg if W.d.get("sgate") is not None else None
@@ -153,7 +154,8 @@ def test_moe_fused_and_staged_paths_agree(eng, oracle, monkeypatch):
 @pytest.mark.parametrize("R", [16, 200, 640])
 def test_moe_batch_chunks(eng, oracle, R):
     """R rows through the grouped matrix-core path: experts with more than one 128-row chunk (the shared expert at
-    R = 200, ~50 rows per routed expert), ties and order checked against the oracle on the GPU's route."""
+    R = 200, ~50 rows per routed expert), ties and order checked against the oracle on the GPU's route. R = 640 takes
+    the many-row router."""
     print(f"moe batch R{R}", flush=True)
     w = synth.moe_layer(70 + R, hid=1024, inter=256, ne=16, topk=4, K=5, shared=True, Ks=6, sgate=True)
     W = oracle.MoeWeights(w)
