@@ -581,7 +581,9 @@ struct GemmIo {
   static constexpr int DA = kDA<K>, DB = kDB<K>;
   static constexpr int RA = DA + 1, RB = DB + 1;           // ring slots
   static constexpr uint32_t LDS_RING = RA * AB + kWavesG * RB * PB;
-  static constexpr uint32_t LDS = LDS_RING > 32768 ? LDS_RING : 32768;  // the epilogue stages 32 x 256 floats
+  // the epilogues exchange 32 x 32 float tiles with a 36-float row pitch: 8 (down), 8 + 4 (gate/up)
+  static constexpr uint32_t EPI = (NA == 2 ? 12u : 8u) * 32u * 36u * 4u;
+  static constexpr uint32_t LDS = LDS_RING > EPI ? LDS_RING : EPI;
   static constexpr int OA = NA, OB = (PB + 1023) / 1024;   // requests per A / B step
   static_assert(LDS <= 81920, "two workgroups per CU");
   static_assert(RB % RA == 0 && DB > DA, "ring shapes");
@@ -652,7 +654,9 @@ __device__ __forceinline__ void decode_step(const uint8_t *src, const BLane<K> &
 // quarter swizzle of A row r: distinct 16-byte bank groups for rows r .. r + 7 (eight lanes of a 128-byte read phase)
 // and for rows r .. r + 15 (sixteen lanes of a 256-byte phase), rows aligned to 8
 __device__ __forceinline__ int a_swz(int r) { return ((r >> 1) ^ ((r >> 3) & 1)) & 3; }
-template <int K, int NA>
+// TR: the weights are the matrix cores' A operand and the rows their B operand, so acc[rb] holds the transposed
+// product: lane (n, h) value i = output column 8 (i / 4) + 4 h + i % 4 of the wave's 32, row 32 rb + n.
+template <int K, int NA, bool TR = false>
 __device__ void chunk_gemm(const uint16_t *A, int lda, int ahalf, int aidx, int nrows, const uint8_t *tr, int IT,
                            int pair, uint8_t *lds, f32x16 (&acc)[kRowBlocks], uint64_t *dbg, int kt0, int nkt) {
   using Io = GemmIo<K, NA>;
@@ -727,7 +731,9 @@ __device__ void chunk_gemm(const uint16_t *A, int lda, int ahalf, int aidx, int 
         for (int rb = 0; rb < kRowBlocks; rb++) af[rb] = *(const f16x8 *)(at + rb * 2048 + (h ? q1 : q0));
 #pragma unroll
         for (int rb = 0; rb < kRowBlocks; rb++)
-          if (rb < nrb) acc[rb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[rb], h ? b1 : b0, acc[rb], 0, 0, 0);
+          if (rb < nrb)
+            acc[rb] = TR ? __builtin_amdgcn_mfma_f32_32x32x16_f16(h ? b1 : b0, af[rb], acc[rb], 0, 0, 0)
+                         : __builtin_amdgcn_mfma_f32_32x32x16_f16(af[rb], h ? b1 : b0, acc[rb], 0, 0, 0);
       }
       IJ_STAMP(t == 20, 1)
       // the matrix cores run while the next step's tiles decode
@@ -737,6 +743,51 @@ __device__ void chunk_gemm(const uint16_t *A, int lda, int ahalf, int aidx, int 
   }
   IJ_STAMP(true, 5)
 #undef IJ_STAMP
+}
+
+// ---------------------------------------------------------------------------------------------------- Hadamard on
+// the matrix cores, for a transposed product tile (lane (n, h) value i = column c = 8 (i / 4) + 4 h + i % 4 of 32,
+// row n). H_128 over 128 columns = H_4 (x) H_32 in the split 32 q + j: each wave multiplies its own 32 columns by H_32
+// here; the four waves of a 128-block combine with H_4 through LDS. With the columns of H permuted by c(k) (bits 2 and
+// 3 of k swapped), k step st's B operand is values 8 st .. 8 st + 7 of the tile itself; output row m of the product
+// is element J(m) of the chunk, J chosen by the caller for the layout it wants.
+__device__ __forceinline__ uint32_t swap23(uint32_t k) { return (k & ~12u) | (((k >> 2) & 1u) << 3) | (((k >> 3) & 1u) << 2); }
+template <typename J>
+__device__ __forceinline__ void h32_operand(int lane, J jmap, f16x8 (&hA)[2]) {
+  const uint32_t j = jmap((uint32_t)(lane & 31));
+#pragma unroll
+  for (int st = 0; st < 2; st++)
+#pragma unroll
+    for (int t = 0; t < 8; t++)
+      hA[st][t] = (__builtin_popcount(j & swap23((uint32_t)(16 * st + 8 * (lane >> 5) + t))) & 1) ? (_Float16)-1.f
+                                                                                                : (_Float16)1.f;
+}
+// T = H_32 . tile per row n: each row scaled by a power of two (its largest element to [2^14, 2^15), taken over the
+// lane pair n, n + 32), split into f16 hi + lo rounded to nearest (about 23 bits, summed in f32), scaled back.
+__device__ __forceinline__ f32x16 h32_tile(const f32x16 &v, const f16x8 (&hA)[2], int lane) {
+  float mx = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; i++) mx = fmaxf(mx, fabsf(v[i]));
+  mx = fmaxf(mx, xor_lane<32>(mx, lane));
+  const int ex = min(max(141 - (int)((__float_as_uint(mx) >> 23) & 0xFFu), -126), 127);
+  f32x16 T;
+#pragma unroll
+  for (int i = 0; i < 16; i++) T[i] = 0.f;
+#pragma unroll
+  for (int st = 0; st < 2; st++) {
+    f16x8 hi, lo;
+#pragma unroll
+    for (int t = 0; t < 8; t++) {
+      const float w = __builtin_ldexpf(v[8 * st + t], ex);
+      hi[t] = (_Float16)w;
+      lo[t] = (_Float16)(w - (float)hi[t]);
+    }
+    T = __builtin_amdgcn_mfma_f32_32x32x16_f16(hA[st], hi, T, 0, 0, 0);
+    T = __builtin_amdgcn_mfma_f32_32x32x16_f16(hA[st], lo, T, 0, 0, 0);
+  }
+#pragma unroll
+  for (int i = 0; i < 16; i++) T[i] = __builtin_ldexpf(T[i], -ex);
+  return T;
 }
 
 // gate/up: chunk ch, 128-column block ib of inter; wave w: projection w / 4 (gate, up), pair 4 ib + w % 4
@@ -755,43 +806,86 @@ __global__ __launch_bounds__(512, 4) void bat_gateup(MoeArgs a, const uint32_t *
   const uint16_t *A = xh + (uint64_t)row0 * 2 * a.hid;  // [row][gate | up][hid]
   const int pair = ib * 4 + (wave & 3);
   if (e >= a.ne)
-    chunk_gemm<KS, 2>(A, 2 * a.hid, a.hid, proj, nrows, blk + tr_of(a, e, proj), a.hid / 16, pair, lds, acc, a.trace, 0, a.hid / 16);
+    chunk_gemm<KS, 2, true>(A, 2 * a.hid, a.hid, proj, nrows, blk + tr_of(a, e, proj), a.hid / 16, pair, lds, acc, a.trace, 0, a.hid / 16);
   else
-    chunk_gemm<K, 2>(A, 2 * a.hid, a.hid, proj, nrows, blk + tr_of(a, e, proj), a.hid / 16, pair, lds, acc, a.trace, 0, a.hid / 16);
-  // epilogue per 32-row block: columns to LDS as [32][256] f32 (gate 0..127, up 128..255), then one wave per row
-  float *ot = (float *)lds;
-  const uint16_t *svg = (const uint16_t *)(blk + sv_of(a, e, 0)) + ib * 128;
-  const uint16_t *svu = (const uint16_t *)(blk + sv_of(a, e, 1)) + ib * 128;
-  const uint16_t *sud = (const uint16_t *)(blk + su_of(a, e, 2)) + ib * 128;
-  const float sg0 = h2f(svg[lane]), sg1 = h2f(svg[lane + 64]), su0 = h2f(svu[lane]), su1 = h2f(svu[lane + 64]);
-  const float sd0 = h2f(sud[lane]), sd1 = h2f(sud[lane + 64]);
+    chunk_gemm<K, 2, true>(A, 2 * a.hid, a.hid, proj, nrows, blk + tr_of(a, e, proj), a.hid / 16, pair, lds, acc, a.trace, 0, a.hid / 16);
+  // epilogue per 32-row block, with the tiles transposed (wave w: projection w / 4, chunk q = w % 4 of block ib):
+  //  1. every wave: H_32 on its tile (element j = 8 (i / 4) + 4 h + i % 4 at lane (n, h) value i), tile to LDS;
+  //  2. waves 0..3 (chunk q): H_4 over the gate tiles and over the up tiles gives g and u of columns 32 q + j; then
+  //     h = silu(g svh_g / sqrt(128)) u svh_u / sqrt(128) suh_d, already in the layout of a tile, and H_32 on it
+  //     with the rows in kp order (lane (n, h) value i = kp position 16 h + i of the chunk), to LDS;
+  //  3. wave w takes rows 4 w .. 4 w + 3 whole: lane l combines kp positions 2 l, 2 l + 1 with H_4, / sqrt(128), and
+  //     each row leaves as one 256-byte store.
+  const int q = wave & 3, n = lane & 31, h = lane >> 5;
+  f16x8 hA1[2], hA2[2];
+  h32_operand(lane, [](uint32_t m) { return m; }, hA1);
+  h32_operand(lane, [](uint32_t m) { return kp_inv32(16u * ((m >> 2) & 1u) + 4u * (m >> 3) + (m & 3u)); }, hA2);
+  // scales of this lane's columns in step 2: 32 q + 8 g + 4 h + r (natural order inside block ib), read per block
+  const int c0 = ib * 128 + 32 * q + 4 * h;
+  const uint16_t *pg = (const uint16_t *)(blk + sv_of(a, e, 0)) + c0, *pu = (const uint16_t *)(blk + sv_of(a, e, 1)) + c0;
+  const uint16_t *pd = (const uint16_t *)(blk + su_of(a, e, 2)) + c0;
+  const float sc = a.sc_inter;
+  // LDS: 8 step-1 tiles then 4 step-2 tiles of 32 rows x 32 elements, row pitch 36 floats
+  float *x1 = (float *)lds, *x2 = x1 + 8 * 32 * 36;
   const int nrb = (nrows + 31) / 32;
 #pragma unroll
-  for (int rb = 0; rb < kRowBlocks; rb++) {  // compile-time rb: acc stays in registers
+  for (int rb = 0; rb < kRowBlocks; rb++) {
     if (rb >= nrb) break;
-    __syncthreads();
+    const f32x16 T = h32_tile(acc[rb], hA1, lane);
+    __syncthreads();  // the ring (first block) or the previous block's tiles are no longer read
 #pragma unroll
-    for (int i = 0; i < 16; i++) {
-      const int r = 4 * (lane >> 5) + (i & 3) + 8 * (i >> 2), col = proj * 128 + (wave & 3) * 32 + (lane & 31);
-      ot[r * 256 + col] = acc[rb][i];
+    for (int g = 0; g < 4; g++)
+      *(float4 *)(x1 + (wave * 32 + n) * 36 + 8 * g + 4 * h) = make_float4(T[4 * g], T[4 * g + 1], T[4 * g + 2], T[4 * g + 3]);
+    __syncthreads();
+    if (wave < 4) {
+      f32x16 hv;
+#pragma unroll
+      for (int g = 0; g < 4; g++) {
+        const f16x4 sgv = *(const f16x4 *)(pg + 8 * g), suv = *(const f16x4 *)(pu + 8 * g), sdv = *(const f16x4 *)(pd + 8 * g);
+        float4 gs = {0.f, 0.f, 0.f, 0.f}, us = gs;
+#pragma unroll
+        for (int qq = 0; qq < 4; qq++) {
+          const float sgn = (__builtin_popcount(q & qq) & 1) ? -1.f : 1.f;
+          const float4 tg = *(const float4 *)(x1 + (qq * 32 + n) * 36 + 8 * g + 4 * h);
+          const float4 tu = *(const float4 *)(x1 + ((4 + qq) * 32 + n) * 36 + 8 * g + 4 * h);
+          gs.x = __builtin_fmaf(sgn, tg.x, gs.x);
+          gs.y = __builtin_fmaf(sgn, tg.y, gs.y);
+          gs.z = __builtin_fmaf(sgn, tg.z, gs.z);
+          gs.w = __builtin_fmaf(sgn, tg.w, gs.w);
+          us.x = __builtin_fmaf(sgn, tu.x, us.x);
+          us.y = __builtin_fmaf(sgn, tu.y, us.y);
+          us.z = __builtin_fmaf(sgn, tu.z, us.z);
+          us.w = __builtin_fmaf(sgn, tu.w, us.w);
+        }
+        const float gv[4] = {gs.x, gs.y, gs.z, gs.w}, uv[4] = {us.x, us.y, us.z, us.w};
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          const float gg = gv[r] * sc * (float)sgv[r], uu = uv[r] * sc * (float)suv[r];
+          // SiLU with the hardware exp2 and reciprocal (~1 ulp each; the layer's tolerance is 1e-2)
+          hv[4 * g + r] = gg * __builtin_amdgcn_rcpf(1.f + __expf(-gg)) * uu * (float)sdv[r];
+        }
+      }
+      const f32x16 T2 = h32_tile(hv, hA2, lane);
+#pragma unroll
+      for (int g = 0; g < 4; g++)
+        *(float4 *)(x2 + (q * 32 + n) * 36 + 16 * h + 4 * g) = make_float4(T2[4 * g], T2[4 * g + 1], T2[4 * g + 2], T2[4 * g + 3]);
     }
     __syncthreads();
-    for (int r = wave; r < 32 && rb * 32 + r < nrows; r += kWavesG) {
-      float g0 = ot[r * 256 + lane], g1 = ot[r * 256 + 64 + lane];
-      float u0 = ot[r * 256 + 128 + lane], u1 = ot[r * 256 + 192 + lane];
-      fwht2(g0, g1, lane, a.had_inter, a.sc_inter);
-      fwht2(u0, u1, lane, a.had_inter, a.sc_inter);
-      g0 = g0 * sg0;
-      u0 = u0 * su0;
-      g1 = g1 * sg1;
-      u1 = u1 * su1;
-      // SiLU with the hardware exp2 and reciprocal (~1 ulp each; the layer's tolerance is 1e-2)
-      float h0 = g0 * __builtin_amdgcn_rcpf(1.f + __expf(-g0)) * u0 * sd0;
-      float h1 = g1 * __builtin_amdgcn_rcpf(1.f + __expf(-g1)) * u1 * sd1;
-      fwht2(h0, h1, lane, a.had_inter, a.sc_inter);
-      uint16_t *out = hh + (uint64_t)(row0 + rb * 32 + r) * a.inter + ib * 128;
-      out[kp(lane)] = f2h(h0);
-      out[kp(lane + 64)] = f2h(h1);
+    const int oq = lane >> 4, op = 2 * (lane & 15);  // this lane's kp positions 32 oq + op, + 1
+#pragma unroll
+    for (int rr = 0; rr < 4; rr++) {
+      const int nr = wave * 4 + rr, r = rb * 32 + nr;
+      if (r >= nrows) break;
+      float o0 = 0.f, o1 = 0.f;
+#pragma unroll
+      for (int qq = 0; qq < 4; qq++) {
+        const float sgn = (__builtin_popcount(oq & qq) & 1) ? -1.f : 1.f;
+        const float2 t = *(const float2 *)(x2 + (qq * 32 + nr) * 36 + op);
+        o0 = __builtin_fmaf(sgn, t.x, o0);
+        o1 = __builtin_fmaf(sgn, t.y, o1);
+      }
+      *(uint32_t *)(hh + (uint64_t)(row0 + r) * a.inter + ib * 128 + 2 * lane) =
+          __builtin_bit_cast(uint32_t, f16x2{(_Float16)(o0 * sc), (_Float16)(o1 * sc)});
     }
   }
 }
@@ -817,43 +911,59 @@ __global__ __launch_bounds__(512, 4) void bat_down(MoeArgs a, const uint32_t *bk
   f32x16 acc[kRowBlocks];
   const uint16_t *A = hh + (uint64_t)row0 * a.inter;
   if (e >= a.ne)
-    chunk_gemm<KS, 1>(A, a.inter, 0, 0, nrows, blk + tr_of(a, e, 2), a.inter / 16, ob2 * 8 + wave, lds, acc, nullptr, 0, a.inter / 16);
+    chunk_gemm<KS, 1, true>(A, a.inter, 0, 0, nrows, blk + tr_of(a, e, 2), a.inter / 16, ob2 * 8 + wave, lds, acc, nullptr, 0, a.inter / 16);
   else
-    chunk_gemm<K, 1>(A, a.inter, 0, 0, nrows, blk + tr_of(a, e, 2), a.inter / 16, ob2 * 8 + wave, lds, acc, nullptr, 0, a.inter / 16);
+    chunk_gemm<K, 1, true>(A, a.inter, 0, 0, nrows, blk + tr_of(a, e, 2), a.inter / 16, ob2 * 8 + wave, lds, acc, nullptr, 0, a.inter / 16);
   if (mt < nrows) {
     const int tok = sl / a.nslot, k = sl % a.nslot;
     m_dst[mt] = sl;
     m_w[mt] = k >= a.topk ? a.sgv[tok] : __uint_as_float(a.route[(uint64_t)tok * 2 * a.topk + a.topk + k]);
   }
-  float *ot = (float *)lds;  // [32][256]
-  const uint16_t *sv = (const uint16_t *)(blk + sv_of(a, e, 2)) + ob2 * 256;
-  float s[2][2];
+  // epilogue: wave w holds columns 32 w .. of this 256 (block bb = w / 4, chunk q = w % 4) for every row, transposed.
+  // Per 32-row block: H_32 on the wave's tile (output element j = 16 h + i of the chunk at lane (n, h)), the tiles to
+  // LDS; then wave w takes rows 4 w .. 4 w + 3 whole: lane l combines columns 4 l .. 4 l + 3 with H_4 across the four
+  // chunks of its block, applies 1/sqrt(128), svh_d and the slot's route weight, and the row leaves as one 1 KB store.
+  f16x8 hA[2];
+  h32_operand(lane, [](uint32_t m) { return 16u * ((m >> 2) & 1u) + 4u * (m >> 3) + (m & 3u); }, hA);
+  const int cb = lane >> 5, cq = (lane >> 3) & 3, cj = 4 * (lane & 7);  // this lane's columns: block, chunk, element
+  float sv[4];
+  {
+    const uint16_t *svp = (const uint16_t *)(blk + sv_of(a, e, 2)) + ob2 * 256 + 4 * lane;
 #pragma unroll
-  for (int bb = 0; bb < 2; bb++) {
-    s[bb][0] = h2f(sv[bb * 128 + lane]);
-    s[bb][1] = h2f(sv[bb * 128 + lane + 64]);
+    for (int t = 0; t < 4; t++) sv[t] = h2f(svp[t]) * a.sc_hid;
   }
+  // 8 tiles of 32 rows x 32 columns: tile w, row n, element j at (w 32 + n) 36 + j floats (the pad spreads the
+  // rows of one write over the banks)
+  float *xt = (float *)lds;
   const int nrb = (nrows + 31) / 32;
 #pragma unroll
   for (int rb = 0; rb < kRowBlocks; rb++) {
     if (rb >= nrb) break;
-    __syncthreads();
+    const f32x16 T = h32_tile(acc[rb], hA, lane);
+    __syncthreads();  // the ring (first block) or the previous block's rows are no longer read
+    {
+      float *tp = xt + (wave * 32 + (lane & 31)) * 36 + 16 * (lane >> 5);
 #pragma unroll
-    for (int i = 0; i < 16; i++) {
-      const int r = 4 * (lane >> 5) + (i & 3) + 8 * (i >> 2), col = wave * 32 + (lane & 31);
-      ot[r * 256 + col] = acc[rb][i];
+      for (int g = 0; g < 4; g++) *(float4 *)(tp + 4 * g) = make_float4(T[4 * g], T[4 * g + 1], T[4 * g + 2], T[4 * g + 3]);
     }
     __syncthreads();
-    for (int r = wave; r < 32 && rb * 32 + r < nrows; r += kWavesG) {
-      const float w = m_w[rb * 32 + r];
-      float *out = dnw + (uint64_t)m_dst[rb * 32 + r] * a.hid + ob2 * 256;  // slot sl = token * nslot + k
 #pragma unroll
-      for (int bb = 0; bb < 2; bb++) {
-        float v0 = ot[r * 256 + bb * 128 + lane], v1 = ot[r * 256 + bb * 128 + 64 + lane];
-        fwht2(v0, v1, lane, a.had_hid, a.sc_hid);
-        out[bb * 128 + lane] = v0 * s[bb][0] * w;
-        out[bb * 128 + lane + 64] = v1 * s[bb][1] * w;
+    for (int rr = 0; rr < 4; rr++) {
+      const int n = wave * 4 + rr, r = rb * 32 + n;
+      if (r >= nrows) break;
+      float4 o = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int qq = 0; qq < 4; qq++) {
+        const float4 t = *(const float4 *)(xt + ((cb * 4 + qq) * 32 + n) * 36 + cj);
+        const float sg = (__builtin_popcount(cq & qq) & 1) ? -1.f : 1.f;
+        o.x = __builtin_fmaf(sg, t.x, o.x);
+        o.y = __builtin_fmaf(sg, t.y, o.y);
+        o.z = __builtin_fmaf(sg, t.z, o.z);
+        o.w = __builtin_fmaf(sg, t.w, o.w);
       }
+      const float w = m_w[r];
+      *(float4 *)(dnw + (uint64_t)m_dst[r] * a.hid + ob2 * 256 + 4 * lane) =  // slot = token nslot + k
+          make_float4(o.x * sv[0] * w, o.y * sv[1] * w, o.z * sv[2] * w, o.w * sv[3] * w);
     }
   }
 }
