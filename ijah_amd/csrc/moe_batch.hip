@@ -791,7 +791,7 @@ __device__ __forceinline__ f32x16 h32_tile(const f32x16 &v, const f16x8 (&hA)[2]
 }
 
 // gate/up: chunk ch, 128-column block ib of inter; wave w: projection w / 4 (gate, up), pair 4 ib + w % 4
-template <int K, int KS>
+template <int K, int KS, bool TR>
 __global__ __launch_bounds__(512, 4) void bat_gateup(MoeArgs a, const uint32_t *bk, const uint32_t *chunks,
                                                      const uint32_t *rows, const uint16_t *xh, uint16_t *hh) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -806,9 +806,48 @@ __global__ __launch_bounds__(512, 4) void bat_gateup(MoeArgs a, const uint32_t *
   const uint16_t *A = xh + (uint64_t)row0 * 2 * a.hid;  // [row][gate | up][hid]
   const int pair = ib * 4 + (wave & 3);
   if (e >= a.ne)
-    chunk_gemm<KS, 2, true>(A, 2 * a.hid, a.hid, proj, nrows, blk + tr_of(a, e, proj), a.hid / 16, pair, lds, acc, a.trace, 0, a.hid / 16);
+    chunk_gemm<KS, 2, TR>(A, 2 * a.hid, a.hid, proj, nrows, blk + tr_of(a, e, proj), a.hid / 16, pair, lds, acc, a.trace, 0, a.hid / 16);
   else
-    chunk_gemm<K, 2, true>(A, 2 * a.hid, a.hid, proj, nrows, blk + tr_of(a, e, proj), a.hid / 16, pair, lds, acc, a.trace, 0, a.hid / 16);
+    chunk_gemm<K, 2, TR>(A, 2 * a.hid, a.hid, proj, nrows, blk + tr_of(a, e, proj), a.hid / 16, pair, lds, acc, a.trace, 0, a.hid / 16);
+  if constexpr (!TR) {
+  // epilogue per 32-row block: columns to LDS as [32][256] f32 (gate 0..127, up 128..255), then one wave per row
+  float *ot = (float *)lds;
+  const uint16_t *svg = (const uint16_t *)(blk + sv_of(a, e, 0)) + ib * 128;
+  const uint16_t *svu = (const uint16_t *)(blk + sv_of(a, e, 1)) + ib * 128;
+  const uint16_t *sud = (const uint16_t *)(blk + su_of(a, e, 2)) + ib * 128;
+  const float sg0 = h2f(svg[lane]), sg1 = h2f(svg[lane + 64]), su0 = h2f(svu[lane]), su1 = h2f(svu[lane + 64]);
+  const float sd0 = h2f(sud[lane]), sd1 = h2f(sud[lane + 64]);
+  const int nrb = (nrows + 31) / 32;
+#pragma unroll
+  for (int rb = 0; rb < kRowBlocks; rb++) {  // compile-time rb: acc stays in registers
+    if (rb >= nrb) break;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      const int r = 4 * (lane >> 5) + (i & 3) + 8 * (i >> 2), col = proj * 128 + (wave & 3) * 32 + (lane & 31);
+      ot[r * 256 + col] = acc[rb][i];
+    }
+    __syncthreads();
+    for (int r = wave; r < 32 && rb * 32 + r < nrows; r += kWavesG) {
+      float g0 = ot[r * 256 + lane], g1 = ot[r * 256 + 64 + lane];
+      float u0 = ot[r * 256 + 128 + lane], u1 = ot[r * 256 + 192 + lane];
+      fwht2(g0, g1, lane, a.had_inter, a.sc_inter);
+      fwht2(u0, u1, lane, a.had_inter, a.sc_inter);
+      g0 = g0 * sg0;
+      u0 = u0 * su0;
+      g1 = g1 * sg1;
+      u1 = u1 * su1;
+      // SiLU with the hardware exp2 and reciprocal (~1 ulp each; the layer's tolerance is 1e-2)
+      float h0 = g0 * __builtin_amdgcn_rcpf(1.f + __expf(-g0)) * u0 * sd0;
+      float h1 = g1 * __builtin_amdgcn_rcpf(1.f + __expf(-g1)) * u1 * sd1;
+      fwht2(h0, h1, lane, a.had_inter, a.sc_inter);
+      uint16_t *out = hh + (uint64_t)(row0 + rb * 32 + r) * a.inter + ib * 128;
+      out[kp(lane)] = f2h(h0);
+      out[kp(lane + 64)] = f2h(h1);
+    }
+  }
+    return;
+  } else {
   // epilogue per 32-row block, with the tiles transposed (wave w: projection w / 4, chunk q = w % 4 of block ib):
   //  1. every wave: H_32 on its tile (element j = 8 (i / 4) + 4 h + i % 4 at lane (n, h) value i), tile to LDS;
   //  2. waves 0..3 (chunk q): H_4 over the gate tiles and over the up tiles gives g and u of columns 32 q + j; then
@@ -888,11 +927,12 @@ __global__ __launch_bounds__(512, 4) void bat_gateup(MoeArgs a, const uint32_t *
           __builtin_bit_cast(uint32_t, f16x2{(_Float16)(o0 * sc), (_Float16)(o1 * sc)});
     }
   }
+  }
 }
 
 // down: chunk ch, 256 columns of hid (output blocks 2 ob2, 2 ob2 + 1); wave w: pair 8 ob2 + w. Output per
 // (token, slot): H over each 128-column block, svh_d, the slot's route weight.
-template <int K, int KS>
+template <int K, int KS, bool TR>
 __global__ __launch_bounds__(512, 4) void bat_down(MoeArgs a, const uint32_t *bk, const uint32_t *chunks,
                                                    const uint32_t *rows, const uint16_t *hh, float *dnw) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -911,14 +951,47 @@ __global__ __launch_bounds__(512, 4) void bat_down(MoeArgs a, const uint32_t *bk
   f32x16 acc[kRowBlocks];
   const uint16_t *A = hh + (uint64_t)row0 * a.inter;
   if (e >= a.ne)
-    chunk_gemm<KS, 1, true>(A, a.inter, 0, 0, nrows, blk + tr_of(a, e, 2), a.inter / 16, ob2 * 8 + wave, lds, acc, nullptr, 0, a.inter / 16);
+    chunk_gemm<KS, 1, TR>(A, a.inter, 0, 0, nrows, blk + tr_of(a, e, 2), a.inter / 16, ob2 * 8 + wave, lds, acc, nullptr, 0, a.inter / 16);
   else
-    chunk_gemm<K, 1, true>(A, a.inter, 0, 0, nrows, blk + tr_of(a, e, 2), a.inter / 16, ob2 * 8 + wave, lds, acc, nullptr, 0, a.inter / 16);
+    chunk_gemm<K, 1, TR>(A, a.inter, 0, 0, nrows, blk + tr_of(a, e, 2), a.inter / 16, ob2 * 8 + wave, lds, acc, nullptr, 0, a.inter / 16);
   if (mt < nrows) {
     const int tok = sl / a.nslot, k = sl % a.nslot;
     m_dst[mt] = sl;
     m_w[mt] = k >= a.topk ? a.sgv[tok] : __uint_as_float(a.route[(uint64_t)tok * 2 * a.topk + a.topk + k]);
   }
+  if constexpr (!TR) {
+  float *ot = (float *)lds;  // [32][256]
+  const uint16_t *sv = (const uint16_t *)(blk + sv_of(a, e, 2)) + ob2 * 256;
+  float s[2][2];
+#pragma unroll
+  for (int bb = 0; bb < 2; bb++) {
+    s[bb][0] = h2f(sv[bb * 128 + lane]);
+    s[bb][1] = h2f(sv[bb * 128 + lane + 64]);
+  }
+  const int nrb = (nrows + 31) / 32;
+#pragma unroll
+  for (int rb = 0; rb < kRowBlocks; rb++) {
+    if (rb >= nrb) break;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      const int r = 4 * (lane >> 5) + (i & 3) + 8 * (i >> 2), col = wave * 32 + (lane & 31);
+      ot[r * 256 + col] = acc[rb][i];
+    }
+    __syncthreads();
+    for (int r = wave; r < 32 && rb * 32 + r < nrows; r += kWavesG) {
+      const float w = m_w[rb * 32 + r];
+      float *out = dnw + (uint64_t)m_dst[rb * 32 + r] * a.hid + ob2 * 256;  // slot sl = token * nslot + k
+#pragma unroll
+      for (int bb = 0; bb < 2; bb++) {
+        float v0 = ot[r * 256 + bb * 128 + lane], v1 = ot[r * 256 + bb * 128 + 64 + lane];
+        fwht2(v0, v1, lane, a.had_hid, a.sc_hid);
+        out[bb * 128 + lane] = v0 * s[bb][0] * w;
+        out[bb * 128 + lane + 64] = v1 * s[bb][1] * w;
+      }
+    }
+  }
+  } else {
   // epilogue: wave w holds columns 32 w .. of this 256 (block bb = w / 4, chunk q = w % 4) for every row, transposed.
   // Per 32-row block: H_32 on the wave's tile (output element j = 16 h + i of the chunk at lane (n, h)), the tiles to
   // LDS; then wave w takes rows 4 w .. 4 w + 3 whole: lane l combines columns 4 l .. 4 l + 3 with H_4 across the four
@@ -965,6 +1038,7 @@ __global__ __launch_bounds__(512, 4) void bat_down(MoeArgs a, const uint32_t *bk
       *(float4 *)(dnw + (uint64_t)m_dst[r] * a.hid + ob2 * 256 + 4 * lane) =  // slot = token nslot + k
           make_float4(o.x * sv[0] * w, o.y * sv[1] * w, o.z * sv[2] * w, o.w * sv[3] * w);
     }
+  }
   }
 }
 
@@ -1037,20 +1111,30 @@ void launch_lin_mm(const LinArgs &a, hipStream_t s) {
 
 // ---------------------------------------------------------------------------------------------------- host side
 namespace {
-template <int K, int KS>
-void launch_gemms(const MoeArgs &a, const MoeBatchBufs &b, hipStream_t s) {
+template <int K, int KS, bool TR>
+void launch_gemms_as(const MoeArgs &a, const MoeBatchBufs &b, hipStream_t s) {
   // the routed (K) and shared (KS) chunks use ring layouts of their own widths: room for the larger of each
   const size_t lg = std::max(GemmIo<K, 2>::LDS, GemmIo<KS, 2>::LDS), ld = std::max(GemmIo<K, 1>::LDS, GemmIo<KS, 1>::LDS);
   static bool attr = false;
   if (!attr) {
-    IJ_HIP(hipFuncSetAttribute((const void *)&bat_gateup<K, KS>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lg));
-    IJ_HIP(hipFuncSetAttribute((const void *)&bat_down<K, KS>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)ld));
+    IJ_HIP(hipFuncSetAttribute((const void *)&bat_gateup<K, KS, TR>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lg));
+    IJ_HIP(hipFuncSetAttribute((const void *)&bat_down<K, KS, TR>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)ld));
     attr = true;
   }
-  hipLaunchKernelGGL((bat_gateup<K, KS>), dim3((b.max_chunks * (a.inter / 128) + 7) & ~7), dim3(64 * kWavesG), lg, s, a, b.bk,
-                     b.chunks, b.rows, b.xh, b.hh);
-  hipLaunchKernelGGL((bat_down<K, KS>), dim3((b.max_chunks * (a.hid / 256) + 7) & ~7), dim3(64 * kWavesG), ld, s, a, b.bk, b.chunks,
-                     b.rows, b.hh, b.dnw);
+  hipLaunchKernelGGL((bat_gateup<K, KS, TR>), dim3((b.max_chunks * (a.inter / 128) + 7) & ~7), dim3(64 * kWavesG), lg, s, a,
+                     b.bk, b.chunks, b.rows, b.xh, b.hh);
+  hipLaunchKernelGGL((bat_down<K, KS, TR>), dim3((b.max_chunks * (a.hid / 256) + 7) & ~7), dim3(64 * kWavesG), ld, s, a,
+                     b.bk, b.chunks, b.rows, b.hh, b.dnw);
+}
+// Chunks of many rows (8 or more per routed expert on average) take the transposed products and the matrix-core
+// Hadamard epilogues; chunks of a row or two (speculative verify) the row-major products and lane butterflies, which
+// cost less there.
+template <int K, int KS>
+void launch_gemms(const MoeArgs &a, const MoeBatchBufs &b, hipStream_t s) {
+  if ((int64_t)a.R * a.topk >= 8LL * a.ne)
+    launch_gemms_as<K, KS, true>(a, b, s);
+  else
+    launch_gemms_as<K, KS, false>(a, b, s);
 }
 }  // namespace
 
