@@ -6,7 +6,8 @@
 // Launches, in order:
 //   bat_router   logits[R][ne (+ shared gate)] = bf16(x . router) in f32 (reference kernels/fn_moe.metal:50-67)
 //   bat_route    per row: top-k, ties to the lower index, weights exp(l - l_max) / sum (kernels/fn_moe.metal:76-131)
-//   bat_scan     one workgroup: slots per expert (a histogram of the route in LDS), per-expert offsets of the
+//   bat_hist     slots per expert: LDS histograms of slices of the route, merged with global atomics
+//   bat_scan     one workgroup: per-expert offsets of the
 //                expert-sorted slot list (the shared expert's rows last) and the list of 128-row chunks (expert,
 //                first row, rows) the GEMMs run over (kernels/prefill/pf_moe.metal:26-83)
 //   bat_place_prep  one wave per slot: its place in its expert's rows (row order inside an expert does not change
@@ -142,7 +143,7 @@ __global__ __launch_bounds__(512) void bat_router(MoeArgs a) {
         hi[e] = (__bf16)xs[e];
         lo[e] = (__bf16)(xs[e] - (float)hi[e]);
       }
-      const bf16x8 wb = __builtin_bit_cast(bf16x8, wv[b][u]);
+      const bf16x8 wb = __builtin_bit_cast(bf16x8, wv[b & 1][u]);
       acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(hi, wb, acc, 0, 0, 0);
       acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(lo, wb, acc, 0, 0, 0);
     }
@@ -310,54 +311,91 @@ __global__ __launch_bounds__(256) void bat_route(MoeArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------------------- sort
+// Routed slots per expert: each workgroup takes a contiguous run of the route's [R][2 topk] words (ids, then
+// weights) in 16-byte groups, counts the ids among them in LDS and adds its nonzero counts to bk[0 .. ne) (zero on
+// entry: set at allocation and again by bat_scan once it has read them).
+constexpr int kHistGroups = 64;
+__global__ __launch_bounds__(256) void bat_hist(MoeArgs a, uint32_t *bk) {
+  __shared__ uint32_t sc[1024];
+  const int tid = threadIdx.x;
+  for (int e = tid; e < a.ne; e += 256) sc[e] = 0u;
+  __syncthreads();
+  const int stride = 2 * a.topk, total = a.R * stride, groups = (total + 3) / 4;
+  const int per = (groups + kHistGroups - 1) / kHistGroups, gb = blockIdx.x * per, ge = min(gb + per, groups);
+  for (int g = gb + tid; g < ge; g += 256) {
+    const int w0 = 4 * g;
+    uint4 v;
+    if (w0 + 4 <= total) {
+      v = *(const uint4 *)(a.route + w0);
+    } else {  // the last, partial group
+      const uint32_t *w = a.route + w0;
+      const int left = total - w0;
+      v = make_uint4(w[0], left > 1 ? w[1] : 0u, left > 2 ? w[2] : 0u, 0u);
+    }
+    const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int q = 0; q < 4; q++)
+      if (w0 + q < total && (w0 + q) % stride < a.topk) atomicAdd(&sc[w4[q] < (uint32_t)a.ne ? w4[q] : 0u], 1u);
+  }
+  __syncthreads();
+  for (int e = tid; e < a.ne; e += 256)
+    if (sc[e]) atomicAdd(bk + e, sc[e]);
+}
 // One workgroup: offsets (exclusive scan over experts; the shared expert's R rows last), the chunk list and the
-// placement cursors. bk: [ne + 1] counts (in), [ne + 1] offsets, [ne + 1] cursors, then 1 chunk count; chunks: u32x3.
-__global__ __launch_bounds__(1024) void bat_scan(MoeArgs a, uint32_t *bk, uint32_t *chunks, int max_chunks) {
+// placement cursors. bk: [ne + 1] counts (in; routed experts from bat_hist), [ne + 1] offsets, [ne + 1] cursors, then
+// 1 chunk count; chunks: u32x3.
+// With self_count (few rows) the workgroup counts the route itself instead (one launch fewer).
+__global__ __launch_bounds__(1024) void bat_scan(MoeArgs a, uint32_t *bk, uint32_t *chunks, int max_chunks,
+                                                 int self_count) {
   __shared__ uint32_t sc[1024 + 1], cc[1024 + 1];
   const int tid = threadIdx.x, n = a.ne + (a.nslot > a.topk ? 1 : 0);
   uint32_t *counts = bk, *offs = bk + (a.ne + 1), *cursor = offs + (a.ne + 1), *nchunks = cursor + (a.ne + 1);
-  // routed slots per expert: a histogram of the route ids in LDS (one workgroup: no global atomics to contend)
-  // The route is [R][2 topk] words (ids, then weights): each thread takes a contiguous run of whole 16-byte groups,
-  // loaded together, and adds the ids among them.
-  sc[tid] = 0u;
-  __syncthreads();
-  {
-    const int stride = 2 * a.topk, total = a.R * stride, groups = (total + 3) / 4;
-    const int per = (groups + 1023) / 1024, g0 = tid * per, g1 = min(g0 + per, groups);
-    constexpr int B = 8;  // groups requested at once
-    int col = (g0 * 4) % stride;  // column of the next word inside its row (ids below topk)
-    for (int g = g0; g < g1; g += B) {
-      uint4 v[B];
+  if (!self_count) {
+    sc[tid] = tid < a.ne ? counts[tid] : 0u;
+  } else {
+    // routed slots per expert: a histogram of the route ids in LDS (one workgroup: no global atomics to contend)
+    // The route is [R][2 topk] words (ids, then weights): each thread takes a contiguous run of whole 16-byte groups,
+    // loaded together, and adds the ids among them.
+    sc[tid] = 0u;
+    __syncthreads();
+    {
+      const int stride = 2 * a.topk, total = a.R * stride, groups = (total + 3) / 4;
+      const int per = (groups + 1023) / 1024, g0 = tid * per, g1 = min(g0 + per, groups);
+      constexpr int B = 8;  // groups requested at once
+      int col = (g0 * 4) % stride;  // column of the next word inside its row (ids below topk)
+      for (int g = g0; g < g1; g += B) {
+        uint4 v[B];
 #pragma unroll
-      for (int j = 0; j < B; j++)
-        if (g + j < g1) {
-          if ((g + j) * 4 + 4 <= total) {
-            v[j] = *(const uint4 *)(a.route + (size_t)(g + j) * 4);
-          } else {  // the last, partial group
-            const uint32_t *w = a.route + (size_t)(g + j) * 4;
-            const int left = total - (g + j) * 4;
-            v[j] = make_uint4(w[0], left > 1 ? w[1] : 0u, left > 2 ? w[2] : 0u, 0u);
-          }
-        }
-#pragma unroll
-      for (int j = 0; j < B; j++)
-        if (g + j < g1) {
-          const uint32_t w4[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
-#pragma unroll
-          for (int q = 0; q < 4; q++) {
-            if ((g + j) * 4 + q < total && col < a.topk) {
-              const uint32_t e = w4[q];
-              atomicAdd(&sc[e < (uint32_t)a.ne ? e : 0u], 1u);
+        for (int j = 0; j < B; j++)
+          if (g + j < g1) {
+            if ((g + j) * 4 + 4 <= total) {
+              v[j] = *(const uint4 *)(a.route + (size_t)(g + j) * 4);
+            } else {  // the last, partial group
+              const uint32_t *w = a.route + (size_t)(g + j) * 4;
+              const int left = total - (g + j) * 4;
+              v[j] = make_uint4(w[0], left > 1 ? w[1] : 0u, left > 2 ? w[2] : 0u, 0u);
             }
-            col = col + 1 == stride ? 0 : col + 1;
           }
-        }
+#pragma unroll
+        for (int j = 0; j < B; j++)
+          if (g + j < g1) {
+            const uint32_t w4[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+              if ((g + j) * 4 + q < total && col < a.topk) {
+                const uint32_t e = w4[q];
+                atomicAdd(&sc[e < (uint32_t)a.ne ? e : 0u], 1u);
+              }
+              col = col + 1 == stride ? 0 : col + 1;
+            }
+          }
+      }
     }
   }
   __syncthreads();
   const uint32_t c = tid < a.ne ? sc[tid] : (tid < n ? (uint32_t)a.R : 0u);  // the shared expert takes every row
   __syncthreads();
-  if (tid < n) counts[tid] = c;
+  if (tid < a.ne) counts[tid] = 0u;  // ready for the next layer's bat_hist
   sc[tid] = c;
   cc[tid] = (c + kChunkRows - 1) / kChunkRows;
   __syncthreads();
@@ -1154,7 +1192,9 @@ void launch_moe_batch(const MoeArgs &a, const MoeBatchBufs &b, hipStream_t s) {
   } else
     hipLaunchKernelGGL(bat_router<1>, dim3((a.R + 31) / 32, (ncol + 31) / 32), dim3(64 * kRouterWaves), 0, s, a);
   hipLaunchKernelGGL(bat_route, dim3((a.R + 3) / 4), dim3(256), 0, s, a);
-  hipLaunchKernelGGL(bat_scan, dim3(1), dim3(1024), 0, s, a, b.bk, b.chunks, b.max_chunks);
+  const int self_count = a.R * a.topk < 4096;  // few slots: counted inside bat_scan
+  if (!self_count) hipLaunchKernelGGL(bat_hist, dim3(kHistGroups), dim3(256), 0, s, a, b.bk);
+  hipLaunchKernelGGL(bat_scan, dim3(1), dim3(1024), 0, s, a, b.bk, b.chunks, b.max_chunks, self_count);
   IJ_CHECK(a.had_hid == 128, "batched MoE: hidden size %d needs a 128-wide Hadamard", a.hid);
   static bool prep_attr = false;
   if (!prep_attr) {
