@@ -650,12 +650,27 @@ __global__ __launch_bounds__(256) void lin_step(LinArgs a) {
   for (int r = wave; r < a.R; r += 4) {
     const int i0 = cb * 128 + lane, i1 = i0 + 64;
     const bool m0 = i0 < a.out, m1 = i1 < a.out;
+    const int j0 = m0 ? i0 : 0, j1 = m1 ? i1 : 0;
     float v0 = 0.f, v1 = 0.f;
-    for (int ss = 0; ss < a.S; ss++) {
-      const float *pp = a.part + ((uint64_t)ss * a.R + r) * OTp * 16;
-      if (m0) v0 += ld_cg(pp + i0);
-      if (m1) v1 += ld_cg(pp + i1);
+    // the splits' partials are requested 8 at a time (one round trip per 8, not per split) and summed in split order
+    constexpr int B = 8;
+    for (int s0 = 0; s0 < a.S; s0 += B) {
+      float t0[B], t1[B];
+#pragma unroll
+      for (int j = 0; j < B; j++) {
+        const float *pp = a.part + ((uint64_t)min(s0 + j, a.S - 1) * a.R + r) * OTp * 16;
+        t0[j] = ld_cg(pp + j0);
+        t1[j] = ld_cg(pp + j1);
+      }
+#pragma unroll
+      for (int j = 0; j < B; j++)
+        if (s0 + j < a.S) {
+          v0 += t0[j];
+          v1 += t1[j];
+        }
     }
+    v0 = m0 ? v0 : 0.f;
+    v1 = m1 ? v1 : 0.f;
     fwht2(v0, v1, lane, a.had_out, a.sc_out);
     if (m0) a.y[(uint64_t)r * a.out + i0] = v0 * h2f(a.svh[i0]);
     if (m1) a.y[(uint64_t)r * a.out + i1] = v1 * h2f(a.svh[i1]);
@@ -670,12 +685,26 @@ __global__ __launch_bounds__(64) void lin_finish(LinArgs a) {
   const int OTp = a.OT + (a.OT & 1);
   const int i0 = c * 128 + lane, i1 = i0 + 64;
   const bool m0 = i0 < a.out, m1 = i1 < a.out;
+  const int j0 = m0 ? i0 : 0, j1 = m1 ? i1 : 0;
   float v0 = 0.f, v1 = 0.f;
-  for (int s = 0; s < a.S; s++) {
-    const float *pp = a.part + ((uint64_t)s * a.R + r) * OTp * 16;
-    if (m0) v0 += pp[i0];
-    if (m1) v1 += pp[i1];
+  constexpr int B = 8;  // splits requested together, summed in split order (as lin_step's finisher)
+  for (int s0 = 0; s0 < a.S; s0 += B) {
+    float t0[B], t1[B];
+#pragma unroll
+    for (int j = 0; j < B; j++) {
+      const float *pp = a.part + ((uint64_t)min(s0 + j, a.S - 1) * a.R + r) * OTp * 16;
+      t0[j] = pp[j0];
+      t1[j] = pp[j1];
+    }
+#pragma unroll
+    for (int j = 0; j < B; j++)
+      if (s0 + j < a.S) {
+        v0 += t0[j];
+        v1 += t1[j];
+      }
   }
+  v0 = m0 ? v0 : 0.f;
+  v1 = m1 ? v1 : 0.f;
   fwht2(v0, v1, lane, a.had_out, a.sc_out);
   if (m0) a.y[(uint64_t)r * a.out + i0] = v0 * h2f(a.svh[i0]);
   if (m1) a.y[(uint64_t)r * a.out + i1] = v1 * h2f(a.svh[i1]);
