@@ -9,8 +9,8 @@ LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libijah_exl3.so"
 
 
 def load_engine():
-    """The ctypes Engine over the built library (raises if it is not built)."""
-    from .engine import Engine
-    if not LIB_PATH.exists():
-        raise RuntimeError(f"{LIB_PATH} is not built: run python -m ijah_amd.build")
-    return Engine(LIB_PATH)
+    """The ctypes Engine over the built library, or the one NE_LIB names (raises if it is not built)."""
+    from .engine import Engine, LIB
+    if not LIB.exists():
+        raise RuntimeError(f"{LIB} is not built: run python -m ijah_amd.build")
+    return Engine(LIB)

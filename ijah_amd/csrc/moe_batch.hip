@@ -475,12 +475,17 @@ __global__ __launch_bounds__(64 * kPrepWaves, 2) void bat_place_prep(MoeArgs a, 
     e = e < a.ne ? e : 0;
   }
   e = __builtin_amdgcn_readfirstlane(e);  // one slot per wave: the expert's layout then stays in scalar registers
-  // the slot's row, first needed by the stores: both requests are issued by hand and waited for with the tile's loads
-  // (the compiler would wait for the atomic's result right here, and sink the offset's load to its use)
-  uint32_t pos = (uint32_t)r, base;  // the shared expert's list is every token in order
-  asm volatile("global_load_dword %0, %1, off" : "=v"(base) : "v"(offs + e) : "memory");
-  if (lane == 0 && k < a.topk)
-    asm volatile("global_atomic_add %0, %1, %2, off sc0" : "=v"(pos) : "v"(cursor + e), "v"(1u) : "memory");
+  // the slot's row, first needed by the stores: the cursor atomic is requested here and its result waited for there.
+  // (The cursor's address goes through an empty asm so that the compiler sees a per-lane address: its rewrite of a
+  // uniform-address atomic would consume the result, and so wait for it, right away.)
+  uint32_t pos = (uint32_t)r;  // the shared expert's list is every token in order
+  if (lane == 0 && k < a.topk) {
+    uint32_t *pc = cursor + e;
+    asm volatile("" : "+v"(pc));
+    pos = __hip_atomic_fetch_add((__attribute__((address_space(1))) uint32_t *)pc, 1u, __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);  // a global (not flat) atomic: no wait for the LDS loads
+  }
+  const uint32_t base = offs[e];
   // A operand: lane (m = n, h) holds H_32[j(m)][16 st + 8 h + t] for k steps st = 0, 1, where output row m is kp
   // position d = 16 ((m >> 2) & 1) + 4 (m >> 3) + (m & 3) of the chunk, i.e. element j(m) = kp^-1(d)
   f16x8 hA[2];
@@ -520,7 +525,7 @@ __global__ __launch_bounds__(64 * kPrepWaves, 2) void bat_place_prep(MoeArgs a, 
         dma16_buf(ru, vs, 1024u * j, lsu + (260 + 65 * j) * 16);
       }
     }
-    asm volatile("s_waitcnt vmcnt(0)" : "+v"(base), "+v"(pos) : : "memory");  // the tile, base and pos arrived
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the tile is in LDS
     // v = x * suh for this lane's 64 elements of vector n, and the vector's largest |v| (lanes n and n + 32)
     float v[4][2][8];
     float mx = 0.f;
