@@ -96,7 +96,14 @@ SIGNATURES = {
     "ne_moe_time": (_i, [C.POINTER(_vp), _i, _i, _vp, _i, _i, _dp]),
     "ne_exl3_lin_time": (_i, [C.POINTER(_vp), _i, _i, _vp, _i, _i, _dp]),
     "ne_moe_time_kernels": (_i, [C.POINTER(_vp), _i, _i, _vp, _i, C.c_void_p, _dp, C.POINTER(_i)]),
+    "ne_pack_align": (_i, [C.c_char_p, C.c_char_p, _u64, _i, C.c_void_p]),
 }
+
+
+class PackAlignStats(C.Structure):
+    """include/ijah_exl3.h ne_pack_align_stats"""
+    _fields_ = [(n, C.c_uint64) for n in ("tensors", "misaligned_tensors", "misaligned_bytes", "files_rewritten",
+                                          "files_linked", "files_kept", "bytes_written")]
 
 
 def bf16_to_f32(u16):
@@ -397,6 +404,14 @@ class Engine:
 
     def pack_open(self, path):
         return Pack(self, path)
+
+    def pack_align(self, src, dst, align=64, dry_run=False):
+        """reference core/pack_align.h align_pack: a copy of the pack in src under dst whose every tensor's data
+        is align-byte aligned in its shard; returns the counts as a dict."""
+        st = PackAlignStats()
+        self._ok(self.lib.ne_pack_align(str(src).encode(), str(dst).encode(), align, int(dry_run), C.byref(st)),
+                 "ne_pack_align")
+        return {n: getattr(st, n) for n, _ in PackAlignStats._fields_}
 
     def kernel_exists(self, fn):
         return self.lib.ne_kernel_exists(fn.encode()) == 1

@@ -21,6 +21,19 @@ NE_API int ne_buf_flush(ne_buf *b);
 /* Waits for all queued GPU work of the library (the reference's Recorder::wait, core/recorder.h:76). */
 NE_API int ne_sync(void);
 
+/* ---- pack alignment ----
+ * reference core/pack_align.h:1-25 (ne::align_pack, the engine-cli `align-pack` command): writes into dst_dir a copy of
+ * the pack in src_dir whose every tensor's data starts at a multiple of align bytes of its shard. Aligned shards,
+ * config.json and other files become symbolic links to the source; a misaligned shard is rewritten (tensor order kept,
+ * offsets rounded up, header padded with spaces), read back and compared byte for byte before it is renamed into
+ * place; a rerun keeps shards already copied. dry_run: only count (dst_dir untouched). Returns 0, or -1 with
+ * ne_last_error(). */
+typedef struct {
+  uint64_t tensors, misaligned_tensors, misaligned_bytes, files_rewritten, files_linked, files_kept, bytes_written;
+} ne_pack_align_stats;
+NE_API int ne_pack_align(const char *src_dir, const char *dst_dir, uint64_t align, int dry_run,
+                         ne_pack_align_stats *stats);
+
 /* ---- one EXL3 linear: y[R][out] = x[R][in] @ W, W = diag(suh) H_in W' H_out diag(svh) ----
  * trellis U16 [in/16][out/16][16K] (tile (tk, tn) = W'[16tk.., 16tn..] in the reference's slot order), suh F16 [in],
  * svh F16 [out]; K 1..8; in, out multiples of 16 and of their Hadamard sizes (128, 64, 32 or 16). */
