@@ -616,19 +616,26 @@ template <int K>
 constexpr int kDA = K >= 6 ? 1 : 2;
 template <int K>
 constexpr int kDB = K >= 6 ? 3 : 5;
-template <int K, int NA>
+// NR: rows of a chunk, 128 (4 row blocks) or 32 (1 row block, for at most 32 rows: a quarter of the A ring, so that
+// three workgroups share a CU)
+template <int K, int NA, int NR = kChunkRows>
 struct GemmIo {
   static constexpr uint32_t TB = 32u * K;                  // bytes of one 16x16 tile
   static constexpr uint32_t PB = 2 * 2 * TB;               // a wave's B bytes per step (a pair x 2 k tiles)
-  static constexpr uint32_t AB = NA * kChunkRows * 64;     // A bytes per step (NA x 128 rows x 32 halves)
+  static constexpr uint32_t AB = NA * NR * 64;             // A bytes per step (NA x NR rows x 32 halves)
   static constexpr int DA = kDA<K>, DB = kDB<K>;
   static constexpr int RA = DA + 1, RB = DB + 1;           // ring slots
   static constexpr uint32_t LDS_RING = RA * AB + kWavesG * RB * PB;
-  // the epilogues exchange 32 x 32 float tiles with a 36-float row pitch: 8 (down), 8 + 4 (gate/up)
-  static constexpr uint32_t EPI = (NA == 2 ? 12u : 8u) * 32u * 36u * 4u;
+  // the epilogues: row-major, 32 x 256 floats; transposed (NR = 128 only), 32 x 32 float tiles with a 36-float row
+  // pitch: 8 (down), 8 + 4 (gate/up)
+  static constexpr uint32_t EPI = NR == kChunkRows ? (NA == 2 ? 12u : 8u) * 32u * 36u * 4u : 32u * 256u * 4u;
   static constexpr uint32_t LDS = LDS_RING > EPI ? LDS_RING : EPI;
-  static constexpr int OA = NA, OB = (PB + 1023) / 1024;   // requests per A / B step
+  // requests per A step: NR = 128, each wave loads 16 rows of each operand; NR = 32, each wave one slice of
+  // NA NR / 8 rows (its lanes past 4 rows each idle)
+  static constexpr int OA = NR == kChunkRows ? NA : 1, OB = (PB + 1023) / 1024;
+  static constexpr int NRB = NR / 32;
   static_assert(LDS <= 81920, "two workgroups per CU");
+  static_assert(NR == kChunkRows || (NR == 32 && LDS <= 53248), "three workgroups per CU at 32 rows");
   static_assert(RB % RA == 0 && DB > DA, "ring shapes");
 };
 // Issue order: prologue A(0) B(0) A(1) B(1) .. A(DA-1) B(DA-1) B(DA) .. B(DB-1); step j then issues A(j + DA) and
@@ -699,10 +706,11 @@ __device__ __forceinline__ void decode_step(const uint8_t *src, const BLane<K> &
 __device__ __forceinline__ int a_swz(int r) { return ((r >> 1) ^ ((r >> 3) & 1)) & 3; }
 // TR: the weights are the matrix cores' A operand and the rows their B operand, so acc[rb] holds the transposed
 // product: lane (n, h) value i = output column 8 (i / 4) + 4 h + i % 4 of the wave's 32, row 32 rb + n.
-template <int K, int NA, bool TR = false>
+template <int K, int NA, bool TR = false, int NR = kChunkRows>
 __device__ void chunk_gemm(const uint16_t *A, int lda, int ahalf, int aidx, int nrows, const uint8_t *tr, int IT,
-                           int pair, uint8_t *lds, f32x16 (&acc)[kRowBlocks], uint64_t *dbg, int kt0, int nkt) {
-  using Io = GemmIo<K, NA>;
+                           int pair, uint8_t *lds, f32x16 (&acc)[NR / 32], uint64_t *dbg, int kt0, int nkt) {
+  using Io = GemmIo<K, NA, NR>;
+  constexpr int NRB = Io::NRB;
 #ifdef IJ_BATCH_TRACE  // debug builds only: shader-clock stamps of step 20 per (workgroup, wave)
   uint64_t *drow = dbg ? dbg + ((uint64_t)8192 + blockIdx.x * 8 + (threadIdx.x >> 6)) * 8 : nullptr;
 #define IJ_STAMP(t_, f_) \
@@ -718,20 +726,28 @@ __device__ void chunk_gemm(const uint16_t *A, int lda, int ahalf, int aidx, int 
   const BLane<K> BL = b_lane<K>((uint32_t)lane);
   const int nrb = (nrows + 31) / 32;
 #pragma unroll
-  for (int rb = 0; rb < kRowBlocks; rb++)
+  for (int rb = 0; rb < NRB; rb++)
 #pragma unroll
     for (int i = 0; i < 16; i++) acc[rb][i] = 0.f;
-  // A(t): 16 rows of this wave per operand. Row r's 64 bytes (four 16-byte quarters q: k 8q .. 8q + 7) sit at
-  // r * 64 with quarter q in position q ^ a_swz(r), so that a read of one quarter of consecutive rows is free of bank
-  // conflicts. DMA lane l fills position l % 4 of row 16 w + l / 4. Stream addresses are a wave-uniform base plus a
-  // fixed per-lane offset.
-  const int rr = min(wave * 16 + (lane >> 2), nrows - 1);
-  const uint32_t a_off = (uint32_t)(rr * lda + ((lane & 3) ^ a_swz(lane >> 2)) * 8) * 2;
+  // A(t): NR = 128: 16 rows of this wave per operand; NR = 32: the wave's slice of RW = 4 NA rows of operand
+  // (RW w) / 32. Row r's 64 bytes (four 16-byte quarters q: k 8q .. 8q + 7) sit at r * 64 with quarter q in position
+  // q ^ a_swz(r), so that a read of one quarter of consecutive rows is free of bank conflicts. DMA lane l fills
+  // position l % 4 of row r0 + l / 4 (r0 the wave's first row). Stream addresses are a wave-uniform base plus a fixed
+  // per-lane offset.
+  constexpr int RW = NR == kChunkRows ? 16 : 4 * NA;
+  const int ao = NR == kChunkRows ? 0 : (wave * RW) / NR, r0 = NR == kChunkRows ? wave * 16 : (wave * RW) % NR;
+  const int rr = min(r0 + (lane >> 2), nrows - 1);
+  const uint32_t a_off = (uint32_t)(rr * lda + ((lane & 3) ^ a_swz(r0 + (lane >> 2))) * 8) * 2;
   const __amdgpu_buffer_rsrc_t ra = stream_rsrc(A + kt0 * 16);
   auto issue_a = [&](int t, int slot) {
+    if constexpr (NR == kChunkRows) {
 #pragma unroll
-    for (int o = 0; o < NA; o++)
-      dma16_buf(ra, a_off, (uint32_t)(o * ahalf * 2 + t * 64), ring_a + slot * Io::AB + o * kChunkRows * 64 + wave * 1024);
+      for (int o = 0; o < NA; o++)
+        dma16_buf(ra, a_off, (uint32_t)(o * ahalf * 2 + t * 64), ring_a + slot * Io::AB + o * NR * 64 + wave * 1024);
+    } else {
+      if (lane < 4 * RW)  // one request per wave and step (the idle lanes load nothing)
+        dma16_buf(ra, a_off, (uint32_t)(ao * ahalf * 2 + t * 64), ring_a + slot * Io::AB + ao * NR * 64 + r0 * 64);
+    }
   };
   // B(t): the wave's pair at k tiles 2t, 2t + 1 (contiguous)
   const __amdgpu_buffer_rsrc_t rb =
@@ -757,7 +773,7 @@ __device__ void chunk_gemm(const uint16_t *A, int lda, int ahalf, int aidx, int 
     issue_b(j, j);
   }
   begin_step(0, 0);
-  const uint8_t *a_lane = ring_a + aidx * kChunkRows * 64 + (lane & 31) * 64;
+  const uint8_t *a_lane = ring_a + aidx * NR * 64 + (lane & 31) * 64;
   const int q0 = ((lane >> 5) ^ a_swz(lane & 31)) * 16, q1 = ((2 + (lane >> 5)) ^ a_swz(lane & 31)) * 16;
   for (int t0 = 0; t0 < NS; t0 += U) {
 #pragma unroll
@@ -769,11 +785,11 @@ __device__ void chunk_gemm(const uint16_t *A, int lda, int ahalf, int aidx, int 
       const f16x8 b0 = bf[0], b1 = bf[1];
 #pragma unroll
       for (int h = 0; h < 2; h++) {  // k tile h of the step for every row block: no two dependent MFMAs adjacent
-        f16x8 af[kRowBlocks];
+        f16x8 af[NRB];
 #pragma unroll
-        for (int rb = 0; rb < kRowBlocks; rb++) af[rb] = *(const f16x8 *)(at + rb * 2048 + (h ? q1 : q0));
+        for (int rb = 0; rb < NRB; rb++) af[rb] = *(const f16x8 *)(at + rb * 2048 + (h ? q1 : q0));
 #pragma unroll
-        for (int rb = 0; rb < kRowBlocks; rb++)
+        for (int rb = 0; rb < NRB; rb++)
           if (rb < nrb)
             acc[rb] = TR ? __builtin_amdgcn_mfma_f32_32x32x16_f16(h ? b1 : b0, af[rb], acc[rb], 0, 0, 0)
                          : __builtin_amdgcn_mfma_f32_32x32x16_f16(af[rb], h ? b1 : b0, acc[rb], 0, 0, 0);
@@ -834,8 +850,8 @@ __device__ __forceinline__ f32x16 h32_tile(const f32x16 &v, const f16x8 (&hA)[2]
 }
 
 // gate/up: chunk ch, 128-column block ib of inter; wave w: projection w / 4 (gate, up), pair 4 ib + w % 4
-template <int K, int KS, bool TR>
-__global__ __launch_bounds__(512, 4) void bat_gateup(MoeArgs a, const uint32_t *bk, const uint32_t *chunks,
+template <int K, int KS, bool TR, int NR>
+__global__ __launch_bounds__(512, NR == kChunkRows ? 4 : 6) void bat_gateup(MoeArgs a, const uint32_t *bk, const uint32_t *chunks,
                                                      const uint32_t *rows, const uint16_t *xh, uint16_t *hh) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int nib = a.inter / 128;
@@ -845,13 +861,15 @@ __global__ __launch_bounds__(512, 4) void bat_gateup(MoeArgs a, const uint32_t *
   const int e = (int)chunks[3 * ch], row0 = (int)chunks[3 * ch + 1], nrows = (int)chunks[3 * ch + 2];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, proj = wave >> 2;
   const uint8_t *blk = expert_block(a, e);
-  f32x16 acc[kRowBlocks];
+  static_assert(!TR || NR == kChunkRows, "transposed products at 128-row chunks");
+  constexpr int NRB = NR / 32;
+  f32x16 acc[NRB];
   const uint16_t *A = xh + (uint64_t)row0 * 2 * a.hid;  // [row][gate | up][hid]
   const int pair = ib * 4 + (wave & 3);
   if (e >= a.ne)
-    chunk_gemm<KS, 2, TR>(A, 2 * a.hid, a.hid, proj, nrows, blk + tr_of(a, e, proj), a.hid / 16, pair, lds, acc, a.trace, 0, a.hid / 16);
+    chunk_gemm<KS, 2, TR, NR>(A, 2 * a.hid, a.hid, proj, nrows, blk + tr_of(a, e, proj), a.hid / 16, pair, lds, acc, a.trace, 0, a.hid / 16);
   else
-    chunk_gemm<K, 2, TR>(A, 2 * a.hid, a.hid, proj, nrows, blk + tr_of(a, e, proj), a.hid / 16, pair, lds, acc, a.trace, 0, a.hid / 16);
+    chunk_gemm<K, 2, TR, NR>(A, 2 * a.hid, a.hid, proj, nrows, blk + tr_of(a, e, proj), a.hid / 16, pair, lds, acc, a.trace, 0, a.hid / 16);
   if constexpr (!TR) {
   // epilogue per 32-row block: columns to LDS as [32][256] f32 (gate 0..127, up 128..255), then one wave per row
   float *ot = (float *)lds;
@@ -862,7 +880,7 @@ __global__ __launch_bounds__(512, 4) void bat_gateup(MoeArgs a, const uint32_t *
   const float sd0 = h2f(sud[lane]), sd1 = h2f(sud[lane + 64]);
   const int nrb = (nrows + 31) / 32;
 #pragma unroll
-  for (int rb = 0; rb < kRowBlocks; rb++) {  // compile-time rb: acc stays in registers
+  for (int rb = 0; rb < NRB; rb++) {  // compile-time rb: acc stays in registers
     if (rb >= nrb) break;
     __syncthreads();
 #pragma unroll
@@ -911,7 +929,7 @@ __global__ __launch_bounds__(512, 4) void bat_gateup(MoeArgs a, const uint32_t *
   float *x1 = (float *)lds, *x2 = x1 + 8 * 32 * 36;
   const int nrb = (nrows + 31) / 32;
 #pragma unroll
-  for (int rb = 0; rb < kRowBlocks; rb++) {
+  for (int rb = 0; rb < NRB; rb++) {
     if (rb >= nrb) break;
     const f32x16 T = h32_tile(acc[rb], hA1, lane);
     __syncthreads();  // the ring (first block) or the previous block's tiles are no longer read
@@ -975,8 +993,8 @@ __global__ __launch_bounds__(512, 4) void bat_gateup(MoeArgs a, const uint32_t *
 
 // down: chunk ch, 256 columns of hid (output blocks 2 ob2, 2 ob2 + 1); wave w: pair 8 ob2 + w. Output per
 // (token, slot): H over each 128-column block, svh_d, the slot's route weight.
-template <int K, int KS, bool TR>
-__global__ __launch_bounds__(512, 4) void bat_down(MoeArgs a, const uint32_t *bk, const uint32_t *chunks,
+template <int K, int KS, bool TR, int NR>
+__global__ __launch_bounds__(512, NR == kChunkRows ? 4 : 6) void bat_down(MoeArgs a, const uint32_t *bk, const uint32_t *chunks,
                                                    const uint32_t *rows, const uint16_t *hh, float *dnw) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int nob = a.hid / 256;
@@ -991,12 +1009,14 @@ __global__ __launch_bounds__(512, 4) void bat_down(MoeArgs a, const uint32_t *bk
   __shared__ float m_w[kChunkRows];
   const int mt = threadIdx.x;
   const uint32_t sl = mt < nrows ? rows[row0 + mt] : 0u;
-  f32x16 acc[kRowBlocks];
+  static_assert(!TR || NR == kChunkRows, "transposed products at 128-row chunks");
+  constexpr int NRB = NR / 32;
+  f32x16 acc[NRB];
   const uint16_t *A = hh + (uint64_t)row0 * a.inter;
   if (e >= a.ne)
-    chunk_gemm<KS, 1, TR>(A, a.inter, 0, 0, nrows, blk + tr_of(a, e, 2), a.inter / 16, ob2 * 8 + wave, lds, acc, nullptr, 0, a.inter / 16);
+    chunk_gemm<KS, 1, TR, NR>(A, a.inter, 0, 0, nrows, blk + tr_of(a, e, 2), a.inter / 16, ob2 * 8 + wave, lds, acc, nullptr, 0, a.inter / 16);
   else
-    chunk_gemm<K, 1, TR>(A, a.inter, 0, 0, nrows, blk + tr_of(a, e, 2), a.inter / 16, ob2 * 8 + wave, lds, acc, nullptr, 0, a.inter / 16);
+    chunk_gemm<K, 1, TR, NR>(A, a.inter, 0, 0, nrows, blk + tr_of(a, e, 2), a.inter / 16, ob2 * 8 + wave, lds, acc, nullptr, 0, a.inter / 16);
   if (mt < nrows) {
     const int tok = sl / a.nslot, k = sl % a.nslot;
     m_dst[mt] = sl;
@@ -1013,7 +1033,7 @@ __global__ __launch_bounds__(512, 4) void bat_down(MoeArgs a, const uint32_t *bk
   }
   const int nrb = (nrows + 31) / 32;
 #pragma unroll
-  for (int rb = 0; rb < kRowBlocks; rb++) {
+  for (int rb = 0; rb < NRB; rb++) {
     if (rb >= nrb) break;
     __syncthreads();
 #pragma unroll
@@ -1053,7 +1073,7 @@ __global__ __launch_bounds__(512, 4) void bat_down(MoeArgs a, const uint32_t *bk
   float *xt = (float *)lds;
   const int nrb = (nrows + 31) / 32;
 #pragma unroll
-  for (int rb = 0; rb < kRowBlocks; rb++) {
+  for (int rb = 0; rb < NRB; rb++) {
     if (rb >= nrb) break;
     const f32x16 T = h32_tile(acc[rb], hA, lane);
     __syncthreads();  // the ring (first block) or the previous block's rows are no longer read
@@ -1114,13 +1134,13 @@ __global__ __launch_bounds__(256) void bat_combine(MoeArgs a, const float *__res
 // workgroup (g, s) multiplies the prepared rows xh (fp16, kp order) by tile pairs 8g .. 8g + 7 (one per wave) over k
 // split s; part[s][r][OTp * 16] as the GEMV path, summed and rotated by lin_finish.
 template <int K>
-__global__ __launch_bounds__(512, 4) void lin_mm(LinArgs a) {
+__global__ __launch_bounds__(512, 6) void lin_mm(LinArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int NP = (a.OT + 1) / 2, OTp = 2 * NP, NG = (NP + kWavesG - 1) / kWavesG;
   const int g = blockIdx.x % NG, s = blockIdx.x / NG, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int p = g * kWavesG + wave, span = a.IT / a.S;
-  f32x16 acc[kRowBlocks];
-  chunk_gemm<K, 1>(a.xh, a.in, 0, 0, a.R, (const uint8_t *)a.tiles, a.IT, min(p, NP - 1), lds, acc, nullptr, s * span,
+  f32x16 acc[1];
+  chunk_gemm<K, 1, false, 32>(a.xh, a.in, 0, 0, a.R, (const uint8_t *)a.tiles, a.IT, min(p, NP - 1), lds, acc, nullptr, s * span,
                    span);
   if (p >= NP) return;
 #pragma unroll
@@ -1131,7 +1151,7 @@ __global__ __launch_bounds__(512, 4) void lin_mm(LinArgs a) {
 }
 template <int K>
 static void lin_mm_launch(const LinArgs &a, hipStream_t s) {
-  const size_t lds = GemmIo<K, 1>::LDS;
+  const size_t lds = GemmIo<K, 1, 32>::LDS;
   static bool attr = false;
   if (!attr) {
     IJ_HIP(hipFuncSetAttribute((const void *)&lin_mm<K>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
@@ -1154,30 +1174,36 @@ void launch_lin_mm(const LinArgs &a, hipStream_t s) {
 
 // ---------------------------------------------------------------------------------------------------- host side
 namespace {
-template <int K, int KS, bool TR>
+template <int K, int KS, bool TR, int NR>
 void launch_gemms_as(const MoeArgs &a, const MoeBatchBufs &b, hipStream_t s) {
   // the routed (K) and shared (KS) chunks use ring layouts of their own widths: room for the larger of each
-  const size_t lg = std::max(GemmIo<K, 2>::LDS, GemmIo<KS, 2>::LDS), ld = std::max(GemmIo<K, 1>::LDS, GemmIo<KS, 1>::LDS);
+  const size_t lg = std::max(GemmIo<K, 2, NR>::LDS, GemmIo<KS, 2, NR>::LDS);
+  const size_t ld = std::max(GemmIo<K, 1, NR>::LDS, GemmIo<KS, 1, NR>::LDS);
   static bool attr = false;
   if (!attr) {
-    IJ_HIP(hipFuncSetAttribute((const void *)&bat_gateup<K, KS, TR>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lg));
-    IJ_HIP(hipFuncSetAttribute((const void *)&bat_down<K, KS, TR>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)ld));
+    IJ_HIP(hipFuncSetAttribute((const void *)&bat_gateup<K, KS, TR, NR>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)lg));
+    IJ_HIP(hipFuncSetAttribute((const void *)&bat_down<K, KS, TR, NR>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)ld));
     attr = true;
   }
-  hipLaunchKernelGGL((bat_gateup<K, KS, TR>), dim3((b.max_chunks * (a.inter / 128) + 7) & ~7), dim3(64 * kWavesG), lg, s, a,
+  hipLaunchKernelGGL((bat_gateup<K, KS, TR, NR>), dim3((b.max_chunks * (a.inter / 128) + 7) & ~7), dim3(64 * kWavesG), lg, s, a,
                      b.bk, b.chunks, b.rows, b.xh, b.hh);
-  hipLaunchKernelGGL((bat_down<K, KS, TR>), dim3((b.max_chunks * (a.hid / 256) + 7) & ~7), dim3(64 * kWavesG), ld, s, a,
+  hipLaunchKernelGGL((bat_down<K, KS, TR, NR>), dim3((b.max_chunks * (a.hid / 256) + 7) & ~7), dim3(64 * kWavesG), ld, s, a,
                      b.bk, b.chunks, b.rows, b.hh, b.dnw);
 }
 // Chunks of many rows (8 or more per routed expert on average) take the transposed products and the matrix-core
 // Hadamard epilogues; chunks of a row or two (speculative verify) the row-major products and lane butterflies, which
 // cost less there.
+// At most 32 rows (speculative verify) no chunk exceeds 32 rows: the one-row-block form, three workgroups per CU.
 template <int K, int KS>
 void launch_gemms(const MoeArgs &a, const MoeBatchBufs &b, hipStream_t s) {
   if ((int64_t)a.R * a.topk >= 8LL * a.ne)
-    launch_gemms_as<K, KS, true>(a, b, s);
+    launch_gemms_as<K, KS, true, kChunkRows>(a, b, s);
+  else if (a.R <= 32)
+    launch_gemms_as<K, KS, false, 32>(a, b, s);
   else
-    launch_gemms_as<K, KS, false>(a, b, s);
+    launch_gemms_as<K, KS, false, kChunkRows>(a, b, s);
 }
 }  // namespace
 
