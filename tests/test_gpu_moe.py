@@ -165,6 +165,19 @@ def test_moe_batch_chunks(eng, oracle, R):
     assert np.array_equal(m.run(x), y)  # deterministic despite the unordered placement inside an expert
 
 
+@pytest.mark.parametrize("R", [32, 33])
+def test_moe_batch_row_block_forms(eng, oracle, R):
+    """64 experts, top-10 + shared: at 32 rows the GEMMs take their one-row-block form and the shared expert fills a
+    whole 32-row chunk; at 33 rows the 128-row form (both row-major: few rows per routed expert)."""
+    print(f"moe batch forms R{R}", flush=True)
+    w = synth.moe_layer(90 + R, hid=1024, inter=256, ne=64, topk=10, K=5, shared=True, Ks=5, sgate=True)
+    W = oracle.MoeWeights(w)
+    m = eng.moe_create(w)
+    x = synth.bf16_values(np.random.default_rng(91), R, 1024)
+    y, _ = check_layer(eng, oracle, m, W, x, exact=False)
+    assert np.array_equal(m.run(x), y)
+
+
 def test_moe_batch_matches_staged(eng, oracle, monkeypatch):
     """The grouped path and the staged kernels compute the same layer for several rows."""
     w = synth.moe_layer(81, hid=2048, inter=512, ne=64, topk=10, K=5, shared=True, Ks=5, sgate=False)
