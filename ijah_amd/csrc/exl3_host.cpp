@@ -179,7 +179,7 @@ static void timed(hipStream_t s, double *gpu_ms, const std::function<void()> &wo
 }  // extern "C"
 
 // LinArgs of one run at R rows (the k-split scratch grown as needed)
-static LinArgs lin_args(ne_exl3_lin *l, int R, const float *x, float *y) {
+static LinArgs lin_args(ne_exl3_lin *l, int R, const float *x, float *y, const LinEpi &epi = LinEpi()) {
   const int S = l->splits(R);
   if (S > l->part_S) {
     dev_free(l->part);
@@ -205,6 +205,7 @@ static LinArgs lin_args(ne_exl3_lin *l, int R, const float *x, float *y) {
   a.y = y;
   a.xh = l->xh;
   a.part = l->part;
+  a.epi = epi;
   // one launch unless its per-workgroup input preparation (each workgroup prepares the 128-blocks of its own k span)
   // adds up to more than ~8K block preparations (large outputs with few splits, e.g. a vocabulary head)
   const long prep_blocks = (long)(l->OTp / 2) * S * ((l->IT / S * 16 + 127) / 128 + 1);
@@ -214,14 +215,18 @@ static LinArgs lin_args(ne_exl3_lin *l, int R, const float *x, float *y) {
 
 // The launches of one run: rows beyond the GEMV's 8 take the matrix-core GEMM when the k tiles pair up (IT even);
 // otherwise they run as groups of 8 rows through the GEMV path.
-static void lin_launch(ne_exl3_lin *l, int R, const float *x, float *y, hipStream_t s) {
+static void lin_launch(ne_exl3_lin *l, int R, const float *x, float *y, hipStream_t s,
+                       const LinEpi &epi = LinEpi()) {
   if (R <= kLinSimdRows || l->IT % 2 == 0) {
-    launch_lin(lin_args(l, R, x, y), s);
+    launch_lin(lin_args(l, R, x, y, epi), s);
     return;
   }
+  const size_t ldy = epi.ldy ? epi.ldy : l->out;
   for (int r0 = 0; r0 < R; r0 += kLinSimdRows) {
     const int n = std::min(kLinSimdRows, R - r0);
-    launch_lin(lin_args(l, n, x + (size_t)r0 * l->in, y + (size_t)r0 * l->out), s);
+    LinEpi e = epi;
+    e.row0 = epi.row0 + r0;
+    launch_lin(lin_args(l, n, x + (size_t)r0 * l->in, y + (size_t)r0 * ldy, e), s);
   }
 }
 
@@ -238,6 +243,51 @@ NE_API int ne_exl3_lin_run(ne_exl3_lin *l, int R, const ne_buf *x, uint64_t x_of
     const float *xp = (const float *)((const char *)x->dev + x_off);
     float *yp = (float *)((char *)y->dev + y_off);
     timed(stream(), gpu_ms, [&] { lin_launch(l, R, xp, yp, stream()); });
+  });
+}
+
+NE_API int ne_exl3_lin_run_epi(ne_exl3_lin *l, int R, const ne_buf *x, uint64_t x_off, ne_buf *y, uint64_t y_off,
+                               const ne_exl3_epi *epi, double *gpu_ms) {
+  return c_call([&] {
+    IJ_CHECK(l && x && y && epi, "null argument");
+    IJ_CHECK(R >= 1 && R <= kLinMaxRows, "rows %d (1..%d)", R, kLinMaxRows);
+    IJ_CHECK(x_off % 4 == 0 && y_off % 4 == 0, "offsets must be 4-byte aligned");
+    const int k = epi->kind;
+    IJ_CHECK(k == 0 || k == 1 || k == 2 || k == 3 || k == 5 || k == 6 || k == 7,
+             "epilogue %d (0, 1, 2, 3, 5, 6 or 7; 4 and 8 are not supported)", k);
+    const int ldy = epi->ldy ? epi->ldy : l->out;
+    IJ_CHECK(ldy >= l->out, "ldy %d below out %d", ldy, l->out);
+    IJ_CHECK(x_off + (uint64_t)R * l->in * 4 <= x->size, "x buffer too small for [%d][%d] f32", R, l->in);
+    IJ_CHECK(y_off + ((uint64_t)(R - 1) * ldy + l->out) * 4 <= y->size, "y buffer too small for %d rows of stride %d",
+             R, ldy);
+    LinEpi e;
+    e.kind = k;
+    e.refr = epi->refr ? 1 : 0;
+    e.ldy = ldy;
+    auto need = [&](const ne_buf *b, uint64_t bytes, const char *name) -> float * {
+      IJ_CHECK(b && b->size >= bytes, "epilogue %d: %s missing or under %llu bytes", k, name,
+               (unsigned long long)bytes);
+      return (float *)b->dev;
+    };
+    if (k == 1) {
+      IJ_CHECK(epi->hc >= 1 && epi->hc <= 8, "epilogue 1: hc %d (1..8)", epi->hc);
+      e.hc = epi->hc;
+      const uint64_t hb = (uint64_t)R * e.hc * l->out * 4;
+      e.e0 = need(epi->e0, hb, "e0 (h)");
+      e.e1 = need(epi->e1, (uint64_t)R * 8 * 4, "e1 (inj)");
+      e.e2 = need(epi->e2, hb, "e2 (hout)");
+    } else if (k == 6) {
+      e.e0 = need(epi->e0, (uint64_t)l->out * 2, "e0 (A_log)");
+      e.e1 = need(epi->e1, (uint64_t)l->out * 2, "e1 (dt_bias)");
+    } else if (k == 7) {
+      IJ_CHECK(l->out <= 640, "epilogue 7: out %d above 640 (512 + one 128-wide key)", l->out);
+      e.e0 = need(epi->e0, 512, "e0 (key cache)");
+      e.e1 = need(epi->e1, 4, "e1 (position)");
+      e.cap = (int)std::min<uint64_t>(epi->e0->size / 512, 1u << 30);
+    }
+    const float *xp = (const float *)((const char *)x->dev + x_off);
+    float *yp = (float *)((char *)y->dev + y_off);
+    timed(stream(), gpu_ms, [&] { lin_launch(l, R, xp, yp, stream(), e); });
   });
 }
 

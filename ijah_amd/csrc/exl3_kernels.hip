@@ -486,6 +486,48 @@ __global__ __launch_bounds__(256) void moe_combine(MoeArgs a) {
 
 
 // ------------------------------------------------------------------------------------------------ trunk linear
+// a finished output v of row r, column c through the linear's epilogue into y (and the epilogue's side buffers)
+__device__ __forceinline__ float epi_rr(float x, int refr) { return refr ? bf16_round(x) : x; }
+__device__ __forceinline__ float epi_bf(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+__device__ __forceinline__ void lin_store(const LinArgs &a, int r, int c, float v) {
+  const LinEpi &e = a.epi;
+  float *y = a.y + (uint64_t)r * (e.ldy ? e.ldy : a.out) + c;
+  const int q = e.refr, R = e.row0 + r;
+  switch (e.kind) {
+    case 1: {
+      const float br = epi_rr(v, q);
+      *y = br;
+      for (int s = 0; s < e.hc; s++) {
+        const uint64_t o = ((uint64_t)R * e.hc + s) * a.out + c;
+        e.e2[o] = epi_rr(e.e0[o] + epi_rr(br * e.e1[R * 8 + s], q), q);
+      }
+      break;
+    }
+    case 2: {
+      const float t = epi_rr(v, q) * 0.25f;
+      *y = epi_rr(t / (1.f + expf(-t)), q);
+      break;
+    }
+    case 3: *y = epi_rr(v, q); break;
+    case 5: *y = epi_rr(1.f / (1.f + expf(-epi_rr(v, q))), q); break;
+    case 6: {
+      const float ex = expf(epi_bf(((const uint16_t *)e.e0)[c])), dt = epi_bf(((const uint16_t *)e.e1)[c]);
+      const float u = epi_rr(epi_rr(v, q) + dt, q);
+      const float sp = epi_rr(u > 20.f ? u : logf(1.f + expf(u)), q);
+      *y = expf(-ex * sp);
+      break;
+    }
+    case 7:
+      *y = v;
+      if (c >= 512) {
+        const uint64_t t = (uint64_t)((const uint32_t *)e.e1)[0] + R;
+        if (t < (uint64_t)e.cap) e.e0[t * 128 + (c - 512)] = v;
+      }
+      break;
+    default: *y = v;
+  }
+}
+
 // lin_prep: xh[r][kp(i)] = fp16(H_in(x * suh)) (reference kernels/trunk6/trunk6.metal:68-85), grid R x ceil(in/128).
 __global__ __launch_bounds__(64) void lin_prep(LinArgs a) {
   const int nch = (a.in + 127) / 128;
@@ -672,8 +714,8 @@ __global__ __launch_bounds__(256) void lin_step(LinArgs a) {
     v0 = m0 ? v0 : 0.f;
     v1 = m1 ? v1 : 0.f;
     fwht2(v0, v1, lane, a.had_out, a.sc_out);
-    if (m0) a.y[(uint64_t)r * a.out + i0] = v0 * h2f(a.svh[i0]);
-    if (m1) a.y[(uint64_t)r * a.out + i1] = v1 * h2f(a.svh[i1]);
+    if (m0) lin_store(a, r, i0, v0 * h2f(a.svh[i0]));
+    if (m1) lin_store(a, r, i1, v1 * h2f(a.svh[i1]));
   }
 }
 
@@ -706,8 +748,8 @@ __global__ __launch_bounds__(64) void lin_finish(LinArgs a) {
   v0 = m0 ? v0 : 0.f;
   v1 = m1 ? v1 : 0.f;
   fwht2(v0, v1, lane, a.had_out, a.sc_out);
-  if (m0) a.y[(uint64_t)r * a.out + i0] = v0 * h2f(a.svh[i0]);
-  if (m1) a.y[(uint64_t)r * a.out + i1] = v1 * h2f(a.svh[i1]);
+  if (m0) lin_store(a, r, i0, v0 * h2f(a.svh[i0]));
+  if (m1) lin_store(a, r, i1, v1 * h2f(a.svh[i1]));
 }
 
 // ------------------------------------------------------------------------------------------------ decode

@@ -100,6 +100,17 @@ inline size_t sync_words(int R, int nslot, int hid, int inter) {
 }
 enum { kSyncErrWord = 3 * kSyncStride };
 
+// Fused epilogue of a linear's finished outputs v (after H_out and svh) (reference kernels/trunk6/trunk6.metal:129-197,
+// t6_epi_col; rr = round to bf16 when refr): 0 y = v; 1 out_hc y = br = rr(v), e2[r][s][c] = rr(e0[r][s][c] +
+// rr(br e1[r][s])) for s < hc (e0, e2 f32 [R][hc][out], e1 f32 [R][8]); 2 y = rr(silu(rr(v) / 4)); 3 y = rr(v);
+// 5 y = rr(sigmoid(rr(v))); 6 y = exp(-exp(A_log[c]) softplus_rr(rr(rr(v) + dt_bias[c]))) (e0 = A_log, e1 = dt_bias,
+// bf16 [out]); 7 y = v, and for c >= 512 e0[(T + r) 128 + c - 512] = v (e0 f32 cache rows of 128, e1 u32 [1] = T).
+// y rows are ldy floats apart; row0 = the launch's first row among the caller's (row-grouped launches); cap = e0's
+// rows of 128 for kind 7 (cache rows at or beyond it are not written).
+struct LinEpi {
+  int kind = 0, refr = 1, hc = 4, ldy = 0, row0 = 0, cap = 0;
+  float *e0 = nullptr, *e1 = nullptr, *e2 = nullptr;
+};
 struct LinArgs {
   const uint32_t *tiles;  // re-laid trellis
   const uint16_t *suh, *svh;
@@ -112,6 +123,7 @@ struct LinArgs {
   float *part;            // [S][R][OTp * 16] (scratch)
   uint32_t *cnt;          // per 128-column output block, kSyncStride apart, zero between launches; null: the staged
                           // three-kernel path (prep, GEMV, finish)
+  LinEpi epi;
 };
 // rows up to kLinSimdRows take the VALU GEMV (lin_gemv), more rows (up to kLinMaxRows) the matrix cores (lin_mm)
 constexpr int kLinSimdRows = 8, kLinMaxRows = 32;

@@ -83,6 +83,7 @@ SIGNATURES = {
     "ne_exl3_lin_free": (None, [_vp]),
     "ne_exl3_lin_info": (_i, [_vp, C.POINTER(_i), C.POINTER(_i), C.POINTER(_i)]),
     "ne_exl3_lin_run": (_i, [_vp, _i, _vp, _u64, _vp, _u64, _dp]),
+    "ne_exl3_lin_run_epi": (_i, [_vp, _i, _vp, _u64, _vp, _u64, _vp, _dp]),
     "ne_exl3_lin_decode": (_i, [_vp, _vp, _dp]),
     "ne_moe_create": (_vp, [C.POINTER(MoeDesc)]),
     "ne_moe_load": (_vp, [_vp, C.c_char_p, _i]),
@@ -104,6 +105,13 @@ class PackAlignStats(C.Structure):
     """include/ijah_exl3.h ne_pack_align_stats"""
     _fields_ = [(n, C.c_uint64) for n in ("tensors", "misaligned_tensors", "misaligned_bytes", "files_rewritten",
                                           "files_linked", "files_kept", "bytes_written")]
+
+
+class Exl3Epi(C.Structure):
+    """include/ijah_exl3.h ne_exl3_epi: a linear's fused epilogue (kind 0/1/2/3/5/6/7, bf16 rounding switch, streams,
+    y row stride in floats, extra buffers)"""
+    _fields_ = [("kind", C.c_int), ("refr", C.c_int), ("hc", C.c_int), ("ldy", C.c_int),
+                ("e0", C.c_void_p), ("e1", C.c_void_p), ("e2", C.c_void_p)]
 
 
 def bf16_to_f32(u16):
@@ -260,6 +268,15 @@ class Exl3Linear:
                                                   C.byref(ms) if timed else None), "ne_exl3_lin_run")
         return ms.value
 
+    def run_epi(self, R, x, y, kind, x_off=0, y_off=0, refr=True, hc=4, ldy=0, e0=None, e1=None, e2=None,
+                timed=False):
+        """ne_exl3_lin_run_epi; e0..e2 are device buffers (or None)"""
+        d = Exl3Epi(kind, int(bool(refr)), hc, ldy, *(None if b is None else b.ptr for b in (e0, e1, e2)))
+        ms = C.c_double(0)
+        self.eng._ok(self.eng.lib.ne_exl3_lin_run_epi(self.ptr, R, x.ptr, x_off, y.ptr, y_off, C.byref(d),
+                                                      C.byref(ms) if timed else None), "ne_exl3_lin_run_epi")
+        return ms.value
+
     def run(self, x):
         x = np.ascontiguousarray(np.atleast_2d(x), np.float32)
         R = x.shape[0]
@@ -297,6 +314,15 @@ class MoeLayer:
         ms = C.c_double(0)
         self.eng._ok(self.eng.lib.ne_moe_run(self.ptr, R, x.ptr, x_off, y.ptr, y_off,
                                              C.byref(ms) if timed else None), "ne_moe_run")
+        return ms.value
+
+    def run_epi(self, R, x, y, kind, x_off=0, y_off=0, refr=True, hc=4, ldy=0, e0=None, e1=None, e2=None,
+                timed=False):
+        """ne_exl3_lin_run_epi; e0..e2 are device buffers (or None)"""
+        d = Exl3Epi(kind, int(bool(refr)), hc, ldy, *(None if b is None else b.ptr for b in (e0, e1, e2)))
+        ms = C.c_double(0)
+        self.eng._ok(self.eng.lib.ne_exl3_lin_run_epi(self.ptr, R, x.ptr, x_off, y.ptr, y_off, C.byref(d),
+                                                      C.byref(ms) if timed else None), "ne_exl3_lin_run_epi")
         return ms.value
 
     def run(self, x):

@@ -50,6 +50,28 @@ NE_API int ne_exl3_lin_info(const ne_exl3_lin *l, int *in, int *out, int *K);
  * x f32 [R][in] at x_off, y f32 [R][out] at y_off; R 1..32 (1..8 on the VALU GEMV, 9..32 on the matrix cores). */
 NE_API int ne_exl3_lin_run(ne_exl3_lin *l, int R, const ne_buf *x, uint64_t x_off, ne_buf *y, uint64_t y_off,
                            double *gpu_ms);
+/* A fused epilogue on a linear's finished outputs v (reference kernels/trunk6/trunk6.metal:129-197, t6_epi_col, the
+ * layer graph's q8 epilogues; rr = round to bf16 when refr, the reference rounding switch FC 0):
+ *   0 none     y = v
+ *   1 out_hc   y = b = rr(v); e2[r][s][c] = rr(e0[r][s][c] + rr(b e1[r][s])), s < hc (e0, e2 f32 [R][hc][out];
+ *              e1 f32 [R][8])
+ *   2 hc act   y = rr(silu(rr(v) / 4))
+ *   3 round    y = rr(v)
+ *   5 beta     y = rr(sigmoid(rr(v)))  (the reference's y[r][48 + c] of gb [R][96]: y_off = 192 bytes, ldy = 96)
+ *   6 decay    y = exp(-exp(A_log[c]) sp), sp = rr(softplus(rr(rr(v) + dt_bias[c]))) (e0 = A_log, e1 = dt_bias,
+ *              bf16 [out]; the reference's gb [R][96]: ldy = 96)
+ *   7 iqk      y = v; for c >= 512, e0[(T + r) 128 + c - 512] = v (e0 f32 key cache of rows of 128, e1 u32 [1] = T;
+ *              rows T + r beyond e0's size are not written)
+ * Kinds 4 (GDN conv1d with state) and 8 (the HC read fused through counters) are not provided. ldy = y's row stride
+ * in floats (0: out). */
+typedef struct ne_exl3_epi {
+  int kind, refr, hc, ldy;
+  const ne_buf *e0, *e1, *e2;
+} ne_exl3_epi;
+/* ne_exl3_lin_run with a fused epilogue (reference kernels/trunk6/trunk6.mm:232-249 with T6_EPI / T6_LDY set,
+ * trunk6.metal:199-222 t6_finish) */
+NE_API int ne_exl3_lin_run_epi(ne_exl3_lin *l, int R, const ne_buf *x, uint64_t x_off, ne_buf *y, uint64_t y_off,
+                               const ne_exl3_epi *epi, double *gpu_ms);
 /* n linears at R rows, all reading x (f32 [R][in_i]) and writing scratch outputs, captured once in a HIP graph and
  * replayed reps times after warmup replays: us_per_lin = GPU time per linear (HIP events). Replaces the reference's
  * differential timing of the trunk stages (kernels/trunk6/trunk6.mm:232-249 replays, core/bench.h:21-24). */

@@ -294,6 +294,54 @@ void orc_exl3_linear_exact(const float *x, int R, const uint16_t *trellis, const
   free(xs);
 }
 
+/* The fused epilogues of a finished linear output v [R][out] (kernels/trunk6/trunk6.metal:129-197, t6_epi_col;
+ * rr = bf16 rounding when refr, kernels/ne_common.h:27-29 for rr, silu and sigm). y rows are ldy floats apart.
+ * kind 1: e0, e2 f32 [R][hc][out], e1 f32 [R][8]; 6: e0 = A_log, e1 = dt_bias (bf16 [out]); 7: e0 f32 key cache
+ * of rows of 128 (cap rows), e1 u32 [1] = first row T. Returns -1 for kinds it does not cover (4, 8). */
+static float rr_(float x, int refr) { return refr ? orc_bf16r(x) : x; }
+int orc_lin_epi(const float *v, int R, int out, int kind, int refr, int hc, int ldy, float *y, void *e0, void *e1,
+                float *e2, long cap) {
+  for (int r = 0; r < R; r++)
+    for (int c = 0; c < out; c++) {
+      const float x = v[(size_t)r * out + c];
+      float *yo = y + (size_t)r * ldy + c;
+      switch (kind) {
+        case 0: *yo = x; break;
+        case 1: { /* trunk6.metal:152-158 */
+          const float br = rr_(x, refr);
+          *yo = br;
+          for (int s = 0; s < hc; s++) {
+            const size_t o = ((size_t)r * hc + s) * out + c;
+            e2[o] = rr_(((float *)e0)[o] + rr_(br * ((float *)e1)[r * 8 + s], refr), refr);
+          }
+          break;
+        }
+        case 2: { /* trunk6.metal:159-160 */
+          const float t = rr_(x, refr) * 0.25f;
+          *yo = rr_(t / (1.0f + expf(-t)), refr);
+          break;
+        }
+        case 3: *yo = rr_(x, refr); break; /* trunk6.metal:161-162 */
+        case 5: *yo = rr_(1.0f / (1.0f + expf(-rr_(x, refr))), refr); break; /* trunk6.metal:180-181 */
+        case 6: { /* trunk6.metal:182-188 */
+          const float ex = expf(orc_bf16_to_f32(((uint16_t *)e0)[c])), dt = orc_bf16_to_f32(((uint16_t *)e1)[c]);
+          const float u = rr_(rr_(x, refr) + dt, refr);
+          const float sp = rr_(u > 20.0f ? u : logf(1.0f + expf(u)), refr);
+          *yo = expf(-ex * sp);
+          break;
+        }
+        case 7: { /* trunk6.metal:189-196 */
+          *yo = x;
+          const long t = (long)((uint32_t *)e1)[0] + r;
+          if (c >= 512 && t < cap) ((float *)e0)[(size_t)t * 128 + (c - 512)] = x;
+          break;
+        }
+        default: return -1;
+      }
+    }
+  return 0;
+}
+
 /* ------------------------------------------------------------------------------------------------ router */
 /* kernels/fn_moe.metal:50-66: logits = x . router row (bf16 weights), rr() to bf16 (reference rounding on) */
 void orc_router_logits(const float *x, const uint16_t *rw, int ne, int hid, int round_bf16, float *logits) {

@@ -14,6 +14,8 @@
  *   orc_slot_rc / orc_decode: bijection + the reference row/column formula; decode vs per-tile codeword lookups.
  *   orc_fwht_*:           the textbook Sylvester matrix (parity of popcount(i & j)), blocks of 16..128.
  *   orc_exl3_linear*:     explicit-matrix numpy restatement diag(suh) H W' H diag(svh).
+ *   orc_lin_epi:          numpy closed forms per kind (silu, sigmoid, softplus, exp decay) with bf16 rounding points
+ *                         placed independently, and the rounding switch off vs plain float math.
  *   orc_router_logits / orc_route: numpy dot + bf16 rounding; ties to the lower index vs numpy stable argsort.
  *   orc_moe_*:            explicit numpy restatement of SwiGLU experts and the slot-order combine.
  * Parity versus upstream exllamav3's codec itself stays unpinned (the module is absent); the restatement follows
@@ -58,6 +60,9 @@ void orc_fwht_f64(double *v, int n, int had);
  * (tests/trunk6/check_kernels.py:96-98, kernels/trunk6/trunk6.metal:68-85,199-214) */
 void orc_exl3_linear(const float *x, int R, const uint16_t *trellis, const uint16_t *suh, const uint16_t *svh,
                      int in, int out, int K, float *y);
+/* fused epilogues of a finished linear output (kernels/trunk6/trunk6.metal:129-197): kinds 0, 1, 2, 3, 5, 6, 7 */
+int orc_lin_epi(const float *v, int R, int out, int kind, int refr, int hc, int ldy, float *y, void *e0, void *e1,
+                float *e2, long cap);
 /* exact: everything in f64, no fp16 rounding of the input (tools/convert_trunk_enc.py:125-128) */
 void orc_exl3_linear_exact(const float *x, int R, const uint16_t *trellis, const uint16_t *suh, const uint16_t *svh,
                            int in, int out, int K, double *y);

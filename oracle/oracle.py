@@ -60,6 +60,9 @@ def lib():
         L.orc_exl3_linear.argtypes = [_f32p, C.c_int, _u16p, _u16p, _u16p, C.c_int, C.c_int, C.c_int, _f32p]
         L.orc_exl3_linear_exact.restype = None
         L.orc_exl3_linear_exact.argtypes = [_f32p, C.c_int, _u16p, _u16p, _u16p, C.c_int, C.c_int, C.c_int, _f64p]
+        L.orc_lin_epi.restype = C.c_int
+        L.orc_lin_epi.argtypes = [_f32p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _f32p, C.c_void_p,
+                                  C.c_void_p, C.c_void_p, C.c_long]
         L.orc_router_logits.restype = None
         L.orc_router_logits.argtypes = [_f32p, _u16p, C.c_int, C.c_int, C.c_int, _f32p]
         L.orc_route.restype, L.orc_route.argtypes = None, [_f32p, C.c_int, C.c_int, _u32p, _f32p]
@@ -134,6 +137,23 @@ def exl3_linear(x, trellis, suh, svh, exact=False):
     y = np.zeros((R, ot * 16), np.float64 if exact else np.float32)
     f = lib().orc_exl3_linear_exact if exact else lib().orc_exl3_linear
     f(x, R, t, _c(suh, np.float16).view(np.uint16), _c(svh, np.float16).view(np.uint16), it * 16, ot * 16, n // 16, y)
+    return y
+
+
+def lin_epi(v, kind, refr=True, hc=4, ldy=None, y=None, e0=None, e1=None, e2=None):
+    """the fused epilogue of a finished linear output v f32 [R, out] (kernels/trunk6/trunk6.metal:129-197).
+    Returns y [R, ldy] (columns beyond out keep y's values); e0..e2 numpy arrays are updated in place."""
+    v = _c(np.atleast_2d(v), np.float32)
+    R, out = v.shape
+    ldy = ldy or out
+    y = np.zeros((R, ldy), np.float32) if y is None else _c(y, np.float32).copy()
+    assert y.shape == (R, ldy)
+    ptr = lambda a: None if a is None else a.ctypes.data
+    for a in (e0, e1, e2):
+        assert a is None or a.flags.c_contiguous
+    cap = e0.nbytes // 512 if (kind == 7 and e0 is not None) else 0
+    rc = lib().orc_lin_epi(v, R, out, kind, int(bool(refr)), hc, ldy, y, ptr(e0), ptr(e1), ptr(e2), cap)
+    assert rc == 0, f"epilogue {kind} not covered"
     return y
 
 

@@ -132,3 +132,91 @@ def test_run_kernel_decode_by_name(eng, oracle):
     eng.run_kernel("exl3_decode", [tiles, np.int32(IT), np.int32(OT), w], grid=((IT * OT + 3) // 4, 1, 1),
                    tg=(256, 1, 1), fconsts=[(10, "u32", K)])
     assert np.array_equal(w.download(np.uint16, (inp, out)), oracle.decode(t).view(np.uint16))
+
+
+# ------------------------------------------------------------------------------------------------ fused epilogues
+def epi_case(eng, oracle, kind, inp, out, K, R, refr=True, ldy=0, yoff=0, seed=0):
+    """The linear with epilogue `kind` (reference kernels/trunk6/trunk6.metal:129-197) against the oracle's epilogue
+    applied to the same launch's plain output v (the GPU's v is deterministic): returns (got, want) pairs."""
+    rng = np.random.default_rng(9000 + 31 * kind + inp + out + K + R + seed)
+    t, su, sv = synth.linear(rng, inp, out, K)
+    x = synth.bf16_values(rng, R, inp)
+    lin = eng.exl3_linear(t, su, sv)
+    v = lin.run(x)
+    ld = ldy or out  # y rows of ld floats, the epilogue's columns at [yoff, yoff + out) (reference gb [R][96])
+    assert yoff + out <= ld
+    base = rng.standard_normal((R, ld)).astype(np.float32)  # columns outside the epilogue's must survive
+    yb = eng.from_numpy(base)
+    e0 = e1 = e2 = None
+    hc, T = 4, 0
+    if kind == 1:
+        e0 = rng.standard_normal((R, hc, out)).astype(np.float32)
+        e1 = rng.standard_normal((R, 8)).astype(np.float32)
+        e2 = np.zeros((R, hc, out), np.float32)
+    elif kind == 6:
+        e0 = synth.bf16(rng.standard_normal(out).astype(np.float32))
+        e1 = synth.bf16(rng.standard_normal(out).astype(np.float32))
+    elif kind == 7:
+        T = 3
+        e0 = np.full((T + R + 2, 128), -1.0, np.float32)
+        e1 = np.array([T], np.uint32)
+    bufs = [None if a is None else eng.from_numpy(a) for a in (e0, e1, e2)]
+    lin.run_epi(R, eng.from_numpy(x), yb, kind, y_off=4 * yoff, refr=refr, hc=hc, ldy=ldy, e0=bufs[0], e1=bufs[1],
+                e2=bufs[2])
+    got = yb.download(np.float32, (R, ld))
+    want_y = base.copy()
+    e0w = None if e0 is None else e0.copy()
+    e2w = None if e2 is None else e2.copy()
+    want_y[:, yoff:yoff + out] = oracle.lin_epi(v, kind, refr=refr, hc=hc, e0=e0w, e1=e1, e2=e2w)
+    pairs = [(got, want_y)]
+    if kind == 1:
+        pairs.append((bufs[2].download(np.float32, e2.shape), e2w))
+    if kind == 7:
+        pairs.append((bufs[0].download(np.float32, e0.shape), e0w))
+    ref_full = oracle.lin_epi(oracle.exl3_linear(x, t, su, sv), kind, refr=refr, hc=hc, e0=None if e0 is None else
+                              e0.copy(), e1=e1, e2=None if e2 is None else e2.copy())
+    return pairs, got[:, yoff:yoff + out], ref_full
+
+
+@pytest.mark.parametrize("kind,inp,out,K,R,refr,ldy,yoff", [
+    (0, 2048, 512, 5, 1, True, 0, 0), (3, 2048, 512, 5, 2, True, 0, 0), (3, 2048, 512, 5, 12, True, 0, 0),
+    (2, 2048, 1024, 6, 1, True, 0, 0), (2, 2048, 1024, 6, 16, True, 0, 0), (2, 2048, 1024, 6, 3, False, 0, 0),
+    (1, 2048, 512, 6, 1, True, 0, 0), (1, 2048, 512, 6, 4, True, 0, 0), (1, 2048, 512, 6, 16, True, 0, 0),
+    (1, 48, 96, 8, 12, True, 0, 0), (1, 2048, 512, 6, 2, False, 0, 0),
+    (5, 2048, 48, 6, 1, True, 96, 48), (5, 2048, 48, 6, 10, True, 96, 48),
+    (6, 2048, 48, 6, 1, True, 96, 0), (6, 2048, 48, 6, 10, True, 96, 0), (6, 2048, 48, 6, 2, False, 96, 0),
+    (7, 2048, 640, 6, 1, True, 0, 0), (7, 2048, 640, 6, 16, True, 0, 0), (7, 48, 640, 5, 12, True, 0, 0)])
+def test_linear_fused_epilogues(eng, oracle, kind, inp, out, K, R, refr, ldy, yoff):
+    print(f"linear epilogue {kind} {inp}x{out} K{K} R{R} refr {refr} ldy {ldy} y_off {yoff}", flush=True)
+    pairs, y, ref_full = epi_case(eng, oracle, kind, inp, out, K, R, refr, ldy, yoff)
+    transcendental = kind in (2, 5, 6)
+    for g, w in pairs:
+        if not transcendental and (refr or kind != 1):
+            assert np.array_equal(g, w)  # adds, products and bf16 rounding only
+            continue
+        d = np.abs(g.astype(np.float64) - w)
+        step = np.maximum(np.abs(g), np.abs(w)) * 2.0 ** -7 + 1e-30
+        if refr and kind == 6:
+            # unrounded exp output; an interior rounding (u, softplus) may flip one step at a boundary, rarely
+            assert (d <= 4e-6 * np.abs(w) + 1e-30).mean() > 0.98
+        elif refr:
+            # GPU expf / logf vs the host's can straddle a bf16 rounding boundary: at most one step, rarely
+            assert (d / step).max() <= 1.0 + 1e-6 and (d == 0).mean() > 0.98
+        else:
+            assert np.allclose(g, w, rtol=1e-5, atol=1e-7)
+    assert rel(y, ref_full) < 1e-2  # end to end against the oracle linear + epilogue
+
+
+def test_linear_epilogue_rejects(eng, oracle):
+    rng = np.random.default_rng(3)
+    t, su, sv = synth.linear(rng, 256, 48, 5)
+    lin = eng.exl3_linear(t, su, sv)
+    x = eng.from_numpy(synth.bf16_values(rng, 2, 256))
+    y = eng.alloc(2 * 96 * 4)
+    for kind, kw, msg in [(4, {}, "not supported"), (8, {}, "not supported"), (6, {}, "e0 (A_log) missing"),
+                          (1, {"hc": 4}, "e0 (h) missing"), (0, {"ldy": 40}, "ldy 40 below out"),
+                          (7, {}, "e0 (key cache) missing")]:
+        with pytest.raises(RuntimeError, match=msg.replace("(", r"\(").replace(")", r"\)")):
+            lin.run_epi(2, x, y, kind, **kw)
+    with pytest.raises(RuntimeError, match="y buffer too small"):
+        lin.run_epi(2, x, y, 5, y_off=4 * 49, ldy=96)

@@ -276,3 +276,105 @@ def test_moe_layer_vs_explicit(oracle, shared, sgate):
     fast, used = oracle.moe_experts(W, x, rt, sg=sg, fast_threads=2)
     assert used >= 1
     assert np.linalg.norm(fast - y) / np.linalg.norm(y) < 1e-5
+
+
+# ------------------------------------------------------------------------------------------------ linear epilogues
+def bfr(x):
+    """f64 -> f32 -> bf16 round to nearest even (independent of the oracle's own rounding)"""
+    u = np.asarray(x, np.float64).astype(np.float32).view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) >> 16 << 16
+    return u.astype(np.uint32).view(np.float32).astype(np.float64)
+
+
+def np_epi(v, kind, refr, hc=4, e0=None, e1=None, T=0):
+    """closed forms of kernels/trunk6/trunk6.metal:129-197 in f64 with the rounding points written out"""
+    q = bfr if refr else (lambda a: np.asarray(a, np.float64))
+    v = v.astype(np.float64)
+    R, out = v.shape
+    if kind == 1:
+        b = q(v)
+        h = e0.astype(np.float64).reshape(R, hc, out)
+        inj = e1.astype(np.float64).reshape(R, 8)[:, :hc]
+        return b, q(h + q(b[:, None, :] * inj[:, :, None]))
+    if kind == 2:
+        t = q(v) / 4
+        return q(t / (1 + np.exp(-t))), None
+    if kind == 3:
+        return q(v), None
+    if kind == 5:
+        return q(1 / (1 + np.exp(-q(v)))), None
+    if kind == 6:
+        A = (e0.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+        dt = (e1.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+        u = q(q(v) + dt)
+        sp = q(np.where(u > 20, u, np.log1p(np.exp(np.minimum(u, 20)))))
+        return np.exp(-np.exp(A) * sp), None
+    raise ValueError(kind)
+
+
+def bf_steps(a, b):
+    """distance in bf16 steps of the larger magnitude"""
+    step = np.maximum(np.abs(a), np.abs(b)) * 2.0 ** -7 + 1e-30
+    return np.abs(a - b) / step
+
+
+@pytest.mark.parametrize("kind", [1, 2, 3, 5, 6])
+@pytest.mark.parametrize("refr", [True, False])
+def test_lin_epi_closed_forms(oracle, kind, refr):
+    rng = np.random.default_rng(40 + kind)
+    R, out, hc = 5, 384, 4
+    v = (rng.standard_normal((R, out)) * 3).astype(np.float32)
+    e0 = e1 = e2 = None
+    if kind == 1:
+        e0 = rng.standard_normal((R, hc, out)).astype(np.float32)
+        e1 = rng.standard_normal((R, 8)).astype(np.float32)
+        e2 = np.zeros_like(e0)
+    if kind == 6:
+        e0 = synth.bf16(rng.standard_normal(out).astype(np.float32))
+        e1 = synth.bf16(rng.standard_normal(out).astype(np.float32))
+        v[0, :8] = [0, 30, -30, 19.9, 20.5, 1e-3, -5, 5]  # both softplus branches
+    y = oracle.lin_epi(v, kind, refr=refr, hc=hc, e0=e0, e1=e1, e2=e2)
+    want, want2 = np_epi(v, kind, refr, hc, e0, e1)
+    got = [(y, want)] + ([(e2, want2)] if kind == 1 else [])
+    for g, w in got:
+        g = g.astype(np.float64).reshape(w.shape)
+        if refr and kind != 6:
+            assert np.array_equal(bfr(g), g)  # the result is a bf16 value
+            assert bf_steps(g, w).max() <= 1.0
+            assert (g == w).mean() > 0.98  # f32 vs f64 transcendental boundaries only
+        elif refr:
+            assert np.allclose(g, w, rtol=2e-2, atol=1e-6)  # one interior rounding may flip a step
+            assert (np.abs(g - w) <= 1e-5 * np.abs(w) + 1e-7).mean() > 0.98
+        else:
+            assert np.allclose(g, w, rtol=2e-5, atol=1e-7)
+
+
+def test_lin_epi_known_answers(oracle):
+    v = np.zeros((1, 2), np.float32)
+    assert np.array_equal(oracle.lin_epi(v, 2), [[0, 0]])            # silu(0) = 0
+    assert np.array_equal(oracle.lin_epi(v, 5), [[0.5, 0.5]])        # sigmoid(0) = 1/2
+    e0 = synth.bf16(np.zeros(2, np.float32))                           # A_log 0: exp = 1; dt_bias 0
+    y = oracle.lin_epi(v, 6, e0=e0, e1=e0.copy())
+    sp = bfr(np.log(2.0))                                              # rr(softplus(0)) = rr(ln 2) = 0.69140625
+    assert sp == 0.69140625 and np.allclose(y, np.exp(-sp), rtol=1e-6)
+    y = oracle.lin_epi(np.array([[30.0, 1.0]], np.float32), 6, e0=e0, e1=e0.copy())
+    assert np.isclose(y[0, 0], np.exp(-30.0), rtol=1e-5)              # u > 20: softplus(u) = u
+    assert np.array_equal(oracle.lin_epi(np.array([[1.00390625, -2.5]], np.float32), 3), [[1.0, -2.5]])  # tie
+
+
+def test_lin_epi_stride_and_cache(oracle):
+    rng = np.random.default_rng(47)
+    R, out = 3, 640
+    v = rng.standard_normal((R, out)).astype(np.float32)
+    base = np.full((R, 700), 7.0, np.float32)
+    y = oracle.lin_epi(v, 0, ldy=700, y=base)
+    assert np.array_equal(y[:, :out], v) and np.all(y[:, out:] == 7.0)
+    cache = np.full((8, 128), -1.0, np.float32)
+    y = oracle.lin_epi(v, 7, e0=cache, e1=np.array([4], np.uint32))
+    assert np.array_equal(y, v)
+    assert np.all(cache[:4] == -1.0)                                   # rows before T untouched
+    assert np.array_equal(cache[4:7], v[:, 512:])                      # rows T..T+R-1 = the key columns
+    assert np.all(cache[7] == -1.0)
+    cache = np.full((5, 128), -1.0, np.float32)                        # capacity bound: row 5 and 6 dropped
+    oracle.lin_epi(v, 7, e0=cache, e1=np.array([4], np.uint32))
+    assert np.array_equal(cache[4], v[0, 512:]) and np.all(cache[:4] == -1.0)
