@@ -480,8 +480,16 @@ struct ne_moe {
     }
   }
   bool fused_ok(int R) const { return fused && plan_grid > 0 && R == 1; }
-  void launch(int R, const float *x, float *y, hipStream_t s) const {
-    const MoeArgs a = args(R, x, y);
+  // hc: the hyper-connection write's fields (MoeArgs::hc ...), or null for the plain layer
+  void launch(int R, const float *x, float *y, hipStream_t s, const MoeArgs *hc = nullptr) const {
+    MoeArgs a = args(R, x, y);
+    if (hc) {
+      a.hc = hc->hc;
+      a.refr = hc->refr;
+      a.hc_h = hc->hc_h;
+      a.hc_inj = hc->hc_inj;
+      a.hc_out = hc->hc_out;
+    }
     if (batch_ok(R) && R <= bat_R) {
       launch_moe_batch(a, bat, s);
       return;
@@ -721,6 +729,35 @@ NE_API int ne_moe_run(ne_moe *m, int R, const ne_buf *x, uint64_t x_off, ne_buf 
     const float *xp = (const float *)((const char *)x->dev + x_off);
     float *yp = (float *)((char *)y->dev + y_off);
     timed(stream(), gpu_ms, [&] { m->launch(R, xp, yp, stream()); });
+    m->last_R = R;
+    m->last_y = yp;
+    if (gpu_ms) m->check_sync(stream());
+  });
+}
+
+NE_API int ne_moe_run_hc(ne_moe *m, int R, const ne_buf *x, uint64_t x_off, ne_buf *y, uint64_t y_off,
+                         const ne_moe_hc *hc, double *gpu_ms) {
+  return c_call([&] {
+    IJ_CHECK(m && x && y && hc, "null argument");
+    IJ_CHECK(R >= 1 && R <= 4096, "rows %d (1..4096)", R);
+    IJ_CHECK(x_off % 16 == 0 && y_off % 4 == 0, "x offset must be 16-byte aligned, y offset 4-byte aligned");
+    IJ_CHECK(x_off + (uint64_t)R * m->hid * 4 <= x->size, "x buffer too small for [%d][%d] f32", R, m->hid);
+    IJ_CHECK(y_off + (uint64_t)R * m->hid * 4 <= y->size, "y buffer too small for [%d][%d] f32", R, m->hid);
+    IJ_CHECK(hc->hc >= 1 && hc->hc <= 8, "hc %d (1..8 streams)", hc->hc);
+    const uint64_t hb = (uint64_t)R * hc->hc * m->hid * 4;
+    IJ_CHECK(hc->h && hc->h->size >= hb, "h missing or under %llu bytes ([R][hc][hid] f32)", (unsigned long long)hb);
+    IJ_CHECK(hc->hout && hc->hout->size >= hb, "hout missing or under %llu bytes", (unsigned long long)hb);
+    IJ_CHECK(hc->inj && hc->inj->size >= (uint64_t)R * 32, "inj missing or under %d bytes ([R][8] f32)", R * 32);
+    m->ensure_scratch(R);
+    MoeArgs f;
+    f.hc = hc->hc;
+    f.refr = hc->refr ? 1 : 0;
+    f.hc_h = (const float *)hc->h->dev;
+    f.hc_inj = (const float *)hc->inj->dev;
+    f.hc_out = (float *)hc->hout->dev;
+    const float *xp = (const float *)((const char *)x->dev + x_off);
+    float *yp = (float *)((char *)y->dev + y_off);
+    timed(stream(), gpu_ms, [&] { m->launch(R, xp, yp, stream(), &f); });
     m->last_R = R;
     m->last_y = yp;
     if (gpu_ms) m->check_sync(stream());

@@ -8,6 +8,7 @@
 
 #include "exl3_device.h"
 #include "kernels.h"
+#include "moe_device.h"
 
 namespace ijah {
 
@@ -293,7 +294,7 @@ __device__ void route_rows(const MoeArgs &a, float *lv, uint32_t *cand, uint32_t
         st_cg(rt + k, sid[k]);
         st_cg(rt + a.topk + k, __float_as_uint(pr[k] / s));
       }
-      st_cg(a.sgv + r, a.has_sgate ? 1.f / (1.f + expf(-ld_cg(a.logits + (uint64_t)r * ld + a.ne))) : 1.f);
+      st_cg(a.sgv + r, moe_shared_gate(a, a.has_sgate ? ld_cg(a.logits + (uint64_t)r * ld + a.ne) : 0.f));
     }
     __syncthreads();
   }
@@ -430,9 +431,10 @@ __device__ void combine_block(const MoeArgs &a, int r, int c, float (*vs)[128]) 
   __syncthreads();
   if (threadIdx.x < 128) {
     const int i = c * 128 + threadIdx.x;
-    float y = 0.f;
-    for (int k = 0; k < a.nslot; k++) y += vs[k][threadIdx.x];
-    if (i < a.hid) a.y[(uint64_t)r * a.hid + i] = y;
+    float s = 0.f;
+    for (int k = 0; k < a.topk; k++) s += vs[k][threadIdx.x];
+    const float t = a.nslot > a.topk ? vs[a.topk][threadIdx.x] : 0.f;
+    if (i < a.hid) a.y[(uint64_t)r * a.hid + i] = moe_finish(a, r, i, s, t);
   }
   __syncthreads();
 }

@@ -53,6 +53,13 @@ struct MoeArgs {
   const uint32_t *units;               // fused kernel: the plan words (MoePlan::words) in device memory
   float *part;                         // fused kernel: column partial sums (MoePlan::part_floats)
   uint32_t *fsync;                     // fused kernel: its counters (moe_fused_sync_words), zero when created
+  // The hyper-connection write fused into the combine (reference kernels/fn_moe.metal:7-10, 420-448), on when hc > 0
+  // (rr = bf16 rounding when refr): the shared gate is rr(sigmoid), y = branch = rr(rr(routed sum) + rr(gated shared)),
+  // hc_out[r][s][c] = rr(hc_h[r][s][c] + rr(branch hc_inj[r][s])) for s < hc; hc_h, hc_out f32 [R][hc][hid], hc_inj
+  // f32 [R][8].
+  int hc = 0, refr = 1;
+  const float *hc_h = nullptr, *hc_inj = nullptr;
+  float *hc_out = nullptr;
 };
 void launch_moe_router(const MoeArgs &a, hipStream_t s);
 void launch_moe_gateup(const MoeArgs &a, hipStream_t s);

@@ -30,6 +30,7 @@
 
 #include "exl3_device.h"
 #include "kernels.h"
+#include "moe_device.h"
 
 namespace ijah {
 
@@ -299,7 +300,7 @@ __device__ void route_one(const MoeArgs &a, int r) {
     a.route[(uint64_t)r * 2 * a.topk + lane] = id;
     a.route[(uint64_t)r * 2 * a.topk + a.topk + lane] = __float_as_uint(pk / sum);
   }
-  if (lane == 0) a.sgv[r] = a.has_sgate ? 1.f / (1.f + expf(-sgl)) : 1.f;
+  if (lane == 0) a.sgv[r] = moe_shared_gate(a, sgl);
 }
 __global__ __launch_bounds__(256) void bat_route(MoeArgs a) {
   const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -1109,7 +1110,7 @@ __global__ __launch_bounds__(512, NR == kChunkRows ? 4 : 6) void bat_down(MoeArg
 __global__ __launch_bounds__(256) void bat_combine(MoeArgs a, const float *__restrict__ dnw) {
   const int r = blockIdx.x, i = (blockIdx.y * 256 + threadIdx.x) * 4;
   if (i >= a.hid) return;
-  float4 y = {0.f, 0.f, 0.f, 0.f};
+  float4 y = {0.f, 0.f, 0.f, 0.f}, sh = {0.f, 0.f, 0.f, 0.f};  // routed sum in slot order; the shared slot
   const float *p = dnw + (uint64_t)r * a.nslot * a.hid + i;
   constexpr int B = 6;  // slots requested together; summed in slot order
   for (int k0 = 0; k0 < a.nslot; k0 += B) {
@@ -1119,14 +1120,18 @@ __global__ __launch_bounds__(256) void bat_combine(MoeArgs a, const float *__res
       if (k0 + j < a.nslot) v[j] = __builtin_nontemporal_load((const f32x4 *)(p + (uint64_t)(k0 + j) * a.hid));
 #pragma unroll
     for (int j = 0; j < B; j++)
-      if (k0 + j < a.nslot) {
+      if (k0 + j < a.topk) {
         y.x += v[j][0];
         y.y += v[j][1];
         y.z += v[j][2];
         y.w += v[j][3];
+      } else if (k0 + j < a.nslot) {
+        sh = make_float4(v[j][0], v[j][1], v[j][2], v[j][3]);
       }
   }
-  *(float4 *)(a.y + (uint64_t)r * a.hid + i) = y;
+  *(float4 *)(a.y + (uint64_t)r * a.hid + i) =
+      make_float4(moe_finish(a, r, i, y.x, sh.x), moe_finish(a, r, i + 1, y.y, sh.y), moe_finish(a, r, i + 2, y.z, sh.z),
+                  moe_finish(a, r, i + 3, y.w, sh.w));
 }
 
 // ---------------------------------------------------------------------------------------------------- trunk

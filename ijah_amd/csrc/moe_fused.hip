@@ -25,6 +25,7 @@
 
 #include "exl3_device.h"
 #include "kernels.h"
+#include "moe_device.h"
 
 namespace ijah {
 
@@ -243,7 +244,7 @@ __device__ bool route_wave(const MoeArgs &a, Route *rt, uint32_t tag) {
   float sum = 0.f;
   for (int k = 0; k < a.topk; k++) sum += __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(pk), k));
   const float wk = pk / sum;
-  const float sg = a.has_sgate ? 1.f / (1.f + expf(-sgl)) : 1.f;
+  const float sg = moe_shared_gate(a, sgl);
   if (lane < a.topk) {
     rt->id[lane] = id;
     rt->w[lane] = wk;
@@ -636,7 +637,7 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
     if (old - s_ep * (uint32_t)a.nslot == (uint32_t)a.nslot - 1u) {  // every slot of the block is stored: y = the sum
                                                                      // over the slots in slot order
       constexpr int U = 12;  // slots loaded in one batch
-      float yv[2] = {0.f, 0.f};
+      float yv[2] = {0.f, 0.f}, sh[2] = {0.f, 0.f};  // routed sum in slot order; the shared slot
       for (int j0 = 0; j0 < a.nslot; j0 += U) {
         float t[U][2];
 #pragma unroll
@@ -647,13 +648,16 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
           }
 #pragma unroll
         for (int u = 0; u < U; u++)
-          if (j0 + u < a.nslot) {
+          if (j0 + u < a.topk) {
             yv[0] += t[u][0];
             yv[1] += t[u][1];
+          } else if (j0 + u < a.nslot) {
+            sh[0] = t[u][0];
+            sh[1] = t[u][1];
           }
       }
-      a.y[i0] = yv[0];
-      a.y[i1] = yv[1];
+      a.y[i0] = moe_finish(a, 0, i0, yv[0], sh[0]);
+      a.y[i1] = moe_finish(a, 0, i1, yv[1], sh[1]);
       if (a.trace && lane == 0) a.trace[(uint64_t)(6001 + blockIdx.x) * 8 + 4] = wall_clock64();
     }
   }

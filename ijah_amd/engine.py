@@ -90,6 +90,7 @@ SIGNATURES = {
     "ne_moe_synth": (_vp, [_i, _i, _i, _i, _i, _i, _i, _u64]),
     "ne_moe_free": (None, [_vp]),
     "ne_moe_run": (_i, [_vp, _i, _vp, _u64, _vp, _u64, _dp]),
+    "ne_moe_run_hc": (_i, [_vp, _i, _vp, _u64, _vp, _u64, _vp, _dp]),
     "ne_moe_read": (_i, [_vp, C.c_char_p, _vp, _u64]),
     "ne_moe_decode": (_i, [_vp, _i, _i, _vp, _dp]),
     "ne_moe_info": (_i, [_vp] + [C.POINTER(_i)] * 6),
@@ -112,6 +113,11 @@ class Exl3Epi(C.Structure):
     y row stride in floats, extra buffers)"""
     _fields_ = [("kind", C.c_int), ("refr", C.c_int), ("hc", C.c_int), ("ldy", C.c_int),
                 ("e0", C.c_void_p), ("e1", C.c_void_p), ("e2", C.c_void_p)]
+
+
+class MoeHc(C.Structure):
+    """include/ijah_exl3.h ne_moe_hc: the hyper-connection write fused into the MoE combine"""
+    _fields_ = [("hc", C.c_int), ("refr", C.c_int), ("h", C.c_void_p), ("inj", C.c_void_p), ("hout", C.c_void_p)]
 
 
 def bf16_to_f32(u16):
@@ -316,13 +322,12 @@ class MoeLayer:
                                              C.byref(ms) if timed else None), "ne_moe_run")
         return ms.value
 
-    def run_epi(self, R, x, y, kind, x_off=0, y_off=0, refr=True, hc=4, ldy=0, e0=None, e1=None, e2=None,
-                timed=False):
-        """ne_exl3_lin_run_epi; e0..e2 are device buffers (or None)"""
-        d = Exl3Epi(kind, int(bool(refr)), hc, ldy, *(None if b is None else b.ptr for b in (e0, e1, e2)))
+    def run_hc(self, R, x, y, h, inj, hout, hc=4, refr=True, x_off=0, y_off=0, timed=False):
+        """ne_moe_run_hc: y = the branch, hout = h + branch * inj per stream (device buffers)"""
+        d = MoeHc(hc, int(bool(refr)), h.ptr, inj.ptr, hout.ptr)
         ms = C.c_double(0)
-        self.eng._ok(self.eng.lib.ne_exl3_lin_run_epi(self.ptr, R, x.ptr, x_off, y.ptr, y_off, C.byref(d),
-                                                      C.byref(ms) if timed else None), "ne_exl3_lin_run_epi")
+        self.eng._ok(self.eng.lib.ne_moe_run_hc(self.ptr, R, x.ptr, x_off, y.ptr, y_off, C.byref(d),
+                                                C.byref(ms) if timed else None), "ne_moe_run_hc")
         return ms.value
 
     def run(self, x):

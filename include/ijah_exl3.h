@@ -107,6 +107,18 @@ NE_API void ne_moe_free(ne_moe *m);
  * x f32 [R][hid] -> y f32 [R][hid] = sum over the top-k slots in slot order of w_k expert_k(x) + g * shared(x). */
 NE_API int ne_moe_run(ne_moe *m, int R, const ne_buf *x, uint64_t x_off, ne_buf *y, uint64_t y_off,
                       double *gpu_ms);
+/* The hyper-connection write fused into the layer's combine (reference kernels/fn_moe.metal:7-10 and :420-448, the
+ * finisher of fn_moe_down; rr = bf16 rounding when refr, the reference rounding switch FC 0): the shared gate is
+ * rr(sigmoid(logit)), y = branch = rr(rr(sum of the routed slots in slot order) + rr(gate * shared expert)), and
+ * hout[r][s][c] = rr(h[r][s][c] + rr(branch * inj[r][s])) for s < hc. h, hout f32 [R][hc][hid] (hout may be h: each
+ * element is read and written by one thread); inj f32 [R][8]. */
+typedef struct ne_moe_hc {
+  int hc, refr;
+  const ne_buf *h, *inj;
+  ne_buf *hout;
+} ne_moe_hc;
+NE_API int ne_moe_run_hc(ne_moe *m, int R, const ne_buf *x, uint64_t x_off, ne_buf *y, uint64_t y_off,
+                         const ne_moe_hc *hc, double *gpu_ms);
 /* reference models/flash_next/layer.h:258-262 (ne_fn_layer_read) for the MoE intermediates of the last run:
  * "logits" f32 [R][ne], "route" u32 [R][2 topk] (ids, f32 weight bits), "shared_gate" f32 [R],
  * "experts_gu" f32 [R][slots][2][inter] (gate / up inner outputs before H_out), "experts_dn" f32 [R][slots][hid]

@@ -563,6 +563,63 @@ int orc_moe_layer(const orc_moe *m, const float *x, int R, float *y, float *logi
   return 0;
 }
 
+/* The layer with the hyper-connection write (kernels/fn_moe.metal:7-10 finisher, :420-448): the routed sum s (slot
+ * order) and the gated shared term t kept apart; sg = rr(sigmoid(shared logit)) (:421, :444 rr(sgt)); y = branch =
+ * rr(rr(s) + rr(t)); hout[r][st][c] = rr(h[r][st][c] + rr(branch * inj[r][st])), inj [R][8]. rr = bf16 when refr. */
+void orc_hc_write(const float *s, const float *t, int R, int hid, int hc, int refr, const float *h, const float *inj,
+                  float *y, float *hout) {
+  for (int r = 0; r < R; r++)
+    for (int c = 0; c < hid; c++) {
+      const size_t i = (size_t)r * hid + c;
+      const float br = rr_(rr_(s[i], refr) + rr_(t ? t[i] : 0.0f, refr), refr);
+      y[i] = br;
+      for (int st = 0; st < hc; st++) {
+        const size_t o = ((size_t)r * hc + st) * hid + c;
+        hout[o] = rr_(h[o] + rr_(br * inj[r * 8 + st], refr), refr);
+      }
+    }
+}
+
+int orc_moe_layer_hc(const orc_moe *m, const float *x, int R, int hc, int refr, const float *h, const float *inj,
+                     float *y, float *hout) {
+  const int ne = m->ne, topk = m->topk, hid = m->hid;
+  float *lg = (float *)malloc(sizeof(float) * (size_t)(ne + 1));
+  uint32_t *rt = (uint32_t *)malloc(sizeof(uint32_t) * (size_t)2 * topk);
+  float *s = (float *)calloc((size_t)hid, sizeof(float)), *t = (float *)calloc((size_t)hid, sizeof(float));
+  float *v = (float *)malloc(sizeof(float) * (size_t)hid);
+  for (int r = 0; r < R; r++) {
+    const float *xr = x + (size_t)r * hid;
+    orc_router_logits(xr, m->router, ne, hid, 1, lg);
+    float w[64];
+    orc_route(lg, ne, topk, rt, w);
+    float sg = 1.0f;
+    if (m->sgate) {
+      float l;
+      orc_router_logits(xr, m->sgate, 1, hid, 1, &l);
+      sg = sigmoidf_(l);
+    }
+    sg = rr_(sg, refr);
+    for (int j = 0; j < hid; j++) s[j] = t[j] = 0.0f;
+    for (int k = 0; k < topk; k++) {
+      lin_view L[3] = {routed(m, 0, (int)rt[k]), routed(m, 1, (int)rt[k]), routed(m, 2, (int)rt[k])};
+      expert_emul(L, xr, w[k], v);
+      for (int j = 0; j < hid; j++) s[j] += v[j];
+    }
+    if (m->sgt) {
+      lin_view L[3] = {shared(m, 0), shared(m, 1), shared(m, 2)};
+      expert_emul(L, xr, sg, t);
+    }
+    orc_hc_write(s, t, 1, hid, hc, refr, h + (size_t)r * hc * hid, inj + (size_t)r * 8, y + (size_t)r * hid,
+                 hout + (size_t)r * hc * hid);
+  }
+  free(lg);
+  free(rt);
+  free(s);
+  free(t);
+  free(v);
+  return 0;
+}
+
 /* ------------------------------------------------------------------------------------------------ CPU baseline */
 static float g_mcg_tab[1 << 15];
 static int g_mcg_ready = 0;

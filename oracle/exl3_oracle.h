@@ -18,6 +18,8 @@
  *                         placed independently, and the rounding switch off vs plain float math.
  *   orc_router_logits / orc_route: numpy dot + bf16 rounding; ties to the lower index vs numpy stable argsort.
  *   orc_moe_*:            explicit numpy restatement of SwiGLU experts and the slot-order combine.
+ *   orc_hc_write / orc_moe_layer_hc: numpy closed form of the finisher; with rounding off the branch equals the plain
+ *                         layer's slot-order sum bit for bit; the shared term is the plain layer minus its routed part.
  * Parity versus upstream exllamav3's codec itself stays unpinned (the module is absent); the restatement follows
  * the reference's Metal kernels, which the reference checks against that codec (docs/trunk6.md:74-84).
  */
@@ -87,6 +89,12 @@ typedef struct {
 /* kernel arithmetic; y [R][hid] f32; logits [R][ne] (may be NULL); route [R][2 topk] u32 (ids, f32 weight bits,
  * may be NULL). Returns 0. */
 int orc_moe_layer(const orc_moe *m, const float *x, int R, float *y, float *logits, uint32_t *route);
+/* the hyper-connection write (kernels/fn_moe.metal:437-448) from the routed sum s and gated shared term t (t may be
+ * null), and the layer with it (shared gate rounded to bf16 when refr) */
+void orc_hc_write(const float *s, const float *t, int R, int hid, int hc, int refr, const float *h, const float *inj,
+                  float *y, float *hout);
+int orc_moe_layer_hc(const orc_moe *m, const float *x, int R, int hc, int refr, const float *h, const float *inj,
+                     float *y, float *hout);
 /* Same layer given a route (ids + f32 weights [R][2 topk]) and shared gate value per row (sg may be NULL -> 1):
  * separates the routing decision from the expert math in tests. */
 int orc_moe_experts(const orc_moe *m, const float *x, int R, const uint32_t *route, const float *sg, float *y);

@@ -63,6 +63,10 @@ def lib():
         L.orc_lin_epi.restype = C.c_int
         L.orc_lin_epi.argtypes = [_f32p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _f32p, C.c_void_p,
                                   C.c_void_p, C.c_void_p, C.c_long]
+        L.orc_hc_write.restype = None
+        L.orc_hc_write.argtypes = [_f32p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, _f32p, _f32p, _f32p, _f32p]
+        L.orc_moe_layer_hc.restype = C.c_int
+        L.orc_moe_layer_hc.argtypes = [C.POINTER(_Moe), _f32p, C.c_int, C.c_int, C.c_int, _f32p, _f32p, _f32p, _f32p]
         L.orc_router_logits.restype = None
         L.orc_router_logits.argtypes = [_f32p, _u16p, C.c_int, C.c_int, C.c_int, _f32p]
         L.orc_route.restype, L.orc_route.argtypes = None, [_f32p, C.c_int, C.c_int, _u32p, _f32p]
@@ -208,6 +212,30 @@ def moe_layer(W, x):
     rt = np.zeros((R, 2 * m.topk), np.uint32)
     lib().orc_moe_layer(C.byref(m), x, R, y, lg, rt)
     return y, lg, rt
+
+
+def hc_write(s, t, h, inj, refr=True):
+    """the MoE finisher's hyper-connection write (kernels/fn_moe.metal:437-448): s, t [R, hid] (t may be None),
+    h [R, hc, hid], inj [R, 8] -> (branch y [R, hid], hout [R, hc, hid])"""
+    s = _c(np.atleast_2d(s), np.float32)
+    R, hid = s.shape
+    h = _c(h, np.float32)
+    hc = h.shape[1]
+    t = None if t is None else _c(t, np.float32).reshape(R, hid)
+    y, hout = np.zeros((R, hid), np.float32), np.zeros_like(h)
+    lib().orc_hc_write(s, None if t is None else t.ctypes.data, R, hid, hc, int(bool(refr)), h,
+                       _c(inj, np.float32), y, hout)
+    return y, hout
+
+
+def moe_layer_hc(W, x, h, inj, refr=True):
+    """the layer with the hyper-connection write: (branch y [R, hid], hout [R, hc, hid])"""
+    x = _c(np.atleast_2d(x), np.float32)
+    R = x.shape[0]
+    h = _c(h, np.float32)
+    y, hout = np.zeros((R, W.m.hid), np.float32), np.zeros_like(h)
+    lib().orc_moe_layer_hc(C.byref(W.m), x, R, h.shape[1], int(bool(refr)), h, _c(inj, np.float32), y, hout)
+    return y, hout
 
 
 def moe_experts(W, x, route_u32, sg=None, exact=False, fast_threads=None):

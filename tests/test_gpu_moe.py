@@ -221,3 +221,58 @@ def test_moe_prefill_config5_rows_match_single_row(eng):
         assert rel(y1[0], y[i]) < 1e-4, i
         same += 1
     assert same >= 3
+
+
+# ------------------------------------------------------------------------------------------------ HC write
+@pytest.mark.parametrize("R,path,dims", [
+    (1, "fused", (2048, 512, 64, 10)), (1, "staged", (2048, 512, 64, 10)), (3, "staged", (1024, 256, 16, 4)),
+    (3, "batched", (1024, 256, 16, 4)), (16, "batched", (1024, 256, 16, 4)), (40, "batched", (1024, 256, 16, 4))])
+def test_moe_hc_write(eng, oracle, R, path, dims, monkeypatch):
+    """ne_moe_run_hc, the hyper-connection write fused into the combine (reference kernels/fn_moe.metal:437-448), on
+    the fused single-row kernel, the staged kernels and the batched GEMM forms (16 rows: the one-row-block form, 40
+    rows x 4 slots over 16 experts: the transposed form). Rounding off: the branch is the plain run's output bit for
+    bit and hout = h + branch * inj exactly. Rounding on: against the oracle layer with the write, within bf16 flips
+    where the GPU's and the oracle's f32 sums straddle a rounding boundary."""
+    hid, inter, ne, topk = dims
+    print(f"moe hc write R{R} {path} hid {hid} ne {ne}", flush=True)
+    if path == "staged":
+        monkeypatch.setenv("IJAH_MOE_PATH", "staged")
+    w = synth.moe_layer(70 + R, hid=hid, inter=inter, ne=ne, topk=topk, K=5, shared=True, Ks=6, sgate=True)
+    W = oracle.MoeWeights(w)
+    moe = eng.moe_create(w)
+    rng = np.random.default_rng(80 + R)
+    x = synth.bf16_values(rng, R, hid)
+    hc = 4
+    h = rng.standard_normal((R, hc, hid)).astype(np.float32)
+    inj = rng.standard_normal((R, 8)).astype(np.float32)
+    xb, hb, ib = eng.from_numpy(x), eng.from_numpy(h), eng.from_numpy(inj)
+    y_plain = moe.run(x)
+    yb, ob = eng.alloc(R * hid * 4), eng.alloc(h.nbytes)
+    moe.run_hc(R, xb, yb, hb, ib, ob, hc=hc, refr=False)
+    y0, o0 = yb.download(np.float32, (R, hid)), ob.download(np.float32, h.shape)
+    assert np.array_equal(y0, y_plain)
+    assert np.array_equal(o0, h + y0[:, None, :] * inj[:, :hc, None])
+    moe.run_hc(R, xb, yb, hb, ib, ob, hc=hc, refr=True)
+    y1, o1 = yb.download(np.float32, (R, hid)), ob.download(np.float32, h.shape)
+    want_y, want_o = oracle.moe_layer_hc(W, x, h, inj, refr=True)
+    for g, wv in ((y1, want_y), (o1, want_o)):
+        assert np.array_equal((g.view(np.uint32) & 0xFFFF), np.zeros(g.shape, np.uint32))  # bf16 values
+        assert (g == wv).mean() > 0.97
+        assert rel(g, wv) < 3e-3
+    assert np.array_equal(moe.read("mlp_out", R), y1)
+    moe.run_hc(R, xb, yb, hb, ib, hb, hc=hc, refr=True)  # in place (hout = h)
+    assert np.array_equal(hb.download(np.float32, h.shape), o1)
+    assert np.array_equal(moe.run(x), y_plain)  # the plain run after the write is unchanged
+
+
+def test_moe_hc_rejects(eng, oracle):
+    w = synth.moe_layer(5, hid=1024, inter=256, ne=16, topk=4, K=5, shared=True, Ks=6, sgate=True)
+    moe = eng.moe_create(w)
+    x = eng.from_numpy(np.zeros((2, 1024), np.float32))
+    y, h, inj = eng.alloc(2 * 1024 * 4), eng.alloc(2 * 4 * 1024 * 4), eng.alloc(2 * 8 * 4)
+    with pytest.raises(RuntimeError, match="hc 0"):
+        moe.run_hc(2, x, y, h, inj, h, hc=0)
+    with pytest.raises(RuntimeError, match="h missing or under"):
+        moe.run_hc(2, x, y, h, inj, h, hc=5)
+    with pytest.raises(RuntimeError, match="inj missing or under"):
+        moe.run_hc(2, x, y, h, eng.alloc(16), h, hc=4)

@@ -378,3 +378,46 @@ def test_lin_epi_stride_and_cache(oracle):
     cache = np.full((5, 128), -1.0, np.float32)                        # capacity bound: row 5 and 6 dropped
     oracle.lin_epi(v, 7, e0=cache, e1=np.array([4], np.uint32))
     assert np.array_equal(cache[4], v[0, 512:]) and np.all(cache[:4] == -1.0)
+
+
+# ------------------------------------------------------------------------------------------------ MoE HC write
+def bf32(x):
+    """f32 -> bf16 round to nearest even, in f32"""
+    u = np.asarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    return (((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16).astype(np.uint32).view(np.float32)
+
+
+@pytest.mark.parametrize("refr", [True, False])
+def test_hc_write_closed_form(oracle, refr):
+    rng = np.random.default_rng(60)
+    R, hid, hc = 3, 256, 4
+    s, t = (rng.standard_normal((R, hid)).astype(np.float32) for _ in range(2))
+    h = rng.standard_normal((R, hc, hid)).astype(np.float32)
+    inj = rng.standard_normal((R, 8)).astype(np.float32)
+    q = bf32 if refr else (lambda a: np.asarray(a, np.float32))
+    br = q(q(s) + q(t))                                                     # f32 adds and products, as in C
+    want_h = q(h + q(br[:, None, :] * inj[:, :hc, None]))
+    y, hout = oracle.hc_write(s, t, h, inj, refr=refr)
+    assert np.array_equal(y, br) and np.array_equal(hout, want_h)
+    y0, _ = oracle.hc_write(s, None, h, inj, refr=refr)                     # no shared expert: t = 0
+    assert np.array_equal(y0, q(q(s)))
+
+
+def test_moe_layer_hc_matches_plain_layer(oracle):
+    """rounding off: the branch is the plain layer's slot-order sum bit for bit (the shared gate unrounded);
+    rounding on: the branch is bf16-valued and within a few bf16 steps of the plain layer"""
+    w = synth.moe_layer(13, hid=256, inter=128, ne=16, topk=4, K=5, shared=True, Ks=6, sgate=True)
+    W = oracle.MoeWeights(w)
+    rng = np.random.default_rng(14)
+    R, hc = 2, 4
+    x = synth.bf16_values(rng, R, 256)
+    h = rng.standard_normal((R, hc, 256)).astype(np.float32)
+    inj = rng.standard_normal((R, 8)).astype(np.float32)
+    y_plain, _, _ = oracle.moe_layer(W, x)
+    y, hout = oracle.moe_layer_hc(W, x, h, inj, refr=False)
+    assert np.array_equal(y, y_plain)
+    assert np.array_equal(hout, h + y[:, None, :] * inj[:, :hc, None])
+    y1, hout1 = oracle.moe_layer_hc(W, x, h, inj, refr=True)
+    assert np.array_equal(bf32(y1), y1) and np.array_equal(bf32(hout1), hout1)
+    step = np.abs(y_plain) * 2.0 ** -7 + 1e-3 * np.abs(y_plain).max()
+    assert np.all(np.abs(y1 - y_plain) <= 4 * step)
