@@ -60,7 +60,10 @@ struct ne_exl3_lin {
   uint32_t *cnt = nullptr; // per 128-column output block (the one-launch path's completion counters)
   bool one_launch = true;  // IJAH_LIN_PATH=staged at creation: prep, GEMV and finish as three launches
   int part_S = 0;
+  float *hc_scr = nullptr;  // the HC read's scratch when this is its up linear (xn, u, ip), hc_rows rows
+  int hc_rows = 0;
   ~ne_exl3_lin() {
+    dev_free(hc_scr);
     dev_free(tiles);
     dev_free(suh);
     dev_free(svh);
@@ -288,6 +291,42 @@ NE_API int ne_exl3_lin_run_epi(ne_exl3_lin *l, int R, const ne_buf *x, uint64_t 
     const float *xp = (const float *)((const char *)x->dev + x_off);
     float *yp = (float *)((char *)y->dev + y_off);
     timed(stream(), gpu_ms, [&] { lin_launch(l, R, xp, yp, stream(), e); });
+  });
+}
+
+NE_API int ne_hc_read(ne_exl3_lin *down, ne_exl3_lin *up, int R, const ne_buf *h, const ne_buf *hc_norm,
+                      const ne_buf *inject, ne_buf *mix, ne_buf *inj, ne_buf *out, int refr, double *gpu_ms) {
+  return c_call([&] {
+    IJ_CHECK(down && up && h && hc_norm && inject && mix && inj && out, "null argument");
+    IJ_CHECK(R >= 1 && R <= kLinMaxRows, "rows %d (1..%d)", R, kLinMaxRows);
+    const int hcd = up->out, hid = hcd / 4, lr = down->out;
+    IJ_CHECK(hcd % 4 == 0 && down->in == hcd && up->in == lr,
+             "down [%d -> %d] and up [%d -> %d] must be 4 hid -> lr -> 4 hid", down->in, down->out, up->in, up->out);
+    IJ_CHECK(h->size >= (uint64_t)R * hcd * 4, "h buffer too small for [%d][4][%d] f32", R, hid);
+    IJ_CHECK(hc_norm->size >= (uint64_t)hcd * 2, "hc_norm must hold %d bf16", hcd);
+    IJ_CHECK(inject->size >= (uint64_t)4 * hcd * 2, "inject must hold [4][%d] bf16", hcd);
+    IJ_CHECK(mix->size >= (uint64_t)R * lr * 4, "mix buffer too small for [%d][%d] f32", R, lr);
+    IJ_CHECK(inj->size >= (uint64_t)R * 8 * 4, "inj buffer too small for [%d][8] f32", R);
+    IJ_CHECK(out->size >= (uint64_t)R * hid * 4, "out buffer too small for [%d][%d] f32", R, hid);
+    if (R > up->hc_rows) {
+      dev_free(up->hc_scr);
+      up->hc_scr = dev_alloc<float>((size_t)kLinMaxRows * (2 * (size_t)hcd + 16));
+      up->hc_rows = kLinMaxRows;
+    }
+    float *xn = up->hc_scr, *u = xn + (size_t)kLinMaxRows * hcd, *ip = u + (size_t)kLinMaxRows * hcd;
+    const float *hp = (const float *)h->dev;
+    const uint16_t *nw = (const uint16_t *)hc_norm->dev;
+    float *injp = (float *)inj->dev;
+    LinEpi act;  // the down linear's epilogue: mix = rr(silu(rr(v) / 4))
+    act.kind = 2;
+    act.refr = refr ? 1 : 0;
+    timed(stream(), gpu_ms, [&] {
+      hipStream_t s = stream();
+      launch_hc_prep(hp, nw, (const uint16_t *)inject->dev, xn, ip, injp, R, hid, s);
+      lin_launch(down, R, xn, (float *)mix->dev, s, act);
+      lin_launch(up, R, (const float *)mix->dev, u, s);
+      launch_hc_out(u, hp, nw, ip, injp, (float *)out->dev, R, hid, refr ? 1 : 0, s);
+    });
   });
 }
 

@@ -754,6 +754,78 @@ __global__ __launch_bounds__(64) void lin_finish(LinArgs a) {
   if (m1) lin_store(a, r, i1, v1 * h2f(a.svh[i1]));
 }
 
+// ------------------------------------------------------------------------------------------------ HC read
+// The hyper-connection read's elementwise steps around the down and up linears (reference
+// kernels/trunk6/t6_epi.metal:16-97). Four streams of hid columns per row; rr = bf16 rounding when refr.
+constexpr int kHcStreams = 4;
+
+__device__ __forceinline__ float block_sum256(float v, float *red) {  // 256 threads; every thread gets the sum
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return ((red[0] + red[1]) + red[2]) + red[3];
+}
+
+// workgroup (row r, stream s), 256 threads (reference t6e_hc_prep, :16-50)
+__global__ __launch_bounds__(256) void hc_prep(const float *__restrict__ h, const uint16_t *__restrict__ nw,
+                                               const uint16_t *__restrict__ iw, float *__restrict__ xn,
+                                               float *__restrict__ ip, float *__restrict__ inj, int hid) {
+  __shared__ float red[4];
+  const int r = blockIdx.x / kHcStreams, s = blockIdx.x % kHcStreams, hcd = kHcStreams * hid;
+  const float *hr = h + (uint64_t)r * hcd + (uint64_t)s * hid;
+  float ss = 0.f, a[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int i = threadIdx.x; i < hid; i += 256) {
+    const float v = hr[i], xv = v * epi_bf(nw[s * hid + i]);
+    ss += v * v;
+#pragma unroll
+    for (int k = 0; k < 4; k++) a[k] += epi_bf(iw[(uint64_t)k * hcd + s * hid + i]) * xv;
+  }
+  ss = block_sum256(ss, red);
+  const float inv = 1.f / sqrtf(ss / (float)hid + 1e-6f);
+  for (int i = threadIdx.x; i < hid; i += 256)
+    xn[(uint64_t)r * hcd + s * hid + i] = hr[i] * epi_bf(nw[s * hid + i]) * inv;
+  float t[4];
+#pragma unroll
+  for (int k = 0; k < 4; k++) t[k] = block_sum256(a[k], red);
+  if (threadIdx.x < 4) ip[(r * kHcStreams + s) * 4 + threadIdx.x] = t[threadIdx.x] * inv;
+  if (threadIdx.x == 0) inj[r * 8 + kHcStreams + s] = inv;
+}
+
+// one thread per (row, column) (reference t6e_hc_out, :80-97, and t6e_hc_act's gates, :53-78)
+__global__ __launch_bounds__(256) void hc_out(const float *__restrict__ u, const float *__restrict__ h,
+                                              const uint16_t *__restrict__ nw, const float *__restrict__ ip,
+                                              float *__restrict__ inj, float *__restrict__ out, int R, int hid,
+                                              int refr) {
+  const int g = blockIdx.x * 256 + threadIdx.x;
+  if (g >= R * hid) return;
+  const int r = g / hid, c = g % hid, hcd = kHcStreams * hid;
+  float v[kHcStreams];
+#pragma unroll
+  for (int s = 0; s < kHcStreams; s++) {
+    const uint64_t row = (uint64_t)s * hid + c;
+    const float inv = inj[r * 8 + kHcStreams + s];
+    const float sg = epi_rr(1.f / (1.f + expf(-epi_rr(u[(uint64_t)r * hcd + row], refr))), refr);
+    v[s] = epi_rr(sg * epi_rr(h[(uint64_t)r * hcd + row] * inv * epi_bf(nw[row]), refr), refr);
+  }
+  out[(uint64_t)r * hid + c] = epi_rr(((v[0] + v[1]) + (v[2] + v[3])) * 0.25f, refr);
+  if (c < 4) {
+    float t = 0.f;
+#pragma unroll
+    for (int s = 0; s < kHcStreams; s++) t += ip[(r * kHcStreams + s) * 4 + c];
+    inj[r * 8 + c] = epi_rr(2.f / (1.f + expf(-epi_rr(t, refr) * 0.25f)), refr);
+  }
+}
+
+void launch_hc_prep(const float *h, const uint16_t *nw, const uint16_t *iw, float *xn, float *ip, float *inj, int R,
+                    int hid, hipStream_t s) {
+  hipLaunchKernelGGL(hc_prep, dim3(R * kHcStreams), dim3(256), 0, s, h, nw, iw, xn, ip, inj, hid);
+}
+void launch_hc_out(const float *u, const float *h, const uint16_t *nw, const float *ip, float *inj, float *out, int R,
+                   int hid, int refr, hipStream_t s) {
+  hipLaunchKernelGGL(hc_out, dim3((R * hid + 255) / 256), dim3(256), 0, s, u, h, nw, ip, inj, out, R, hid, refr);
+}
+
 // ------------------------------------------------------------------------------------------------ decode
 // W' fp16 bits [IT*16][OT*16] from re-laid tiles: one wave per tile, grid ceil(IT * OTp / 4) x 256.
 template <int K>

@@ -84,6 +84,7 @@ SIGNATURES = {
     "ne_exl3_lin_info": (_i, [_vp, C.POINTER(_i), C.POINTER(_i), C.POINTER(_i)]),
     "ne_exl3_lin_run": (_i, [_vp, _i, _vp, _u64, _vp, _u64, _dp]),
     "ne_exl3_lin_run_epi": (_i, [_vp, _i, _vp, _u64, _vp, _u64, _vp, _dp]),
+    "ne_hc_read": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _dp]),
     "ne_exl3_lin_decode": (_i, [_vp, _vp, _dp]),
     "ne_moe_create": (_vp, [C.POINTER(MoeDesc)]),
     "ne_moe_load": (_vp, [_vp, C.c_char_p, _i]),
@@ -305,6 +306,15 @@ class Exl3Linear:
             self.free()
         except Exception:
             pass
+
+
+def hc_read(down, up, R, h, hc_norm, inject, mix, inj, out, refr=True, timed=False):
+    """ne_hc_read: the hyper-connection read through two Exl3Linear mixes (device buffers throughout)"""
+    eng = down.eng
+    ms = C.c_double(0)
+    eng._ok(eng.lib.ne_hc_read(down.ptr, up.ptr, R, h.ptr, hc_norm.ptr, inject.ptr, mix.ptr, inj.ptr, out.ptr,
+                               int(bool(refr)), C.byref(ms) if timed else None), "ne_hc_read")
+    return ms.value
 
 
 class MoeLayer:

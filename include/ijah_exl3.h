@@ -72,6 +72,15 @@ typedef struct ne_exl3_epi {
  * trunk6.metal:199-222 t6_finish) */
 NE_API int ne_exl3_lin_run_epi(ne_exl3_lin *l, int R, const ne_buf *x, uint64_t x_off, ne_buf *y, uint64_t y_off,
                                const ne_exl3_epi *epi, double *gpu_ms);
+/* The hyper-connection read on EXL3 mixes (reference models/flash_next/layer_t6.mm:89-133, t6_hc_read, with
+ * kernels/trunk6/t6_epi.metal:16-97; rr = bf16 rounding when refr): for each row and stream s of h f32 [R][4][hid],
+ * inv_s = 1/sqrt(mean(h_s^2) + 1e-6), xn = h w inv_s (w = hc_norm bf16 [4 hid]); mix f32 [R][lr] = rr(silu(rr(down(xn))
+ * / 4)) (down: 4 hid -> lr); u = up(mix) (lr -> 4 hid); out f32 [R][hid] = rr(((v_0 + v_1) + (v_2 + v_3)) / 4),
+ * v_s = rr(rr(sigmoid(rr(u_s))) rr(h_s inv_s w_s)); inj f32 [R][8] = the 4 block-inject gates rr(2 sigmoid(rr(sum_s
+ * inject_j . (h_s w_s) inv_s) / 4)) (inject bf16 [4][4 hid]), then inv_0..3. out is the MoE (or attention) input and
+ * inj the gates of the HC write that follows (ne_moe_run_hc). R 1..32. */
+NE_API int ne_hc_read(ne_exl3_lin *down, ne_exl3_lin *up, int R, const ne_buf *h, const ne_buf *hc_norm,
+                      const ne_buf *inject, ne_buf *mix, ne_buf *inj, ne_buf *out, int refr, double *gpu_ms);
 /* n linears at R rows, all reading x (f32 [R][in_i]) and writing scratch outputs, captured once in a HIP graph and
  * replayed reps times after warmup replays: us_per_lin = GPU time per linear (HIP events). Replaces the reference's
  * differential timing of the trunk stages (kernels/trunk6/trunk6.mm:232-249 replays, core/bench.h:21-24). */

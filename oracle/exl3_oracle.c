@@ -563,6 +563,52 @@ int orc_moe_layer(const orc_moe *m, const float *x, int R, float *y, float *logi
   return 0;
 }
 
+/* The hyper-connection read's steps around its down / up linears (kernels/trunk6/t6_epi.metal:16-97), 4 streams of
+ * hid per row. prep (:16-50): inv_s = 1/sqrt(sum(h_s^2) / hid + 1e-6), xn = (h w) inv_s, ip[r][s][j] = (sum_i
+ * inject_j[s hid + i] (h w)[i]) inv_s, inj[r][4 + s] = inv_s. out (:80-97): v_s = rr(rr(sigmoid(rr(u_s))) rr((h_s
+ * inv_s) w_s)), out = rr(((v_0 + v_1) + (v_2 + v_3)) / 4); gates (:53-78) inj[r][j] = rr(2 sigmoid(rr(sum_s ip) / 4)).
+ * Sums over i in f64 (the GPU's f32 order is its own). */
+void orc_hc_prep(const float *h, const uint16_t *nw, const uint16_t *iw, int R, int hid, float *xn, float *ip,
+                 float *inj) {
+  const size_t hcd = 4 * (size_t)hid;
+  for (int r = 0; r < R; r++)
+    for (int s = 0; s < 4; s++) {
+      const float *hr = h + r * hcd + (size_t)s * hid;
+      double ss = 0.0, a[4] = {0, 0, 0, 0};
+      for (int i = 0; i < hid; i++) {
+        const float xv = hr[i] * orc_bf16_to_f32(nw[s * hid + i]);
+        ss += (double)hr[i] * hr[i];
+        for (int k = 0; k < 4; k++) a[k] += (double)orc_bf16_to_f32(iw[k * hcd + s * hid + i]) * xv;
+      }
+      const float inv = 1.0f / sqrtf((float)ss / (float)hid + 1e-6f);
+      for (int i = 0; i < hid; i++) xn[r * hcd + s * hid + i] = hr[i] * orc_bf16_to_f32(nw[s * hid + i]) * inv;
+      for (int k = 0; k < 4; k++) ip[(r * 4 + s) * 4 + k] = (float)a[k] * inv;
+      inj[r * 8 + 4 + s] = inv;
+    }
+}
+
+void orc_hc_out(const float *u, const float *h, const uint16_t *nw, const float *ip, int R, int hid, int refr,
+                float *inj, float *out) {
+  const size_t hcd = 4 * (size_t)hid;
+  for (int r = 0; r < R; r++) {
+    for (int c = 0; c < hid; c++) {
+      float v[4];
+      for (int s = 0; s < 4; s++) {
+        const size_t row = (size_t)s * hid + c;
+        const float inv = inj[r * 8 + 4 + s];
+        const float sg = rr_(sigmoidf_(rr_(u[r * hcd + row], refr)), refr);
+        v[s] = rr_(sg * rr_(h[r * hcd + row] * inv * orc_bf16_to_f32(nw[row]), refr), refr);
+      }
+      out[(size_t)r * hid + c] = rr_(((v[0] + v[1]) + (v[2] + v[3])) * 0.25f, refr);
+    }
+    for (int j = 0; j < 4; j++) {
+      float t = 0.0f;
+      for (int s = 0; s < 4; s++) t += ip[(r * 4 + s) * 4 + j];
+      inj[r * 8 + j] = rr_(2.0f * sigmoidf_(rr_(t, refr) * 0.25f), refr);
+    }
+  }
+}
+
 /* The layer with the hyper-connection write (kernels/fn_moe.metal:7-10 finisher, :420-448): the routed sum s (slot
  * order) and the gated shared term t kept apart; sg = rr(sigmoid(shared logit)) (:421, :444 rr(sgt)); y = branch =
  * rr(rr(s) + rr(t)); hout[r][st][c] = rr(h[r][st][c] + rr(branch * inj[r][st])), inj [R][8]. rr = bf16 when refr. */

@@ -18,6 +18,8 @@
  *                         placed independently, and the rounding switch off vs plain float math.
  *   orc_router_logits / orc_route: numpy dot + bf16 rounding; ties to the lower index vs numpy stable argsort.
  *   orc_moe_*:            explicit numpy restatement of SwiGLU experts and the slot-order combine.
+ *   orc_hc_prep / orc_hc_out: numpy closed forms (rms, inject dots, sigmoid-weighted stream mean) and, composed with
+ *                         the oracle linears, an f64 numpy restatement of the whole HC read.
  *   orc_hc_write / orc_moe_layer_hc: numpy closed form of the finisher; with rounding off the branch equals the plain
  *                         layer's slot-order sum bit for bit; the shared term is the plain layer minus its routed part.
  * Parity versus upstream exllamav3's codec itself stays unpinned (the module is absent); the restatement follows
@@ -89,6 +91,11 @@ typedef struct {
 /* kernel arithmetic; y [R][hid] f32; logits [R][ne] (may be NULL); route [R][2 topk] u32 (ids, f32 weight bits,
  * may be NULL). Returns 0. */
 int orc_moe_layer(const orc_moe *m, const float *x, int R, float *y, float *logits, uint32_t *route);
+/* the hyper-connection read's prep and output steps (kernels/trunk6/t6_epi.metal:16-97) */
+void orc_hc_prep(const float *h, const uint16_t *nw, const uint16_t *iw, int R, int hid, float *xn, float *ip,
+                 float *inj);
+void orc_hc_out(const float *u, const float *h, const uint16_t *nw, const float *ip, int R, int hid, int refr,
+                float *inj, float *out);
 /* the hyper-connection write (kernels/fn_moe.metal:437-448) from the routed sum s and gated shared term t (t may be
  * null), and the layer with it (shared gate rounded to bf16 when refr) */
 void orc_hc_write(const float *s, const float *t, int R, int hid, int hc, int refr, const float *h, const float *inj,

@@ -63,6 +63,10 @@ def lib():
         L.orc_lin_epi.restype = C.c_int
         L.orc_lin_epi.argtypes = [_f32p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _f32p, C.c_void_p,
                                   C.c_void_p, C.c_void_p, C.c_long]
+        L.orc_hc_prep.restype = None
+        L.orc_hc_prep.argtypes = [_f32p, _u16p, _u16p, C.c_int, C.c_int, _f32p, _f32p, _f32p]
+        L.orc_hc_out.restype = None
+        L.orc_hc_out.argtypes = [_f32p, _f32p, _u16p, _f32p, C.c_int, C.c_int, C.c_int, _f32p, _f32p]
         L.orc_hc_write.restype = None
         L.orc_hc_write.argtypes = [_f32p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, _f32p, _f32p, _f32p, _f32p]
         L.orc_moe_layer_hc.restype = C.c_int
@@ -212,6 +216,36 @@ def moe_layer(W, x):
     rt = np.zeros((R, 2 * m.topk), np.uint32)
     lib().orc_moe_layer(C.byref(m), x, R, y, lg, rt)
     return y, lg, rt
+
+
+def hc_prep(h, nw, iw):
+    """h f32 [R, 4, hid], hc_norm bf16 bits [4 hid], inject bf16 bits [4, 4 hid] -> xn [R, 4 hid], ip [R, 4, 4],
+    inj [R, 8] (inv_s filled, gates 0)"""
+    h = _c(h, np.float32)
+    R, _, hid = h.shape
+    xn, ip, inj = np.zeros((R, 4 * hid), np.float32), np.zeros((R, 4, 4), np.float32), np.zeros((R, 8), np.float32)
+    lib().orc_hc_prep(h, _c(nw, np.uint16), _c(iw, np.uint16), R, hid, xn, ip, inj)
+    return xn, ip, inj
+
+
+def hc_out(u, h, nw, ip, inj, refr=True):
+    """u [R, 4 hid] (the up linear's output) -> out [R, hid]; inj [R, 8] gets its gates (a copy is returned)"""
+    h = _c(h, np.float32)
+    R, _, hid = h.shape
+    inj = _c(inj, np.float32).copy()
+    out = np.zeros((R, hid), np.float32)
+    lib().orc_hc_out(_c(u, np.float32), h, _c(nw, np.uint16), _c(ip, np.float32), R, hid, int(bool(refr)), inj, out)
+    return out, inj
+
+
+def hc_read(h, nw, iw, down, up, refr=True):
+    """the HC read on EXL3 mixes (models/flash_next/layer_t6.mm:89-133): down / up = (trellis, suh, svh) of the
+    4 hid -> lr and lr -> 4 hid linears. Returns mix [R, lr], inj [R, 8], out [R, hid]."""
+    xn, ip, inj = hc_prep(h, nw, iw)
+    mix = lin_epi(exl3_linear(xn, *down), 2, refr=refr)
+    u = exl3_linear(mix, *up)
+    out, inj = hc_out(u, h, nw, ip, inj, refr=refr)
+    return mix, inj, out
 
 
 def hc_write(s, t, h, inj, refr=True):

@@ -220,3 +220,83 @@ def test_linear_epilogue_rejects(eng, oracle):
             lin.run_epi(2, x, y, kind, **kw)
     with pytest.raises(RuntimeError, match="y buffer too small"):
         lin.run_epi(2, x, y, 5, y_off=4 * 49, ldy=96)
+
+
+# ------------------------------------------------------------------------------------------------ HC read
+def bf_steps(a, b):
+    return np.abs(a.astype(np.float64) - b) / (np.maximum(np.abs(a), np.abs(b)) * 2.0 ** -7 + 1e-30)
+
+
+@pytest.mark.parametrize("hid,lr,K,R", [(2560, 320, 6, 1), (2560, 320, 6, 4), (2560, 320, 6, 16), (128, 64, 5, 3)])
+def test_hc_read(eng, oracle, hid, lr, K, R):
+    """ne_hc_read (reference models/flash_next/layer_t6.mm:89-133 with kernels/trunk6/t6_epi.metal:16-97) against the
+    oracle read on the same inputs: 1/rms bit-close, mix / out / gates within bf16 flips where the GPU's f32 sums and
+    the oracle's straddle a rounding boundary; rounding off, rel-L2 within the linears' own bar."""
+    print(f"hc read hid {hid} lr {lr} K{K} R{R}", flush=True)
+    rng = np.random.default_rng(hid + lr + K + R)
+    h = (rng.standard_normal((R, 4, hid)) * np.array([0.5, 1, 2, 4])[None, :, None]).astype(np.float32)
+    nw = synth.bf16((1 + 0.1 * rng.standard_normal(4 * hid)).astype(np.float32))
+    iw = synth.bf16((rng.standard_normal((4, 4 * hid)) / np.sqrt(4 * hid)).astype(np.float32))
+    down, up = synth.linear(rng, 4 * hid, lr, K), synth.linear(rng, lr, 4 * hid, K)
+    ld, lu = eng.exl3_linear(*down), eng.exl3_linear(*up)
+    hb, nb, ib = eng.from_numpy(h), eng.from_numpy(nw), eng.from_numpy(iw)
+    mb, jb, ob = eng.alloc(R * lr * 4), eng.alloc(R * 32), eng.alloc(R * hid * 4)
+    from ijah_amd.engine import hc_read
+    for refr in (True, False):
+        hc_read(ld, lu, R, hb, nb, ib, mb, jb, ob, refr=refr)
+        mix, inj, out = mb.download(np.float32, (R, lr)), jb.download(np.float32, (R, 8)), ob.download(np.float32,
+                                                                                                     (R, hid))
+        want_mix, want_inj, want_out = oracle.hc_read(h, nw, iw, down, up, refr=refr)
+        assert np.allclose(inj[:, 4:], want_inj[:, 4:], rtol=2e-6)
+        if refr:
+            # the inner rounding rr(v) before silu / sigmoid may flip one step where the GPU's and the oracle's f32
+            # sums straddle a boundary (the activation can then move the output by many steps: silu(t) ~ t e^t for
+            # t << 0): each value is the activation of the oracle's rr(v) or of one of its bf16 neighbours
+            xn, ip, _ = oracle.hc_prep(h, nw, iw)
+            v = oracle.exl3_linear(xn, *down)
+            assert act_of_neighbour(mix, v, lambda c: c / 4 / (1 + np.exp(-c / 4)))
+            assert act_of_neighbour(inj[:, :4], ip.astype(np.float64).sum(axis=1), lambda c: 2 / (1 + np.exp(-c / 4)))
+            assert (mix == want_mix).mean() > 0.97
+            assert (out == want_out).mean() > 0.95 and rel(out, want_out) < 3e-3
+        else:
+            # out is a mean over streams whose normed terms often cancel: the up linear's own error (5e-5) grows
+            assert rel(mix, want_mix) < 1e-4 and rel(out, want_out) < 1e-3
+            assert np.allclose(inj[:, :4], want_inj[:, :4], rtol=1e-5)
+    hc_read(ld, lu, R, hb, nb, ib, mb, jb, ob, refr=True)
+    assert np.array_equal(ob.download(np.float32, (R, hid)), hc_read_again(ld, lu, R, hb, nb, ib, eng, lr, hid))
+
+
+def act_of_neighbour(got, v, act):
+    """got == rr(act(c)) within one bf16 step, for c = rr(v) or a bf16 neighbour of it"""
+    b = oracle_bf16(v)
+    u = b.view(np.uint32)
+    ok = np.zeros(got.shape, bool)
+    for d in (-1, 0, 1):
+        c = ((u.astype(np.int64) >> 16) + d).astype(np.uint32) << 16
+        cand = oracle_bf16(act(c.view(np.float32).astype(np.float64)))
+        ok |= bf_steps(got, cand) <= 1.0 + 1e-6
+    return bool(ok.all())
+
+
+def oracle_bf16(x):
+    u = np.asarray(x, np.float64).astype(np.float32).view(np.uint32).astype(np.uint64)
+    return (((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16).astype(np.uint32).view(np.float32)
+
+
+def hc_read_again(ld, lu, R, hb, nb, ib, eng, lr, hid):
+    from ijah_amd.engine import hc_read
+    mb, jb, ob = eng.alloc(R * lr * 4), eng.alloc(R * 32), eng.alloc(R * hid * 4)
+    hc_read(ld, lu, R, hb, nb, ib, mb, jb, ob, refr=True)
+    return ob.download(np.float32, (R, hid))  # deterministic across runs and output buffers
+
+
+def test_hc_read_rejects(eng, oracle):
+    rng = np.random.default_rng(4)
+    from ijah_amd.engine import hc_read
+    ld, lu = eng.exl3_linear(*synth.linear(rng, 512, 64, 5)), eng.exl3_linear(*synth.linear(rng, 64, 256, 5))
+    b = eng.alloc(1 << 16)
+    with pytest.raises(RuntimeError, match="must be 4 hid -> lr -> 4 hid"):
+        hc_read(ld, lu, 1, b, b, b, b, b, b)
+    lu = eng.exl3_linear(*synth.linear(rng, 64, 512, 5))
+    with pytest.raises(RuntimeError, match="h buffer too small"):
+        hc_read(ld, lu, 1, eng.alloc(16), b, b, b, b, b)

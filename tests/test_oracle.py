@@ -421,3 +421,80 @@ def test_moe_layer_hc_matches_plain_layer(oracle):
     assert np.array_equal(bf32(y1), y1) and np.array_equal(bf32(hout1), hout1)
     step = np.abs(y_plain) * 2.0 ** -7 + 1e-3 * np.abs(y_plain).max()
     assert np.all(np.abs(y1 - y_plain) <= 4 * step)
+
+
+# ------------------------------------------------------------------------------------------------ HC read
+def hc_case(seed, R=2, hid=128, lr=64, K=5):
+    rng = np.random.default_rng(seed)
+    h = (rng.standard_normal((R, 4, hid)) * np.array([0.5, 1, 2, 4])[None, :, None]).astype(np.float32)
+    nw = synth.bf16((1 + 0.1 * rng.standard_normal(4 * hid)).astype(np.float32))
+    iw = synth.bf16((rng.standard_normal((4, 4 * hid)) / np.sqrt(4 * hid)).astype(np.float32))
+    down = synth.linear(rng, 4 * hid, lr, K)
+    up = synth.linear(rng, lr, 4 * hid, K)
+    return h, nw, iw, down, up
+
+
+def np_hc_prep(h, nw, iw):
+    R, _, hid = h.shape
+    w = bf16_f64(nw).reshape(4, hid)
+    inv = 1 / np.sqrt((h.astype(np.float64) ** 2).mean(axis=2) + 1e-6)         # [R, 4]
+    xw = h.astype(np.float64) * w[None]
+    xn = (xw * inv[:, :, None]).reshape(R, 4 * hid)
+    ip = np.einsum("rsi,jsi->rsj", xw, bf16_f64(iw).reshape(4, 4, hid)) * inv[:, :, None]
+    return xn, ip, inv
+
+
+def bf16_f64(b):
+    return (np.asarray(b, np.uint16).astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+
+
+def test_hc_prep_closed_form(oracle):
+    h, nw, iw, _, _ = hc_case(90)
+    xn, ip, inj = oracle.hc_prep(h, nw, iw)
+    want_xn, want_ip, inv = np_hc_prep(h, nw, iw)
+    assert np.allclose(inj[:, 4:], inv, rtol=1e-6) and np.all(inj[:, :4] == 0)
+    assert np.allclose(xn, want_xn, rtol=2e-6, atol=1e-7)
+    assert np.allclose(ip, want_ip, rtol=1e-5, atol=1e-6)
+    # scale invariance: 1/rms cancels a scale of h (up to the 1e-6 epsilon: ~4e-6 relative at rms 0.5)
+    xn2, _, inj2 = oracle.hc_prep(h * np.float32(8.0), nw, iw)
+    assert np.allclose(xn2, xn, rtol=2e-5, atol=1e-7) and np.allclose(inj2[:, 4:] * 8, inj[:, 4:], rtol=2e-5)
+
+
+@pytest.mark.parametrize("refr", [True, False])
+def test_hc_out_closed_form(oracle, refr):
+    rng = np.random.default_rng(91)
+    h, nw, iw, _, _ = hc_case(92)
+    R, _, hid = h.shape
+    _, ip, inj = oracle.hc_prep(h, nw, iw)
+    u = (rng.standard_normal((R, 4 * hid)) * 2).astype(np.float32)
+    out, inj2 = oracle.hc_out(u, h, nw, ip, inj, refr=refr)
+    q = bfr if refr else (lambda a: np.asarray(a, np.float64))
+    inv = inj[:, 4:].astype(np.float64)
+    sg = q(1 / (1 + np.exp(-q(u.reshape(R, 4, hid)))))
+    v = q(sg * q(h * inv[:, :, None] * bf16_f64(nw).reshape(1, 4, hid)))
+    want = q(((v[:, 0] + v[:, 1]) + (v[:, 2] + v[:, 3])) * 0.25)
+    gates = q(2 / (1 + np.exp(-q(ip.astype(np.float64).sum(axis=1)) * 0.25)))
+    if refr:
+        assert bf_steps(out, want).max() <= 1.0 and (out == want).mean() > 0.97
+        assert bf_steps(inj2[:, :4], gates).max() <= 1.0
+    else:
+        assert np.allclose(out, want, rtol=1e-5, atol=1e-7) and np.allclose(inj2[:, :4], gates, rtol=1e-6)
+    assert np.array_equal(inj2[:, 4:], inj[:, 4:])
+
+
+def test_hc_read_vs_f64(oracle):
+    """the whole read (prep, down linear + silu(/4), up linear, sigmoid-weighted stream mean, gates) against f64
+    numpy with explicit decoded matrices and no rounding: within the fp16 input preparation of the two linears"""
+    h, nw, iw, down, up = hc_case(93)
+    R, _, hid = h.shape
+    mix, inj, out = oracle.hc_read(h, nw, iw, down, up, refr=False)
+    xn, ip, inv = np_hc_prep(h, nw, iw)
+    d = np_linear_exact(oracle, xn, *down) / 4
+    want_mix = d / (1 + np.exp(-d))
+    u = np_linear_exact(oracle, want_mix, *up).reshape(R, 4, hid)
+    normed = h * inv[:, :, None] * bf16_f64(nw).reshape(1, 4, hid)
+    want_out = (normed / (1 + np.exp(-u))).mean(axis=1)
+    assert np.linalg.norm(mix - want_mix) / np.linalg.norm(want_mix) < 3e-3
+    assert np.linalg.norm(out - want_out) / np.linalg.norm(want_out) < 3e-3
+    assert np.allclose(inj[:, :4], 2 / (1 + np.exp(-ip.sum(axis=1) / 4)), rtol=1e-5)
+    assert np.allclose(inj[:, 4:], inv, rtol=1e-6)
