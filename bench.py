@@ -142,6 +142,29 @@ def measure_trunk(eng, R, steps, seed, min_bytes=300e6):
     return out
 
 
+def measure_hc_read(eng, R, steps, seed, hid=2560, lr=320, K=6):
+    """The hyper-connection read (ne_hc_read: prep, down linear + silu epilogue, up linear, output) at R rows on
+    synthetic EXL3 mixes of the reference shape. GPU time per call from HIP events around its four launches, averaged
+    over calls on the same weights (4.9 MB: they stay in the last-level cache between calls)."""
+    from ijah_amd import synth
+    from ijah_amd.engine import hc_read
+    rng = np.random.default_rng(seed)
+    ld, lu = eng.exl3_linear(*synth.linear(rng, 4 * hid, lr, K)), eng.exl3_linear(*synth.linear(rng, lr, 4 * hid, K))
+    h = eng.from_numpy(rng.standard_normal((R, 4, hid)).astype(np.float32))
+    nw = eng.from_numpy(synth.bf16((1 + 0.1 * rng.standard_normal(4 * hid)).astype(np.float32)))
+    iw = eng.from_numpy(synth.bf16((rng.standard_normal((4, 4 * hid)) / 100).astype(np.float32)))
+    mix, inj, out = eng.alloc(R * lr * 4), eng.alloc(R * 32), eng.alloc(R * hid * 4)
+    for _ in range(3):
+        hc_read(ld, lu, R, h, nw, iw, mix, inj, out)
+    ms = [hc_read(ld, lu, R, h, nw, iw, mix, inj, out, timed=True) for _ in range(max(10, steps))]
+    res = {"rows": R, "hid": hid, "mix_rows": lr, "K": K, "us": round(1e3 * float(np.median(ms)), 3),
+           "launches": 4}
+    ld.free()
+    lu.free()
+    print(f"hc read R={R}: {res}", file=sys.stderr, flush=True)
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -155,6 +178,7 @@ def main():
                     help="run the layer chain eagerly --steps times and exit (for rocprofv3 --pmc passes)")
     ap.add_argument("--no-trunk", action="store_true", help="skip the trunk (config 3) lines")
     ap.add_argument("--trunk-only", action="store_true", help="only measure the trunk linears (config 3) and exit")
+    ap.add_argument("--hc-only", action="store_true", help="only measure the hyper-connection read and exit")
     ap.add_argument("--batch-rows", type=int, default=0, metavar="R",
                     help="only measure the grouped matrix-core layer at R rows (a 4-layer graph) and exit")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MB",
@@ -174,8 +198,14 @@ def main():
             eng.run_kernel("copy_u128", [src, dst, np.uint64(n // 16)], (2048, 1, 1), (256, 1, 1))
         print(json.dumps({"copy_probe_bytes": n, "launches": 5}), flush=True)
         return
+    if a.hc_only:
+        print(json.dumps({"hc_read_m1": measure_hc_read(eng, 1, a.steps, a.seed + 5),
+                          "hc_read_m16": measure_hc_read(eng, 16, a.steps, a.seed + 6)}), flush=True)
+        return
     if a.trunk_only:
-        print(json.dumps({"m1": measure_trunk(eng, 1, a.steps, a.seed), "m16": measure_trunk(eng, 16, a.steps, a.seed)}),
+        print(json.dumps({"m1": measure_trunk(eng, 1, a.steps, a.seed), "m16": measure_trunk(eng, 16, a.steps, a.seed),
+                          "hc_read_m1": measure_hc_read(eng, 1, a.steps, a.seed + 5),
+                          "hc_read_m16": measure_hc_read(eng, 16, a.steps, a.seed + 6)}),
               flush=True)
         return
     if a.batch_rows:
@@ -233,6 +263,8 @@ def main():
     if not a.no_trunk:
         extra["trunk_m1"] = measure_trunk(eng, 1, max(5, a.steps // 5), a.seed + 3)
         extra["trunk_m16"] = measure_trunk(eng, 16, max(5, a.steps // 5), a.seed + 4)
+        extra["hc_read_m1"] = measure_hc_read(eng, 1, a.steps, a.seed + 5)
+        extra["hc_read_m16"] = measure_hc_read(eng, 16, a.steps, a.seed + 6)
     cpu = None if a.no_cpu else cpu_baseline()
     line = {
         "metric": "MoE layer us + effective packed-weight GB/s (% HBM peak), 5-bit EXL3, M=1",

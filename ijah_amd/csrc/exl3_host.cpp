@@ -302,6 +302,7 @@ NE_API int ne_hc_read(ne_exl3_lin *down, ne_exl3_lin *up, int R, const ne_buf *h
     const int hcd = up->out, hid = hcd / 4, lr = down->out;
     IJ_CHECK(hcd % 4 == 0 && down->in == hcd && up->in == lr,
              "down [%d -> %d] and up [%d -> %d] must be 4 hid -> lr -> 4 hid", down->in, down->out, up->in, up->out);
+    IJ_CHECK(hid % 64 == 0, "hid %d must be a multiple of 64", hid);
     IJ_CHECK(h->size >= (uint64_t)R * hcd * 4, "h buffer too small for [%d][4][%d] f32", R, hid);
     IJ_CHECK(hc_norm->size >= (uint64_t)hcd * 2, "hc_norm must hold %d bf16", hcd);
     IJ_CHECK(inject->size >= (uint64_t)4 * hcd * 2, "inject must hold [4][%d] bf16", hcd);
@@ -310,7 +311,7 @@ NE_API int ne_hc_read(ne_exl3_lin *down, ne_exl3_lin *up, int R, const ne_buf *h
     IJ_CHECK(out->size >= (uint64_t)R * hid * 4, "out buffer too small for [%d][%d] f32", R, hid);
     if (R > up->hc_rows) {
       dev_free(up->hc_scr);
-      up->hc_scr = dev_alloc<float>((size_t)kLinMaxRows * (2 * (size_t)hcd + 16));
+      up->hc_scr = dev_alloc<float>((size_t)kLinMaxRows * (2 * (size_t)hcd + 16 * (size_t)((hid + 255) / 256)));
       up->hc_rows = kLinMaxRows;
     }
     float *xn = up->hc_scr, *u = xn + (size_t)kLinMaxRows * hcd, *ip = u + (size_t)kLinMaxRows * hcd;

@@ -759,37 +759,46 @@ __global__ __launch_bounds__(64) void lin_finish(LinArgs a) {
 // kernels/trunk6/t6_epi.metal:16-97). Four streams of hid columns per row; rr = bf16 rounding when refr.
 constexpr int kHcStreams = 4;
 
-__device__ __forceinline__ float block_sum256(float v, float *red) {  // 256 threads; every thread gets the sum
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-  __syncthreads();
-  return ((red[0] + red[1]) + red[2]) + red[3];
-}
-
-// workgroup (row r, stream s), 256 threads (reference t6e_hc_prep, :16-50)
+// workgroup (row r, stream s, 256-column chunk ch), 256 threads (reference t6e_hc_prep, :16-50): every workgroup
+// sums the whole stream's squares (independent loads, hid floats from L2), then prepares its own chunk:
+// xn = (h w) inv, ip[r][s][ch][j] = (inject_j . (h w) over the chunk) inv, inj[r][4 + s] = inv (chunk 0).
 __global__ __launch_bounds__(256) void hc_prep(const float *__restrict__ h, const uint16_t *__restrict__ nw,
                                                const uint16_t *__restrict__ iw, float *__restrict__ xn,
                                                float *__restrict__ ip, float *__restrict__ inj, int hid) {
-  __shared__ float red[4];
-  const int r = blockIdx.x / kHcStreams, s = blockIdx.x % kHcStreams, hcd = kHcStreams * hid;
+  __shared__ float red[4][5];
+  const int nch = (hid + 255) / 256;
+  const int ch = blockIdx.x % nch, rs = blockIdx.x / nch, r = rs / kHcStreams, s = rs % kHcStreams;
+  const int hcd = kHcStreams * hid, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const float *hr = h + (uint64_t)r * hcd + (uint64_t)s * hid;
-  float ss = 0.f, a[4] = {0.f, 0.f, 0.f, 0.f};
-  for (int i = threadIdx.x; i < hid; i += 256) {
-    const float v = hr[i], xv = v * epi_bf(nw[s * hid + i]);
-    ss += v * v;
+  float ss = 0.f;
+  for (int i0 = 0; i0 < hid; i0 += 256 * 4) {  // four loads in flight per thread
+    float v[4];
 #pragma unroll
-    for (int k = 0; k < 4; k++) a[k] += epi_bf(iw[(uint64_t)k * hcd + s * hid + i]) * xv;
+    for (int u = 0; u < 4; u++) {
+      const int i = i0 + 256 * u + threadIdx.x;
+      v[u] = i < hid ? hr[i] : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < 4; u++) ss += v[u] * v[u];
   }
-  ss = block_sum256(ss, red);
-  const float inv = 1.f / sqrtf(ss / (float)hid + 1e-6f);
-  for (int i = threadIdx.x; i < hid; i += 256)
-    xn[(uint64_t)r * hcd + s * hid + i] = hr[i] * epi_bf(nw[s * hid + i]) * inv;
-  float t[4];
+  const int i = ch * 256 + threadIdx.x;
+  const bool in = i < hid;
+  const float xv = in ? hr[i] * epi_bf(nw[s * hid + i]) : 0.f;
+  float t[5] = {ss, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int k = 0; k < 4; k++) t[k] = block_sum256(a[k], red);
-  if (threadIdx.x < 4) ip[(r * kHcStreams + s) * 4 + threadIdx.x] = t[threadIdx.x] * inv;
-  if (threadIdx.x == 0) inj[r * 8 + kHcStreams + s] = inv;
+  for (int k = 0; k < 4; k++) t[1 + k] = in ? epi_bf(iw[(uint64_t)k * hcd + s * hid + i]) * xv : 0.f;
+#pragma unroll
+  for (int k = 0; k < 5; k++)
+    for (int o = 32; o >= 1; o >>= 1) t[k] += __shfl_xor(t[k], o, 64);
+  if (lane == 0)
+    for (int k = 0; k < 5; k++) red[wave][k] = t[k];
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < 5; k++) t[k] = ((red[0][k] + red[1][k]) + red[2][k]) + red[3][k];
+  const float inv = 1.f / sqrtf(t[0] / (float)hid + 1e-6f);
+  if (in) xn[(uint64_t)r * hcd + s * hid + i] = xv * inv;
+  if (threadIdx.x < 4) ip[((r * kHcStreams + s) * nch + ch) * 4 + threadIdx.x] = t[1 + threadIdx.x] * inv;
+  if (threadIdx.x == 0 && ch == 0) inj[r * 8 + kHcStreams + s] = inv;
 }
 
 // one thread per (row, column) (reference t6e_hc_out, :80-97, and t6e_hc_act's gates, :53-78)
@@ -809,17 +818,22 @@ __global__ __launch_bounds__(256) void hc_out(const float *__restrict__ u, const
     v[s] = epi_rr(sg * epi_rr(h[(uint64_t)r * hcd + row] * inv * epi_bf(nw[row]), refr), refr);
   }
   out[(uint64_t)r * hid + c] = epi_rr(((v[0] + v[1]) + (v[2] + v[3])) * 0.25f, refr);
-  if (c < 4) {
+  if (c < 64) {  // one whole wave (hid % 64 == 0): the row's 4 gates from the inject partials, lane = (phase, s, j)
+    const int nch = (hid + 255) / 256, j = c & 3, st = (c >> 2) & 3, ph = c >> 4;
     float t = 0.f;
-#pragma unroll
-    for (int s = 0; s < kHcStreams; s++) t += ip[(r * kHcStreams + s) * 4 + c];
-    inj[r * 8 + c] = epi_rr(2.f / (1.f + expf(-epi_rr(t, refr) * 0.25f)), refr);
+    for (int ch = ph; ch < nch; ch += 4) t += ip[((r * kHcStreams + st) * nch + ch) * 4 + j];
+    t += __shfl_xor(t, 16, 64);  // the chunk phases
+    t += __shfl_xor(t, 32, 64);
+    t += __shfl_xor(t, 4, 64);   // the streams
+    t += __shfl_xor(t, 8, 64);
+    if (c < 4) inj[r * 8 + c] = epi_rr(2.f / (1.f + expf(-epi_rr(t, refr) * 0.25f)), refr);
   }
 }
 
 void launch_hc_prep(const float *h, const uint16_t *nw, const uint16_t *iw, float *xn, float *ip, float *inj, int R,
                     int hid, hipStream_t s) {
-  hipLaunchKernelGGL(hc_prep, dim3(R * kHcStreams), dim3(256), 0, s, h, nw, iw, xn, ip, inj, hid);
+  hipLaunchKernelGGL(hc_prep, dim3(R * kHcStreams * ((hid + 255) / 256)), dim3(256), 0, s, h, nw, iw, xn, ip, inj,
+                     hid);
 }
 void launch_hc_out(const float *u, const float *h, const uint16_t *nw, const float *ip, float *inj, float *out, int R,
                    int hid, int refr, hipStream_t s) {

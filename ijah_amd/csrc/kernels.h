@@ -137,8 +137,8 @@ constexpr int kLinSimdRows = 8, kLinMaxRows = 32;
 void launch_lin(const LinArgs &a, hipStream_t s);
 // The hyper-connection read around its two EXL3 linears (reference models/flash_next/layer_t6.mm:89-133, t6_hc_read,
 // with kernels/trunk6/t6_epi.metal:16-97): h f32 [R][4][hid], hc_norm bf16 [4 hid], inject bf16 [4][4 hid].
-// hc_prep: xn [R][4 hid] = h w inv_s (inv_s = 1/rms of stream s), ip [R][4 streams][4 gates] = the inject dots of
-// h w (times inv_s), inj[r][4 + s] = inv_s. hc_out (after the up linear's u [R][4 hid]): out [R][hid] and the gates
+// hc_prep: xn [R][4 hid] = h w inv_s (inv_s = 1/rms of stream s), ip [R][4 streams][ceil(hid / 256) chunks][4
+// gates] = the inject dots of h w over each chunk (times inv_s), inj[r][4 + s] = inv_s. hc_out (after the up linear's u [R][4 hid]): out [R][hid] and the gates
 // inj[r][j < 4] = rr(2 sigmoid(rr(sum_s ip[r][s][j]) / 4)).
 void launch_hc_prep(const float *h, const uint16_t *nw, const uint16_t *iw, float *xn, float *ip, float *inj, int R,
                     int hid, hipStream_t s);
