@@ -59,6 +59,8 @@ struct ne_exl3_lin {
   float *part = nullptr;   // [S][kLinMaxRows][OTp*16]
   uint32_t *cnt = nullptr; // per 128-column output block (the one-launch path's completion counters)
   bool one_launch = true;  // IJAH_LIN_PATH=staged at creation: prep, GEMV and finish as three launches
+  int min_kt = 16;         // fewest k tiles per split on the GEMV path (IJAH_LIN_MINKT at creation): 16 beats 8
+                           // (k / v 2048 -> 512: 6.1 vs 6.5 us; more splits cost more in the finisher's sums)
   int part_S = 0;
   float *hc_scr = nullptr;  // the HC read's scratch when this is its up linear (xn, u, ip), hc_rows rows
   int hc_rows = 0;
@@ -71,7 +73,7 @@ struct ne_exl3_lin {
     dev_free(part);
     dev_free(cnt);
   }
-  // k splits: smallest S (dividing IT, >= 8 k tiles per split) that gives >= 1024 workgroups, then enough to keep
+  // k splits: smallest S (dividing IT, >= min_kt k tiles per split) that gives >= 1024 workgroups, then enough to keep
   // the staged input within 32 KiB of LDS at R rows
   int splits(int R) const {
     const int NP = OTp / 2;
@@ -80,7 +82,7 @@ struct ne_exl3_lin {
       while ((NP + 7) / 8 * S < 512 && IT % (2 * S) == 0 && IT / (2 * S) >= 16) S *= 2;
       return S;
     }
-    while (NP * S < 1024 && IT % (2 * S) == 0 && IT / (2 * S) >= 8) S *= 2;
+    while (NP * S < 1024 && IT % (2 * S) == 0 && IT / (2 * S) >= min_kt) S *= 2;
     const int RT = R <= 1 ? 1 : R <= 2 ? 2 : R <= 4 ? 4 : 8;
     while ((size_t)RT * (IT / S) * 32 > 32768 && IT % (2 * S) == 0) S *= 2;
     return S;
@@ -116,6 +118,7 @@ static ne_exl3_lin *lin_create(const uint16_t *trellis, const uint16_t *suh, con
   IJ_HIP(hipMemset(l->cnt, 0, nc * 4));
   const char *path = getenv("IJAH_LIN_PATH");
   l->one_launch = !(path && std::string(path) == "staged");
+  if (const char *e = getenv("IJAH_LIN_MINKT")) l->min_kt = std::min(64, std::max(4, atoi(e)));
   return l.release();
 }
 
