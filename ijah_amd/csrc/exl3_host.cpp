@@ -59,6 +59,8 @@ struct ne_exl3_lin {
   float *part = nullptr;   // [S][kLinMaxRows][OTp*16]
   uint32_t *cnt = nullptr; // per 128-column output block (the one-launch path's completion counters)
   bool one_launch = true;  // IJAH_LIN_PATH=staged at creation: prep, GEMV and finish as three launches
+  int mm_min_kt = 8;       // the same for the matrix-core path (IJAH_LIN_MM_MINKT at creation, at least
+                           // kLinMmMinSpan): 8 beats 16 (q + k + v + o at 16 rows 50 vs 57 us)
   int min_kt = 16;         // fewest k tiles per split on the GEMV path (IJAH_LIN_MINKT at creation): 16 beats 8
                            // (k / v 2048 -> 512: 6.1 vs 6.5 us; more splits cost more in the finisher's sums)
   int part_S = 0;
@@ -79,7 +81,7 @@ struct ne_exl3_lin {
     const int NP = OTp / 2;
     int S = 1;
     if (R > kLinSimdRows) {  // matrix cores: 8 pairs per workgroup, >= 512 workgroups, >= 16 k tiles per split
-      while ((NP + 7) / 8 * S < 512 && IT % (2 * S) == 0 && IT / (2 * S) >= 16) S *= 2;
+      while ((NP + 7) / 8 * S < 512 && IT % (2 * S) == 0 && IT / (2 * S) >= mm_min_kt) S *= 2;
       return S;
     }
     while (NP * S < 1024 && IT % (2 * S) == 0 && IT / (2 * S) >= min_kt) S *= 2;
@@ -119,6 +121,7 @@ static ne_exl3_lin *lin_create(const uint16_t *trellis, const uint16_t *suh, con
   const char *path = getenv("IJAH_LIN_PATH");
   l->one_launch = !(path && std::string(path) == "staged");
   if (const char *e = getenv("IJAH_LIN_MINKT")) l->min_kt = std::min(64, std::max(4, atoi(e)));
+  if (const char *e = getenv("IJAH_LIN_MM_MINKT")) l->mm_min_kt = std::min(64, std::max(kLinMmMinSpan, atoi(e)));
   return l.release();
 }
 
@@ -219,11 +222,11 @@ static LinArgs lin_args(ne_exl3_lin *l, int R, const float *x, float *y, const L
   return a;
 }
 
-// The launches of one run: rows beyond the GEMV's 8 take the matrix-core GEMM when the k tiles pair up (IT even);
-// otherwise they run as groups of 8 rows through the GEMV path.
+// The launches of one run: rows beyond the GEMV's 8 take the matrix-core GEMM when the k tiles pair up (IT even) and
+// its k spans hold at least kLinMmMinSpan tiles; otherwise they run as groups of 8 rows through the GEMV path.
 static void lin_launch(ne_exl3_lin *l, int R, const float *x, float *y, hipStream_t s,
                        const LinEpi &epi = LinEpi()) {
-  if (R <= kLinSimdRows || l->IT % 2 == 0) {
+  if (R <= kLinSimdRows || (l->IT % 2 == 0 && l->IT >= kLinMmMinSpan)) {
     launch_lin(lin_args(l, R, x, y, epi), s);
     return;
   }

@@ -64,10 +64,11 @@ def test_linear_trunk_shapes(eng, oracle, inp, out, K, R):
 
 @pytest.mark.parametrize("inp,out,K,R", [(2048, 512, 5, 9), (2048, 512, 5, 16), (2048, 512, 5, 32),
                                          (2048, 4096, 6, 16), (4096, 2048, 6, 16), (320, 640, 7, 12), (96, 48, 4, 12),
-                                         (2048, 1024, 8, 16), (2048, 640, 3, 20), (2048, 512, 2, 10), (48, 96, 8, 12)])
+                                         (2048, 1024, 8, 16), (2048, 640, 3, 20), (2048, 512, 2, 10), (48, 96, 8, 12),
+                                         (64, 256, 5, 12), (32, 128, 6, 16)])
 def test_linear_matrix_cores(eng, oracle, inp, out, K, R):
-    """9..32 rows take the grouped matrix-core GEMM (lin_mm; 48 inputs = 3 k tiles, odd, run as groups of 8 rows on
-    the GEMV): same tolerances as the GEMV rows."""
+    """9..32 rows take the grouped matrix-core GEMM (lin_mm; 48 inputs = 3 k tiles, odd, and 64 or 32 inputs, fewer
+    k tiles than its shortest span, run as groups of 8 rows on the GEMV): same tolerances as the GEMV rows."""
     print(f"linear mfma {inp}x{out} K{K} R{R}", flush=True)
     rng = np.random.default_rng(inp * 5 + out + K + R)
     t, su, sv = synth.linear(rng, inp, out, K)
