@@ -770,23 +770,31 @@ __global__ __launch_bounds__(256) void hc_prep(const float *__restrict__ h, cons
   const int ch = blockIdx.x % nch, rs = blockIdx.x / nch, r = rs / kHcStreams, s = rs % kHcStreams;
   const int hcd = kHcStreams * hid, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const float *hr = h + (uint64_t)r * hcd + (uint64_t)s * hid;
-  float ss = 0.f;
-  for (int i0 = 0; i0 < hid; i0 += 256 * 4) {  // four loads in flight per thread
-    float v[4];
-#pragma unroll
-    for (int u = 0; u < 4; u++) {
-      const int i = i0 + 256 * u + threadIdx.x;
-      v[u] = i < hid ? hr[i] : 0.f;
-    }
-#pragma unroll
-    for (int u = 0; u < 4; u++) ss += v[u] * v[u];
-  }
+  // every load first (one round trip): the chunk's h, norm and inject weights, then the stream in batches of 16
   const int i = ch * 256 + threadIdx.x;
   const bool in = i < hid;
-  const float xv = in ? hr[i] * epi_bf(nw[s * hid + i]) : 0.f;
+  const int ic = in ? i : 0;
+  const float hv = hr[ic], wv = epi_bf(nw[s * hid + ic]);
+  uint16_t iwv[4];
+#pragma unroll
+  for (int k = 0; k < 4; k++) iwv[k] = iw[(uint64_t)k * hcd + s * hid + ic];
+  float ss = 0.f;
+  constexpr int B = 16;
+  for (int i0 = 0; i0 < hid; i0 += 256 * B) {
+    float v[B];
+#pragma unroll
+    for (int u = 0; u < B; u++) {
+      const int j = i0 + 256 * u + threadIdx.x;
+      v[u] = hr[j < hid ? j : 0];
+    }
+#pragma unroll
+    for (int u = 0; u < B; u++)
+      if (i0 + 256 * u + (int)threadIdx.x < hid) ss += v[u] * v[u];
+  }
+  const float xv = in ? hv * wv : 0.f;
   float t[5] = {ss, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int k = 0; k < 4; k++) t[1 + k] = in ? epi_bf(iw[(uint64_t)k * hcd + s * hid + i]) * xv : 0.f;
+  for (int k = 0; k < 4; k++) t[1 + k] = in ? epi_bf(iwv[k]) * xv : 0.f;
 #pragma unroll
   for (int k = 0; k < 5; k++)
     for (int o = 32; o >= 1; o >>= 1) t[k] += __shfl_xor(t[k], o, 64);
