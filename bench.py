@@ -143,8 +143,8 @@ def measure_trunk(eng, R, steps, seed, min_bytes=300e6):
 
 
 def measure_hc_read(eng, R, steps, seed, hid=2560, lr=320, K=6):
-    """The hyper-connection read (ne_hc_read: prep, down linear + silu epilogue, up linear, output) at R rows on
-    synthetic EXL3 mixes of the reference shape. GPU time per call from HIP events around its four launches, averaged
+    """The hyper-connection read (ne_hc_read: prep, down linear + silu epilogue, up linear + output epilogue) at R rows on
+    synthetic EXL3 mixes of the reference shape. GPU time per call from HIP events around its three launches, averaged
     over calls on the same weights (4.9 MB: they stay in the last-level cache between calls)."""
     from ijah_amd import synth
     from ijah_amd.engine import hc_read
@@ -158,7 +158,7 @@ def measure_hc_read(eng, R, steps, seed, hid=2560, lr=320, K=6):
         hc_read(ld, lu, R, h, nw, iw, mix, inj, out)
     ms = [hc_read(ld, lu, R, h, nw, iw, mix, inj, out, timed=True) for _ in range(max(10, steps))]
     res = {"rows": R, "hid": hid, "mix_rows": lr, "K": K, "us": round(1e3 * float(np.median(ms)), 3),
-           "launches": 4}
+           "launches": 3}
     ld.free()
     lu.free()
     print(f"hc read R={R}: {res}", file=sys.stderr, flush=True)

@@ -315,24 +315,40 @@ NE_API int ne_hc_read(ne_exl3_lin *down, ne_exl3_lin *up, int R, const ne_buf *h
     IJ_CHECK(mix->size >= (uint64_t)R * lr * 4, "mix buffer too small for [%d][%d] f32", R, lr);
     IJ_CHECK(inj->size >= (uint64_t)R * 8 * 4, "inj buffer too small for [%d][8] f32", R);
     IJ_CHECK(out->size >= (uint64_t)R * hid * 4, "out buffer too small for [%d][%d] f32", R, hid);
+    IJ_CHECK(hid % 128 == 0, "hid %d must be a multiple of 128", hid);
+    const int nbs = hid / 128;
     if (R > up->hc_rows) {
       dev_free(up->hc_scr);
-      up->hc_scr = dev_alloc<float>((size_t)kLinMaxRows * (2 * (size_t)hcd + 16 * (size_t)((hid + 255) / 256)));
+      const size_t nctr = (size_t)(1 + kLinMaxRows) * nbs * kSyncStride;
+      up->hc_scr = dev_alloc<float>((size_t)kLinMaxRows * (2 * (size_t)hcd + 16 * (size_t)((hid + 255) / 256)) + nctr);
       up->hc_rows = kLinMaxRows;
+      float *c0 = up->hc_scr + (size_t)kLinMaxRows * (2 * (size_t)hcd + 16 * (size_t)((hid + 255) / 256));
+      IJ_HIP(hipMemset(c0, 0, nctr * 4));  // the output counters (each reset by its last arrival)
     }
     float *xn = up->hc_scr, *u = xn + (size_t)kLinMaxRows * hcd, *ip = u + (size_t)kLinMaxRows * hcd;
+    uint32_t *ctr = (uint32_t *)(up->hc_scr + (size_t)kLinMaxRows * (2 * (size_t)hcd + 16 * (size_t)((hid + 255) / 256)));
     const float *hp = (const float *)h->dev;
     const uint16_t *nw = (const uint16_t *)hc_norm->dev;
     float *injp = (float *)inj->dev;
     LinEpi act;  // the down linear's epilogue: mix = rr(silu(rr(v) / 4))
     act.kind = 2;
     act.refr = refr ? 1 : 0;
+    LinEpi fin;  // the up linear's: u to scratch, then the output columns and gates (kind 8)
+    fin.kind = 8;
+    fin.refr = act.refr;
+    fin.hid = hid;
+    fin.e0 = u;
+    fin.e1 = const_cast<float *>(hp);
+    fin.e2 = (float *)out->dev;
+    fin.e3 = ip;
+    fin.e4 = injp;
+    fin.w16 = nw;
+    fin.ctr = ctr;
     timed(stream(), gpu_ms, [&] {
       hipStream_t s = stream();
       launch_hc_prep(hp, nw, (const uint16_t *)inject->dev, xn, ip, injp, R, hid, s);
       lin_launch(down, R, xn, (float *)mix->dev, s, act);
-      lin_launch(up, R, (const float *)mix->dev, u, s);
-      launch_hc_out(u, hp, nw, ip, injp, (float *)out->dev, R, hid, refr ? 1 : 0, s);
+      lin_launch(up, R, (const float *)mix->dev, u, s, fin);
     });
   });
 }

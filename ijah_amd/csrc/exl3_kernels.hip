@@ -519,6 +519,7 @@ __device__ __forceinline__ void lin_store(const LinArgs &a, int r, int c, float 
       *y = expf(-ex * sp);
       break;
     }
+    case 8: st_cg(e.e0 + (uint64_t)R * a.out + c, v); break;
     case 7:
       *y = v;
       if (c >= 512) {
@@ -528,6 +529,46 @@ __device__ __forceinline__ void lin_store(const LinArgs &a, int r, int c, float 
       break;
     default: *y = v;
   }
+}
+
+// The HC read's output step fused into the up linear's finisher (LinEpi kind 8; reference
+// kernels/trunk6/t6_epi.metal:80-97 for the arithmetic): row r (global), column cc of the hid outputs, from the four
+// streams' u (coherent loads: other workgroups stored them)
+__device__ __forceinline__ void hc_fin_col(const LinArgs &a, int r, int cc) {
+  const LinEpi &e = a.epi;
+  const int hid = e.hid, q = e.refr;
+  float v[4];
+#pragma unroll
+  for (int st = 0; st < 4; st++) {
+    const uint64_t row = (uint64_t)st * hid + cc;
+    const float u = ld_cg(e.e0 + (uint64_t)r * a.out + row), inv = e.e4[r * 8 + 4 + st];
+    const float sg = epi_rr(1.f / (1.f + expf(-epi_rr(u, q))), q);
+    v[st] = epi_rr(sg * epi_rr(e.e1[(uint64_t)r * a.out + row] * inv * epi_bf(e.w16[row]), q), q);
+  }
+  e.e2[(uint64_t)r * hid + cc] = epi_rr(((v[0] + v[1]) + (v[2] + v[3])) * 0.25f, q);
+}
+// the row's four inject gates from the prep's partials, on one whole wave (lane = (chunk phase, stream, gate))
+__device__ __forceinline__ void hc_fin_gates(const LinArgs &a, int r, int lane) {
+  const LinEpi &e = a.epi;
+  const int nch = (e.hid + 255) / 256, j = lane & 3, st = (lane >> 2) & 3, ph = lane >> 4;
+  float t = 0.f;
+  for (int ch = ph; ch < nch; ch += 4) t += e.e3[((r * 4 + st) * nch + ch) * 4 + j];
+  t += __shfl_xor(t, 16, 64);  // the chunk phases
+  t += __shfl_xor(t, 32, 64);
+  t += __shfl_xor(t, 4, 64);   // the streams
+  t += __shfl_xor(t, 8, 64);
+  if (lane < 4) e.e4[r * 8 + lane] = epi_rr(2.f / (1.f + expf(-epi_rr(t, e.refr) * 0.25f)), e.refr);
+}
+// after a finisher stored u for rows [r0, r1) of 128-column block cb: the last of the four streams' blocks of those
+// columns (counter ctr, reset by it) writes their outputs; the first column block's last arrival also the gates
+__device__ void hc_fin_block(const LinArgs &a, uint32_t *ctr, int r0, int r1, int cb, int *flag) {
+  const int nbs = a.epi.hid / 128, cs = cb % nbs, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nw = (int)(blockDim.x >> 6);
+  if (block_signal(ctr, flag) != 3u) return;
+  if (threadIdx.x == 0) st_cg(ctr, 0u);
+  for (int i = threadIdx.x; i < (r1 - r0) * 128; i += blockDim.x) hc_fin_col(a, r0 + i / 128, cs * 128 + i % 128);
+  if (cs == 0)
+    for (int r = r0 + wave; r < r1; r += nw) hc_fin_gates(a, r, lane);
 }
 
 // lin_prep: xh[r][kp(i)] = fp16(H_in(x * suh)) (reference kernels/trunk6/trunk6.metal:68-85), grid R x ceil(in/128).
@@ -719,11 +760,15 @@ __global__ __launch_bounds__(256) void lin_step(LinArgs a) {
     if (m0) lin_store(a, r, i0, v0 * h2f(a.svh[i0]));
     if (m1) lin_store(a, r, i1, v1 * h2f(a.svh[i1]));
   }
+  if (a.epi.kind == 8)
+    hc_fin_block(a, a.epi.ctr + (uint64_t)(cb % (a.epi.hid / 128)) * kSyncStride, a.epi.row0, a.epi.row0 + a.R, cb,
+                 &flag);
 }
 
 // lin_finish: y = H_out(sum over splits in order) * svh (reference kernels/trunk6/trunk6.metal:199-214),
 // grid R x ceil(out/128).
 __global__ __launch_bounds__(64) void lin_finish(LinArgs a) {
+  __shared__ int flag;
   const int nch = (a.out + 127) / 128;
   const int r = blockIdx.x / nch, c = blockIdx.x % nch, lane = threadIdx.x;
   const int OTp = a.OT + (a.OT & 1);
@@ -752,6 +797,10 @@ __global__ __launch_bounds__(64) void lin_finish(LinArgs a) {
   fwht2(v0, v1, lane, a.had_out, a.sc_out);
   if (m0) lin_store(a, r, i0, v0 * h2f(a.svh[i0]));
   if (m1) lin_store(a, r, i1, v1 * h2f(a.svh[i1]));
+  if (a.epi.kind == 8) {
+    const int nbs = a.epi.hid / 128, rg = a.epi.row0 + r;
+    hc_fin_block(a, a.epi.ctr + (uint64_t)(nbs + rg * nbs + c % nbs) * kSyncStride, rg, rg + 1, c, &flag);
+  }
 }
 
 // ------------------------------------------------------------------------------------------------ HC read
@@ -809,43 +858,10 @@ __global__ __launch_bounds__(256) void hc_prep(const float *__restrict__ h, cons
   if (threadIdx.x == 0 && ch == 0) inj[r * 8 + kHcStreams + s] = inv;
 }
 
-// one thread per (row, column) (reference t6e_hc_out, :80-97, and t6e_hc_act's gates, :53-78)
-__global__ __launch_bounds__(256) void hc_out(const float *__restrict__ u, const float *__restrict__ h,
-                                              const uint16_t *__restrict__ nw, const float *__restrict__ ip,
-                                              float *__restrict__ inj, float *__restrict__ out, int R, int hid,
-                                              int refr) {
-  const int g = blockIdx.x * 256 + threadIdx.x;
-  if (g >= R * hid) return;
-  const int r = g / hid, c = g % hid, hcd = kHcStreams * hid;
-  float v[kHcStreams];
-#pragma unroll
-  for (int s = 0; s < kHcStreams; s++) {
-    const uint64_t row = (uint64_t)s * hid + c;
-    const float inv = inj[r * 8 + kHcStreams + s];
-    const float sg = epi_rr(1.f / (1.f + expf(-epi_rr(u[(uint64_t)r * hcd + row], refr))), refr);
-    v[s] = epi_rr(sg * epi_rr(h[(uint64_t)r * hcd + row] * inv * epi_bf(nw[row]), refr), refr);
-  }
-  out[(uint64_t)r * hid + c] = epi_rr(((v[0] + v[1]) + (v[2] + v[3])) * 0.25f, refr);
-  if (c < 64) {  // one whole wave (hid % 64 == 0): the row's 4 gates from the inject partials, lane = (phase, s, j)
-    const int nch = (hid + 255) / 256, j = c & 3, st = (c >> 2) & 3, ph = c >> 4;
-    float t = 0.f;
-    for (int ch = ph; ch < nch; ch += 4) t += ip[((r * kHcStreams + st) * nch + ch) * 4 + j];
-    t += __shfl_xor(t, 16, 64);  // the chunk phases
-    t += __shfl_xor(t, 32, 64);
-    t += __shfl_xor(t, 4, 64);   // the streams
-    t += __shfl_xor(t, 8, 64);
-    if (c < 4) inj[r * 8 + c] = epi_rr(2.f / (1.f + expf(-epi_rr(t, refr) * 0.25f)), refr);
-  }
-}
-
 void launch_hc_prep(const float *h, const uint16_t *nw, const uint16_t *iw, float *xn, float *ip, float *inj, int R,
                     int hid, hipStream_t s) {
   hipLaunchKernelGGL(hc_prep, dim3(R * kHcStreams * ((hid + 255) / 256)), dim3(256), 0, s, h, nw, iw, xn, ip, inj,
                      hid);
-}
-void launch_hc_out(const float *u, const float *h, const uint16_t *nw, const float *ip, float *inj, float *out, int R,
-                   int hid, int refr, hipStream_t s) {
-  hipLaunchKernelGGL(hc_out, dim3((R * hid + 255) / 256), dim3(256), 0, s, u, h, nw, ip, inj, out, R, hid, refr);
 }
 
 // ------------------------------------------------------------------------------------------------ decode

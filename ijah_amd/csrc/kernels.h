@@ -114,9 +114,15 @@ enum { kSyncErrWord = 3 * kSyncStride };
 // bf16 [out]); 7 y = v, and for c >= 512 e0[(T + r) 128 + c - 512] = v (e0 f32 cache rows of 128, e1 u32 [1] = T).
 // y rows are ldy floats apart; row0 = the launch's first row among the caller's (row-grouped launches); cap = e0's
 // rows of 128 for kind 7 (cache rows at or beyond it are not written).
+// Kind 8 (internal to the HC read, reference trunk6.metal:223-258 t6_hc_out fused into the up linear's finisher):
+// u is stored to e0 [R][4 hid] and counted per 128-column block of a stream (ctr); the last of the four streams'
+// blocks writes out e2 [R][hid] from u, h (e1), the norm (w16) and inv (e4 [R][8] + 4), and, for the first block,
+// the gates e4[r][0..3] from the inject partials e3 [R][4][hid / 256][4].
 struct LinEpi {
-  int kind = 0, refr = 1, hc = 4, ldy = 0, row0 = 0, cap = 0;
-  float *e0 = nullptr, *e1 = nullptr, *e2 = nullptr;
+  int kind = 0, refr = 1, hc = 4, ldy = 0, row0 = 0, cap = 0, hid = 0;
+  float *e0 = nullptr, *e1 = nullptr, *e2 = nullptr, *e3 = nullptr, *e4 = nullptr;
+  const uint16_t *w16 = nullptr;
+  uint32_t *ctr = nullptr;  // kind 8: [hid / 128] (one-launch finisher), then [R][hid / 128], kSyncStride apart
 };
 struct LinArgs {
   const uint32_t *tiles;  // re-laid trellis
@@ -141,12 +147,10 @@ void launch_lin(const LinArgs &a, hipStream_t s);
 // The hyper-connection read around its two EXL3 linears (reference models/flash_next/layer_t6.mm:89-133, t6_hc_read,
 // with kernels/trunk6/t6_epi.metal:16-97): h f32 [R][4][hid], hc_norm bf16 [4 hid], inject bf16 [4][4 hid].
 // hc_prep: xn [R][4 hid] = h w inv_s (inv_s = 1/rms of stream s), ip [R][4 streams][ceil(hid / 256) chunks][4
-// gates] = the inject dots of h w over each chunk (times inv_s), inj[r][4 + s] = inv_s. hc_out (after the up linear's u [R][4 hid]): out [R][hid] and the gates
-// inj[r][j < 4] = rr(2 sigmoid(rr(sum_s ip[r][s][j]) / 4)).
+// gates] = the inject dots of h w over each chunk (times inv_s), inj[r][4 + s] = inv_s. The up linear's finisher
+// (LinEpi kind 8) then writes out [R][hid] and the gates inj[r][j < 4] = rr(2 sigmoid(rr(sum_s ip[r][s][j]) / 4)).
 void launch_hc_prep(const float *h, const uint16_t *nw, const uint16_t *iw, float *xn, float *ip, float *inj, int R,
                     int hid, hipStream_t s);
-void launch_hc_out(const float *u, const float *h, const uint16_t *nw, const float *ip, float *inj, float *out, int R,
-                   int hid, int refr, hipStream_t s);
 void launch_lin_mm(const LinArgs &a, hipStream_t s);  // rows kLinSimdRows+1 .. kLinMaxRows (matrix cores)
 // W' fp16 bits [IT*16][OT*16] from re-laid tiles
 void launch_decode(const uint32_t *tiles, int IT, int OT, int K, uint16_t *w, hipStream_t s);

@@ -62,7 +62,8 @@ NE_API int ne_exl3_lin_run(ne_exl3_lin *l, int R, const ne_buf *x, uint64_t x_of
  *              bf16 [out]; the reference's gb [R][96]: ldy = 96)
  *   7 iqk      y = v; for c >= 512, e0[(T + r) 128 + c - 512] = v (e0 f32 key cache of rows of 128, e1 u32 [1] = T;
  *              rows T + r beyond e0's size are not written)
- * Kinds 4 (GDN conv1d with state) and 8 (the HC read fused through counters) are not provided. ldy = y's row stride
+ * Kind 4 (GDN conv1d with state) is not provided; kind 8 (the HC read's output step, through counters) runs inside
+ * ne_hc_read only. ldy = y's row stride
  * in floats (0: out). */
 typedef struct ne_exl3_epi {
   int kind, refr, hc, ldy;
