@@ -276,3 +276,31 @@ def test_moe_hc_rejects(eng, oracle):
         moe.run_hc(2, x, y, h, inj, h, hc=5)
     with pytest.raises(RuntimeError, match="inj missing or under"):
         moe.run_hc(2, x, y, h, eng.alloc(16), h, hc=4)
+
+
+def test_hc_read_then_moe_hc_write(eng, oracle):
+    """The reference's MLP block order (models/flash_next/layer_t6.mm:141-144, then kernels/fn_moe.metal:437-448): the
+    HC read's out and inj buffers feed ne_moe_run_hc directly. Against the oracle layer with the write run on the
+    GPU read's own outputs (the read itself is checked against the oracle in test_hc_read)."""
+    from ijah_amd.engine import hc_read
+    print("hc read -> moe hc write, hid 1024", flush=True)
+    hid, R = 1024, 3
+    rng = np.random.default_rng(97)
+    w = synth.moe_layer(97, hid=hid, inter=256, ne=16, topk=4, K=5, shared=True, Ks=6, sgate=True)
+    W = oracle.MoeWeights(w)
+    moe = eng.moe_create(w)
+    h = (rng.standard_normal((R, 4, hid)) * np.array([0.5, 1, 2, 4])[None, :, None]).astype(np.float32)
+    nw = synth.bf16((1 + 0.1 * rng.standard_normal(4 * hid)).astype(np.float32))
+    iw = synth.bf16((rng.standard_normal((4, 4 * hid)) / np.sqrt(4 * hid)).astype(np.float32))
+    ld, lu = eng.exl3_linear(*synth.linear(rng, 4 * hid, 128, 6)), eng.exl3_linear(*synth.linear(rng, 128, 4 * hid, 6))
+    hb = eng.from_numpy(h)
+    mb, jb, xb = eng.alloc(R * 128 * 4), eng.alloc(R * 32), eng.alloc(R * hid * 4)
+    hc_read(ld, lu, R, hb, eng.from_numpy(nw), eng.from_numpy(iw), mb, jb, xb)
+    yb, ob = eng.alloc(R * hid * 4), eng.alloc(h.nbytes)
+    moe.run_hc(R, xb, yb, hb, jb, ob, hc=4)
+    x, inj = xb.download(np.float32, (R, hid)), jb.download(np.float32, (R, 8))
+    y, hout = yb.download(np.float32, (R, hid)), ob.download(np.float32, h.shape)
+    want_y, want_o = oracle.moe_layer_hc(W, x, h, inj, refr=True)
+    for g, wv in ((y, want_y), (hout, want_o)):
+        assert (g == wv).mean() > 0.97 and rel(g, wv) < 3e-3
+    assert np.all(np.abs(inj[:, :4]) <= 2) and np.all(inj[:, 4:] > 0)  # gates 2 sigmoid, 1/rms
