@@ -61,6 +61,7 @@ struct ne_exl3_lin {
   bool one_launch = true;  // IJAH_LIN_PATH=staged at creation: prep, GEMV and finish as three launches
   int mm_min_kt = 8;       // the same for the matrix-core path (IJAH_LIN_MM_MINKT at creation, at least
                            // kLinMmMinSpan): 8 beats 16 (q + k + v + o at 16 rows 50 vs 57 us)
+  int lin_wg_target = 512; // the GEMV's split count stops once tile pairs x splits reach this (IJAH_LIN_WGS)
   int min_kt = 16;         // fewest k tiles per split on the GEMV path (IJAH_LIN_MINKT at creation): 16 beats 8
                            // (k / v 2048 -> 512: 6.1 vs 6.5 us; more splits cost more in the finisher's sums)
   int part_S = 0;
@@ -75,7 +76,7 @@ struct ne_exl3_lin {
     dev_free(part);
     dev_free(cnt);
   }
-  // k splits: smallest S (dividing IT, >= min_kt k tiles per split) that gives >= 1024 workgroups, then enough to keep
+  // k splits: smallest S (dividing IT, >= min_kt k tiles per split) that gives >= lin_wg_target workgroups, then enough to keep
   // the staged input within 32 KiB of LDS at R rows
   int splits(int R) const {
     const int NP = OTp / 2;
@@ -84,7 +85,7 @@ struct ne_exl3_lin {
       while ((NP + 7) / 8 * S < 512 && IT % (2 * S) == 0 && IT / (2 * S) >= mm_min_kt) S *= 2;
       return S;
     }
-    while (NP * S < 1024 && IT % (2 * S) == 0 && IT / (2 * S) >= min_kt) S *= 2;
+    while (NP * S < lin_wg_target && IT % (2 * S) == 0 && IT / (2 * S) >= min_kt) S *= 2;
     const int RT = R <= 1 ? 1 : R <= 2 ? 2 : R <= 4 ? 4 : 8;
     while ((size_t)RT * (IT / S) * 32 > 32768 && IT % (2 * S) == 0) S *= 2;
     return S;
@@ -121,6 +122,7 @@ static ne_exl3_lin *lin_create(const uint16_t *trellis, const uint16_t *suh, con
   const char *path = getenv("IJAH_LIN_PATH");
   l->one_launch = !(path && std::string(path) == "staged");
   if (const char *e = getenv("IJAH_LIN_MINKT")) l->min_kt = std::min(64, std::max(4, atoi(e)));
+  if (const char *e = getenv("IJAH_LIN_WGS")) l->lin_wg_target = std::min(8192, std::max(64, atoi(e)));
   if (const char *e = getenv("IJAH_LIN_MM_MINKT")) l->mm_min_kt = std::min(64, std::max(kLinMmMinSpan, atoi(e)));
   return l.release();
 }
