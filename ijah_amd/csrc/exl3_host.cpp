@@ -81,8 +81,9 @@ struct ne_exl3_lin {
   int splits(int R) const {
     const int NP = OTp / 2;
     int S = 1;
-    if (R > kLinSimdRows) {  // matrix cores: 8 pairs per workgroup, >= 512 workgroups, >= 16 k tiles per split
-      while ((NP + 7) / 8 * S < 512 && IT % (2 * S) == 0 && IT / (2 * S) >= mm_min_kt) S *= 2;
+    if (R > kLinSimdRows) {  // matrix cores: 8 pairs per workgroup, >= 512 workgroups, >= mm_min_kt k tiles per
+                             // split; the span IT / S must stay even (the GEMM runs it as steps of two k tiles)
+      while ((NP + 7) / 8 * S < 512 && IT % (4 * S) == 0 && IT / (2 * S) >= mm_min_kt) S *= 2;
       return S;
     }
     while (NP * S < lin_wg_target && IT % (2 * S) == 0 && IT / (2 * S) >= min_kt) S *= 2;

@@ -140,9 +140,9 @@ struct LinArgs {
 };
 // rows up to kLinSimdRows take the VALU GEMV (lin_gemv), more rows (up to kLinMaxRows) the matrix cores (lin_mm)
 constexpr int kLinSimdRows = 8, kLinMaxRows = 32;
-// fewest k tiles per split of the matrix-core linear: 4-tile spans (two pipeline steps) gave wrong sums on the GPU
-// and are never launched; spans of 6 and more pass the parity tests
-constexpr int kLinMmMinSpan = 8;
+// fewest k tiles per split of the matrix-core linear (one pipeline step of two tiles); the default split stops at 8
+// (a performance choice, IJAH_LIN_MM_MINKT overrides it at creation)
+constexpr int kLinMmMinSpan = 2;
 void launch_lin(const LinArgs &a, hipStream_t s);
 // The hyper-connection read around its two EXL3 linears (reference models/flash_next/layer_t6.mm:89-133, t6_hc_read,
 // with kernels/trunk6/t6_epi.metal:16-97): h f32 [R][4][hid], hc_norm bf16 [4 hid], inject bf16 [4][4 hid].

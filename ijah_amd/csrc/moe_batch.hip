@@ -1166,6 +1166,9 @@ static void lin_mm_launch(const LinArgs &a, hipStream_t s) {
   hipLaunchKernelGGL(lin_mm<K>, dim3(NG * a.S), dim3(64 * kWavesG), lds, s, a);
 }
 void launch_lin_mm(const LinArgs &a, hipStream_t s) {
+  // chunk_gemm runs a split's k span as steps of two k tiles: an odd span would drop its last tile
+  IJ_CHECK(a.S >= 1 && a.IT % a.S == 0 && (a.IT / a.S) % 2 == 0, "lin_mm: k span %d / %d not an even tile count",
+           a.IT, a.S);
   switch (a.K) {
     case 2: lin_mm_launch<2>(a, s); break;
     case 3: lin_mm_launch<3>(a, s); break;

@@ -82,6 +82,24 @@ def test_linear_matrix_cores(eng, oracle, inp, out, K, R):
     assert rel(y1, y[:1]) < 5e-5
 
 
+@pytest.mark.parametrize("minkt", [2, 4])
+@pytest.mark.parametrize("inp,out,K,R", [(320, 640, 7, 12), (288, 640, 5, 12), (576, 640, 6, 16), (352, 640, 5, 16),
+                                         (2048, 512, 5, 16), (128, 256, 4, 9), (256, 2048, 6, 24)])
+def test_linear_matrix_cores_short_spans(eng, oracle, inp, out, K, R, minkt, monkeypatch):
+    """The matrix-core GEMM with its k split allowed down to 2- and 4-tile spans (IJAH_LIN_MM_MINKT): every span must
+    stay an even tile count (the GEMM's steps take two tiles), including in = 288 / 352 / 576, whose halvings reach
+    odd spans (9, 11, 9) if the split does not stop first."""
+    print(f"linear mfma short spans {inp}x{out} K{K} R{R} minkt {minkt}", flush=True)
+    monkeypatch.setenv("IJAH_LIN_MM_MINKT", str(minkt))
+    rng = np.random.default_rng(inp * 3 + out + K + R + minkt)
+    t, su, sv = synth.linear(rng, inp, out, K)
+    x = synth.bf16_values(rng, R, inp)
+    lin = eng.exl3_linear(t, su, sv)
+    y = lin.run(x)
+    assert rel(y, oracle.exl3_linear(x, t, su, sv)) < 5e-5
+    assert rel(y, oracle.exl3_linear(x, t, su, sv, exact=True)) < 1e-2
+
+
 @pytest.mark.parametrize("inp,out,K,R", [(2048, 512, 5, 1), (2048, 4096, 6, 3), (320, 640, 7, 8), (96, 48, 4, 2)])
 def test_linear_one_launch_matches_staged(eng, oracle, inp, out, K, R, monkeypatch):
     """The one-launch linear (in-workgroup prep, last-arriver finish) against the three-launch path: bit-identical
