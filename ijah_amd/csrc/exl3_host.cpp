@@ -423,8 +423,9 @@ struct ne_moe {
   float *logits = nullptr, *sgv = nullptr, *guo = nullptr, *dn = nullptr;
   uint16_t *hprep = nullptr;
   uint32_t *route = nullptr, *sync = nullptr, *plan = nullptr;
-  float *part = nullptr;
-  uint32_t *fsync = nullptr;  // the fused step's counters
+  float *part = nullptr;      // the fused step's tagged partials
+  size_t part_floats = 0;
+  uint32_t *fsync = nullptr;  // the fused step's launch epoch
   int plan_grid = 0;  // fused step: its grid (0: no plan, the staged path runs)
   MoeBatchBufs bat;   // batched path (R >= 2)
   int bat_R = 0;      // rows the batched buffers hold
@@ -480,6 +481,8 @@ struct ne_moe {
         plan = dev_alloc<uint32_t>(pl.words.size());
         IJ_HIP(hipMemcpy(plan, pl.words.data(), pl.words.size() * 4, hipMemcpyHostToDevice));
         part = dev_alloc<float>(pl.part_floats);
+        part_floats = pl.part_floats;
+        IJ_HIP(hipMemset(part, 0, sizeof(float) * pl.part_floats));  // tagged partials: tag 0 is never a launch's
         fsync = dev_alloc<uint32_t>(moe_fused_sync_words(nslot(), hid, inter));
         IJ_HIP(hipMemset(fsync, 0, 4 * moe_fused_sync_words(nslot(), hid, inter)));
         plan_grid = pl.grid;
@@ -525,6 +528,8 @@ struct ne_moe {
     a.dn = dn;
     a.sync = sync;
     a.trace = trace;
+    if (trace)
+      if (const char *e = getenv("IJAH_MOE_DBG")) a.dbg = atoi(e);
     a.hprep = hprep;
     a.units = plan;
     a.part = part;
@@ -540,6 +545,7 @@ struct ne_moe {
       IJ_HIP(hipMemsetAsync(sync, 0, 4 * sync_words(Rcap, nslot(), hid, inter), s));
       IJ_HIP(hipMemsetAsync(logits, 0, sizeof(float) * logit_floats(Rcap), s));  // launch tags restart with the epoch
       if (fsync) IJ_HIP(hipMemsetAsync(fsync, 0, 4 * moe_fused_sync_words(nslot(), hid, inter), s));
+      if (part) IJ_HIP(hipMemsetAsync(part, 0, sizeof(float) * part_floats, s));  // the epoch restarts: no stale tags
       IJ_HIP(hipStreamSynchronize(s));
       throw Error("moe: a cross-workgroup wait timed out (layer output invalid)");
     }

@@ -48,7 +48,8 @@ struct MoeArgs {
   float *guo;                          // [R nslot][2][ksplit][inter]
   float *dn;                           // [R nslot][hid]
   uint32_t *sync;                      // counters: see sync_words(); zero between launches (kernels reset them)
-  uint64_t *trace;                     // fused kernel: per unit {grab, ready, done} wall-clock ticks, or null
+  uint64_t *trace;                     // fused kernel: per-wave wall-clock stamps of its phases, or null
+  int dbg = 0;                         // fused kernel, with trace only: timing experiments (IJAH_MOE_DBG)
   uint16_t *hprep;                     // fused kernel: [R nslot][inter] fp16 down inputs (kp order)
   const uint32_t *units;               // fused kernel: the plan words (MoePlan::words) in device memory
   float *part;                         // fused kernel: column partial sums (MoePlan::part_floats)
@@ -96,7 +97,7 @@ int moe_batch_max_chunks(int R, int ne, int topk, bool shared);
 void launch_moe_batch(const MoeArgs &a, const MoeBatchBufs &b, hipStream_t s);
 // Fused step logits: kLogitReplicas copies of [ne + 1] floats, moe_logit_stride(ne) floats apart (replica 0 is the
 // [R = 1][ne + 1] logits buffer the staged path uses); the copies spread the workgroups' polling over memory channels.
-constexpr int kLogitReplicas = 8;
+constexpr int kLogitReplicas = 32;
 __host__ __device__ inline int moe_logit_stride(int ne) { return (ne + 1 + 63) / 64 * 64 + 1024; }
 // The sync block for R rows: header counters, per-slot gate/up counters, per-(row, 128-column block) counters; every
 // counter sits alone in a 256-byte line so that polling workgroups do not contend on one line.

@@ -2,22 +2,24 @@
 // experts' gate/up and down EXL3 GEMVs with SwiGLU, and the weighted combine (reference kernels/fn_moe.metal:26-452,
 // driven by models/flash_next/layer.mm:532-568).
 //
-// One 16-wave workgroup per CU. Every wave of the grid gets, from a host-built plan, an equal slice of the layer's
-// gate/up work and of its down work: consecutive k tiles of output tile pairs ("columns"), at most two segments each.
-// The step:
-//   1. router: wave w of workgroup b computes router row b + G w and stores its bf16 logit with this launch's tag in
-//      the (always zero) low 16 bits; waves whose gate/up slice belongs to the shared expert request its tiles.
-//   2. route: one wave of every workgroup waits until all logits carry the tag and ranks them itself (no exchange).
-//   3. gate/up: each wave streams its slice's tiles into its own LDS area (global_load_lds), prepares the input
-//      chunks it needs (x * suh, Hadamard, fp16), decodes and multiplies, and stores one partial per column segment.
-//      Per (slot, 128-column block) a counter collects the partials; the workgroup that completes it sums them in
-//      segment order and applies the down prologue (H, svh, SwiGLU, suh_d, H) into fp16 `hprep`.
-//   4. down: each wave streams and decodes its down slice into registers while the gate/up blocks finish, waits for
-//      its slot's blocks, multiplies, and stores its partials; the workgroup completing a 128-column block of the
-//      output combines it: per slot the partials in segment order, H, svh and the route weight, slots in slot order.
-// Cross-workgroup data moves through coherent (sc1) stores and loads; counters are single atomics per workgroup and
-// target; every wait is bounded and raises the error word. The last workgroup out resets the counters and advances
-// the launch epoch. All workgroups must be resident together (grid = CU count, one workgroup per CU).
+// One 16-wave workgroup per CU, all resident. Data moves between workgroups only as tagged values: a u64 holding
+// the f32 value and the launch's 32-bit tag (router logits carry a 16-bit tag in their zero low bits), stored and
+// polled with device-coherent (sc1) accesses. A consumer sees the data itself arrive, so a hand-off costs one store's
+// visibility (~0.45 us between XCDs), with no counters, atomics or store-completion waits in between.
+//
+// Work (a host-built plan; slots in plan order: the shared expert first, then the routed slots):
+//   gate/up  rows (matrix m = 2 slot + proj, group g of 4 tile-pair columns, k tile), 4 tile pairs each. Workgroup b
+//            takes an equal run of the routed rows (waves: pair w & 3, a quarter w >> 2 of the run's k range) and the
+//            waves' products are summed in LDS: one partial per (column, workgroup run), `jj` numbering the runs of a
+//            column in k order. The shared expert's rows (one pair, 16 k tiles per workgroup at 2048 x 512, one k
+//            tile per wave) are requested at launch and decoded before the route is known.
+//   down     units (slot, 128-wide block cb of the intermediate, 128-column output block c, pair) of 8 k tiles, one
+//            per wave: a workgroup takes an equal run (and a shared unit). It computes the h blocks its units read
+//            (H(g) svh_g, H(u) svh_u, SwiGLU, suh_d, H, fp16) from the gate/up partials itself, then stores one
+//            tagged partial per unit.
+//   combine  16 workgroups, one per 128-column output block: per slot the cb partials in order, H, svh_d, the route
+//            weight; the slots in slot order (the shared one last); the hyper-connection write when asked.
+// The launch tag comes from a u64 epoch that workgroup 0 advances at its end with one store.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -32,39 +34,37 @@ namespace ijah {
 namespace {
 
 constexpr int kWaves = 16;
-// Control wave: the route and the counting run on the last wave, which requests no tiles before the route. Vector
-// memory waits are in order, so a wave with tile streams in flight would wait for them before any load or atomic
-// result of its control duty.
+// Control wave: polls the logits and ranks them. Vector memory waits are in order, so a wave with tile streams in
+// flight would wait for them before its poll results: the control wave requests no tiles before the route.
 constexpr int kCtl = kWaves - 1;
-constexpr int kMaxGu = 12;                 // gate/up k tiles per wave (its LDS area)
-constexpr int kMaxDn = 8;                  // down k tiles per wave (held decoded in registers)
-constexpr int kMaxSeg = 16;                // partial sums per column
-constexpr int kMaxPrep = 8;                 // prepared 128-chunks of input per workgroup (shared by its waves)
+constexpr int kMaxRg = 11;         // routed gate/up tile pairs per wave
+constexpr int kMaxSg = 1;          // shared gate/up tile pairs per wave
+constexpr int kDnKt = 8;           // k tiles of a down unit (one 128-wide h block)
+constexpr int kMaxPrep = 8;        // prepared 128-chunks of the routed rows per workgroup
+constexpr int kMaxSPrep = 2;       // ... of the shared rows
+constexpr int kMaxH = 3;           // h blocks per workgroup (2 loader waves each)
 constexpr int kMaxExpertsV = 1024;
-constexpr int kMaxTopkV = 32;
-constexpr uint32_t kSpin = 1u << 22;       // bounded waits: polls of ~0.1-1 us each, far beyond any real wait
-enum { kWordErr = kSyncErrWord };  // the error word of the layer's sync block (shared with the staged kernels)
-// The fused step's own counters (MoeArgs::fsync), one per 256-byte line, never reset: line 0 holds a u64 count of
-// finished workgroups over all launches, so a launch's epoch e = count / grid; then fin[nslot * NBI] (gate/up
-// partials per (slot, 128-column block)) and blk[NBLK] (slots stored per output block), which grow by the same
-// amount T every launch and are compared as (value - e T) mod 2^32. No workgroup has to reset anything at the end.
+constexpr int kMaxTopkV = 16;      // the combine stages svh_d of every slot in LDS
+constexpr int kPW = 32;            // plan words per workgroup
+constexpr uint32_t kNone = ~0u;
+constexpr uint32_t kSpin = 1u << 22;  // bounded waits: far beyond any real wait
+enum { kWordErr = kSyncErrWord };
+
+// plan word offsets (per workgroup)
+enum {
+  P_R0 = 0, P_R1, P_JJ0, P_JJ1,       // routed gate/up rows [r0, r1); partial index of its first / second column run
+  P_SCOL, P_SK0, P_SN, P_SJJ,         // shared gate/up: column, first k tile, k tiles (one per wave), partial index
+  P_COMB,                              // combine output block, or kNone
+  P_NH, P_HB,                          // h blocks: count, then kMaxH ids (slot * NBI + cb); bit 31: store its g / u sums
+  P_DN = 16                            // per wave: down unit | h slot << 24, or kNone
+};
 
 __device__ __forceinline__ uint32_t ld_relaxed(const uint32_t *p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ void mark(const MoeArgs &a, int field) {
-  if (a.trace && threadIdx.x == 0) a.trace[(uint64_t)blockIdx.x * 8 + field] = wall_clock64();
-}
-// second trace row of the workgroup, written by lane 0 of the calling wave
-__device__ __forceinline__ void mark2(const MoeArgs &a, int field) {
-  if (a.trace && (threadIdx.x & 63) == 0) a.trace[(uint64_t)(256 + blockIdx.x) * 8 + field] = wall_clock64();
-}
-// Workgroup barrier ordering LDS (ds_*) and scalar traffic only. Outstanding vector memory operations, including the
-// wave's LDS-DMA tile streams, stay in flight: __syncthreads() would wait for them (its release fence covers the LDS
-// the DMA writes). Every use here exchanges only ds_write data; each wave waits for its own DMA itself.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-// s_waitcnt vmcnt(n) for a run-time n: at most n vector memory operations of this wave still outstanding (n above 15
-// waits as for 15, which only waits longer). Operation completion is counted in issue order.
+// s_waitcnt vmcnt(n) for a run-time n (n above 15 waits as for 15, which only waits longer); completion is counted
+// in issue order, stores included
 __device__ __forceinline__ void wait_vm(int n) {
   switch (n < 15 ? n : 15) {
 #define IJ_VM(k) \
@@ -74,15 +74,27 @@ __device__ __forceinline__ void wait_vm(int n) {
 #undef IJ_VM
   }
 }
-// global_load_lds instructions a stream of `bytes` issues (one per 1 KB)
 __device__ __forceinline__ int dma_ops(uint32_t bytes) { return (int)((bytes + 1023u) >> 10); }
 constexpr int had_of(int d) { return d % 128 == 0 ? 128 : d % 64 == 0 ? 64 : d % 32 == 0 ? 32 : 16; }
+__device__ __forceinline__ uint32_t rfl(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
 
-struct Seg {  // a segment of a wave's slice: k tiles [k0, k0 + n) of column col; partial jj of that column
-  int col, k0, n, jj;
-};
-__device__ __forceinline__ Seg seg_of(uint32_t d) {
-  return {(int)(d & 0xFFFu), (int)((d >> 12) & 0xFFu), (int)((d >> 20) & 0x7Fu), (int)(d >> 27)};
+// tagged values
+__device__ __forceinline__ void st_tag(uint64_t *p, float v, uint32_t tag) {
+  st_cg(p, (uint64_t)__float_as_uint(v) | ((uint64_t)tag << 32));
+}
+__device__ __forceinline__ float tag_val(uint64_t t) { return __uint_as_float((uint32_t)t); }
+__device__ __forceinline__ bool tag_ok(uint64_t t, uint32_t tag) { return (uint32_t)(t >> 32) == tag; }
+
+__device__ __forceinline__ void stamp_r(const MoeArgs &a, int field) {  // the route's own steps
+  if (a.trace && (threadIdx.x & 63) == 0) a.trace[((uint64_t)4096 + blockIdx.x) * 8 + field] = wall_clock64();
+}
+__device__ __forceinline__ void stamp_w(const MoeArgs &a, int field) {  // per-wave extra stamps
+  if (a.trace && (threadIdx.x & 63) == 0)
+    a.trace[((uint64_t)4096 + 256 + blockIdx.x * kWaves + (threadIdx.x >> 6)) * 8 + field] = wall_clock64();
+}
+__device__ __forceinline__ void stamp(const MoeArgs &a, int field) {
+  if (a.trace && (threadIdx.x & 63) == 0)
+    a.trace[((uint64_t)blockIdx.x * kWaves + (threadIdx.x >> 6)) * 8 + field] = wall_clock64();
 }
 
 struct Route {  // the workgroup's copy of the route of the row
@@ -91,12 +103,11 @@ struct Route {  // the workgroup's copy of the route of the row
   float sg;
 };
 
-// slot order in the plan (ls): the shared expert first (its work needs no route), then the routed slots k = 0..topk-1.
-// Slot index j as the reference numbers it: routed k -> k, shared -> topk.
+// plan slot ls (the shared expert first): the reference's slot index j (routed k -> k, shared -> topk)
+__device__ __forceinline__ bool slot_shared(const MoeArgs &a, int ls) { return a.nslot > a.topk && ls == 0; }
 __device__ __forceinline__ int slot_j(const MoeArgs &a, int ls) {
   return a.nslot > a.topk ? (ls == 0 ? a.topk : ls - 1) : ls;
 }
-__device__ __forceinline__ bool slot_shared(const MoeArgs &a, int ls) { return a.nslot > a.topk && ls == 0; }
 __device__ __forceinline__ const uint8_t *slot_block(const MoeArgs &a, const Route &rt, int ls) {
   if (slot_shared(a, ls)) return a.shared;
   uint32_t e = rt.id[slot_j(a, ls)];
@@ -119,29 +130,38 @@ __device__ __forceinline__ uint64_t sv_off(const MoeArgs &a, int ls, int proj) {
 }
 
 // ---------------------------------------------------------------------------------------------------- router
-// Router row b + G w on wave w (reference kernels/fn_moe.metal:50-67): the bf16 row and x are loaded straight into
-// registers; the logit is rounded to bf16 (the reference rounding), so its low 16 bits are zero and carry the tag.
-// It goes to kLogitReplicas copies (a few KB apart), so that the workgroups polling for the logits spread over as many
-// memory channels instead of all reading the same lines.
+// Router row b + G w on wave w (reference kernels/fn_moe.metal:50-67): the bf16 row and x straight into registers;
+// the logit is rounded to bf16 (the reference rounding), so its low 16 bits are zero and carry the tag. It goes to
+// kLogitReplicas copies so that the polling workgroups spread over memory channels.
 template <int HID>
-__device__ __forceinline__ void router_row(const MoeArgs &a, const uint32_t *tag_lds) {
+struct RouterRow {
+  uint4 wv[HID / 512];
+  float4 x0[HID / 512], x1[HID / 512];
+};
+template <int HID>
+__device__ __forceinline__ bool router_active(const MoeArgs &a) {
+  return (int)blockIdx.x + (int)gridDim.x * (int)(threadIdx.x >> 6) < a.ne + a.has_sgate;
+}
+template <int HID>
+__device__ __forceinline__ void router_load(const MoeArgs &a, RouterRow<HID> &r) {
   constexpr int NC = HID / 512;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int row = (int)blockIdx.x + (int)gridDim.x * wave;
-  const bool active = row < a.ne + a.has_sgate;
-  uint4 wv[NC];
-  float4 x0[NC], x1[NC];
-  if (active) {
-    const uint16_t *w = a.router + (uint64_t)row * HID;
+  const int lane = threadIdx.x & 63;
+  const int row = (int)blockIdx.x + (int)gridDim.x * (int)(threadIdx.x >> 6);
+  const uint16_t *w = a.router + (uint64_t)row * HID;
 #pragma unroll
-    for (int j = 0; j < NC; j++) {
-      wv[j] = *(const uint4 *)(w + j * 512 + lane * 8);
-      x0[j] = *(const float4 *)(a.x + j * 512 + lane * 8);
-      x1[j] = *(const float4 *)(a.x + j * 512 + lane * 8 + 4);
-    }
+  for (int j = 0; j < NC; j++) {
+    r.wv[j] = *(const uint4 *)(w + j * 512 + lane * 8);
+    r.x0[j] = *(const float4 *)(a.x + j * 512 + lane * 8);
+    r.x1[j] = *(const float4 *)(a.x + j * 512 + lane * 8 + 4);
   }
-  lds_barrier();  // the tag (thread 0) is visible after this
-  if (!active) return;
+}
+template <int HID>
+__device__ __forceinline__ void router_finish(const MoeArgs &a, const RouterRow<HID> &r, uint32_t tag16) {
+  constexpr int NC = HID / 512;
+  const int lane = threadIdx.x & 63;
+  const int row = (int)blockIdx.x + (int)gridDim.x * (int)(threadIdx.x >> 6);
+  const uint4 *wv = r.wv;
+  const float4 *x0 = r.x0, *x1 = r.x1;
   float acc = 0.f;
 #pragma unroll
   for (int j = 0; j < NC; j++) {
@@ -156,7 +176,7 @@ __device__ __forceinline__ void router_row(const MoeArgs &a, const uint32_t *tag
   }
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) acc += __shfl_xor(acc, o, 64);
-  const uint32_t v = (__float_as_uint(bf16_round(acc)) & 0xFFFF0000u) | *tag_lds;
+  const uint32_t v = (__float_as_uint(bf16_round(acc)) & 0xFFFF0000u) | tag16;
   const int stride = moe_logit_stride(a.ne);
   if (lane < kLogitReplicas) st_cg((uint32_t *)a.logits + lane * stride + row, v);
 }
@@ -183,36 +203,35 @@ __device__ __forceinline__ void sort_desc(uint32_t (&k)[J]) {
         }
       }
 }
-// The route, by one wave of every workgroup (reference kernels/fn_moe.metal:76-131): waits until every logit carries
-// this launch's tag (bounded), then top-k by logit with ties to the lower index, weights exp(l - l_max) / sum over the
-// top k in f32 summed in slot order, and the shared gate sigmoid(logit). Each lane sorts its J keys once; a round
-// takes the wave max of the lanes' heads and the winning lane shifts its list. A NaN logit ranks as -inf (weight 0).
+// The route, by the control wave of every workgroup (reference kernels/fn_moe.metal:76-131): waits until every logit
+// carries this launch's tag (bounded), then top-k by logit with ties to the lower index, weights exp(l - l_max) / sum
+// over the top k in f32 summed in slot order, and the shared gate. Each lane sorts its J keys once; a round takes the
+// wave max of the lanes' heads and the winning lane shifts its list. A NaN logit ranks as -inf (weight 0).
 // Workgroup 0 also writes the route to the route / shared-gate buffers for the host.
 template <int J>
-__device__ bool route_wave(const MoeArgs &a, Route *rt, uint32_t tag) {
+__device__ bool route_wave(const MoeArgs &a, Route *rt, uint32_t tag16) {
   const int lane = threadIdx.x & 63, n = a.ne + a.has_sgate;
   const uint32_t *lg = (const uint32_t *)a.logits + (blockIdx.x % kLogitReplicas) * moe_logit_stride(a.ne);
   uint32_t v[J + 1];
   bool ok = false;
+  if (a.trace && (a.dbg & 1))  // timing experiment: no polling traffic before ~4 us
+    for (int i = 0; i < 2; i++) __builtin_amdgcn_s_sleep(127);
   for (uint32_t it = 0; it < kSpin; it++) {
     bool mine = true;
 #pragma unroll
     for (int j = 0; j <= J; j++) {
       const int i = j * 64 + lane;
-      v[j] = i < n ? ld_cg(lg + i) : tag;
-      mine = mine && ((v[j] & 0xFFFFu) == tag);
+      v[j] = i < n ? ld_cg(lg + i) : tag16;
+      mine = mine && ((v[j] & 0xFFFFu) == tag16);
     }
     if (__all(mine)) {
       ok = true;
-      if (a.trace && lane == 0) {
-        a.trace[(uint64_t)(5000 + blockIdx.x) * 8] = wall_clock64();
-        a.trace[(uint64_t)(5000 + blockIdx.x) * 8 + 2] = it;
-      }
       break;
     }
     if ((it & 63u) == 63u && ld_relaxed(a.sync + kWordErr)) break;
     __builtin_amdgcn_s_sleep(1);
   }
+  stamp(a, 1);
   if (!ok) {
     if (lane == 0) atomicOr(a.sync + kWordErr, 1u);
     return false;
@@ -223,11 +242,17 @@ __device__ bool route_wave(const MoeArgs &a, Route *rt, uint32_t tag) {
   for (int j = 0; j <= J; j++) {
     const int i = j * 64 + lane;
     const float val = __uint_as_float(v[j] & 0xFFFF0000u);
-    if (j < J) key[j] = i < a.ne ? topk_key(val, i) : 0u;
+    if (j < J) {  // topk_key, branch-free: NaN -> -inf (max), -0 -> +0 (+ 0), then the order transform
+      const uint32_t u = __float_as_uint(fmaxf(val, -INFINITY) + 0.f);
+      const uint32_t k = ((u ^ ((uint32_t)((int)u >> 31) | 0x80000000u)) & 0xFFFF0000u) | (0xFFFFu - (uint32_t)i);
+      key[j] = i < a.ne ? k : 0u;
+    }
     if (i == a.ne) sgl = val;
   }
   sgl = __shfl(sgl, a.ne & 63, 64);
+  stamp_r(a, 0);
   sort_desc<J>(key);
+  stamp_r(a, 1);
   uint32_t mykey = 0u;  // lane t < topk: the t-th largest key
   for (int t = 0; t < a.topk; t++) {
     const uint32_t m = wave_max_u32(key[0]);
@@ -238,7 +263,7 @@ __device__ bool route_wave(const MoeArgs &a, Route *rt, uint32_t tag) {
     key[J - 1] = win ? 0u : key[J - 1];
   }
   const uint32_t id = 0xFFFFu - (mykey & 0xFFFFu);
-  if (a.trace && lane == 0) a.trace[(uint64_t)(5000 + blockIdx.x) * 8 + 1] = wall_clock64();
+  stamp_r(a, 2);
   const float top = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(key_value(mykey)), 0));
   const float pk = lane < a.topk ? expf(key_value(mykey) - top) : 0.f;
   float sum = 0.f;
@@ -257,12 +282,14 @@ __device__ bool route_wave(const MoeArgs &a, Route *rt, uint32_t tag) {
     rt->sg = sg;
     if (blockIdx.x == 0) st_cg(a.sgv, sg);
   }
+  stamp_r(a, 3);
   return true;
 }
 
-// ---------------------------------------------------------------------------------------------------- streaming
-// n k tiles of pair p starting at k0 of a re-laid matrix with IT k tiles (tile bytes tb) into LDS at dst
-__device__ __forceinline__ void stream_tiles(const uint8_t *tr, int IT, int p, int k0, int n, uint32_t tb, uint8_t *dst) {
+// ---------------------------------------------------------------------------------------------------- tiles
+// n k tiles of pair p starting at k0 of a re-laid matrix with IT k tiles (tile bytes tb) into LDS at dst; returns the
+// number of 1 KB requests issued
+__device__ __forceinline__ int stream_tiles(const uint8_t *tr, int IT, int p, int k0, int n, uint32_t tb, uint8_t *dst) {
   const int lane = threadIdx.x & 63;
   const uint8_t *src = tr + ((uint64_t)p * IT + k0) * 2 * tb;
   const uint32_t bytes = (uint32_t)n * 2 * tb;
@@ -270,97 +297,58 @@ __device__ __forceinline__ void stream_tiles(const uint8_t *tr, int IT, int p, i
     if (o + (uint32_t)lane * 16 < bytes)
       __builtin_amdgcn_global_load_lds((const void *)(src + o + lane * 16),
                                        (__attribute__((address_space(3))) void *)(dst + o), 16, 0, 0);
+  return dma_ops(bytes);
 }
-// one wave: output tile pair over k tiles [kt0, kt1) staged in LDS, on the matrix cores: the weights are decoded
-// straight into the B operand of v_mfma_f32_32x32x16_f16 and A repeats the prepared input row (xs, kp order) in all
-// 32 rows, so every row of the product holds the pair's 32 column sums: lanes 0-31 read them from acc[0].
+// the B operand of k tile kt of a staged pair (the trellis words decoded straight into v_mfma_f32_32x32x16_f16's B)
 template <int K>
-__device__ __forceinline__ void pair_mfma_range(const uint8_t *tl, const _Float16 *xs, int kt0, int kt1, f32x16 &acc) {
+__device__ __forceinline__ f16x8 decode_pair(const uint8_t *tl, int kt) {
   constexpr int TW = 8 * K;
   const int lane = threadIdx.x & 63;
   const BLane<K> B = b_lane<K>((uint32_t)lane);
-  const uint32_t *T = (const uint32_t *)tl + B.tile * TW;
-  const _Float16 *xa = xs + 8 * (lane >> 5);
-#pragma unroll 4
-  for (int kt = kt0; kt < kt1; kt++) {
-    const uint32_t *T0 = T + kt * 2 * TW;
-    TileWords w0, w1;
-    w0.w0 = T0[B.g0.i0];
-    w0.w1 = T0[B.g0.i1];
-    w0.w2 = kThreeWords<K> ? T0[B.g0.i2] : 0u;
-    w1.w0 = T0[B.g1.i0];
-    w1.w1 = T0[B.g1.i1];
-    w1.w2 = kThreeWords<K> ? T0[B.g1.i2] : 0u;
-    const f16x8 av = *(const f16x8 *)(xa + kt * 16);
-    f16x2 l0, h0, l1, h1;
-    decode4<K>(w0, B.g0.sh, l0, h0);
-    decode4<K>(w1, B.g1.sh, l1, h1);
-    const f16x8 bv = {l0.x, l0.y, h0.x, h0.y, l1.x, l1.y, h1.x, h1.y};
-    acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bv, acc, 0, 0, 0);
-  }
+  const uint32_t *T0 = (const uint32_t *)tl + B.tile * TW + kt * 2 * TW;
+  TileWords w0, w1;
+  w0.w0 = T0[B.g0.i0];
+  w0.w1 = T0[B.g0.i1];
+  w0.w2 = kThreeWords<K> ? T0[B.g0.i2] : 0u;
+  w1.w0 = T0[B.g1.i0];
+  w1.w1 = T0[B.g1.i1];
+  w1.w2 = kThreeWords<K> ? T0[B.g1.i2] : 0u;
+  f16x2 l0, h0, l1, h1;
+  decode4<K>(w0, B.g0.sh, l0, h0);
+  decode4<K>(w1, B.g1.sh, l1, h1);
+  return f16x8{l0.x, l0.y, h0.x, h0.y, l1.x, l1.y, h1.x, h1.y};
 }
-// decode k tiles [0, n) of the staged pair tiles into the lane's B operands w[kt] (the wave's down slice)
-template <int K>
-__device__ __forceinline__ void decode_b(const uint8_t *tl, int n, f16x8 (&w)[kMaxDn]) {
-  constexpr int TW = 8 * K;
-  const int lane = threadIdx.x & 63;
-  const BLane<K> B = b_lane<K>((uint32_t)lane);
-  const uint32_t *T = (const uint32_t *)tl + B.tile * TW;
+// k tiles [kt0, kt1) of a staged pair times the prepared input xs (kp order, xs[16 kt] = k tile kt), on the matrix
+// cores: A repeats the input row in all 32 rows, so row 0 of the product (lanes 0-31, acc[0]) holds the pair's 32
+// column sums
+// (at most MAXN tiles: unrolled, so that the tile and input offsets fold into the LDS reads' immediates)
+template <int K, int MAXN>
+__device__ __forceinline__ void pair_mfma(const uint8_t *tl, const _Float16 *xs, int kt0, int kt1, f32x16 &acc) {
+  const uint8_t *t = tl + kt0 * 64 * K;
+  const _Float16 *xa = xs + kt0 * 16 + 8 * ((threadIdx.x & 63) >> 5);
+  const int n = kt1 - kt0;
 #pragma unroll
-  for (int kt = 0; kt < kMaxDn; kt++) {
-    if (kt < n) {
-      const uint32_t *T0 = T + kt * 2 * TW;
-      TileWords w0, w1;
-      w0.w0 = T0[B.g0.i0];
-      w0.w1 = T0[B.g0.i1];
-      w0.w2 = kThreeWords<K> ? T0[B.g0.i2] : 0u;
-      w1.w0 = T0[B.g1.i0];
-      w1.w1 = T0[B.g1.i1];
-      w1.w2 = kThreeWords<K> ? T0[B.g1.i2] : 0u;
-      f16x2 l0, h0, l1, h1;
-      decode4<K>(w0, B.g0.sh, l0, h0);
-      decode4<K>(w1, B.g1.sh, l1, h1);
-      w[kt] = f16x8{l0.x, l0.y, h0.x, h0.y, l1.x, l1.y, h1.x, h1.y};
+  for (int i = 0; i < MAXN; i++) {
+    if (i < n) {
+      const f16x8 bv = decode_pair<K>(t, i);
+      const f16x8 av = *(const f16x8 *)(xa + i * 16);
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bv, acc, 0, 0, 0);
     }
   }
 }
-// ---------------------------------------------------------------------------------------------------- counting
-// Each wave posts up to two counter indices (or ~0u) in ids[2 wave + s]; wave kCtl merges runs of equal neighbours
-// and adds each run to its counter with one atomic. All threads call it (barriers inside).
-__device__ void add_runs(uint32_t *ctr, const uint32_t *ids) {
+__device__ __forceinline__ void zero16(f32x16 &v) {
+#pragma unroll
+  for (int i = 0; i < 16; i++) v[i] = 0.f;
+}
+// one 128-chunk of prepared input: fp16(H(x suh)) in kp order, from the suh chunk staged at dst (in place)
+template <int HH>
+__device__ __forceinline__ void prep_chunk(const float *x, int chunk, _Float16 *dst, float sc) {
   const int lane = threadIdx.x & 63;
-  lds_barrier();
-  if ((int)(threadIdx.x >> 6) == kCtl) {
-    const bool in = lane < 2 * kWaves;
-    const uint32_t id = in ? ids[lane] : ~0u;
-    const uint32_t nxt = __shfl_down(id, 1, 64);
-    const uint32_t prv = __shfl_up(id, 1, 64);
-    const bool valid = id != ~0u;
-    const bool head = valid && (lane == 0 || prv != id);
-    const bool tail = valid && (lane == 2 * kWaves - 1 || nxt != id);
-    const uint64_t tails = __ballot(tail);
-    if (head) atomicAdd(ctr + (uint64_t)id * kSyncStride, (uint32_t)__builtin_ctzll(tails >> lane) + 1u);
-  }
-  lds_barrier();
-}
-
-// The partials of one output column c32 of a gate/up column, [column][kMaxSeg][32] floats: every segment slot is loaded
-// (lanes of a wave read 32 consecutive floats per load; the slots past ns hold stale data and are not added), then the
-// ns valid ones are summed in segment order.
-struct Partials {
-  float v[kMaxSeg];
-};
-__device__ __forceinline__ Partials load_partials(const float *p) {
-  Partials r;
-#pragma unroll
-  for (int jj = 0; jj < kMaxSeg; jj++) r.v[jj] = ld_cg(p + jj * 32);
-  return r;
-}
-__device__ __forceinline__ float sum_partials(const Partials &r, int ns) {
-  float s = r.v[0];
-#pragma unroll
-  for (int jj = 1; jj < kMaxSeg; jj++) s = jj < ns ? s + r.v[jj] : s;
-  return s;
+  const float s0 = (float)dst[lane], s1 = (float)dst[lane + 64];
+  float v0 = x[chunk * 128 + lane] * s0, v1 = x[chunk * 128 + lane + 64] * s1;
+  fwht2(v0, v1, lane, HH, sc);
+  dst[kp(lane)] = to_f16(v0);
+  dst[kp(lane + 64)] = to_f16(v1);
 }
 
 }  // namespace
@@ -369,301 +357,395 @@ __device__ __forceinline__ float sum_partials(const Partials &r, int ns) {
 template <int K, int KS, int HID, int INTER>
 __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
   constexpr int KM = K > KS ? K : KS;
-  constexpr int IT = HID / 16, ITd = INTER / 16, NPg = INTER / 32, NBI = INTER / 128,
-                NBLK = HID / 128, HH = had_of(HID), HI = had_of(INTER);
-  constexpr uint32_t GUB = kMaxGu * 64 * KM, AREA = GUB + kMaxDn * 64 * KM;  // a wave's gate/up + down tile bytes
-  extern __shared__ __attribute__((aligned(16))) uint8_t tiles[];  // kWaves x AREA
-  // the workgroup's prepared input chunks (suh by DMA, then fp16(H(x suh)) in place); later the slot's down input
-  constexpr int PW = kMaxPrep * 128 > INTER ? kMaxPrep * 128 : INTER;
-  __shared__ __attribute__((aligned(16))) _Float16 prepw[PW];
-  __shared__ __attribute__((aligned(16))) float xl[HID];  // the input row
+  constexpr int IT = HID / 16, NP = INTER / 32, NG = NP / 4, NBI = INTER / 128, NBLK = HID / 128;
+  constexpr int ITd = INTER / 16, UPS = NBI * NBLK * 4;  // down units per slot
+  constexpr int HH = had_of(HID), HI = had_of(INTER);
+  constexpr uint32_t RG_B = kMaxRg * 64 * KM, SG_B = kMaxSg * 64 * KM, DN_B = kDnKt * 64 * KM;
+  constexpr uint32_t AREA = RG_B + SG_B + DN_B;  // a wave's tile bytes
+  extern __shared__ __attribute__((aligned(16))) uint8_t tiles[];  // kWaves x AREA; the combine reuses it
+  __shared__ __attribute__((aligned(16))) _Float16 prep[kMaxPrep][128];
+  __shared__ __attribute__((aligned(16))) _Float16 sprep[kMaxSPrep][128];
+  __shared__ __attribute__((aligned(16))) _Float16 hl[kMaxH][128];
+  __shared__ float red[2][4][4][32];   // routed gate/up: [run column][quarter][pair][32]
+  __shared__ float sred[kWaves][32];   // shared gate/up per wave
+  __shared__ float hsum[kMaxH][2][128];
+  __shared__ __attribute__((aligned(16))) uint16_t hvec[kMaxH][3][128];   // svh_g, svh_u, suh_d of each h block
+  __shared__ __attribute__((aligned(16))) uint16_t csv[kMaxTopkV + 1][128]; // the combine's svh_d per slot
+  __shared__ __attribute__((aligned(16))) float xl[HID];                    // the input row (staged at launch)
   __shared__ Route rt;
-  __shared__ uint32_t s_tag, s_ok, s_ep, ids[2 * kWaves];
-  const float sch = a.sc_hid, sci = a.sc_inter;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, G = (int)gridDim.x;
-  const int NW = G * kWaves, CG = a.nslot * 2 * NPg;
-  const uint32_t *plan = a.units;
-  // per wave: gate/up segments s0, s1 and the index of each one's first chunk in the workgroup's prepared input;
-  // per workgroup: the count of its prepared chunks and each one's (matrix << 8 | chunk)
-  const uint32_t *pwp = plan + 3 * (blockIdx.x * kWaves + wave);
-  const uint32_t *wpl = plan + 3 * NW + blockIdx.x * (1 + kMaxPrep);
-  uint2 pw = *(const uint2 *)pwp;
-  uint32_t pidx = pwp[2], np = wpl[0], pe = wpl[1 + (wave < kMaxPrep ? wave : 0)];
-  pw.x = __builtin_amdgcn_readfirstlane(pw.x);  // wave-uniform: scalar registers and branches
-  pw.y = __builtin_amdgcn_readfirstlane(pw.y);
-  pidx = __builtin_amdgcn_readfirstlane(pidx);
-  np = __builtin_amdgcn_readfirstlane(np);
-  pe = __builtin_amdgcn_readfirstlane(pe);
-  const bool preps = wave < (int)np;  // this wave prepares chunk `wave` of the workgroup's list
-  const uint32_t *gu_nseg = plan + 3 * NW + G * (1 + kMaxPrep), *fin_tgt = gu_nseg + CG;
-  uint32_t *sync = a.sync;
-  uint32_t *fin_cnt = a.fsync + kSyncStride;                  // [ls * NBI + cb]: gate/up partials of a block
-  uint32_t *blk_cnt = fin_cnt + a.nslot * NBI * kSyncStride;  // [c]: slots stored of output block c
-  float *part_gu = a.part, *part_dn = a.part + (size_t)CG * kMaxSeg * 32;  // gate/up partials; weighted slot outputs
+  __shared__ uint32_t s_tag, s_ok;
+  const int lane = threadIdx.x & 63, wave = (int)rfl(threadIdx.x >> 6), G = (int)gridDim.x;
+  const int hs = a.nslot > a.topk ? 1 : 0;
+  // the workgroup's plan words, one per lane, read before any tile request and picked with readlane (a vector load
+  // later would wait for the wave's tile streams)
+  const uint32_t plw = a.units[(size_t)blockIdx.x * kPW + (lane & (kPW - 1))];
+  auto PL = [&](int i) { return (uint32_t)__builtin_amdgcn_readlane((int)plw, i); };
+  const uint32_t *nseg = a.units + (size_t)G * kPW;
+  uint64_t *part_gu = (uint64_t *)a.part;                                   // [column][seg][32]
+  uint64_t *part_dn = part_gu + (size_t)a.nslot * 2 * NP * IT * 32;         // [slot][cb][HID]
   uint8_t *area = tiles + wave * AREA;
-  mark(a, 0);
-  if (threadIdx.x == 0) {
-    const uint64_t e = ld_cg((const uint64_t *)a.fsync) / (uint64_t)G;
-    s_tag = (uint32_t)(e % 65535u) + 1u;  // 1..65535, never the initial 0
-    s_ep = (uint32_t)e;
-  }
-
-  const Seg g0 = seg_of(pw.x), g1 = seg_of(pw.y);
-  // gate/up column c = (ls * 2 + proj) * NPg + p; down column c = ls * NPd + p
-  auto gu_ls = [&](const Seg &s) { return s.col / (2 * NPg); };
-  auto gu_proj = [&](const Seg &s) { return (s.col / NPg) & 1; };
-  auto gu_p = [&](const Seg &s) { return s.col % NPg; };
-  auto tbytes = [&](int ls) { return 32u * (uint32_t)(slot_shared(a, ls) ? KS : K); };
-  const uint32_t off1 = (uint32_t)g0.n * 2 * (g0.n ? tbytes(gu_ls(g0)) : 0u);  // second segment's LDS offset
-  auto issue_gu = [&](const Seg &s, uint32_t off) {
-    const int ls = gu_ls(s);
-    stream_tiles(slot_block(a, rt, ls) + tr_off(a, ls, gu_proj(s)), IT, gu_p(s), s.k0, s.n, tbytes(ls), area + off);
-  };
-
-  // ---- 1. router; the control wave stages x in LDS; the shared expert's gate/up tiles need no route
-  if (wave == kCtl) {
-#pragma unroll
-    for (int o = 0; o < HID * 4; o += 1024)
-      __builtin_amdgcn_global_load_lds((const void *)((const uint8_t *)a.x + o + lane * 16),
-                                       (__attribute__((address_space(3))) void *)((uint8_t *)xl + o), 16, 0, 0);
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): x is in LDS before the next barrier
-  }
-  router_row<HID>(a, &s_tag);
-  mark(a, 1);
-  const bool pre0 = wave != kCtl && g0.n && slot_shared(a, gu_ls(g0));
-  const bool pre1 = wave != kCtl && g1.n && slot_shared(a, gu_ls(g1));
-  if (pre0) issue_gu(g0, 0);
-  if (pre1) issue_gu(g1, off1);
-
-  // ---- 2. route
+  const float sch = a.sc_hid, sci = a.sc_inter;
+  stamp(a, 0);
+  // ---- 0. before the route: router rows first (the route waits for them); the shared expert's gate/up tile, its
+  // suh chunks and its down unit, placed by the same closed-form splits the host plan uses (no plan word is needed
+  // before the route)
+  const bool rrow = router_active<HID>(a);
+  RouterRow<HID> rr;
+  if (rrow) router_load<HID>(a, rr);
   if (threadIdx.x == 0) s_ok = 1;
-  lds_barrier();
+  if (wave == kCtl) {  // the epoch, then x into LDS for the routed prep (its polls' waits cover these requests)
+    __builtin_amdgcn_s_setprio(3);  // the route is the critical path: this wave first on its SIMD
+    uint64_t ep = 0;
+    if (lane == 0) ep = ld_cg((const uint64_t *)a.fsync);
+    if (lane == 0) s_tag = (uint32_t)ep + 1u;
+    stream_tiles((const uint8_t *)a.x, 0, 0, 0, HID / 4, 8, (uint8_t *)xl);  // 4 HID bytes
+  }
+  constexpr uint32_t SROWS = 2u * NP * IT;  // shared gate/up rows (proj, pair, k tile): [S b / G, S (b + 1) / G)
+  const uint32_t ss0 = hs ? SROWS * blockIdx.x / G : 0u, ss1 = hs ? SROWS * (blockIdx.x + 1) / G : 0u;
+  const uint32_t scol = ss1 > ss0 ? ss0 / IT : kNone, sk0 = ss0 % IT, sn = ss1 - ss0;
+  const bool has_sg = scol != kNone && wave < (int)sn;  // this wave's shared k tile: sk0 + wave
+  const int sm = (int)(scol / NP), sp = (int)(scol % NP);  // shared matrix (proj), pair
+  const int nsp = scol != kNone ? (int)((sk0 + sn - 1) / 8 - sk0 / 8 + 1) : 0;  // shared prep chunks
+  // the shared down unit [UPS b / G, UPS (b + 1) / G) (at most one) sits on wave 0
+  const uint32_t su0 = hs ? (uint32_t)UPS * blockIdx.x / G : 0u, su1 = hs ? (uint32_t)UPS * (blockIdx.x + 1) / G : 0u;
+  const bool dn_shared = su1 > su0 && wave == 0;
+  lds_barrier();  // the epoch is known
+  const uint32_t tag = s_tag, tag16 = (tag - 1u) % 65535u + 1u;
+  if (rrow) router_finish<HID>(a, rr, tag16);
+  lds_barrier();  // this workgroup's logits are out: the router rows had HBM to themselves, the shared expert goes now
+  if (has_sg && wave != kCtl)  // (the control wave requests its tile after the route: its polls must not wait on it)
+    stream_tiles(a.shared + (sm ? a.slay.tr[1] : a.slay.tr[0]), IT, sp, (int)sk0 + wave, 1, 32u * KS, area + RG_B);
+  if (wave < nsp && lane < 16) {
+    const uint8_t *src = a.shared + (sm ? a.slay.su[1] : a.slay.su[0]) + (sk0 / 8 + wave) * 256;
+    __builtin_amdgcn_global_load_lds((const void *)(src + lane * 16),
+                                     (__attribute__((address_space(3))) void *)(sprep[wave]), 16, 0, 0);
+  }
+  if (dn_shared) {
+    const int u = (int)su0, cb = (u / (NBLK * 4)) % NBI, c = (u / 4) % NBLK, p = u % 4;
+    stream_tiles(a.shared + a.slay.tr[2], ITd, c * 4 + p, cb * kDnKt, kDnKt, 32u * KS, area + RG_B + SG_B);
+  }
+  f16x8 sgb = {}, dw[kDnKt];
+
+  // ---- 1. route (control wave), shared to every wave through LDS
   if (wave == kCtl) {
-    const bool ok = a.ne <= 512 ? route_wave<8>(a, &rt, s_tag) : route_wave<16>(a, &rt, s_tag);
+    const bool ok = a.ne <= 512 ? route_wave<8>(a, &rt, tag16) : route_wave<16>(a, &rt, tag16);
     if (!ok && lane == 0) s_ok = 0;
+    stamp(a, 2);
+  } else {
+    stamp(a, 1);
   }
   lds_barrier();
-  mark(a, 2);
+  if (wave != kCtl) stamp(a, 2);
   const bool ok = s_ok != 0;
 
-  // ---- 3. gate/up. Requests, in order: the suh of the chunk the wave prepares (waves below the workgroup's chunk
-  // count), its gate/up tiles (unless already requested), the down tiles. Then: suh -> the prepared chunk -> a
-  // barrier; each 1 KB of gate/up tiles -> the k tiles it completes.
-  // down: workgroup b < nslot * NBLK owns slot ls_d's 128-column output block bd; wave w takes pair 4 bd + w / 4,
-  // k quarter w % 4 (QK k tiles)
-  constexpr int QK = ITd / 4;
-  const bool has_dn = ok && (int)blockIdx.x < a.nslot * NBLK;
-  const int ls_d = (int)blockIdx.x / NBLK, bd = (int)blockIdx.x % NBLK, dpair = bd * 4 + (wave >> 2), dq = wave & 3;
-  const uint32_t gb0 = g0.n ? (uint32_t)g0.n * 2 * tbytes(gu_ls(g0)) : 0u, gb1 = g1.n ? (uint32_t)g1.n * 2 * tbytes(gu_ls(g1)) : 0u;
-  const int n_g0 = (ok && !pre0) ? dma_ops(gb0) : 0, n_g1 = (ok && !pre1) ? dma_ops(gb1) : 0;
-  const int n_dn = has_dn ? dma_ops((uint32_t)QK * 2 * tbytes(ls_d)) : 0;
-  const int pm = (int)(pe >> 8), pc = (int)(pe & 0xFFu);  // the chunk this wave prepares: matrix, 128-chunk
-  if (ok && preps && lane < 16) {  // its suh chunk (256 bytes)
-    const uint8_t *src = slot_block(a, rt, pm >> 1) + su_off(a, pm >> 1, pm & 1) + pc * 256;
-    __builtin_amdgcn_global_load_lds((const void *)(src + lane * 16),
-                                     (__attribute__((address_space(3))) void *)(prepw + wave * 128), 16, 0, 0);
+  // ---- 2. requests: the routed prep chunks' suh, the routed gate/up tiles (up to two pieces), the routed down unit
+  // routed rows [r0, r1): row r = (matrix mr, group g, k tile); the run meets at most two (matrix, group) columns
+  const uint32_t dnw = PL(P_DN + wave);  // this wave's down unit (the shared one as above) and its h slot
+  const int du = dnw == kNone ? -1 : (int)(dnw & 0xFFFFFFu), dhs = (int)(dnw >> 24);
+  const int d_ls = du / UPS, d_cb = (du / (NBLK * 4)) % NBI, d_c = (du / 4) % NBLK, d_p = du % 4;
+  const uint32_t r0 = PL(P_R0), r1 = PL(P_R1);
+  struct Run {
+    int ls, proj, g, ka, kb;  // columns (ls, proj, 4 g .. 4 g + 3), k tiles [ka, kb)
+  };
+  auto mk_run = [&](uint32_t colg, uint32_t ka, uint32_t kb) {
+    const int mr = (int)(colg / NG);
+    return Run{hs + mr / 2, mr & 1, (int)(colg % NG), (int)ka, (int)kb};
+  };
+  const uint32_t eA = min(r1, (r0 / IT + 1) * IT);
+  const bool two = eA < r1;
+  const int nrun = r1 > r0 ? (two ? 2 : 1) : 0;
+  const Run run[2] = {mk_run(r0 / IT, r0 % IT, r0 % IT + (eA - r0)), mk_run(eA / IT, 0, two ? r1 - eA : 0)};
+  const int npc0 = nrun ? (run[0].kb - 1) / 8 - run[0].ka / 8 + 1 : 0;
+  const int npc = npc0 + (two ? (run[1].kb - 1) / 8 + 1 : 0);
+  const int pc0[2] = {0, npc0};  // first prep chunk index of each run
+  // this wave: pair w & 3 of each run, quarter w >> 2 of the rows [r0, r1)
+  const uint32_t wq0 = r0 + (r1 - r0) * (uint32_t)(wave >> 2) / 4, wq1 = r0 + (r1 - r0) * (uint32_t)((wave >> 2) + 1) / 4;
+  int pk0[2], pn[2];  // the wave's piece of each run: k tiles [pk0, pk0 + pn)
+  {
+    const uint32_t lo0 = max(r0, wq0), hi0 = min(eA, wq1), lo1 = max(eA, wq0), hi1 = min(r1, wq1);
+    pn[0] = hi0 > lo0 ? (int)(hi0 - lo0) : 0;
+    pk0[0] = run[0].ka + (int)(lo0 - r0);
+    pn[1] = two && hi1 > lo1 ? (int)(hi1 - lo1) : 0;
+    pk0[1] = (int)(lo1 - eA);
   }
-  if (ok && g0.n && !pre0) issue_gu(g0, 0);
-  if (ok && g1.n && !pre1) issue_gu(g1, off1);
-  if (has_dn) stream_tiles(slot_block(a, rt, ls_d) + tr_off(a, ls_d, 2), ITd, dpair, dq * QK, QK, tbytes(ls_d), area + GUB);
-  if (a.trace && lane == 0) a.trace[(uint64_t)(512 + blockIdx.x * kWaves + wave) * 8 + 3] = wall_clock64();
-  if (ok && preps) {  // fp16(H(x * suh)) of the chunk, in kp order, in place of its suh
-    wait_vm(n_g0 + n_g1 + n_dn);  // the suh chunk is in
-    _Float16 *dst = prepw + wave * 128;
-    const float s0 = (float)dst[lane], s1 = (float)dst[lane + 64];
-    float v0 = xl[pc * 128 + lane] * s0, v1 = xl[pc * 128 + lane + 64] * s1;
-    fwht2(v0, v1, lane, HH, sch);
-    dst[kp(lane)] = to_f16(v0);
-    dst[kp(lane + 64)] = to_f16(v1);
-  }
-  lds_barrier();  // every chunk of the workgroup is prepared
-  if (a.trace && lane == 0) a.trace[(uint64_t)(512 + blockIdx.x * kWaves + wave) * 8 + 4] = wall_clock64();
-  mark(a, 3);
-  // a segment's dot, k tiles taken as each 1 KB request lands (n_after: requests issued after the segment's; stores
-  // come only after both segments, so they are never counted as "after": a wait may be stricter, never looser)
-  auto gu_dot = [&](const Seg &s, uint32_t off, const _Float16 *pr, int n_seg, int n_after, f32x16 &acc) {
-    const _Float16 *xs = pr + (s.k0 - 8 * (s.k0 / 8)) * 16;
-    const bool sh = slot_shared(a, gu_ls(s));
-    const uint32_t pb = 2 * tbytes(gu_ls(s));  // bytes of one k tile pair
-    int kt0 = 0;
-    const int steps = n_seg > 0 ? n_seg : 1;
-    for (int j = 0; j < steps; j++) {
-      if (n_seg > 0) wait_vm(n_after + n_seg - 1 - j);
-      if (a.trace && lane == 0 && j == steps - 1) a.trace[(uint64_t)(512 + blockIdx.x * kWaves + wave) * 8 + 1] = wall_clock64();
-      if (a.trace && lane == 0 && j == 0 && n_seg > 0) a.trace[(uint64_t)(512 + blockIdx.x * kWaves + wave) * 8 + 5] = wall_clock64();
-      const int kt1 = j == steps - 1 ? s.n : (int)((uint32_t)(j + 1) * 1024u / pb);
-      if (kt1 > kt0) {
-        if (sh)
-          pair_mfma_range<KS>(area + off, xs, kt0, kt1, acc);
-        else
-          pair_mfma_range<K>(area + off, xs, kt0, kt1, acc);
-        kt0 = kt1;
-      }
+  const int nh = (int)PL(P_NH);
+  const uint32_t comb = PL(P_COMB);
+  // Requests, in the order they are consumed. A CU returns its waves' requests roughly in issue order, and a wave
+  // issues all its requests before the next wave of its SIMD does: so every wave first requests the routed prep
+  // chunks' suh and its gate/up tiles (up to two pieces), and only after a workgroup barrier its later needs (down
+  // unit, small vectors), which would otherwise hold back the other waves' gate/up tiles.
+  int n_su = 0, n_p[2] = {0, 0}, n_dn = 0, n_pf = 0;
+  const _Float16 *pxs[2] = {nullptr, nullptr};
+  uint32_t poff[2] = {0, 0};
+  if (wave == kCtl && has_sg)
+    stream_tiles(a.shared + (sm ? a.slay.tr[1] : a.slay.tr[0]), IT, sp, (int)sk0 + wave, 1, 32u * KS, area + RG_B);
+  if (ok) {
+    if (wave < npc && lane < 16) {  // suh of prep chunk `wave`
+      const bool second = two && wave >= npc0;
+      const int rls = second ? run[1].ls : run[0].ls, rproj = second ? run[1].proj : run[0].proj;
+      const int kc = (second ? run[1].ka : run[0].ka) / 8 + (wave - (second ? npc0 : 0));
+      const uint8_t *src = slot_block(a, rt, rls) + su_off(a, rls, rproj) + kc * 256;
+      __builtin_amdgcn_global_load_lds((const void *)(src + lane * 16),
+                                       (__attribute__((address_space(3))) void *)(prep[wave]), 16, 0, 0);
     }
-  };
-  auto gu_store = [&](const Seg &s, const f32x16 &acc) {
-    if (lane < 32) st_cg(part_gu + ((size_t)s.col * kMaxSeg + s.jj) * 32 + lane, acc[0]);  // [column][kMaxSeg][32]
-  };
-  f32x16 ga, gb;
+    n_su = wave < npc ? 1 : 0;
+    uint32_t off = 0;
 #pragma unroll
-  for (int i = 0; i < 16; i++) ga[i] = gb[i] = 0.f;
-  if (ok && g0.n) gu_dot(g0, 0, prepw + (pidx & 0xFu) * 128, n_g0, n_g1 + n_dn, ga);
-  if (ok && g1.n) gu_dot(g1, off1, prepw + ((pidx >> 4) & 0xFu) * 128, n_g1, n_dn, gb);
-  if (a.trace && lane == 0) a.trace[(uint64_t)(512 + blockIdx.x * kWaves + wave) * 8 + 2] = wall_clock64();
-  if (ok && g0.n) gu_store(g0, ga);
-  if (ok && g1.n) gu_store(g1, gb);
-  if (wave == 0) mark2(a, 0);
-  __builtin_amdgcn_s_waitcnt(0);  // partials stored before they are counted
-  if (wave == 0) mark2(a, 1);
-  if (a.trace && lane == 0) a.trace[(uint64_t)(512 + blockIdx.x * kWaves + wave) * 8] = wall_clock64();
-  if (lane == 0) {
-    ids[2 * wave] = (ok && g0.n) ? (uint32_t)(gu_ls(g0) * NBI + gu_p(g0) / 4) : ~0u;
-    ids[2 * wave + 1] = (ok && g1.n) ? (uint32_t)(gu_ls(g1) * NBI + gu_p(g1) / 4) : ~0u;
-  }
-  if (a.trace && threadIdx.x == 0) a.trace[(uint64_t)(256 + blockIdx.x) * 8 + 6] = wall_clock64();
-  add_runs(fin_cnt, ids);
-  mark(a, 4);
-  // ---- 4. down. The workgroup of (slot ls_d, output block bd) first finishes the slot's gate/up blocks itself:
-  // wave cb < NBI waits until every partial of block cb is stored, sums them in segment order and applies the down
-  // prologue (reference kernels/fn_moe.metal:370-384): g = H(inner_g) svh_g, u = H(inner_u) svh_u,
-  // h = H(silu(g) u suh_d) -> fp16 in kp order, into LDS. Its down slice is decoded into registers meanwhile.
-  f16x8 dw[kMaxDn];
-  if (has_dn) {
-    if (slot_shared(a, ls_d)) decode_b<KS>(area + GUB, QK, dw);
-    else decode_b<K>(area + GUB, QK, dw);
-  }
-  mark(a, 5);
-  _Float16 *hl = prepw;  // the slot's down input, INTER halves (the prepared chunks are no longer read)
-  if (has_dn && wave < NBI) {
-    const int cb = wave, ls = ls_d, id = ls * NBI + cb;
-    bool got = false;
-    if (lane == 0) {
-      for (uint32_t it = 0; it < kSpin; it++) {
-        if (ld_relaxed(fin_cnt + id * kSyncStride) - s_ep * fin_tgt[id] >= fin_tgt[id]) {
-          got = true;
-          break;
-        }
-        if ((it & 63u) == 63u && ld_relaxed(sync + kWordErr)) break;
-        __builtin_amdgcn_s_sleep(1);
-      }
-      if (!got) atomicOr(sync + kWordErr, 1u);
+    for (int i = 0; i < 2; i++) {
+      if (!pn[i]) continue;
+      const int ls = run[i].ls;
+      poff[i] = off;
+      pxs[i] = &prep[pc0[i] + (pk0[i] / 8 - run[i].ka / 8)][0] + (pk0[i] % 8) * 16;
+      n_p[i] = stream_tiles(slot_block(a, rt, ls) + tr_off(a, ls, run[i].proj), IT, run[i].g * 4 + (wave & 3),
+                            pk0[i], pn[i], 32u * K, area + off);
+      off += (uint32_t)pn[i] * 64u * K;
     }
-    if (__shfl(got ? 1 : 0, 0, 64)) {
-      mark2(a, 2);
+  }
+  lds_barrier();
+  if (ok) {
+    // after the barrier: every wave's gate/up requests are ahead of these in the CU's queue. The routed down unit's
+    // tiles; the small vectors the later phases read into LDS (the h prologue's svh_g, svh_u, suh_d of block `wave`;
+    // the combine's svh_d of slot ls = wave (mod 16))
+    if (du >= 0 && !dn_shared)
+      n_dn = stream_tiles(slot_block(a, rt, d_ls) + tr_off(a, d_ls, 2), ITd, d_c * 4 + d_p, d_cb * kDnKt, kDnKt,
+                          32u * K, area + RG_B + SG_B);
+    if (wave < nh) {
+      const uint32_t hb = PL(P_HB + wave) & 0x7FFFFFFFu;
+      const int ls = (int)(hb / NBI), cb = (int)(hb % NBI);
       const uint8_t *blk = slot_block(a, rt, ls);
-      const int i0 = cb * 128 + lane, i1 = i0 + 64;
-      Partials pp[2][2];
-      int ns[2][2];
+      const uint64_t offs[3] = {sv_off(a, ls, 0), sv_off(a, ls, 1), su_off(a, ls, 2)};
 #pragma unroll
-      for (int proj = 0; proj < 2; proj++)
-#pragma unroll
-        for (int h = 0; h < 2; h++) {
-          const int i = cb * 128 + h * 64 + lane, c = (ls * 2 + proj) * NPg + i / 32;
-          pp[proj][h] = load_partials(part_gu + (size_t)c * kMaxSeg * 32 + (i & 31));
-          ns[proj][h] = (int)gu_nseg[c];
-        }
-      const uint16_t *svg = (const uint16_t *)(blk + sv_off(a, ls, 0)), *svu = (const uint16_t *)(blk + sv_off(a, ls, 1));
-      const uint16_t *sud = (const uint16_t *)(blk + su_off(a, ls, 2));
-      const float sg0 = h2f(svg[i0]), sg1 = h2f(svg[i1]), su0 = h2f(svu[i0]), su1 = h2f(svu[i1]);
-      const float sd0 = h2f(sud[i0]), sd1 = h2f(sud[i1]);
-      float gu[2][2];
-#pragma unroll
-      for (int proj = 0; proj < 2; proj++)
-#pragma unroll
-        for (int h = 0; h < 2; h++) gu[proj][h] = sum_partials(pp[proj][h], ns[proj][h]);
-      mark2(a, 3);
-      float g0v = gu[0][0], g1v = gu[0][1], u0v = gu[1][0], u1v = gu[1][1];
-      fwht2(g0v, g1v, lane, HI, sci);
-      fwht2(u0v, u1v, lane, HI, sci);
-      g0v = g0v * sg0;
-      u0v = u0v * su0;
-      g1v = g1v * sg1;
-      u1v = u1v * su1;
-      float h0 = g0v / (1.f + expf(-g0v)) * u0v * sd0;
-      float h1 = g1v / (1.f + expf(-g1v)) * u1v * sd1;
-      fwht2(h0, h1, lane, HI, sci);
-      hl[cb * 128 + kp(lane)] = to_f16(h0);
-      hl[cb * 128 + kp(lane + 64)] = to_f16(h1);
-      if (bd == 0) {  // inner gate / up outputs, for reads (one workgroup per slot; nothing waits for them)
-        float *gsum = a.guo + (size_t)slot_j(a, ls) * 2 * INTER;
-        st_cg(gsum + i0, gu[0][0]);
-        st_cg(gsum + i1, gu[0][1]);
-        st_cg(gsum + INTER + i0, gu[1][0]);
-        st_cg(gsum + INTER + i1, gu[1][1]);
+      for (int v = 0; v < 3; v++)
+        if (lane < 16)
+          __builtin_amdgcn_global_load_lds((const void *)(blk + offs[v] + cb * 256 + lane * 16),
+                                           (__attribute__((address_space(3))) void *)(hvec[wave][v]), 16, 0, 0);
+      n_pf += 3;
+    }
+    if (comb != kNone) {
+      for (int ls = wave; ls < a.nslot; ls += kWaves) {
+        if (lane < 16)
+          __builtin_amdgcn_global_load_lds(
+              (const void *)(slot_block(a, rt, ls) + sv_off(a, ls, 2) + comb * 256 + lane * 16),
+              (__attribute__((address_space(3))) void *)(csv[ls]), 16, 0, 0);
+        n_pf++;
       }
-      mark2(a, 4);
     }
   }
-  bool dok = has_dn;
-  lds_barrier();
-  mark(a, 6);
-  float(*red)[32] = (float(*)[32])tiles;  // [wave][32] column sums: the tile areas are no longer read
-  if (dok) {  // on the matrix cores, A = the down input repeated in all rows (as the gate/up dot)
-    const _Float16 *hp = hl + dq * QK * 16 + 8 * (lane >> 5);
-    f16x8 hv[kMaxDn];
+  stamp(a, 3);
+  // the shared expert while the routed tiles are on their way (its requests went out before the route): its prep
+  // chunks, its gate/up tile and its down unit's B operands; then the routed prep
+  wait_vm(n_su + n_p[0] + n_p[1] + n_dn + n_pf);
+  if (wave < nsp) prep_chunk<HH>(xl, (int)(sk0 / 8) + wave, sprep[wave], sch);
+  if (has_sg) sgb = decode_pair<KS>(area + RG_B, 0);
+  if (dn_shared) {
 #pragma unroll
-    for (int kt = 0; kt < QK; kt++) hv[kt] = *(const f16x8 *)(hp + kt * 16);
+    for (int kt = 0; kt < kDnKt; kt++) dw[kt] = decode_pair<KS>(area + RG_B + SG_B, kt);
+  }
+  stamp_w(a, 2);
+  if (ok && n_su) {  // the routed prep: suh chunk -> fp16(H(x suh)) in kp order (x from LDS: a global load now would
+                     // wait for the tile streams)
+    wait_vm(n_p[0] + n_p[1] + n_dn + n_pf);
+    const bool second = two && wave >= npc0;
+    const int kc = (second ? run[1].ka : run[0].ka) / 8 + (wave - (second ? npc0 : 0));
+    prep_chunk<HH>(xl, kc, prep[wave], sch);
+  }
+  lds_barrier();  // shared and routed prep chunks ready
+  {  // the shared gate/up product, summed over the waves in wave order by wave 0
     f32x16 acc;
-#pragma unroll
-    for (int i = 0; i < 16; i++) acc[i] = 0.f;
-#pragma unroll
-    for (int kt = 0; kt < QK; kt++) acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(hv[kt], dw[kt], acc, 0, 0, 0);
-    if (lane < 32) red[wave][lane] = acc[0];
+    zero16(acc);
+    if (has_sg) {
+      const f16x8 av = *(const f16x8 *)(&sprep[0][0] + (sk0 % 8 + wave) * 16 + 8 * (lane >> 5));
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, sgb, acc, 0, 0, 0);
+    }
+    if (lane < 32) sred[wave][lane] = acc[0];
   }
   lds_barrier();
-  mark(a, 7);
-  if (dok && wave == 0) {
-    const int j = slot_j(a, ls_d), i0 = bd * 128 + lane, i1 = i0 + 64;
-    const uint16_t *sv = (const uint16_t *)(slot_block(a, rt, ls_d) + sv_off(a, ls_d, 2));
-    const float s0 = h2f(sv[i0]), s1 = h2f(sv[i1]);
-    float v[2];
+  // the shared partial goes out now: every workgroup's down units need the shared h block, so it must not wait for
+  // the routed gate/up
+  int n_st = 0;  // stores issued after the down requests (counted by vmcnt)
+  if (ok && scol != kNone && wave == 0 && lane < 32) {
+    float s = sred[0][lane];
+    for (int w = 1; w < kWaves; w++) s += sred[w][lane];
+    st_tag(part_gu + ((size_t)scol * IT + PL(P_SJJ)) * 32 + lane, s, tag);
+  }
+  if (ok && scol != kNone && wave == 0) n_st = 1;
+  stamp_w(a, 3);
+  // ---- 4. routed gate/up: each 1 KB of tiles -> the k tiles it completes
+  f32x16 acc[2];
+  zero16(acc[0]);
+  zero16(acc[1]);
+  if (ok) {
+    const uint32_t pb = 64u * K;  // bytes of one k tile pair
 #pragma unroll
-    for (int h = 0; h < 2; h++) {  // column 64 h + lane of the block: pair (64 h + lane) / 32, quarters in order
-      const int w4 = ((h * 64 + lane) >> 5) * 4, c = lane & 31;
-      v[h] = ((red[w4][c] + red[w4 + 1][c]) + red[w4 + 2][c]) + red[w4 + 3][c];
-    }
-    st_cg(a.dn + (size_t)j * HID + i0, v[0]);  // inner down outputs, for reads
-    st_cg(a.dn + (size_t)j * HID + i1, v[1]);
-    fwht2(v[0], v[1], lane, HH, sch);
-    const float w = slot_shared(a, ls_d) ? rt.sg : rt.w[j];
-    float *ys = part_dn + (size_t)j * HID;  // per-slot weighted outputs
-    st_cg(ys + i0, v[0] * s0 * w);
-    st_cg(ys + i1, v[1] * s1 * w);
-    __builtin_amdgcn_s_waitcnt(0);
-    uint32_t old = 0;
-    if (lane == 0) old = atomicAdd(blk_cnt + bd * kSyncStride, 1u);
-    old = __shfl(old, 0, 64);
-    if (a.trace && lane == 0) a.trace[(uint64_t)(6001 + blockIdx.x) * 8 + 3] = wall_clock64();
-    if (old - s_ep * (uint32_t)a.nslot == (uint32_t)a.nslot - 1u) {  // every slot of the block is stored: y = the sum
-                                                                     // over the slots in slot order
-      constexpr int U = 12;  // slots loaded in one batch
-      float yv[2] = {0.f, 0.f}, sh[2] = {0.f, 0.f};  // routed sum in slot order; the shared slot
-      for (int j0 = 0; j0 < a.nslot; j0 += U) {
-        float t[U][2];
-#pragma unroll
-        for (int u = 0; u < U; u++)
-          if (j0 + u < a.nslot) {
-            t[u][0] = ld_cg(part_dn + (size_t)(j0 + u) * HID + i0);
-            t[u][1] = ld_cg(part_dn + (size_t)(j0 + u) * HID + i1);
-          }
-#pragma unroll
-        for (int u = 0; u < U; u++)
-          if (j0 + u < a.topk) {
-            yv[0] += t[u][0];
-            yv[1] += t[u][1];
-          } else if (j0 + u < a.nslot) {
-            sh[0] = t[u][0];
-            sh[1] = t[u][1];
-          }
+    for (int i = 0; i < 2; i++) {
+      if (!pn[i]) continue;
+      const int after = (i == 0 ? n_p[1] : 0) + n_dn + n_pf + n_st;
+      int kt0 = 0;
+      for (int j = 0; j < n_p[i]; j++) {
+        wait_vm(after + n_p[i] - 1 - j);
+        if (i == 0 && j == 0) stamp_w(a, 0);
+        if (j == n_p[i] - 1) stamp_w(a, 1);
+        const int kt1 = j == n_p[i] - 1 ? pn[i] : (int)((uint32_t)(j + 1) * 1024u / pb);
+        if (kt1 > kt0) pair_mfma<K, 1024 / (64 * K) + 2>(area + poff[i], pxs[i], kt0, kt1, acc[i]);
+        kt0 = max(kt0, kt1);
       }
-      a.y[i0] = moe_finish(a, 0, i0, yv[0], sh[0]);
-      a.y[i1] = moe_finish(a, 0, i1, yv[1], sh[1]);
-      if (a.trace && lane == 0) a.trace[(uint64_t)(6001 + blockIdx.x) * 8 + 4] = wall_clock64();
     }
   }
+  if (lane < 32) {
+    red[0][wave >> 2][wave & 3][lane] = acc[0][0];
+    red[1][wave >> 2][wave & 3][lane] = acc[1][0];
+  }
+  stamp(a, 4);
+  lds_barrier();
+  if (ok && wave < 4 * nrun && lane < 32) {  // run i = wave >> 2, pair wave & 3: the quarters in order
+    const int i = wave >> 2, p = wave & 3;
+    const float s = ((red[i][0][p][lane] + red[i][1][p][lane]) + red[i][2][p][lane]) + red[i][3][p][lane];
+    const int rls = i ? run[1].ls : run[0].ls, rproj = i ? run[1].proj : run[0].proj, rg = i ? run[1].g : run[0].g;
+    const uint32_t col = (uint32_t)((rls * 2 + rproj) * NP + rg * 4 + p);
+    st_tag(part_gu + ((size_t)col * IT + PL(P_JJ0 + i)) * 32 + lane, s, tag);
+  }
+  if (ok && wave < 4 * nrun) n_st++;
 
-  // ---- done: count this workgroup (the next launch derives its epoch from the count)
-  if (threadIdx.x == 0) atomicAdd((unsigned long long *)a.fsync, 1ull);
+  // ---- 5. the routed down unit's tiles into B operands; then the h blocks from the gate/up partials
+  if (ok && du >= 0 && !dn_shared) {
+    wait_vm(n_pf + n_st);
+#pragma unroll
+    for (int kt = 0; kt < kDnKt; kt++) dw[kt] = decode_pair<K>(area + RG_B + SG_B, kt);
+  }
+  // h loaders: the first 2 nh waves, which the SIMDs serve first (oldest first) and so finish their gate/up first;
+  // the routed down units sit on the last waves, whose decode then yields to the remaining gate/up work. Wave (h slot,
+  // proj), lane: columns o = lane, lane + 64 of the block
+  const int lw = wave;
+  if (ok && lw < 2 * nh) {
+    const int hslot = lw >> 1, proj = lw & 1;
+    const uint32_t hb = PL(P_HB + hslot) & 0x7FFFFFFFu;
+    const int ls = (int)(hb / NBI), cb = (int)(hb % NBI);
+    const uint32_t col0 = (uint32_t)((ls * 2 + proj) * NP + cb * 4 + (lane >> 5)), col1 = col0 + 2;
+    const int ns0 = (int)nseg[col0], ns1 = (int)nseg[col1];
+    const uint64_t *src0 = part_gu + (size_t)col0 * IT * 32 + (lane & 31), *src1 = part_gu + (size_t)col1 * IT * 32 + (lane & 31);
+    float s0 = 0.f, s1 = 0.f;
+    bool got = false;
+    for (uint32_t it = 0; it < kSpin; it++) {
+      bool all = true;
+#pragma unroll 4
+      for (int jj = 0; jj < ns0; jj++) {
+        const uint64_t t = ld_cg(src0 + jj * 32);
+        all = all && tag_ok(t, tag);
+        s0 = jj == 0 ? tag_val(t) : s0 + tag_val(t);
+      }
+#pragma unroll 4
+      for (int jj = 0; jj < ns1; jj++) {
+        const uint64_t t = ld_cg(src1 + jj * 32);
+        all = all && tag_ok(t, tag);
+        s1 = jj == 0 ? tag_val(t) : s1 + tag_val(t);
+      }
+      if (__all(all)) {
+        got = true;
+        break;
+      }
+      if ((it & 15u) == 15u && ld_relaxed(a.sync + kWordErr)) break;
+    }
+    if (!got) atomicOr(a.sync + kWordErr, 1u);
+    hsum[hslot][proj][lane] = s0;
+    hsum[hslot][proj][lane + 64] = s1;
+    if (PL(P_HB + hslot) >> 31) {  // the inner gate / up output, for reads
+      float *gu = a.guo + ((size_t)slot_j(a, ls) * 2 + proj) * INTER + cb * 128;
+      st_cg(gu + lane, s0);
+      st_cg(gu + lane + 64, s1);
+    }
+  }
+  stamp(a, 5);
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): every wave's LDS prefetches (svh / suh vectors) have landed
+  lds_barrier();
+  if (ok && wave < nh) {  // the down prologue of h block `wave` (reference kernels/fn_moe.metal:370-384)
+    const uint16_t *svg = hvec[wave][0], *svu = hvec[wave][1], *sud = hvec[wave][2];
+    float g0v = hsum[wave][0][lane], g1v = hsum[wave][0][lane + 64];
+    float u0v = hsum[wave][1][lane], u1v = hsum[wave][1][lane + 64];
+    fwht2(g0v, g1v, lane, HI, sci);
+    fwht2(u0v, u1v, lane, HI, sci);
+    g0v = g0v * h2f(svg[lane]);
+    u0v = u0v * h2f(svu[lane]);
+    g1v = g1v * h2f(svg[lane + 64]);
+    u1v = u1v * h2f(svu[lane + 64]);
+    float h0 = g0v / (1.f + expf(-g0v)) * u0v * h2f(sud[lane]);
+    float h1 = g1v / (1.f + expf(-g1v)) * u1v * h2f(sud[lane + 64]);
+    fwht2(h0, h1, lane, HI, sci);
+    hl[wave][kp(lane)] = to_f16(h0);
+    hl[wave][kp(lane + 64)] = to_f16(h1);
+  }
+  lds_barrier();
+  // ---- 6. down: 8 k tiles of h against the unit's decoded tiles; one tagged partial per unit
+  if (ok && du >= 0) {
+    f32x16 d;
+    zero16(d);
+    const _Float16 *ha = &hl[dhs][0] + 8 * (lane >> 5);
+#pragma unroll
+    for (int kt = 0; kt < kDnKt; kt++)
+      d = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const f16x8 *)(ha + kt * 16), dw[kt], d, 0, 0, 0);
+    if (lane < 32)
+      st_tag(part_dn + ((size_t)d_ls * NBI + d_cb) * HID + d_c * 128 + d_p * 32 + lane, d[0], tag);
+  }
+  stamp(a, 6);
+
+  // ---- 7. combine of output block c (16 workgroups): per slot the cb partials in order -> H, svh_d, weight; the
+  // slots in slot order (routed, then the shared one) -> y (reference kernels/fn_moe.metal:420-450)
+  if (ok && comb != kNone) {
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the svh_d prefetches of every wave have landed
+    const int c = (int)comb, o = threadIdx.x & 127;
+    float *cv = (float *)tiles;  // [nslot][128]
+    // thread: column o, slots g, g + 8, g + 16 (g = t / 128), all polled together
+    const int g = threadIdx.x >> 7;
+    const uint64_t *src = part_dn + c * 128 + o;
+    float sv[3] = {0.f, 0.f, 0.f};
+    bool got = false;
+    for (uint32_t it = 0; it < kSpin; it++) {
+      bool all = true;
+#pragma unroll
+      for (int q = 0; q < 3; q++) {
+        const int ls = g + 8 * q;
+        if (ls < a.nslot) {
+#pragma unroll
+          for (int cb = 0; cb < NBI; cb++) {
+            const uint64_t t = ld_cg(src + ((size_t)ls * NBI + cb) * HID);
+            all = all && tag_ok(t, tag);
+            sv[q] = cb == 0 ? tag_val(t) : sv[q] + tag_val(t);
+          }
+        }
+      }
+      if (__all(all)) {
+        got = true;
+        break;
+      }
+      if ((it & 15u) == 15u && ld_relaxed(a.sync + kWordErr)) break;
+    }
+    if (!got) atomicOr(a.sync + kWordErr, 1u);
+#pragma unroll
+    for (int q = 0; q < 3; q++)
+      if (g + 8 * q < a.nslot) cv[(g + 8 * q) * 128 + o] = sv[q];
+    lds_barrier();
+    for (int ls = wave; ls < a.nslot; ls += kWaves) {
+      const int j = slot_j(a, ls), i0 = c * 128 + lane, i1 = i0 + 64;
+      float v0 = cv[ls * 128 + lane], v1 = cv[ls * 128 + lane + 64];
+      st_cg(a.dn + (size_t)j * HID + i0, v0);  // inner down outputs, for reads
+      st_cg(a.dn + (size_t)j * HID + i1, v1);
+      fwht2(v0, v1, lane, HH, sch);
+      const float w = slot_shared(a, ls) ? rt.sg : rt.w[j];
+      cv[ls * 128 + lane] = v0 * h2f(csv[ls][lane]) * w;
+      cv[ls * 128 + lane + 64] = v1 * h2f(csv[ls][lane + 64]) * w;
+    }
+    lds_barrier();
+    if (wave < 2) {
+      const int i = c * 128 + wave * 64 + lane, oo = wave * 64 + lane;
+      float yv = 0.f;
+      for (int k = 0; k < a.topk; k++) yv += cv[(hs + k) * 128 + oo];
+      const float sh = hs ? cv[oo] : 0.f;
+      a.y[i] = moe_finish(a, 0, i, yv, sh);
+    }
+  }
+  stamp(a, 7);
+  // ---- done: workgroup 0 advances the epoch (one store). It finishes only after every workgroup published its
+  // router logit, i.e. after every workgroup read this launch's epoch.
+  if (blockIdx.x == 0 && threadIdx.x == 0) st_cg((uint64_t *)a.fsync, (uint64_t)tag);
 }
 
 // ---------------------------------------------------------------------------------------------------- host side
@@ -680,10 +762,9 @@ StepFn step_for_k(int K, int KS) {
 StepFn step_fn(int K, int KS, int hid, int inter) {
   if (hid == 2048 && inter == 512) return step_for_k<2048, 512>(K, KS);
   if (hid == 1024 && inter == 256) return step_for_k<1024, 256>(K, KS);
-  if (hid == 2560 && inter == 640) return step_for_k<2560, 640>(K, KS);
   return nullptr;
 }
-size_t step_lds(int K, int KS) { return (size_t)kWaves * (kMaxGu + kMaxDn) * 64 * std::max(K, KS); }  // = kWaves AREA
+size_t step_lds(int K, int KS) { return (size_t)kWaves * (kMaxRg + kMaxSg + kDnKt) * 64 * std::max(K, KS); }
 }  // namespace
 
 int moe_fused_grid() {
@@ -696,73 +777,106 @@ int moe_fused_grid() {
   return cus;
 }
 
-// Gate/up work plan. The 2 nslot gate/up matrices (m = 2 ls + proj, NPg tile-pair columns x IT k tiles each) are
-// cut by k rows: workgroup b takes an equal run of the nslot * 2 * IT (matrix, k tile) rows, all NPg columns of
-// them. Its kWaves / NPg waves per column split the run's k range; a run that crosses into the next matrix gives each
-// wave a second segment. So a workgroup needs the prepared input of only the 128-chunks its k rows cover (one or two
-// per matrix), which it computes once and shares in LDS.
+// The work plan (see the kernel's header). Returns ok = false when the shape does not fit the kernel's per-wave
+// limits; the layer then runs the staged path.
 MoePlan moe_fused_plan(int hid, int inter, int topk, int nslot, int G) {
   MoePlan pl;
-  const int IT = hid / 16, ITd = inter / 16, NPg = inter / 32, NBI = inter / 128, NBLK = hid / 128;
-  const int NW = G * kWaves, CG = nslot * 2 * NPg, NM = nslot * 2;
-  const long TR = (long)NM * IT;  // k rows
-  const int W = NPg > 0 && kWaves % NPg == 0 ? kWaves / NPg : 0;  // waves per column
-  const long rows = (TR + G - 1) / G;
-  pl.ok = W > 0 && rows <= IT && (rows + W - 1) / W <= kMaxGu && CG < 4096 && IT < 256 && ITd % 4 == 0 &&
-          ITd / 4 <= kMaxDn && nslot * NBLK <= G;
-  if (!pl.ok) return pl;
-  std::vector<uint32_t> wv((size_t)NW * 3, 0u), prep((size_t)G * (1 + kMaxPrep), 0u), gnseg(CG, 0u);
+  const int IT = hid / 16, NP = inter / 32, NG = NP / 4, NBI = inter / 128, NBLK = hid / 128, UPS = NBI * NBLK * 4;
+  const int hs = nslot > topk ? 1 : 0, NCOL = nslot * 2 * NP;
+  if (inter % 128 || hid % 512 || G < 1 || NBLK > G) return pl;
+  std::vector<uint32_t> w((size_t)G * kPW, kNone), nseg(NCOL, 0u);
+  // routed gate/up rows: (routed matrix, group, k tile); workgroup b takes [R b / G, R (b + 1) / G)
+  const long R = (long)topk * 2 * NG * IT;
   for (int b = 0; b < G; b++) {
-    const long r0 = std::min<long>((long)b * rows, TR), r1 = std::min<long>(r0 + rows, TR);
-    std::vector<uint32_t> chunks;  // (m << 8 | c), sorted
-    int nseg = 0;
-    for (long r = r0; r < r1;) {  // parts of the run inside one matrix
-      const int m = (int)(r / IT), k0 = (int)(r % IT), kn = (int)std::min<long>(r1 - r, IT - k0);
-      for (int c = k0 / 8; c <= (k0 + kn - 1) / 8; c++) chunks.push_back((uint32_t)m << 8 | (uint32_t)c);
-      for (int w = 0; w < kWaves; w++) {
-        const int col = m * NPg + w % NPg, sub = w / NPg;
-        const int a0 = k0 + (int)((long)kn * sub / W), a1 = k0 + (int)((long)kn * (sub + 1) / W);
-        if (a1 <= a0) continue;
-        uint32_t *seg = &wv[((size_t)b * kWaves + w) * 3];
-        const int si = seg[0] ? 1 : 0;
-        if (si == 1 && seg[1]) { pl.ok = false; return pl; }
-        seg[si] = (uint32_t)col | (uint32_t)a0 << 12 | (uint32_t)(a1 - a0) << 20 | gnseg[col] << 27;
-        gnseg[col]++;
+    const long r0 = R * b / G, r1 = R * (b + 1) / G;
+    if ((r1 - r0 + 3) / 4 > kMaxRg || r1 - r0 > IT) return pl;
+    w[(size_t)b * kPW + P_R0] = (uint32_t)r0;
+    w[(size_t)b * kPW + P_R1] = (uint32_t)r1;
+    int nrun = 0, npc = 0;
+    for (long r = r0; r < r1;) {
+      const long colg = r / IT, e = std::min(r1, (colg + 1) * IT);
+      const int mr = (int)(colg / NG), g = (int)(colg % NG), ls = hs + mr / 2, proj = mr & 1;
+      const int ka = (int)(r % IT), kb = ka + (int)(e - r);
+      npc += (kb - 1) / 8 - ka / 8 + 1;
+      for (int p = 0; p < 4; p++) {
+        const int col = (ls * 2 + proj) * NP + g * 4 + p;
+        if (p == 0) w[(size_t)b * kPW + P_JJ0 + nrun] = nseg[col];
+        nseg[col]++;
       }
-      nseg++;
-      r += kn;
+      nrun++;
+      r = e;
     }
-    if ((int)chunks.size() > kMaxPrep) { pl.ok = false; return pl; }
-    prep[(size_t)b * (1 + kMaxPrep)] = (uint32_t)chunks.size();
-    for (size_t i = 0; i < chunks.size(); i++) prep[(size_t)b * (1 + kMaxPrep) + 1 + i] = chunks[i];
-    for (int w = 0; w < kWaves; w++) {  // each segment's first chunk in the workgroup's list
-      uint32_t *seg = &wv[((size_t)b * kWaves + w) * 3];
-      for (int si = 0; si < 2; si++) {
-        if (!seg[si]) continue;
-        const int col = (int)(seg[si] & 0xFFFu), k0 = (int)((seg[si] >> 12) & 0xFFu);
-        const uint32_t key = (uint32_t)(col / NPg) << 8 | (uint32_t)(k0 / 8);
-        const size_t idx = (size_t)(std::find(chunks.begin(), chunks.end(), key) - chunks.begin());
-        seg[2] |= (uint32_t)idx << (4 * si);
-      }
-    }
-    (void)nseg;
+    if (nrun > 2 || npc > kMaxPrep) return pl;
   }
-  for (int c = 0; c < CG; c++)
-    if (gnseg[c] > (uint32_t)kMaxSeg) { pl.ok = false; return pl; }
-  std::vector<uint32_t> fin_t((size_t)nslot * NBI, 0u);
-  for (int c = 0; c < CG; c++) fin_t[(c / (2 * NPg)) * NBI + (c % NPg) / 4] += gnseg[c];
-  pl.words = wv;
-  pl.words.insert(pl.words.end(), prep.begin(), prep.end());
-  pl.words.insert(pl.words.end(), gnseg.begin(), gnseg.end());
-  pl.words.insert(pl.words.end(), fin_t.begin(), fin_t.end());
-  pl.part_floats = (size_t)CG * kMaxSeg * 32 + (size_t)nslot * hid;
+  // shared gate/up rows (one pair each): workgroup b takes [S b / G, S (b + 1) / G) inside one column
+  if (hs) {
+    const long S = 2L * NP * IT;
+    for (int b = 0; b < G; b++) {
+      const long s0 = S * b / G, s1 = S * (b + 1) / G;
+      if (s1 == s0) continue;
+      const int col = (int)(s0 / IT), k0 = (int)(s0 % IT), n = (int)(s1 - s0);
+      if ((s1 - 1) / IT != s0 / IT || n > kWaves || (k0 + n - 1) / 8 - k0 / 8 + 1 > kMaxSPrep) return pl;
+      w[(size_t)b * kPW + P_SCOL] = (uint32_t)col;
+      w[(size_t)b * kPW + P_SK0] = (uint32_t)k0;
+      w[(size_t)b * kPW + P_SN] = (uint32_t)n;
+      w[(size_t)b * kPW + P_SJJ] = nseg[col]++;
+    }
+  }
+  // down units: the shared slot's units and the routed ones, each split evenly; one unit per wave (the shared one on
+  // the last non-control wave), the control wave none
+  const long US = hs ? UPS : 0, UR = (long)topk * UPS;
+  std::vector<int> hb_first((size_t)nslot * NBI, -1);
+  for (int b = 0; b < G; b++) {
+    std::vector<long> units;
+    const long s0 = US * b / G, s1 = US * (b + 1) / G, q0 = UR * b / G, q1 = UR * (b + 1) / G;
+    for (long u = q0; u < q1; u++) units.push_back(US + u);
+    if (s1 - s0 > 1) return pl;
+    const bool sh_unit = s1 > s0;
+    if ((long)units.size() + (sh_unit ? 1 : 0) > kWaves) return pl;
+    std::vector<uint32_t> hbs;
+    auto hslot = [&](long u) -> int {
+      const uint32_t id = (uint32_t)((u / UPS) * NBI + (u / (NBLK * 4)) % NBI);
+      for (size_t i = 0; i < hbs.size(); i++)
+        if (hbs[i] == id) return (int)i;
+      hbs.push_back(id);
+      return (int)hbs.size() - 1;
+    };
+    for (size_t i = 0; i < units.size(); i++) {  // routed units on the last waves
+      const int h = hslot(units[i]);
+      w[(size_t)b * kPW + P_DN + kWaves - units.size() + i] = (uint32_t)units[i] | (uint32_t)h << 24;
+    }
+    if (sh_unit) {  // the shared unit on wave 0
+      const int h = hslot(s0);
+      w[(size_t)b * kPW + P_DN + 0] = (uint32_t)s0 | (uint32_t)h << 24;
+    }
+    if ((int)hbs.size() > kMaxH) return pl;
+    if ((long)units.size() > kWaves - 2 * (long)hbs.size()) return pl;  // h loaders: the first 2 nh waves
+    if (sh_unit && units.size() == (size_t)kWaves) return pl;
+    w[(size_t)b * kPW + P_NH] = (uint32_t)hbs.size();
+    for (size_t i = 0; i < hbs.size(); i++) {
+      uint32_t v = hbs[i];
+      if (hb_first[hbs[i]] < 0) {  // the first workgroup computing an h block also stores its g / u sums
+        hb_first[hbs[i]] = b;
+        v |= 1u << 31;
+      }
+      w[(size_t)b * kPW + P_HB + i] = v;
+    }
+  }
+  // combine: output block c on workgroup c G / NBLK (spread over the XCDs)
+  for (int c = 0; c < NBLK; c++) w[(size_t)(c * G / NBLK) * kPW + P_COMB] = (uint32_t)c;
+  for (int c = 0; c < NCOL; c++)
+    if (nseg[c] > (uint32_t)IT) return pl;
+  pl.words = w;
+  pl.words.insert(pl.words.end(), nseg.begin(), nseg.end());
+  // tagged partials (u64 = 2 floats): gate/up [column][IT segs][32], down [slot][cb][hid]
+  pl.part_floats = 2 * ((size_t)NCOL * IT * 32 + (size_t)nslot * NBI * hid);
   pl.grid = G;
+  pl.ok = true;
   return pl;
 }
 
 bool moe_fused_supported(int K, int KS, int R, int hid, int inter, int ne, int topk) {
-  return R == 1 && step_fn(K, KS, hid, inter) != nullptr && ne <= kMaxExpertsV && topk <= kMaxTopkV &&
-         topk <= 64;
+  return R == 1 && step_fn(K, KS, hid, inter) != nullptr && ne <= kMaxExpertsV && topk <= kMaxTopkV;
 }
 
 void launch_moe_fused(const MoeArgs &a, int grid, hipStream_t s) {
@@ -772,6 +886,7 @@ void launch_moe_fused(const MoeArgs &a, int grid, hipStream_t s) {
            a.inter, a.R);
   if (grid <= 0) grid = moe_fused_grid();
   IJ_CHECK(grid * kWaves >= a.ne + a.has_sgate, "fused MoE: %d router rows on %d workgroups", a.ne + a.has_sgate, grid);
+  IJ_CHECK(a.units && a.part && a.fsync, "fused MoE: no plan");
   const size_t lds = step_lds(a.lay.K, KS);
   static std::vector<StepFn> attr_set;  // functions whose dynamic LDS limit is raised already
   if (std::find(attr_set.begin(), attr_set.end(), f) == attr_set.end()) {
