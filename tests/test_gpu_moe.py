@@ -150,6 +150,35 @@ def test_moe_fused_and_staged_paths_agree(eng, oracle, monkeypatch):
     check_layer(eng, oracle, m, oracle.MoeWeights(w), x)
 
 
+@pytest.mark.parametrize("Ks", [4, 5, 6])
+def test_moe_m1_k4_mtp_head(eng, oracle, Ks, monkeypatch):
+    """The MTP head's MoE at M=1: K4 routed experts (reference core/main_test.mm:371, mtp_k = 4) at the config-2
+    shape, with a K4 / K5 / K6 shared expert, on the fused single-row kernel (moe_step<4, Ks>); against the oracle
+    and the staged kernels."""
+    print(f"moe M=1 K4 shared K{Ks}", flush=True)
+    w = synth.moe_layer(110 + Ks, hid=2048, inter=512, ne=64, topk=10, K=4, shared=True, Ks=Ks, sgate=True)
+    W = oracle.MoeWeights(w)
+    m = eng.moe_create(w)
+    x = synth.bf16_values(np.random.default_rng(111 + Ks), 1, 2048)
+    y, _ = check_layer(eng, oracle, m, W, x)
+    assert np.array_equal(m.run(x), y)
+    monkeypatch.setenv("IJAH_MOE_PATH", "staged")
+    assert rel(eng.moe_create(w).run(x), y) < 5e-5  # same arithmetic, other f32 accumulation orders
+
+
+@pytest.mark.parametrize("R", [1, 4])
+def test_moe_reference_shape_2560(eng, oracle, R):
+    """The reference's own layer shape (hidden 2560, intermediate 640: kernels/fn_moe.metal:16), top-10 + shared,
+    K5 routed and K6 shared; one row (staged kernels) and four rows (the grouped matrix-core path)."""
+    print(f"moe 2560x640 R{R}", flush=True)
+    w = synth.moe_layer(120 + R, hid=2560, inter=640, ne=64, topk=10, K=5, shared=True, Ks=6, sgate=True)
+    W = oracle.MoeWeights(w)
+    m = eng.moe_create(w)
+    x = synth.bf16_values(np.random.default_rng(121 + R), R, 2560)
+    y, _ = check_layer(eng, oracle, m, W, x)
+    assert np.array_equal(m.run(x), y)
+
+
 # ---------------------------------------------------------------------------------------------- batched path (R >= 2)
 @pytest.mark.parametrize("R", [16, 200, 640])
 def test_moe_batch_chunks(eng, oracle, R):
@@ -197,6 +226,38 @@ def test_moe_verify_config4(eng, oracle):
     m = eng.moe_create(w)
     x = synth.bf16_values(np.random.default_rng(44), 16, 2048)
     check_layer(eng, oracle, m, W, x, exact=False)
+
+
+def test_moe_verify_config4_k4(eng, oracle):
+    """Config 4's K4 variant at full size: 16 rows of a 512-expert layer, top-10, K4 routed + K4 shared."""
+    print("moe verify R16 ne512 K4", flush=True)
+    w = synth.moe_layer(44, hid=2048, inter=512, ne=512, topk=10, K=4, shared=True, Ks=4)
+    W = oracle.MoeWeights(w)
+    m = eng.moe_create(w)
+    x = synth.bf16_values(np.random.default_rng(45), 16, 2048)
+    check_layer(eng, oracle, m, W, x, exact=False)
+
+
+def test_moe_prefill_config5_rows_vs_oracle(eng, oracle):
+    """Config 5 at full size with host weights (4096 rows, 512 experts, top-10 + shared, K5): sampled rows of the
+    grouped layer against the oracle directly (logits within one bf16 step, the route on the GPU's logits, the
+    row's output at rel-L2 1e-4 of the oracle's kernel arithmetic)."""
+    print("moe config5 R4096 sampled rows vs oracle", flush=True)
+    w = synth.moe_layer(5, hid=2048, inter=512, ne=512, topk=10, K=5, shared=True, Ks=5)
+    W = oracle.MoeWeights(w)
+    m = eng.moe_create(w)
+    x = synth.bf16_values(np.random.default_rng(6), 4096, 2048)
+    y = m.run(x)
+    assert np.isfinite(y).all()
+    lg, rt = m.read("logits", 4096), m.read("route", 4096)
+    for i in (0, 1, 777, 2048, 3001, 4095):
+        want_lg = oracle.router_logits(x[i], W.d["router"])
+        assert np.all(np.abs(lg[i] - want_lg) <= np.abs(want_lg) * 2 ** -7 + 1e-6), i
+        ids, wt = oracle.route(lg[i], 10)
+        assert np.array_equal(rt[i, :10], ids), i
+        assert np.allclose(rt[i, 10:].view(np.float32), wt, rtol=1e-6, atol=0), i
+        want = oracle.moe_experts(W, x[i:i + 1], rt[i:i + 1])
+        assert rel(y[i:i + 1], want) < 1e-4, i
 
 
 def test_moe_prefill_config5_rows_match_single_row(eng):
