@@ -45,7 +45,16 @@ void ensure_device() {
   static std::string err;
   std::call_once(once, [] {
     int n = 0;
-    if (hipGetDeviceCount(&n) != hipSuccess || n == 0) err = "no HIP device visible";
+    if (hipGetDeviceCount(&n) != hipSuccess || n == 0) {
+      err = "no HIP device visible";
+      return;
+    }
+    try {  // kernel attributes before any launch (and so before any stream capture)
+      init_batch_attrs();
+      init_fused_attrs();
+    } catch (const std::exception &e) {
+      err = e.what();
+    }
   });
   IJ_CHECK(err.empty(), "%s", err.c_str());
 }

@@ -169,6 +169,25 @@ NE_API int ne_exl3_lin_info(const ne_exl3_lin *l, int *in, int *out, int *K) {
   });
 }
 
+// Captures `work` on s into an executable graph. The capture is always ended, also when `work` throws: a stream left
+// capturing would record every later launch into an abandoned graph.
+static hipGraphExec_t capture_graph(hipStream_t s, hipGraph_t &g, const std::function<void()> &work) {
+  IJ_HIP(hipStreamSynchronize(s));
+  IJ_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+  try {
+    work();
+  } catch (...) {
+    hipGraph_t dead = nullptr;
+    (void)hipStreamEndCapture(s, &dead);
+    if (dead) (void)hipGraphDestroy(dead);
+    throw;
+  }
+  IJ_HIP(hipStreamEndCapture(s, &g));
+  hipGraphExec_t ge = nullptr;
+  IJ_HIP(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0));
+  return ge;
+}
+
 static void timed(hipStream_t s, double *gpu_ms, const std::function<void()> &work) {
   if (!gpu_ms) {
     work();
@@ -193,7 +212,10 @@ static void timed(hipStream_t s, double *gpu_ms, const std::function<void()> &wo
 // LinArgs of one run at R rows (the k-split scratch grown as needed)
 static LinArgs lin_args(ne_exl3_lin *l, int R, const float *x, float *y, const LinEpi &epi = LinEpi()) {
   const int S = l->splits(R);
-  if (S > l->part_S) {
+  if (S > l->part_S) {  // never while the stream is captured: a captured launch would keep the freed buffer
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    IJ_HIP(hipStreamIsCapturing(stream(), &cs));
+    IJ_CHECK(cs == hipStreamCaptureStatusNone, "linear: split scratch must grow before a stream capture");
     dev_free(l->part);
     l->part = dev_alloc<float>((size_t)S * kLinMaxRows * l->OTp * 16);
     l->part_S = S;
@@ -380,15 +402,13 @@ NE_API int ne_exl3_lin_time(ne_exl3_lin *const *lins, int n, int R, const ne_buf
         lin_args(lins[i], R, nullptr, nullptr);
         lin_args(lins[i], std::min(R, kLinSimdRows), nullptr, nullptr);
       }
-      IJ_HIP(hipStreamSynchronize(s));
-      IJ_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
-      size_t yo = 0;
-      for (int i = 0; i < n; i++) {
-        lin_launch(lins[i], R, (const float *)x->dev, ys + yo, s);
-        yo += (size_t)R * lins[i]->out;
-      }
-      IJ_HIP(hipStreamEndCapture(s, &g));
-      IJ_HIP(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0));
+      ge = capture_graph(s, g, [&] {
+        size_t yo = 0;
+        for (int i = 0; i < n; i++) {
+          lin_launch(lins[i], R, (const float *)x->dev, ys + yo, s);
+          yo += (size_t)R * lins[i]->out;
+        }
+      });
       for (int i = 0; i < warmup; i++) IJ_HIP(hipGraphLaunch(ge, s));
       double ms = 0;
       timed(s, &ms, [&] {
@@ -945,11 +965,9 @@ NE_API int ne_moe_time(ne_moe *const *layers, int n, int R, const ne_buf *x, int
       dev_free(ys);
     };
     try {
-      IJ_HIP(hipStreamSynchronize(s));
-      IJ_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
-      for (int i = 0; i < n; i++) layers[i]->launch(R, xp, ys + (size_t)i * R * hid, s);
-      IJ_HIP(hipStreamEndCapture(s, &g));
-      IJ_HIP(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0));
+      ge = capture_graph(s, g, [&] {
+        for (int i = 0; i < n; i++) layers[i]->launch(R, xp, ys + (size_t)i * R * hid, s);
+      });
       for (int i = 0; i < warmup; i++) IJ_HIP(hipGraphLaunch(ge, s));
       double ms = 0;
       timed(s, &ms, [&] {

@@ -987,6 +987,9 @@ static int rows_tier(int R) { return R <= 1 ? 1 : R <= 2 ? 2 : R <= 4 ? 4 : 8; }
 
 void launch_lin(const LinArgs &a, hipStream_t s) {
   const int NP = (a.OT + 1) / 2;
+  // every buffer a (possibly captured) launch uses is present and sized for this split
+  IJ_CHECK(a.tiles && a.suh && a.svh && a.x && a.y && a.xh && a.part && a.S >= 1 && a.IT % a.S == 0,
+           "linear launch: missing buffer or bad split (S %d of %d k tiles)", a.S, a.IT);
   if (a.R > kLinSimdRows || !a.cnt) hipLaunchKernelGGL(lin_prep, dim3(a.R * ((a.in + 127) / 128)), dim3(64), 0, s, a);
   if (a.R > kLinSimdRows) {
     launch_lin_mm(a, s);

@@ -153,6 +153,9 @@ void launch_lin(const LinArgs &a, hipStream_t s);
 void launch_hc_prep(const float *h, const uint16_t *nw, const uint16_t *iw, float *xn, float *ip, float *inj, int R,
                     int hid, hipStream_t s);
 void launch_lin_mm(const LinArgs &a, hipStream_t s);  // rows kLinSimdRows+1 .. kLinMaxRows (matrix cores)
+// raise the dynamic LDS limits of the kernels that need it: once, at device set-up (capi.cpp ensure_device)
+void init_batch_attrs();
+void init_fused_attrs();
 // W' fp16 bits [IT*16][OT*16] from re-laid tiles
 void launch_decode(const uint32_t *tiles, int IT, int OT, int K, uint16_t *w, hipStream_t s);
 

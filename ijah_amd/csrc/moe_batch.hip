@@ -1156,12 +1156,7 @@ __global__ __launch_bounds__(512, 6) void lin_mm(LinArgs a) {
 }
 template <int K>
 static void lin_mm_launch(const LinArgs &a, hipStream_t s) {
-  const size_t lds = GemmIo<K, 1, 32>::LDS;
-  static bool attr = false;
-  if (!attr) {
-    IJ_HIP(hipFuncSetAttribute((const void *)&lin_mm<K>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    attr = true;
-  }
+  const size_t lds = GemmIo<K, 1, 32>::LDS;  // (its dynamic LDS limit is raised by init_batch_attrs)
   const int NG = ((a.OT + 1) / 2 + kWavesG - 1) / kWavesG;
   hipLaunchKernelGGL(lin_mm<K>, dim3(NG * a.S), dim3(64 * kWavesG), lds, s, a);
 }
@@ -1187,14 +1182,6 @@ void launch_gemms_as(const MoeArgs &a, const MoeBatchBufs &b, hipStream_t s) {
   // the routed (K) and shared (KS) chunks use ring layouts of their own widths: room for the larger of each
   const size_t lg = std::max(GemmIo<K, 2, NR>::LDS, GemmIo<KS, 2, NR>::LDS);
   const size_t ld = std::max(GemmIo<K, 1, NR>::LDS, GemmIo<KS, 1, NR>::LDS);
-  static bool attr = false;
-  if (!attr) {
-    IJ_HIP(hipFuncSetAttribute((const void *)&bat_gateup<K, KS, TR, NR>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                              (int)lg));
-    IJ_HIP(hipFuncSetAttribute((const void *)&bat_down<K, KS, TR, NR>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                              (int)ld));
-    attr = true;
-  }
   hipLaunchKernelGGL((bat_gateup<K, KS, TR, NR>), dim3((b.max_chunks * (a.inter / 128) + 7) & ~7), dim3(64 * kWavesG), lg, s, a,
                      b.bk, b.chunks, b.rows, b.xh, b.hh);
   hipLaunchKernelGGL((bat_down<K, KS, TR, NR>), dim3((b.max_chunks * (a.hid / 256) + 7) & ~7), dim3(64 * kWavesG), ld, s, a,
@@ -1214,6 +1201,36 @@ void launch_gemms(const MoeArgs &a, const MoeBatchBufs &b, hipStream_t s) {
     launch_gemms_as<K, KS, false, kChunkRows>(a, b, s);
 }
 }  // namespace
+
+// Raises the dynamic LDS limit of every kernel that needs more than the default, once at device set-up: never
+// lazily at a first launch, which may happen inside a stream capture.
+template <int K, int KS, bool TR, int NR>
+static void gemm_attrs() {
+  const size_t lg = std::max(GemmIo<K, 2, NR>::LDS, GemmIo<KS, 2, NR>::LDS);
+  const size_t ld = std::max(GemmIo<K, 1, NR>::LDS, GemmIo<KS, 1, NR>::LDS);
+  IJ_HIP(hipFuncSetAttribute((const void *)&bat_gateup<K, KS, TR, NR>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)lg));
+  IJ_HIP(hipFuncSetAttribute((const void *)&bat_down<K, KS, TR, NR>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)ld));
+}
+template <int K, int KS>
+static void gemm_attrs_all() {
+  gemm_attrs<K, KS, true, kChunkRows>();
+  gemm_attrs<K, KS, false, 32>();
+  gemm_attrs<K, KS, false, kChunkRows>();
+}
+template <int K>
+static void lin_mm_attr() {
+  IJ_HIP(hipFuncSetAttribute((const void *)&lin_mm<K>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)GemmIo<K, 1, 32>::LDS));
+}
+void init_batch_attrs() {
+  IJ_HIP(hipFuncSetAttribute((const void *)&bat_place_prep, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPrepLds));
+  gemm_attrs_all<4, 4>(); gemm_attrs_all<5, 5>(); gemm_attrs_all<6, 6>(); gemm_attrs_all<4, 5>();
+  gemm_attrs_all<4, 6>(); gemm_attrs_all<5, 6>(); gemm_attrs_all<5, 4>(); gemm_attrs_all<6, 4>();
+  gemm_attrs_all<6, 5>();
+  lin_mm_attr<2>(); lin_mm_attr<3>(); lin_mm_attr<4>(); lin_mm_attr<5>(); lin_mm_attr<6>(); lin_mm_attr<7>(); lin_mm_attr<8>();
+}
 
 bool moe_batch_supported(int K, int KS, int hid, int inter, int ne, int topk) {
   const bool ks = (K >= 4 && K <= 6) && (KS >= 4 && KS <= 6);
@@ -1235,11 +1252,6 @@ void launch_moe_batch(const MoeArgs &a, const MoeBatchBufs &b, hipStream_t s) {
   if (!self_count) hipLaunchKernelGGL(bat_hist, dim3(kHistGroups), dim3(256), 0, s, a, b.bk);
   hipLaunchKernelGGL(bat_scan, dim3(1), dim3(1024), 0, s, a, b.bk, b.chunks, b.max_chunks, self_count);
   IJ_CHECK(a.had_hid == 128, "batched MoE: hidden size %d needs a 128-wide Hadamard", a.hid);
-  static bool prep_attr = false;
-  if (!prep_attr) {
-    IJ_HIP(hipFuncSetAttribute((const void *)&bat_place_prep, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPrepLds));
-    prep_attr = true;
-  }
   hipLaunchKernelGGL(bat_place_prep, dim3((S + kPrepWaves - 1) / kPrepWaves), dim3(64 * kPrepWaves), kPrepLds, s, a,
                      b.bk, b.rows, b.xh);
   const int KS = a.nslot > a.topk ? a.slay.K : a.lay.K;

@@ -887,16 +887,20 @@ void launch_moe_fused(const MoeArgs &a, int grid, hipStream_t s) {
   if (grid <= 0) grid = moe_fused_grid();
   IJ_CHECK(grid * kWaves >= a.ne + a.has_sgate, "fused MoE: %d router rows on %d workgroups", a.ne + a.has_sgate, grid);
   IJ_CHECK(a.units && a.part && a.fsync, "fused MoE: no plan");
-  const size_t lds = step_lds(a.lay.K, KS);
-  static std::vector<StepFn> attr_set;  // functions whose dynamic LDS limit is raised already
-  if (std::find(attr_set.begin(), attr_set.end(), f) == attr_set.end()) {
-    IJ_HIP(hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    attr_set.push_back(f);
-  }
+  const size_t lds = step_lds(a.lay.K, KS);  // (the dynamic LDS limit is raised by init_fused_attrs)
   void *args[] = {const_cast<MoeArgs *>(&a)};
   IJ_HIP(hipLaunchKernel(f, dim3(grid), dim3(64 * kWaves), args, lds, s));
 }
 
 const void *moe_fused_kernel(int K, int KS, int hid, int inter) { return step_fn(K, KS, hid, inter); }
+
+// every instance's dynamic LDS limit, once at device set-up (never inside a stream capture)
+void init_fused_attrs() {
+  for (int hid : {1024, 2048})
+    for (int K = 4; K <= 6; K++)
+      for (int KS = 4; KS <= 6; KS++)
+        if (const StepFn f = step_fn(K, KS, hid, hid / 4))
+          IJ_HIP(hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)step_lds(K, KS)));
+}
 
 }  // namespace ijah
