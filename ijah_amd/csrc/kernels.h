@@ -93,6 +93,7 @@ struct MoeBatchBufs {
   int max_chunks = 0;
 };
 bool moe_batch_supported(int K, int KS, int hid, int inter, int ne, int topk);
+bool moe_batch_exact(const MoeArgs &a);  // the batch keeps the one-row step's arithmetic (few rows)
 int moe_batch_max_chunks(int R, int ne, int topk, bool shared);
 void launch_moe_batch(const MoeArgs &a, const MoeBatchBufs &b, hipStream_t s);
 // Fused step logits: kLogitReplicas copies of [ne + 1] floats, moe_logit_stride(ne) floats apart (replica 0 is the

@@ -255,6 +255,35 @@ __global__ __launch_bounds__(512, 2) void bat_router_rows(MoeArgs a, int ngroups
   }
 }
 
+// Few rows (speculative verify): logits with the one-row step's arithmetic, so that a row of a batch routes exactly
+// as it would alone. Wave w of workgroup b: router column 4 b + w for every row; lane l keeps elements
+// [512 j + 8 l, +8) of the column, j < hid / 512, and chains one fmaf per element in that order, then the lanes'
+// sums meet in an xor butterfly over lane distances 32, 16, .., 1 (reference kernels/fn_moe.metal:50-67).
+__global__ __launch_bounds__(256) void bat_router_exact(MoeArgs a) {
+  const int lane = threadIdx.x & 63, col = blockIdx.x * 4 + (threadIdx.x >> 6), nc = a.hid / 512;
+  if (col >= a.ne + a.has_sgate) return;
+  const uint16_t *w = a.router + (uint64_t)col * a.hid + lane * 8;
+  for (int r = 0; r < a.R; r++) {
+    const float *x = a.x + (uint64_t)r * a.hid + lane * 8;
+    float acc = 0.f;
+    for (int j = 0; j < nc; j++) {
+      const uint4 wv = *(const uint4 *)(w + j * 512);
+      const float4 x0 = *(const float4 *)(x + j * 512), x1 = *(const float4 *)(x + j * 512 + 4);
+      acc = fmaf(x0.x, bf16_f32(wv.x & 0xFFFFu), acc);
+      acc = fmaf(x0.y, bf16_f32(wv.x >> 16), acc);
+      acc = fmaf(x0.z, bf16_f32(wv.y & 0xFFFFu), acc);
+      acc = fmaf(x0.w, bf16_f32(wv.y >> 16), acc);
+      acc = fmaf(x1.x, bf16_f32(wv.z & 0xFFFFu), acc);
+      acc = fmaf(x1.y, bf16_f32(wv.z >> 16), acc);
+      acc = fmaf(x1.z, bf16_f32(wv.w & 0xFFFFu), acc);
+      acc = fmaf(x1.w, bf16_f32(wv.w >> 16), acc);
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) acc += __shfl_xor(acc, o, 64);
+    if (lane == 0) a.logits[(uint64_t)r * (a.ne + 1) + col] = bf16_round(acc);
+  }
+}
+
 // ---------------------------------------------------------------------------------------------------- route
 // one wave per row
 template <int J>
@@ -602,6 +631,40 @@ __global__ __launch_bounds__(64 * kPrepWaves, 2) void bat_place_prep(MoeArgs a, 
   if (lane == 0) rows[(orow_p - xh) / (2 * a.hid)] = (uint32_t)s;
 }
 
+// Few rows (speculative verify): the same placement with the one-row step's prepared input, a lane butterfly per
+// 128-wide chunk: v = x * suh (f32), H_128 with 1/sqrt(128), fp16, kp order (reference kernels/fn_moe.metal:140-160)
+__global__ __launch_bounds__(256) void bat_place_exact(MoeArgs a, uint32_t *bk, uint32_t *rows, uint16_t *xh) {
+  const int lane = threadIdx.x & 63, s = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (s >= a.R * a.nslot) return;
+  const int r = s / a.nslot, k = s % a.nslot;
+  const uint32_t *offs = bk + (a.ne + 1);
+  uint32_t *cursor = bk + 2 * (a.ne + 1);
+  int e = a.ne;
+  if (k < a.topk) {
+    e = (int)a.route[(uint64_t)r * 2 * a.topk + k];
+    e = e < a.ne ? e : 0;
+  }
+  uint32_t pos = (uint32_t)r;  // the shared expert's list is every token in order
+  if (k < a.topk) {
+    uint32_t p0 = 0u;
+    if (lane == 0) p0 = atomicAdd(cursor + e, 1u);
+    pos = (uint32_t)__shfl(p0, 0, 64);
+  }
+  const uint32_t row = offs[e] + pos;
+  const uint8_t *eb = expert_block(a, e);
+  const float *x = a.x + (uint64_t)r * a.hid;
+  for (int q = 0; q < 2 * (a.hid / 128); q++) {
+    const int proj = q & 1, c = q >> 1;
+    const uint16_t *su = (const uint16_t *)(eb + su_of(a, e, proj)) + c * 128;
+    float v0 = x[c * 128 + lane] * h2f(su[lane]), v1 = x[c * 128 + lane + 64] * h2f(su[lane + 64]);
+    fwht2(v0, v1, lane, 128, a.sc_hid);
+    uint16_t *o = xh + (uint64_t)row * 2 * a.hid + proj * a.hid + c * 128;
+    o[kp(lane)] = f2h(v0);
+    o[kp(lane + 64)] = f2h(v1);
+  }
+  if (lane == 0) rows[row] = (uint32_t)s;
+}
+
 // ---------------------------------------------------------------------------------------------------- grouped GEMM
 // One workgroup (8 waves, two per SIMD) multiplies a chunk of up to 128 expert-sorted rows of A by one tile pair (32
 // columns) per wave of the expert's re-laid matrix (IT k tiles, IT even), two k tiles per step. There are NA A
@@ -707,7 +770,10 @@ __device__ __forceinline__ void decode_step(const uint8_t *src, const BLane<K> &
 __device__ __forceinline__ int a_swz(int r) { return ((r >> 1) ^ ((r >> 3) & 1)) & 3; }
 // TR: the weights are the matrix cores' A operand and the rows their B operand, so acc[rb] holds the transposed
 // product: lane (n, h) value i = output column 8 (i / 4) + 4 h + i % 4 of the wave's 32, row 32 rb + n.
-template <int K, int NA, bool TR = false, int NR = kChunkRows>
+// FG > 0 (k range a whole number of 128-wide k chunks from a chunk boundary): the one-row step's summation order
+// instead of one chain: each k chunk's sum a chain of 8 MFMAs from zero, the chunk sums folded left in groups of FG,
+// the group sums folded left (FG at least the chunk count: one left fold over the chunks).
+template <int K, int NA, bool TR = false, int NR = kChunkRows, int FG = 0>
 __device__ void chunk_gemm(const uint16_t *A, int lda, int ahalf, int aidx, int nrows, const uint8_t *tr, int IT,
                            int pair, uint8_t *lds, f32x16 (&acc)[NR / 32], uint64_t *dbg, int kt0, int nkt) {
   using Io = GemmIo<K, NA, NR>;
@@ -730,6 +796,8 @@ __device__ void chunk_gemm(const uint16_t *A, int lda, int ahalf, int aidx, int 
   for (int rb = 0; rb < NRB; rb++)
 #pragma unroll
     for (int i = 0; i < 16; i++) acc[rb][i] = 0.f;
+  static_assert(FG == 0 || !TR, "the one-row order on row-major products");
+  f32x16 grp[FG ? NRB : 1], tot[FG ? NRB : 1];  // FG: the open group's fold, the closed groups' fold
   // A(t): NR = 128: 16 rows of this wave per operand; NR = 32: the wave's slice of RW = 4 NA rows of operand
   // (RW w) / 32. Row r's 64 bytes (four 16-byte quarters q: k 8q .. 8q + 7) sit at r * 64 with quarter q in position
   // q ^ a_swz(r), so that a read of one quarter of consecutive rows is free of bank conflicts. DMA lane l fills
@@ -795,11 +863,37 @@ __device__ void chunk_gemm(const uint16_t *A, int lda, int ahalf, int aidx, int 
             acc[rb] = TR ? __builtin_amdgcn_mfma_f32_32x32x16_f16(h ? b1 : b0, af[rb], acc[rb], 0, 0, 0)
                          : __builtin_amdgcn_mfma_f32_32x32x16_f16(af[rb], h ? b1 : b0, acc[rb], 0, 0, 0);
       }
+      if constexpr (FG > 0) {
+        if (((t + 1) & 3) == 0) {  // k chunk (t + 1) / 4 - 1 complete (4 steps of 2 k tiles)
+          const int c = (t + 1) / 4 - 1, ci = c % FG;
+#pragma unroll
+          for (int rb = 0; rb < NRB; rb++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+              grp[rb][i] = ci == 0 ? acc[rb][i] : grp[rb][i] + acc[rb][i];
+              acc[rb][i] = 0.f;
+            }
+          if (ci == FG - 1) {
+#pragma unroll
+            for (int rb = 0; rb < NRB; rb++)
+#pragma unroll
+              for (int i = 0; i < 16; i++) tot[rb][i] = c + 1 == FG ? grp[rb][i] : tot[rb][i] + grp[rb][i];
+          }
+        }
+      }
       IJ_STAMP(t == 20, 1)
       // the matrix cores run while the next step's tiles decode
       if (t + 1 < NS) begin_step(t + 1, (u + 1) % U);
       IJ_STAMP(t == 20, 2)
     }
+  }
+  if constexpr (FG > 0) {
+    const int nc = NS / 4;  // k chunks; closed groups, and an open one past them
+    const bool closed = nc >= FG, open = nc % FG != 0;
+#pragma unroll
+    for (int rb = 0; rb < NRB; rb++)
+#pragma unroll
+      for (int i = 0; i < 16; i++) acc[rb][i] = !closed ? grp[rb][i] : open ? tot[rb][i] + grp[rb][i] : tot[rb][i];
   }
   IJ_STAMP(true, 5)
 #undef IJ_STAMP
@@ -850,9 +944,13 @@ __device__ __forceinline__ f32x16 h32_tile(const f32x16 &v, const f16x8 (&hA)[2]
   return T;
 }
 
+// EX (few rows, speculative verify): the one-row step's arithmetic throughout, so that every row is bit-identical
+// to that row run alone: k chunk sums folded in its order, and the SiLU with the precise exp and divide.
+constexpr int kFoldGroup = 4;        // gate/up: k chunks per group (the one-row step's tasks span 512 of k)
+constexpr int kFoldAll = 1 << 20;    // down: one left fold over the k chunks (the one-row step's per-block partials)
 // gate/up: chunk ch, 128-column block ib of inter; wave w: projection w / 4 (gate, up), pair 4 ib + w % 4
-template <int K, int KS, bool TR, int NR>
-__global__ __launch_bounds__(512, NR == kChunkRows ? 4 : 6) void bat_gateup(MoeArgs a, const uint32_t *bk, const uint32_t *chunks,
+template <int K, int KS, bool TR, int NR, bool EX = false>
+__global__ __launch_bounds__(512, NR == kChunkRows || EX ? 4 : 6) void bat_gateup(MoeArgs a, const uint32_t *bk, const uint32_t *chunks,
                                                      const uint32_t *rows, const uint16_t *xh, uint16_t *hh) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int nib = a.inter / 128;
@@ -868,9 +966,11 @@ __global__ __launch_bounds__(512, NR == kChunkRows ? 4 : 6) void bat_gateup(MoeA
   const uint16_t *A = xh + (uint64_t)row0 * 2 * a.hid;  // [row][gate | up][hid]
   const int pair = ib * 4 + (wave & 3);
   if (e >= a.ne)
-    chunk_gemm<KS, 2, TR, NR>(A, 2 * a.hid, a.hid, proj, nrows, blk + tr_of(a, e, proj), a.hid / 16, pair, lds, acc, a.trace, 0, a.hid / 16);
+    chunk_gemm<KS, 2, TR, NR, EX ? kFoldGroup : 0>(A, 2 * a.hid, a.hid, proj, nrows, blk + tr_of(a, e, proj), a.hid / 16,
+                                                   pair, lds, acc, a.trace, 0, a.hid / 16);
   else
-    chunk_gemm<K, 2, TR, NR>(A, 2 * a.hid, a.hid, proj, nrows, blk + tr_of(a, e, proj), a.hid / 16, pair, lds, acc, a.trace, 0, a.hid / 16);
+    chunk_gemm<K, 2, TR, NR, EX ? kFoldGroup : 0>(A, 2 * a.hid, a.hid, proj, nrows, blk + tr_of(a, e, proj), a.hid / 16,
+                                                  pair, lds, acc, a.trace, 0, a.hid / 16);
   if constexpr (!TR) {
   // epilogue per 32-row block: columns to LDS as [32][256] f32 (gate 0..127, up 128..255), then one wave per row
   float *ot = (float *)lds;
@@ -899,9 +999,16 @@ __global__ __launch_bounds__(512, NR == kChunkRows ? 4 : 6) void bat_gateup(MoeA
       u0 = u0 * su0;
       g1 = g1 * sg1;
       u1 = u1 * su1;
-      // SiLU with the hardware exp2 and reciprocal (~1 ulp each; the layer's tolerance is 1e-2)
-      float h0 = g0 * __builtin_amdgcn_rcpf(1.f + __expf(-g0)) * u0 * sd0;
-      float h1 = g1 * __builtin_amdgcn_rcpf(1.f + __expf(-g1)) * u1 * sd1;
+      // SiLU with the hardware exp2 and reciprocal (~1 ulp each; the layer's tolerance is 1e-2), or (EX) as the
+      // one-row step computes it
+      float h0, h1;
+      if constexpr (EX) {
+        h0 = g0 / (1.f + expf(-g0)) * u0 * sd0;
+        h1 = g1 / (1.f + expf(-g1)) * u1 * sd1;
+      } else {
+        h0 = g0 * __builtin_amdgcn_rcpf(1.f + __expf(-g0)) * u0 * sd0;
+        h1 = g1 * __builtin_amdgcn_rcpf(1.f + __expf(-g1)) * u1 * sd1;
+      }
       fwht2(h0, h1, lane, a.had_inter, a.sc_inter);
       uint16_t *out = hh + (uint64_t)(row0 + rb * 32 + r) * a.inter + ib * 128;
       out[kp(lane)] = f2h(h0);
@@ -994,8 +1101,8 @@ __global__ __launch_bounds__(512, NR == kChunkRows ? 4 : 6) void bat_gateup(MoeA
 
 // down: chunk ch, 256 columns of hid (output blocks 2 ob2, 2 ob2 + 1); wave w: pair 8 ob2 + w. Output per
 // (token, slot): H over each 128-column block, svh_d, the slot's route weight.
-template <int K, int KS, bool TR, int NR>
-__global__ __launch_bounds__(512, NR == kChunkRows ? 4 : 6) void bat_down(MoeArgs a, const uint32_t *bk, const uint32_t *chunks,
+template <int K, int KS, bool TR, int NR, bool EX = false>
+__global__ __launch_bounds__(512, NR == kChunkRows || EX ? 4 : 6) void bat_down(MoeArgs a, const uint32_t *bk, const uint32_t *chunks,
                                                    const uint32_t *rows, const uint16_t *hh, float *dnw) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int nob = a.hid / 256;
@@ -1015,9 +1122,11 @@ __global__ __launch_bounds__(512, NR == kChunkRows ? 4 : 6) void bat_down(MoeArg
   f32x16 acc[NRB];
   const uint16_t *A = hh + (uint64_t)row0 * a.inter;
   if (e >= a.ne)
-    chunk_gemm<KS, 1, TR, NR>(A, a.inter, 0, 0, nrows, blk + tr_of(a, e, 2), a.inter / 16, ob2 * 8 + wave, lds, acc, nullptr, 0, a.inter / 16);
+    chunk_gemm<KS, 1, TR, NR, EX ? kFoldAll : 0>(A, a.inter, 0, 0, nrows, blk + tr_of(a, e, 2), a.inter / 16,
+                                                 ob2 * 8 + wave, lds, acc, nullptr, 0, a.inter / 16);
   else
-    chunk_gemm<K, 1, TR, NR>(A, a.inter, 0, 0, nrows, blk + tr_of(a, e, 2), a.inter / 16, ob2 * 8 + wave, lds, acc, nullptr, 0, a.inter / 16);
+    chunk_gemm<K, 1, TR, NR, EX ? kFoldAll : 0>(A, a.inter, 0, 0, nrows, blk + tr_of(a, e, 2), a.inter / 16,
+                                                ob2 * 8 + wave, lds, acc, nullptr, 0, a.inter / 16);
   if (mt < nrows) {
     const int tok = sl / a.nslot, k = sl % a.nslot;
     m_dst[mt] = sl;
@@ -1177,26 +1286,29 @@ void launch_lin_mm(const LinArgs &a, hipStream_t s) {
 
 // ---------------------------------------------------------------------------------------------------- host side
 namespace {
-template <int K, int KS, bool TR, int NR>
+template <int K, int KS, bool TR, int NR, bool EX = false>
 void launch_gemms_as(const MoeArgs &a, const MoeBatchBufs &b, hipStream_t s) {
   // the routed (K) and shared (KS) chunks use ring layouts of their own widths: room for the larger of each
   const size_t lg = std::max(GemmIo<K, 2, NR>::LDS, GemmIo<KS, 2, NR>::LDS);
   const size_t ld = std::max(GemmIo<K, 1, NR>::LDS, GemmIo<KS, 1, NR>::LDS);
-  hipLaunchKernelGGL((bat_gateup<K, KS, TR, NR>), dim3((b.max_chunks * (a.inter / 128) + 7) & ~7), dim3(64 * kWavesG), lg, s, a,
-                     b.bk, b.chunks, b.rows, b.xh, b.hh);
-  hipLaunchKernelGGL((bat_down<K, KS, TR, NR>), dim3((b.max_chunks * (a.hid / 256) + 7) & ~7), dim3(64 * kWavesG), ld, s, a,
-                     b.bk, b.chunks, b.rows, b.hh, b.dnw);
+  hipLaunchKernelGGL((bat_gateup<K, KS, TR, NR, EX>), dim3((b.max_chunks * (a.inter / 128) + 7) & ~7),
+                     dim3(64 * kWavesG), lg, s, a, b.bk, b.chunks, b.rows, b.xh, b.hh);
+  hipLaunchKernelGGL((bat_down<K, KS, TR, NR, EX>), dim3((b.max_chunks * (a.hid / 256) + 7) & ~7), dim3(64 * kWavesG),
+                     ld, s, a, b.bk, b.chunks, b.rows, b.hh, b.dnw);
 }
 // Chunks of many rows (8 or more per routed expert on average) take the transposed products and the matrix-core
 // Hadamard epilogues; chunks of a row or two (speculative verify) the row-major products and lane butterflies, which
 // cost less there.
-// At most 32 rows (speculative verify) no chunk exceeds 32 rows: the one-row-block form, three workgroups per CU.
+// At most 32 rows (speculative verify) no chunk exceeds 32 rows: the one-row-block form, three workgroups per CU,
+// with the one-row step's arithmetic (every row bit-identical to the row run alone).
 template <int K, int KS>
 void launch_gemms(const MoeArgs &a, const MoeBatchBufs &b, hipStream_t s) {
-  if ((int64_t)a.R * a.topk >= 8LL * a.ne)
-    launch_gemms_as<K, KS, true, kChunkRows>(a, b, s);
+  if (moe_batch_exact(a))
+    launch_gemms_as<K, KS, false, 32, true>(a, b, s);
   else if (a.R <= 32)
     launch_gemms_as<K, KS, false, 32>(a, b, s);
+  else if ((int64_t)a.R * a.topk >= 8LL * a.ne)
+    launch_gemms_as<K, KS, true, kChunkRows>(a, b, s);
   else
     launch_gemms_as<K, KS, false, kChunkRows>(a, b, s);
 }
@@ -1204,18 +1316,19 @@ void launch_gemms(const MoeArgs &a, const MoeBatchBufs &b, hipStream_t s) {
 
 // Raises the dynamic LDS limit of every kernel that needs more than the default, once at device set-up: never
 // lazily at a first launch, which may happen inside a stream capture.
-template <int K, int KS, bool TR, int NR>
+template <int K, int KS, bool TR, int NR, bool EX = false>
 static void gemm_attrs() {
   const size_t lg = std::max(GemmIo<K, 2, NR>::LDS, GemmIo<KS, 2, NR>::LDS);
   const size_t ld = std::max(GemmIo<K, 1, NR>::LDS, GemmIo<KS, 1, NR>::LDS);
-  IJ_HIP(hipFuncSetAttribute((const void *)&bat_gateup<K, KS, TR, NR>, hipFuncAttributeMaxDynamicSharedMemorySize,
+  IJ_HIP(hipFuncSetAttribute((const void *)&bat_gateup<K, KS, TR, NR, EX>, hipFuncAttributeMaxDynamicSharedMemorySize,
                             (int)lg));
-  IJ_HIP(hipFuncSetAttribute((const void *)&bat_down<K, KS, TR, NR>, hipFuncAttributeMaxDynamicSharedMemorySize,
+  IJ_HIP(hipFuncSetAttribute((const void *)&bat_down<K, KS, TR, NR, EX>, hipFuncAttributeMaxDynamicSharedMemorySize,
                             (int)ld));
 }
 template <int K, int KS>
 static void gemm_attrs_all() {
   gemm_attrs<K, KS, true, kChunkRows>();
+  gemm_attrs<K, KS, false, 32, true>();
   gemm_attrs<K, KS, false, 32>();
   gemm_attrs<K, KS, false, kChunkRows>();
 }
@@ -1232,6 +1345,9 @@ void init_batch_attrs() {
   lin_mm_attr<2>(); lin_mm_attr<3>(); lin_mm_attr<4>(); lin_mm_attr<5>(); lin_mm_attr<6>(); lin_mm_attr<7>(); lin_mm_attr<8>();
 }
 
+// Few rows: every kernel keeps the one-row step's arithmetic (hidden size a multiple of 512 for its router rows)
+bool moe_batch_exact(const MoeArgs &a) { return a.R <= 32 && a.hid % 512 == 0; }
+
 bool moe_batch_supported(int K, int KS, int hid, int inter, int ne, int topk) {
   const bool ks = (K >= 4 && K <= 6) && (KS >= 4 && KS <= 6);
   return ks && hid % 256 == 0 && inter % 128 == 0 && hid <= 8192 && inter <= 4096 && ne < 1024 && topk <= 32;
@@ -1245,15 +1361,21 @@ void launch_moe_batch(const MoeArgs &a, const MoeBatchBufs &b, hipStream_t s) {
   if (a.R >= 512) {
     const int ng = (a.R + kRtRows - 1) / kRtRows;
     hipLaunchKernelGGL(bat_router_rows, dim3((ng * ((ncol + 127) / 128) + 7) & ~7), dim3(512), 0, s, a, ng);
-  } else
+  } else if (moe_batch_exact(a)) {
+    hipLaunchKernelGGL(bat_router_exact, dim3((ncol + 3) / 4), dim3(256), 0, s, a);
+  } else {
     hipLaunchKernelGGL(bat_router<1>, dim3((a.R + 31) / 32, (ncol + 31) / 32), dim3(64 * kRouterWaves), 0, s, a);
+  }
   hipLaunchKernelGGL(bat_route, dim3((a.R + 3) / 4), dim3(256), 0, s, a);
   const int self_count = a.R * a.topk < 4096;  // few slots: counted inside bat_scan
   if (!self_count) hipLaunchKernelGGL(bat_hist, dim3(kHistGroups), dim3(256), 0, s, a, b.bk);
   hipLaunchKernelGGL(bat_scan, dim3(1), dim3(1024), 0, s, a, b.bk, b.chunks, b.max_chunks, self_count);
   IJ_CHECK(a.had_hid == 128, "batched MoE: hidden size %d needs a 128-wide Hadamard", a.hid);
-  hipLaunchKernelGGL(bat_place_prep, dim3((S + kPrepWaves - 1) / kPrepWaves), dim3(64 * kPrepWaves), kPrepLds, s, a,
-                     b.bk, b.rows, b.xh);
+  if (moe_batch_exact(a))
+    hipLaunchKernelGGL(bat_place_exact, dim3((S + 3) / 4), dim3(256), 0, s, a, b.bk, b.rows, b.xh);
+  else
+    hipLaunchKernelGGL(bat_place_prep, dim3((S + kPrepWaves - 1) / kPrepWaves), dim3(64 * kPrepWaves), kPrepLds, s,
+                       a, b.bk, b.rows, b.xh);
   const int KS = a.nslot > a.topk ? a.slay.K : a.lay.K;
   bool done = false;
 #define IJ_BAT(k, ks)                        \

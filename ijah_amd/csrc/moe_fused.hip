@@ -8,15 +8,16 @@
 // visibility (~0.45 us between XCDs), with no counters, atomics or store-completion waits in between.
 //
 // Work (a host-built plan; slots in plan order: the shared expert first, then the routed slots):
-//   gate/up  rows (matrix m = 2 slot + proj, group g of 4 tile-pair columns, k tile), 4 tile pairs each. Workgroup b
-//            takes an equal run of the routed rows (waves: pair w & 3, a quarter w >> 2 of the run's k range) and the
-//            waves' products are summed in LDS: one partial per (column, workgroup run), `jj` numbering the runs of a
-//            column in k order. The shared expert's rows (one pair, 16 k tiles per workgroup at 2048 x 512, one k
-//            tile per wave) are requested at launch and decoded before the route is known.
+//   gate/up  tasks (matrix m = 2 slot + proj, group g of 4 tile-pair columns, k group of 512, tile pair): four
+//            128-wide k chunks, each on a wave of its own (the SIMDs share the decode), each chunk's sum a chain of 8
+//            MFMAs from zero; the chunk sums folded left, stored as the column's partial of that k group; a column's
+//            value is the left fold of its k group partials. The sums do not depend on how the tasks are spread over
+//            workgroups, and the batched kernels fold their k chunks the same way, so a row of a batch is
+//            bit-identical to the one-row step. Workgroup b takes an equal run of the routed tasks and of the shared
+//            expert's; the shared expert's tiles are requested at launch, before the route is known.
 //   down     units (slot, 128-wide block cb of the intermediate, 128-column output block c, pair) of 8 k tiles, one
-//            per wave: a workgroup takes an equal run (and a shared unit). It computes the h blocks its units read
-//            (H(g) svh_g, H(u) svh_u, SwiGLU, suh_d, H, fp16) from the gate/up partials itself, then stores one
-//            tagged partial per unit.
+//            per wave: a workgroup takes an equal run. It computes the h blocks its units read (H(g) svh_g, H(u)
+//            svh_u, SwiGLU, suh_d, H, fp16) from the gate/up partials itself, then stores one tagged partial per unit.
 //   combine  16 workgroups, one per 128-column output block: per slot the cb partials in order, H, svh_d, the route
 //            weight; the slots in slot order (the shared one last); the hyper-connection write when asked.
 // The launch tag comes from a u64 epoch that workgroup 0 advances at its end with one store.
@@ -37,40 +38,48 @@ constexpr int kWaves = 16;
 // Control wave: polls the logits and ranks them. Vector memory waits are in order, so a wave with tile streams in
 // flight would wait for them before its poll results: the control wave requests no tiles before the route.
 constexpr int kCtl = kWaves - 1;
-constexpr int kMaxRg = 11;         // routed gate/up tile pairs per wave
-constexpr int kMaxSg = 1;          // shared gate/up tile pairs per wave
-constexpr int kDnKt = 8;           // k tiles of a down unit (one 128-wide h block)
-constexpr int kMaxPrep = 8;        // prepared 128-chunks of the routed rows per workgroup
-constexpr int kMaxSPrep = 2;       // ... of the shared rows
+constexpr int kDnKt = 8;           // k tiles of a down unit (one 128-wide h block) and of a k chunk (LDS slot size)
+constexpr int kGrp = 4;            // k chunks per k group (a gate/up task: 32 k tiles of one tile pair)
+constexpr int kMaxSlots = 36;      // LDS slots (8 k tile pairs each) per workgroup
+constexpr int kUnitsPerWave = 3;
+constexpr int kMaxGT = 8;          // gate/up tasks per workgroup (shared and routed)
+constexpr int kMaxPrep = 8;        // routed prepared k chunks per workgroup (2 k groups)
+constexpr int kSpw = 8;            // the waves preparing the shared k group's chunks: kSpw .. kSpw + 3
 constexpr int kMaxH = 3;           // h blocks per workgroup (2 loader waves each)
+constexpr uint32_t kURouted = 1, kUShared = 2, kUDown = 3;  // unit word types (bits 31:30)
 constexpr int kMaxExpertsV = 1024;
 constexpr int kMaxTopkV = 16;      // the combine stages svh_d of every slot in LDS
-constexpr int kPW = 32;            // plan words per workgroup
+constexpr int kPW = 64;            // plan words per workgroup (one per lane)
 constexpr uint32_t kNone = ~0u;
 constexpr uint32_t kSpin = 1u << 22;  // bounded waits: far beyond any real wait
 enum { kWordErr = kSyncErrWord };
 
 // plan word offsets (per workgroup)
 enum {
-  P_R0 = 0, P_R1, P_JJ0, P_JJ1,       // routed gate/up rows [r0, r1); partial index of its first / second column run
-  P_SCOL, P_SK0, P_SN, P_SJJ,         // shared gate/up: column, first k tile, k tiles (one per wave), partial index
+  P_RT0 = 0, P_NRT,                    // routed gate/up tasks [rt0, rt0 + nrt) (global task index)
+  P_ST0, P_NST,                        // shared gate/up tasks
+  P_NRP, P_RP,                         // routed prep groups: count, then 2 keys (matrix * NKG + k group)
+  P_SPK = P_RP + 2,                    // the shared tasks' prep key (proj * NKG + k group), or kNone
   P_COMB,                              // combine output block, or kNone
   P_NH, P_HB,                          // h blocks: count, then kMaxH ids (slot * NBI + cb); bit 31: store its g / u sums
-  P_DN = 16                            // per wave: down unit | h slot << 24, or kNone
-};
+  P_U = 16                             // per wave kUnitsPerWave unit words: type << 30 | LDS slot << 24 | payload
+};                                     // (a k chunk of a gate/up task: prep group << 8 | task - rt0 (or - st0) << 2 |
+                                       // chunk; down unit: h slot << 20 | unit), or kNone
 
 __device__ __forceinline__ uint32_t ld_relaxed(const uint32_t *p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-// s_waitcnt vmcnt(n) for a run-time n (n above 15 waits as for 15, which only waits longer); completion is counted
-// in issue order, stores included
+// s_waitcnt vmcnt(n) for a run-time n (6-bit count: low 4 bits at [3:0], high 2 at [15:14]; n above 63 waits as for
+// 63, which only waits longer); completion is counted in issue order, stores included
 __device__ __forceinline__ void wait_vm(int n) {
-  switch (n < 15 ? n : 15) {
+  switch (n < 63 ? n : 63) {
 #define IJ_VM(k) \
-  case k: __builtin_amdgcn_s_waitcnt(0x0F70 | k); break;
-    IJ_VM(0) IJ_VM(1) IJ_VM(2) IJ_VM(3) IJ_VM(4) IJ_VM(5) IJ_VM(6) IJ_VM(7)
-    IJ_VM(8) IJ_VM(9) IJ_VM(10) IJ_VM(11) IJ_VM(12) IJ_VM(13) IJ_VM(14) IJ_VM(15)
+  case k: __builtin_amdgcn_s_waitcnt(0x0F70 | ((k) & 15) | (((k) >> 4) << 14)); break;
+#define IJ_VM4(k) IJ_VM(k) IJ_VM(k + 1) IJ_VM(k + 2) IJ_VM(k + 3)
+    IJ_VM4(0) IJ_VM4(4) IJ_VM4(8) IJ_VM4(12) IJ_VM4(16) IJ_VM4(20) IJ_VM4(24) IJ_VM4(28)
+    IJ_VM4(32) IJ_VM4(36) IJ_VM4(40) IJ_VM4(44) IJ_VM4(48) IJ_VM4(52) IJ_VM4(56) IJ_VM4(60)
+#undef IJ_VM4
 #undef IJ_VM
   }
 }
@@ -356,75 +365,92 @@ __device__ __forceinline__ void prep_chunk(const float *x, int chunk, _Float16 *
 // ---------------------------------------------------------------------------------------------------- the kernel
 template <int K, int KS, int HID, int INTER>
 __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
-  constexpr int KM = K > KS ? K : KS;
   constexpr int IT = HID / 16, NP = INTER / 32, NG = NP / 4, NBI = INTER / 128, NBLK = HID / 128;
+  constexpr int NKG = HID / (128 * kGrp);  // k groups
   constexpr int ITd = INTER / 16, UPS = NBI * NBLK * 4;  // down units per slot
   constexpr int HH = had_of(HID), HI = had_of(INTER);
-  constexpr uint32_t RG_B = kMaxRg * 64 * KM, SG_B = kMaxSg * 64 * KM, DN_B = kDnKt * 64 * KM;
-  constexpr uint32_t AREA = RG_B + SG_B + DN_B;  // a wave's tile bytes
-  extern __shared__ __attribute__((aligned(16))) uint8_t tiles[];  // kWaves x AREA; the combine reuses it
-  __shared__ __attribute__((aligned(16))) _Float16 prep[kMaxPrep][128];
-  __shared__ __attribute__((aligned(16))) _Float16 sprep[kMaxSPrep][128];
+  constexpr uint32_t SLOT = kDnKt * 64 * (K > KS ? K : KS);  // LDS bytes of one slot (8 k tile pairs)
+  extern __shared__ __attribute__((aligned(16))) uint8_t tiles[];  // kMaxSlots x SLOT; the combine reuses it
+  __shared__ __attribute__((aligned(16))) _Float16 prep[kMaxPrep][128];   // routed prep group i's chunk c at 4 i + c
+  __shared__ __attribute__((aligned(16))) _Float16 sprep[kGrp][128];      // the shared prep group's chunks
   __shared__ __attribute__((aligned(16))) _Float16 hl[kMaxH][128];
-  __shared__ float red[2][4][4][32];   // routed gate/up: [run column][quarter][pair][32]
-  __shared__ float sred[kWaves][32];   // shared gate/up per wave
   __shared__ float hsum[kMaxH][2][128];
+  __shared__ float csum[kMaxGT][kGrp][32];                                 // k chunk sums of the gate/up tasks
   __shared__ __attribute__((aligned(16))) uint16_t hvec[kMaxH][3][128];   // svh_g, svh_u, suh_d of each h block
   __shared__ __attribute__((aligned(16))) uint16_t csv[kMaxTopkV + 1][128]; // the combine's svh_d per slot
   __shared__ __attribute__((aligned(16))) float xl[HID];                    // the input row (staged at launch)
   __shared__ Route rt;
   __shared__ uint32_t s_tag, s_ok;
-  const int lane = threadIdx.x & 63, wave = (int)rfl(threadIdx.x >> 6), G = (int)gridDim.x;
+  const int lane = threadIdx.x & 63, wave = (int)rfl(threadIdx.x >> 6);
   const int hs = a.nslot > a.topk ? 1 : 0;
   // the workgroup's plan words, one per lane, read before any tile request and picked with readlane (a vector load
   // later would wait for the wave's tile streams)
-  const uint32_t plw = a.units[(size_t)blockIdx.x * kPW + (lane & (kPW - 1))];
+  const uint32_t plw = a.units[(size_t)blockIdx.x * kPW + lane];
   auto PL = [&](int i) { return (uint32_t)__builtin_amdgcn_readlane((int)plw, i); };
-  const uint32_t *nseg = a.units + (size_t)G * kPW;
-  uint64_t *part_gu = (uint64_t *)a.part;                                   // [column][seg][32]
-  uint64_t *part_dn = part_gu + (size_t)a.nslot * 2 * NP * IT * 32;         // [slot][cb][HID]
-  uint8_t *area = tiles + wave * AREA;
+  uint64_t *part_gu = (uint64_t *)a.part;                                   // [column][NKG groups][32]
+  uint64_t *part_dn = part_gu + (size_t)a.nslot * 2 * NP * NKG * 32;        // [slot][cb][HID]
   const float sch = a.sc_hid, sci = a.sc_inter;
+  // this wave's units (plan words; tiles in LDS slot `slot`): k chunks of gate/up tasks (a task: 32 k tiles of one
+  // tile pair, four k chunks of 8; each chunk's sum a chain of 8 MFMAs from zero, into LDS; the task's chunk sums are
+  // folded left in k order and stored as the column's partial of that k group), and at most one down unit (8 k
+  // tiles: one h block)
+  uint32_t uw[kUnitsPerWave];
+#pragma unroll
+  for (int k = 0; k < kUnitsPerWave; k++) uw[k] = PL(P_U + kUnitsPerWave * wave + k);
+  const uint32_t rt0 = PL(P_RT0), st0 = PL(P_ST0), spk = PL(P_SPK), nst = PL(P_NST), nrt = PL(P_NRT);
+  const int nrp = (int)PL(P_NRP), nh = (int)PL(P_NH);
+  const uint32_t comb = PL(P_COMB);
+  // task t (global, tile pair fastest) -> matrix (2 slot + proj for a routed one, proj for a shared one), group,
+  // k group, pair
+  auto task = [&](uint32_t t, int &m, int &g, int &kg, int &p) {
+    p = (int)(t & 3u);
+    kg = (int)((t >> 2) % NKG);
+    g = (int)((t / (4 * NKG)) % NG);
+    m = (int)(t / (4 * NKG * NG));
+  };
+  int nops = 0;  // tile / vector requests (loads) this wave has issued: waits count the ones issued after
   stamp(a, 0);
-  // ---- 0. before the route: router rows first (the route waits for them); the shared expert's gate/up tile, its
-  // suh chunks and its down unit, placed by the same closed-form splits the host plan uses (no plan word is needed
-  // before the route)
+
+  // ---- 0. before the route: router rows first (the route waits for them); the shared expert's units, its suh
+  // chunks, once this workgroup's logits are out
   const bool rrow = router_active<HID>(a);
   RouterRow<HID> rr;
   if (rrow) router_load<HID>(a, rr);
   if (threadIdx.x == 0) s_ok = 1;
-  if (wave == kCtl) {  // the epoch, then x into LDS for the routed prep (its polls' waits cover these requests)
+  if (wave == kCtl) {  // the epoch, then x into LDS (its polls' waits cover these requests)
     __builtin_amdgcn_s_setprio(3);  // the route is the critical path: this wave first on its SIMD
     uint64_t ep = 0;
     if (lane == 0) ep = ld_cg((const uint64_t *)a.fsync);
     if (lane == 0) s_tag = (uint32_t)ep + 1u;
     stream_tiles((const uint8_t *)a.x, 0, 0, 0, HID / 4, 8, (uint8_t *)xl);  // 4 HID bytes
   }
-  constexpr uint32_t SROWS = 2u * NP * IT;  // shared gate/up rows (proj, pair, k tile): [S b / G, S (b + 1) / G)
-  const uint32_t ss0 = hs ? SROWS * blockIdx.x / G : 0u, ss1 = hs ? SROWS * (blockIdx.x + 1) / G : 0u;
-  const uint32_t scol = ss1 > ss0 ? ss0 / IT : kNone, sk0 = ss0 % IT, sn = ss1 - ss0;
-  const bool has_sg = scol != kNone && wave < (int)sn;  // this wave's shared k tile: sk0 + wave
-  const int sm = (int)(scol / NP), sp = (int)(scol % NP);  // shared matrix (proj), pair
-  const int nsp = scol != kNone ? (int)((sk0 + sn - 1) / 8 - sk0 / 8 + 1) : 0;  // shared prep chunks
-  // the shared down unit [UPS b / G, UPS (b + 1) / G) (at most one) sits on wave 0
-  const uint32_t su0 = hs ? (uint32_t)UPS * blockIdx.x / G : 0u, su1 = hs ? (uint32_t)UPS * (blockIdx.x + 1) / G : 0u;
-  const bool dn_shared = su1 > su0 && wave == 0;
   lds_barrier();  // the epoch is known
   const uint32_t tag = s_tag, tag16 = (tag - 1u) % 65535u + 1u;
   if (rrow) router_finish<HID>(a, rr, tag16);
-  lds_barrier();  // this workgroup's logits are out: the router rows had HBM to themselves, the shared expert goes now
-  if (has_sg && wave != kCtl)  // (the control wave requests its tile after the route: its polls must not wait on it)
-    stream_tiles(a.shared + (sm ? a.slay.tr[1] : a.slay.tr[0]), IT, sp, (int)sk0 + wave, 1, 32u * KS, area + RG_B);
-  if (wave < nsp && lane < 16) {
-    const uint8_t *src = a.shared + (sm ? a.slay.su[1] : a.slay.su[0]) + (sk0 / 8 + wave) * 256;
+  lds_barrier();  // this workgroup's logits are out: the router rows had HBM to themselves
+  const bool sprep_w = spk != kNone && wave >= kSpw && wave < kSpw + kGrp;
+  if (sprep_w && lane < 16) {  // chunk c of the shared prep group's suh
+    const int proj = (int)(spk / NKG), kc = (int)(spk % NKG) * kGrp + (wave - kSpw);
+    const uint8_t *src = a.shared + (proj ? a.slay.su[1] : a.slay.su[0]) + kc * 256;
     __builtin_amdgcn_global_load_lds((const void *)(src + lane * 16),
-                                     (__attribute__((address_space(3))) void *)(sprep[wave]), 16, 0, 0);
+                                     (__attribute__((address_space(3))) void *)(sprep[wave - kSpw]), 16, 0, 0);
   }
-  if (dn_shared) {
-    const int u = (int)su0, cb = (u / (NBLK * 4)) % NBI, c = (u / 4) % NBLK, p = u % 4;
-    stream_tiles(a.shared + a.slay.tr[2], ITd, c * 4 + p, cb * kDnKt, kDnKt, 32u * KS, area + RG_B + SG_B);
+#pragma unroll
+  for (int k = 0; k < kUnitsPerWave; k++) {
+    const uint32_t u = uw[k];
+    if (u == kNone) continue;
+    const uint32_t type = u >> 30, slot = (u >> 24) & 0x3Fu;
+    if (type == kUShared) {
+      int m, g, kg, p;
+      task(st0 + ((u >> 2) & 0xFu), m, g, kg, p);
+      stream_tiles(a.shared + (m ? a.slay.tr[1] : a.slay.tr[0]), IT, g * 4 + p, (kg * kGrp + (int)(u & 3u)) * 8, 8,
+                   32u * KS, tiles + slot * SLOT);
+    } else if (type == kUDown && hs && (int)(u & 0xFFFFFu) / UPS == 0) {  // the shared slot's down unit
+      const int du = (int)(u & 0xFFFFFu), cb = (du / (NBLK * 4)) % NBI, c = (du / 4) % NBLK, p = du % 4;
+      stream_tiles(a.shared + a.slay.tr[2], ITd, c * 4 + p, cb * kDnKt, kDnKt, 32u * KS, tiles + slot * SLOT);
+    }
   }
-  f16x8 sgb = {}, dw[kDnKt];
+  f16x8 dw[kDnKt];
 
   // ---- 1. route (control wave), shared to every wave through LDS
   if (wave == kCtl) {
@@ -438,77 +464,56 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
   if (wave != kCtl) stamp(a, 2);
   const bool ok = s_ok != 0;
 
-  // ---- 2. requests: the routed prep chunks' suh, the routed gate/up tiles (up to two pieces), the routed down unit
-  // routed rows [r0, r1): row r = (matrix mr, group g, k tile); the run meets at most two (matrix, group) columns
-  const uint32_t dnw = PL(P_DN + wave);  // this wave's down unit (the shared one as above) and its h slot
-  const int du = dnw == kNone ? -1 : (int)(dnw & 0xFFFFFFu), dhs = (int)(dnw >> 24);
-  const int d_ls = du / UPS, d_cb = (du / (NBLK * 4)) % NBI, d_c = (du / 4) % NBLK, d_p = du % 4;
-  const uint32_t r0 = PL(P_R0), r1 = PL(P_R1);
-  struct Run {
-    int ls, proj, g, ka, kb;  // columns (ls, proj, 4 g .. 4 g + 3), k tiles [ka, kb)
-  };
-  auto mk_run = [&](uint32_t colg, uint32_t ka, uint32_t kb) {
-    const int mr = (int)(colg / NG);
-    return Run{hs + mr / 2, mr & 1, (int)(colg % NG), (int)ka, (int)kb};
-  };
-  const uint32_t eA = min(r1, (r0 / IT + 1) * IT);
-  const bool two = eA < r1;
-  const int nrun = r1 > r0 ? (two ? 2 : 1) : 0;
-  const Run run[2] = {mk_run(r0 / IT, r0 % IT, r0 % IT + (eA - r0)), mk_run(eA / IT, 0, two ? r1 - eA : 0)};
-  const int npc0 = nrun ? (run[0].kb - 1) / 8 - run[0].ka / 8 + 1 : 0;
-  const int npc = npc0 + (two ? (run[1].kb - 1) / 8 + 1 : 0);
-  const int pc0[2] = {0, npc0};  // first prep chunk index of each run
-  // this wave: pair w & 3 of each run, quarter w >> 2 of the rows [r0, r1)
-  const uint32_t wq0 = r0 + (r1 - r0) * (uint32_t)(wave >> 2) / 4, wq1 = r0 + (r1 - r0) * (uint32_t)((wave >> 2) + 1) / 4;
-  int pk0[2], pn[2];  // the wave's piece of each run: k tiles [pk0, pk0 + pn)
-  {
-    const uint32_t lo0 = max(r0, wq0), hi0 = min(eA, wq1), lo1 = max(eA, wq0), hi1 = min(r1, wq1);
-    pn[0] = hi0 > lo0 ? (int)(hi0 - lo0) : 0;
-    pk0[0] = run[0].ka + (int)(lo0 - r0);
-    pn[1] = two && hi1 > lo1 ? (int)(hi1 - lo1) : 0;
-    pk0[1] = (int)(lo1 - eA);
-  }
-  const int nh = (int)PL(P_NH);
-  const uint32_t comb = PL(P_COMB);
-  // Requests, in the order they are consumed. A CU returns its waves' requests roughly in issue order, and a wave
-  // issues all its requests before the next wave of its SIMD does: so every wave first requests the routed prep
-  // chunks' suh and its gate/up tiles (up to two pieces), and only after a workgroup barrier its later needs (down
-  // unit, small vectors), which would otherwise hold back the other waves' gate/up tiles.
-  int n_su = 0, n_p[2] = {0, 0}, n_dn = 0, n_pf = 0;
-  const _Float16 *pxs[2] = {nullptr, nullptr};
-  uint32_t poff[2] = {0, 0};
-  if (wave == kCtl && has_sg)
-    stream_tiles(a.shared + (sm ? a.slay.tr[1] : a.slay.tr[0]), IT, sp, (int)sk0 + wave, 1, 32u * KS, area + RG_B);
-  if (ok) {
-    if (wave < npc && lane < 16) {  // suh of prep chunk `wave`
-      const bool second = two && wave >= npc0;
-      const int rls = second ? run[1].ls : run[0].ls, rproj = second ? run[1].proj : run[0].proj;
-      const int kc = (second ? run[1].ka : run[0].ka) / 8 + (wave - (second ? npc0 : 0));
-      const uint8_t *src = slot_block(a, rt, rls) + su_off(a, rls, rproj) + kc * 256;
-      __builtin_amdgcn_global_load_lds((const void *)(src + lane * 16),
-                                       (__attribute__((address_space(3))) void *)(prep[wave]), 16, 0, 0);
-    }
-    n_su = wave < npc ? 1 : 0;
-    uint32_t off = 0;
+  // ---- 2. requests, in the order they are consumed. A CU returns its waves' requests roughly in issue order, and a
+  // wave issues all its requests before the next wave of its SIMD does: so every wave first requests the routed prep
+  // chunks' suh and its routed gate/up tasks' tiles, and only after a workgroup barrier its later needs (its routed
+  // down unit, small vectors), which would otherwise hold back the other waves' gate/up tiles.
+  int end_u[kUnitsPerWave];  // per unit: requests issued up to and including its own
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
-      if (!pn[i]) continue;
-      const int ls = run[i].ls;
-      poff[i] = off;
-      pxs[i] = &prep[pc0[i] + (pk0[i] / 8 - run[i].ka / 8)][0] + (pk0[i] % 8) * 16;
-      n_p[i] = stream_tiles(slot_block(a, rt, ls) + tr_off(a, ls, run[i].proj), IT, run[i].g * 4 + (wave & 3),
-                            pk0[i], pn[i], 32u * K, area + off);
-      off += (uint32_t)pn[i] * 64u * K;
+  for (int k = 0; k < kUnitsPerWave; k++) end_u[k] = 0;
+  const int n_su = ok && wave < kGrp * nrp ? 1 : 0;
+  if (n_su && lane < 16) {  // suh of chunk wave & 3 of routed prep group wave >> 2
+    const uint32_t key = PL(P_RP + (wave >> 2));
+    const int m = (int)(key / NKG), ls = hs + m / 2, kc = (int)(key % NKG) * kGrp + (wave & 3);
+    const uint8_t *src = slot_block(a, rt, ls) + su_off(a, ls, m & 1) + kc * 256;
+    __builtin_amdgcn_global_load_lds((const void *)(src + lane * 16),
+                                     (__attribute__((address_space(3))) void *)(prep[wave]), 16, 0, 0);
+  }
+  nops += n_su;
+  const int end_su = nops;
+  lds_barrier();  // every prep chunk's suh is requested ahead of the tile streams
+  if (ok) {
+#pragma unroll
+    for (int k = 0; k < kUnitsPerWave; k++) {
+      const uint32_t u = uw[k];
+      if (u == kNone || (u >> 30) != kURouted) continue;
+      int m, g, kg, p;
+      task(rt0 + ((u >> 2) & 0xFu), m, g, kg, p);
+      const int ls = hs + m / 2;
+      nops += stream_tiles(slot_block(a, rt, ls) + tr_off(a, ls, m & 1), IT, g * 4 + p, (kg * kGrp + (int)(u & 3u)) * 8,
+                           8, 32u * K, tiles + ((u >> 24) & 0x3Fu) * SLOT);
+      end_u[k] = nops;
     }
   }
   lds_barrier();
+  int dunit = -1, dslot = 0, dhs = 0, end_dn = 0;  // this wave's down unit, its LDS slot and h slot
+#pragma unroll
+  for (int k = 0; k < kUnitsPerWave; k++)
+    if (uw[k] != kNone && (uw[k] >> 30) == kUDown) {
+      dunit = (int)(uw[k] & 0xFFFFFu);
+      dhs = (int)((uw[k] >> 20) & 3u);
+      dslot = (int)((uw[k] >> 24) & 0x3Fu);
+    }
+  const int d_ls = dunit / UPS, d_cb = (dunit / (NBLK * 4)) % NBI, d_c = (dunit / 4) % NBLK, d_p = dunit % 4;
+  const bool dn_shared = dunit >= 0 && hs && d_ls == 0;
   if (ok) {
-    // after the barrier: every wave's gate/up requests are ahead of these in the CU's queue. The routed down unit's
-    // tiles; the small vectors the later phases read into LDS (the h prologue's svh_g, svh_u, suh_d of block `wave`;
-    // the combine's svh_d of slot ls = wave (mod 16))
-    if (du >= 0 && !dn_shared)
-      n_dn = stream_tiles(slot_block(a, rt, d_ls) + tr_off(a, d_ls, 2), ITd, d_c * 4 + d_p, d_cb * kDnKt, kDnKt,
-                          32u * K, area + RG_B + SG_B);
+    if (dunit >= 0 && !dn_shared) {
+      nops += stream_tiles(slot_block(a, rt, d_ls) + tr_off(a, d_ls, 2), ITd, d_c * 4 + d_p, d_cb * kDnKt, kDnKt,
+                           32u * K, tiles + dslot * SLOT);
+      end_dn = nops;
+    }
+    // small vectors the later phases read, into LDS: the h prologue's svh_g, svh_u, suh_d of block `wave`; the
+    // combine's svh_d of slot ls = wave (mod 16)
     if (wave < nh) {
       const uint32_t hb = PL(P_HB + wave) & 0x7FFFFFFFu;
       const int ls = (int)(hb / NBI), cb = (int)(hb % NBI);
@@ -519,7 +524,7 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
         if (lane < 16)
           __builtin_amdgcn_global_load_lds((const void *)(blk + offs[v] + cb * 256 + lane * 16),
                                            (__attribute__((address_space(3))) void *)(hvec[wave][v]), 16, 0, 0);
-      n_pf += 3;
+      nops += 3;
     }
     if (comb != kNone) {
       for (int ls = wave; ls < a.nslot; ls += kWaves) {
@@ -527,117 +532,100 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
           __builtin_amdgcn_global_load_lds(
               (const void *)(slot_block(a, rt, ls) + sv_off(a, ls, 2) + comb * 256 + lane * 16),
               (__attribute__((address_space(3))) void *)(csv[ls]), 16, 0, 0);
-        n_pf++;
+        nops++;
       }
     }
   }
   stamp(a, 3);
   // the shared expert while the routed tiles are on their way (its requests went out before the route): its prep
-  // chunks, its gate/up tile and its down unit's B operands; then the routed prep
-  wait_vm(n_su + n_p[0] + n_p[1] + n_dn + n_pf);
-  if (wave < nsp) prep_chunk<HH>(xl, (int)(sk0 / 8) + wave, sprep[wave], sch);
-  if (has_sg) sgb = decode_pair<KS>(area + RG_B, 0);
+  // chunks and its down unit's B operands; then the routed prep (suh chunk -> fp16(H(x suh)) in kp order, x from LDS:
+  // a global load now would wait for the tile streams)
+  wait_vm(nops);  // the requests issued before the route
+  if (sprep_w) prep_chunk<HH>(xl, (int)(spk % NKG) * kGrp + (wave - kSpw), sprep[wave - kSpw], sch);
   if (dn_shared) {
 #pragma unroll
-    for (int kt = 0; kt < kDnKt; kt++) dw[kt] = decode_pair<KS>(area + RG_B + SG_B, kt);
+    for (int kt = 0; kt < kDnKt; kt++) dw[kt] = decode_pair<KS>(tiles + dslot * SLOT, kt);
   }
-  stamp_w(a, 2);
-  if (ok && n_su) {  // the routed prep: suh chunk -> fp16(H(x suh)) in kp order (x from LDS: a global load now would
-                     // wait for the tile streams)
-    wait_vm(n_p[0] + n_p[1] + n_dn + n_pf);
-    const bool second = two && wave >= npc0;
-    const int kc = (second ? run[1].ka : run[0].ka) / 8 + (wave - (second ? npc0 : 0));
-    prep_chunk<HH>(xl, kc, prep[wave], sch);
+  if (n_su) {
+    wait_vm(nops - end_su);
+    const uint32_t key = PL(P_RP + (wave >> 2));
+    prep_chunk<HH>(xl, (int)(key % NKG) * kGrp + (wave & 3), prep[wave], sch);
   }
   lds_barrier();  // shared and routed prep chunks ready
-  {  // the shared gate/up product, summed over the waves in wave order by wave 0
-    f32x16 acc;
-    zero16(acc);
-    if (has_sg) {
-      const f16x8 av = *(const f16x8 *)(&sprep[0][0] + (sk0 % 8 + wave) * 16 + 8 * (lane >> 5));
-      acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, sgb, acc, 0, 0, 0);
-    }
-    if (lane < 32) sred[wave][lane] = acc[0];
-  }
-  lds_barrier();
-  // the shared partial goes out now: every workgroup's down units need the shared h block, so it must not wait for
-  // the routed gate/up
-  int n_st = 0;  // stores issued after the down requests (counted by vmcnt)
-  if (ok && scol != kNone && wave == 0 && lane < 32) {
-    float s = sred[0][lane];
-    for (int w = 1; w < kWaves; w++) s += sred[w][lane];
-    st_tag(part_gu + ((size_t)scol * IT + PL(P_SJJ)) * 32 + lane, s, tag);
-  }
-  if (ok && scol != kNone && wave == 0) n_st = 1;
-  stamp_w(a, 3);
-  // ---- 4. routed gate/up: each 1 KB of tiles -> the k tiles it completes
-  f32x16 acc[2];
-  zero16(acc[0]);
-  zero16(acc[1]);
+  // ---- 3. gate/up k chunks: the shared ones (tiles in since before the route), then the routed ones as their tiles
+  // arrive, each chunk's sum into LDS; then per task the fold of its chunk sums in k order, stored at once
   if (ok) {
-    const uint32_t pb = 64u * K;  // bytes of one k tile pair
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
-      if (!pn[i]) continue;
-      const int after = (i == 0 ? n_p[1] : 0) + n_dn + n_pf + n_st;
-      int kt0 = 0;
-      for (int j = 0; j < n_p[i]; j++) {
-        wait_vm(after + n_p[i] - 1 - j);
-        if (i == 0 && j == 0) stamp_w(a, 0);
-        if (j == n_p[i] - 1) stamp_w(a, 1);
-        const int kt1 = j == n_p[i] - 1 ? pn[i] : (int)((uint32_t)(j + 1) * 1024u / pb);
-        if (kt1 > kt0) pair_mfma<K, 1024 / (64 * K) + 2>(area + poff[i], pxs[i], kt0, kt1, acc[i]);
-        kt0 = max(kt0, kt1);
+    for (int k = 0; k < kUnitsPerWave; k++) {
+      const uint32_t u = uw[k];
+      if (u == kNone || (u >> 30) != kUShared) continue;
+      const int c = (int)(u & 3u);
+      f32x16 acc;
+      zero16(acc);
+      pair_mfma<KS, 8>(tiles + ((u >> 24) & 0x3Fu) * SLOT, &sprep[c][0], 0, 8, acc);
+      if (lane < 32) csum[(u >> 2) & 0xFu][c][lane] = acc[0];
+    }
+    constexpr uint32_t pb = 64u * K;  // bytes of one k tile pair
+#pragma unroll
+    for (int k = 0; k < kUnitsPerWave; k++) {
+      const uint32_t u = uw[k];
+      if (u == kNone || (u >> 30) != kURouted) continue;
+      const uint8_t *tl = tiles + ((u >> 24) & 0x3Fu) * SLOT;
+      const int c = (int)(u & 3u);
+      const _Float16 *xs = &prep[kGrp * ((u >> 8) & 1u) + c][0] + 8 * (lane >> 5);
+      const int first = end_u[k] - dma_ops(8 * pb);  // requests issued before this chunk's
+      f32x16 acc;
+      zero16(acc);
+#pragma unroll
+      for (int kt = 0; kt < 8; kt++) {
+        const int req = (int)(((uint32_t)(kt + 1) * pb - 1u) >> 10);  // the request completing k tile kt
+        if (kt == 0 || req != (int)(((uint32_t)kt * pb - 1u) >> 10)) wait_vm(nops - (first + req + 1));
+        const f16x8 bv = decode_pair<K>(tl, kt);
+        const f16x8 av = *(const f16x8 *)(xs + kt * 16);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bv, acc, 0, 0, 0);
       }
+      if (lane < 32) csum[nst + ((u >> 2) & 0xFu)][c][lane] = acc[0];
     }
   }
-  if (lane < 32) {
-    red[0][wave >> 2][wave & 3][lane] = acc[0][0];
-    red[1][wave >> 2][wave & 3][lane] = acc[1][0];
+  lds_barrier();  // every k chunk sum is in LDS
+  if (ok && wave < (int)(nst + nrt) && lane < 32) {  // task `wave`: the shared ones, then the routed ones
+    const bool sh = wave < (int)nst;
+    int m, g, kg, p;
+    task(sh ? st0 + (uint32_t)wave : rt0 + (uint32_t)wave - nst, m, g, kg, p);
+    float sv = csum[wave][0][lane];
+#pragma unroll
+    for (int c = 1; c < kGrp; c++) sv = sv + csum[wave][c][lane];
+    const uint32_t col = sh ? (uint32_t)(m * NP + g * 4 + p) : (uint32_t)(((hs + m / 2) * 2 + (m & 1)) * NP + g * 4 + p);
+    st_tag(part_gu + ((size_t)col * NKG + kg) * 32 + lane, sv, tag);
   }
   stamp(a, 4);
-  lds_barrier();
-  if (ok && wave < 4 * nrun && lane < 32) {  // run i = wave >> 2, pair wave & 3: the quarters in order
-    const int i = wave >> 2, p = wave & 3;
-    const float s = ((red[i][0][p][lane] + red[i][1][p][lane]) + red[i][2][p][lane]) + red[i][3][p][lane];
-    const int rls = i ? run[1].ls : run[0].ls, rproj = i ? run[1].proj : run[0].proj, rg = i ? run[1].g : run[0].g;
-    const uint32_t col = (uint32_t)((rls * 2 + rproj) * NP + rg * 4 + p);
-    st_tag(part_gu + ((size_t)col * IT + PL(P_JJ0 + i)) * 32 + lane, s, tag);
-  }
-  if (ok && wave < 4 * nrun) n_st++;
 
-  // ---- 5. the routed down unit's tiles into B operands; then the h blocks from the gate/up partials
-  if (ok && du >= 0 && !dn_shared) {
-    wait_vm(n_pf + n_st);
+  // ---- 4. the routed down unit's tiles into B operands; the h blocks from the gate/up partials (the NKG k group
+  // sums of each column folded left in k order)
+  if (ok && dunit >= 0 && !dn_shared) {
+    wait_vm(nops - end_dn);
 #pragma unroll
-    for (int kt = 0; kt < kDnKt; kt++) dw[kt] = decode_pair<K>(area + RG_B + SG_B, kt);
+    for (int kt = 0; kt < kDnKt; kt++) dw[kt] = decode_pair<K>(tiles + dslot * SLOT, kt);
   }
-  // h loaders: the first 2 nh waves, which the SIMDs serve first (oldest first) and so finish their gate/up first;
-  // the routed down units sit on the last waves, whose decode then yields to the remaining gate/up work. Wave (h slot,
-  // proj), lane: columns o = lane, lane + 64 of the block
-  const int lw = wave;
-  if (ok && lw < 2 * nh) {
-    const int hslot = lw >> 1, proj = lw & 1;
+  // h loaders: the first 2 nh waves, which the SIMDs serve first (oldest first); wave (h slot, proj), lane: columns
+  // o = lane, lane + 64 of the block
+  if (ok && wave < 2 * nh) {
+    const int hslot = wave >> 1, proj = wave & 1;
     const uint32_t hb = PL(P_HB + hslot) & 0x7FFFFFFFu;
     const int ls = (int)(hb / NBI), cb = (int)(hb % NBI);
     const uint32_t col0 = (uint32_t)((ls * 2 + proj) * NP + cb * 4 + (lane >> 5)), col1 = col0 + 2;
-    const int ns0 = (int)nseg[col0], ns1 = (int)nseg[col1];
-    const uint64_t *src0 = part_gu + (size_t)col0 * IT * 32 + (lane & 31), *src1 = part_gu + (size_t)col1 * IT * 32 + (lane & 31);
+    const uint64_t *src0 = part_gu + (size_t)col0 * NKG * 32 + (lane & 31);
+    const uint64_t *src1 = part_gu + (size_t)col1 * NKG * 32 + (lane & 31);
     float s0 = 0.f, s1 = 0.f;
     bool got = false;
     for (uint32_t it = 0; it < kSpin; it++) {
       bool all = true;
-#pragma unroll 4
-      for (int jj = 0; jj < ns0; jj++) {
-        const uint64_t t = ld_cg(src0 + jj * 32);
-        all = all && tag_ok(t, tag);
-        s0 = jj == 0 ? tag_val(t) : s0 + tag_val(t);
-      }
-#pragma unroll 4
-      for (int jj = 0; jj < ns1; jj++) {
-        const uint64_t t = ld_cg(src1 + jj * 32);
-        all = all && tag_ok(t, tag);
-        s1 = jj == 0 ? tag_val(t) : s1 + tag_val(t);
+#pragma unroll
+      for (int jj = 0; jj < NKG; jj++) {
+        const uint64_t t0 = ld_cg(src0 + jj * 32), t1 = ld_cg(src1 + jj * 32);
+        all = all && tag_ok(t0, tag) && tag_ok(t1, tag);
+        s0 = jj == 0 ? tag_val(t0) : s0 + tag_val(t0);
+        s1 = jj == 0 ? tag_val(t1) : s1 + tag_val(t1);
       }
       if (__all(all)) {
         got = true;
@@ -674,8 +662,8 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
     hl[wave][kp(lane + 64)] = to_f16(h1);
   }
   lds_barrier();
-  // ---- 6. down: 8 k tiles of h against the unit's decoded tiles; one tagged partial per unit
-  if (ok && du >= 0) {
+  // ---- 5. down: 8 k tiles of h against the unit's decoded tiles; one tagged partial per unit
+  if (ok && dunit >= 0) {
     f32x16 d;
     zero16(d);
     const _Float16 *ha = &hl[dhs][0] + 8 * (lane >> 5);
@@ -764,7 +752,7 @@ StepFn step_fn(int K, int KS, int hid, int inter) {
   if (hid == 1024 && inter == 256) return step_for_k<1024, 256>(K, KS);
   return nullptr;
 }
-size_t step_lds(int K, int KS) { return (size_t)kWaves * (kMaxRg + kMaxSg + kDnKt) * 64 * std::max(K, KS); }
+size_t step_lds(int K, int KS) { return (size_t)kMaxSlots * kDnKt * 64 * std::max(K, KS); }
 }  // namespace
 
 int moe_fused_grid() {
@@ -781,95 +769,82 @@ int moe_fused_grid() {
 // limits; the layer then runs the staged path.
 MoePlan moe_fused_plan(int hid, int inter, int topk, int nslot, int G) {
   MoePlan pl;
-  const int IT = hid / 16, NP = inter / 32, NG = NP / 4, NBI = inter / 128, NBLK = hid / 128, UPS = NBI * NBLK * 4;
-  const int hs = nslot > topk ? 1 : 0, NCOL = nslot * 2 * NP;
-  if (inter % 128 || hid % 512 || G < 1 || NBLK > G) return pl;
-  std::vector<uint32_t> w((size_t)G * kPW, kNone), nseg(NCOL, 0u);
-  // routed gate/up rows: (routed matrix, group, k tile); workgroup b takes [R b / G, R (b + 1) / G)
-  const long R = (long)topk * 2 * NG * IT;
-  for (int b = 0; b < G; b++) {
-    const long r0 = R * b / G, r1 = R * (b + 1) / G;
-    if ((r1 - r0 + 3) / 4 > kMaxRg || r1 - r0 > IT) return pl;
-    w[(size_t)b * kPW + P_R0] = (uint32_t)r0;
-    w[(size_t)b * kPW + P_R1] = (uint32_t)r1;
-    int nrun = 0, npc = 0;
-    for (long r = r0; r < r1;) {
-      const long colg = r / IT, e = std::min(r1, (colg + 1) * IT);
-      const int mr = (int)(colg / NG), g = (int)(colg % NG), ls = hs + mr / 2, proj = mr & 1;
-      const int ka = (int)(r % IT), kb = ka + (int)(e - r);
-      npc += (kb - 1) / 8 - ka / 8 + 1;
-      for (int p = 0; p < 4; p++) {
-        const int col = (ls * 2 + proj) * NP + g * 4 + p;
-        if (p == 0) w[(size_t)b * kPW + P_JJ0 + nrun] = nseg[col];
-        nseg[col]++;
-      }
-      nrun++;
-      r = e;
-    }
-    if (nrun > 2 || npc > kMaxPrep) return pl;
-  }
-  // shared gate/up rows (one pair each): workgroup b takes [S b / G, S (b + 1) / G) inside one column
-  if (hs) {
-    const long S = 2L * NP * IT;
-    for (int b = 0; b < G; b++) {
-      const long s0 = S * b / G, s1 = S * (b + 1) / G;
-      if (s1 == s0) continue;
-      const int col = (int)(s0 / IT), k0 = (int)(s0 % IT), n = (int)(s1 - s0);
-      if ((s1 - 1) / IT != s0 / IT || n > kWaves || (k0 + n - 1) / 8 - k0 / 8 + 1 > kMaxSPrep) return pl;
-      w[(size_t)b * kPW + P_SCOL] = (uint32_t)col;
-      w[(size_t)b * kPW + P_SK0] = (uint32_t)k0;
-      w[(size_t)b * kPW + P_SN] = (uint32_t)n;
-      w[(size_t)b * kPW + P_SJJ] = nseg[col]++;
-    }
-  }
-  // down units: the shared slot's units and the routed ones, each split evenly; one unit per wave (the shared one on
-  // the last non-control wave), the control wave none
+  const int NP = inter / 32, NG = NP / 4, NBI = inter / 128, NBLK = hid / 128, UPS = NBI * NBLK * 4;
+  const int NKG = hid / (128 * kGrp), hs = nslot > topk ? 1 : 0, NCOL = nslot * 2 * NP;
+  if (inter % 128 || hid % (128 * kGrp) || G < 1 || NBLK > G) return pl;
+  std::vector<uint32_t> w((size_t)G * kPW, kNone);
+  // gate/up tasks (matrix, group, k group, pair; pair fastest): routed and shared; down units: shared, routed
+  const long TR = (long)topk * 2 * NG * NKG * 4, TS = hs ? 2L * NG * NKG * 4 : 0;
   const long US = hs ? UPS : 0, UR = (long)topk * UPS;
+  auto key_of = [&](long t) { return (uint32_t)((t / (4L * NKG * NG)) * NKG + (t / 4) % NKG); };  // matrix, k group
   std::vector<int> hb_first((size_t)nslot * NBI, -1);
   for (int b = 0; b < G; b++) {
-    std::vector<long> units;
-    const long s0 = US * b / G, s1 = US * (b + 1) / G, q0 = UR * b / G, q1 = UR * (b + 1) / G;
-    for (long u = q0; u < q1; u++) units.push_back(US + u);
-    if (s1 - s0 > 1) return pl;
-    const bool sh_unit = s1 > s0;
-    if ((long)units.size() + (sh_unit ? 1 : 0) > kWaves) return pl;
-    std::vector<uint32_t> hbs;
-    auto hslot = [&](long u) -> int {
-      const uint32_t id = (uint32_t)((u / UPS) * NBI + (u / (NBLK * 4)) % NBI);
-      for (size_t i = 0; i < hbs.size(); i++)
-        if (hbs[i] == id) return (int)i;
-      hbs.push_back(id);
-      return (int)hbs.size() - 1;
+    uint32_t *pw = &w[(size_t)b * kPW];
+    const long t0 = TR * b / G, t1 = TR * (b + 1) / G, s0 = TS * b / G, s1 = TS * (b + 1) / G;
+    if (t1 - t0 > 16 || s1 - s0 > 16) return pl;
+    pw[P_RT0] = (uint32_t)t0;
+    pw[P_NRT] = (uint32_t)(t1 - t0);
+    pw[P_ST0] = (uint32_t)s0;
+    pw[P_NST] = (uint32_t)(s1 - s0);
+    // prep groups: the distinct (matrix, k group) of the routed run (at most 2); one of the shared run
+    std::vector<uint32_t> keys;
+    for (long t = t0; t < t1; t++)
+      if (std::find(keys.begin(), keys.end(), key_of(t)) == keys.end()) keys.push_back(key_of(t));
+    if ((int)keys.size() * kGrp > kMaxPrep) return pl;
+    pw[P_NRP] = (uint32_t)keys.size();
+    for (size_t i = 0; i < keys.size(); i++) pw[P_RP + i] = keys[i];
+    for (long t = s0; t < s1; t++)
+      if (key_of(t) != key_of(s0)) return pl;
+    if (s1 > s0) pw[P_SPK] = key_of(s0);
+    int slot = 0;
+    std::vector<int> nu(kWaves, 0);
+    auto put = [&](int wave, uint32_t word) {
+      if (nu[wave] >= kUnitsPerWave || slot >= kMaxSlots) return false;
+      pw[P_U + kUnitsPerWave * wave + nu[wave]++] = word | (uint32_t)slot++ << 24;
+      return true;
     };
-    for (size_t i = 0; i < units.size(); i++) {  // routed units on the last waves
-      const int h = hslot(units[i]);
-      w[(size_t)b * kPW + P_DN + kWaves - units.size() + i] = (uint32_t)units[i] | (uint32_t)h << 24;
+    // gate/up tasks round robin over the waves (the control wave aside): the shared ones first (requested before the
+    // route), then the routed ones
+    int wv = 0;
+    if ((s1 - s0) + (t1 - t0) > kMaxGT) return pl;
+    for (long t = s0; t < s1; t++)
+      for (int c = 0; c < kGrp; c++, wv = (wv + 1) % kCtl)
+        if (!put(wv, kUShared << 30 | (uint32_t)(t - s0) << 2 | (uint32_t)c)) return pl;
+    for (long t = t0; t < t1; t++) {
+      const uint32_t pg = (uint32_t)(std::find(keys.begin(), keys.end(), key_of(t)) - keys.begin());
+      for (int c = 0; c < kGrp; c++, wv = (wv + 1) % kCtl)
+        if (!put(wv, kURouted << 30 | pg << 8 | (uint32_t)(t - t0) << 2 | (uint32_t)c)) return pl;
     }
-    if (sh_unit) {  // the shared unit on wave 0
-      const int h = hslot(s0);
-      w[(size_t)b * kPW + P_DN + 0] = (uint32_t)s0 | (uint32_t)h << 24;
+    // down units (global unit index: the shared slot's first), one per wave from the last non-control wave down
+    std::vector<long> units;
+    for (long u = US * b / G; u < US * (b + 1) / G; u++) units.push_back(u);
+    for (long u = UR * b / G; u < UR * (b + 1) / G; u++) units.push_back(US + u);
+    std::vector<uint32_t> hbs;
+    for (size_t i = 0; i < units.size(); i++) {
+      const long u = units[i];
+      const uint32_t id = (uint32_t)((u / UPS) * NBI + (u / (NBLK * 4)) % NBI);
+      size_t h = 0;
+      while (h < hbs.size() && hbs[h] != id) h++;
+      if (h == hbs.size()) hbs.push_back(id);
+      const int wave = kCtl - 1 - (int)i;
+      if (wave < 0 || h >= (size_t)kMaxH) return pl;
+      if (!put(wave, kUDown << 30 | (uint32_t)h << 20 | (uint32_t)u)) return pl;
     }
-    if ((int)hbs.size() > kMaxH) return pl;
-    if ((long)units.size() > kWaves - 2 * (long)hbs.size()) return pl;  // h loaders: the first 2 nh waves
-    if (sh_unit && units.size() == (size_t)kWaves) return pl;
-    w[(size_t)b * kPW + P_NH] = (uint32_t)hbs.size();
+    pw[P_NH] = (uint32_t)hbs.size();
     for (size_t i = 0; i < hbs.size(); i++) {
       uint32_t v = hbs[i];
       if (hb_first[hbs[i]] < 0) {  // the first workgroup computing an h block also stores its g / u sums
         hb_first[hbs[i]] = b;
         v |= 1u << 31;
       }
-      w[(size_t)b * kPW + P_HB + i] = v;
+      pw[P_HB + i] = v;
     }
   }
   // combine: output block c on workgroup c G / NBLK (spread over the XCDs)
   for (int c = 0; c < NBLK; c++) w[(size_t)(c * G / NBLK) * kPW + P_COMB] = (uint32_t)c;
-  for (int c = 0; c < NCOL; c++)
-    if (nseg[c] > (uint32_t)IT) return pl;
   pl.words = w;
-  pl.words.insert(pl.words.end(), nseg.begin(), nseg.end());
-  // tagged partials (u64 = 2 floats): gate/up [column][IT segs][32], down [slot][cb][hid]
-  pl.part_floats = 2 * ((size_t)NCOL * IT * 32 + (size_t)nslot * NBI * hid);
+  // tagged partials (u64 = 2 floats): gate/up [column][NKG k groups][32], down [slot][cb][hid]
+  pl.part_floats = 2 * ((size_t)NCOL * NKG * 32 + (size_t)nslot * NBI * hid);
   pl.grid = G;
   pl.ok = true;
   return pl;

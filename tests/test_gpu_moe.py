@@ -238,6 +238,46 @@ def test_moe_verify_config4_k4(eng, oracle):
     check_layer(eng, oracle, m, W, x, exact=False)
 
 
+def _rows_match_one_row(m, x, R):
+    """every row of an R-row batch equals the one-row step on that row, bit for bit: logits, route, shared gate,
+    layer output"""
+    y = m.run(x)
+    lg, rt, sg = m.read("logits", R), m.read("route", R), m.read("shared_gate", R)
+    for i in range(R):
+        y1 = m.run(x[i:i + 1])
+        assert np.array_equal(m.read("logits", 1)[0], lg[i]), ("logits", i)
+        assert np.array_equal(m.read("route", 1)[0], rt[i]), ("route", i)
+        assert np.array_equal(m.read("shared_gate", 1)[0], sg[i]), ("shared gate", i)
+        assert np.array_equal(y1[0], y[i]), ("output", i, rel(y1[0], y[i]))
+    return y
+
+
+@pytest.mark.parametrize("ne,K,Ks,sgate", [(64, 5, 5, True), (64, 4, 6, False), (64, 6, 6, True)])
+def test_moe_verify_rows_bit_identical_to_one_row(eng, ne, K, Ks, sgate):
+    """Speculative verify (16 rows through the grouped matrix-core kernels) against the fused one-row step: the same
+    router arithmetic, prepared input and k-chunk fold order, so each row is bit-identical to that row run alone."""
+    print(f"moe verify rows vs one row ne{ne} K{K}/{Ks} sgate={sgate}", flush=True)
+    w = synth.moe_layer(130 + K + Ks, hid=2048, inter=512, ne=ne, topk=10, K=K, shared=True, Ks=Ks, sgate=sgate)
+    m = eng.moe_create(w)
+    _rows_match_one_row(m, synth.bf16_values(np.random.default_rng(131 + K), 16, 2048), 16)
+
+
+def test_moe_verify_config4_rows_bit_identical(eng):
+    """Config 4 at full size (512 experts, top-10 + shared, K5, device-generated): every one of the 16 verify rows
+    equals the fused one-row step on that row, bit for bit."""
+    print("moe verify config4 rows vs one row", flush=True)
+    m = eng.moe_synth(2048, 512, 512, 10, 5, True, 5, seed=4)
+    _rows_match_one_row(m, synth.bf16_values(np.random.default_rng(46), 16, 2048), 16)
+
+
+def test_moe_verify_32_rows_small_shape_bit_identical(eng):
+    """The largest verify batch (32 rows) at hidden 1024 / inter 256 (two k groups per column), no shared expert."""
+    print("moe verify R32 1024x256 rows vs one row", flush=True)
+    w = synth.moe_layer(140, hid=1024, inter=256, ne=32, topk=8, K=5, shared=False)
+    m = eng.moe_create(w)
+    _rows_match_one_row(m, synth.bf16_values(np.random.default_rng(141), 32, 1024), 32)
+
+
 def test_moe_prefill_config5_rows_vs_oracle(eng, oracle):
     """Config 5 at full size with host weights (4096 rows, 512 experts, top-10 + shared, K5): sampled rows of the
     grouped layer against the oracle directly (logits within one bf16 step, the route on the GPU's logits, the
