@@ -98,6 +98,7 @@ static ne_exl3_lin *lin_create(const uint16_t *trellis, const uint16_t *suh, con
   check_dims(in, out, K);
   IJ_CHECK(trellis && suh && svh, "null array");
   ensure_device();
+  stream();  // the library's stream exists before any run (the allocation-free run then sets nothing up)
   auto l = std::make_unique<ne_exl3_lin>();
   l->in = in;
   l->out = out;
@@ -209,10 +210,19 @@ static void timed(hipStream_t s, double *gpu_ms, const std::function<void()> &wo
 
 }  // extern "C"
 
-// LinArgs of one run at R rows (the k-split scratch grown as needed)
-static LinArgs lin_args(ne_exl3_lin *l, int R, const float *x, float *y, const LinEpi &epi = LinEpi()) {
+// The buffers of one run taken from caller-provided scratch instead of the linear's own (the allocation-free entry
+// point): completion counters, prepared input, k-split partials.
+struct LinScratch {
+  uint32_t *cnt;
+  uint16_t *xh;
+  float *part;
+};
+
+// LinArgs of one run at R rows (the k-split scratch grown as needed, or taken from sc)
+static LinArgs lin_args(ne_exl3_lin *l, int R, const float *x, float *y, const LinEpi &epi = LinEpi(),
+                        const LinScratch *sc = nullptr) {
   const int S = l->splits(R);
-  if (S > l->part_S) {  // never while the stream is captured: a captured launch would keep the freed buffer
+  if (!sc && S > l->part_S) {  // never while the stream is captured: a captured launch would keep the freed buffer
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     IJ_HIP(hipStreamIsCapturing(stream(), &cs));
     IJ_CHECK(cs == hipStreamCaptureStatusNone, "linear: split scratch must grow before a stream capture");
@@ -237,22 +247,25 @@ static LinArgs lin_args(ne_exl3_lin *l, int R, const float *x, float *y, const L
   a.S = S;
   a.x = x;
   a.y = y;
-  a.xh = l->xh;
-  a.part = l->part;
+  a.xh = sc ? sc->xh : l->xh;
+  a.part = sc ? sc->part : l->part;
   a.epi = epi;
   // one launch unless its per-workgroup input preparation (each workgroup prepares the 128-blocks of its own k span)
   // adds up to more than ~8K block preparations (large outputs with few splits, e.g. a vocabulary head)
   const long prep_blocks = (long)(l->OTp / 2) * S * ((l->IT / S * 16 + 127) / 128 + 1);
-  a.cnt = (l->one_launch && R <= kLinSimdRows && prep_blocks <= 8192) ? l->cnt : nullptr;
+  a.cnt = (l->one_launch && R <= kLinSimdRows && prep_blocks <= 8192) ? (sc ? sc->cnt : l->cnt) : nullptr;
   return a;
 }
 
 // The launches of one run: rows beyond the GEMV's 8 take the matrix-core GEMM when the k tiles pair up (IT even) and
 // its k spans hold at least kLinMmMinSpan tiles; otherwise they run as groups of 8 rows through the GEMV path.
+static bool lin_one_pass(const ne_exl3_lin *l, int R) {
+  return R <= kLinSimdRows || (l->IT % 2 == 0 && l->IT >= kLinMmMinSpan);
+}
 static void lin_launch(ne_exl3_lin *l, int R, const float *x, float *y, hipStream_t s,
-                       const LinEpi &epi = LinEpi()) {
-  if (R <= kLinSimdRows || (l->IT % 2 == 0 && l->IT >= kLinMmMinSpan)) {
-    launch_lin(lin_args(l, R, x, y, epi), s);
+                       const LinEpi &epi = LinEpi(), const LinScratch *sc = nullptr) {
+  if (lin_one_pass(l, R)) {
+    launch_lin(lin_args(l, R, x, y, epi, sc), s);
     return;
   }
   const size_t ldy = epi.ldy ? epi.ldy : l->out;
@@ -260,8 +273,26 @@ static void lin_launch(ne_exl3_lin *l, int R, const float *x, float *y, hipStrea
     const int n = std::min(kLinSimdRows, R - r0);
     LinEpi e = epi;
     e.row0 = epi.row0 + r0;
-    launch_lin(lin_args(l, n, x + (size_t)r0 * l->in, y + (size_t)r0 * ldy, e), s);
+    launch_lin(lin_args(l, n, x + (size_t)r0 * l->in, y + (size_t)r0 * ldy, e, sc), s);
   }
+}
+
+// Scratch bytes of one run at R rows from the caller-provided scratch: counters, prepared input, partials (the
+// largest split of the run's launches), each part on a 256-byte boundary
+static size_t lin_scratch_layout(const ne_exl3_lin *l, int R, LinScratch *sc, uint8_t *base) {
+  auto up = [](size_t b) { return (b + 255) & ~(size_t)255; };
+  const int rows = lin_one_pass(l, R) ? R : std::min(R, kLinSimdRows);
+  int S = l->splits(rows);
+  if (!lin_one_pass(l, R)) S = std::max(S, l->splits(R % kLinSimdRows ? R % kLinSimdRows : kLinSimdRows));
+  const size_t ncnt = (size_t)((l->out + 127) / 128) * kSyncStride;
+  const size_t o_xh = up(ncnt * 4), o_part = o_xh + up((size_t)rows * l->in * 2);
+  const size_t total = o_part + up((size_t)S * rows * l->OTp * 16 * 4);
+  if (sc) {
+    sc->cnt = (uint32_t *)base;
+    sc->xh = (uint16_t *)(base + o_xh);
+    sc->part = (float *)(base + o_part);
+  }
+  return total;
 }
 
 extern "C" {
@@ -277,6 +308,30 @@ NE_API int ne_exl3_lin_run(ne_exl3_lin *l, int R, const ne_buf *x, uint64_t x_of
     const float *xp = (const float *)((const char *)x->dev + x_off);
     float *yp = (float *)((char *)y->dev + y_off);
     timed(stream(), gpu_ms, [&] { lin_launch(l, R, xp, yp, stream()); });
+  });
+}
+
+NE_API int ne_exl3_lin_run_noalloc(ne_exl3_lin *l, int R, const ne_buf *x, uint64_t x_off, ne_buf *y,
+                                   uint64_t y_off) {
+  return c_call([&] {
+    IJ_CHECK(l && x && y, "null argument");
+    IJ_CHECK(R >= 1 && R <= kLinMaxRows, "rows %d (1..%d)", R, kLinMaxRows);
+    IJ_CHECK(x_off % 4 == 0 && y_off % 4 == 0, "offsets must be 4-byte aligned");
+    IJ_CHECK(x_off + (uint64_t)R * l->in * 4 <= x->size, "x buffer too small for [%d][%d] f32", R, l->in);
+    IJ_CHECK(y_off + (uint64_t)R * l->out * 4 <= y->size, "y buffer too small for [%d][%d] f32", R, l->out);
+    const size_t need = lin_scratch_layout(l, R, nullptr, nullptr);
+    IJ_CHECK(need <= kNoAllocScratchBytes,
+             "no-alloc linear %d -> %d at %d rows needs %zu bytes of scratch; the maximum is %zu (use fewer rows "
+             "or ne_exl3_lin_run)", l->in, l->out, R, need, kNoAllocScratchBytes);
+    ensure_device();
+    LinScratch sc;
+    lin_scratch_layout(l, R, &sc, noalloc_scratch());
+    const hipStream_t s = stream();
+    // the completion counters start at zero (the previous call on this GPU left them so unless it failed)
+    launch_fill_u32(sc.cnt, (size_t)((l->out + 127) / 128) * kSyncStride, 0u, s);
+    lin_launch(l, R, (const float *)((const char *)x->dev + x_off), (float *)((char *)y->dev + y_off), s, LinEpi(),
+               &sc);
+    IJ_HIP(hipGetLastError());
   });
 }
 

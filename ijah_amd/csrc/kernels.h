@@ -103,6 +103,10 @@ __host__ __device__ inline int moe_logit_stride(int ne) { return (ne + 1 + 63) /
 // The sync block for R rows: header counters, per-slot gate/up counters, per-(row, 128-column block) counters; every
 // counter sits alone in a 256-byte line so that polling workgroups do not contend on one line.
 constexpr int kSyncStride = 64;  // u32 words between counters
+// the allocation-free linear's scratch (per GPU, for the process's lifetime): counters, prepared input, partials
+constexpr size_t kNoAllocScratchBytes = size_t(32) << 20;
+uint8_t *noalloc_scratch();  // this device's scratch address (taken at device set-up or the first call on it)
+void launch_fill_u32(uint32_t *p, size_t n, uint32_t v, hipStream_t s);
 inline size_t sync_words(int R, int nslot, int hid, int inter) {
   return kSyncStride * (8 + (size_t)R * nslot + (size_t)R * ((hid + 127) / 128) +
                         (size_t)R * nslot * ((inter + 127) / 128));

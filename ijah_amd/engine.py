@@ -83,6 +83,7 @@ SIGNATURES = {
     "ne_exl3_lin_free": (None, [_vp]),
     "ne_exl3_lin_info": (_i, [_vp, C.POINTER(_i), C.POINTER(_i), C.POINTER(_i)]),
     "ne_exl3_lin_run": (_i, [_vp, _i, _vp, _u64, _vp, _u64, _dp]),
+    "ne_exl3_lin_run_noalloc": (_i, [_vp, _i, _vp, _u64, _vp, _u64]),
     "ne_exl3_lin_run_epi": (_i, [_vp, _i, _vp, _u64, _vp, _u64, _vp, _dp]),
     "ne_hc_read": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _dp]),
     "ne_exl3_lin_decode": (_i, [_vp, _vp, _dp]),

@@ -50,6 +50,13 @@ NE_API int ne_exl3_lin_info(const ne_exl3_lin *l, int *in, int *out, int *K);
  * x f32 [R][in] at x_off, y f32 [R][out] at y_off; R 1..32 (1..8 on the VALU GEMV, 9..32 on the matrix cores). */
 NE_API int ne_exl3_lin_run(ne_exl3_lin *l, int R, const ne_buf *x, uint64_t x_off, ne_buf *y, uint64_t y_off,
                            double *gpu_ms);
+/* ne_exl3_lin_run that allocates nothing: no counterpart in the reference; for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops). Its counters, prepared input and k-split partials live
+ * in one fixed 32 MiB scratch array per GPU, held until the process ends; a run needing more (e.g. a 151936-wide
+ * vocabulary head at 32 rows) is rejected with an error. Same results as ne_exl3_lin_run. Every call on one GPU
+ * shares that array: calls that overlap on one GPU (other streams or threads) race. Not timed (no gpu_ms). */
+NE_API int ne_exl3_lin_run_noalloc(ne_exl3_lin *l, int R, const ne_buf *x, uint64_t x_off, ne_buf *y,
+                                   uint64_t y_off);
 /* A fused epilogue on a linear's finished outputs v (reference kernels/trunk6/trunk6.metal:129-197, t6_epi_col, the
  * layer graph's q8 epilogues; rr = round to bf16 when refr, the reference rounding switch FC 0):
  *   0 none     y = v
