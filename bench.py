@@ -135,10 +135,80 @@ def measure_trunk(eng, R, steps, seed, min_bytes=300e6):
         out[name] = {"in": inp, "out": o, "K": K, "us": round(us, 3), "bytes": int(nbytes), "GBps": round(gbs, 1),
                      "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2)}
         print(f"trunk {name} R={R}: {out[name]}", file=sys.stderr, flush=True)
+    # q, k and v in one launch (one input, three linears: record_multi), over copies of the triple
+    trip = []
+    for name, inp, o, K in TRUNK[:3]:
+        rng = np.random.default_rng(seed + inp + o + K)
+        trip.append(synth.linear(rng, inp, o, K))
+    nb = sum(t.nbytes + su.nbytes + sv.nbytes for t, su, sv in trip)
+    copies = int(min(32, max(2, np.ceil(min_bytes / nb))))
+    lins = [eng.exl3_linear(*w) for _ in range(copies) for w in trip]
+    del trip
+    us = eng.lin_time_multi(lins, R, xb, group=3, warmup=2, reps=max(3, steps)) / copies
+    for m in lins:
+        m.free()
+    gbs = nb / (us * 1e-6) / 1e9
+    out["qkv_one_launch"] = {"us": round(us, 3), "bytes": int(nb), "GBps": round(gbs, 1),
+                             "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2)}
+    print(f"trunk qkv one launch R={R}: {out['qkv_one_launch']}", file=sys.stderr, flush=True)
     # at R rows the weights are read once for all rows: "GBps" is weight bytes over time
     qkvo = sum(out[n]["us"] for n in ("q", "k", "v", "o"))
     qkvo_b = sum(out[n]["bytes"] for n in ("q", "k", "v", "o"))
     out["qkvo_sum"] = {"us": round(qkvo, 3), "GBps": round(qkvo_b / (qkvo * 1e-6) / 1e9, 1)}
+    q1 = out["qkv_one_launch"]["us"] + out["o"]["us"]
+    out["qkv_one_launch_plus_o"] = {"us": round(q1, 3), "GBps": round(qkvo_b / (q1 * 1e-6) / 1e9, 1)}
+    return out
+
+
+def run_probes(eng, iters=4000):
+    """probe_mix (ijah_amd/csrc/probes.hip) on every CU at 1, 2, 4 and 8 waves per SIMD: mode 0 decode only, 1 MFMA
+    only, 2 decode feeding each wave's MFMA chain, 3 even waves decode / odd waves MFMA (ms per launch). Decode: weights
+    per second and SIMD cycles per weight at the measured shader clock; MFMA: dense f16 TFLOP/s."""
+    cus = eng.device_info().get("cus", 256) if hasattr(eng, "device_info") else 256
+    out = {}
+    for K in (5, 8):
+        rng = np.random.default_rng(K)
+        tiles = eng.from_numpy(rng.integers(0, 1 << 32, 8 * 64 * K // 4, dtype=np.uint32))
+        for wps in (1, 2, 4, 8):
+            grid = cus * wps  # 4 waves per workgroup: wps waves per SIMD
+            res = eng.alloc(grid * 4 * 64 * 4)
+            t, cyc = {}, {}
+            for mode in range(4):
+                eng.run_kernel("probe_mix", [tiles, np.int32(iters), np.int32(mode), res], (grid, 1, 1), (256, 1, 1),
+                               fconsts=[(10, "u32", K)], tg_mem=4 * 8 * 64 * K)  # warm
+                t[mode] = eng.run_kernel("probe_mix", [tiles, np.int32(iters), np.int32(mode), res], (grid, 1, 1),
+                                         (256, 1, 1), fconsts=[(10, "u32", K)], tg_mem=4 * 8 * 64 * K, reps=3) / 3
+                w = res.download(np.uint32, (grid * 4, 64))
+                cyc[mode] = float(np.median(w[:, 1]))
+                if mode == 0:  # where the waves ran: distinct (XCC, SE, SH, CU) and waves per SIMD; the s_memtime rate
+                    hw, xcc = w[:, 2].astype(np.int64), w[:, 3].astype(np.int64) & 0xF
+                    cu = (xcc << 8) | ((hw >> 8) & 0xFF)
+                    simd = (cu << 2) | ((hw >> 4) & 3)
+                    places = {"cus_used": int(len(np.unique(cu))),
+                              "max_waves_per_simd": int(np.bincount(np.unique(simd, return_inverse=True)[1]).max()),
+                              "memtime_MHz": round(float(np.median(w[:, 1] / np.maximum(w[:, 4], 1))) * 100, 1)}
+            waves = grid * 4
+            clk = places["memtime_MHz"] * 1e6  # the shader clock the waves saw (s_memtime vs the 100 MHz counter)
+            wts = waves * iters * 8 * 512  # weights decoded in modes 0 and 2
+            flops = waves * iters * 8 * 2 * 32 * 32 * 16  # modes 1 and 2
+            simds = cus * 4
+            key = f"K{K}_w{wps}"
+            out[key] = {
+                "ms": {str(m): round(v, 4) for m, v in t.items()},
+                "decode_Gweights_s": round(wts / (t[0] * 1e-3) / 1e9, 1),
+                "decode_simd_cycles_per_weight": round(t[0] * 1e-3 * clk * simds / wts, 4),
+                "mfma_TFLOPs": round(flops / (t[1] * 1e-3) / 1e12, 1),
+                "fused_vs_sum": round(t[2] / (t[0] + t[1]), 3),  # 1.0: no overlap, max/sum: full overlap
+                "fused_vs_max": round(t[2] / max(t[0], t[1]), 3),
+                "split_vs_half_sum": round(t[3] / ((t[0] + t[1]) / 2), 3),
+                "wave_cycles_median": {str(m): cyc[m] for m in cyc},
+                # s_memtime cycles per weight of one wave (its own view, no sharing assumptions)
+                "wave_cycles_per_weight_decode": round(cyc[0] / (iters * 8 * 512), 4),
+                **places,
+            }
+            res.free()
+            print(f"probe {key}: {out[key]}", file=sys.stderr, flush=True)
+        tiles.free()
     return out
 
 
@@ -181,6 +251,8 @@ def main():
     ap.add_argument("--hc-only", action="store_true", help="only measure the hyper-connection read and exit")
     ap.add_argument("--batch-rows", type=int, default=0, metavar="R",
                     help="only measure the grouped matrix-core layer at R rows (a 4-layer graph) and exit")
+    ap.add_argument("--probe", action="store_true",
+                    help="only run the decode / matrix-core probes (decode cost per weight, MFMA and decode overlap)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MB",
                     help="only run the plain copy kernel over MB MiB 5 times (scales --pmc byte counters) and exit")
     a = ap.parse_args()
@@ -197,6 +269,9 @@ def main():
         for _ in range(5):
             eng.run_kernel("copy_u128", [src, dst, np.uint64(n // 16)], (2048, 1, 1), (256, 1, 1))
         print(json.dumps({"copy_probe_bytes": n, "launches": 5}), flush=True)
+        return
+    if a.probe:
+        print(json.dumps(run_probes(eng)), flush=True)
         return
     if a.hc_only:
         print(json.dumps({"hc_read_m1": measure_hc_read(eng, 1, a.steps, a.seed + 5),

@@ -52,6 +52,7 @@ void ensure_device() {
     try {  // kernel attributes before any launch (and so before any stream capture)
       init_batch_attrs();
       init_fused_attrs();
+      init_lin_attrs();
       noalloc_scratch();  // the allocation-free linear's scratch address on this device
     } catch (const std::exception &e) {
       err = e.what();

@@ -211,6 +211,57 @@ __device__ __forceinline__ void decode4(const TileWords &w, uint32_t sh, f16x2 &
   b = mcg_pair(c[2], c[3]);
 }
 
+// s_waitcnt vmcnt(n) for a run-time n (6-bit count: low 4 bits at [3:0], high 2 at [15:14]; n above 63 waits as for
+// 63, which only waits longer); completion is counted in issue order, stores included
+__device__ __forceinline__ void wait_vm(int n) {
+  switch (n < 63 ? n : 63) {
+#define IJ_VM(k) \
+  case k: __builtin_amdgcn_s_waitcnt(0x0F70 | ((k) & 15) | (((k) >> 4) << 14)); break;
+#define IJ_VM4(k) IJ_VM(k) IJ_VM(k + 1) IJ_VM(k + 2) IJ_VM(k + 3)
+    IJ_VM4(0) IJ_VM4(4) IJ_VM4(8) IJ_VM4(12) IJ_VM4(16) IJ_VM4(20) IJ_VM4(24) IJ_VM4(28)
+    IJ_VM4(32) IJ_VM4(36) IJ_VM4(40) IJ_VM4(44) IJ_VM4(48) IJ_VM4(52) IJ_VM4(56) IJ_VM4(60)
+#undef IJ_VM4
+#undef IJ_VM
+  }
+}
+// Tagged values between workgroups of one launch: the f32 value in the low word and the launch's tag in the high
+// word, stored and polled with device-coherent accesses, so that a consumer sees the data itself arrive.
+__device__ __forceinline__ void st_tag(uint64_t *p, float v, uint32_t tag) {
+  st_cg(p, (uint64_t)__float_as_uint(v) | ((uint64_t)tag << 32));
+}
+__device__ __forceinline__ float tag_val(uint64_t t) { return __uint_as_float((uint32_t)t); }
+__device__ __forceinline__ bool tag_ok(uint64_t t, uint32_t tag) { return (uint32_t)(t >> 32) == tag; }
+// the same with the count capped at 15 (waits at least as long): a 16-case switch, for k loops where the 64-case one
+// costs registers
+__device__ __forceinline__ void wait_vm15(int n) {
+  switch (n < 15 ? n : 15) {
+#define IJ_VM(k) \
+  case k: __builtin_amdgcn_s_waitcnt(0x0F70 | (k)); break;
+    IJ_VM(0) IJ_VM(1) IJ_VM(2) IJ_VM(3) IJ_VM(4) IJ_VM(5) IJ_VM(6) IJ_VM(7)
+    IJ_VM(8) IJ_VM(9) IJ_VM(10) IJ_VM(11) IJ_VM(12) IJ_VM(13) IJ_VM(14) IJ_VM(15)
+#undef IJ_VM
+  }
+}
+// the B operand of k tile kt of a pair staged in LDS (tile pairs of 64 K bytes in k order; the trellis words decoded
+// straight into v_mfma_f32_32x32x16_f16's B)
+template <int K>
+__device__ __forceinline__ f16x8 decode_pair(const uint8_t *tl, int kt) {
+  constexpr int TW = 8 * K;
+  const int lane = threadIdx.x & 63;
+  const BLane<K> B = b_lane<K>((uint32_t)lane);
+  const uint32_t *T0 = (const uint32_t *)tl + B.tile * TW + kt * 2 * TW;
+  TileWords w0, w1;
+  w0.w0 = T0[B.g0.i0];
+  w0.w1 = T0[B.g0.i1];
+  w0.w2 = kThreeWords<K> ? T0[B.g0.i2] : 0u;
+  w1.w0 = T0[B.g1.i0];
+  w1.w1 = T0[B.g1.i1];
+  w1.w2 = kThreeWords<K> ? T0[B.g1.i2] : 0u;
+  f16x2 l0, h0, l1, h1;
+  decode4<K>(w0, B.g0.sh, l0, h0);
+  decode4<K>(w1, B.g1.sh, l1, h1);
+  return f16x8{l0.x, l0.y, h0.x, h0.y, l1.x, l1.y, h1.x, h1.y};
+}
 __device__ __forceinline__ float dot4(f16x2 a, f16x2 b, f16x4 x, float acc) {
   acc = __builtin_amdgcn_fdot2(a, f16x2{x.x, x.y}, acc, false);
   return __builtin_amdgcn_fdot2(b, f16x2{x.z, x.w}, acc, false);

@@ -56,15 +56,10 @@ struct ne_exl3_lin {
   uint32_t *tiles = nullptr;
   uint16_t *suh = nullptr, *svh = nullptr;
   uint16_t *xh = nullptr;  // [kLinMaxRows][in]
-  float *part = nullptr;   // [S][kLinMaxRows][OTp*16]
+  float *part = nullptr;   // [S][part_rows][OTp*16]: k group partials
   uint32_t *cnt = nullptr; // per 128-column output block (the one-launch path's completion counters)
-  bool one_launch = true;  // IJAH_LIN_PATH=staged at creation: prep, GEMV and finish as three launches
-  int mm_min_kt = 8;       // the same for the matrix-core path (IJAH_LIN_MM_MINKT at creation, at least
-                           // kLinMmMinSpan): 8 beats 16 (q + k + v + o at 16 rows 50 vs 57 us)
-  int lin_wg_target = 512; // the GEMV's split count stops once tile pairs x splits reach this (IJAH_LIN_WGS)
-  int min_kt = 16;         // fewest k tiles per split on the GEMV path (IJAH_LIN_MINKT at creation): 16 beats 8
-                           // (k / v 2048 -> 512: 6.1 vs 6.5 us; more splits cost more in the finisher's sums)
-  int part_S = 0;
+  bool one_launch = true;  // IJAH_LIN_PATH=staged at creation: prep, GEMM and finish as three launches
+  int part_rows = 0;
   float *hc_scr = nullptr;  // the HC read's scratch when this is its up linear (xn, u, ip), hc_rows rows
   int hc_rows = 0;
   ~ne_exl3_lin() {
@@ -76,21 +71,11 @@ struct ne_exl3_lin {
     dev_free(part);
     dev_free(cnt);
   }
-  // k splits: smallest S (dividing IT, >= min_kt k tiles per split) that gives >= lin_wg_target workgroups, then enough to keep
-  // the staged input within 32 KiB of LDS at R rows
-  int splits(int R) const {
-    const int NP = OTp / 2;
-    int S = 1;
-    if (R > kLinSimdRows) {  // matrix cores: 8 pairs per workgroup, >= 512 workgroups, >= mm_min_kt k tiles per
-                             // split; the span IT / S must stay even (the GEMM runs it as steps of two k tiles)
-      while ((NP + 7) / 8 * S < 512 && IT % (4 * S) == 0 && IT / (2 * S) >= mm_min_kt) S *= 2;
-      return S;
-    }
-    while (NP * S < lin_wg_target && IT % (2 * S) == 0 && IT / (2 * S) >= min_kt) S *= 2;
-    const int RT = R <= 1 ? 1 : R <= 2 ? 2 : R <= 4 ? 4 : 8;
-    while ((size_t)RT * (IT / S) * 32 > 32768 && IT % (2 * S) == 0) S *= 2;
-    return S;
-  }
+  // k groups (the partials each output column sums in the finisher): fixed by the shape
+  int groups() const { return (IT + kLinGroupKt - 1) / kLinGroupKt; }
+  // the input preparation runs inside the GEMM (each tile pair's workgroups prepare their own k chunks) unless that
+  // repeats too much work: many tile pairs times many rows take one prep launch instead (same results)
+  bool prep_launch(int R) const { return (long)(OTp / 2) * R > 2048; }
 };
 
 static ne_exl3_lin *lin_create(const uint16_t *trellis, const uint16_t *suh, const uint16_t *svh, int in, int out,
@@ -123,9 +108,6 @@ static ne_exl3_lin *lin_create(const uint16_t *trellis, const uint16_t *suh, con
   IJ_HIP(hipMemset(l->cnt, 0, nc * 4));
   const char *path = getenv("IJAH_LIN_PATH");
   l->one_launch = !(path && std::string(path) == "staged");
-  if (const char *e = getenv("IJAH_LIN_MINKT")) l->min_kt = std::min(64, std::max(4, atoi(e)));
-  if (const char *e = getenv("IJAH_LIN_WGS")) l->lin_wg_target = std::min(8192, std::max(64, atoi(e)));
-  if (const char *e = getenv("IJAH_LIN_MM_MINKT")) l->mm_min_kt = std::min(64, std::max(kLinMmMinSpan, atoi(e)));
   return l.release();
 }
 
@@ -218,17 +200,19 @@ struct LinScratch {
   float *part;
 };
 
-// LinArgs of one run at R rows (the k-split scratch grown as needed, or taken from sc)
+// LinArgs of one run at R rows (the k group partials grown to R rows as needed, or taken from sc)
 static LinArgs lin_args(ne_exl3_lin *l, int R, const float *x, float *y, const LinEpi &epi = LinEpi(),
                         const LinScratch *sc = nullptr) {
-  const int S = l->splits(R);
-  if (!sc && S > l->part_S) {  // never while the stream is captured: a captured launch would keep the freed buffer
+  const int S = l->groups();
+  if (!sc && R > l->part_rows) {  // never while the stream is captured: a captured launch would keep the freed buffer
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     IJ_HIP(hipStreamIsCapturing(stream(), &cs));
-    IJ_CHECK(cs == hipStreamCaptureStatusNone, "linear: split scratch must grow before a stream capture");
+    IJ_CHECK(cs == hipStreamCaptureStatusNone, "linear: partial scratch must grow before a stream capture");
     dev_free(l->part);
-    l->part = dev_alloc<float>((size_t)S * kLinMaxRows * l->OTp * 16);
-    l->part_S = S;
+    const size_t n = (size_t)S * R * l->OTp * 16 * 2;  // u64 tagged partials on the one-launch path
+    l->part = dev_alloc<float>(n);
+    IJ_HIP(hipMemset(l->part, 0, n * 4));  // tag 0: no launch's (tags start at 1)
+    l->part_rows = R;
   }
   LinArgs a;
   a.tiles = l->tiles;
@@ -250,43 +234,39 @@ static LinArgs lin_args(ne_exl3_lin *l, int R, const float *x, float *y, const L
   a.xh = sc ? sc->xh : l->xh;
   a.part = sc ? sc->part : l->part;
   a.epi = epi;
-  // one launch unless its per-workgroup input preparation (each workgroup prepares the 128-blocks of its own k span)
-  // adds up to more than ~8K block preparations (large outputs with few splits, e.g. a vocabulary head)
-  const long prep_blocks = (long)(l->OTp / 2) * S * ((l->IT / S * 16 + 127) / 128 + 1);
-  a.cnt = (l->one_launch && R <= kLinSimdRows && prep_blocks <= 8192) ? (sc ? sc->cnt : l->cnt) : nullptr;
+  a.cnt = l->one_launch ? (sc ? sc->cnt : l->cnt) : nullptr;
+  a.xh_in = (!l->one_launch || l->prep_launch(R)) ? 1 : 0;
   return a;
 }
 
-// The launches of one run: rows beyond the GEMV's 8 take the matrix-core GEMM when the k tiles pair up (IT even) and
-// its k spans hold at least kLinMmMinSpan tiles; otherwise they run as groups of 8 rows through the GEMV path.
-static bool lin_one_pass(const ne_exl3_lin *l, int R) {
-  return R <= kLinSimdRows || (l->IT % 2 == 0 && l->IT >= kLinMmMinSpan);
-}
 static void lin_launch(ne_exl3_lin *l, int R, const float *x, float *y, hipStream_t s,
                        const LinEpi &epi = LinEpi(), const LinScratch *sc = nullptr) {
-  if (lin_one_pass(l, R)) {
-    launch_lin(lin_args(l, R, x, y, epi, sc), s);
-    return;
+  launch_lin(lin_args(l, R, x, y, epi, sc), s);
+}
+// several linears at R rows: one launch per run of consecutive linears of one K and path (at most `group` each)
+static void lin_launch_multi(ne_exl3_lin *const *l, int n, int R, const float *const *x, float *const *y,
+                             const LinEpi *epi, hipStream_t s, int group = kLinMulti) {
+  LinArgs a[kLinMulti];
+  int k = 0;
+  for (int i = 0; i < n; i++) {
+    const LinArgs ai = lin_args(l[i], R, x[i], y[i], epi ? epi[i] : LinEpi());
+    if (k > 0 && (k == group || ai.K != a[0].K || (bool)ai.cnt != (bool)a[0].cnt)) {
+      launch_lin_multi(a, k, s);
+      k = 0;
+    }
+    a[k++] = ai;
   }
-  const size_t ldy = epi.ldy ? epi.ldy : l->out;
-  for (int r0 = 0; r0 < R; r0 += kLinSimdRows) {
-    const int n = std::min(kLinSimdRows, R - r0);
-    LinEpi e = epi;
-    e.row0 = epi.row0 + r0;
-    launch_lin(lin_args(l, n, x + (size_t)r0 * l->in, y + (size_t)r0 * ldy, e, sc), s);
-  }
+  if (k) launch_lin_multi(a, k, s);
 }
 
-// Scratch bytes of one run at R rows from the caller-provided scratch: counters, prepared input, partials (the
-// largest split of the run's launches), each part on a 256-byte boundary
+static size_t lin_part_bytes(const ne_exl3_lin *l, int R) { return (size_t)l->groups() * R * l->OTp * 16 * 8; }
+// Scratch bytes of one run at R rows from the caller-provided scratch: counters, prepared input, partials, each part
+// on a 256-byte boundary
 static size_t lin_scratch_layout(const ne_exl3_lin *l, int R, LinScratch *sc, uint8_t *base) {
   auto up = [](size_t b) { return (b + 255) & ~(size_t)255; };
-  const int rows = lin_one_pass(l, R) ? R : std::min(R, kLinSimdRows);
-  int S = l->splits(rows);
-  if (!lin_one_pass(l, R)) S = std::max(S, l->splits(R % kLinSimdRows ? R % kLinSimdRows : kLinSimdRows));
   const size_t ncnt = (size_t)((l->out + 127) / 128) * kSyncStride;
-  const size_t o_xh = up(ncnt * 4), o_part = o_xh + up((size_t)rows * l->in * 2);
-  const size_t total = o_part + up((size_t)S * rows * l->OTp * 16 * 4);
+  const size_t o_xh = up(ncnt * 4), o_part = o_xh + up((size_t)R * l->in * 2);
+  const size_t total = o_part + up(lin_part_bytes(l, R));
   if (sc) {
     sc->cnt = (uint32_t *)base;
     sc->xh = (uint16_t *)(base + o_xh);
@@ -327,8 +307,10 @@ NE_API int ne_exl3_lin_run_noalloc(ne_exl3_lin *l, int R, const ne_buf *x, uint6
     LinScratch sc;
     lin_scratch_layout(l, R, &sc, noalloc_scratch());
     const hipStream_t s = stream();
-    // the completion counters start at zero (the previous call on this GPU left them so unless it failed)
-    launch_fill_u32(sc.cnt, (size_t)((l->out + 127) / 128) * kSyncStride, 0u, s);
+    // the block epochs and the tagged partials start at zero (tags restart at 1: no earlier call's partial, of this
+    // or another linear, carries a tag of this call)
+    launch_zero_u32(sc.cnt, (size_t)((l->out + 127) / 128) * kSyncStride, s);
+    launch_zero_u32((uint32_t *)sc.part, lin_part_bytes(l, R) / 4, s);
     lin_launch(l, R, (const float *)((const char *)x->dev + x_off), (float *)((char *)y->dev + y_off), s, LinEpi(),
                &sc);
     IJ_HIP(hipGetLastError());
@@ -433,48 +415,88 @@ NE_API int ne_hc_read(ne_exl3_lin *down, ne_exl3_lin *up, int R, const ne_buf *h
   });
 }
 
+}  // extern "C"
+
+// n linears at R rows reading x, captured once (one launch per linear, or multi-linear launches) and replayed:
+// GPU time per replay in us
+static double lin_time(ne_exl3_lin *const *lins, int n, int R, const ne_buf *x, int warmup, int reps, int group) {
+  IJ_CHECK(lins && n >= 1 && x && reps >= 1 && R >= 1 && R <= kLinMaxRows, "bad arguments");
+  size_t ytot = 0;
+  for (int i = 0; i < n; i++) {
+    IJ_CHECK(lins[i], "null linear %d", i);
+    IJ_CHECK((uint64_t)R * lins[i]->in * 4 <= x->size, "x buffer too small for linear %d", i);
+    ytot += (size_t)R * lins[i]->out;
+  }
+  hipStream_t s = stream();
+  float *ys = dev_alloc<float>(ytot);
+  hipGraph_t g = nullptr;
+  hipGraphExec_t ge = nullptr;
+  auto cleanup = [&] {
+    if (ge) (void)hipGraphExecDestroy(ge);
+    if (g) (void)hipGraphDestroy(g);
+    dev_free(ys);
+  };
+  double ms = 0;
+  try {
+    for (int i = 0; i < n; i++) lin_args(lins[i], R, nullptr, nullptr);  // grow the partials before capture
+    std::vector<const float *> xp(n, (const float *)x->dev);
+    std::vector<float *> yp(n);
+    for (int i = 0, yo = 0; i < n; yo += R * lins[i]->out, i++) yp[i] = ys + yo;
+    ge = capture_graph(s, g, [&] {
+      if (group > 1) {
+        lin_launch_multi(lins, n, R, xp.data(), yp.data(), nullptr, s, group);
+      } else {
+        for (int i = 0; i < n; i++) lin_launch(lins[i], R, xp[i], yp[i], s);
+      }
+    });
+    for (int i = 0; i < warmup; i++) IJ_HIP(hipGraphLaunch(ge, s));
+    timed(s, &ms, [&] {
+      for (int i = 0; i < reps; i++) IJ_HIP(hipGraphLaunch(ge, s));
+    });
+  } catch (...) {
+    cleanup();
+    throw;
+  }
+  cleanup();
+  return ms * 1000.0 / reps;
+}
+
+extern "C" {
+
 NE_API int ne_exl3_lin_time(ne_exl3_lin *const *lins, int n, int R, const ne_buf *x, int warmup, int reps,
                             double *us_per_lin) {
   return c_call([&] {
-    IJ_CHECK(lins && n >= 1 && x && us_per_lin && reps >= 1 && R >= 1 && R <= kLinMaxRows, "bad arguments");
-    size_t ytot = 0;
+    IJ_CHECK(us_per_lin, "null argument");
+    *us_per_lin = lin_time(lins, n, R, x, warmup, reps, 1) / n;
+  });
+}
+
+NE_API int ne_exl3_lin_time_multi(ne_exl3_lin *const *lins, int n, int group, int R, const ne_buf *x, int warmup,
+                                  int reps, double *us) {
+  return c_call([&] {
+    IJ_CHECK(us && group >= 1 && group <= kLinMulti, "bad arguments");
+    *us = lin_time(lins, n, R, x, warmup, reps, group);
+  });
+}
+
+NE_API int ne_exl3_lin_run_multi(ne_exl3_lin *const *lins, int n, int R, const ne_buf *const *x,
+                                 const uint64_t *x_off, ne_buf *const *y, const uint64_t *y_off, double *gpu_ms) {
+  return c_call([&] {
+    IJ_CHECK(lins && x && y && x_off && y_off && n >= 1 && n <= 64, "bad arguments");
+    IJ_CHECK(R >= 1 && R <= kLinMaxRows, "rows %d (1..%d)", R, kLinMaxRows);
+    std::vector<const float *> xp(n);
+    std::vector<float *> yp(n);
     for (int i = 0; i < n; i++) {
-      IJ_CHECK(lins[i], "null linear %d", i);
-      IJ_CHECK((uint64_t)R * lins[i]->in * 4 <= x->size, "x buffer too small for linear %d", i);
-      ytot += (size_t)R * lins[i]->out;
+      IJ_CHECK(lins[i] && x[i] && y[i], "null linear / buffer %d", i);
+      IJ_CHECK(x_off[i] % 4 == 0 && y_off[i] % 4 == 0, "offsets must be 4-byte aligned");
+      IJ_CHECK(x_off[i] + (uint64_t)R * lins[i]->in * 4 <= x[i]->size, "x %d too small for [%d][%d] f32", i, R,
+               lins[i]->in);
+      IJ_CHECK(y_off[i] + (uint64_t)R * lins[i]->out * 4 <= y[i]->size, "y %d too small for [%d][%d] f32", i, R,
+               lins[i]->out);
+      xp[i] = (const float *)((const char *)x[i]->dev + x_off[i]);
+      yp[i] = (float *)((char *)y[i]->dev + y_off[i]);
     }
-    hipStream_t s = stream();
-    float *ys = dev_alloc<float>(ytot);
-    hipGraph_t g = nullptr;
-    hipGraphExec_t ge = nullptr;
-    auto cleanup = [&] {
-      if (ge) (void)hipGraphExecDestroy(ge);
-      if (g) (void)hipGraphDestroy(g);
-      dev_free(ys);
-    };
-    try {
-      for (int i = 0; i < n; i++) {  // grow the split scratch before capture (both row paths lin_launch may take)
-        lin_args(lins[i], R, nullptr, nullptr);
-        lin_args(lins[i], std::min(R, kLinSimdRows), nullptr, nullptr);
-      }
-      ge = capture_graph(s, g, [&] {
-        size_t yo = 0;
-        for (int i = 0; i < n; i++) {
-          lin_launch(lins[i], R, (const float *)x->dev, ys + yo, s);
-          yo += (size_t)R * lins[i]->out;
-        }
-      });
-      for (int i = 0; i < warmup; i++) IJ_HIP(hipGraphLaunch(ge, s));
-      double ms = 0;
-      timed(s, &ms, [&] {
-        for (int i = 0; i < reps; i++) IJ_HIP(hipGraphLaunch(ge, s));
-      });
-      *us_per_lin = ms * 1000.0 / ((double)reps * n);
-    } catch (...) {
-      cleanup();
-      throw;
-    }
-    cleanup();
+    timed(stream(), gpu_ms, [&] { lin_launch_multi(lins, n, R, xp.data(), yp.data(), nullptr, stream()); });
   });
 }
 

@@ -584,212 +584,47 @@ __global__ __launch_bounds__(64) void lin_prep(LinArgs a) {
   if (i1 < a.in) a.xh[(uint64_t)r * a.in + kp(i1)] = f2h(v1);
 }
 
-// lin_gemv: grid = OT/2 pairs x S k-splits; 256 threads; xs = the split's span of xh for RT rows (zeros past R).
-// part[s][r][OTp*16] = raw inner outputs.
-template <int K, int RT>
-__global__ __launch_bounds__(256) void lin_gemv(LinArgs a) {
-  extern __shared__ _Float16 xs[];
-  const int NP = (a.OT + 1) / 2, OTp = 2 * NP;
-  const int p = blockIdx.x % NP, s = blockIdx.x / NP;
-  const int span = a.IT / a.S, k0 = s * span, k1 = k0 + span, n = span * 16;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const TileLane<K> L = tile_lane<K>((uint32_t)lane);
-  const uint32_t *pb = a.tiles + (uint64_t)p * a.IT * 2 * 8 * K;
-  PairBuf<K> buf;
-  pair_load<K>(buf, pb, L, k0 + wave, k1);
-  for (int i = threadIdx.x; i < RT * n / 8; i += blockDim.x) {
-    const int r = (i * 8) / n, o = (i * 8) % n;
-    uint4 v = make_uint4(0, 0, 0, 0);
-    if (r < a.R) v = *(const uint4 *)(a.xh + (uint64_t)r * a.in + k0 * 16 + o);
-    *(uint4 *)(xs + r * n + o) = v;
-  }
-  __syncthreads();
-  const int q = (lane >> 1) & 3;
-  float acc0[RT], acc1[RT];
-#pragma unroll
-  for (int r = 0; r < RT; r++) acc0[r] = acc1[r] = 0.f;
-  for (int tk0 = k0 + wave; tk0 < k1; tk0 += 4 * kPrefetch) {
-    if (tk0 != k0 + wave) pair_load<K>(buf, pb, L, tk0, k1);
-#pragma unroll
-    for (int j = 0; j < kPrefetch; j++) {
-      const int tk = tk0 + 4 * j;
-      if (tk < k1) {
-        f16x2 a0, b0, a1, b1;
-        decode4<K>(buf.w[j][0], L.sh, a0, b0);
-        decode4<K>(buf.w[j][1], L.sh, a1, b1);
-#pragma unroll
-        for (int r = 0; r < RT; r++) {
-          const f16x4 xv = *(const f16x4 *)(xs + r * n + (tk - k0) * 16 + 4 * q);
-          acc0[r] = dot4(a0, b0, xv, acc0[r]);
-          acc1[r] = dot4(a1, b1, xv, acc1[r]);
-        }
-      }
-    }
-  }
-  __shared__ float red[4 * 32 * RT];
-  const int col = (lane >> 3) + 8 * (lane & 1);
-#pragma unroll
-  for (int r = 0; r < RT; r++) {
-    float v0 = acc0[r], v1 = acc1[r];
-    v0 += __shfl_xor(v0, 2, 64);
-    v0 += __shfl_xor(v0, 4, 64);
-    v1 += __shfl_xor(v1, 2, 64);
-    v1 += __shfl_xor(v1, 4, 64);
-    if ((lane & 6) == 0) {
-      red[(r * 4 + wave) * 32 + col] = v0;
-      red[(r * 4 + wave) * 32 + 16 + col] = v1;
-    }
-  }
-  __syncthreads();
-  for (int i = threadIdx.x; i < a.R * 32; i += blockDim.x) {
-    const int r = i / 32, t = i % 32;
-    const float v = (red[(r * 4 + 0) * 32 + t] + red[(r * 4 + 1) * 32 + t]) +
-                    (red[(r * 4 + 2) * 32 + t] + red[(r * 4 + 3) * 32 + t]);
-    a.part[((uint64_t)s * a.R + r) * OTp * 16 + p * 32 + t] = v;
-  }
-}
-
-// lin_step: the whole linear at R <= 8 rows in one launch (reference kernels/trunk6/trunk6.metal: t6_prep :68-85,
-// t6_simd, t6_finish :199-214). Grid and GEMV as lin_gemv. Each workgroup first requests its weights, then prepares
-// the fp16(H_in(x * suh)) input of its own k span in LDS (the 128-element blocks overlapping the span; workgroups of
-// other pairs redo the same few blocks), runs the pair GEMV and stores its partials coherently. The last workgroup to
-// store into a 128-column output block (a counter per block, reset to 0 by that workgroup for the next launch) sums
-// the block's splits in split order and applies H_out and svh.
-template <int K, int RT>
-__global__ __launch_bounds__(256) void lin_step(LinArgs a) {
-  extern __shared__ _Float16 xs[];
-  __shared__ float red[4 * 32 * RT];
-  __shared__ int flag;
-  const int NP = (a.OT + 1) / 2, OTp = 2 * NP;
-  const int p = blockIdx.x % NP, s = blockIdx.x / NP;
-  const int span = a.IT / a.S, k0 = s * span, k1 = k0 + span, n = span * 16;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const TileLane<K> L = tile_lane<K>((uint32_t)lane);
-  const uint32_t *pb = a.tiles + (uint64_t)p * a.IT * 2 * 8 * K;
-  PairBuf<K> buf;
-  pair_load<K>(buf, pb, L, k0 + wave, k1);
-  // prepared input of the span: block b covers elements [128 b, 128 b + 128), lanes hold (lane, lane + 64)
-  const int e0 = k0 * 16, e1 = k1 * 16, b0 = e0 / 128, nb = (e1 + 127) / 128 - b0;
-  for (int it = wave; it < RT * nb; it += 4) {
-    const int r = it / nb, b = b0 + it % nb;
-    const int i0 = b * 128 + lane, i1 = i0 + 64;
-    float v0 = 0.f, v1 = 0.f;
-    if (r < a.R) {
-      const float *x = a.x + (uint64_t)r * a.in;
-      v0 = i0 < a.in ? x[i0] * h2f(a.suh[i0]) : 0.f;
-      v1 = i1 < a.in ? x[i1] * h2f(a.suh[i1]) : 0.f;
-      fwht2(v0, v1, lane, a.had_in, a.sc_in);
-    }
-    const int j0 = (int)kp((uint32_t)i0), j1 = (int)kp((uint32_t)i1);  // kp keeps an element in its 16-block
-    if (j0 >= e0 && j0 < e1) xs[r * n + j0 - e0] = to_f16(v0);
-    if (j1 >= e0 && j1 < e1) xs[r * n + j1 - e0] = to_f16(v1);
-  }
-  __syncthreads();
-  const int q = (lane >> 1) & 3;
-  float acc0[RT], acc1[RT];
-#pragma unroll
-  for (int r = 0; r < RT; r++) acc0[r] = acc1[r] = 0.f;
-  for (int tk0 = k0 + wave; tk0 < k1; tk0 += 4 * kPrefetch) {
-    if (tk0 != k0 + wave) pair_load<K>(buf, pb, L, tk0, k1);
-#pragma unroll
-    for (int j = 0; j < kPrefetch; j++) {
-      const int tk = tk0 + 4 * j;
-      if (tk < k1) {
-        f16x2 a0, b0v, a1, b1v;
-        decode4<K>(buf.w[j][0], L.sh, a0, b0v);
-        decode4<K>(buf.w[j][1], L.sh, a1, b1v);
-#pragma unroll
-        for (int r = 0; r < RT; r++) {
-          const f16x4 xv = *(const f16x4 *)(xs + r * n + (tk - k0) * 16 + 4 * q);
-          acc0[r] = dot4(a0, b0v, xv, acc0[r]);
-          acc1[r] = dot4(a1, b1v, xv, acc1[r]);
-        }
-      }
-    }
-  }
-  const int col = (lane >> 3) + 8 * (lane & 1);
-#pragma unroll
-  for (int r = 0; r < RT; r++) {
-    float v0 = acc0[r], v1 = acc1[r];
-    v0 += __shfl_xor(v0, 2, 64);
-    v0 += __shfl_xor(v0, 4, 64);
-    v1 += __shfl_xor(v1, 2, 64);
-    v1 += __shfl_xor(v1, 4, 64);
-    if ((lane & 6) == 0) {
-      red[(r * 4 + wave) * 32 + col] = v0;
-      red[(r * 4 + wave) * 32 + 16 + col] = v1;
-    }
-  }
-  __syncthreads();
-  for (int i = threadIdx.x; i < a.R * 32; i += blockDim.x) {
-    const int r = i / 32, t = i % 32;
-    const float v = (red[(r * 4 + 0) * 32 + t] + red[(r * 4 + 1) * 32 + t]) +
-                    (red[(r * 4 + 2) * 32 + t] + red[(r * 4 + 3) * 32 + t]);
-    st_cg(a.part + ((uint64_t)s * a.R + r) * OTp * 16 + p * 32 + t, v);
-  }
-  // completion of the 128-column output block cb (pairs 4 cb .. 4 cb + 3)
-  const int cb = p / 4, npb = min(4, NP - 4 * cb);
-  uint32_t *ctr = a.cnt + (uint64_t)cb * kSyncStride;
-  if (block_signal(ctr, &flag) != (uint32_t)(npb * a.S - 1)) return;
-  if (threadIdx.x == 0) st_cg(ctr, 0u);
-  for (int r = wave; r < a.R; r += 4) {
-    const int i0 = cb * 128 + lane, i1 = i0 + 64;
-    const bool m0 = i0 < a.out, m1 = i1 < a.out;
-    const int j0 = m0 ? i0 : 0, j1 = m1 ? i1 : 0;
-    float v0 = 0.f, v1 = 0.f;
-    // the splits' partials are requested 8 at a time (one round trip per 8, not per split) and summed in split order
-    constexpr int B = 8;
-    for (int s0 = 0; s0 < a.S; s0 += B) {
-      float t0[B], t1[B];
-#pragma unroll
-      for (int j = 0; j < B; j++) {
-        const float *pp = a.part + ((uint64_t)min(s0 + j, a.S - 1) * a.R + r) * OTp * 16;
-        t0[j] = ld_cg(pp + j0);
-        t1[j] = ld_cg(pp + j1);
-      }
-#pragma unroll
-      for (int j = 0; j < B; j++)
-        if (s0 + j < a.S) {
-          v0 += t0[j];
-          v1 += t1[j];
-        }
-    }
-    v0 = m0 ? v0 : 0.f;
-    v1 = m1 ? v1 : 0.f;
-    fwht2(v0, v1, lane, a.had_out, a.sc_out);
-    if (m0) lin_store(a, r, i0, v0 * h2f(a.svh[i0]));
-    if (m1) lin_store(a, r, i1, v1 * h2f(a.svh[i1]));
-  }
-  if (a.epi.kind == 8)
-    hc_fin_block(a, a.epi.ctr + (uint64_t)(cb % (a.epi.hid / 128)) * kSyncStride, a.epi.row0, a.epi.row0 + a.R, cb,
-                 &flag);
-}
-
-// lin_finish: y = H_out(sum over splits in order) * svh (reference kernels/trunk6/trunk6.metal:199-214),
-// grid R x ceil(out/128).
-__global__ __launch_bounds__(64) void lin_finish(LinArgs a) {
-  __shared__ int flag;
-  const int nch = (a.out + 127) / 128;
-  const int r = blockIdx.x / nch, c = blockIdx.x % nch, lane = threadIdx.x;
-  const int OTp = a.OT + (a.OT & 1);
-  const int i0 = c * 128 + lane, i1 = i0 + 64;
+// The finished outputs of 128-column block cb for row r: the k group partials folded left in k order, H_out, svh, the
+// epilogue (reference kernels/trunk6/trunk6.metal:199-214, t6_finish). tag != 0: the partials are tagged values of
+// this launch (other workgroups are still storing them: polled until every one carries the tag; a bounded wait);
+// tag == 0: plain floats from an earlier launch.
+constexpr uint32_t kLinSpin = 1u << 20;
+__device__ void lin_finish_row(const LinArgs &a, int r, int cb, uint32_t tag) {
+  const int lane = threadIdx.x & 63, OTp = a.OT + (a.OT & 1);
+  const int i0 = cb * 128 + lane, i1 = i0 + 64;
   const bool m0 = i0 < a.out, m1 = i1 < a.out;
   const int j0 = m0 ? i0 : 0, j1 = m1 ? i1 : 0;
   float v0 = 0.f, v1 = 0.f;
-  constexpr int B = 8;  // splits requested together, summed in split order (as lin_step's finisher)
-  for (int s0 = 0; s0 < a.S; s0 += B) {
+  constexpr int B = 8;  // groups requested together (one round trip per 8)
+  for (int g0 = 0; g0 < a.S; g0 += B) {
     float t0[B], t1[B];
+    if (tag) {
+      const uint64_t *pt = (const uint64_t *)a.part;
+      for (uint32_t it = 0; it < kLinSpin; it++) {
+        bool all = true;
 #pragma unroll
-    for (int j = 0; j < B; j++) {
-      const float *pp = a.part + ((uint64_t)min(s0 + j, a.S - 1) * a.R + r) * OTp * 16;
-      t0[j] = pp[j0];
-      t1[j] = pp[j1];
+        for (int j = 0; j < B; j++) {
+          const uint64_t *pp = pt + ((uint64_t)min(g0 + j, a.S - 1) * a.R + r) * OTp * 16;
+          const uint64_t u0 = ld_cg(pp + j0), u1 = ld_cg(pp + j1);
+          all = all && tag_ok(u0, tag) && tag_ok(u1, tag);
+          t0[j] = tag_val(u0);
+          t1[j] = tag_val(u1);
+        }
+        if (__all(all)) break;
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < B; j++) {
+        const float *pp = a.part + ((uint64_t)min(g0 + j, a.S - 1) * a.R + r) * OTp * 16;
+        t0[j] = pp[j0];
+        t1[j] = pp[j1];
+      }
     }
 #pragma unroll
     for (int j = 0; j < B; j++)
-      if (s0 + j < a.S) {
-        v0 += t0[j];
-        v1 += t1[j];
+      if (g0 + j < a.S) {
+        v0 = g0 + j == 0 ? t0[j] : v0 + t0[j];
+        v1 = g0 + j == 0 ? t1[j] : v1 + t1[j];
       }
   }
   v0 = m0 ? v0 : 0.f;
@@ -797,6 +632,147 @@ __global__ __launch_bounds__(64) void lin_finish(LinArgs a) {
   fwht2(v0, v1, lane, a.had_out, a.sc_out);
   if (m0) lin_store(a, r, i0, v0 * h2f(a.svh[i0]));
   if (m1) lin_store(a, r, i1, v1 * h2f(a.svh[i1]));
+}
+
+// lin_mx: up to kLinMulti linears at R <= 32 rows in one launch, on the matrix cores (reference
+// kernels/trunk6/trunk6.metal: t6_prep :68-85, t6_simd / t6_nax, t6_finish :199-214; trunk6.mm record_multi).
+// Workgroup (linear, tile pair p, k group g), 4 waves; wave c takes k chunk c of the group (8 k tiles):
+//   1. requests the chunk's tiles into its LDS slot; prepares the chunk's input rows (fp16(H_in(x suh)), kp order)
+//      in LDS meanwhile (x and suh requested before the tiles, so that waiting for them does not wait for the
+//      tiles), or (xh_in) requests the rows a prep launch wrote;
+//   2. decodes the tiles straight into the B operand of v_mfma_f32_32x32x16_f16 (A: the input rows; a row beyond R
+//      repeats row R - 1, its products unused) in one chain from zero;
+// then the chunk sums of the 4 waves are folded left in LDS and stored as the group's partials: tagged with the
+// launch's tag (one launch: the block's epoch word + 1, read at the start), where the block's finisher polls them.
+// The finisher of a 128-column output block is its producer with the highest workgroup index (the last group's last
+// pair): workgroups are dispatched in index order (per XCD), so every producer it waits for has been dispatched and
+// waits for nothing. It then advances the block's epoch. (Staged path: plain floats, finished by lin_finish.)
+// Every row's arithmetic is the same at any R: a row of a batch is bit-identical to that row run alone.
+struct LinMulti {
+  int n;
+  int wg0[kLinMulti + 1];  // first workgroup of each linear
+  LinArgs l[kLinMulti];
+};
+__device__ __forceinline__ LinArgs lin_pick(const LinMulti &m, int i) {  // uniform i; no dynamic struct indexing
+  return i == 0 ? m.l[0] : i == 1 ? m.l[1] : i == 2 ? m.l[2] : m.l[3];
+}
+// LDS of one wave: its tiles (8 k tile pairs), then RT prepared rows of its chunk (128 halves each)
+template <int K, int RT>
+constexpr uint32_t lin_wave_lds() { return kLinChunkKt * 64 * K + RT * 256; }
+template <int K, int RT>
+constexpr uint32_t lin_mx_lds() { return 4 * lin_wave_lds<K, RT>() + 4 * RT * 32 * 4; }
+
+template <int K, int RT>
+__global__ __launch_bounds__(256) void lin_mx(LinMulti m) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  __shared__ int flag;
+  int li = 0;
+#pragma unroll
+  for (int i = 1; i < kLinMulti; i++)
+    if (i < m.n && (int)blockIdx.x >= m.wg0[i]) li = i;
+  const LinArgs a = lin_pick(m, li);
+  const int NP = (a.OT + 1) / 2, OTp = 2 * NP, R = a.R;
+  const int b = (int)blockIdx.x - m.wg0[li], p = b % NP, g = b / NP;
+  const int lane = threadIdx.x & 63, c = (int)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int kt0 = g * kLinGroupKt + c * kLinChunkKt, nkt = max(0, min(kLinChunkKt, a.IT - kt0));
+  uint8_t *tl = lds + c * lin_wave_lds<K, RT>();
+  _Float16 *xs = (_Float16 *)(tl + kLinChunkKt * 64 * K);
+  float *csum = (float *)(lds + 4 * lin_wave_lds<K, RT>());  // [4 chunks][RT rows][32 columns]
+  const int e0 = kt0 * 16, i0 = e0 + lane, i1 = i0 + 64;    // the chunk's elements of this lane
+  const int cb = p / 4;
+  uint32_t *epoch = a.cnt ? a.cnt + (uint64_t)cb * kSyncStride : nullptr;
+  uint32_t ep = 0;
+  if (epoch) ep = ld_cg(epoch);  // requested first: in by the time the partials go out
+  // 1. input rows and tiles
+  float xv0[RT], xv1[RT], s0 = 0.f, s1 = 0.f;
+  if (!a.xh_in && nkt > 0) {
+    s0 = i0 < a.in ? h2f(a.suh[i0]) : 0.f;
+    s1 = i1 < a.in ? h2f(a.suh[i1]) : 0.f;
+#pragma unroll
+    for (int r = 0; r < RT; r++)
+      if (r < R) {
+        xv0[r] = i0 < a.in ? a.x[(uint64_t)r * a.in + i0] : 0.f;
+        xv1[r] = i1 < a.in ? a.x[(uint64_t)r * a.in + i1] : 0.f;
+      }
+  }
+  int ndma = 0;
+  if (nkt > 0) {
+    const uint8_t *src = (const uint8_t *)a.tiles + ((uint64_t)p * a.IT + kt0) * 64 * K;
+    const uint32_t bytes = (uint32_t)nkt * 64 * K;
+    for (uint32_t o = 0; o < bytes; o += 1024, ndma++)
+      if (o + (uint32_t)lane * 16 < bytes)
+        __builtin_amdgcn_global_load_lds((const void *)(src + o + lane * 16),
+                                         (__attribute__((address_space(3))) void *)(tl + o), 16, 0, 0);
+    if (a.xh_in) {  // rows r .. r + 3 per request: 16 lanes of 16 bytes each (the chunk's nkt * 32 bytes)
+      for (int r = 0; r < R; r += 4) {
+        const int rr = r + (lane >> 4), q = lane & 15;
+        if (rr < R && q * 16 < nkt * 32)
+          __builtin_amdgcn_global_load_lds((const void *)(a.xh + (uint64_t)rr * a.in + e0 + q * 8),
+                                           (__attribute__((address_space(3))) void *)(xs + r * 128), 16, 0, 0);
+      }
+    }
+  }
+  if (!a.xh_in && nkt > 0) wait_vm(ndma);  // x and suh are in (the tiles, requested after them, may not be)
+  f32x16 acc;
+#pragma unroll
+  for (int i = 0; i < 16; i++) acc[i] = 0.f;
+  if (nkt > 0) {
+    if (!a.xh_in) {
+#pragma unroll
+      for (int r = 0; r < RT; r++)
+        if (r < R) {
+          float v0 = xv0[r] * s0, v1 = xv1[r] * s1;
+          fwht2(v0, v1, lane, a.had_in, a.sc_in);
+          xs[r * 128 + kp((uint32_t)lane)] = to_f16(v0);
+          xs[r * 128 + kp((uint32_t)lane + 64)] = to_f16(v1);
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the tiles (and rows) are in LDS
+    // 2. the chunk's chain on the matrix cores
+    const _Float16 *xa = xs + min(lane & 31, R - 1) * 128 + 8 * (lane >> 5);
+#pragma unroll
+    for (int kt = 0; kt < kLinChunkKt; kt++)
+      if (kt < nkt) {
+        const f16x8 bv = decode_pair<K>(tl, kt);
+        const f16x8 av = *(const f16x8 *)(xa + kt * 16);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bv, acc, 0, 0, 0);
+      }
+  }
+  // 3. chunk sums (lane (n, h), value i: row 8 (i / 4) + 4 h + i % 4, column n) -> LDS; the group's fold -> partials
+#pragma unroll
+  for (int i = 0; i < 16; i++) {
+    const int r = 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+    if (r < RT && r < R) csum[(c * RT + r) * 32 + (lane & 31)] = acc[i];
+  }
+  __syncthreads();
+  const int nc = (min(kLinGroupKt, a.IT - g * kLinGroupKt) + kLinChunkKt - 1) / kLinChunkKt;
+  const uint32_t tag = (uint32_t)__builtin_amdgcn_readfirstlane(ep) + 1u;
+  for (int e = threadIdx.x; e < R * 32; e += 256) {
+    const int r = e >> 5, n = e & 31;
+    float v = csum[r * 32 + n];
+    for (int cc = 1; cc < nc; cc++) v = v + csum[(cc * RT + r) * 32 + n];
+    const uint64_t o = ((uint64_t)g * R + r) * OTp * 16 + p * 32 + n;
+    if (epoch)
+      st_tag((uint64_t *)a.part + o, v, tag);
+    else
+      a.part[o] = v;
+  }
+  // 4. the block's finisher: its rows from the tagged partials, then the block's epoch
+  if (!epoch || g != a.S - 1 || p != min(4 * cb + 3, NP - 1)) return;
+  for (int r = c; r < R; r += 4) lin_finish_row(a, r, cb, tag);
+  __syncthreads();
+  if (threadIdx.x == 0) st_cg(epoch, tag);
+  if (a.epi.kind == 8)
+    hc_fin_block(a, a.epi.ctr + (uint64_t)(cb % (a.epi.hid / 128)) * kSyncStride, a.epi.row0, a.epi.row0 + R, cb,
+                 &flag);
+}
+
+// lin_finish: the finisher of the staged path, grid R x ceil(out/128) (one workgroup per row and output block)
+__global__ __launch_bounds__(64) void lin_finish(LinArgs a) {
+  __shared__ int flag;
+  const int nch = (a.out + 127) / 128;
+  const int r = blockIdx.x / nch, c = blockIdx.x % nch;
+  lin_finish_row(a, r, c, 0u);
   if (a.epi.kind == 8) {
     const int nbs = a.epi.hid / 128, rg = a.epi.row0 + r;
     hc_fin_block(a, a.epi.ctr + (uint64_t)(nbs + rg * nbs + c % nbs) * kSyncStride, rg, rg + 1, c, &flag);
@@ -954,57 +930,73 @@ void launch_moe_down(const MoeArgs &a, hipStream_t s) {
 void launch_moe_combine(const MoeArgs &a, hipStream_t s) {
   hipLaunchKernelGGL(moe_combine, dim3(a.R * ((a.hid + 127) / 128)), dim3(256), 0, s, a);
 }
+static int rows_tier(int R) { return R <= 1 ? 1 : R <= 2 ? 2 : R <= 4 ? 4 : R <= 8 ? 8 : R <= 16 ? 16 : 32; }
 template <int K>
-static const void *lin_gemv_fn(int RT) {
+static const void *lin_mx_fn(int RT) {
   switch (RT) {
-    case 1: return (const void *)&lin_gemv<K, 1>;
-    case 2: return (const void *)&lin_gemv<K, 2>;
-    case 4: return (const void *)&lin_gemv<K, 4>;
-    default: return (const void *)&lin_gemv<K, 8>;
+    case 1: return (const void *)&lin_mx<K, 1>;
+    case 2: return (const void *)&lin_mx<K, 2>;
+    case 4: return (const void *)&lin_mx<K, 4>;
+    case 8: return (const void *)&lin_mx<K, 8>;
+    case 16: return (const void *)&lin_mx<K, 16>;
+    default: return (const void *)&lin_mx<K, 32>;
   }
 }
-static const void *lin_gemv_any(int K, int RT) {
+static const void *lin_mx_any(int K, int RT) {
   const void *f = nullptr;
-  IJ_DISPATCH_K(K, f = lin_gemv_fn<KK>(RT));
+  IJ_DISPATCH_K(K, f = lin_mx_fn<KK>(RT));
   return f;
 }
 template <int K>
-static const void *lin_step_fn(int RT) {
+static size_t lin_mx_lds_fn(int RT) {
   switch (RT) {
-    case 1: return (const void *)&lin_step<K, 1>;
-    case 2: return (const void *)&lin_step<K, 2>;
-    case 4: return (const void *)&lin_step<K, 4>;
-    default: return (const void *)&lin_step<K, 8>;
+    case 1: return lin_mx_lds<K, 1>();
+    case 2: return lin_mx_lds<K, 2>();
+    case 4: return lin_mx_lds<K, 4>();
+    case 8: return lin_mx_lds<K, 8>();
+    case 16: return lin_mx_lds<K, 16>();
+    default: return lin_mx_lds<K, 32>();
   }
 }
-static const void *lin_step_any(int K, int RT) {
-  const void *f = nullptr;
-  IJ_DISPATCH_K(K, f = lin_step_fn<KK>(RT));
-  return f;
+static size_t lin_mx_lds_any(int K, int RT) {
+  size_t n = 0;
+  IJ_DISPATCH_K(K, n = lin_mx_lds_fn<KK>(RT));
+  return n;
 }
-static int rows_tier(int R) { return R <= 1 ? 1 : R <= 2 ? 2 : R <= 4 ? 4 : 8; }
 
+void launch_lin_multi(const LinArgs *l, int n, hipStream_t s) {
+  IJ_CHECK(n >= 1 && n <= kLinMulti, "multi-linear launch of %d linears (1..%d)", n, kLinMulti);
+  LinMulti m{};
+  m.n = n;
+  int wg = 0;
+  for (int i = 0; i < n; i++) {
+    const LinArgs &a = l[i];
+    // every buffer a (possibly captured) launch uses is present, and the k groups fixed by the shape
+    IJ_CHECK(a.tiles && a.suh && a.svh && a.x && a.y && a.xh && a.part && a.S == (a.IT + kLinGroupKt - 1) / kLinGroupKt,
+             "linear launch: missing buffer or bad k groups (S %d of %d k tiles)", a.S, a.IT);
+    IJ_CHECK(a.K == l[0].K && a.R == l[0].R && a.R >= 1 && a.R <= kLinMaxRows && (bool)a.cnt == (bool)l[0].cnt,
+             "multi-linear launch: K, R and path must agree");
+    if (a.xh_in) hipLaunchKernelGGL(lin_prep, dim3(a.R * ((a.in + 127) / 128)), dim3(64), 0, s, a);
+    m.l[i] = a;
+    m.wg0[i] = wg;
+    wg += ((a.OT + 1) / 2) * a.S;
+  }
+  m.wg0[n] = wg;
+  const int RT = rows_tier(l[0].R);
+  void *args[] = {&m};
+  IJ_HIP(hipLaunchKernel(lin_mx_any(l[0].K, RT), dim3(wg), dim3(256), args, lin_mx_lds_any(l[0].K, RT), s));
+  if (!l[0].cnt)  // staged path: the finisher as its own launch
+    for (int i = 0; i < n; i++)
+      hipLaunchKernelGGL(lin_finish, dim3(l[i].R * ((l[i].out + 127) / 128)), dim3(64), 0, s, l[i]);
+}
+void launch_lin(const LinArgs &a, hipStream_t s) { launch_lin_multi(&a, 1, s); }
 
-void launch_lin(const LinArgs &a, hipStream_t s) {
-  const int NP = (a.OT + 1) / 2;
-  // every buffer a (possibly captured) launch uses is present and sized for this split
-  IJ_CHECK(a.tiles && a.suh && a.svh && a.x && a.y && a.xh && a.part && a.S >= 1 && a.IT % a.S == 0,
-           "linear launch: missing buffer or bad split (S %d of %d k tiles)", a.S, a.IT);
-  if (a.R > kLinSimdRows || !a.cnt) hipLaunchKernelGGL(lin_prep, dim3(a.R * ((a.in + 127) / 128)), dim3(64), 0, s, a);
-  if (a.R > kLinSimdRows) {
-    launch_lin_mm(a, s);
-    hipLaunchKernelGGL(lin_finish, dim3(a.R * ((a.out + 127) / 128)), dim3(64), 0, s, a);
-    return;
-  }
-  const int RT = rows_tier(a.R);
-  const size_t lds = (size_t)RT * (a.IT / a.S) * 16 * sizeof(uint16_t);
-  void *args[] = {const_cast<LinArgs *>(&a)};
-  if (a.cnt) {  // one launch
-    IJ_HIP(hipLaunchKernel(lin_step_any(a.K, RT), dim3(NP * a.S), dim3(256), args, lds, s));
-    return;
-  }
-  IJ_HIP(hipLaunchKernel(lin_gemv_any(a.K, RT), dim3(NP * a.S), dim3(256), args, lds, s));
-  hipLaunchKernelGGL(lin_finish, dim3(a.R * ((a.out + 127) / 128)), dim3(64), 0, s, a);
+// the dynamic LDS limits of lin_mx, once at device set-up
+void init_lin_attrs() {
+  for (int K = 2; K <= 8; K++)
+    for (int RT : {1, 2, 4, 8, 16, 32})
+      IJ_HIP(hipFuncSetAttribute(lin_mx_any(K, RT), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                 (int)lin_mx_lds_any(K, RT)));
 }
 
 static const void *decode_fn(int K) {
@@ -1026,8 +1018,7 @@ static std::vector<KernelEntry> build_registry() {
   const uint32_t P = sizeof(void *), I = sizeof(int);
   for (int K = 2; K <= 8; K++) {
     v.push_back({"exl3_decode", decode_fn(K), {P, I, I, P}, K, -1});
-    for (int RT : {1, 2, 4, 8}) v.push_back({"lin_gemv", lin_gemv_any(K, RT), {(uint32_t)sizeof(LinArgs)}, K, RT});
-    for (int RT : {1, 2, 4, 8}) v.push_back({"lin_step", lin_step_any(K, RT), {(uint32_t)sizeof(LinArgs)}, K, RT});
+    for (int RT : {1, 2, 4, 8, 16, 32}) v.push_back({"lin_mx", lin_mx_any(K, RT), {(uint32_t)sizeof(LinMulti)}, K, RT});
   }
   v.push_back({"lin_prep", (const void *)&lin_prep, {(uint32_t)sizeof(LinArgs)}, -1, -1});
   v.push_back({"lin_finish", (const void *)&lin_finish, {(uint32_t)sizeof(LinArgs)}, -1, -1});
@@ -1041,6 +1032,7 @@ static std::vector<KernelEntry> build_registry() {
         v.push_back({"moe_step_2048x512_ks" + std::to_string(KS), f, {(uint32_t)sizeof(MoeArgs)}, K, -1});
   v.push_back({"fill_u32", (const void *)&fill_u32, {P, 8, 8}, -1, -1});
   v.push_back({"copy_u128", (const void *)&copy_u128, {P, P, 8}, -1, -1});
+  probe_kernels(v);
   return v;
 }
 

@@ -16,6 +16,8 @@ struct KernelEntry {
 };
 // name + optional function constants (index 10 = K, 16 = R) -> entry, or nullptr
 const KernelEntry *find_kernel(const char *name, const ne_fconst *fc, int nfc);
+void probe_kernels(std::vector<KernelEntry> &v);  // the measurement probes (probes.hip)
+size_t probe_lds(int K);
 
 // Byte offsets of one expert's (or one linear's) regions inside its HBM block. Tiles of a projection are re-laid as
 // [n-pair p][k-tile tk][2], so a workgroup working on output tiles (2p, 2p+1) streams one contiguous span.
@@ -106,7 +108,7 @@ constexpr int kSyncStride = 64;  // u32 words between counters
 // the allocation-free linear's scratch (per GPU, for the process's lifetime): counters, prepared input, partials
 constexpr size_t kNoAllocScratchBytes = size_t(32) << 20;
 uint8_t *noalloc_scratch();  // this device's scratch address (taken at device set-up or the first call on it)
-void launch_fill_u32(uint32_t *p, size_t n, uint32_t v, hipStream_t s);
+void launch_zero_u32(uint32_t *p, size_t n, hipStream_t s);  // p[0 .. n) = 0 by a kernel (capture-safe)
 inline size_t sync_words(int R, int nslot, int hid, int inter) {
   return kSyncStride * (8 + (size_t)R * nslot + (size_t)R * ((hid + 127) / 128) +
                         (size_t)R * nslot * ((inter + 127) / 128));
@@ -135,21 +137,25 @@ struct LinArgs {
   const uint16_t *suh, *svh;
   int in, out, K, IT, OT, had_in, had_out;
   float sc_in, sc_out;
-  int R, S;               // rows, k splits
+  int R, S;               // rows, k groups (S = ceil(IT / kLinGroupKt): fixed by the shape, not by R)
   const float *x;
   float *y;
   uint16_t *xh;           // [R][in] prepared fp16 input (scratch)
-  float *part;            // [S][R][OTp * 16] (scratch)
-  uint32_t *cnt;          // per 128-column output block, kSyncStride apart, zero between launches; null: the staged
-                          // three-kernel path (prep, GEMV, finish)
+  float *part;            // [S][R][OTp * 16] (scratch): k group partials (u64 tagged values on the one-launch path)
+  uint32_t *cnt;          // per 128-column output block, kSyncStride apart: the block's epoch (the tag of its last
+                          // launch; zero at creation); null: the staged three-kernel path (prep, GEMM, finish)
+  int xh_in;              // 1: xh holds this run's prepared rows (a prep launch ran); 0: the GEMM prepares its chunks
   LinEpi epi;
 };
-// rows up to kLinSimdRows take the VALU GEMV (lin_gemv), more rows (up to kLinMaxRows) the matrix cores (lin_mm)
-constexpr int kLinSimdRows = 8, kLinMaxRows = 32;
-// fewest k tiles per split of the matrix-core linear (one pipeline step of two tiles); the default split stops at 8
-// (a performance choice, IJAH_LIN_MM_MINKT overrides it at creation)
-constexpr int kLinMmMinSpan = 2;
+constexpr int kLinMaxRows = 32;
+// The k order of every linear: k chunks of 8 k tiles (one MFMA chain from zero each), folded left in k groups of
+// 4 chunks, the groups folded left by the finisher; a row's outputs do not depend on the other rows or on R.
+constexpr int kLinChunkKt = 8, kLinGroupKt = 32;
+constexpr int kLinMulti = 4;  // linears of one multi-linear launch
 void launch_lin(const LinArgs &a, hipStream_t s);
+// several linears at the same row count in one launch (reference kernels/trunk6/trunk6.h:78, record_multi); each its
+// own input, output, scratch and epilogue. Linears of different K go to separate launches.
+void launch_lin_multi(const LinArgs *a, int n, hipStream_t s);
 // The hyper-connection read around its two EXL3 linears (reference models/flash_next/layer_t6.mm:89-133, t6_hc_read,
 // with kernels/trunk6/t6_epi.metal:16-97): h f32 [R][4][hid], hc_norm bf16 [4 hid], inject bf16 [4][4 hid].
 // hc_prep: xn [R][4 hid] = h w inv_s (inv_s = 1/rms of stream s), ip [R][4 streams][ceil(hid / 256) chunks][4
@@ -157,10 +163,10 @@ void launch_lin(const LinArgs &a, hipStream_t s);
 // (LinEpi kind 8) then writes out [R][hid] and the gates inj[r][j < 4] = rr(2 sigmoid(rr(sum_s ip[r][s][j]) / 4)).
 void launch_hc_prep(const float *h, const uint16_t *nw, const uint16_t *iw, float *xn, float *ip, float *inj, int R,
                     int hid, hipStream_t s);
-void launch_lin_mm(const LinArgs &a, hipStream_t s);  // rows kLinSimdRows+1 .. kLinMaxRows (matrix cores)
 // raise the dynamic LDS limits of the kernels that need it: once, at device set-up (capi.cpp ensure_device)
 void init_batch_attrs();
 void init_fused_attrs();
+void init_lin_attrs();
 // W' fp16 bits [IT*16][OT*16] from re-laid tiles
 void launch_decode(const uint32_t *tiles, int IT, int OT, int K, uint16_t *w, hipStream_t s);
 

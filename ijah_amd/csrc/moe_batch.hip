@@ -41,15 +41,6 @@ constexpr int kChunkRows = 128;   // rows of one GEMM chunk (4 matrix-core row b
 constexpr int kRowBlocks = kChunkRows / 32;
 
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-__device__ __forceinline__ void wait_vm(int n) {
-  switch (n < 15 ? n : 15) {
-#define IJ_VM(k) \
-  case k: __builtin_amdgcn_s_waitcnt(0x0F70 | k); break;
-    IJ_VM(0) IJ_VM(1) IJ_VM(2) IJ_VM(3) IJ_VM(4) IJ_VM(5) IJ_VM(6) IJ_VM(7)
-    IJ_VM(8) IJ_VM(9) IJ_VM(10) IJ_VM(11) IJ_VM(12) IJ_VM(13) IJ_VM(14) IJ_VM(15)
-#undef IJ_VM
-  }
-}
 __device__ __forceinline__ void dma16(const void *src, void *lds_dst) {
   __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)lds_dst, 16, 0, 0);
 }
@@ -737,7 +728,7 @@ __device__ __forceinline__ void wait_step(int t, int NS) {
   if (t >= DB && t + DB < NS)
     __builtin_amdgcn_s_waitcnt(0x0F70 | kAfterSteady<OA, OB, DA>);
   else
-    wait_vm(after_step<OA, OB, DA, DB>(t, NS));
+    wait_vm15(after_step<OA, OB, DA, DB>(t, NS));
 }
 
 // decodes the lane's B operand for both k tiles of one step straight from the ring bytes src
@@ -1243,46 +1234,6 @@ __global__ __launch_bounds__(256) void bat_combine(MoeArgs a, const float *__res
                   moe_finish(a, r, i + 3, y.w, sh.w));
 }
 
-// ---------------------------------------------------------------------------------------------------- trunk
-// A trunk linear at 9..32 rows on the same grouped GEMM (reference kernels/trunk6/trunk6.metal:431-539, t6_nax):
-// workgroup (g, s) multiplies the prepared rows xh (fp16, kp order) by tile pairs 8g .. 8g + 7 (one per wave) over k
-// split s; part[s][r][OTp * 16] as the GEMV path, summed and rotated by lin_finish.
-template <int K>
-__global__ __launch_bounds__(512, 6) void lin_mm(LinArgs a) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-  const int NP = (a.OT + 1) / 2, OTp = 2 * NP, NG = (NP + kWavesG - 1) / kWavesG;
-  const int g = blockIdx.x % NG, s = blockIdx.x / NG, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int p = g * kWavesG + wave, span = a.IT / a.S;
-  f32x16 acc[1];
-  chunk_gemm<K, 1, false, 32>(a.xh, a.in, 0, 0, a.R, (const uint8_t *)a.tiles, a.IT, min(p, NP - 1), lds, acc, nullptr, s * span,
-                   span);
-  if (p >= NP) return;
-#pragma unroll
-  for (int i = 0; i < 16; i++) {
-    const int r = 4 * (lane >> 5) + (i & 3) + 8 * (i >> 2);
-    if (r < a.R) a.part[((uint64_t)s * a.R + r) * OTp * 16 + p * 32 + (lane & 31)] = acc[0][i];
-  }
-}
-template <int K>
-static void lin_mm_launch(const LinArgs &a, hipStream_t s) {
-  const size_t lds = GemmIo<K, 1, 32>::LDS;  // (its dynamic LDS limit is raised by init_batch_attrs)
-  const int NG = ((a.OT + 1) / 2 + kWavesG - 1) / kWavesG;
-  hipLaunchKernelGGL(lin_mm<K>, dim3(NG * a.S), dim3(64 * kWavesG), lds, s, a);
-}
-void launch_lin_mm(const LinArgs &a, hipStream_t s) {
-  // chunk_gemm runs a split's k span as steps of two k tiles: an odd span would drop its last tile
-  IJ_CHECK(a.S >= 1 && a.IT % a.S == 0 && (a.IT / a.S) % 2 == 0, "lin_mm: k span %d / %d not an even tile count",
-           a.IT, a.S);
-  switch (a.K) {
-    case 2: lin_mm_launch<2>(a, s); break;
-    case 3: lin_mm_launch<3>(a, s); break;
-    case 4: lin_mm_launch<4>(a, s); break;
-    case 5: lin_mm_launch<5>(a, s); break;
-    case 6: lin_mm_launch<6>(a, s); break;
-    case 7: lin_mm_launch<7>(a, s); break;
-    default: lin_mm_launch<8>(a, s); break;
-  }
-}
 
 // ---------------------------------------------------------------------------------------------------- host side
 namespace {
@@ -1332,17 +1283,11 @@ static void gemm_attrs_all() {
   gemm_attrs<K, KS, false, 32>();
   gemm_attrs<K, KS, false, kChunkRows>();
 }
-template <int K>
-static void lin_mm_attr() {
-  IJ_HIP(hipFuncSetAttribute((const void *)&lin_mm<K>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)GemmIo<K, 1, 32>::LDS));
-}
 void init_batch_attrs() {
   IJ_HIP(hipFuncSetAttribute((const void *)&bat_place_prep, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPrepLds));
   gemm_attrs_all<4, 4>(); gemm_attrs_all<5, 5>(); gemm_attrs_all<6, 6>(); gemm_attrs_all<4, 5>();
   gemm_attrs_all<4, 6>(); gemm_attrs_all<5, 6>(); gemm_attrs_all<5, 4>(); gemm_attrs_all<6, 4>();
   gemm_attrs_all<6, 5>();
-  lin_mm_attr<2>(); lin_mm_attr<3>(); lin_mm_attr<4>(); lin_mm_attr<5>(); lin_mm_attr<6>(); lin_mm_attr<7>(); lin_mm_attr<8>();
 }
 
 // Few rows: every kernel keeps the one-row step's arithmetic (hidden size a multiple of 512 for its router rows)

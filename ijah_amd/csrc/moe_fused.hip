@@ -70,29 +70,10 @@ __device__ __forceinline__ uint32_t ld_relaxed(const uint32_t *p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-// s_waitcnt vmcnt(n) for a run-time n (6-bit count: low 4 bits at [3:0], high 2 at [15:14]; n above 63 waits as for
-// 63, which only waits longer); completion is counted in issue order, stores included
-__device__ __forceinline__ void wait_vm(int n) {
-  switch (n < 63 ? n : 63) {
-#define IJ_VM(k) \
-  case k: __builtin_amdgcn_s_waitcnt(0x0F70 | ((k) & 15) | (((k) >> 4) << 14)); break;
-#define IJ_VM4(k) IJ_VM(k) IJ_VM(k + 1) IJ_VM(k + 2) IJ_VM(k + 3)
-    IJ_VM4(0) IJ_VM4(4) IJ_VM4(8) IJ_VM4(12) IJ_VM4(16) IJ_VM4(20) IJ_VM4(24) IJ_VM4(28)
-    IJ_VM4(32) IJ_VM4(36) IJ_VM4(40) IJ_VM4(44) IJ_VM4(48) IJ_VM4(52) IJ_VM4(56) IJ_VM4(60)
-#undef IJ_VM4
-#undef IJ_VM
-  }
-}
 __device__ __forceinline__ int dma_ops(uint32_t bytes) { return (int)((bytes + 1023u) >> 10); }
 constexpr int had_of(int d) { return d % 128 == 0 ? 128 : d % 64 == 0 ? 64 : d % 32 == 0 ? 32 : 16; }
 __device__ __forceinline__ uint32_t rfl(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
 
-// tagged values
-__device__ __forceinline__ void st_tag(uint64_t *p, float v, uint32_t tag) {
-  st_cg(p, (uint64_t)__float_as_uint(v) | ((uint64_t)tag << 32));
-}
-__device__ __forceinline__ float tag_val(uint64_t t) { return __uint_as_float((uint32_t)t); }
-__device__ __forceinline__ bool tag_ok(uint64_t t, uint32_t tag) { return (uint32_t)(t >> 32) == tag; }
 
 __device__ __forceinline__ void stamp_r(const MoeArgs &a, int field) {  // the route's own steps
   if (a.trace && (threadIdx.x & 63) == 0) a.trace[((uint64_t)4096 + blockIdx.x) * 8 + field] = wall_clock64();
@@ -307,25 +288,6 @@ __device__ __forceinline__ int stream_tiles(const uint8_t *tr, int IT, int p, in
       __builtin_amdgcn_global_load_lds((const void *)(src + o + lane * 16),
                                        (__attribute__((address_space(3))) void *)(dst + o), 16, 0, 0);
   return dma_ops(bytes);
-}
-// the B operand of k tile kt of a staged pair (the trellis words decoded straight into v_mfma_f32_32x32x16_f16's B)
-template <int K>
-__device__ __forceinline__ f16x8 decode_pair(const uint8_t *tl, int kt) {
-  constexpr int TW = 8 * K;
-  const int lane = threadIdx.x & 63;
-  const BLane<K> B = b_lane<K>((uint32_t)lane);
-  const uint32_t *T0 = (const uint32_t *)tl + B.tile * TW + kt * 2 * TW;
-  TileWords w0, w1;
-  w0.w0 = T0[B.g0.i0];
-  w0.w1 = T0[B.g0.i1];
-  w0.w2 = kThreeWords<K> ? T0[B.g0.i2] : 0u;
-  w1.w0 = T0[B.g1.i0];
-  w1.w1 = T0[B.g1.i1];
-  w1.w2 = kThreeWords<K> ? T0[B.g1.i2] : 0u;
-  f16x2 l0, h0, l1, h1;
-  decode4<K>(w0, B.g0.sh, l0, h0);
-  decode4<K>(w1, B.g1.sh, l1, h1);
-  return f16x8{l0.x, l0.y, h0.x, h0.y, l1.x, l1.y, h1.x, h1.y};
 }
 // k tiles [kt0, kt1) of a staged pair times the prepared input xs (kp order, xs[16 kt] = k tile kt), on the matrix
 // cores: A repeats the input row in all 32 rows, so row 0 of the product (lanes 0-31, acc[0]) holds the pair's 32

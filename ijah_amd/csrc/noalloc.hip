@@ -3,9 +3,9 @@
 // with that device current (at the library's device set-up, or at the first call on another device); host code only
 // ever passes that address, never the array's name (a host-side stand-in that is not device memory).
 //
-// Every call on one GPU shares its array and finds the previous call's contents: the completion counters are
-// cleared by a fill kernel at the start of each call (a kernel, not a memset, so that a captured call replays
-// correctly). Calls that overlap on one GPU (two streams, two threads) race on the array.
+// Every call on one GPU shares its array and finds the previous call's contents: the block epochs and the tagged
+// partials are cleared by a fill kernel at the start of each call (a kernel, not a memset, so that a captured call
+// replays correctly). Calls that overlap on one GPU (two streams, two threads) race on the array.
 #include <hip/hip_runtime.h>
 
 #include <mutex>
@@ -22,8 +22,8 @@ constexpr int kMaxDevices = 64;
 void *g_scratch[kMaxDevices] = {};
 std::mutex g_mu;
 
-__global__ __launch_bounds__(256) void fill_u32(uint32_t *p, uint32_t n, uint32_t v) {
-  for (uint32_t i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) p[i] = v;
+__global__ __launch_bounds__(256) void zero_u32(uint32_t *p, uint32_t n) {
+  for (uint32_t i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) p[i] = 0u;
 }
 
 }  // namespace
@@ -42,11 +42,11 @@ uint8_t *noalloc_scratch() {
   return (uint8_t *)g_scratch[dev];
 }
 
-void launch_fill_u32(uint32_t *p, size_t n, uint32_t v, hipStream_t s) {
+void launch_zero_u32(uint32_t *p, size_t n, hipStream_t s) {
   if (!n) return;
-  IJ_CHECK(n < (1ull << 32), "fill: %zu words", n);
+  IJ_CHECK(n < (1ull << 32), "zero fill: %zu words", n);
   const unsigned grid = (unsigned)std::min<size_t>((n + 255) / 256, 1024);
-  hipLaunchKernelGGL(fill_u32, dim3(grid), dim3(256), 0, s, p, (uint32_t)n, v);
+  hipLaunchKernelGGL(zero_u32, dim3(grid), dim3(256), 0, s, p, (uint32_t)n);
 }
 
 }  // namespace ijah

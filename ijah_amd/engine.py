@@ -84,6 +84,8 @@ SIGNATURES = {
     "ne_exl3_lin_info": (_i, [_vp, C.POINTER(_i), C.POINTER(_i), C.POINTER(_i)]),
     "ne_exl3_lin_run": (_i, [_vp, _i, _vp, _u64, _vp, _u64, _dp]),
     "ne_exl3_lin_run_noalloc": (_i, [_vp, _i, _vp, _u64, _vp, _u64]),
+    "ne_exl3_lin_run_multi": (_i, [_vp, _i, _i, _vp, _vp, _vp, _vp, _dp]),
+    "ne_exl3_lin_time_multi": (_i, [_vp, _i, _i, _i, _vp, _i, _i, _dp]),
     "ne_exl3_lin_run_epi": (_i, [_vp, _i, _vp, _u64, _vp, _u64, _vp, _dp]),
     "ne_hc_read": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _dp]),
     "ne_exl3_lin_decode": (_i, [_vp, _vp, _dp]),
@@ -560,6 +562,26 @@ class Engine:
         us = C.c_double(0)
         self._ok(self.lib.ne_exl3_lin_time(arr, len(lins), R, x.ptr, warmup, reps, C.byref(us)), "ne_exl3_lin_time")
         return us.value
+
+    def lin_time_multi(self, lins, R, x, group, warmup=3, reps=20):
+        """GPU microseconds per replay of the linears recorded together, `group` per launch (ne_exl3_lin_time_multi)."""
+        arr = (C.c_void_p * len(lins))(*[m.ptr for m in lins])
+        us = C.c_double(0)
+        self._ok(self.lib.ne_exl3_lin_time_multi(arr, len(lins), group, R, x.ptr, warmup, reps, C.byref(us)),
+                 "ne_exl3_lin_time_multi")
+        return us.value
+
+    def lin_run_multi(self, lins, xs):
+        """ne_exl3_lin_run_multi: linear i on rows xs[i] (f32 [R][in_i], one R for all); returns the outputs"""
+        R = np.atleast_2d(xs[0]).shape[0]
+        xb = [self.from_numpy(np.ascontiguousarray(np.atleast_2d(x), np.float32)) for x in xs]
+        yb = [self.alloc(R * m.out * 4) for m in lins]
+        n = len(lins)
+        self._ok(self.lib.ne_exl3_lin_run_multi((C.c_void_p * n)(*[m.ptr for m in lins]), n, R,
+                                                (C.c_void_p * n)(*[b.ptr for b in xb]), (C.c_uint64 * n)(),
+                                                (C.c_void_p * n)(*[b.ptr for b in yb]), (C.c_uint64 * n)(), None),
+                 "ne_exl3_lin_run_multi")
+        return [b.download(np.float32, (R, m.out)) for b, m in zip(yb, lins)]
 
     def moe_time_kernels(self, layers, R, x, reps=5):
         arr = (C.c_void_p * len(layers))(*[m.ptr for m in layers])

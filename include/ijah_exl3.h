@@ -51,7 +51,7 @@ NE_API int ne_exl3_lin_info(const ne_exl3_lin *l, int *in, int *out, int *K);
 NE_API int ne_exl3_lin_run(ne_exl3_lin *l, int R, const ne_buf *x, uint64_t x_off, ne_buf *y, uint64_t y_off,
                            double *gpu_ms);
 /* ne_exl3_lin_run that allocates nothing: no counterpart in the reference; for callers that cannot allocate device
- * memory (code under HIP graph capture, tight serving loops). Its counters, prepared input and k-split partials live
+ * memory (code under HIP graph capture, tight serving loops). Its block epochs, prepared input and k group partials live
  * in one fixed 32 MiB scratch array per GPU, held until the process ends; a run needing more (e.g. a 151936-wide
  * vocabulary head at 32 rows) is rejected with an error. Same results as ne_exl3_lin_run. Every call on one GPU
  * shares that array: calls that overlap on one GPU (other streams or threads) race. Not timed (no gpu_ms). */
@@ -94,6 +94,16 @@ NE_API int ne_hc_read(ne_exl3_lin *down, ne_exl3_lin *up, int R, const ne_buf *h
  * differential timing of the trunk stages (kernels/trunk6/trunk6.mm:232-249 replays, core/bench.h:21-24). */
 NE_API int ne_exl3_lin_time(ne_exl3_lin *const *lins, int n, int R, const ne_buf *x, int warmup, int reps,
                             double *us_per_lin);
+/* ne_exl3_lin_time with the linears recorded together, consecutive runs of up to `group` (1..4) linears of one K per
+ * launch: us = GPU time of all n per replay (reference kernels/trunk6/trunk6.mm:251-280, record_multi, timed as one
+ * stage). */
+NE_API int ne_exl3_lin_time_multi(ne_exl3_lin *const *lins, int n, int group, int R, const ne_buf *x, int warmup,
+                                  int reps, double *us);
+/* reference kernels/trunk6/trunk6.h:78 (t6::record_multi): n linears at R rows recorded to run concurrently, linear i
+ * from x[i] at x_off[i] into y[i] at y_off[i] (each its own scratch); consecutive linears of one K share a launch.
+ * R 1..32. */
+NE_API int ne_exl3_lin_run_multi(ne_exl3_lin *const *lins, int n, int R, const ne_buf *const *x,
+                                 const uint64_t *x_off, ne_buf *const *y, const uint64_t *y_off, double *gpu_ms);
 /* W' decoded on the GPU from the re-laid tiles: fp16 bits [in][out] into w (at least in*out*2 bytes). Replaces the
  * reference's decoded-weight check through exl3_codec.decode_inner (tests/trunk6/check_kernels.py:86). */
 NE_API int ne_exl3_lin_decode(ne_exl3_lin *l, ne_buf *w, double *gpu_ms);

@@ -65,11 +65,13 @@ def test_linear_trunk_shapes(eng, oracle, inp, out, K, R):
 @pytest.mark.parametrize("inp,out,K,R", [(2048, 512, 5, 9), (2048, 512, 5, 16), (2048, 512, 5, 32),
                                          (2048, 4096, 6, 16), (4096, 2048, 6, 16), (320, 640, 7, 12), (96, 48, 4, 12),
                                          (2048, 1024, 8, 16), (2048, 640, 3, 20), (2048, 512, 2, 10), (48, 96, 8, 12),
-                                         (64, 256, 5, 12), (32, 128, 6, 16)])
-def test_linear_matrix_cores(eng, oracle, inp, out, K, R):
-    """9..32 rows take the grouped matrix-core GEMM (lin_mm; 48 inputs = 3 k tiles, odd, and 64 or 32 inputs, fewer
-    k tiles than its shortest span, run as groups of 8 rows on the GEMV): same tolerances as the GEMV rows."""
-    print(f"linear mfma {inp}x{out} K{K} R{R}", flush=True)
+                                         (64, 256, 5, 12), (32, 128, 6, 16), (288, 640, 5, 12), (576, 640, 6, 16),
+                                         (352, 640, 5, 16), (144, 272, 4, 24)])
+def test_linear_rows_bit_identical(eng, oracle, inp, out, K, R):
+    """Many rows on the matrix cores, every row bit-identical to that row run alone (the k chunk / k group order is
+    fixed by the shape, not by R), and within the oracle's tolerances. The shapes cover partial k chunks (48, 144,
+    352 inputs), partial k groups (288, 320, 576) and single-chunk linears (32, 64)."""
+    print(f"linear rows {inp}x{out} K{K} R{R}", flush=True)
     rng = np.random.default_rng(inp * 5 + out + K + R)
     t, su, sv = synth.linear(rng, inp, out, K)
     x = synth.bf16_values(rng, R, inp)
@@ -78,32 +80,33 @@ def test_linear_matrix_cores(eng, oracle, inp, out, K, R):
     assert rel(y, oracle.exl3_linear(x, t, su, sv)) < 5e-5
     assert rel(y, oracle.exl3_linear(x, t, su, sv, exact=True)) < 1e-2
     assert np.array_equal(y, lin.run(x))  # deterministic
-    y1 = lin.run(x[:1])  # the GEMV path on the first row agrees with the matrix-core row
-    assert rel(y1, y[:1]) < 5e-5
+    for r in sorted({0, 1, R // 2, R - 1}):
+        assert np.array_equal(lin.run(x[r:r + 1])[0], y[r]), r
+    assert np.array_equal(lin.run(x[:3]), y[:3])
 
 
-@pytest.mark.parametrize("minkt", [2, 4])
-@pytest.mark.parametrize("inp,out,K,R", [(320, 640, 7, 12), (288, 640, 5, 12), (576, 640, 6, 16), (352, 640, 5, 16),
-                                         (2048, 512, 5, 16), (128, 256, 4, 9), (256, 2048, 6, 24)])
-def test_linear_matrix_cores_short_spans(eng, oracle, inp, out, K, R, minkt, monkeypatch):
-    """The matrix-core GEMM with its k split allowed down to 2- and 4-tile spans (IJAH_LIN_MM_MINKT): every span must
-    stay an even tile count (the GEMM's steps take two tiles), including in = 288 / 352 / 576, whose halvings reach
-    odd spans (9, 11, 9) if the split does not stop first."""
-    print(f"linear mfma short spans {inp}x{out} K{K} R{R} minkt {minkt}", flush=True)
-    monkeypatch.setenv("IJAH_LIN_MM_MINKT", str(minkt))
-    rng = np.random.default_rng(inp * 3 + out + K + R + minkt)
-    t, su, sv = synth.linear(rng, inp, out, K)
-    x = synth.bf16_values(rng, R, inp)
-    lin = eng.exl3_linear(t, su, sv)
-    y = lin.run(x)
-    assert rel(y, oracle.exl3_linear(x, t, su, sv)) < 5e-5
-    assert rel(y, oracle.exl3_linear(x, t, su, sv, exact=True)) < 1e-2
+@pytest.mark.parametrize("R", [1, 4, 16])
+def test_linear_multi_launch_matches_single(eng, oracle, R):
+    """q, k and v of config 3 (2048 -> 4096 / 512 / 512, K6) and a K5 linear recorded together
+    (ne_exl3_lin_run_multi; reference trunk6.h:78 record_multi): each output bit-identical to the linear run alone
+    (the K5 one in a launch of its own), each on its own input rows."""
+    print(f"linear multi q/k/v R{R}", flush=True)
+    rng = np.random.default_rng(300 + R)
+    shapes = [(2048, 4096, 6), (2048, 512, 6), (2048, 512, 6), (1024, 256, 5)]
+    lins, xs = [], []
+    for inp, out, K in shapes:
+        lins.append(eng.exl3_linear(*synth.linear(rng, inp, out, K)))
+        xs.append(synth.bf16_values(rng, R, inp))
+    ys = eng.lin_run_multi(lins, xs)
+    for lin, x, y in zip(lins, xs, ys):
+        assert np.array_equal(y, lin.run(x))
+    assert np.array_equal(eng.lin_run_multi(lins, xs)[1], ys[1])  # again: the counters reset themselves
 
 
 @pytest.mark.parametrize("inp,out,K,R", [(2048, 512, 5, 1), (2048, 4096, 6, 3), (320, 640, 7, 8), (96, 48, 4, 2)])
 def test_linear_one_launch_matches_staged(eng, oracle, inp, out, K, R, monkeypatch):
-    """The one-launch linear (in-workgroup prep, last-arriver finish) against the three-launch path: bit-identical
-    (same per-element arithmetic and split order), over repeated runs (the block counters reset themselves)."""
+    """The one-launch linear (in-workgroup prep, last-arriver finish) against the three-launch path (prep launch, GEMM,
+    finish launch): bit-identical, over repeated runs (the block counters reset themselves)."""
     print(f"linear one-launch vs staged {inp}x{out} K{K} R{R}", flush=True)
     rng = np.random.default_rng(inp + out + K + R)
     t, su, sv = synth.linear(rng, inp, out, K)

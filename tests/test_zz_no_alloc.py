@@ -1,7 +1,7 @@
 """The allocation-free linear (ne_exl3_lin_run_noalloc) through the C ABI against ne_exl3_lin_run on the same linear
 and input: bit-identical outputs (the same kernels over the same partials, only their memory differs), on two calls in
-a row with the second smaller, over the one-launch GEMV (counters), the matrix-core GEMM and the 8-row-group paths;
-and a run needing more scratch than the fixed per-GPU array is rejected with an error."""
+a row with the second smaller, with the input prepared inside the GEMM and by a prep launch (many tile pairs times
+many rows); and a run needing more scratch than the fixed per-GPU array is rejected with an error."""
 import numpy as np
 import pytest
 
@@ -19,9 +19,9 @@ def run_noalloc(eng, lin, x):
 
 
 @pytest.mark.parametrize("inp,out,K,rows", [
-    (2048, 512, 5, (8, 3)),     # VALU GEMV, one launch with completion counters
-    (2048, 4096, 6, (16, 9)),   # matrix-core GEMM with k splits
-    (144, 272, 4, (20, 5)),     # odd k-tile count: groups of 8 rows through the GEMV
+    (2048, 512, 5, (8, 3)),     # one launch, completion counters, the input prepared inside the GEMM
+    (2048, 4096, 6, (32, 9)),   # 32 rows: a prep launch first; then 9 rows prepared inside the GEMM
+    (144, 272, 4, (20, 5)),     # a partial k chunk
 ])
 def test_noalloc_matches_run(eng, inp, out, K, rows):
     print(f"noalloc linear {inp}x{out} K{K} rows {rows}", flush=True)
