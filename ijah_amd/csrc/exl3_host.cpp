@@ -3,6 +3,8 @@
 #include <cmath>
 #include <cstring>
 #include <functional>
+#include <map>
+#include <mutex>
 #include <set>
 
 #include "kernels.h"
@@ -511,6 +513,38 @@ NE_API int ne_exl3_lin_decode(ne_exl3_lin *l, ne_buf *w, double *gpu_ms) {
 }  // extern "C"
 
 // ---------------------------------------------------------------------------------------------------- MoE layer
+// The few-row MoE kernels' tagged partials and epochs, one pool per layer shape shared by every layer of that shape
+// (the layers run one after another on the library's stream). Its layout is fixed by the shape and the chunk index,
+// so a stale partial never sits where a launch of another layer expects one with the same tag; it only grows (new
+// memory zeroed: tag 0 is never a launch's), never while a stream is captured.
+static void few_pool(int hid, int inter, int chunks, uint64_t **part, uint32_t **ep) {
+  struct Pool {
+    uint64_t *part = nullptr;
+    uint32_t *ep = nullptr;
+    int chunks = 0;
+  };
+  static std::mutex mu;
+  static std::map<std::pair<int, int>, Pool> pools;
+  std::lock_guard<std::mutex> g(mu);
+  Pool &p = pools[{hid, inter}];
+  if (chunks > p.chunks) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    IJ_HIP(hipStreamIsCapturing(stream(), &cs));
+    IJ_CHECK(cs == hipStreamCaptureStatusNone, "MoE: few-row scratch must grow before a stream capture");
+    IJ_HIP(hipStreamSynchronize(stream()));  // no launch still uses the old pool
+    dev_free(p.part);
+    dev_free(p.ep);
+    const size_t np = moe_batch_few_part(chunks, hid, inter), ne = moe_batch_few_epochs(chunks, inter);
+    p.part = dev_alloc<uint64_t>(np);
+    p.ep = dev_alloc<uint32_t>(ne);
+    IJ_HIP(hipMemset(p.part, 0, np * 8));
+    IJ_HIP(hipMemset(p.ep, 0, ne * 4));
+    p.chunks = chunks;
+  }
+  *part = p.part;
+  *ep = p.ep;
+}
+
 struct ne_moe {
   int hid = 0, inter = 0, ne = 0, topk = 0, K = 0, Ks = 0, has_shared = 0, has_sgate = 0, ksplit = 4;
   ExpertLayout lay, slay;
@@ -548,8 +582,12 @@ struct ne_moe {
   void ensure_batch(int R) {
     if (R <= bat_R || !batch_ok(R)) return;
     free_batch();
+    if (moe_batch_few(R, hid, inter, K, has_shared ? Ks : K)) {
+      bat.vmax_chunks = moe_batch_few_chunks(R, ne, topk, has_shared);
+      few_pool(hid, inter, bat.vmax_chunks, &bat.vpart, &bat.vep);
+    }
     const size_t S = (size_t)R * nslot();
-    bat.max_chunks = moe_batch_max_chunks(R, ne, topk, has_shared);
+    bat.max_chunks = std::max(moe_batch_max_chunks(R, ne, topk, has_shared), bat.vmax_chunks);
     bat.bk = dev_alloc<uint32_t>(3 * (size_t)(ne + 1) + 1);
     IJ_HIP(hipMemset(bat.bk, 0, sizeof(uint32_t) * (3 * (size_t)(ne + 1) + 1)));  // bat_hist adds into the counts
     bat.chunks = dev_alloc<uint32_t>(3 * (size_t)bat.max_chunks);

@@ -93,10 +93,20 @@ struct MoeBatchBufs {
   uint16_t *hh = nullptr;      // [R nslot][inter] prepared down inputs
   float *dnw = nullptr;        // [R][nslot][hid] weighted slot outputs
   int max_chunks = 0;
+  // few rows (moe_batch_few): the k group partials and the (chunk, block) epochs, shared by the layers of one shape
+  uint64_t *vpart = nullptr;   // [chunk][2][inter / 32][k groups][8 rows][32] tagged
+  uint32_t *vep = nullptr;     // [chunk][inter / 128] epochs, kSyncStride apart
+  int vmax_chunks = 0;
 };
 bool moe_batch_supported(int K, int KS, int hid, int inter, int ne, int topk);
 bool moe_batch_exact(const MoeArgs &a);  // the batch keeps the one-row step's arithmetic (few rows)
 int moe_batch_max_chunks(int R, int ne, int topk, bool shared);
+// few rows: the grouped-k kernels (R <= 32, exact arithmetic, intermediate size within their LDS); their chunk bound
+// (one chunk per touched expert) and scratch
+bool moe_batch_few(int R, int hid, int inter, int K, int KS);
+int moe_batch_few_chunks(int R, int ne, int topk, bool shared);
+size_t moe_batch_few_part(int chunks, int hid, int inter);  // u64 words of vpart
+size_t moe_batch_few_epochs(int chunks, int inter);         // u32 words of vep
 void launch_moe_batch(const MoeArgs &a, const MoeBatchBufs &b, hipStream_t s);
 // Fused step logits: kLogitReplicas copies of [ne + 1] floats, moe_logit_stride(ne) floats apart (replica 0 is the
 // [R = 1][ne + 1] logits buffer the staged path uses); the copies spread the workgroups' polling over memory channels.

@@ -247,32 +247,41 @@ __global__ __launch_bounds__(512, 2) void bat_router_rows(MoeArgs a, int ngroups
 }
 
 // Few rows (speculative verify): logits with the one-row step's arithmetic, so that a row of a batch routes exactly
-// as it would alone. Wave w of workgroup b: router column 4 b + w for every row; lane l keeps elements
-// [512 j + 8 l, +8) of the column, j < hid / 512, and chains one fmaf per element in that order, then the lanes'
-// sums meet in an xor butterfly over lane distances 32, 16, .., 1 (reference kernels/fn_moe.metal:50-67).
+// as it would alone. Wave w of workgroup (b, r): router column 4 b + w for row r; lane l holds elements
+// [512 j + 8 l, +8) of the column, j < hid / 512 (all requested at once), and chains one fmaf per element in that
+// order, then the lanes' sums meet in an xor butterfly over lane distances 32, 16, .., 1 (reference
+// kernels/fn_moe.metal:50-67).
+constexpr int kRouterExactChunks = 16;  // hid <= 8192
 __global__ __launch_bounds__(256) void bat_router_exact(MoeArgs a) {
-  const int lane = threadIdx.x & 63, col = blockIdx.x * 4 + (threadIdx.x >> 6), nc = a.hid / 512;
+  const int lane = threadIdx.x & 63, col = blockIdx.x * 4 + (threadIdx.x >> 6), r = blockIdx.y, nc = a.hid / 512;
   if (col >= a.ne + a.has_sgate) return;
   const uint16_t *w = a.router + (uint64_t)col * a.hid + lane * 8;
-  for (int r = 0; r < a.R; r++) {
-    const float *x = a.x + (uint64_t)r * a.hid + lane * 8;
-    float acc = 0.f;
-    for (int j = 0; j < nc; j++) {
-      const uint4 wv = *(const uint4 *)(w + j * 512);
-      const float4 x0 = *(const float4 *)(x + j * 512), x1 = *(const float4 *)(x + j * 512 + 4);
-      acc = fmaf(x0.x, bf16_f32(wv.x & 0xFFFFu), acc);
-      acc = fmaf(x0.y, bf16_f32(wv.x >> 16), acc);
-      acc = fmaf(x0.z, bf16_f32(wv.y & 0xFFFFu), acc);
-      acc = fmaf(x0.w, bf16_f32(wv.y >> 16), acc);
-      acc = fmaf(x1.x, bf16_f32(wv.z & 0xFFFFu), acc);
-      acc = fmaf(x1.y, bf16_f32(wv.z >> 16), acc);
-      acc = fmaf(x1.z, bf16_f32(wv.w & 0xFFFFu), acc);
-      acc = fmaf(x1.w, bf16_f32(wv.w >> 16), acc);
+  const float *x = a.x + (uint64_t)r * a.hid + lane * 8;
+  uint4 wv[kRouterExactChunks];
+  float4 x0[kRouterExactChunks], x1[kRouterExactChunks];
+#pragma unroll
+  for (int j = 0; j < kRouterExactChunks; j++)
+    if (j < nc) {
+      wv[j] = *(const uint4 *)(w + j * 512);
+      x0[j] = *(const float4 *)(x + j * 512);
+      x1[j] = *(const float4 *)(x + j * 512 + 4);
+    }
+  float acc = 0.f;
+#pragma unroll
+  for (int j = 0; j < kRouterExactChunks; j++)
+    if (j < nc) {
+      acc = fmaf(x0[j].x, bf16_f32(wv[j].x & 0xFFFFu), acc);
+      acc = fmaf(x0[j].y, bf16_f32(wv[j].x >> 16), acc);
+      acc = fmaf(x0[j].z, bf16_f32(wv[j].y & 0xFFFFu), acc);
+      acc = fmaf(x0[j].w, bf16_f32(wv[j].y >> 16), acc);
+      acc = fmaf(x1[j].x, bf16_f32(wv[j].z & 0xFFFFu), acc);
+      acc = fmaf(x1[j].y, bf16_f32(wv[j].z >> 16), acc);
+      acc = fmaf(x1[j].z, bf16_f32(wv[j].w & 0xFFFFu), acc);
+      acc = fmaf(x1[j].w, bf16_f32(wv[j].w >> 16), acc);
     }
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) acc += __shfl_xor(acc, o, 64);
-    if (lane == 0) a.logits[(uint64_t)r * (a.ne + 1) + col] = bf16_round(acc);
-  }
+  for (int o = 32; o >= 1; o >>= 1) acc += __shfl_xor(acc, o, 64);
+  if (lane == 0) a.logits[(uint64_t)r * (a.ne + 1) + col] = bf16_round(acc);
 }
 
 // ---------------------------------------------------------------------------------------------------- route
@@ -367,7 +376,7 @@ __global__ __launch_bounds__(256) void bat_hist(MoeArgs a, uint32_t *bk) {
 // 1 chunk count; chunks: u32x3.
 // With self_count (few rows) the workgroup counts the route itself instead (one launch fewer).
 __global__ __launch_bounds__(1024) void bat_scan(MoeArgs a, uint32_t *bk, uint32_t *chunks, int max_chunks,
-                                                 int self_count) {
+                                                 int self_count, uint32_t crows) {
   __shared__ uint32_t sc[1024 + 1], cc[1024 + 1];
   const int tid = threadIdx.x, n = a.ne + (a.nslot > a.topk ? 1 : 0);
   uint32_t *counts = bk, *offs = bk + (a.ne + 1), *cursor = offs + (a.ne + 1), *nchunks = cursor + (a.ne + 1);
@@ -418,7 +427,7 @@ __global__ __launch_bounds__(1024) void bat_scan(MoeArgs a, uint32_t *bk, uint32
   __syncthreads();
   if (tid < a.ne) counts[tid] = 0u;  // ready for the next layer's bat_hist
   sc[tid] = c;
-  cc[tid] = (c + kChunkRows - 1) / kChunkRows;
+  cc[tid] = (c + crows - 1) / crows;
   __syncthreads();
   for (int d = 1; d < 1024; d <<= 1) {  // inclusive Hillis-Steele scans of rows and chunks
     const uint32_t v = tid >= d ? sc[tid - d] : 0u, w = tid >= d ? cc[tid - d] : 0u;
@@ -428,14 +437,14 @@ __global__ __launch_bounds__(1024) void bat_scan(MoeArgs a, uint32_t *bk, uint32
     __syncthreads();
   }
   if (tid < n) {
-    const uint32_t off = sc[tid] - c, ch0 = cc[tid] - (c + kChunkRows - 1) / kChunkRows;
+    const uint32_t off = sc[tid] - c, ch0 = cc[tid] - (c + crows - 1) / crows;
     offs[tid] = off;
     cursor[tid] = 0u;
-    for (uint32_t r = 0, q = ch0; r < c; r += kChunkRows, q++)
+    for (uint32_t r = 0, q = ch0; r < c; r += crows, q++)
       if ((int)q < max_chunks) {
         chunks[3 * q] = (uint32_t)tid;
         chunks[3 * q + 1] = off + r;
-        chunks[3 * q + 2] = min(c - r, (uint32_t)kChunkRows);
+        chunks[3 * q + 2] = min(c - r, crows);
       }
   }
   if (tid == 0) *nchunks = min(cc[n > 0 ? n - 1 : 0], (uint32_t)max_chunks);
@@ -622,38 +631,44 @@ __global__ __launch_bounds__(64 * kPrepWaves, 2) void bat_place_prep(MoeArgs a, 
   if (lane == 0) rows[(orow_p - xh) / (2 * a.hid)] = (uint32_t)s;
 }
 
-// Few rows (speculative verify): the same placement with the one-row step's prepared input, a lane butterfly per
-// 128-wide chunk: v = x * suh (f32), H_128 with 1/sqrt(128), fp16, kp order (reference kernels/fn_moe.metal:140-160)
-__global__ __launch_bounds__(256) void bat_place_exact(MoeArgs a, uint32_t *bk, uint32_t *rows, uint16_t *xh) {
-  const int lane = threadIdx.x & 63, s = blockIdx.x * 4 + (threadIdx.x >> 6);
+// Few rows (speculative verify): the placement, then the one-row step's prepared input.
+// bat_place_rows: one thread per slot (r, k): its row in its expert's list (rows[row] = r * nslot + k; the shared
+// expert's list is every token in order; the order inside an expert changes no result).
+__global__ __launch_bounds__(256) void bat_place_rows(MoeArgs a, uint32_t *bk, uint32_t *rows) {
+  const int s = blockIdx.x * 256 + threadIdx.x;
   if (s >= a.R * a.nslot) return;
   const int r = s / a.nslot, k = s % a.nslot;
   const uint32_t *offs = bk + (a.ne + 1);
   uint32_t *cursor = bk + 2 * (a.ne + 1);
   int e = a.ne;
+  uint32_t pos = (uint32_t)r;
+  if (k < a.topk) {
+    e = (int)a.route[(uint64_t)r * 2 * a.topk + k];
+    e = e < a.ne ? e : 0;
+    pos = atomicAdd(cursor + e, 1u);
+  }
+  rows[offs[e] + pos] = (uint32_t)s;
+}
+// bat_prep_rows: wave (row, 128-wide chunk c, projection) of the placed rows: a lane butterfly per chunk,
+// v = x * suh (f32), H_128 with 1/sqrt(128), fp16, kp order (reference kernels/fn_moe.metal:140-160)
+__global__ __launch_bounds__(256) void bat_prep_rows(MoeArgs a, const uint32_t *rows, uint16_t *xh) {
+  const int lane = threadIdx.x & 63, nq = 2 * (a.hid / 128);
+  const int w = blockIdx.x * 4 + (threadIdx.x >> 6), row = w / nq, q = w % nq, proj = q & 1, c = q >> 1;
+  if (row >= a.R * a.nslot) return;
+  const uint32_t s = rows[row];
+  const int r = (int)s / a.nslot, k = (int)s % a.nslot;
+  int e = a.ne;
   if (k < a.topk) {
     e = (int)a.route[(uint64_t)r * 2 * a.topk + k];
     e = e < a.ne ? e : 0;
   }
-  uint32_t pos = (uint32_t)r;  // the shared expert's list is every token in order
-  if (k < a.topk) {
-    uint32_t p0 = 0u;
-    if (lane == 0) p0 = atomicAdd(cursor + e, 1u);
-    pos = (uint32_t)__shfl(p0, 0, 64);
-  }
-  const uint32_t row = offs[e] + pos;
-  const uint8_t *eb = expert_block(a, e);
-  const float *x = a.x + (uint64_t)r * a.hid;
-  for (int q = 0; q < 2 * (a.hid / 128); q++) {
-    const int proj = q & 1, c = q >> 1;
-    const uint16_t *su = (const uint16_t *)(eb + su_of(a, e, proj)) + c * 128;
-    float v0 = x[c * 128 + lane] * h2f(su[lane]), v1 = x[c * 128 + lane + 64] * h2f(su[lane + 64]);
-    fwht2(v0, v1, lane, 128, a.sc_hid);
-    uint16_t *o = xh + (uint64_t)row * 2 * a.hid + proj * a.hid + c * 128;
-    o[kp(lane)] = f2h(v0);
-    o[kp(lane + 64)] = f2h(v1);
-  }
-  if (lane == 0) rows[row] = (uint32_t)s;
+  const uint16_t *su = (const uint16_t *)(expert_block(a, e) + su_of(a, e, proj)) + c * 128;
+  const float *x = a.x + (uint64_t)r * a.hid + c * 128;
+  float v0 = x[lane] * h2f(su[lane]), v1 = x[lane + 64] * h2f(su[lane + 64]);
+  fwht2(v0, v1, lane, 128, a.sc_hid);
+  uint16_t *o = xh + ((uint64_t)row * 2 + proj) * a.hid + c * 128;
+  o[kp((uint32_t)lane)] = f2h(v0);
+  o[kp((uint32_t)lane + 64)] = f2h(v1);
 }
 
 // ---------------------------------------------------------------------------------------------------- grouped GEMM
@@ -1235,6 +1250,224 @@ __global__ __launch_bounds__(256) void bat_combine(MoeArgs a, const float *__res
 }
 
 
+// ---------------------------------------------------------------------------------------------------- few rows
+// Speculative verify (at most 32 rows, so an expert's rows are one chunk) with the k order of the one-row step and of
+// the trunk linear, spread so that every SIMD decodes:
+//   bat_gu_grp  workgroup (chunk, 128-column block cb of inter, projection, pair q of the block), looping over the k
+//               groups of 512 (the next group's requests in flight while one decodes); wave c takes k chunk c of each
+//               group (8 k tiles, one MFMA chain from zero); the chunk sums are folded left in LDS, the groups left in
+//               registers, and the pair's sums stored as tagged values. The block's finisher, the highest-numbered of
+//               its producers (workgroups are dispatched in index order per XCD, so it waits only for dispatched
+//               ones), writes the block's rows of hh (H(g) svh_g, SiLU, H(u) svh_u, suh_d, H, fp16, kp order), then
+//               advances the block's epoch;
+//   bat_dn_blk  workgroup (chunk, 128-column output block c), wave q one pair: every k chunk of inter (chains from zero,
+//               folded left), then H, svh_d and the slot's route weight per row (no hand-off between workgroups).
+// Tags: the epoch of the (chunk, block) slot plus one; the partials and epochs are shared by every layer (one
+// stream), so tags only grow and no stale partial carries a current tag.
+constexpr int kVChunk = 8;  // k tiles of a k chunk
+constexpr int kFewChunkRows = 4;  // rows of a chunk on the few-row path (its LDS tier)
+constexpr int kFewMaxGroups = 8;  // k groups of 512 (hidden size up to 4096)
+template <int KD, int RT>
+__device__ __forceinline__ f32x16 v_chain(const uint8_t *tl, const _Float16 *xs, int pitch, int nkt, int nrows) {
+  const int lane = threadIdx.x & 63;
+  const _Float16 *xa = xs + min(lane & 31, nrows - 1) * pitch + 8 * (lane >> 5);
+  f32x16 acc;
+#pragma unroll
+  for (int i = 0; i < 16; i++) acc[i] = 0.f;
+#pragma unroll
+  for (int kt = 0; kt < kVChunk; kt++)
+    if (kt < nkt) {
+      const f16x8 bv = decode_pair<KD>(tl, kt);
+      const f16x8 av = *(const f16x8 *)(xa + kt * 16);
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bv, acc, 0, 0, 0);
+    }
+  return acc;
+}
+// bytes staged per wave and buffer: 8 k tile pairs at the larger K, then RT rows of the chunk (128 halves each); two
+// buffers per wave (the next k group's requests in flight while this one decodes)
+template <int KM, int RT>
+constexpr uint32_t v_gu_wave() { return kVChunk * 64 * KM + RT * 256; }
+template <int KM, int RT>
+constexpr uint32_t v_gu_lds(int G) { return 8 * v_gu_wave<KM, RT>() + (uint32_t)G * 4 * RT * 32 * 4; }
+
+template <int K, int KS, int RT>
+__global__ __launch_bounds__(256) void bat_gu_grp(MoeArgs a, const uint32_t *bk, const uint32_t *chunks,
+                                                  const uint16_t *xh, uint16_t *hh, uint64_t *part, uint32_t *epochs) {
+  constexpr int KM = K > KS ? K : KS;
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const int NP = a.inter / 32, NBI = a.inter / 128, IT = a.hid / 16, G = (IT + 31) / 32;
+  const int upc = NBI * 8, ch = (int)blockIdx.x / upc, rem = (int)blockIdx.x % upc;
+  if (ch >= (int)bk[3 * (a.ne + 1)]) return;
+  const int q = rem & 3, proj = (rem >> 2) & 1, cb = rem >> 3, p = cb * 4 + q;
+  const int e = (int)chunks[3 * ch], row0 = (int)chunks[3 * ch + 1], nrows = (int)chunks[3 * ch + 2];
+  const int lane = threadIdx.x & 63, c = (int)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const bool sh = e >= a.ne;
+  const int KE = sh ? KS : K;
+  float *csum = (float *)(lds + 8 * v_gu_wave<KM, RT>());  // [k group][4 chunks][RT][32]
+  uint32_t *ep = epochs + ((uint64_t)ch * NBI + cb) * kSyncStride;
+  const uint32_t e0 = ld_cg(ep);
+  const uint8_t *blk = expert_block(a, e);
+  const uint8_t *tr = blk + tr_of(a, e, proj) + (uint64_t)p * IT * 64 * KE;
+  // requests of k group g into buffer g & 1: this wave's chunk of tiles, then its rows; returns their count
+  auto stage = [&](int g) {
+    const int kt0 = g * 32 + c * kVChunk, nkt = max(0, min(kVChunk, IT - kt0));
+    uint8_t *tl = lds + (2 * c + (g & 1)) * v_gu_wave<KM, RT>();
+    _Float16 *xs = (_Float16 *)(tl + kVChunk * 64 * KM);
+    int n = 0;
+    if (nkt > 0) {
+      const uint32_t bytes = (uint32_t)nkt * 64 * KE;
+      for (uint32_t o = 0; o < bytes; o += 1024, n++)
+        if (o + (uint32_t)lane * 16 < bytes) dma16(tr + (uint64_t)kt0 * 64 * KE + o + lane * 16, tl + o);
+      for (int r = 0; r < nrows; r += 4, n++) {  // rows r .. r + 3: 16 lanes of 16 bytes each
+        const int rr = r + (lane >> 4), qq = lane & 15;
+        if (rr < nrows && qq * 16 < nkt * 32)
+          dma16(xh + ((uint64_t)(row0 + rr) * 2 + proj) * a.hid + kt0 * 16 + qq * 8, xs + r * 128);
+      }
+    }
+    return n;
+  };
+  stage(0);
+  // each wave on its own through the k groups (no barrier until every chunk sum is in LDS)
+  for (int g = 0; g < G; g++) {
+    const int nnext = g + 1 < G ? stage(g + 1) : 0;
+    wait_vm15(nnext);  // group g's requests are in (the next group's may not be)
+    const int kt0 = g * 32 + c * kVChunk, nkt = max(0, min(kVChunk, IT - kt0));
+    const uint8_t *tl = lds + (2 * c + (g & 1)) * v_gu_wave<KM, RT>();
+    const _Float16 *xs = (const _Float16 *)(tl + kVChunk * 64 * KM);
+    f32x16 acc;
+    if (sh && KS != K)
+      acc = v_chain<KS, RT>(tl, xs, 128, nkt, nrows);
+    else
+      acc = v_chain<K, RT>(tl, xs, 128, nkt, nrows);
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      const int r = 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+      if (r < RT && r < nrows) csum[((g * 4 + c) * RT + r) * 32 + (lane & 31)] = acc[i];
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this group's buffer reads are done before it is refilled
+  }
+  __syncthreads();
+  // per (row, column): the chunks of each group folded left, the groups folded left
+  const int ent = threadIdx.x;
+  float tot = 0.f;
+  if (ent < nrows * 32)
+    for (int g = 0; g < G; g++) {
+      const int nc = (min(32, IT - g * 32) + kVChunk - 1) / kVChunk;
+      float v = csum[(g * 4) * RT * 32 + ent];
+      for (int cc = 1; cc < nc; cc++) v = v + csum[(g * 4 + cc) * RT * 32 + ent];
+      tot = g == 0 ? v : tot + v;
+    }
+  const uint32_t tag = (uint32_t)__builtin_amdgcn_readfirstlane(e0) + 1u;
+  if (ent < nrows * 32)
+    st_tag(part + ((((uint64_t)ch * 2 + proj) * NP + p) * kFewChunkRows + (ent >> 5)) * 32 + (ent & 31), tot, tag);
+  if (proj != 1 || q != 3) return;
+  // the block's finisher: rows r = wave, wave + 4, ..; lane: columns o = lane, lane + 64 of block cb
+  const uint16_t *svg = (const uint16_t *)(blk + sv_of(a, e, 0)) + cb * 128;
+  const uint16_t *svu = (const uint16_t *)(blk + sv_of(a, e, 1)) + cb * 128;
+  const uint16_t *sud = (const uint16_t *)(blk + su_of(a, e, 2)) + cb * 128;
+  const int pr0 = cb * 4 + (lane >> 5), n0 = lane & 31;  // column lane: pair pr0; column lane + 64: pair pr0 + 2
+  for (int r = c; r < nrows; r += 4) {
+    float gs[2] = {0.f, 0.f}, us[2] = {0.f, 0.f};
+    for (uint32_t it = 0; it < (1u << 20); it++) {
+      bool all = true;
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        const uint64_t ug = ld_cg(part + ((((uint64_t)ch * 2 + 0) * NP + pr0 + 2 * h) * kFewChunkRows + r) * 32 + n0);
+        const uint64_t uu = ld_cg(part + ((((uint64_t)ch * 2 + 1) * NP + pr0 + 2 * h) * kFewChunkRows + r) * 32 + n0);
+        all = all && tag_ok(ug, tag) && tag_ok(uu, tag);
+        gs[h] = tag_val(ug);
+        us[h] = tag_val(uu);
+      }
+      if (__all(all)) break;
+    }
+    float g0 = gs[0], g1 = gs[1], u0 = us[0], u1 = us[1];
+    fwht2(g0, g1, lane, a.had_inter, a.sc_inter);
+    fwht2(u0, u1, lane, a.had_inter, a.sc_inter);
+    g0 = g0 * h2f(svg[lane]);
+    u0 = u0 * h2f(svu[lane]);
+    g1 = g1 * h2f(svg[lane + 64]);
+    u1 = u1 * h2f(svu[lane + 64]);
+    float h0 = g0 / (1.f + expf(-g0)) * u0 * h2f(sud[lane]);
+    float h1 = g1 / (1.f + expf(-g1)) * u1 * h2f(sud[lane + 64]);
+    fwht2(h0, h1, lane, a.had_inter, a.sc_inter);
+    uint16_t *out = hh + (uint64_t)(row0 + r) * a.inter + cb * 128;
+    out[kp((uint32_t)lane)] = f2h(h0);
+    out[kp((uint32_t)lane + 64)] = f2h(h1);
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) st_cg(ep, tag);
+}
+
+// LDS: per wave its pair's k tile pairs (all of inter), then the chunk's RT rows of hh (inter halves each), then the
+// [RT][128] outputs
+template <int KM, int RT>
+__host__ __device__ constexpr uint32_t v_dn_lds(int inter) {
+  return 4u * (uint32_t)(inter / 16) * 64 * KM + (uint32_t)RT * inter * 2 + RT * 128 * 4;
+}
+template <int K, int KS, int RT>
+__global__ __launch_bounds__(256) void bat_dn_blk(MoeArgs a, const uint32_t *bk, const uint32_t *chunks,
+                                                  const uint32_t *rows, const uint16_t *hh, float *dnw) {
+  constexpr int KM = K > KS ? K : KS;
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const int NBLK = a.hid / 128, ITd = a.inter / 16, ch = (int)blockIdx.x / NBLK, cblk = (int)blockIdx.x % NBLK;
+  if (ch >= (int)bk[3 * (a.ne + 1)]) return;
+  const int e = (int)chunks[3 * ch], row0 = (int)chunks[3 * ch + 1], nrows = (int)chunks[3 * ch + 2];
+  const int lane = threadIdx.x & 63, q = (int)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6), p = cblk * 4 + q;
+  const bool sh = e >= a.ne;
+  const int KE = sh ? KS : K;
+  const uint32_t wb = (uint32_t)ITd * 64 * KM;
+  uint8_t *tl = lds + q * wb;
+  _Float16 *xs = (_Float16 *)(lds + 4 * wb);
+  float *ot = (float *)(lds + 4 * wb + RT * a.inter * 2);
+  const uint8_t *blk = expert_block(a, e);
+  // each row's slot (token, k) and route weight; then the rows of hh (nrows x inter halves, contiguous; 1 KB per
+  // request, spread over the 4 waves), then the wave's tiles: the k chunks arrive in order while earlier ones decode
+  const uint32_t sl = lane < nrows ? rows[row0 + lane] : 0u;
+  {
+    const uint32_t rb = (uint32_t)nrows * a.inter * 2;
+    const uint8_t *hs = (const uint8_t *)(hh + (uint64_t)row0 * a.inter);
+    for (uint32_t o = (uint32_t)q * 1024; o < rb; o += 4096)
+      if (o + (uint32_t)lane * 16 < rb) dma16(hs + o + lane * 16, (uint8_t *)xs + o);
+  }
+  const uint32_t cbytes = kVChunk * 64 * KE, bytes = (uint32_t)ITd * 64 * KE;
+  const int nops = (int)((bytes + 1023) / 1024);
+  {
+    const uint8_t *src = blk + tr_of(a, e, 2) + (uint64_t)p * ITd * 64 * KE;
+    for (uint32_t o = 0; o < bytes; o += 1024)
+      if (o + (uint32_t)lane * 16 < bytes) dma16(src + o + lane * 16, tl + o);
+  }
+  wait_vm15(nops);  // this wave's rows of hh are in
+  __syncthreads();  // every wave's
+  f32x16 s;
+  for (int cc = 0; cc < ITd / kVChunk; cc++) {  // the k chunks of inter, folded left
+    wait_vm15(nops - (int)(((uint32_t)(cc + 1) * cbytes + 1023) / 1024));  // chunk cc's tiles are in
+    f32x16 acc = (sh && KS != K) ? v_chain<KS, RT>(tl + cc * kVChunk * 64 * KS, xs + cc * kVChunk * 16, a.inter,
+                                                   kVChunk, nrows)
+                                 : v_chain<K, RT>(tl + cc * kVChunk * 64 * K, xs + cc * kVChunk * 16, a.inter,
+                                                  kVChunk, nrows);
+#pragma unroll
+    for (int i = 0; i < 16; i++) s[i] = cc == 0 ? acc[i] : s[i] + acc[i];
+  }
+#pragma unroll
+  for (int i = 0; i < 16; i++) {
+    const int r = 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+    if (r < RT && r < nrows) ot[r * 128 + q * 32 + (lane & 31)] = s[i];
+  }
+  __syncthreads();
+  const uint16_t *svd = (const uint16_t *)(blk + sv_of(a, e, 2)) + cblk * 128;
+  const float s0 = h2f(svd[lane]), s1 = h2f(svd[lane + 64]);
+  for (int r = q; r < nrows; r += 4) {
+    const uint32_t slr = (uint32_t)__shfl((int)sl, r, 64);
+    const int tok = (int)(slr / a.nslot), k = (int)(slr % a.nslot);
+    const float w = k >= a.topk ? a.sgv[tok] : __uint_as_float(a.route[(uint64_t)tok * 2 * a.topk + a.topk + k]);
+    float v0 = ot[r * 128 + lane], v1 = ot[r * 128 + 64 + lane];
+    fwht2(v0, v1, lane, a.had_hid, a.sc_hid);
+    float *out = dnw + (uint64_t)slr * a.hid + cblk * 128;
+    out[lane] = v0 * s0 * w;
+    out[lane + 64] = v1 * s1 * w;
+  }
+}
+
 // ---------------------------------------------------------------------------------------------------- host side
 namespace {
 template <int K, int KS, bool TR, int NR, bool EX = false>
@@ -1265,6 +1498,33 @@ void launch_gemms(const MoeArgs &a, const MoeBatchBufs &b, hipStream_t s) {
 }
 }  // namespace
 
+template <int K, int KS, int RT>
+void launch_few_rt(const MoeArgs &a, const MoeBatchBufs &b, hipStream_t s) {
+  constexpr int KM = K > KS ? K : KS;
+  const int NBI = a.inter / 128, NBLK = a.hid / 128;
+  const size_t lg = v_gu_lds<KM, RT>(a.hid / 512), ld = v_dn_lds<KM, RT>(a.inter);
+  hipLaunchKernelGGL((bat_gu_grp<K, KS, RT>), dim3(b.vmax_chunks * NBI * 8), dim3(256), lg, s, a, b.bk, b.chunks,
+                     b.xh, b.hh, b.vpart, b.vep);
+  hipLaunchKernelGGL((bat_dn_blk<K, KS, RT>), dim3(b.vmax_chunks * NBLK), dim3(256), ld, s, a, b.bk, b.chunks, b.rows,
+                     b.hh, b.dnw);
+}
+template <int K, int KS>
+void launch_few(const MoeArgs &a, const MoeBatchBufs &b, hipStream_t s) {
+  launch_few_rt<K, KS, kFewChunkRows>(a, b, s);
+}
+template <int K, int KS, int RT>
+static void few_attrs_rt() {
+  constexpr int KM = K > KS ? K : KS;
+  IJ_HIP(hipFuncSetAttribute((const void *)&bat_gu_grp<K, KS, RT>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)v_gu_lds<KM, RT>(kFewMaxGroups)));
+  IJ_HIP(hipFuncSetAttribute((const void *)&bat_dn_blk<K, KS, RT>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            160 * 1024));
+}
+template <int K, int KS>
+static void few_attrs() {
+  few_attrs_rt<K, KS, kFewChunkRows>();
+}
+
 // Raises the dynamic LDS limit of every kernel that needs more than the default, once at device set-up: never
 // lazily at a first launch, which may happen inside a stream capture.
 template <int K, int KS, bool TR, int NR, bool EX = false>
@@ -1288,10 +1548,28 @@ void init_batch_attrs() {
   gemm_attrs_all<4, 4>(); gemm_attrs_all<5, 5>(); gemm_attrs_all<6, 6>(); gemm_attrs_all<4, 5>();
   gemm_attrs_all<4, 6>(); gemm_attrs_all<5, 6>(); gemm_attrs_all<5, 4>(); gemm_attrs_all<6, 4>();
   gemm_attrs_all<6, 5>();
+  few_attrs<4, 4>(); few_attrs<5, 5>(); few_attrs<6, 6>(); few_attrs<4, 5>(); few_attrs<4, 6>(); few_attrs<5, 6>();
+  few_attrs<5, 4>(); few_attrs<6, 4>(); few_attrs<6, 5>();
 }
 
 // Few rows: every kernel keeps the one-row step's arithmetic (hidden size a multiple of 512 for its router rows)
 bool moe_batch_exact(const MoeArgs &a) { return a.R <= 32 && a.hid % 512 == 0; }
+static size_t v_dn_bytes(int inter, int KM) {
+  return 4ull * (inter / 16) * 64 * KM + (size_t)kFewChunkRows * inter * 2 + (size_t)kFewChunkRows * 128 * 4;
+}
+bool moe_batch_few(int R, int hid, int inter, int K, int KS) {
+  return R <= 32 && hid % 512 == 0 && hid / 512 <= kFewMaxGroups && v_dn_bytes(inter, std::max(K, KS)) <= 160 * 1024;
+}
+int moe_batch_few_chunks(int R, int ne, int topk, bool shared) {
+  // chunks of at most kFewChunkRows rows: one per touched expert, plus one per further kFewChunkRows rows
+  return std::min(ne, R * topk) + (R * topk + kFewChunkRows - 1) / kFewChunkRows +
+         (shared ? (R + kFewChunkRows - 1) / kFewChunkRows : 0);
+}
+size_t moe_batch_few_part(int chunks, int hid, int inter) {
+  (void)hid;
+  return (size_t)chunks * 2 * (inter / 32) * kFewChunkRows * 32;
+}
+size_t moe_batch_few_epochs(int chunks, int inter) { return (size_t)chunks * (inter / 128) * kSyncStride; }
 
 bool moe_batch_supported(int K, int KS, int hid, int inter, int ne, int topk) {
   const bool ks = (K >= 4 && K <= 6) && (KS >= 4 && KS <= 6);
@@ -1307,21 +1585,39 @@ void launch_moe_batch(const MoeArgs &a, const MoeBatchBufs &b, hipStream_t s) {
     const int ng = (a.R + kRtRows - 1) / kRtRows;
     hipLaunchKernelGGL(bat_router_rows, dim3((ng * ((ncol + 127) / 128) + 7) & ~7), dim3(512), 0, s, a, ng);
   } else if (moe_batch_exact(a)) {
-    hipLaunchKernelGGL(bat_router_exact, dim3((ncol + 3) / 4), dim3(256), 0, s, a);
+    IJ_CHECK(a.hid / 512 <= kRouterExactChunks, "few-row router: hidden %d above %d", a.hid, 512 * kRouterExactChunks);
+    hipLaunchKernelGGL(bat_router_exact, dim3((ncol + 3) / 4, a.R), dim3(256), 0, s, a);
   } else {
     hipLaunchKernelGGL(bat_router<1>, dim3((a.R + 31) / 32, (ncol + 31) / 32), dim3(64 * kRouterWaves), 0, s, a);
   }
   hipLaunchKernelGGL(bat_route, dim3((a.R + 3) / 4), dim3(256), 0, s, a);
   const int self_count = a.R * a.topk < 4096;  // few slots: counted inside bat_scan
   if (!self_count) hipLaunchKernelGGL(bat_hist, dim3(kHistGroups), dim3(256), 0, s, a, b.bk);
-  hipLaunchKernelGGL(bat_scan, dim3(1), dim3(1024), 0, s, a, b.bk, b.chunks, b.max_chunks, self_count);
+  const int KS = a.nslot > a.topk ? a.slay.K : a.lay.K;
+  const bool few = moe_batch_exact(a) && b.vpart && moe_batch_few(a.R, a.hid, a.inter, a.lay.K, KS);
+  hipLaunchKernelGGL(bat_scan, dim3(1), dim3(1024), 0, s, a, b.bk, b.chunks, b.max_chunks, self_count,
+                     (uint32_t)(few ? kFewChunkRows : kChunkRows));
   IJ_CHECK(a.had_hid == 128, "batched MoE: hidden size %d needs a 128-wide Hadamard", a.hid);
-  if (moe_batch_exact(a))
-    hipLaunchKernelGGL(bat_place_exact, dim3((S + 3) / 4), dim3(256), 0, s, a, b.bk, b.rows, b.xh);
-  else
+  if (moe_batch_exact(a)) {
+    hipLaunchKernelGGL(bat_place_rows, dim3((S + 255) / 256), dim3(256), 0, s, a, b.bk, b.rows);
+    hipLaunchKernelGGL(bat_prep_rows, dim3((S * 2 * (a.hid / 128) + 3) / 4), dim3(256), 0, s, a, b.rows, b.xh);
+  } else
     hipLaunchKernelGGL(bat_place_prep, dim3((S + kPrepWaves - 1) / kPrepWaves), dim3(64 * kPrepWaves), kPrepLds, s,
                        a, b.bk, b.rows, b.xh);
-  const int KS = a.nslot > a.topk ? a.slay.K : a.lay.K;
+  if (few) {
+    IJ_CHECK(b.vmax_chunks >= moe_batch_few_chunks(a.R, a.ne, a.topk, a.nslot > a.topk), "few-row MoE: scratch");
+    bool ok = false;
+#define IJ_FEW(k, ks)                                  \
+  if (!ok && a.lay.K == k && KS == ks) {               \
+    launch_few<k, ks>(a, b, s);                        \
+    ok = true;                                         \
+  }
+    IJ_FEW(4, 4) IJ_FEW(5, 5) IJ_FEW(6, 6) IJ_FEW(4, 5) IJ_FEW(4, 6) IJ_FEW(5, 6) IJ_FEW(5, 4) IJ_FEW(6, 4) IJ_FEW(6, 5)
+#undef IJ_FEW
+    IJ_CHECK(ok, "few-row MoE: K%d / shared K%d not instantiated", a.lay.K, KS);
+    hipLaunchKernelGGL(bat_combine, dim3(a.R, (a.hid + 1023) / 1024), dim3(256), 0, s, a, b.dnw);
+    return;
+  }
   bool done = false;
 #define IJ_BAT(k, ks)                        \
   if (!done && a.lay.K == k && KS == ks) {   \
