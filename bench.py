@@ -160,6 +160,31 @@ def measure_trunk(eng, R, steps, seed, min_bytes=300e6):
     return out
 
 
+def run_trunk_eager(eng, steps, seed):
+    """Config 3's trunk linears launched one by one (ne_exl3_lin_run, and q/k/v through ne_exl3_lin_run_multi), no
+    graphs: a kernel trace of this run gives each shape's kernel time at 1 and 16 rows."""
+    from ijah_amd import synth
+    lins = {}
+    for name, inp, o, K in TRUNK:
+        rng = np.random.default_rng(seed + inp + o + K)
+        lins[name] = eng.exl3_linear(*synth.linear(rng, inp, o, K))
+    out = {}
+    for R in (1, 16):
+        x = synth.bf16_values(np.random.default_rng(seed + R), R, 4096)
+        for name, inp, o, K in TRUNK:
+            xb, yb = eng.from_numpy(np.ascontiguousarray(x[:, :inp])), eng.alloc(R * o * 4)
+            for _ in range(steps):
+                lins[name].run_bufs(R, xb, yb)
+        q = [lins[n] for n in ("q", "k", "v")]
+        for _ in range(steps):
+            eng.lin_run_multi(q, [x[:, :2048]] * 3)
+        eng.sync()
+        out[f"R{R}"] = steps
+    for m in lins.values():
+        m.free()
+    return {"trunk_eager_runs": out}
+
+
 def run_probes(eng, iters=4000):
     """probe_mix (ijah_amd/csrc/probes.hip) on every CU at 1, 2, 4 and 8 waves per SIMD: mode 0 decode only, 1 MFMA
     only, 2 decode feeding each wave's MFMA chain, 3 even waves decode / odd waves MFMA (ms per launch). Decode: weights
@@ -248,6 +273,9 @@ def main():
                     help="run the layer chain eagerly --steps times and exit (for rocprofv3 --pmc passes)")
     ap.add_argument("--no-trunk", action="store_true", help="skip the trunk (config 3) lines")
     ap.add_argument("--trunk-only", action="store_true", help="only measure the trunk linears (config 3) and exit")
+    ap.add_argument("--trunk-eager", action="store_true",
+                    help="only run the trunk linears (config 3, 1 and 16 rows, q/k/v also as one launch) eagerly "
+                         "--steps times, no graphs (for rocprofv3 kernel traces), and exit")
     ap.add_argument("--hc-only", action="store_true", help="only measure the hyper-connection read and exit")
     ap.add_argument("--batch-rows", type=int, default=0, metavar="R",
                     help="only measure the grouped matrix-core layer at R rows (a 4-layer graph) and exit")
@@ -276,6 +304,9 @@ def main():
     if a.hc_only:
         print(json.dumps({"hc_read_m1": measure_hc_read(eng, 1, a.steps, a.seed + 5),
                           "hc_read_m16": measure_hc_read(eng, 16, a.steps, a.seed + 6)}), flush=True)
+        return
+    if a.trunk_eager:
+        print(json.dumps(run_trunk_eager(eng, a.steps, a.seed)), flush=True)
         return
     if a.trunk_only:
         print(json.dumps({"m1": measure_trunk(eng, 1, a.steps, a.seed), "m16": measure_trunk(eng, 16, a.steps, a.seed),

@@ -78,6 +78,8 @@ struct ne_exl3_lin {
   // the input preparation runs inside the GEMM (each tile pair's workgroups prepare their own k chunks) unless that
   // repeats too much work: many tile pairs times many rows take one prep launch instead (same results)
   bool prep_launch(int R) const { return (long)(OTp / 2) * R > 2048; }
+  // many tile pairs (a vocabulary head): one workgroup per pair loops over the k groups (same results)
+  bool k_loop(int R) const { return OTp / 2 >= 2048 && groups() <= 16 && R <= 4 && prep_launch(R); }
 };
 
 static ne_exl3_lin *lin_create(const uint16_t *trellis, const uint16_t *suh, const uint16_t *svh, int in, int out,
@@ -205,7 +207,8 @@ struct LinScratch {
 // LinArgs of one run at R rows (the k group partials grown to R rows as needed, or taken from sc)
 static LinArgs lin_args(ne_exl3_lin *l, int R, const float *x, float *y, const LinEpi &epi = LinEpi(),
                         const LinScratch *sc = nullptr) {
-  const int S = l->groups();
+  const bool kloop = l->one_launch && l->k_loop(R);
+  const int S = kloop ? 1 : l->groups();
   if (!sc && R > l->part_rows) {  // never while the stream is captured: a captured launch would keep the freed buffer
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     IJ_HIP(hipStreamIsCapturing(stream(), &cs));
@@ -238,6 +241,7 @@ static LinArgs lin_args(ne_exl3_lin *l, int R, const float *x, float *y, const L
   a.epi = epi;
   a.cnt = l->one_launch ? (sc ? sc->cnt : l->cnt) : nullptr;
   a.xh_in = (!l->one_launch || l->prep_launch(R)) ? 1 : 0;
+  a.kloop = kloop ? 1 : 0;
   return a;
 }
 
@@ -252,7 +256,7 @@ static void lin_launch_multi(ne_exl3_lin *const *l, int n, int R, const float *c
   int k = 0;
   for (int i = 0; i < n; i++) {
     const LinArgs ai = lin_args(l[i], R, x[i], y[i], epi ? epi[i] : LinEpi());
-    if (k > 0 && (k == group || ai.K != a[0].K || (bool)ai.cnt != (bool)a[0].cnt)) {
+    if (k > 0 && (k == group || ai.K != a[0].K || (bool)ai.cnt != (bool)a[0].cnt || ai.kloop != a[0].kloop)) {
       launch_lin_multi(a, k, s);
       k = 0;
     }

@@ -767,6 +767,104 @@ __global__ __launch_bounds__(256) void lin_mx(LinMulti m) {
                  &flag);
 }
 
+// lin_mxl: lin_mx for linears with many tile pairs (a vocabulary head), one workgroup per tile pair looping over the
+// k groups: wave c takes chunk c of every group, the next group's requests in flight while one decodes; the chunk sums
+// go to LDS, and at the end each (row, column) folds the chunks of each group left and the groups left - the order of
+// lin_mx, so the results are bit-identical - and stores one tagged total per pair (S = 1). The block finisher is the
+// block's last pair, as in lin_mx.
+template <int K, int RT>
+constexpr uint32_t lin_mxl_wave() { return kLinChunkKt * 64 * K + RT * 256; }
+template <int K, int RT>
+constexpr uint32_t lin_mxl_lds(int G) { return 8 * lin_mxl_wave<K, RT>() + (uint32_t)G * 4 * RT * 32 * 4; }
+constexpr int kLinLoopMaxGroups = 16;  // in <= 8192
+template <int K, int RT>
+__global__ __launch_bounds__(256) void lin_mxl(LinMulti m) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  int li = 0;
+#pragma unroll
+  for (int i = 1; i < kLinMulti; i++)
+    if (i < m.n && (int)blockIdx.x >= m.wg0[i]) li = i;
+  const LinArgs a = lin_pick(m, li);
+  const int NP = (a.OT + 1) / 2, OTp = 2 * NP, R = a.R, IT = a.IT, G = (IT + kLinGroupKt - 1) / kLinGroupKt;
+  const int p = (int)blockIdx.x - m.wg0[li];
+  const int lane = threadIdx.x & 63, c = (int)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  float *csum = (float *)(lds + 8 * lin_mxl_wave<K, RT>());  // [group][4 chunks][RT][32]
+  const int cb = p / 4;
+  uint32_t *epoch = a.cnt ? a.cnt + (uint64_t)cb * kSyncStride : nullptr;
+  uint32_t ep = 0;
+  if (epoch) ep = ld_cg(epoch);
+  const uint8_t *tiles = (const uint8_t *)a.tiles + (uint64_t)p * IT * 64 * K;
+  auto stage = [&](int g) {  // group g's requests into buffer g & 1 (the rows come from the prep launch)
+    const int kt0 = g * kLinGroupKt + c * kLinChunkKt, nkt = max(0, min(kLinChunkKt, IT - kt0));
+    uint8_t *tl = lds + (2 * c + (g & 1)) * lin_mxl_wave<K, RT>();
+    _Float16 *xs = (_Float16 *)(tl + kLinChunkKt * 64 * K);
+    int n = 0;
+    if (nkt > 0) {
+      const uint32_t bytes = (uint32_t)nkt * 64 * K;
+      for (uint32_t o = 0; o < bytes; o += 1024, n++)
+        if (o + (uint32_t)lane * 16 < bytes)
+          __builtin_amdgcn_global_load_lds((const void *)(tiles + (uint64_t)kt0 * 64 * K + o + lane * 16),
+                                           (__attribute__((address_space(3))) void *)(tl + o), 16, 0, 0);
+      for (int r = 0; r < R; r += 4, n++) {
+        const int rr = r + (lane >> 4), q = lane & 15;
+        if (rr < R && q * 16 < nkt * 32)
+          __builtin_amdgcn_global_load_lds((const void *)(a.xh + (uint64_t)rr * a.in + kt0 * 16 + q * 8),
+                                           (__attribute__((address_space(3))) void *)(xs + r * 128), 16, 0, 0);
+      }
+    }
+    return n;
+  };
+  stage(0);
+  for (int g = 0; g < G; g++) {
+    const int nnext = g + 1 < G ? stage(g + 1) : 0;
+    wait_vm(nnext);  // group g's requests are in (the next group's may not be)
+    const int kt0 = g * kLinGroupKt + c * kLinChunkKt, nkt = max(0, min(kLinChunkKt, IT - kt0));
+    const uint8_t *tl = lds + (2 * c + (g & 1)) * lin_mxl_wave<K, RT>();
+    const _Float16 *xa = (const _Float16 *)(tl + kLinChunkKt * 64 * K) + min(lane & 31, R - 1) * 128 + 8 * (lane >> 5);
+    f32x16 acc;
+#pragma unroll
+    for (int i = 0; i < 16; i++) acc[i] = 0.f;
+#pragma unroll
+    for (int kt = 0; kt < kLinChunkKt; kt++)
+      if (kt < nkt) {
+        const f16x8 bv = decode_pair<K>(tl, kt);
+        const f16x8 av = *(const f16x8 *)(xa + kt * 16);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bv, acc, 0, 0, 0);
+      }
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      const int r = 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+      if (r < RT && r < R) csum[((g * 4 + c) * RT + r) * 32 + (lane & 31)] = acc[i];
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this buffer's reads are done before it is refilled
+  }
+  __syncthreads();
+  const uint32_t tag = (uint32_t)__builtin_amdgcn_readfirstlane(ep) + 1u;
+  for (int e = threadIdx.x; e < R * 32; e += 256) {
+    float tot = 0.f;
+    for (int g = 0; g < G; g++) {
+      const int nc = (min(kLinGroupKt, IT - g * kLinGroupKt) + kLinChunkKt - 1) / kLinChunkKt;
+      float v = csum[(g * 4) * RT * 32 + e];
+      for (int cc = 1; cc < nc; cc++) v = v + csum[(g * 4 + cc) * RT * 32 + e];
+      tot = g == 0 ? v : tot + v;
+    }
+    const uint64_t o = (uint64_t)(e >> 5) * OTp * 16 + p * 32 + (e & 31);
+    if (epoch)
+      st_tag((uint64_t *)a.part + o, tot, tag);
+    else
+      a.part[o] = tot;
+  }
+  if (!epoch || p != min(4 * cb + 3, NP - 1)) return;
+  for (int r = c; r < R; r += 4) lin_finish_row(a, r, cb, tag);
+  __syncthreads();
+  if (threadIdx.x == 0) st_cg(epoch, tag);
+  if (a.epi.kind == 8) {
+    __shared__ int flag;
+    hc_fin_block(a, a.epi.ctr + (uint64_t)(cb % (a.epi.hid / 128)) * kSyncStride, a.epi.row0, a.epi.row0 + R, cb,
+                 &flag);
+  }
+}
+
 // lin_finish: the finisher of the staged path, grid R x ceil(out/128) (one workgroup per row and output block)
 __global__ __launch_bounds__(64) void lin_finish(LinArgs a) {
   __shared__ int flag;
@@ -948,6 +1046,38 @@ static const void *lin_mx_any(int K, int RT) {
   return f;
 }
 template <int K>
+static const void *lin_mxl_fn(int RT) {
+  switch (RT) {
+    case 1: return (const void *)&lin_mxl<K, 1>;
+    case 2: return (const void *)&lin_mxl<K, 2>;
+    case 4: return (const void *)&lin_mxl<K, 4>;
+    case 8: return (const void *)&lin_mxl<K, 8>;
+    case 16: return (const void *)&lin_mxl<K, 16>;
+    default: return (const void *)&lin_mxl<K, 32>;
+  }
+}
+static const void *lin_mxl_any(int K, int RT) {
+  const void *f = nullptr;
+  IJ_DISPATCH_K(K, f = lin_mxl_fn<KK>(RT));
+  return f;
+}
+template <int K>
+static size_t lin_mxl_lds_fn(int RT, int G) {
+  switch (RT) {
+    case 1: return lin_mxl_lds<K, 1>(G);
+    case 2: return lin_mxl_lds<K, 2>(G);
+    case 4: return lin_mxl_lds<K, 4>(G);
+    case 8: return lin_mxl_lds<K, 8>(G);
+    case 16: return lin_mxl_lds<K, 16>(G);
+    default: return lin_mxl_lds<K, 32>(G);
+  }
+}
+static size_t lin_mxl_lds_any(int K, int RT, int G) {
+  size_t n = 0;
+  IJ_DISPATCH_K(K, n = lin_mxl_lds_fn<KK>(RT, G));
+  return n;
+}
+template <int K>
 static size_t lin_mx_lds_fn(int RT) {
   switch (RT) {
     case 1: return lin_mx_lds<K, 1>();
@@ -972,19 +1102,28 @@ void launch_lin_multi(const LinArgs *l, int n, hipStream_t s) {
   for (int i = 0; i < n; i++) {
     const LinArgs &a = l[i];
     // every buffer a (possibly captured) launch uses is present, and the k groups fixed by the shape
-    IJ_CHECK(a.tiles && a.suh && a.svh && a.x && a.y && a.xh && a.part && a.S == (a.IT + kLinGroupKt - 1) / kLinGroupKt,
+    const int G = (a.IT + kLinGroupKt - 1) / kLinGroupKt;
+    IJ_CHECK(a.tiles && a.suh && a.svh && a.x && a.y && a.xh && a.part && a.S == (a.kloop ? 1 : G),
              "linear launch: missing buffer or bad k groups (S %d of %d k tiles)", a.S, a.IT);
-    IJ_CHECK(a.K == l[0].K && a.R == l[0].R && a.R >= 1 && a.R <= kLinMaxRows && (bool)a.cnt == (bool)l[0].cnt,
+    IJ_CHECK(!a.kloop || (a.xh_in && G <= kLinLoopMaxGroups), "linear launch: the k-group loop needs the prep launch");
+    IJ_CHECK(a.K == l[0].K && a.R == l[0].R && a.R >= 1 && a.R <= kLinMaxRows && (bool)a.cnt == (bool)l[0].cnt &&
+                 a.kloop == l[0].kloop,
              "multi-linear launch: K, R and path must agree");
     if (a.xh_in) hipLaunchKernelGGL(lin_prep, dim3(a.R * ((a.in + 127) / 128)), dim3(64), 0, s, a);
     m.l[i] = a;
     m.wg0[i] = wg;
-    wg += ((a.OT + 1) / 2) * a.S;
+    wg += ((a.OT + 1) / 2) * (a.kloop ? 1 : a.S);
   }
   m.wg0[n] = wg;
   const int RT = rows_tier(l[0].R);
   void *args[] = {&m};
-  IJ_HIP(hipLaunchKernel(lin_mx_any(l[0].K, RT), dim3(wg), dim3(256), args, lin_mx_lds_any(l[0].K, RT), s));
+  if (l[0].kloop) {
+    int G = 0;
+    for (int i = 0; i < n; i++) G = std::max(G, (l[i].IT + kLinGroupKt - 1) / kLinGroupKt);
+    IJ_HIP(hipLaunchKernel(lin_mxl_any(l[0].K, RT), dim3(wg), dim3(256), args, lin_mxl_lds_any(l[0].K, RT, G), s));
+  } else {
+    IJ_HIP(hipLaunchKernel(lin_mx_any(l[0].K, RT), dim3(wg), dim3(256), args, lin_mx_lds_any(l[0].K, RT), s));
+  }
   if (!l[0].cnt)  // staged path: the finisher as its own launch
     for (int i = 0; i < n; i++)
       hipLaunchKernelGGL(lin_finish, dim3(l[i].R * ((l[i].out + 127) / 128)), dim3(64), 0, s, l[i]);
@@ -997,6 +1136,10 @@ void init_lin_attrs() {
     for (int RT : {1, 2, 4, 8, 16, 32})
       IJ_HIP(hipFuncSetAttribute(lin_mx_any(K, RT), hipFuncAttributeMaxDynamicSharedMemorySize,
                                  (int)lin_mx_lds_any(K, RT)));
+  for (int K = 2; K <= 8; K++)
+    for (int RT : {1, 2, 4, 8, 16, 32})
+      IJ_HIP(hipFuncSetAttribute(lin_mxl_any(K, RT), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                 (int)std::min<size_t>(160 * 1024 - 256, lin_mxl_lds_any(K, RT, kLinLoopMaxGroups))));
 }
 
 static const void *decode_fn(int K) {

@@ -155,6 +155,7 @@ struct LinArgs {
   uint32_t *cnt;          // per 128-column output block, kSyncStride apart: the block's epoch (the tag of its last
                           // launch; zero at creation); null: the staged three-kernel path (prep, GEMM, finish)
   int xh_in;              // 1: xh holds this run's prepared rows (a prep launch ran); 0: the GEMM prepares its chunks
+  int kloop;              // 1: one workgroup per tile pair loops over the k groups (S = 1: one total per pair)
   LinEpi epi;
 };
 constexpr int kLinMaxRows = 32;
