@@ -197,7 +197,46 @@ using namespace ijah;
 ne_buf::~ne_buf() {
   if (dev && !external) (void)hipFree(dev);
   free(host);
+  free(snap);
 }
+
+namespace ijah {
+void mirror_push(const ne_buf *cb) {
+  ne_buf *b = const_cast<ne_buf *>(cb);
+  if (!b || !b->host || !b->snap || b->readonly || !b->size) return;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(stream(), &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return;
+  const uint8_t *h = (const uint8_t *)b->host;
+  uint8_t *sn = (uint8_t *)b->snap;
+  const uint64_t n = b->size;
+  bool synced = false;
+  uint64_t i = 0;
+  while (i < n) {
+    // next changed byte (8 bytes at a time), then the end of the run of changed 8-byte words
+    while (i + 8 <= n && memcmp(h + i, sn + i, 8) == 0) i += 8;
+    while (i < n && h[i] == sn[i]) i++;
+    if (i >= n) break;
+    uint64_t e = i + 1;
+    while (e < n) {
+      const uint64_t w = std::min<uint64_t>(8, n - e);
+      if (memcmp(h + e, sn + e, w) == 0) break;
+      e += w;
+    }
+    while (e > i + 1 && h[e - 1] == sn[e - 1]) e--;  // trim unchanged bytes at the end of the run
+    if (!synced) {
+      IJ_HIP(hipStreamSynchronize(stream()));
+      synced = true;
+    }
+    IJ_HIP(hipMemcpy((uint8_t *)b->dev + i, h + i, e - i, hipMemcpyHostToDevice));
+    memcpy(sn + i, h + i, e - i);
+    i = e;
+  }
+}
+void *ne_dev(const ne_buf *b) {
+  mirror_push(b);
+  return b ? b->dev : nullptr;
+}
+}  // namespace ijah
 
 static ne_buf *new_device_buf(uint64_t n) {
   ensure_device();
@@ -251,11 +290,14 @@ NE_API void *ne_buf_contents(const ne_buf *b) {
   c_call([&] {
     IJ_CHECK(b, "null buffer");
     ne_buf *m = const_cast<ne_buf *>(b);
+    mirror_push(m);  // writes made through an earlier pointer reach the device first
     if (!m->host) m->host = calloc(1, m->size ? m->size : 1);
-    IJ_CHECK(m->host, "host mirror allocation failed");
+    if (!m->snap) m->snap = calloc(1, m->size ? m->size : 1);
+    IJ_CHECK(m->host && m->snap, "host mirror allocation failed");
     if (m->size) {
       IJ_HIP(hipStreamSynchronize(stream()));
       IJ_HIP(hipMemcpy(m->host, m->dev, m->size, hipMemcpyDeviceToHost));
+      memcpy(m->snap, m->host, m->size);
     }
     r = m->host;
   });
@@ -268,6 +310,7 @@ NE_API int ne_upload(ne_buf *b, uint64_t offset, const void *src, uint64_t n) {
     IJ_CHECK(!b->readonly, "upload into a pack tensor (read-only)");
     IJ_CHECK(src || n == 0, "null source");
     if (!n) return;
+    mirror_push(b);
     IJ_HIP(hipStreamSynchronize(stream()));
     IJ_HIP(hipMemcpy((char *)b->dev + offset, src, n, hipMemcpyHostToDevice));
   });
@@ -277,6 +320,7 @@ NE_API int ne_download(const ne_buf *b, uint64_t offset, void *dst, uint64_t n) 
     IJ_CHECK(b && offset <= b->size && n <= b->size - offset, "download out of range");
     IJ_CHECK(dst || n == 0, "null destination");
     if (!n) return;
+    mirror_push(b);
     IJ_HIP(hipStreamSynchronize(stream()));
     IJ_HIP(hipMemcpy(dst, (const char *)b->dev + offset, n, hipMemcpyDeviceToHost));
   });
@@ -288,6 +332,7 @@ NE_API int ne_buf_flush(ne_buf *b) {
     if (!b->host || !b->size) return;
     IJ_HIP(hipStreamSynchronize(stream()));
     IJ_HIP(hipMemcpy(b->dev, b->host, b->size, hipMemcpyHostToDevice));
+    if (b->snap) memcpy(b->snap, b->host, b->size);
   });
 }
 NE_API int ne_sync(void) {
@@ -395,6 +440,7 @@ NE_API int ne_run_kernel(const char *fn, const ne_fconst *fc, int nfc, const ne_
         addr[i] = const_cast<void *>(args[i].bytes);
       } else {
         IJ_CHECK(args[i].buf && args[i].buf->dev, "argument %d: null buffer", i);
+        mirror_push(args[i].buf);
         IJ_CHECK(k->arg_sizes[i] == sizeof(void *), "%s: argument %d must be inline bytes", fn, i);
         IJ_CHECK(args[i].offset <= args[i].buf->size, "argument %d: offset beyond buffer", i);
         ptrs[i] = (char *)args[i].buf->dev + args[i].offset;

@@ -52,14 +52,23 @@ hipStream_t stream();
 void ensure_device();
 bool device_available();  // a HIP device is visible (no throw)
 
+// the caller's pending mirror writes of b pushed to the device (not while the library stream is captured), then
+// b's device address
+void mirror_push(const struct ::ne_buf *b);
+void *ne_dev(const struct ::ne_buf *b);
+
 }  // namespace ijah
 
 // Device memory handle. The reference's buffers are unified memory; here the bytes live in HBM and `host` is a lazily
-// allocated mirror that ne_buf_contents() refreshes (device -> host) and ne_buf_flush() writes back.
+// allocated mirror that ne_buf_contents() refreshes (device -> host). `snap` holds what the mirror last received from
+// the device: before any library call uses the buffer, the bytes the caller changed in the mirror since then (and
+// only those) go to the device (ne_dev), so the reference's write-through-numpy-then-run pattern works, and an
+// untouched mirror never overwrites newer device data.
 struct ne_buf {
   void *dev = nullptr;
   uint64_t size = 0;
   void *host = nullptr;
+  void *snap = nullptr;
   bool owned = true;     // ne_free releases the memory
   bool readonly = false; // pack-owned tensor copies refuse ne_upload (reference core/capi.mm:65)
   bool external = false; // dev memory not owned by this handle (a view)

@@ -291,8 +291,8 @@ NE_API int ne_exl3_lin_run(ne_exl3_lin *l, int R, const ne_buf *x, uint64_t x_of
     IJ_CHECK(x_off % 4 == 0 && y_off % 4 == 0, "offsets must be 4-byte aligned");
     IJ_CHECK(x_off + (uint64_t)R * l->in * 4 <= x->size, "x buffer too small for [%d][%d] f32", R, l->in);
     IJ_CHECK(y_off + (uint64_t)R * l->out * 4 <= y->size, "y buffer too small for [%d][%d] f32", R, l->out);
-    const float *xp = (const float *)((const char *)x->dev + x_off);
-    float *yp = (float *)((char *)y->dev + y_off);
+    const float *xp = (const float *)((const char *)ne_dev(x) + x_off);
+    float *yp = (float *)((char *)ne_dev(y) + y_off);
     timed(stream(), gpu_ms, [&] { lin_launch(l, R, xp, yp, stream()); });
   });
 }
@@ -317,7 +317,7 @@ NE_API int ne_exl3_lin_run_noalloc(ne_exl3_lin *l, int R, const ne_buf *x, uint6
     // or another linear, carries a tag of this call)
     launch_zero_u32(sc.cnt, (size_t)((l->out + 127) / 128) * kSyncStride, s);
     launch_zero_u32((uint32_t *)sc.part, lin_part_bytes(l, R) / 4, s);
-    lin_launch(l, R, (const float *)((const char *)x->dev + x_off), (float *)((char *)y->dev + y_off), s, LinEpi(),
+    lin_launch(l, R, (const float *)((const char *)ne_dev(x) + x_off), (float *)((char *)ne_dev(y) + y_off), s, LinEpi(),
                &sc);
     IJ_HIP(hipGetLastError());
   });
@@ -344,7 +344,7 @@ NE_API int ne_exl3_lin_run_epi(ne_exl3_lin *l, int R, const ne_buf *x, uint64_t 
     auto need = [&](const ne_buf *b, uint64_t bytes, const char *name) -> float * {
       IJ_CHECK(b && b->size >= bytes, "epilogue %d: %s missing or under %llu bytes", k, name,
                (unsigned long long)bytes);
-      return (float *)b->dev;
+      return (float *)ne_dev(b);
     };
     if (k == 1) {
       IJ_CHECK(epi->hc >= 1 && epi->hc <= 8, "epilogue 1: hc %d (1..8)", epi->hc);
@@ -362,8 +362,8 @@ NE_API int ne_exl3_lin_run_epi(ne_exl3_lin *l, int R, const ne_buf *x, uint64_t 
       e.e1 = need(epi->e1, 4, "e1 (position)");
       e.cap = (int)std::min<uint64_t>(epi->e0->size / 512, 1u << 30);
     }
-    const float *xp = (const float *)((const char *)x->dev + x_off);
-    float *yp = (float *)((char *)y->dev + y_off);
+    const float *xp = (const float *)((const char *)ne_dev(x) + x_off);
+    float *yp = (float *)((char *)ne_dev(y) + y_off);
     timed(stream(), gpu_ms, [&] { lin_launch(l, R, xp, yp, stream(), e); });
   });
 }
@@ -395,9 +395,9 @@ NE_API int ne_hc_read(ne_exl3_lin *down, ne_exl3_lin *up, int R, const ne_buf *h
     }
     float *xn = up->hc_scr, *u = xn + (size_t)kLinMaxRows * hcd, *ip = u + (size_t)kLinMaxRows * hcd;
     uint32_t *ctr = (uint32_t *)(up->hc_scr + (size_t)kLinMaxRows * (2 * (size_t)hcd + 16 * (size_t)((hid + 255) / 256)));
-    const float *hp = (const float *)h->dev;
-    const uint16_t *nw = (const uint16_t *)hc_norm->dev;
-    float *injp = (float *)inj->dev;
+    const float *hp = (const float *)ne_dev(h);
+    const uint16_t *nw = (const uint16_t *)ne_dev(hc_norm);
+    float *injp = (float *)ne_dev(inj);
     LinEpi act;  // the down linear's epilogue: mix = rr(silu(rr(v) / 4))
     act.kind = 2;
     act.refr = refr ? 1 : 0;
@@ -407,16 +407,16 @@ NE_API int ne_hc_read(ne_exl3_lin *down, ne_exl3_lin *up, int R, const ne_buf *h
     fin.hid = hid;
     fin.e0 = u;
     fin.e1 = const_cast<float *>(hp);
-    fin.e2 = (float *)out->dev;
+    fin.e2 = (float *)ne_dev(out);
     fin.e3 = ip;
     fin.e4 = injp;
     fin.w16 = nw;
     fin.ctr = ctr;
     timed(stream(), gpu_ms, [&] {
       hipStream_t s = stream();
-      launch_hc_prep(hp, nw, (const uint16_t *)inject->dev, xn, ip, injp, R, hid, s);
-      lin_launch(down, R, xn, (float *)mix->dev, s, act);
-      lin_launch(up, R, (const float *)mix->dev, u, s, fin);
+      launch_hc_prep(hp, nw, (const uint16_t *)ne_dev(inject), xn, ip, injp, R, hid, s);
+      lin_launch(down, R, xn, (float *)ne_dev(mix), s, act);
+      lin_launch(up, R, (const float *)ne_dev(mix), u, s, fin);
     });
   });
 }
@@ -445,7 +445,7 @@ static double lin_time(ne_exl3_lin *const *lins, int n, int R, const ne_buf *x, 
   double ms = 0;
   try {
     for (int i = 0; i < n; i++) lin_args(lins[i], R, nullptr, nullptr);  // grow the partials before capture
-    std::vector<const float *> xp(n, (const float *)x->dev);
+    std::vector<const float *> xp(n, (const float *)ne_dev(x));
     std::vector<float *> yp(n);
     for (int i = 0, yo = 0; i < n; yo += R * lins[i]->out, i++) yp[i] = ys + yo;
     ge = capture_graph(s, g, [&] {
@@ -499,8 +499,8 @@ NE_API int ne_exl3_lin_run_multi(ne_exl3_lin *const *lins, int n, int R, const n
                lins[i]->in);
       IJ_CHECK(y_off[i] + (uint64_t)R * lins[i]->out * 4 <= y[i]->size, "y %d too small for [%d][%d] f32", i, R,
                lins[i]->out);
-      xp[i] = (const float *)((const char *)x[i]->dev + x_off[i]);
-      yp[i] = (float *)((char *)y[i]->dev + y_off[i]);
+      xp[i] = (const float *)((const char *)ne_dev(x[i]) + x_off[i]);
+      yp[i] = (float *)((char *)ne_dev(y[i]) + y_off[i]);
     }
     timed(stream(), gpu_ms, [&] { lin_launch_multi(lins, n, R, xp.data(), yp.data(), nullptr, stream()); });
   });
@@ -510,7 +510,7 @@ NE_API int ne_exl3_lin_decode(ne_exl3_lin *l, ne_buf *w, double *gpu_ms) {
   return c_call([&] {
     IJ_CHECK(l && w, "null argument");
     IJ_CHECK(w->size >= (uint64_t)l->in * l->out * 2, "w buffer too small for [%d][%d] fp16", l->in, l->out);
-    timed(stream(), gpu_ms, [&] { launch_decode(l->tiles, l->IT, l->OT, l->K, (uint16_t *)w->dev, stream()); });
+    timed(stream(), gpu_ms, [&] { launch_decode(l->tiles, l->IT, l->OT, l->K, (uint16_t *)ne_dev(w), stream()); });
   });
 }
 
@@ -936,8 +936,8 @@ NE_API int ne_moe_run(ne_moe *m, int R, const ne_buf *x, uint64_t x_off, ne_buf 
     IJ_CHECK(x_off + (uint64_t)R * m->hid * 4 <= x->size, "x buffer too small for [%d][%d] f32", R, m->hid);
     IJ_CHECK(y_off + (uint64_t)R * m->hid * 4 <= y->size, "y buffer too small for [%d][%d] f32", R, m->hid);
     m->ensure_scratch(R);
-    const float *xp = (const float *)((const char *)x->dev + x_off);
-    float *yp = (float *)((char *)y->dev + y_off);
+    const float *xp = (const float *)((const char *)ne_dev(x) + x_off);
+    float *yp = (float *)((char *)ne_dev(y) + y_off);
     timed(stream(), gpu_ms, [&] { m->launch(R, xp, yp, stream()); });
     m->last_R = R;
     m->last_y = yp;
@@ -962,11 +962,11 @@ NE_API int ne_moe_run_hc(ne_moe *m, int R, const ne_buf *x, uint64_t x_off, ne_b
     MoeArgs f;
     f.hc = hc->hc;
     f.refr = hc->refr ? 1 : 0;
-    f.hc_h = (const float *)hc->h->dev;
-    f.hc_inj = (const float *)hc->inj->dev;
-    f.hc_out = (float *)hc->hout->dev;
-    const float *xp = (const float *)((const char *)x->dev + x_off);
-    float *yp = (float *)((char *)y->dev + y_off);
+    f.hc_h = (const float *)ne_dev(hc->h);
+    f.hc_inj = (const float *)ne_dev(hc->inj);
+    f.hc_out = (float *)ne_dev(hc->hout);
+    const float *xp = (const float *)((const char *)ne_dev(x) + x_off);
+    float *yp = (float *)((char *)ne_dev(y) + y_off);
     timed(stream(), gpu_ms, [&] { m->launch(R, xp, yp, stream(), &f); });
     m->last_R = R;
     m->last_y = yp;
@@ -1036,7 +1036,7 @@ NE_API int ne_moe_decode(ne_moe *m, int e, int proj, ne_buf *w, double *gpu_ms) 
     const int in = proj == 2 ? m->inter : m->hid, out = proj == 2 ? m->hid : m->inter;
     IJ_CHECK(w->size >= (uint64_t)in * out * 2, "w buffer too small");
     timed(stream(), gpu_ms, [&] {
-      launch_decode((const uint32_t *)(blk + L.tr[proj]), in / 16, out / 16, L.K, (uint16_t *)w->dev, stream());
+      launch_decode((const uint32_t *)(blk + L.tr[proj]), in / 16, out / 16, L.K, (uint16_t *)ne_dev(w), stream());
     });
   });
 }
@@ -1075,7 +1075,7 @@ NE_API int ne_moe_time(ne_moe *const *layers, int n, int R, const ne_buf *x, int
     IJ_CHECK((uint64_t)R * hid * 4 <= x->size, "x buffer too small");
     hipStream_t s = stream();
     float *ys = dev_alloc<float>((size_t)n * R * hid);
-    const float *xp = (const float *)x->dev;
+    const float *xp = (const float *)ne_dev(x);
     hipGraph_t g = nullptr;
     hipGraphExec_t ge = nullptr;
     auto cleanup = [&] {
@@ -1115,7 +1115,7 @@ NE_API int ne_moe_time_kernels(ne_moe *const *layers, int n, int R, const ne_buf
     IJ_CHECK((uint64_t)R * hid * 4 <= x->size, "x buffer too small");
     hipStream_t s = stream();
     float *ys = dev_alloc<float>((size_t)n * R * hid);
-    const float *xp = (const float *)x->dev;
+    const float *xp = (const float *)ne_dev(x);
     std::vector<MoeArgs> a;
     for (int i = 0; i < n; i++) {
       layers[i]->ensure_scratch(R);

@@ -161,7 +161,8 @@ class Buf:
         return out.reshape(shape) if shape is not None else out
 
     def numpy(self, dtype=np.float32, shape=None, offset=0):
-        """Host mirror refreshed from the device now (a copy on a discrete GPU; write back with flush())."""
+        """Host mirror refreshed from the device now (a copy on a discrete GPU). Bytes changed through it reach the
+        device before the next library call that uses this buffer; flush() pushes the whole mirror."""
         dtype = np.dtype(dtype)
         n = (self.size - offset) // dtype.itemsize if shape is None else int(np.prod(shape))
         addr = self.contents()

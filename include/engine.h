@@ -7,7 +7,11 @@
  * Conventions (reference include/engine.h:3-12)
  * - int functions: 0 = ok, -1 = error, message in ne_last_error() (per thread). Pointer functions: NULL = error.
  * - Buffers live in HBM. ne_buf_contents() returns a host mirror refreshed from the device at that call (the
- *   reference's unified memory has no copy); writes to the mirror reach the GPU with ne_buf_flush() (ijah_exl3.h).
+ *   reference's unified memory has no copy). Bytes the caller changes in the mirror reach the GPU before the next
+ *   library call that uses the buffer (a kernel or hot-path run, an upload, a download, ne_buf_contents itself),
+ *   and only the changed bytes, so the reference's write-then-run pattern works; ne_buf_flush() (ijah_exl3.h)
+ *   writes the whole mirror at once. A caller that reads results must call ne_buf_contents() again after the run
+ *   (the GPU's writes do not reach an existing mirror), and must not change bytes the GPU is still writing.
  * - Pack tensors are uploaded to HBM on first use; their ne_buf handles belong to the pack (do not ne_free them).
  */
 #ifndef NATIVE_ENGINE_H

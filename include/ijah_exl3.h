@@ -15,8 +15,9 @@ extern "C" {
 #endif
 
 /* ---- buffers on a discrete GPU ---- */
-/* Writes the host mirror returned by ne_buf_contents back to the device. No reference counterpart: the reference's
- * buffers are unified memory (reference include/engine.h:6-7), where this is a no-op. */
+/* Writes the whole host mirror returned by ne_buf_contents back to the device now (changed bytes also go on their
+ * own before the next library call that uses the buffer). No reference counterpart: the reference's buffers are
+ * unified memory (reference include/engine.h:6-7), where this is a no-op. */
 NE_API int ne_buf_flush(ne_buf *b);
 /* Waits for all queued GPU work of the library (the reference's Recorder::wait, core/recorder.h:76). */
 NE_API int ne_sync(void);
