@@ -188,6 +188,35 @@ def run_trunk_eager(eng, steps, seed):
     return {"trunk_eager_runs": out}
 
 
+def run_stream_probe(eng, total_mb=24, region_mb=2048):
+    """probe_stream: 256 workgroups x 16 waves (the fused step's shape) stream total_mb of cold data (a different
+    slice of a region_mb buffer each launch, beyond the 256 MB last-level cache), per wave total_mb / 4096, into LDS
+    (mode 0) or registers (mode 1); and the same bytes over 1024 x 4 waves. us per launch (median of 8)."""
+    region = eng.alloc(region_mb << 20)
+    res = eng.alloc(4096 * 64 * 4)
+    out = {}
+    nb = total_mb << 20
+    for shape in ((256, 1024), (512, 512), (1024, 256)):
+        waves = shape[0] * shape[1] // 64
+        per = nb // waves // 1024 * 1024
+        for mode in (0, 1):
+            ts, off = [], 0
+            for i in range(10):
+                if off + nb > (region_mb << 20):
+                    off = 0
+                t = eng.run_kernel("probe_stream", [(region, off), np.uint32(per), np.int32(mode), res],
+                                   (shape[0], 1, 1), (shape[1], 1, 1), tg_mem=(shape[1] // 64) * 4096)
+                off += nb
+                if i >= 2:
+                    ts.append(t)
+            us = 1e3 * float(np.median(ts))
+            out[f"wg{shape[0]}x{shape[1] // 64}_{'lds' if mode == 0 else 'vgpr'}"] = {
+                "us": round(us, 2), "TBps": round(waves * per / (us * 1e-6) / 1e12, 2), "KB_per_wave": per // 1024}
+    region.free()
+    res.free()
+    return out
+
+
 def run_probes(eng, iters=4000):
     """probe_mix (ijah_amd/csrc/probes.hip) on every CU at 1, 2, 4 and 8 waves per SIMD: mode 0 decode only, 1 MFMA
     only, 2 decode feeding each wave's MFMA chain, 3 even waves decode / odd waves MFMA (ms per launch). Decode: weights
@@ -302,7 +331,8 @@ def main():
         print(json.dumps({"copy_probe_bytes": n, "launches": 5}), flush=True)
         return
     if a.probe:
-        print(json.dumps(run_probes(eng)), flush=True)
+        print(json.dumps({"stream": run_stream_probe(eng), "stream96": run_stream_probe(eng, 96), **run_probes(eng)}),
+              flush=True)
         return
     if a.hc_only:
         print(json.dumps({"hc_read_m1": measure_hc_read(eng, 1, a.steps, a.seed + 5),

@@ -214,9 +214,7 @@ static LinArgs lin_args(ne_exl3_lin *l, int R, const float *x, float *y, const L
     IJ_HIP(hipStreamIsCapturing(stream(), &cs));
     IJ_CHECK(cs == hipStreamCaptureStatusNone, "linear: partial scratch must grow before a stream capture");
     dev_free(l->part);
-    const size_t n = (size_t)S * R * l->OTp * 16 * 2;  // u64 tagged partials on the one-launch path
-    l->part = dev_alloc<float>(n);
-    IJ_HIP(hipMemset(l->part, 0, n * 4));  // tag 0: no launch's (tags start at 1)
+    l->part = dev_alloc<float>((size_t)S * R * l->OTp * 16);
     l->part_rows = R;
   }
   LinArgs a;
@@ -265,7 +263,7 @@ static void lin_launch_multi(ne_exl3_lin *const *l, int n, int R, const float *c
   if (k) launch_lin_multi(a, k, s);
 }
 
-static size_t lin_part_bytes(const ne_exl3_lin *l, int R) { return (size_t)l->groups() * R * l->OTp * 16 * 8; }
+static size_t lin_part_bytes(const ne_exl3_lin *l, int R) { return (size_t)l->groups() * R * l->OTp * 16 * 4; }
 // Scratch bytes of one run at R rows from the caller-provided scratch: counters, prepared input, partials, each part
 // on a 256-byte boundary
 static size_t lin_scratch_layout(const ne_exl3_lin *l, int R, LinScratch *sc, uint8_t *base) {
@@ -313,10 +311,8 @@ NE_API int ne_exl3_lin_run_noalloc(ne_exl3_lin *l, int R, const ne_buf *x, uint6
     LinScratch sc;
     lin_scratch_layout(l, R, &sc, noalloc_scratch());
     const hipStream_t s = stream();
-    // the block epochs and the tagged partials start at zero (tags restart at 1: no earlier call's partial, of this
-    // or another linear, carries a tag of this call)
+    // the block counters start at zero (the previous call on this GPU left them so unless it failed)
     launch_zero_u32(sc.cnt, (size_t)((l->out + 127) / 128) * kSyncStride, s);
-    launch_zero_u32((uint32_t *)sc.part, lin_part_bytes(l, R) / 4, s);
     lin_launch(l, R, (const float *)((const char *)ne_dev(x) + x_off), (float *)((char *)ne_dev(y) + y_off), s, LinEpi(),
                &sc);
     IJ_HIP(hipGetLastError());
@@ -517,10 +513,9 @@ NE_API int ne_exl3_lin_decode(ne_exl3_lin *l, ne_buf *w, double *gpu_ms) {
 }  // extern "C"
 
 // ---------------------------------------------------------------------------------------------------- MoE layer
-// The few-row MoE kernels' tagged partials and epochs, one pool per layer shape shared by every layer of that shape
-// (the layers run one after another on the library's stream). Its layout is fixed by the shape and the chunk index,
-// so a stale partial never sits where a launch of another layer expects one with the same tag; it only grows (new
-// memory zeroed: tag 0 is never a launch's), never while a stream is captured.
+// The few-row MoE kernels' partials and block counters, one pool per layer shape shared by every layer of that shape
+// (the layers run one after another on the library's stream; the counters are back at zero after each launch). It
+// only grows (counters zeroed), never while a stream is captured.
 static void few_pool(int hid, int inter, int chunks, uint64_t **part, uint32_t **ep) {
   struct Pool {
     uint64_t *part = nullptr;

@@ -585,11 +585,9 @@ __global__ __launch_bounds__(64) void lin_prep(LinArgs a) {
 }
 
 // The finished outputs of 128-column block cb for row r: the k group partials folded left in k order, H_out, svh, the
-// epilogue (reference kernels/trunk6/trunk6.metal:199-214, t6_finish). tag != 0: the partials are tagged values of
-// this launch (other workgroups are still storing them: polled until every one carries the tag; a bounded wait);
-// tag == 0: plain floats from an earlier launch.
-constexpr uint32_t kLinSpin = 1u << 20;
-__device__ void lin_finish_row(const LinArgs &a, int r, int cb, uint32_t tag) {
+// epilogue (reference kernels/trunk6/trunk6.metal:199-214, t6_finish). coherent: the partials were stored by other
+// workgroups of this launch (device-coherent loads); else by an earlier launch.
+__device__ void lin_finish_row(const LinArgs &a, int r, int cb, bool coherent) {
   const int lane = threadIdx.x & 63, OTp = a.OT + (a.OT & 1);
   const int i0 = cb * 128 + lane, i1 = i0 + 64;
   const bool m0 = i0 < a.out, m1 = i1 < a.out;
@@ -598,19 +596,12 @@ __device__ void lin_finish_row(const LinArgs &a, int r, int cb, uint32_t tag) {
   constexpr int B = 8;  // groups requested together (one round trip per 8)
   for (int g0 = 0; g0 < a.S; g0 += B) {
     float t0[B], t1[B];
-    if (tag) {
-      const uint64_t *pt = (const uint64_t *)a.part;
-      for (uint32_t it = 0; it < kLinSpin; it++) {
-        bool all = true;
+    if (coherent) {
 #pragma unroll
-        for (int j = 0; j < B; j++) {
-          const uint64_t *pp = pt + ((uint64_t)min(g0 + j, a.S - 1) * a.R + r) * OTp * 16;
-          const uint64_t u0 = ld_cg(pp + j0), u1 = ld_cg(pp + j1);
-          all = all && tag_ok(u0, tag) && tag_ok(u1, tag);
-          t0[j] = tag_val(u0);
-          t1[j] = tag_val(u1);
-        }
-        if (__all(all)) break;
+      for (int j = 0; j < B; j++) {
+        const float *pp = a.part + ((uint64_t)min(g0 + j, a.S - 1) * a.R + r) * OTp * 16;
+        t0[j] = ld_cg(pp + j0);
+        t1[j] = ld_cg(pp + j1);
       }
     } else {
 #pragma unroll
@@ -642,11 +633,9 @@ __device__ void lin_finish_row(const LinArgs &a, int r, int cb, uint32_t tag) {
 //      tiles), or (xh_in) requests the rows a prep launch wrote;
 //   2. decodes the tiles straight into the B operand of v_mfma_f32_32x32x16_f16 (A: the input rows; a row beyond R
 //      repeats row R - 1, its products unused) in one chain from zero;
-// then the chunk sums of the 4 waves are folded left in LDS and stored as the group's partials: tagged with the
-// launch's tag (one launch: the block's epoch word + 1, read at the start), where the block's finisher polls them.
-// The finisher of a 128-column output block is its producer with the highest workgroup index (the last group's last
-// pair): workgroups are dispatched in index order (per XCD), so every producer it waits for has been dispatched and
-// waits for nothing. It then advances the block's epoch. (Staged path: plain floats, finished by lin_finish.)
+// then the chunk sums of the 4 waves are folded left in LDS and stored as the group's partials (device-coherent
+// stores); the last workgroup to store into a 128-column output block (a counter per block, which it resets to 0)
+// finishes the block's rows. (Staged path: no counter; lin_finish finishes.)
 // Every row's arithmetic is the same at any R: a row of a batch is bit-identical to that row run alone.
 struct LinMulti {
   int n;
@@ -680,9 +669,6 @@ __global__ __launch_bounds__(256) void lin_mx(LinMulti m) {
   float *csum = (float *)(lds + 4 * lin_wave_lds<K, RT>());  // [4 chunks][RT rows][32 columns]
   const int e0 = kt0 * 16, i0 = e0 + lane, i1 = i0 + 64;    // the chunk's elements of this lane
   const int cb = p / 4;
-  uint32_t *epoch = a.cnt ? a.cnt + (uint64_t)cb * kSyncStride : nullptr;
-  uint32_t ep = 0;
-  if (epoch) ep = ld_cg(epoch);  // requested first: in by the time the partials go out
   // 1. input rows and tiles
   float xv0[RT], xv1[RT], s0 = 0.f, s1 = 0.f;
   if (!a.xh_in && nkt > 0) {
@@ -746,22 +732,19 @@ __global__ __launch_bounds__(256) void lin_mx(LinMulti m) {
   }
   __syncthreads();
   const int nc = (min(kLinGroupKt, a.IT - g * kLinGroupKt) + kLinChunkKt - 1) / kLinChunkKt;
-  const uint32_t tag = (uint32_t)__builtin_amdgcn_readfirstlane(ep) + 1u;
   for (int e = threadIdx.x; e < R * 32; e += 256) {
     const int r = e >> 5, n = e & 31;
     float v = csum[r * 32 + n];
     for (int cc = 1; cc < nc; cc++) v = v + csum[(cc * RT + r) * 32 + n];
-    const uint64_t o = ((uint64_t)g * R + r) * OTp * 16 + p * 32 + n;
-    if (epoch)
-      st_tag((uint64_t *)a.part + o, v, tag);
-    else
-      a.part[o] = v;
+    st_cg(a.part + ((uint64_t)g * R + r) * OTp * 16 + p * 32 + n, v);
   }
-  // 4. the block's finisher: its rows from the tagged partials, then the block's epoch
-  if (!epoch || g != a.S - 1 || p != min(4 * cb + 3, NP - 1)) return;
-  for (int r = c; r < R; r += 4) lin_finish_row(a, r, cb, tag);
-  __syncthreads();
-  if (threadIdx.x == 0) st_cg(epoch, tag);
+  if (!a.cnt) return;
+  // 4. the last workgroup of the 128-column output block finishes its rows
+  const int npb = min(4, NP - 4 * cb);
+  uint32_t *ctr = a.cnt + (uint64_t)cb * kSyncStride;
+  if (block_signal(ctr, &flag) != (uint32_t)(npb * a.S - 1)) return;
+  if (threadIdx.x == 0) st_cg(ctr, 0u);
+  for (int r = c; r < R; r += 4) lin_finish_row(a, r, cb, true);
   if (a.epi.kind == 8)
     hc_fin_block(a, a.epi.ctr + (uint64_t)(cb % (a.epi.hid / 128)) * kSyncStride, a.epi.row0, a.epi.row0 + R, cb,
                  &flag);
@@ -770,8 +753,8 @@ __global__ __launch_bounds__(256) void lin_mx(LinMulti m) {
 // lin_mxl: lin_mx for linears with many tile pairs (a vocabulary head), one workgroup per tile pair looping over the
 // k groups: wave c takes chunk c of every group, the next group's requests in flight while one decodes; the chunk sums
 // go to LDS, and at the end each (row, column) folds the chunks of each group left and the groups left - the order of
-// lin_mx, so the results are bit-identical - and stores one tagged total per pair (S = 1). The block finisher is the
-// block's last pair, as in lin_mx.
+// lin_mx, so the results are bit-identical - and stores one total per pair (S = 1). The block's last arriving pair
+// finishes it, as in lin_mx.
 template <int K, int RT>
 constexpr uint32_t lin_mxl_wave() { return kLinChunkKt * 64 * K + RT * 256; }
 template <int K, int RT>
@@ -790,9 +773,7 @@ __global__ __launch_bounds__(256) void lin_mxl(LinMulti m) {
   const int lane = threadIdx.x & 63, c = (int)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   float *csum = (float *)(lds + 8 * lin_mxl_wave<K, RT>());  // [group][4 chunks][RT][32]
   const int cb = p / 4;
-  uint32_t *epoch = a.cnt ? a.cnt + (uint64_t)cb * kSyncStride : nullptr;
-  uint32_t ep = 0;
-  if (epoch) ep = ld_cg(epoch);
+  __shared__ int flag;
   const uint8_t *tiles = (const uint8_t *)a.tiles + (uint64_t)p * IT * 64 * K;
   auto stage = [&](int g) {  // group g's requests into buffer g & 1 (the rows come from the prep launch)
     const int kt0 = g * kLinGroupKt + c * kLinChunkKt, nkt = max(0, min(kLinChunkKt, IT - kt0));
@@ -839,7 +820,6 @@ __global__ __launch_bounds__(256) void lin_mxl(LinMulti m) {
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this buffer's reads are done before it is refilled
   }
   __syncthreads();
-  const uint32_t tag = (uint32_t)__builtin_amdgcn_readfirstlane(ep) + 1u;
   for (int e = threadIdx.x; e < R * 32; e += 256) {
     float tot = 0.f;
     for (int g = 0; g < G; g++) {
@@ -848,21 +828,17 @@ __global__ __launch_bounds__(256) void lin_mxl(LinMulti m) {
       for (int cc = 1; cc < nc; cc++) v = v + csum[(g * 4 + cc) * RT * 32 + e];
       tot = g == 0 ? v : tot + v;
     }
-    const uint64_t o = (uint64_t)(e >> 5) * OTp * 16 + p * 32 + (e & 31);
-    if (epoch)
-      st_tag((uint64_t *)a.part + o, tot, tag);
-    else
-      a.part[o] = tot;
+    st_cg(a.part + (uint64_t)(e >> 5) * OTp * 16 + p * 32 + (e & 31), tot);
   }
-  if (!epoch || p != min(4 * cb + 3, NP - 1)) return;
-  for (int r = c; r < R; r += 4) lin_finish_row(a, r, cb, tag);
-  __syncthreads();
-  if (threadIdx.x == 0) st_cg(epoch, tag);
-  if (a.epi.kind == 8) {
-    __shared__ int flag;
+  if (!a.cnt) return;
+  const int npb = min(4, NP - 4 * cb);
+  uint32_t *ctr = a.cnt + (uint64_t)cb * kSyncStride;
+  if (block_signal(ctr, &flag) != (uint32_t)(npb - 1)) return;
+  if (threadIdx.x == 0) st_cg(ctr, 0u);
+  for (int r = c; r < R; r += 4) lin_finish_row(a, r, cb, true);
+  if (a.epi.kind == 8)
     hc_fin_block(a, a.epi.ctr + (uint64_t)(cb % (a.epi.hid / 128)) * kSyncStride, a.epi.row0, a.epi.row0 + R, cb,
                  &flag);
-  }
 }
 
 // lin_finish: the finisher of the staged path, grid R x ceil(out/128) (one workgroup per row and output block)
@@ -870,7 +846,7 @@ __global__ __launch_bounds__(64) void lin_finish(LinArgs a) {
   __shared__ int flag;
   const int nch = (a.out + 127) / 128;
   const int r = blockIdx.x / nch, c = blockIdx.x % nch;
-  lin_finish_row(a, r, c, 0u);
+  lin_finish_row(a, r, c, false);
   if (a.epi.kind == 8) {
     const int nbs = a.epi.hid / 128, rg = a.epi.row0 + r;
     hc_fin_block(a, a.epi.ctr + (uint64_t)(nbs + rg * nbs + c % nbs) * kSyncStride, rg, rg + 1, c, &flag);

@@ -94,8 +94,8 @@ struct MoeBatchBufs {
   float *dnw = nullptr;        // [R][nslot][hid] weighted slot outputs
   int max_chunks = 0;
   // few rows (moe_batch_few): the k group partials and the (chunk, block) epochs, shared by the layers of one shape
-  uint64_t *vpart = nullptr;   // [chunk][2][inter / 32][k groups][8 rows][32] tagged
-  uint32_t *vep = nullptr;     // [chunk][inter / 128] epochs, kSyncStride apart
+  uint64_t *vpart = nullptr;   // [chunk][2][inter / 32][4 rows][32] f32 pair sums (u64 words of storage)
+  uint32_t *vep = nullptr;     // [chunk][inter / 128] counters, kSyncStride apart, zero between launches
   int vmax_chunks = 0;
 };
 bool moe_batch_supported(int K, int KS, int hid, int inter, int ne, int topk);
@@ -151,9 +151,9 @@ struct LinArgs {
   const float *x;
   float *y;
   uint16_t *xh;           // [R][in] prepared fp16 input (scratch)
-  float *part;            // [S][R][OTp * 16] (scratch): k group partials (u64 tagged values on the one-launch path)
-  uint32_t *cnt;          // per 128-column output block, kSyncStride apart: the block's epoch (the tag of its last
-                          // launch; zero at creation); null: the staged three-kernel path (prep, GEMM, finish)
+  float *part;            // [S][R][OTp * 16] (scratch): k group partials
+  uint32_t *cnt;          // per 128-column output block, kSyncStride apart, zero between launches (the block's last
+                          // arriver resets it); null: the staged three-kernel path (prep, GEMM, finish)
   int xh_in;              // 1: xh holds this run's prepared rows (a prep launch ran); 0: the GEMM prepares its chunks
   int kloop;              // 1: one workgroup per tile pair loops over the k groups (S = 1: one total per pair)
   LinEpi epi;

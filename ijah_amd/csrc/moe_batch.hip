@@ -449,6 +449,64 @@ __global__ __launch_bounds__(1024) void bat_scan(MoeArgs a, uint32_t *bk, uint32
   }
   if (tid == 0) *nchunks = min(cc[n > 0 ? n - 1 : 0], (uint32_t)max_chunks);
 }
+// Few rows (R <= 32): the route, the chunk list and the placement in one workgroup (three launches fewer). Waves take
+// rows for the top-k (route_one: the one-row step's keys and weights); then the routed slots per expert are counted in
+// LDS, scanned into offsets and chunks of at most crows rows (the shared expert takes every row, last), and each slot
+// takes its row in its expert's list (rows[row] = r * nslot + k; the order inside an expert changes no result).
+__global__ __launch_bounds__(1024) void bat_route_place(MoeArgs a, uint32_t *bk, uint32_t *chunks, int max_chunks,
+                                                        uint32_t crows, uint32_t *rows) {
+  __shared__ uint32_t sc[1024], cc[1024], offl[1024], cur[1024];
+  const int tid = threadIdx.x, wave = tid >> 6, n = a.ne + (a.nslot > a.topk ? 1 : 0);
+  for (int r = wave; r < a.R; r += 16) {
+    if (a.ne <= 512)
+      route_one<8>(a, r);
+    else
+      route_one<16>(a, r);
+  }
+  sc[tid] = 0u;
+  cur[tid] = 0u;
+  __threadfence();
+  __syncthreads();  // the route is stored (read back below through L2)
+  for (int s = tid; s < a.R * a.topk; s += 1024) {
+    const uint32_t e = ld_cg(a.route + (uint64_t)(s / a.topk) * 2 * a.topk + s % a.topk);
+    atomicAdd(&sc[e < (uint32_t)a.ne ? e : 0u], 1u);
+  }
+  __syncthreads();
+  const uint32_t c = tid < a.ne ? sc[tid] : (tid < n ? (uint32_t)a.R : 0u);  // the shared expert takes every row
+  __syncthreads();
+  sc[tid] = c;
+  cc[tid] = (c + crows - 1) / crows;
+  __syncthreads();
+  for (int d = 1; d < 1024; d <<= 1) {  // inclusive Hillis-Steele scans of rows and chunks
+    const uint32_t v = tid >= d ? sc[tid - d] : 0u, w = tid >= d ? cc[tid - d] : 0u;
+    __syncthreads();
+    sc[tid] += v;
+    cc[tid] += w;
+    __syncthreads();
+  }
+  if (tid < n) {
+    const uint32_t off = sc[tid] - c, ch0 = cc[tid] - (c + crows - 1) / crows;
+    offl[tid] = off;
+    for (uint32_t r = 0, q = ch0; r < c; r += crows, q++)
+      if ((int)q < max_chunks) {
+        chunks[3 * q] = (uint32_t)tid;
+        chunks[3 * q + 1] = off + r;
+        chunks[3 * q + 2] = min(c - r, crows);
+      }
+  }
+  if (tid == 0) bk[3 * (a.ne + 1)] = min(cc[n > 0 ? n - 1 : 0], (uint32_t)max_chunks);
+  __syncthreads();
+  for (int s = tid; s < a.R * a.nslot; s += 1024) {
+    const int r = s / a.nslot, k = s % a.nslot;
+    uint32_t e = (uint32_t)a.ne, pos = (uint32_t)r;  // the shared expert's list is every token in order
+    if (k < a.topk) {
+      e = ld_cg(a.route + (uint64_t)r * 2 * a.topk + k);
+      e = e < (uint32_t)a.ne ? e : 0u;
+      pos = atomicAdd(&cur[e], 1u);
+    }
+    rows[offl[e] + pos] = (uint32_t)s;
+  }
+}
 // One wave per slot (r, k): takes the slot's row in its expert's list (rows[row] = r * nslot + k; k == topk: the
 // shared expert, whose list is every token in order) and writes that row of the A operand:
 // xh[row] = [gate | up] fp16(H(x[r] * suh_e)) in kp order (the two projections have their own suh).
@@ -1256,14 +1314,23 @@ __global__ __launch_bounds__(256) void bat_combine(MoeArgs a, const float *__res
 //   bat_gu_grp  workgroup (chunk, 128-column block cb of inter, projection, pair q of the block), looping over the k
 //               groups of 512 (the next group's requests in flight while one decodes); wave c takes k chunk c of each
 //               group (8 k tiles, one MFMA chain from zero); the chunk sums are folded left in LDS, the groups left in
-//               registers, and the pair's sums stored as tagged values. The block's finisher, the highest-numbered of
-//               its producers (workgroups are dispatched in index order per XCD, so it waits only for dispatched
-//               ones), writes the block's rows of hh (H(g) svh_g, SiLU, H(u) svh_u, suh_d, H, fp16, kp order), then
-//               advances the block's epoch;
+//               registers, and the pair's sums stored (device-coherent). The last of the block's 8 workgroups to
+//               arrive (a counter per block, reset by it) writes the block's rows of hh (H(g) svh_g, SiLU, H(u)
+//               svh_u, suh_d, H, fp16, kp order);
 //   bat_dn_blk  workgroup (chunk, 128-column output block c), wave q one pair: every k chunk of inter (chains from zero,
 //               folded left), then H, svh_d and the slot's route weight per row (no hand-off between workgroups).
-// Tags: the epoch of the (chunk, block) slot plus one; the partials and epochs are shared by every layer (one
-// stream), so tags only grow and no stale partial carries a current tag.
+// The partials and counters live in one pool per layer shape, shared by the layers (one stream; every counter is back
+// at zero when a launch ends).
+// the workgroup's arrival at a counter after its stores completed; returns the count before it
+__device__ uint32_t block_signal8(uint32_t *p, int *flag) {
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) *flag = (int)atomicAdd(p, 1u);
+  __syncthreads();
+  const uint32_t old = (uint32_t)*flag;
+  __syncthreads();
+  return old;
+}
 constexpr int kVChunk = 8;  // k tiles of a k chunk
 constexpr int kFewChunkRows = 4;  // rows of a chunk on the few-row path (its LDS tier)
 constexpr int kFewMaxGroups = 8;  // k groups of 512 (hidden size up to 4096)
@@ -1304,8 +1371,9 @@ __global__ __launch_bounds__(256) void bat_gu_grp(MoeArgs a, const uint32_t *bk,
   const bool sh = e >= a.ne;
   const int KE = sh ? KS : K;
   float *csum = (float *)(lds + 8 * v_gu_wave<KM, RT>());  // [k group][4 chunks][RT][32]
-  uint32_t *ep = epochs + ((uint64_t)ch * NBI + cb) * kSyncStride;
-  const uint32_t e0 = ld_cg(ep);
+  __shared__ int flag;
+  uint32_t *ctr = epochs + ((uint64_t)ch * NBI + cb) * kSyncStride;
+  float *pf = (float *)part;
   const uint8_t *blk = expert_block(a, e);
   const uint8_t *tr = blk + tr_of(a, e, proj) + (uint64_t)p * IT * 64 * KE;
   // requests of k group g into buffer g & 1: this wave's chunk of tiles, then its rows; returns their count
@@ -1357,28 +1425,22 @@ __global__ __launch_bounds__(256) void bat_gu_grp(MoeArgs a, const uint32_t *bk,
       for (int cc = 1; cc < nc; cc++) v = v + csum[(g * 4 + cc) * RT * 32 + ent];
       tot = g == 0 ? v : tot + v;
     }
-  const uint32_t tag = (uint32_t)__builtin_amdgcn_readfirstlane(e0) + 1u;
   if (ent < nrows * 32)
-    st_tag(part + ((((uint64_t)ch * 2 + proj) * NP + p) * kFewChunkRows + (ent >> 5)) * 32 + (ent & 31), tot, tag);
-  if (proj != 1 || q != 3) return;
+    st_cg(pf + ((((uint64_t)ch * 2 + proj) * NP + p) * kFewChunkRows + (ent >> 5)) * 32 + (ent & 31), tot);
+  // the last of the block's 8 workgroups (2 projections x 4 pairs) finishes it and resets its counter
+  if (block_signal8(ctr, &flag) != 7u) return;
+  if (threadIdx.x == 0) st_cg(ctr, 0u);
   // the block's finisher: rows r = wave, wave + 4, ..; lane: columns o = lane, lane + 64 of block cb
   const uint16_t *svg = (const uint16_t *)(blk + sv_of(a, e, 0)) + cb * 128;
   const uint16_t *svu = (const uint16_t *)(blk + sv_of(a, e, 1)) + cb * 128;
   const uint16_t *sud = (const uint16_t *)(blk + su_of(a, e, 2)) + cb * 128;
   const int pr0 = cb * 4 + (lane >> 5), n0 = lane & 31;  // column lane: pair pr0; column lane + 64: pair pr0 + 2
   for (int r = c; r < nrows; r += 4) {
-    float gs[2] = {0.f, 0.f}, us[2] = {0.f, 0.f};
-    for (uint32_t it = 0; it < (1u << 20); it++) {
-      bool all = true;
+    float gs[2], us[2];
 #pragma unroll
-      for (int h = 0; h < 2; h++) {
-        const uint64_t ug = ld_cg(part + ((((uint64_t)ch * 2 + 0) * NP + pr0 + 2 * h) * kFewChunkRows + r) * 32 + n0);
-        const uint64_t uu = ld_cg(part + ((((uint64_t)ch * 2 + 1) * NP + pr0 + 2 * h) * kFewChunkRows + r) * 32 + n0);
-        all = all && tag_ok(ug, tag) && tag_ok(uu, tag);
-        gs[h] = tag_val(ug);
-        us[h] = tag_val(uu);
-      }
-      if (__all(all)) break;
+    for (int h = 0; h < 2; h++) {
+      gs[h] = ld_cg(pf + ((((uint64_t)ch * 2 + 0) * NP + pr0 + 2 * h) * kFewChunkRows + r) * 32 + n0);
+      us[h] = ld_cg(pf + ((((uint64_t)ch * 2 + 1) * NP + pr0 + 2 * h) * kFewChunkRows + r) * 32 + n0);
     }
     float g0 = gs[0], g1 = gs[1], u0 = us[0], u1 = us[1];
     fwht2(g0, g1, lane, a.had_inter, a.sc_inter);
@@ -1394,8 +1456,6 @@ __global__ __launch_bounds__(256) void bat_gu_grp(MoeArgs a, const uint32_t *bk,
     out[kp((uint32_t)lane)] = f2h(h0);
     out[kp((uint32_t)lane + 64)] = f2h(h1);
   }
-  __syncthreads();
-  if (threadIdx.x == 0) st_cg(ep, tag);
 }
 
 // LDS: per wave its pair's k tile pairs (all of inter), then the chunk's RT rows of hh (inter halves each), then the
@@ -1590,15 +1650,23 @@ void launch_moe_batch(const MoeArgs &a, const MoeBatchBufs &b, hipStream_t s) {
   } else {
     hipLaunchKernelGGL(bat_router<1>, dim3((a.R + 31) / 32, (ncol + 31) / 32), dim3(64 * kRouterWaves), 0, s, a);
   }
-  hipLaunchKernelGGL(bat_route, dim3((a.R + 3) / 4), dim3(256), 0, s, a);
-  const int self_count = a.R * a.topk < 4096;  // few slots: counted inside bat_scan
-  if (!self_count) hipLaunchKernelGGL(bat_hist, dim3(kHistGroups), dim3(256), 0, s, a, b.bk);
   const int KS = a.nslot > a.topk ? a.slay.K : a.lay.K;
   const bool few = moe_batch_exact(a) && b.vpart && moe_batch_few(a.R, a.hid, a.inter, a.lay.K, KS);
-  hipLaunchKernelGGL(bat_scan, dim3(1), dim3(1024), 0, s, a, b.bk, b.chunks, b.max_chunks, self_count,
-                     (uint32_t)(few ? kFewChunkRows : kChunkRows));
+  if (few) {  // route, chunks and placement in one workgroup
+    IJ_CHECK(a.ne < 1024 && a.R * a.nslot <= 1024 * 32, "few-row MoE: %d experts", a.ne);
+    hipLaunchKernelGGL(bat_route_place, dim3(1), dim3(1024), 0, s, a, b.bk, b.chunks, b.max_chunks,
+                       (uint32_t)kFewChunkRows, b.rows);
+  } else {
+    hipLaunchKernelGGL(bat_route, dim3((a.R + 3) / 4), dim3(256), 0, s, a);
+    const int self_count = a.R * a.topk < 4096;  // few slots: counted inside bat_scan
+    if (!self_count) hipLaunchKernelGGL(bat_hist, dim3(kHistGroups), dim3(256), 0, s, a, b.bk);
+    hipLaunchKernelGGL(bat_scan, dim3(1), dim3(1024), 0, s, a, b.bk, b.chunks, b.max_chunks, self_count,
+                       (uint32_t)kChunkRows);
+  }
   IJ_CHECK(a.had_hid == 128, "batched MoE: hidden size %d needs a 128-wide Hadamard", a.hid);
-  if (moe_batch_exact(a)) {
+  if (few) {
+    hipLaunchKernelGGL(bat_prep_rows, dim3((S * 2 * (a.hid / 128) + 3) / 4), dim3(256), 0, s, a, b.rows, b.xh);
+  } else if (moe_batch_exact(a)) {
     hipLaunchKernelGGL(bat_place_rows, dim3((S + 255) / 256), dim3(256), 0, s, a, b.bk, b.rows);
     hipLaunchKernelGGL(bat_prep_rows, dim3((S * 2 * (a.hid / 128) + 3) / 4), dim3(256), 0, s, a, b.rows, b.xh);
   } else

@@ -3,9 +3,8 @@
 // with that device current (at the library's device set-up, or at the first call on another device); host code only
 // ever passes that address, never the array's name (a host-side stand-in that is not device memory).
 //
-// Every call on one GPU shares its array and finds the previous call's contents: the block epochs and the tagged
-// partials are cleared by a fill kernel at the start of each call (a kernel, not a memset, so that a captured call
-// replays correctly). Calls that overlap on one GPU (two streams, two threads) race on the array.
+// Every call on one GPU shares its array and finds the previous call's contents: the block counters are cleared by a
+// fill kernel at the start of each call (a kernel, not a memset, so that a captured call replays correctly). Calls that overlap on one GPU (two streams, two threads) race on the array.
 #include <hip/hip_runtime.h>
 
 #include <mutex>

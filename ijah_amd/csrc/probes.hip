@@ -6,6 +6,7 @@
 //                    real kernels: one dependent 32x32x16 f16 MFMA per decoded tile pair), 2 each wave decodes a tile
 //                    and feeds it to its MFMA chain (the fused loop of the GEMMs), 3 even waves decode and odd waves
 //                    run MFMA chains (specialised waves). Comparing the times says whether the two overlap.
+//   probe_stream     cold streams into LDS (global_load_lds) against plain 16-byte loads into registers.
 // Per wave (64 words of out): lane 0 the results folded (so that nothing is optimised away), lane 1 the s_memtime
 // ticks of its loop, lanes 2-3 its HW_ID and XCC_ID (where it ran), lane 4 the loop in 100 MHz real-time ticks.
 #include <hip/hip_runtime.h>
@@ -75,6 +76,43 @@ __global__ __launch_bounds__(256) void probe_mix(const uint8_t *tiles, int iters
   out[(blockIdx.x * 4 + wave) * 64 + lane] = v;
 }
 
+// probe_stream: every wave streams `bytes` (a multiple of 1 KB) from its own span of src: mode 0 into LDS with
+// global_load_lds (1 KB per request, the fused kernels' tile streams), mode 1 into registers with 16-byte loads
+// (folded into a checksum). One wait at the end; lane 1 of out records the wave's s_memtime ticks.
+__global__ __launch_bounds__(1024) void probe_stream(const uint8_t *src, uint32_t bytes, int mode, uint32_t *out) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const uint8_t *p = src + ((uint64_t)blockIdx.x * nw + wave) * bytes;
+  const uint64_t t0 = __builtin_amdgcn_s_memtime();
+  uint32_t h = 0;
+  if (mode == 0) {
+    uint8_t *dst = lds + wave * 4096;  // 4 KB per wave, reused round robin (the data is not read)
+    for (uint32_t o = 0; o < bytes; o += 1024)
+      __builtin_amdgcn_global_load_lds((const void *)(p + o + lane * 16),
+                                       (__attribute__((address_space(3))) void *)(dst + (o & 4095)), 16, 0, 0);
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    h = ((const uint32_t *)dst)[lane];
+  } else {
+    uint4 acc = make_uint4(0, 0, 0, 0);
+    for (uint32_t o = 0; o < bytes; o += 8192) {
+      uint4 v[8];
+#pragma unroll
+      for (int j = 0; j < 8; j++)
+        v[j] = o + j * 1024 < bytes ? *(const uint4 *)(p + o + j * 1024 + lane * 16) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        acc.x ^= v[j].x;
+        acc.y ^= v[j].y;
+        acc.z ^= v[j].z;
+        acc.w ^= v[j].w;
+      }
+    }
+    h = acc.x ^ acc.y ^ acc.z ^ acc.w;
+  }
+  const uint32_t cyc = (uint32_t)(__builtin_amdgcn_s_memtime() - t0);
+  out[(blockIdx.x * nw + wave) * 64 + lane] = lane == 1 ? cyc : h;
+}
+
 }  // namespace
 
 size_t probe_lds(int K) { return (size_t)4 * kProbeTiles * 64 * K; }
@@ -88,6 +126,7 @@ void probe_kernels(std::vector<KernelEntry> &v) {
   v.push_back({"probe_mix", (const void *)&probe_mix<6>, {P, I, I, P}, 6, -1});
   v.push_back({"probe_mix", (const void *)&probe_mix<7>, {P, I, I, P}, 7, -1});
   v.push_back({"probe_mix", (const void *)&probe_mix<8>, {P, I, I, P}, 8, -1});
+  v.push_back({"probe_stream", (const void *)&probe_stream, {P, I, I, P}, -1, -1});
 }
 
 }  // namespace ijah

@@ -52,7 +52,7 @@ NE_API int ne_exl3_lin_info(const ne_exl3_lin *l, int *in, int *out, int *K);
 NE_API int ne_exl3_lin_run(ne_exl3_lin *l, int R, const ne_buf *x, uint64_t x_off, ne_buf *y, uint64_t y_off,
                            double *gpu_ms);
 /* ne_exl3_lin_run that allocates nothing: no counterpart in the reference; for callers that cannot allocate device
- * memory (code under HIP graph capture, tight serving loops). Its block epochs, prepared input and k group partials live
+ * memory (code under HIP graph capture, tight serving loops). Its block counters, prepared input and k group partials live
  * in one fixed 32 MiB scratch array per GPU, held until the process ends; a run needing more (e.g. a 151936-wide
  * vocabulary head at 32 rows) is rejected with an error. Same results as ne_exl3_lin_run. Every call on one GPU
  * shares that array: calls that overlap on one GPU (other streams or threads) race. Not timed (no gpu_ms). */
