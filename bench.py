@@ -265,6 +265,28 @@ def run_probes(eng, iters=4000):
             }
             res.free()
             print(f"probe {key}: {out[key]}", file=sys.stderr, flush=True)
+        # the same decode through a 64 KB LDS codebook table (probe_lut): one workgroup per CU of 4, 8 or 16 waves
+        for nw in (4, 8, 16):
+            res = eng.alloc(cus * nw * 64 * 4)
+            t = {}
+            for mode in (0, 1, 2, 3):
+                args = [tiles, np.int32(iters), np.int32(mode), res]
+                kw = dict(fconsts=[(10, "u32", K)], tg_mem=65536 + nw * 8 * 64 * K)
+                eng.run_kernel("probe_lut", args, (cus, 1, 1), (nw * 64, 1, 1), **kw)
+                t[mode] = eng.run_kernel("probe_lut", args, (cus, 1, 1), (nw * 64, 1, 1), reps=3, **kw) / 3
+            w = res.download(np.uint32, (cus * nw, 64))
+            wts = cus * nw * iters * 8 * 512
+            clk = float(np.median(w[:, 1] / np.maximum(w[:, 4], 1))) * 100e6
+            key = f"K{K}_lut_w{nw // 4}"
+            out[key] = {"ms": {str(m): round(v, 4) for m, v in t.items()},
+                        "decode_Gweights_s": round(wts / (t[0] * 1e-3) / 1e9, 1),
+                        "decode_simd_cycles_per_weight": round(t[0] * 1e-3 * clk * cus * 4 / wts, 4),
+                        "with_mfma_vs_decode": round(t[2] / t[0], 3),
+                        "half_table_Gweights_s": round(wts / (t[1] * 1e-3) / 1e9, 1),
+                        "quarter_table_Gweights_s": round(wts / (t[3] * 1e-3) / 1e9, 1),
+                        "mismatched_words": int(w[:, 5].sum())}
+            res.free()
+            print(f"probe {key}: {out[key]}", file=sys.stderr, flush=True)
         tiles.free()
     return out
 

@@ -178,6 +178,7 @@ void launch_hc_prep(const float *h, const uint16_t *nw, const uint16_t *iw, floa
 void init_batch_attrs();
 void init_fused_attrs();
 void init_lin_attrs();
+void init_probe_attrs();  // the probes' dynamic LDS limits (once per device)
 // W' fp16 bits [IT*16][OT*16] from re-laid tiles
 void launch_decode(const uint32_t *tiles, int IT, int OT, int K, uint16_t *w, hipStream_t s);
 

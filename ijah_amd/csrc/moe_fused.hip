@@ -75,16 +75,25 @@ constexpr int had_of(int d) { return d % 128 == 0 ? 128 : d % 64 == 0 ? 64 : d %
 __device__ __forceinline__ uint32_t rfl(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
 
 
-__device__ __forceinline__ void stamp_r(const MoeArgs &a, int field) {  // the route's own steps
-  if (a.trace && (threadIdx.x & 63) == 0) a.trace[((uint64_t)4096 + blockIdx.x) * 8 + field] = wall_clock64();
+// Trace mode (a.trace set; a measurement aid): per-wave wall-clock stamps kept in LDS, so that they add nothing to the
+// wave's vector-memory counter (which the hand-counted waits rely on), and written out at the end of the launch:
+// trace[(workgroup * 16 + wave) * 32 + field]; fields 0-7 the phases, 8-15 and 16-23 finer steps, 24-27 the route's.
+constexpr int kTraceFields = 32;
+__device__ __forceinline__ uint64_t *trace_lds() {
+  __shared__ uint64_t t[kWaves * kTraceFields];
+  return t;
 }
-__device__ __forceinline__ void stamp_w(const MoeArgs &a, int field) {  // per-wave extra stamps
-  if (a.trace && (threadIdx.x & 63) == 0)
-    a.trace[((uint64_t)4096 + 256 + blockIdx.x * kWaves + (threadIdx.x >> 6)) * 8 + field] = wall_clock64();
+__device__ __forceinline__ void stamp_at(const MoeArgs &a, int field) {
+  if (a.trace && (threadIdx.x & 63) == 0) trace_lds()[(threadIdx.x >> 6) * kTraceFields + field] = wall_clock64();
 }
-__device__ __forceinline__ void stamp(const MoeArgs &a, int field) {
-  if (a.trace && (threadIdx.x & 63) == 0)
-    a.trace[((uint64_t)blockIdx.x * kWaves + (threadIdx.x >> 6)) * 8 + field] = wall_clock64();
+__device__ __forceinline__ void stamp(const MoeArgs &a, int field) { stamp_at(a, field); }
+__device__ __forceinline__ void stamp_w(const MoeArgs &a, int field) { stamp_at(a, 8 + field); }
+__device__ __forceinline__ void stamp_x(const MoeArgs &a, int field) { stamp_at(a, 16 + field); }
+__device__ __forceinline__ void stamp_r(const MoeArgs &a, int field) { stamp_at(a, 24 + field); }
+__device__ __forceinline__ void trace_out(const MoeArgs &a) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (a.trace && lane < kTraceFields)
+    a.trace[((uint64_t)blockIdx.x * kWaves + wave) * kTraceFields + lane] = trace_lds()[wave * kTraceFields + lane];
 }
 
 struct Route {  // the workgroup's copy of the route of the row
@@ -338,6 +347,8 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
   __shared__ __attribute__((aligned(16))) _Float16 hl[kMaxH][128];
   __shared__ float hsum[kMaxH][2][128];
   __shared__ float csum[kMaxGT][kGrp][32];                                 // k chunk sums of the gate/up tasks
+  __shared__ uint32_t tcnt[kMaxGT];                                        // chunk sums of each task in LDS
+  __shared__ uint32_t s_prep;                                              // prep chunks ready: routed bits 0-7, shared 8-11
   __shared__ __attribute__((aligned(16))) uint16_t hvec[kMaxH][3][128];   // svh_g, svh_u, suh_d of each h block
   __shared__ __attribute__((aligned(16))) uint16_t csv[kMaxTopkV + 1][128]; // the combine's svh_d per slot
   __shared__ __attribute__((aligned(16))) float xl[HID];                    // the input row (staged at launch)
@@ -345,8 +356,19 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
   __shared__ uint32_t s_tag, s_ok;
   const int lane = threadIdx.x & 63, wave = (int)rfl(threadIdx.x >> 6);
   const int hs = a.nslot > a.topk ? 1 : 0;
-  // the workgroup's plan words, one per lane, read before any tile request and picked with readlane (a vector load
-  // later would wait for the wave's tile streams)
+  // ---- 0. every launch-time load at once, so that their latencies overlap rather than add: the router rows, the
+  // epoch and x into LDS (control wave; its polls' waits cover these requests), then the workgroup's plan words (one
+  // per lane, read before any tile request and picked with readlane: a vector load later would wait for the wave's
+  // tile streams)
+  const bool rrow = router_active<HID>(a);
+  RouterRow<HID> rr;
+  if (rrow) router_load<HID>(a, rr);
+  uint64_t ep = 0;
+  if (wave == kCtl) {
+    __builtin_amdgcn_s_setprio(3);  // the route is the critical path: this wave first on its SIMD
+    ep = ld_cg((const uint64_t *)a.fsync);  // every lane (one request; no branch whose end would wait for it)
+    stream_tiles((const uint8_t *)a.x, 0, 0, 0, HID / 4, 8, (uint8_t *)xl);  // 4 HID bytes
+  }
   const uint32_t plw = a.units[(size_t)blockIdx.x * kPW + lane];
   auto PL = [&](int i) { return (uint32_t)__builtin_amdgcn_readlane((int)plw, i); };
   uint64_t *part_gu = (uint64_t *)a.part;                                   // [column][NKG groups][32]
@@ -371,23 +393,39 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
     m = (int)(t / (4 * NKG * NG));
   };
   int nops = 0;  // tile / vector requests (loads) this wave has issued: waits count the ones issued after
+  if (a.trace && lane < kTraceFields) trace_lds()[wave * kTraceFields + lane] = 0;
   stamp(a, 0);
 
-  // ---- 0. before the route: router rows first (the route waits for them); the shared expert's units, its suh
-  // chunks, once this workgroup's logits are out
-  const bool rrow = router_active<HID>(a);
-  RouterRow<HID> rr;
-  if (rrow) router_load<HID>(a, rr);
+  // the router logits, then the shared expert's units and its suh chunks once this workgroup's logits are out
   if (threadIdx.x == 0) s_ok = 1;
-  if (wave == kCtl) {  // the epoch, then x into LDS (its polls' waits cover these requests)
-    __builtin_amdgcn_s_setprio(3);  // the route is the critical path: this wave first on its SIMD
-    uint64_t ep = 0;
-    if (lane == 0) ep = ld_cg((const uint64_t *)a.fsync);
-    if (lane == 0) s_tag = (uint32_t)ep + 1u;
-    stream_tiles((const uint8_t *)a.x, 0, 0, 0, HID / 4, 8, (uint8_t *)xl);  // 4 HID bytes
-  }
+  if (threadIdx.x < kMaxGT) tcnt[threadIdx.x] = 0;
+  if (threadIdx.x == 0) s_prep = 0;
+  uint32_t ep_lo = (uint32_t)ep;
+  asm volatile("" : "+v"(ep_lo));  // its first use here, after the plan words' request (not at the branch's end)
+  if (wave == kCtl && lane == 0) s_tag = ep_lo + 1u;
   lds_barrier();  // the epoch is known
   const uint32_t tag = s_tag, tag16 = (tag - 1u) % 65535u + 1u;
+  // a k chunk's sum into LDS; the wave completing a task's fourth chunk folds the four in k order and stores the
+  // column's k-group partial at once (task index: the shared tasks, then the routed ones)
+  auto task_done = [&](int ti, bool sh, int c, float v) {
+    if (lane < 32) csum[ti][c][lane] = v;
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the sums are in LDS before the count says so
+    uint32_t prev = 0;
+    if (lane == 0) prev = atomicAdd(&tcnt[ti], 1u);
+    prev = (uint32_t)__shfl((int)prev, 0, 64);
+    asm volatile("" ::: "memory");
+    if (prev != kGrp - 1) return;
+    if (lane < 32) {
+      int m, g, kg, p;
+      task(sh ? st0 + (uint32_t)ti : rt0 + (uint32_t)ti - nst, m, g, kg, p);
+      float sv = csum[ti][0][lane];
+#pragma unroll
+      for (int cc = 1; cc < kGrp; cc++) sv = sv + csum[ti][cc][lane];
+      const uint32_t col =
+          sh ? (uint32_t)(m * NP + g * 4 + p) : (uint32_t)(((hs + m / 2) * 2 + (m & 1)) * NP + g * 4 + p);
+      st_tag(part_gu + ((size_t)col * NKG + kg) * 32 + lane, sv, tag);
+    }
+  };
   if (rrow) router_finish<HID>(a, rr, tag16);
   lds_barrier();  // this workgroup's logits are out: the router rows had HBM to themselves
   const bool sprep_w = spk != kNone && wave >= kSpw && wave < kSpw + kGrp;
@@ -418,6 +456,7 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
   if (wave == kCtl) {
     const bool ok = a.ne <= 512 ? route_wave<8>(a, &rt, tag16) : route_wave<16>(a, &rt, tag16);
     if (!ok && lane == 0) s_ok = 0;
+    __builtin_amdgcn_s_setprio(0);  // from here on a wave like the others (it takes routed units)
     stamp(a, 2);
   } else {
     stamp(a, 1);
@@ -443,7 +482,9 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
   }
   nops += n_su;
   const int end_su = nops;
+  stamp_w(a, 3);
   lds_barrier();  // every prep chunk's suh is requested ahead of the tile streams
+  stamp_w(a, 4);
   if (ok) {
 #pragma unroll
     for (int k = 0; k < kUnitsPerWave; k++) {
@@ -457,7 +498,9 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
       end_u[k] = nops;
     }
   }
+  stamp_w(a, 5);
   lds_barrier();
+  stamp_w(a, 6);
   int dunit = -1, dslot = 0, dhs = 0, end_dn = 0;  // this wave's down unit, its LDS slot and h slot
 #pragma unroll
   for (int k = 0; k < kUnitsPerWave; k++)
@@ -500,34 +543,57 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
   }
   stamp(a, 3);
   // the shared expert while the routed tiles are on their way (its requests went out before the route): its prep
-  // chunks and its down unit's B operands; then the routed prep (suh chunk -> fp16(H(x suh)) in kp order, x from LDS:
-  // a global load now would wait for the tile streams)
+  // chunks, its k chunks and its down unit's B operands; then the routed prep (suh chunk -> fp16(H(x suh)) in kp
+  // order, x from LDS: a global load now would wait for the tile streams)
   wait_vm(nops);  // the requests issued before the route
-  if (sprep_w) prep_chunk<HH>(xl, (int)(spk % NKG) * kGrp + (wave - kSpw), sprep[wave - kSpw], sch);
-  if (dn_shared) {
-#pragma unroll
-    for (int kt = 0; kt < kDnKt; kt++) dw[kt] = decode_pair<KS>(tiles + dslot * SLOT, kt);
+  // a prep chunk is announced by its bit in s_prep (after its LDS writes); a wave waits only for the chunks it reads
+  auto prep_ready = [&](uint32_t bit) {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    if (lane == 0) atomicOr(&s_prep, bit);
+  };
+  auto prep_wait = [&](uint32_t bit) {
+    for (uint32_t it = 0; it < kSpin; it++) {
+      if (__hip_atomic_load(&s_prep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) & bit) break;
+      __builtin_amdgcn_s_sleep(1);
+    }
+    asm volatile("" ::: "memory");
+  };
+  if (sprep_w) {
+    prep_chunk<HH>(xl, (int)(spk % NKG) * kGrp + (wave - kSpw), sprep[wave - kSpw], sch);
+    prep_ready(1u << (8 + wave - kSpw));
   }
+  stamp_w(a, 7);
+  // ---- 3. gate/up k chunks: the shared ones (tiles in since before the route) and the shared down unit's B
+  // operands while the routed tiles are on their way, then the routed ones as their tiles arrive; each chunk's sum
+  // into LDS, and the fold of a task's chunk sums in k order by the wave completing it
+  stamp_x(a, 0);
   if (n_su) {
     wait_vm(nops - end_su);
+    stamp_x(a, 2);
     const uint32_t key = PL(P_RP + (wave >> 2));
     prep_chunk<HH>(xl, (int)(key % NKG) * kGrp + (wave & 3), prep[wave], sch);
+    prep_ready(1u << wave);
   }
-  lds_barrier();  // shared and routed prep chunks ready
-  // ---- 3. gate/up k chunks: the shared ones (tiles in since before the route), then the routed ones as their tiles
-  // arrive, each chunk's sum into LDS; then per task the fold of its chunk sums in k order, stored at once
   if (ok) {
 #pragma unroll
     for (int k = 0; k < kUnitsPerWave; k++) {
       const uint32_t u = uw[k];
       if (u == kNone || (u >> 30) != kUShared) continue;
       const int c = (int)(u & 3u);
+      prep_wait(1u << (8 + c));
       f32x16 acc;
       zero16(acc);
       pair_mfma<KS, 8>(tiles + ((u >> 24) & 0x3Fu) * SLOT, &sprep[c][0], 0, 8, acc);
-      if (lane < 32) csum[(u >> 2) & 0xFu][c][lane] = acc[0];
+      task_done((int)((u >> 2) & 0xFu), true, c, acc[0]);
     }
+    if (dn_shared) {
+#pragma unroll
+      for (int kt = 0; kt < kDnKt; kt++) dw[kt] = decode_pair<KS>(tiles + dslot * SLOT, kt);
+    }
+  }
+  if (ok) {
     constexpr uint32_t pb = 64u * K;  // bytes of one k tile pair
+    bool fst = true;
 #pragma unroll
     for (int k = 0; k < kUnitsPerWave; k++) {
       const uint32_t u = uw[k];
@@ -535,6 +601,7 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
       const uint8_t *tl = tiles + ((u >> 24) & 0x3Fu) * SLOT;
       const int c = (int)(u & 3u);
       const _Float16 *xs = &prep[kGrp * ((u >> 8) & 1u) + c][0] + 8 * (lane >> 5);
+      prep_wait(1u << (kGrp * ((u >> 8) & 1u) + c));
       const int first = end_u[k] - dma_ops(8 * pb);  // requests issued before this chunk's
       f32x16 acc;
       zero16(acc);
@@ -542,24 +609,16 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
       for (int kt = 0; kt < 8; kt++) {
         const int req = (int)(((uint32_t)(kt + 1) * pb - 1u) >> 10);  // the request completing k tile kt
         if (kt == 0 || req != (int)(((uint32_t)kt * pb - 1u) >> 10)) wait_vm(nops - (first + req + 1));
+        if (kt == 0 && fst) stamp_w(a, 0);
         const f16x8 bv = decode_pair<K>(tl, kt);
         const f16x8 av = *(const f16x8 *)(xs + kt * 16);
         acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bv, acc, 0, 0, 0);
       }
-      if (lane < 32) csum[nst + ((u >> 2) & 0xFu)][c][lane] = acc[0];
+      task_done((int)(nst + ((u >> 2) & 0xFu)), false, c, acc[0]);
+      fst = false;
     }
   }
-  lds_barrier();  // every k chunk sum is in LDS
-  if (ok && wave < (int)(nst + nrt) && lane < 32) {  // task `wave`: the shared ones, then the routed ones
-    const bool sh = wave < (int)nst;
-    int m, g, kg, p;
-    task(sh ? st0 + (uint32_t)wave : rt0 + (uint32_t)wave - nst, m, g, kg, p);
-    float sv = csum[wave][0][lane];
-#pragma unroll
-    for (int c = 1; c < kGrp; c++) sv = sv + csum[wave][c][lane];
-    const uint32_t col = sh ? (uint32_t)(m * NP + g * 4 + p) : (uint32_t)(((hs + m / 2) * 2 + (m & 1)) * NP + g * 4 + p);
-    st_tag(part_gu + ((size_t)col * NKG + kg) * 32 + lane, sv, tag);
-  }
+  stamp_w(a, 1);
   stamp(a, 4);
 
   // ---- 4. the routed down unit's tiles into B operands; the h blocks from the gate/up partials (the NKG k group
@@ -569,6 +628,7 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
 #pragma unroll
     for (int kt = 0; kt < kDnKt; kt++) dw[kt] = decode_pair<K>(tiles + dslot * SLOT, kt);
   }
+  stamp_w(a, 2);
   // h loaders: the first 2 nh waves, which the SIMDs serve first (oldest first); wave (h slot, proj), lane: columns
   // o = lane, lane + 64 of the block
   if (ok && wave < 2 * nh) {
@@ -693,6 +753,7 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
     }
   }
   stamp(a, 7);
+  trace_out(a);
   // ---- done: workgroup 0 advances the epoch (one store). It finishes only after every workgroup published its
   // router logit, i.e. after every workgroup read this launch's epoch.
   if (blockIdx.x == 0 && threadIdx.x == 0) st_cg((uint64_t *)a.fsync, (uint64_t)tag);
@@ -759,25 +820,36 @@ MoePlan moe_fused_plan(int hid, int inter, int topk, int nslot, int G) {
       if (key_of(t) != key_of(s0)) return pl;
     if (s1 > s0) pw[P_SPK] = key_of(s0);
     int slot = 0;
-    std::vector<int> nu(kWaves, 0);
-    auto put = [&](int wave, uint32_t word) {
-      if (nu[wave] >= kUnitsPerWave || slot >= kMaxSlots) return false;
-      pw[P_U + kUnitsPerWave * wave + nu[wave]++] = word | (uint32_t)slot++ << 24;
-      return true;
+    std::vector<int> nu(kWaves, 0), simd(4, 0), ndn(kWaves, 0);
+    // every unit (a k chunk or a down unit: 8 k tile pairs to decode) goes to the wave whose SIMD has the least routed
+    // work so far (then the wave with the fewest units): after the route the decode is the step's VALU bound, and a
+    // SIMD's waves share it. The shared expert's units (requested before the route) go to waves kSpw .. kCtl - 1: not the control
+    // wave (it polls the logits meanwhile) and not the routed prep waves (their prep gates the routed chunks). A wave
+    // holds at most one down unit.
+    auto put = [&](bool pre_route, uint32_t word) {
+      const bool dn = (word >> 30) == kUDown;
+      int best = -1;
+      for (int w = pre_route ? kSpw : 0; w < (pre_route ? kCtl : kWaves); w++) {
+        if (nu[w] >= kUnitsPerWave || (dn && ndn[w])) continue;
+        if (best < 0 || simd[w % 4] < simd[best % 4] || (simd[w % 4] == simd[best % 4] && nu[w] < nu[best])) best = w;
+      }
+      if (best < 0 || slot >= kMaxSlots) return -1;
+      pw[P_U + kUnitsPerWave * best + nu[best]++] = word | (uint32_t)slot++ << 24;
+      simd[best % 4] += pre_route ? 0 : 1;  // the shared units run while the routed tiles are on their way
+      ndn[best] += dn ? 1 : 0;
+      return best;
     };
-    // gate/up tasks round robin over the waves (the control wave aside): the shared ones first (requested before the
-    // route), then the routed ones
-    int wv = 0;
+    // gate/up tasks: the shared ones first (requested before the route), then the routed ones
     if ((s1 - s0) + (t1 - t0) > kMaxGT) return pl;
     for (long t = s0; t < s1; t++)
-      for (int c = 0; c < kGrp; c++, wv = (wv + 1) % kCtl)
-        if (!put(wv, kUShared << 30 | (uint32_t)(t - s0) << 2 | (uint32_t)c)) return pl;
+      for (int c = 0; c < kGrp; c++)
+        if (put(true, kUShared << 30 | (uint32_t)(t - s0) << 2 | (uint32_t)c) < 0) return pl;
     for (long t = t0; t < t1; t++) {
       const uint32_t pg = (uint32_t)(std::find(keys.begin(), keys.end(), key_of(t)) - keys.begin());
-      for (int c = 0; c < kGrp; c++, wv = (wv + 1) % kCtl)
-        if (!put(wv, kURouted << 30 | pg << 8 | (uint32_t)(t - t0) << 2 | (uint32_t)c)) return pl;
+      for (int c = 0; c < kGrp; c++)
+        if (put(false, kURouted << 30 | pg << 8 | (uint32_t)(t - t0) << 2 | (uint32_t)c) < 0) return pl;
     }
-    // down units (global unit index: the shared slot's first), one per wave from the last non-control wave down
+    // down units (global unit index: the shared slot's first)
     std::vector<long> units;
     for (long u = US * b / G; u < US * (b + 1) / G; u++) units.push_back(u);
     for (long u = UR * b / G; u < UR * (b + 1) / G; u++) units.push_back(US + u);
@@ -788,9 +860,8 @@ MoePlan moe_fused_plan(int hid, int inter, int topk, int nslot, int G) {
       size_t h = 0;
       while (h < hbs.size() && hbs[h] != id) h++;
       if (h == hbs.size()) hbs.push_back(id);
-      const int wave = kCtl - 1 - (int)i;
-      if (wave < 0 || h >= (size_t)kMaxH) return pl;
-      if (!put(wave, kUDown << 30 | (uint32_t)h << 20 | (uint32_t)u)) return pl;
+      if (h >= (size_t)kMaxH) return pl;
+      if (put(u < US, kUDown << 30 | (uint32_t)h << 20 | (uint32_t)u) < 0) return pl;
     }
     pw[P_NH] = (uint32_t)hbs.size();
     for (size_t i = 0; i < hbs.size(); i++) {

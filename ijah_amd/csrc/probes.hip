@@ -113,7 +113,100 @@ __global__ __launch_bounds__(1024) void probe_stream(const uint8_t *src, uint32_
   out[(blockIdx.x * nw + wave) * 64 + lane] = lane == 1 ? cyc : h;
 }
 
+
+// probe_lut<K>: the trellis decode through a 32768-entry fp16 codebook table in LDS (64 KB, built by the workgroup
+// from the same arithmetic at launch) instead of evaluating the codebook per weight: a field extract, an address and
+// one 2-byte LDS read per weight. One workgroup per CU, blockDim / 256 waves per SIMD. Mode 0 decode only, mode 2
+// decode feeding each wave's MFMA chain, modes 1 and 3 a mix of table and evaluated tile pairs; lane 5 of out: the lanes' weights that differ from decode_pair (checked once
+// before the timed loop).
+template <int K>
+__device__ __forceinline__ f16x8 decode_pair_lut(const uint8_t *tl, int kt, const _Float16 *lut) {
+  constexpr int TW = 8 * K;
+  const int lane = threadIdx.x & 63;
+  const BLane<K> B = b_lane<K>((uint32_t)lane);
+  const uint32_t *T0 = (const uint32_t *)tl + B.tile * TW + kt * 2 * TW;
+  TileWords w[2];
+  w[0].w0 = T0[B.g0.i0];
+  w[0].w1 = T0[B.g0.i1];
+  w[0].w2 = kThreeWords<K> ? T0[B.g0.i2] : 0u;
+  w[1].w0 = T0[B.g1.i0];
+  w[1].w1 = T0[B.g1.i1];
+  w[1].w2 = kThreeWords<K> ? T0[B.g1.i2] : 0u;
+  const uint32_t sh[2] = {B.g0.sh, B.g1.sh};
+  f16x8 r;
+#pragma unroll
+  for (int g = 0; g < 2; g++) {
+    const uint32_t hi = __builtin_amdgcn_alignbit(w[g].w0, w[g].w1, sh[g]);
+    const uint32_t lo = kThreeWords<K> ? __builtin_amdgcn_alignbit(w[g].w1, w[g].w2, sh[g]) : 0u;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      uint32_t c;
+      if constexpr (!kThreeWords<K>) {
+        c = (hi >> (17 - i * K)) & 0x7FFFu;
+      } else {
+        const int s = 49 - i * K;
+        c = (s >= 32 ? (hi >> (s - 32)) : __builtin_amdgcn_alignbit(hi, lo, (uint32_t)s)) & 0x7FFFu;
+      }
+      r[4 * g + i] = lut[c];
+    }
+  }
+  return r;
+}
+template <int K>
+__global__ __launch_bounds__(1024) void probe_lut(const uint8_t *tiles, int iters, int mode, uint32_t *out) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  _Float16 *lut = (_Float16 *)lds;
+  constexpr uint32_t B = kProbeTiles * 64 * K;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (uint32_t c = threadIdx.x; c < 32768u; c += blockDim.x) {
+    const f16x2 v = mcg_pair(c, c);
+    lut[c] = v.x;
+  }
+  uint8_t *slot = lds + 65536 + wave * B;
+  for (uint32_t o = lane * 16; o < B; o += 1024) *(uint4 *)(slot + o) = *(const uint4 *)(tiles + o);
+  __syncthreads();
+  uint32_t bad = 0;
+#pragma unroll
+  for (int kt = 0; kt < kProbeTiles; kt++) {
+    const uint4 u = __builtin_bit_cast(uint4, decode_pair_lut<K>(slot, kt, lut));
+    const uint4 v = __builtin_bit_cast(uint4, decode_pair<K>(slot, kt));
+    bad += (u.x != v.x) + (u.y != v.y) + (u.z != v.z) + (u.w != v.w);
+  }
+  uint32_t h = 0;
+  const uint64_t t0 = __builtin_amdgcn_s_memtime(), r0 = __builtin_amdgcn_s_memrealtime();
+  f32x16 acc;
+#pragma unroll
+  for (int i = 0; i < 16; i++) acc[i] = 0.f;
+  f16x8 a;
+#pragma unroll
+  for (int i = 0; i < 8; i++) a[i] = (_Float16)(0.001f * (lane + i));
+  for (int it = 0; it < iters; it++) {
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int kt = 0; kt < kProbeTiles; kt++) {
+      // mode 1/3: a mix, tile pairs kt % 4 < 2 (mode 1) or kt % 4 < 1 (mode 3) through the table, the others evaluated
+      const bool use_lut = mode == 1 ? (kt & 3) < 2 : mode == 3 ? (kt & 3) < 1 : true;
+      const f16x8 b = use_lut ? decode_pair_lut<K>(slot, kt, lut) : decode_pair<K>(slot, kt);
+      const uint4 u = __builtin_bit_cast(uint4, b);
+      h ^= u.x ^ u.y ^ u.z ^ u.w;
+      if (mode == 2) acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc, 0, 0, 0);
+    }
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; i++) s += acc[i];
+  const uint32_t cyc = (uint32_t)(__builtin_amdgcn_s_memtime() - t0);
+  const uint32_t rt = (uint32_t)(__builtin_amdgcn_s_memrealtime() - r0);
+  const uint32_t v = lane == 1 ? cyc : lane == 4 ? rt : lane == 5 ? bad : (h ^ __float_as_uint(s));
+  out[(blockIdx.x * (blockDim.x >> 6) + wave) * 64 + lane] = v;
+}
+
 }  // namespace
+
+void init_probe_attrs() {
+  for (const void *f : {(const void *)&probe_lut<5>, (const void *)&probe_lut<8>})
+    IJ_HIP(hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 65536 + 16 * kProbeTiles * 64 * 8));
+}
 
 size_t probe_lds(int K) { return (size_t)4 * kProbeTiles * 64 * K; }
 
@@ -126,6 +219,8 @@ void probe_kernels(std::vector<KernelEntry> &v) {
   v.push_back({"probe_mix", (const void *)&probe_mix<6>, {P, I, I, P}, 6, -1});
   v.push_back({"probe_mix", (const void *)&probe_mix<7>, {P, I, I, P}, 7, -1});
   v.push_back({"probe_mix", (const void *)&probe_mix<8>, {P, I, I, P}, 8, -1});
+  v.push_back({"probe_lut", (const void *)&probe_lut<5>, {P, I, I, P}, 5, -1});
+  v.push_back({"probe_lut", (const void *)&probe_lut<8>, {P, I, I, P}, 8, -1});
   v.push_back({"probe_stream", (const void *)&probe_stream, {P, I, I, P}, -1, -1});
 }
 
