@@ -263,6 +263,17 @@ def run_probes(eng, iters=4000):
                 "wave_cycles_per_weight_decode": round(cyc[0] / (iters * 8 * 512), 4),
                 **places,
             }
+            if K == 5:  # four chains per decoded tile pair (a 128-row grouped GEMM), accumulators in VGPRs / AGPRs
+                for ag in (0, 1):
+                    tx = {}
+                    for mode in (0, 1):
+                        kw = dict(fconsts=[(10, "u32", K), (16, "u32", ag)], tg_mem=4 * 8 * 64 * K)
+                        args = [tiles, np.int32(iters), np.int32(mode), res]
+                        eng.run_kernel("probe_x4", args, (grid, 1, 1), (256, 1, 1), **kw)
+                        tx[mode] = eng.run_kernel("probe_x4", args, (grid, 1, 1), (256, 1, 1), reps=3, **kw) / 3
+                    out[key][f"x4_{'agpr' if ag else 'vgpr'}"] = {
+                        "ms_chains": round(tx[0], 4), "ms_decode_chains": round(tx[1], 4),
+                        "vs_max": round(tx[1] / max(t[0], tx[0]), 3), "vs_sum": round(tx[1] / (t[0] + tx[0]), 3)}
             res.free()
             print(f"probe {key}: {out[key]}", file=sys.stderr, flush=True)
         # the same decode through a 64 KB LDS codebook table (probe_lut): one workgroup per CU of 4, 8 or 16 waves

@@ -201,6 +201,58 @@ __global__ __launch_bounds__(1024) void probe_lut(const uint8_t *tiles, int iter
   out[(blockIdx.x * (blockDim.x >> 6) + wave) * 64 + lane] = v;
 }
 
+
+// probe_x4<K, AG>: each decoded tile pair feeds four independent MFMA chains (the ratio of a 128-row grouped GEMM);
+// mode 0 the four chains alone (a fixed operand), mode 1 decode + chains. AG: the accumulators in AGPRs (the MFMA
+// written as inline asm with an "a" operand), else in VGPRs. Output as probe_mix.
+template <int K, bool AG>
+__global__ __launch_bounds__(256) void probe_x4(const uint8_t *tiles, int iters, int mode, uint32_t *out) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const uint8_t *slot = probe_stage<K>(tiles, lds);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  uint32_t h = 0;
+  const uint64_t t0 = __builtin_amdgcn_s_memtime(), r0 = __builtin_amdgcn_s_memrealtime();
+  f32x16 acc[4];
+#pragma unroll
+  for (int r = 0; r < 4; r++)
+#pragma unroll
+    for (int i = 0; i < 16; i++) acc[r][i] = 0.f;
+  f16x8 a, bfix;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    a[i] = (_Float16)(0.001f * (lane + i));
+    bfix[i] = (_Float16)(0.002f * (lane - i));
+  }
+  for (int it = 0; it < iters; it++) {
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int kt = 0; kt < kProbeTiles; kt++) {
+      f16x8 b = bfix;
+      if (mode == 1) {
+        b = decode_pair<K>(slot, kt);
+        const uint4 u = __builtin_bit_cast(uint4, b);
+        h ^= u.x ^ u.y ^ u.z ^ u.w;
+      }
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        if constexpr (AG)
+          asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+a"(acc[r]) : "v"(a), "v"(b));
+        else
+          acc[r] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc[r], 0, 0, 0);
+      }
+    }
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int r = 0; r < 4; r++)
+#pragma unroll
+    for (int i = 0; i < 16; i++) s += acc[r][i];
+  const uint32_t cyc = (uint32_t)(__builtin_amdgcn_s_memtime() - t0);
+  const uint32_t rt = (uint32_t)(__builtin_amdgcn_s_memrealtime() - r0);
+  const uint32_t v = lane == 1 ? cyc : lane == 4 ? rt : (h ^ __float_as_uint(s));
+  out[(blockIdx.x * 4 + wave) * 64 + lane] = v;
+}
+
 }  // namespace
 
 void init_probe_attrs() {
@@ -221,6 +273,8 @@ void probe_kernels(std::vector<KernelEntry> &v) {
   v.push_back({"probe_mix", (const void *)&probe_mix<8>, {P, I, I, P}, 8, -1});
   v.push_back({"probe_lut", (const void *)&probe_lut<5>, {P, I, I, P}, 5, -1});
   v.push_back({"probe_lut", (const void *)&probe_lut<8>, {P, I, I, P}, 8, -1});
+  v.push_back({"probe_x4", (const void *)&probe_x4<5, false>, {P, I, I, P}, 5, 0});
+  v.push_back({"probe_x4", (const void *)&probe_x4<5, true>, {P, I, I, P}, 5, 1});
   v.push_back({"probe_stream", (const void *)&probe_stream, {P, I, I, P}, -1, -1});
 }
 
