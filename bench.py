@@ -325,6 +325,39 @@ def measure_hc_read(eng, R, steps, seed, hid=2560, lr=320, K=6):
     return res
 
 
+TRACE_FIELDS = {0: "start", 1: "pre-route work done", 2: "route known", 3: "requests issued", 4: "gate/up chunks done",
+                5: "h blocks loaded", 6: "down partials stored", 7: "end", 8: "first routed tile in",
+                9: "last gate/up chunk done", 10: "down tiles decoded", 11: "prep suh requested", 12: "barrier 1",
+                13: "gate/up tiles requested", 14: "barrier 2", 15: "shared prep done", 16: "routed prep start",
+                18: "routed suh in", 24: "route: keys", 25: "route: sorted", 26: "route: top-k rounds",
+                27: "route: softmax"}
+
+
+def run_moe_trace(eng, layers, seed):
+    """The fused M=1 step's per-wave timeline (trace mode: IJAH_MOE_TRACE=1 before the layers exist; stamps kept in
+    LDS, written at the end of each launch): a `layers`-layer graph timed as bench does, then for the middle layer
+    the stamp of each step in us from the launch's first wave start, p0 / p50 / p100 over the waves that reach it."""
+    from ijah_amd import synth
+    lyr = [eng.moe_synth(2048, 512, 512, 10, 5, True, 5, seed=seed + 7919 * i) for i in range(layers)]
+    x = eng.from_numpy(synth.bf16_values(np.random.default_rng(seed), 1, 2048))
+    us = eng.moe_time(lyr, 1, x, warmup=2, reps=5)
+    out = np.zeros(8 * 65536, np.uint64)
+    eng.lib.ne_moe_read(lyr[layers // 2].ptr, b"trace", out.ctypes.data, out.nbytes)
+    t = out[: 256 * 16 * 32].astype(np.int64).reshape(256, 16, 32)
+    base = t[:, :, 0][t[:, :, 0] > 0].min()
+    rows = []
+    for f, name in TRACE_FIELDS.items():
+        m = t[:, :, f] > 0
+        if m.any():
+            v = (t[:, :, f][m] - base) / 100.0  # 100 MHz wall clock
+            rows.append((float(np.median(v)), name, round(float(v.min()), 2), round(float(np.median(v)), 2),
+                         round(float(v.max()), 2), int(m.sum())))
+    rows.sort()
+    for _, name, p0, p50, p100, n in rows:
+        print(f"{name:26s} {p0:7.2f} {p50:7.2f} {p100:7.2f}  waves={n}", flush=True)
+    return {"us_per_layer_traced": round(us, 3), "layers": layers}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -344,6 +377,8 @@ def main():
     ap.add_argument("--hc-only", action="store_true", help="only measure the hyper-connection read and exit")
     ap.add_argument("--batch-rows", type=int, default=0, metavar="R",
                     help="only measure the grouped matrix-core layer at R rows (a 4-layer graph) and exit")
+    ap.add_argument("--moe-trace", action="store_true",
+                    help="the fused M=1 step's per-wave timeline (trace mode), then exit")
     ap.add_argument("--probe", action="store_true",
                     help="only run the decode / matrix-core probes (decode cost per weight, MFMA and decode overlap)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MB",
@@ -355,6 +390,8 @@ def main():
         sys.exit(2)
 
     import ijah_amd
+    if a.moe_trace:
+        os.environ["IJAH_MOE_TRACE"] = "1"  # read when a layer is created
     eng = ijah_amd.load_engine()
     if a.copy_probe:
         n = a.copy_probe << 20
@@ -362,6 +399,9 @@ def main():
         for _ in range(5):
             eng.run_kernel("copy_u128", [src, dst, np.uint64(n // 16)], (2048, 1, 1), (256, 1, 1))
         print(json.dumps({"copy_probe_bytes": n, "launches": 5}), flush=True)
+        return
+    if a.moe_trace:
+        print(json.dumps(run_moe_trace(eng, 16, a.seed + 11)), flush=True)
         return
     if a.probe:
         print(json.dumps({"stream": run_stream_probe(eng), "stream96": run_stream_probe(eng, 96), **run_probes(eng)}),
