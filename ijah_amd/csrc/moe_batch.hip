@@ -287,7 +287,7 @@ __global__ __launch_bounds__(256) void bat_router_exact(MoeArgs a) {
 // ---------------------------------------------------------------------------------------------------- route
 // one wave per row
 template <int J>
-__device__ void route_one(const MoeArgs &a, int r) {
+__device__ void route_one(const MoeArgs &a, int r, uint32_t *lid = nullptr) {
   const int lane = threadIdx.x & 63;
   const float *lg = a.logits + (uint64_t)r * (a.ne + 1);
   const float sgl = a.has_sgate ? lg[a.ne] : 0.f;  // the shared-expert gate logit, requested with the others
@@ -328,6 +328,7 @@ __device__ void route_one(const MoeArgs &a, int r) {
   if (lane < a.topk) {
     a.route[(uint64_t)r * 2 * a.topk + lane] = id;
     a.route[(uint64_t)r * 2 * a.topk + a.topk + lane] = __float_as_uint(pk / sum);
+    if (lid) lid[r * a.topk + lane] = id;  // the caller's LDS copy of the ids
   }
   if (lane == 0) a.sgv[r] = moe_shared_gate(a, sgl);
 }
@@ -455,20 +456,19 @@ __global__ __launch_bounds__(1024) void bat_scan(MoeArgs a, uint32_t *bk, uint32
 // takes its row in its expert's list (rows[row] = r * nslot + k; the order inside an expert changes no result).
 __global__ __launch_bounds__(1024) void bat_route_place(MoeArgs a, uint32_t *bk, uint32_t *chunks, int max_chunks,
                                                         uint32_t crows, uint32_t *rows) {
-  __shared__ uint32_t sc[1024], cc[1024], offl[1024], cur[1024];
+  __shared__ uint32_t sc[1024], cc[1024], offl[1024], cur[1024], lid[1024];
   const int tid = threadIdx.x, wave = tid >> 6, n = a.ne + (a.nslot > a.topk ? 1 : 0);
-  for (int r = wave; r < a.R; r += 16) {
+  for (int r = wave; r < a.R; r += 16) {  // the route, its ids also kept in LDS for the counts and the placement
     if (a.ne <= 512)
-      route_one<8>(a, r);
+      route_one<8>(a, r, lid);
     else
-      route_one<16>(a, r);
+      route_one<16>(a, r, lid);
   }
   sc[tid] = 0u;
   cur[tid] = 0u;
-  __threadfence();
-  __syncthreads();  // the route is stored (read back below through L2)
+  __syncthreads();
   for (int s = tid; s < a.R * a.topk; s += 1024) {
-    const uint32_t e = ld_cg(a.route + (uint64_t)(s / a.topk) * 2 * a.topk + s % a.topk);
+    const uint32_t e = lid[s];
     atomicAdd(&sc[e < (uint32_t)a.ne ? e : 0u], 1u);
   }
   __syncthreads();
@@ -500,7 +500,7 @@ __global__ __launch_bounds__(1024) void bat_route_place(MoeArgs a, uint32_t *bk,
     const int r = s / a.nslot, k = s % a.nslot;
     uint32_t e = (uint32_t)a.ne, pos = (uint32_t)r;  // the shared expert's list is every token in order
     if (k < a.topk) {
-      e = ld_cg(a.route + (uint64_t)r * 2 * a.topk + k);
+      e = lid[r * a.topk + k];
       e = e < (uint32_t)a.ne ? e : 0u;
       pos = atomicAdd(&cur[e], 1u);
     }
@@ -1653,7 +1653,8 @@ void launch_moe_batch(const MoeArgs &a, const MoeBatchBufs &b, hipStream_t s) {
   const int KS = a.nslot > a.topk ? a.slay.K : a.lay.K;
   const bool few = moe_batch_exact(a) && b.vpart && moe_batch_few(a.R, a.hid, a.inter, a.lay.K, KS);
   if (few) {  // route, chunks and placement in one workgroup
-    IJ_CHECK(a.ne < 1024 && a.R * a.nslot <= 1024 * 32, "few-row MoE: %d experts", a.ne);
+    IJ_CHECK(a.ne < 1024 && a.R * a.nslot <= 1024 * 32 && a.R * a.topk <= 1024, "few-row MoE: %d experts, %d slots",
+             a.ne, a.R * a.topk);
     hipLaunchKernelGGL(bat_route_place, dim3(1), dim3(1024), 0, s, a, b.bk, b.chunks, b.max_chunks,
                        (uint32_t)kFewChunkRows, b.rows);
   } else {
