@@ -29,6 +29,7 @@
 #include <algorithm>
 
 #include "exl3_device.h"
+#include "ring_schedule.h"
 #include "kernels.h"
 #include "moe_device.h"
 
@@ -766,39 +767,10 @@ struct GemmIo {
   static_assert(NR == kChunkRows || (NR == 32 && LDS <= 53248), "three workgroups per CU at 32 rows");
   static_assert(RB % RA == 0 && DB > DA, "ring shapes");
 };
-// Issue order: prologue A(0) B(0) A(1) B(1) .. A(DA-1) B(DA-1) B(DA) .. B(DB-1); step j then issues A(j + DA) and
-// B(j + DB) (while < NS). Returns how many requests were issued after A(t) and B(t), counted at step t before it
-// issues: the s_waitcnt vmcnt that makes both complete (completion is in issue order).
-template <int OA, int OB, int DA, int DB>
-__host__ __device__ constexpr int after_step(int t, int NS) {
-  auto mn = [](int x, int y) { return x < y ? x : y; };
-  auto mx = [](int x, int y) { return x > y ? x : y; };
-  auto sum_ops = [&](int n) { return OA * mn(n, mx(NS - DA, 0)) + OB * mn(n, mx(NS - DB, 0)); };
-  const int pa = mn(DA, NS), pb = mn(DB, NS);
-  const int prologue = OA * pa + OB * pb;
-  const int total = prologue + sum_ops(t);
-  int last = 0;  // one past the position of the later of A(t), B(t)
-  if (t < DA) {
-    last = (OA + OB) * (t + 1);
-  } else if (t < DB) {
-    last = mx(prologue + sum_ops(t - DA) + OA, (OA + OB) * pa + OB * (t - pa) + OB);
-  } else {
-    last = mx(prologue + sum_ops(t - DA) + OA, prologue + sum_ops(t - DB) + ((t - DB) + DA < NS ? OA : 0) + OB);
-  }
-  return total - last;
-}
-// the count of steps t with DB <= t and t + DB < NS (both streams still issuing): A(t) is the later request,
-// followed by B(t - DA + DB) and DA - 1 full steps
-template <int OA, int OB, int DA>
-constexpr int kAfterSteady = OB + (DA - 1) * (OA + OB);
-static_assert(after_step<2, 1, 2, 5>(5, 1000) == kAfterSteady<2, 1, 2> &&
-                  after_step<1, 1, 2, 5>(9, 1000) == kAfterSteady<1, 1, 2> &&
-                  after_step<2, 1, 1, 3>(7, 1000) == kAfterSteady<2, 1, 1>,
-              "steady-state wait count");
 template <int OA, int OB, int DA, int DB>
 __device__ __forceinline__ void wait_step(int t, int NS) {
   static_assert(kAfterSteady<OA, OB, DA> <= 15, "vmcnt immediate");
-  if (t >= DB && t + DB < NS)
+  if (steady_step<DB>(t, NS))
     __builtin_amdgcn_s_waitcnt(0x0F70 | kAfterSteady<OA, OB, DA>);
   else
     wait_vm15(after_step<OA, OB, DA, DB>(t, NS));
