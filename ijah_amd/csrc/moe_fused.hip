@@ -349,6 +349,7 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
   __shared__ float csum[kMaxGT][kGrp][32];                                 // k chunk sums of the gate/up tasks
   __shared__ uint32_t tcnt[kMaxGT];                                        // chunk sums of each task in LDS
   __shared__ uint32_t s_prep;                                              // prep chunks ready: routed bits 0-7, shared 8-11
+  __shared__ uint32_t s_hrdy;  // h sums loaded: bit 2 h slot + proj; h block ready: bit 8 + h slot
   __shared__ __attribute__((aligned(16))) uint16_t hvec[kMaxH][3][128];   // svh_g, svh_u, suh_d of each h block
   __shared__ __attribute__((aligned(16))) uint16_t csv[kMaxTopkV + 1][128]; // the combine's svh_d per slot
   __shared__ __attribute__((aligned(16))) float xl[HID];                    // the input row (staged at launch)
@@ -400,6 +401,7 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
   if (threadIdx.x == 0) s_ok = 1;
   if (threadIdx.x < kMaxGT) tcnt[threadIdx.x] = 0;
   if (threadIdx.x == 0) s_prep = 0;
+  if (threadIdx.x == 0) s_hrdy = 0;
   uint32_t ep_lo = (uint32_t)ep;
   asm volatile("" : "+v"(ep_lo));  // its first use here, after the plan words' request (not at the branch's end)
   if (wave == kCtl && lane == 0) s_tag = ep_lo + 1u;
@@ -546,18 +548,26 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
   // chunks, its k chunks and its down unit's B operands; then the routed prep (suh chunk -> fp16(H(x suh)) in kp
   // order, x from LDS: a global load now would wait for the tile streams)
   wait_vm(nops);  // the requests issued before the route
-  // a prep chunk is announced by its bit in s_prep (after its LDS writes); a wave waits only for the chunks it reads
-  auto prep_ready = [&](uint32_t bit) {
+  // LDS flags (bits of s_prep, s_hrdy): a producer sets its bit after its LDS writes; a consumer waits only for the
+  // bits it reads (bounded: a wait that never ends marks the launch invalid)
+  auto flag_set = [&](uint32_t *w, uint32_t bit) {
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    if (lane == 0) atomicOr(&s_prep, bit);
+    if (lane == 0) atomicOr(w, bit);
   };
-  auto prep_wait = [&](uint32_t bit) {
+  auto flag_wait = [&](uint32_t *w, uint32_t bits) {
+    bool got = false;
     for (uint32_t it = 0; it < kSpin; it++) {
-      if (__hip_atomic_load(&s_prep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) & bit) break;
+      if ((__hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) & bits) == bits) {
+        got = true;
+        break;
+      }
       __builtin_amdgcn_s_sleep(1);
     }
+    if (!got && lane == 0) atomicOr(a.sync + kWordErr, 1u);
     asm volatile("" ::: "memory");
   };
+  auto prep_ready = [&](uint32_t bit) { flag_set(&s_prep, bit); };
+  auto prep_wait = [&](uint32_t bit) { flag_wait(&s_prep, bit); };
   if (sprep_w) {
     prep_chunk<HH>(xl, (int)(spk % NKG) * kGrp + (wave - kSpw), sprep[wave - kSpw], sch);
     prep_ready(1u << (8 + wave - kSpw));
@@ -567,6 +577,9 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
   // operands while the routed tiles are on their way, then the routed ones as their tiles arrive; each chunk's sum
   // into LDS, and the fold of a task's chunk sums in k order by the wave completing it
   stamp_x(a, 0);
+  // the gate/up k chunks feed every workgroup's h blocks (the step's critical path): their waves go first on their
+  // SIMDs; the down units' decode, which waits for the h blocks anyway, yields to them
+  __builtin_amdgcn_s_setprio(2);
   if (n_su) {
     wait_vm(nops - end_su);
     stamp_x(a, 2);
@@ -618,6 +631,7 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
       fst = false;
     }
   }
+  __builtin_amdgcn_s_setprio(0);
   stamp_w(a, 1);
   stamp(a, 4);
 
@@ -663,11 +677,12 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
       st_cg(gu + lane, s0);
       st_cg(gu + lane + 64, s1);
     }
+    flag_set(&s_hrdy, 1u << wave);
   }
   stamp(a, 5);
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): every wave's LDS prefetches (svh / suh vectors) have landed
-  lds_barrier();
   if (ok && wave < nh) {  // the down prologue of h block `wave` (reference kernels/fn_moe.metal:370-384)
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's svh_g / svh_u / suh_d prefetches have landed
+    flag_wait(&s_hrdy, 3u << (2 * wave));  // its gate and up sums
     const uint16_t *svg = hvec[wave][0], *svu = hvec[wave][1], *sud = hvec[wave][2];
     float g0v = hsum[wave][0][lane], g1v = hsum[wave][0][lane + 64];
     float u0v = hsum[wave][1][lane], u1v = hsum[wave][1][lane + 64];
@@ -682,10 +697,11 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
     fwht2(h0, h1, lane, HI, sci);
     hl[wave][kp(lane)] = to_f16(h0);
     hl[wave][kp(lane + 64)] = to_f16(h1);
+    flag_set(&s_hrdy, 1u << (8 + wave));
   }
-  lds_barrier();
   // ---- 5. down: 8 k tiles of h against the unit's decoded tiles; one tagged partial per unit
   if (ok && dunit >= 0) {
+    flag_wait(&s_hrdy, 1u << (8 + dhs));  // its h block
     f32x16 d;
     zero16(d);
     const _Float16 *ha = &hl[dhs][0] + 8 * (lane >> 5);
@@ -729,6 +745,7 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
       if ((it & 15u) == 15u && ld_relaxed(a.sync + kWordErr)) break;
     }
     if (!got) atomicOr(a.sync + kWordErr, 1u);
+    lds_barrier();  // every wave is past its decodes: the tiles' LDS is free for the combine
 #pragma unroll
     for (int q = 0; q < 3; q++)
       if (g + 8 * q < a.nslot) cv[(g + 8 * q) * 128 + o] = sv[q];
