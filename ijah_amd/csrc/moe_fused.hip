@@ -646,6 +646,7 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
   // h loaders: the first 2 nh waves, which the SIMDs serve first (oldest first); wave (h slot, proj), lane: columns
   // o = lane, lane + 64 of the block
   if (ok && wave < 2 * nh) {
+    __builtin_amdgcn_s_setprio(1);  // the h path comes before the down decode of other waves on this SIMD
     const int hslot = wave >> 1, proj = wave & 1;
     const uint32_t hb = PL(P_HB + hslot) & 0x7FFFFFFFu;
     const int ls = (int)(hb / NBI), cb = (int)(hb % NBI);
@@ -699,6 +700,7 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
     hl[wave][kp(lane + 64)] = to_f16(h1);
     flag_set(&s_hrdy, 1u << (8 + wave));
   }
+  __builtin_amdgcn_s_setprio(0);
   // ---- 5. down: 8 k tiles of h against the unit's decoded tiles; one tagged partial per unit
   if (ok && dunit >= 0) {
     flag_wait(&s_hrdy, 1u << (8 + dhs));  // its h block
