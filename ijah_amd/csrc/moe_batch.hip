@@ -1504,6 +1504,9 @@ __global__ __launch_bounds__(256) void bat_dn_blk(MoeArgs a, const uint32_t *bk,
 namespace {
 template <int K, int KS, bool TR, int NR, bool EX = false>
 void launch_gemms_as(const MoeArgs &a, const MoeBatchBufs &b, hipStream_t s) {
+  // chunk_gemm runs k in steps of 2 tiles: an odd tile count would drop the last tile
+  IJ_CHECK(a.hid % 32 == 0 && a.inter % 32 == 0, "grouped GEMM: k tiles must be even (hid %d, inter %d)", a.hid,
+           a.inter);
   // the routed (K) and shared (KS) chunks use ring layouts of their own widths: room for the larger of each
   const size_t lg = std::max(GemmIo<K, 2, NR>::LDS, GemmIo<KS, 2, NR>::LDS);
   const size_t ld = std::max(GemmIo<K, 1, NR>::LDS, GemmIo<KS, 1, NR>::LDS);
