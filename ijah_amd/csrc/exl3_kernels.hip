@@ -587,42 +587,60 @@ __global__ __launch_bounds__(64) void lin_prep(LinArgs a) {
 // The finished outputs of 128-column block cb for row r: the k group partials folded left in k order, H_out, svh, the
 // epilogue (reference kernels/trunk6/trunk6.metal:199-214, t6_finish). coherent: the partials were stored by other
 // workgroups of this launch (device-coherent loads); else by an earlier launch.
-__device__ void lin_finish_row(const LinArgs &a, int r, int cb, bool coherent) {
+// Rows r0, r0 + rs, .. (NR of them, those below R) of output block cb: each row's k-group partials folded left in
+// group order, H_out, svh and the epilogue. The partials of all NR rows are requested together (rounds of 8 groups
+// for one row, 4 for several), so a wave finishing several rows pays one round trip per round, not one per row.
+template <int NR>
+__device__ void lin_finish_rows(const LinArgs &a, int r0, int rs, int cb, bool coherent) {
   const int lane = threadIdx.x & 63, OTp = a.OT + (a.OT & 1);
   const int i0 = cb * 128 + lane, i1 = i0 + 64;
   const bool m0 = i0 < a.out, m1 = i1 < a.out;
   const int j0 = m0 ? i0 : 0, j1 = m1 ? i1 : 0;
-  float v0 = 0.f, v1 = 0.f;
-  constexpr int B = 8;  // groups requested together (one round trip per 8)
+  float v0[NR], v1[NR];
+#pragma unroll
+  for (int q = 0; q < NR; q++) v0[q] = v1[q] = 0.f;
+  constexpr int B = NR == 1 ? 8 : 4;  // groups requested together (2 NR B values in flight per lane)
   for (int g0 = 0; g0 < a.S; g0 += B) {
-    float t0[B], t1[B];
-    if (coherent) {
+    float t0[NR][B], t1[NR][B];
+#pragma unroll
+    for (int q = 0; q < NR; q++) {
+      const int r = min(r0 + q * rs, a.R - 1);
 #pragma unroll
       for (int j = 0; j < B; j++) {
         const float *pp = a.part + ((uint64_t)min(g0 + j, a.S - 1) * a.R + r) * OTp * 16;
-        t0[j] = ld_cg(pp + j0);
-        t1[j] = ld_cg(pp + j1);
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < B; j++) {
-        const float *pp = a.part + ((uint64_t)min(g0 + j, a.S - 1) * a.R + r) * OTp * 16;
-        t0[j] = pp[j0];
-        t1[j] = pp[j1];
+        t0[q][j] = coherent ? ld_cg(pp + j0) : pp[j0];
+        t1[q][j] = coherent ? ld_cg(pp + j1) : pp[j1];
       }
     }
 #pragma unroll
-    for (int j = 0; j < B; j++)
-      if (g0 + j < a.S) {
-        v0 = g0 + j == 0 ? t0[j] : v0 + t0[j];
-        v1 = g0 + j == 0 ? t1[j] : v1 + t1[j];
-      }
+    for (int q = 0; q < NR; q++)
+#pragma unroll
+      for (int j = 0; j < B; j++)
+        if (g0 + j < a.S) {
+          v0[q] = g0 + j == 0 ? t0[q][j] : v0[q] + t0[q][j];
+          v1[q] = g0 + j == 0 ? t1[q][j] : v1[q] + t1[q][j];
+        }
   }
-  v0 = m0 ? v0 : 0.f;
-  v1 = m1 ? v1 : 0.f;
-  fwht2(v0, v1, lane, a.had_out, a.sc_out);
-  if (m0) lin_store(a, r, i0, v0 * h2f(a.svh[i0]));
-  if (m1) lin_store(a, r, i1, v1 * h2f(a.svh[i1]));
+#pragma unroll
+  for (int q = 0; q < NR; q++) {
+    const int r = r0 + q * rs;
+    if (r >= a.R) break;
+    float w0 = m0 ? v0[q] : 0.f, w1 = m1 ? v1[q] : 0.f;
+    fwht2(w0, w1, lane, a.had_out, a.sc_out);
+    if (m0) lin_store(a, r, i0, w0 * h2f(a.svh[i0]));
+    if (m1) lin_store(a, r, i1, w1 * h2f(a.svh[i1]));
+  }
+}
+__device__ void lin_finish_row(const LinArgs &a, int r, int cb, bool coherent) {
+  lin_finish_rows<1>(a, r, 1, cb, coherent);
+}
+// the block's rows over the workgroup's 4 waves (wave c: rows c, c + 4, ..), four rows per request round
+__device__ void lin_finish_block(const LinArgs &a, int c, int cb) {
+  if (a.R <= 4) {
+    if (c < a.R) lin_finish_rows<1>(a, c, 4, cb, true);
+  } else {
+    for (int r = c; r < a.R; r += 16) lin_finish_rows<4>(a, r, 4, cb, true);
+  }
 }
 
 // lin_mx: up to kLinMulti linears at R <= 32 rows in one launch, on the matrix cores (reference
@@ -744,7 +762,7 @@ __global__ __launch_bounds__(256) void lin_mx(LinMulti m) {
   uint32_t *ctr = a.cnt + (uint64_t)cb * kSyncStride;
   if (block_signal(ctr, &flag) != (uint32_t)(npb * a.S - 1)) return;
   if (threadIdx.x == 0) st_cg(ctr, 0u);
-  for (int r = c; r < R; r += 4) lin_finish_row(a, r, cb, true);
+  lin_finish_block(a, c, cb);
   if (a.epi.kind == 8)
     hc_fin_block(a, a.epi.ctr + (uint64_t)(cb % (a.epi.hid / 128)) * kSyncStride, a.epi.row0, a.epi.row0 + R, cb,
                  &flag);
@@ -835,7 +853,7 @@ __global__ __launch_bounds__(256) void lin_mxl(LinMulti m) {
   uint32_t *ctr = a.cnt + (uint64_t)cb * kSyncStride;
   if (block_signal(ctr, &flag) != (uint32_t)(npb - 1)) return;
   if (threadIdx.x == 0) st_cg(ctr, 0u);
-  for (int r = c; r < R; r += 4) lin_finish_row(a, r, cb, true);
+  lin_finish_block(a, c, cb);
   if (a.epi.kind == 8)
     hc_fin_block(a, a.epi.ctr + (uint64_t)(cb % (a.epi.hid / 128)) * kSyncStride, a.epi.row0, a.epi.row0 + R, cb,
                  &flag);
