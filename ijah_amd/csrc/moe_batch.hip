@@ -1430,16 +1430,17 @@ __global__ __launch_bounds__(256) void bat_gu_grp(MoeArgs a, const uint32_t *bk,
   }
 }
 
-// LDS: per wave its pair's k tile pairs (all of inter), then the chunk's RT rows of hh (inter halves each), then the
-// [RT][128] outputs
+// LDS: per wave two buffers of one k chunk (8 k tile pairs at the larger K), then the chunk's RT rows of hh (inter
+// halves each), then the [RT][128] outputs (about 26 KB at K5, inter 512: six workgroups per CU)
 template <int KM, int RT>
 __host__ __device__ constexpr uint32_t v_dn_lds(int inter) {
-  return 4u * (uint32_t)(inter / 16) * 64 * KM + (uint32_t)RT * inter * 2 + RT * 128 * 4;
+  return 4u * 2u * kVChunk * 64 * KM + (uint32_t)RT * inter * 2 + RT * 128 * 4;
 }
 template <int K, int KS, int RT>
 __global__ __launch_bounds__(256) void bat_dn_blk(MoeArgs a, const uint32_t *bk, const uint32_t *chunks,
                                                   const uint32_t *rows, const uint16_t *hh, float *dnw) {
   constexpr int KM = K > KS ? K : KS;
+  constexpr uint32_t kBuf = kVChunk * 64 * KM;  // one k chunk's LDS buffer
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int NBLK = a.hid / 128, ITd = a.inter / 16, ch = (int)blockIdx.x / NBLK, cblk = (int)blockIdx.x % NBLK;
   if (ch >= (int)bk[3 * (a.ne + 1)]) return;
@@ -1447,13 +1448,13 @@ __global__ __launch_bounds__(256) void bat_dn_blk(MoeArgs a, const uint32_t *bk,
   const int lane = threadIdx.x & 63, q = (int)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6), p = cblk * 4 + q;
   const bool sh = e >= a.ne;
   const int KE = sh ? KS : K;
-  const uint32_t wb = (uint32_t)ITd * 64 * KM;
-  uint8_t *tl = lds + q * wb;
-  _Float16 *xs = (_Float16 *)(lds + 4 * wb);
-  float *ot = (float *)(lds + 4 * wb + RT * a.inter * 2);
+  uint8_t *tl = lds + q * 2 * kBuf;  // this wave's two chunk buffers
+  _Float16 *xs = (_Float16 *)(lds + 4 * 2 * kBuf);
+  float *ot = (float *)(lds + 4 * 2 * kBuf + RT * a.inter * 2);
   const uint8_t *blk = expert_block(a, e);
   // each row's slot (token, k) and route weight; then the rows of hh (nrows x inter halves, contiguous; 1 KB per
-  // request, spread over the 4 waves), then the wave's tiles: the k chunks arrive in order while earlier ones decode
+  // request, spread over the 4 waves), then the wave's first two k chunks; each later chunk is requested into the
+  // buffer its chunk two before has left, so the next chunk is in flight while one decodes
   const uint32_t sl = lane < nrows ? rows[row0 + lane] : 0u;
   {
     const uint32_t rb = (uint32_t)nrows * a.inter * 2;
@@ -1461,24 +1462,29 @@ __global__ __launch_bounds__(256) void bat_dn_blk(MoeArgs a, const uint32_t *bk,
     for (uint32_t o = (uint32_t)q * 1024; o < rb; o += 4096)
       if (o + (uint32_t)lane * 16 < rb) dma16(hs + o + lane * 16, (uint8_t *)xs + o);
   }
-  const uint32_t cbytes = kVChunk * 64 * KE, bytes = (uint32_t)ITd * 64 * KE;
-  const int nops = (int)((bytes + 1023) / 1024);
-  {
-    const uint8_t *src = blk + tr_of(a, e, 2) + (uint64_t)p * ITd * 64 * KE;
-    for (uint32_t o = 0; o < bytes; o += 1024)
-      if (o + (uint32_t)lane * 16 < bytes) dma16(src + o + lane * 16, tl + o);
-  }
-  wait_vm15(nops);  // this wave's rows of hh are in
-  __syncthreads();  // every wave's
+  const uint32_t cbytes = kVChunk * 64 * KE;
+  const int cops = (int)((cbytes + 1023) / 1024), NC = ITd / kVChunk;
+  const uint8_t *src = blk + tr_of(a, e, 2) + (uint64_t)p * ITd * 64 * KE;
+  auto stage = [&](int cc) {
+    for (uint32_t o = 0; o < cbytes; o += 1024)
+      if (o + (uint32_t)lane * 16 < cbytes) dma16(src + (uint64_t)cc * cbytes + o + lane * 16, tl + (cc & 1) * kBuf + o);
+  };
+  stage(0);
+  if (NC > 1) stage(1);
+  wait_vm15(NC > 1 ? 2 * cops : cops);  // this wave's rows of hh are in
+  __syncthreads();                      // every wave's
   f32x16 s;
-  for (int cc = 0; cc < ITd / kVChunk; cc++) {  // the k chunks of inter, folded left
-    wait_vm15(nops - (int)(((uint32_t)(cc + 1) * cbytes + 1023) / 1024));  // chunk cc's tiles are in
-    f32x16 acc = (sh && KS != K) ? v_chain<KS, RT>(tl + cc * kVChunk * 64 * KS, xs + cc * kVChunk * 16, a.inter,
-                                                   kVChunk, nrows)
-                                 : v_chain<K, RT>(tl + cc * kVChunk * 64 * K, xs + cc * kVChunk * 16, a.inter,
-                                                  kVChunk, nrows);
+  for (int cc = 0; cc < NC; cc++) {  // the k chunks of inter, folded left
+    wait_vm15(cc + 1 < NC ? cops : 0);  // chunk cc's tiles are in (chunk cc + 1's may not be)
+    const uint8_t *tb = tl + (cc & 1) * kBuf;
+    f32x16 acc = (sh && KS != K) ? v_chain<KS, RT>(tb, xs + cc * kVChunk * 16, a.inter, kVChunk, nrows)
+                                 : v_chain<K, RT>(tb, xs + cc * kVChunk * 16, a.inter, kVChunk, nrows);
 #pragma unroll
     for (int i = 0; i < 16; i++) s[i] = cc == 0 ? acc[i] : s[i] + acc[i];
+    if (cc + 2 < NC) {
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this buffer's reads are done before it is refilled
+      stage(cc + 2);
+    }
   }
 #pragma unroll
   for (int i = 0; i < 16; i++) {
@@ -1589,8 +1595,8 @@ void init_batch_attrs() {
 
 // Few rows: every kernel keeps the one-row step's arithmetic (hidden size a multiple of 512 for its router rows)
 bool moe_batch_exact(const MoeArgs &a) { return a.R <= 32 && a.hid % 512 == 0; }
-static size_t v_dn_bytes(int inter, int KM) {
-  return 4ull * (inter / 16) * 64 * KM + (size_t)kFewChunkRows * inter * 2 + (size_t)kFewChunkRows * 128 * 4;
+static size_t v_dn_bytes(int inter, int KM) {  // bat_dn_blk's LDS (v_dn_lds at run-time K)
+  return 4ull * 2 * kVChunk * 64 * KM + (size_t)kFewChunkRows * inter * 2 + (size_t)kFewChunkRows * 128 * 4;
 }
 bool moe_batch_few(int R, int hid, int inter, int K, int KS) {
   return R <= 32 && hid % 512 == 0 && hid / 512 <= kFewMaxGroups && v_dn_bytes(inter, std::max(K, KS)) <= 160 * 1024;
