@@ -1326,8 +1326,12 @@ __device__ __forceinline__ f32x16 v_chain(const uint8_t *tl, const _Float16 *xs,
 // buffers per wave (the next k group's requests in flight while this one decodes)
 template <int KM, int RT>
 constexpr uint32_t v_gu_wave() { return kVChunk * 64 * KM + RT * 256; }
+// (the chunk sums of every group stay in registers through the k loop, then go to the wave's own buffers)
 template <int KM, int RT>
-constexpr uint32_t v_gu_lds(int G) { return 8 * v_gu_wave<KM, RT>() + (uint32_t)G * 4 * RT * 32 * 4; }
+constexpr uint32_t v_gu_lds(int G) {
+  static_assert(2 * v_gu_wave<KM, RT>() >= kFewMaxGroups * RT * 32 * 4, "a wave's chunk sums fit its buffers");
+  return 8 * v_gu_wave<KM, RT>() + 0 * G;
+}
 
 template <int K, int KS, int RT>
 __global__ __launch_bounds__(256) void bat_gu_grp(MoeArgs a, const uint32_t *bk, const uint32_t *chunks,
@@ -1342,7 +1346,9 @@ __global__ __launch_bounds__(256) void bat_gu_grp(MoeArgs a, const uint32_t *bk,
   const int lane = threadIdx.x & 63, c = (int)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const bool sh = e >= a.ne;
   const int KE = sh ? KS : K;
-  float *csum = (float *)(lds + 8 * v_gu_wave<KM, RT>());  // [k group][4 chunks][RT][32]
+  // after the k loop: wave c's chunk sums [k group][RT][32] at the start of its own two buffers
+  auto csum_at = [&](int cw) { return (float *)(lds + 2 * cw * v_gu_wave<KM, RT>()); };
+  float cs[kFewMaxGroups][4];  // this wave's chunk sum of each group: rows 0..3 of its 32 columns (lanes 0-31)
   __shared__ int flag;
   uint32_t *ctr = epochs + ((uint64_t)ch * NBI + cb) * kSyncStride;
   float *pf = (float *)part;
@@ -1379,12 +1385,23 @@ __global__ __launch_bounds__(256) void bat_gu_grp(MoeArgs a, const uint32_t *bk,
       acc = v_chain<KS, RT>(tl, xs, 128, nkt, nrows);
     else
       acc = v_chain<K, RT>(tl, xs, 128, nkt, nrows);
+    static_assert(RT <= 4, "rows 0..3 of the product: values 0..3 of lanes 0-31");
 #pragma unroll
-    for (int i = 0; i < 16; i++) {
-      const int r = 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
-      if (r < RT && r < nrows) csum[((g * 4 + c) * RT + r) * 32 + (lane & 31)] = acc[i];
-    }
+    for (int gg = 0; gg < kFewMaxGroups; gg++)  // a compile-time register index
+      if (gg == g)
+#pragma unroll
+        for (int i = 0; i < 4; i++) cs[gg][i] = acc[i];
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this group's buffer reads are done before it is refilled
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // every request of this wave has landed: its buffers are free
+  {
+    float *mine = csum_at(c);
+#pragma unroll
+    for (int gg = 0; gg < kFewMaxGroups; gg++)
+      if (gg < G && lane < 32)
+#pragma unroll
+        for (int r = 0; r < RT; r++)
+          if (r < nrows) mine[(gg * RT + r) * 32 + lane] = cs[gg][r];
   }
   __syncthreads();
   // per (row, column): the chunks of each group folded left, the groups folded left
@@ -1393,8 +1410,8 @@ __global__ __launch_bounds__(256) void bat_gu_grp(MoeArgs a, const uint32_t *bk,
   if (ent < nrows * 32)
     for (int g = 0; g < G; g++) {
       const int nc = (min(32, IT - g * 32) + kVChunk - 1) / kVChunk;
-      float v = csum[(g * 4) * RT * 32 + ent];
-      for (int cc = 1; cc < nc; cc++) v = v + csum[(g * 4 + cc) * RT * 32 + ent];
+      float v = csum_at(0)[g * RT * 32 + ent];
+      for (int cc = 1; cc < nc; cc++) v = v + csum_at(cc)[g * RT * 32 + ent];
       tot = g == 0 ? v : tot + v;
     }
   if (ent < nrows * 32)
