@@ -474,17 +474,37 @@ __global__ __launch_bounds__(1024) void bat_route_place(MoeArgs a, uint32_t *bk,
   }
   __syncthreads();
   const uint32_t c = tid < a.ne ? sc[tid] : (tid < n ? (uint32_t)a.R : 0u);  // the shared expert takes every row
-  __syncthreads();
-  sc[tid] = c;
-  cc[tid] = (c + crows - 1) / crows;
-  __syncthreads();
-  for (int d = 1; d < 1024; d <<= 1) {  // inclusive Hillis-Steele scans of rows and chunks
-    const uint32_t v = tid >= d ? sc[tid - d] : 0u, w = tid >= d ? cc[tid - d] : 0u;
-    __syncthreads();
-    sc[tid] += v;
-    cc[tid] += w;
-    __syncthreads();
+  // inclusive scans of rows and chunks: within each wave by lane shifts, then the 16 wave totals by wave 0
+  const int lane = tid & 63;
+  uint32_t sv = c, cv = (c + crows - 1) / crows;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const uint32_t v = (uint32_t)__shfl_up((int)sv, d, 64), w = (uint32_t)__shfl_up((int)cv, d, 64);
+    if (lane >= d) {
+      sv += v;
+      cv += w;
+    }
   }
+  __shared__ uint32_t wsum[2][16];
+  if (lane == 63) {
+    wsum[0][wave] = sv;
+    wsum[1][wave] = cv;
+  }
+  __syncthreads();
+  if (wave == 0 && lane < 32) {  // lanes 0-15: the rows' wave totals; 16-31: the chunks'
+    const int t = lane & 15, arr = lane >> 4;
+    uint32_t x = wsum[arr][t];
+#pragma unroll
+    for (int d = 1; d < 16; d <<= 1) {
+      const uint32_t v = (uint32_t)__shfl_up((int)x, d, 16);
+      if (t >= d) x += v;
+    }
+    wsum[arr][t] = x;  // inclusive over waves
+  }
+  __syncthreads();
+  sc[tid] = sv + (wave > 0 ? wsum[0][wave - 1] : 0u);
+  cc[tid] = cv + (wave > 0 ? wsum[1][wave - 1] : 0u);
+  __syncthreads();
   if (tid < n) {
     const uint32_t off = sc[tid] - c, ch0 = cc[tid] - (c + crows - 1) / crows;
     offl[tid] = off;
