@@ -21,6 +21,11 @@
 //   combine  16 workgroups, one per 128-column output block: per slot the cb partials in order, H, svh_d, the route
 //            weight; the slots in slot order (the shared one last); the hyper-connection write when asked.
 // The launch tag comes from a u64 epoch that workgroup 0 advances at its end with one store.
+// Inside a workgroup, waves meet at barriers only where every wave's data is needed (the epoch, the route, the order
+// of the requests, the combine); elsewhere an LDS flag bit per producer (prepared input chunks, h sums, h blocks) or
+// a per-task LDS counter (the wave completing a task's fourth k chunk folds it) lets a wave wait only for what it
+// reads. The gate/up k chunks, which every workgroup's h blocks wait for, run at raised wave priority; the down
+// units' decode yields to them.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
