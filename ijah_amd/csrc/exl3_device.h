@@ -262,6 +262,25 @@ __device__ __forceinline__ f16x8 decode_pair(const uint8_t *tl, int kt) {
   decode4<K>(w1, B.g1.sh, l1, h1);
   return f16x8{l0.x, l0.y, h0.x, h0.y, l1.x, l1.y, h1.x, h1.y};
 }
+// One MFMA chain over the first nkt (<= NT) tile pairs staged at tl, onto acc; xa: the lane's A operand of tile 0
+// (tile kt at xa + 16 kt). A full chunk takes a branch-free path, so the tiles' LDS reads can be issued ahead of the
+// decode; the products and their order are the same on both paths.
+template <int K, int NT>
+__device__ __forceinline__ f32x16 mfma_chunk(const uint8_t *tl, const _Float16 *xa, int nkt, f32x16 acc) {
+  if (nkt == NT) {
+#pragma unroll
+    for (int kt = 0; kt < NT; kt++)
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const f16x8 *)(xa + kt * 16), decode_pair<K>(tl, kt), acc, 0, 0,
+                                                   0);
+    return acc;
+  }
+#pragma unroll
+  for (int kt = 0; kt < NT; kt++)
+    if (kt < nkt)
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const f16x8 *)(xa + kt * 16), decode_pair<K>(tl, kt), acc, 0, 0,
+                                                   0);
+  return acc;
+}
 __device__ __forceinline__ float dot4(f16x2 a, f16x2 b, f16x4 x, float acc) {
   acc = __builtin_amdgcn_fdot2(a, f16x2{x.x, x.y}, acc, false);
   return __builtin_amdgcn_fdot2(b, f16x2{x.z, x.w}, acc, false);

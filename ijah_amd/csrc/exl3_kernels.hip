@@ -734,13 +734,7 @@ __global__ __launch_bounds__(256) void lin_mx(LinMulti m) {
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the tiles (and rows) are in LDS
     // 2. the chunk's chain on the matrix cores
     const _Float16 *xa = xs + min(lane & 31, R - 1) * 128 + 8 * (lane >> 5);
-#pragma unroll
-    for (int kt = 0; kt < kLinChunkKt; kt++)
-      if (kt < nkt) {
-        const f16x8 bv = decode_pair<K>(tl, kt);
-        const f16x8 av = *(const f16x8 *)(xa + kt * 16);
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bv, acc, 0, 0, 0);
-      }
+    acc = mfma_chunk<K, kLinChunkKt>(tl, xa, nkt, acc);
   }
   // 3. chunk sums (lane (n, h), value i: row 8 (i / 4) + 4 h + i % 4, column n) -> LDS; the group's fold -> partials
 #pragma unroll
@@ -823,13 +817,7 @@ __global__ __launch_bounds__(256) void lin_mxl(LinMulti m) {
     f32x16 acc;
 #pragma unroll
     for (int i = 0; i < 16; i++) acc[i] = 0.f;
-#pragma unroll
-    for (int kt = 0; kt < kLinChunkKt; kt++)
-      if (kt < nkt) {
-        const f16x8 bv = decode_pair<K>(tl, kt);
-        const f16x8 av = *(const f16x8 *)(xa + kt * 16);
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bv, acc, 0, 0, 0);
-      }
+    acc = mfma_chunk<K, kLinChunkKt>(tl, xa, nkt, acc);
 #pragma unroll
     for (int i = 0; i < 16; i++) {
       const int r = 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);

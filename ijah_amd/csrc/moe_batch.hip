@@ -1333,13 +1333,7 @@ __device__ __forceinline__ f32x16 v_chain(const uint8_t *tl, const _Float16 *xs,
   f32x16 acc;
 #pragma unroll
   for (int i = 0; i < 16; i++) acc[i] = 0.f;
-#pragma unroll
-  for (int kt = 0; kt < kVChunk; kt++)
-    if (kt < nkt) {
-      const f16x8 bv = decode_pair<KD>(tl, kt);
-      const f16x8 av = *(const f16x8 *)(xa + kt * 16);
-      acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bv, acc, 0, 0, 0);
-    }
+  acc = mfma_chunk<KD, kVChunk>(tl, xa, nkt, acc);
   return acc;
 }
 // bytes staged per wave and buffer: 8 k tile pairs at the larger K, then RT rows of the chunk (128 halves each); two
