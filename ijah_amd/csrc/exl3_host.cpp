@@ -82,6 +82,8 @@ struct ne_exl3_lin {
   bool prep_launch(int R) const { return (long)(OTp / 2) * R > 256; }
   // many tile pairs (a vocabulary head): one workgroup per pair loops over the k groups (same results)
   bool k_loop(int R) const { return OTp / 2 >= 2048 && groups() <= 16 && R <= 4 && prep_launch(R); }
+  // the same linears at 5..32 rows: 8 tile pairs per workgroup share each k chunk's staged rows (same results)
+  bool k_wide(int R) const { return OTp / 2 >= 2048 && R > 4 && R <= kLinMaxRows && prep_launch(R); }
 };
 
 static ne_exl3_lin *lin_create(const uint16_t *trellis, const uint16_t *suh, const uint16_t *svh, int in, int out,
@@ -210,6 +212,8 @@ struct LinScratch {
 static LinArgs lin_args(ne_exl3_lin *l, int R, const float *x, float *y, const LinEpi &epi = LinEpi(),
                         const LinScratch *sc = nullptr) {
   const bool kloop = l->one_launch && l->k_loop(R);
+  static const bool no_wide = getenv("IJAH_LIN_NO_WIDE") != nullptr;  // A/B switch: lin_mx instead
+  const bool wide = l->one_launch && epi.kind != 8 && l->k_wide(R) && !no_wide;
   const int S = kloop ? 1 : l->groups();
   if (!sc && R > l->part_rows) {  // never while the stream is captured: a captured launch would keep the freed buffer
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
@@ -241,7 +245,7 @@ static LinArgs lin_args(ne_exl3_lin *l, int R, const float *x, float *y, const L
   a.epi = epi;
   a.cnt = l->one_launch ? (sc ? sc->cnt : l->cnt) : nullptr;
   a.xh_in = (!l->one_launch || l->prep_launch(R)) ? 1 : 0;
-  a.kloop = kloop ? 1 : 0;
+  a.kloop = kloop ? 1 : wide ? 2 : 0;
   return a;
 }
 
@@ -256,7 +260,8 @@ static void lin_launch_multi(ne_exl3_lin *const *l, int n, int R, const float *c
   int k = 0;
   for (int i = 0; i < n; i++) {
     const LinArgs ai = lin_args(l[i], R, x[i], y[i], epi ? epi[i] : LinEpi());
-    if (k > 0 && (k == group || ai.K != a[0].K || (bool)ai.cnt != (bool)a[0].cnt || ai.kloop != a[0].kloop)) {
+    if (k > 0 && (k == group || ai.K != a[0].K || (bool)ai.cnt != (bool)a[0].cnt || ai.kloop != a[0].kloop ||
+                  ai.kloop == 2)) {
       launch_lin_multi(a, k, s);
       k = 0;
     }

@@ -847,6 +847,92 @@ __global__ __launch_bounds__(256) void lin_mxl(LinMulti m) {
                  &flag);
 }
 
+// lin_mxw: lin_mx for wide linears (a vocabulary head) at 5..32 rows. Workgroup (8 tile pairs = two 128-column
+// output blocks, k group g), 8 waves; wave w takes pair 8 bp + w through the group's k chunks, each one MFMA chain
+// from zero folded left in registers (lin_mx's order: the same bits), the next chunk's requests in flight while one
+// decodes. A chunk's input rows are staged in LDS once for the 8 waves (lin_mx stages them per wave). The group
+// partials, the block counters and the finish are lin_mx's (two blocks per workgroup).
+template <int K, int RT>
+constexpr uint32_t lin_mxw_stage() { return RT * 256 + 8 * kLinChunkKt * 64 * K; }
+template <int K, int RT>
+constexpr uint32_t lin_mxw_lds() { return 2 * lin_mxw_stage<K, RT>(); }
+template <int K, int RT>
+__global__ __launch_bounds__(512) void lin_mxw(LinMulti m) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  __shared__ int flag;
+  const LinArgs a = m.l[0];  // one linear per launch
+  const int NP = (a.OT + 1) / 2, OTp = 2 * NP, R = a.R, IT = a.IT, NBP = (NP + 7) / 8;
+  const int bp = (int)blockIdx.x % NBP, g = (int)blockIdx.x / NBP;
+  const int lane = threadIdx.x & 63, w = (int)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6), p = bp * 8 + w;
+  const bool live = p < NP;
+  const int nck = min(kLinGroupKt / kLinChunkKt, (IT - g * kLinGroupKt + kLinChunkKt - 1) / kLinChunkKt);
+  const uint8_t *tiles = (const uint8_t *)a.tiles + (uint64_t)min(p, NP - 1) * IT * 64 * K;
+  // chunk c's requests into stage buffer c & 1: this wave's tiles, then the row quads 4 j .. 4 j + 3 with j = w mod 8
+  auto stage = [&](int c) {
+    const int kt0 = g * kLinGroupKt + c * kLinChunkKt, nkt = min(kLinChunkKt, IT - kt0);
+    uint8_t *sb = lds + (c & 1) * lin_mxw_stage<K, RT>();
+    uint8_t *tl = sb + RT * 256 + w * kLinChunkKt * 64 * K;
+    int n = 0;
+    if (live) {
+      const uint32_t bytes = (uint32_t)nkt * 64 * K;
+      for (uint32_t o = 0; o < bytes; o += 1024, n++)
+        if (o + (uint32_t)lane * 16 < bytes)
+          __builtin_amdgcn_global_load_lds((const void *)(tiles + (uint64_t)kt0 * 64 * K + o + lane * 16),
+                                           (__attribute__((address_space(3))) void *)(tl + o), 16, 0, 0);
+    }
+    for (int j = w; 4 * j < R; j += 8, n++) {
+      const int rr = 4 * j + (lane >> 4), q = lane & 15;
+      if (rr < R && q * 16 < nkt * 32)
+        __builtin_amdgcn_global_load_lds((const void *)(a.xh + (uint64_t)rr * a.in + kt0 * 16 + q * 8),
+                                         (__attribute__((address_space(3))) void *)(sb + 4 * j * 256), 16, 0, 0);
+    }
+    return n;
+  };
+  stage(0);
+  f32x16 v;
+#pragma unroll
+  for (int i = 0; i < 16; i++) v[i] = 0.f;
+  for (int c = 0; c < nck; c++) {
+    int nn = 0;
+    if (c + 1 < nck) {
+      __syncthreads();  // every wave is done with chunk c - 1's buffer before it is refilled
+      nn = stage(c + 1);
+    }
+    wait_vm(nn);      // this wave's requests of chunk c are in (chunk c + 1's may not be)
+    __syncthreads();  // and every wave's (the rows)
+    if (live) {
+      const int kt0 = g * kLinGroupKt + c * kLinChunkKt, nkt = min(kLinChunkKt, IT - kt0);
+      const uint8_t *sb = lds + (c & 1) * lin_mxw_stage<K, RT>();
+      const _Float16 *xa = (const _Float16 *)sb + min(lane & 31, R - 1) * 128 + 8 * (lane >> 5);
+      f32x16 acc;
+#pragma unroll
+      for (int i = 0; i < 16; i++) acc[i] = 0.f;
+      acc = mfma_chunk<K, kLinChunkKt>(sb + RT * 256 + w * kLinChunkKt * 64 * K, xa, nkt, acc);
+#pragma unroll
+      for (int i = 0; i < 16; i++) v[i] = c == 0 ? acc[i] : v[i] + acc[i];
+    }
+  }
+  if (live)
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      const int r = 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+      if (r < RT && r < R) st_cg(a.part + ((uint64_t)g * R + r) * OTp * 16 + p * 32 + (lane & 31), v[i]);
+    }
+  if (!a.cnt) return;
+  // each of the (one or two) blocks: its last arriving k group finishes it (waves 0-3 the first, 4-7 the second)
+  const int nb = min(2, (NP - 8 * bp + 3) / 4);
+  uint32_t last = 0;
+  for (int b = 0; b < nb; b++) {
+    uint32_t *ctr = a.cnt + (uint64_t)(2 * bp + b) * kSyncStride;
+    if (block_signal(ctr, &flag) == (uint32_t)(a.S - 1)) {
+      last |= 1u << b;
+      if (threadIdx.x == 0) st_cg(ctr, 0u);
+    }
+  }
+  const int b = w >> 2;
+  if (last & (1u << b)) lin_finish_block(a, w & 3, 2 * bp + b);
+}
+
 // lin_finish: the finisher of the staged path, grid R x ceil(out/128) (one workgroup per row and output block)
 __global__ __launch_bounds__(64) void lin_finish(LinArgs a) {
   __shared__ int flag;
@@ -1060,6 +1146,24 @@ static size_t lin_mxl_lds_any(int K, int RT, int G) {
   return n;
 }
 template <int K>
+static const void *lin_mxw_fn(int RT) {
+  return RT <= 8 ? (const void *)&lin_mxw<K, 8> : RT <= 16 ? (const void *)&lin_mxw<K, 16> : (const void *)&lin_mxw<K, 32>;
+}
+static const void *lin_mxw_any(int K, int RT) {
+  const void *f = nullptr;
+  IJ_DISPATCH_K(K, f = lin_mxw_fn<KK>(RT));
+  return f;
+}
+template <int K>
+static size_t lin_mxw_lds_fn(int RT) {
+  return RT <= 8 ? lin_mxw_lds<K, 8>() : RT <= 16 ? lin_mxw_lds<K, 16>() : lin_mxw_lds<K, 32>();
+}
+static size_t lin_mxw_lds_any(int K, int RT) {
+  size_t n = 0;
+  IJ_DISPATCH_K(K, n = lin_mxw_lds_fn<KK>(RT));
+  return n;
+}
+template <int K>
 static size_t lin_mx_lds_fn(int RT) {
   switch (RT) {
     case 1: return lin_mx_lds<K, 1>();
@@ -1085,21 +1189,25 @@ void launch_lin_multi(const LinArgs *l, int n, hipStream_t s) {
     const LinArgs &a = l[i];
     // every buffer a (possibly captured) launch uses is present, and the k groups fixed by the shape
     const int G = (a.IT + kLinGroupKt - 1) / kLinGroupKt;
-    IJ_CHECK(a.tiles && a.suh && a.svh && a.x && a.y && a.xh && a.part && a.S == (a.kloop ? 1 : G),
+    IJ_CHECK(a.tiles && a.suh && a.svh && a.x && a.y && a.xh && a.part && a.S == (a.kloop == 1 ? 1 : G),
              "linear launch: missing buffer or bad k groups (S %d of %d k tiles)", a.S, a.IT);
     IJ_CHECK(!a.kloop || (a.xh_in && G <= kLinLoopMaxGroups), "linear launch: the k-group loop needs the prep launch");
+    IJ_CHECK(a.kloop != 2 || (n == 1 && a.R > 4 && a.R <= kLinMaxRows && a.cnt && a.epi.kind != 8),
+             "linear launch: the wide form takes one linear of 5..32 rows with its counters and no HC epilogue");
     IJ_CHECK(a.K == l[0].K && a.R == l[0].R && a.R >= 1 && a.R <= kLinMaxRows && (bool)a.cnt == (bool)l[0].cnt &&
                  a.kloop == l[0].kloop,
              "multi-linear launch: K, R and path must agree");
     if (a.xh_in) hipLaunchKernelGGL(lin_prep, dim3(a.R * ((a.in + 127) / 128)), dim3(64), 0, s, a);
     m.l[i] = a;
     m.wg0[i] = wg;
-    wg += ((a.OT + 1) / 2) * (a.kloop ? 1 : a.S);
+    wg += a.kloop == 2 ? ((a.OT + 1) / 2 + 7) / 8 * a.S : ((a.OT + 1) / 2) * (a.kloop ? 1 : a.S);
   }
   m.wg0[n] = wg;
   const int RT = rows_tier(l[0].R);
   void *args[] = {&m};
-  if (l[0].kloop) {
+  if (l[0].kloop == 2) {
+    IJ_HIP(hipLaunchKernel(lin_mxw_any(l[0].K, RT), dim3(wg), dim3(512), args, lin_mxw_lds_any(l[0].K, RT), s));
+  } else if (l[0].kloop) {
     int G = 0;
     for (int i = 0; i < n; i++) G = std::max(G, (l[i].IT + kLinGroupKt - 1) / kLinGroupKt);
     IJ_HIP(hipLaunchKernel(lin_mxl_any(l[0].K, RT), dim3(wg), dim3(256), args, lin_mxl_lds_any(l[0].K, RT, G), s));
@@ -1122,6 +1230,10 @@ void init_lin_attrs() {
     for (int RT : {1, 2, 4, 8, 16, 32})
       IJ_HIP(hipFuncSetAttribute(lin_mxl_any(K, RT), hipFuncAttributeMaxDynamicSharedMemorySize,
                                  (int)std::min<size_t>(160 * 1024 - 256, lin_mxl_lds_any(K, RT, kLinLoopMaxGroups))));
+  for (int K = 2; K <= 8; K++)
+    for (int RT : {8, 16, 32})
+      IJ_HIP(hipFuncSetAttribute(lin_mxw_any(K, RT), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                 (int)lin_mxw_lds_any(K, RT)));
 }
 
 static const void *decode_fn(int K) {

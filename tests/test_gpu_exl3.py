@@ -138,6 +138,33 @@ def test_lm_head_k8_column_blocks(eng, oracle):
         assert rel(y[:, cols], want) < 5e-5, blk
 
 
+@pytest.mark.parametrize("inp,out,K,R", [(576, 65536 + 96, 5, 16), (2048, 65536, 8, 9), (512, 65536 + 256, 4, 32)])
+def test_wide_linear_rows_bit_identical(eng, oracle, inp, out, K, R):
+    """Linears of >= 2048 tile pairs (vocabulary heads) at 5..32 rows take the wide form (8 tile pairs per
+    workgroup, one k group each, a k chunk's rows staged once for the 8 waves): every row bit-identical to that row
+    run alone (the one-row k-loop form) and to the first rows run as a batch of 3; sampled column blocks (the output
+    Hadamard's width) within the oracle's tolerance. The shapes cover a partial last k group (576 inputs: one 4-tile chunk), a last workgroup
+    with 3 of its 8 tile pairs (65632 outputs), and a last workgroup with one full block of its two (65792)."""
+    print(f"wide linear {inp}x{out} K{K} R{R}", flush=True)
+    rng = np.random.default_rng(inp + out + K + R)
+    t = rng.integers(0, 1 << 16, (inp // 16, out // 16, 16 * K), dtype=np.uint16)
+    su, sv = synth.scales(rng, inp), synth.scales(rng, out)
+    x = synth.bf16_values(rng, R, inp)
+    lin = eng.exl3_linear(t, su, sv)
+    y = lin.run(x)
+    assert np.isfinite(y).all()
+    assert np.array_equal(y, lin.run(x))  # deterministic; the block counters reset themselves
+    for r in sorted({0, 1, R // 2, R - 1}):
+        assert np.array_equal(lin.run(x[r:r + 1])[0], y[r]), r
+    assert np.array_equal(lin.run(x[:3]), y[:3])
+    W = oracle.had_size(out)  # H_out is block-diagonal over W columns: a W-column slice is a linear of its own
+    assert out % W == 0 and oracle.had_size(W) == W
+    for blk in (0, 1, 2 * out // W // 3, out // W - 1):
+        cols = slice(blk * W, blk * W + W)
+        tb = np.ascontiguousarray(t[:, blk * W // 16:(blk + 1) * W // 16])
+        assert rel(y[:, cols], oracle.exl3_linear(x, tb, su, sv[cols])) < 5e-5, blk
+
+
 def test_run_kernel_decode_by_name(eng, oracle):
     """ne_run_kernel drives a registered kernel by name with function constants (reference tools/engine.py)."""
     K, inp, out = 5, 64, 64
