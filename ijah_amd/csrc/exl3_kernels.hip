@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cstdlib>
 #include <cmath>
 #include <cstring>
 
@@ -852,25 +853,25 @@ __global__ __launch_bounds__(256) void lin_mxl(LinMulti m) {
 // from zero folded left in registers (lin_mx's order: the same bits), the next chunk's requests in flight while one
 // decodes. A chunk's input rows are staged in LDS once for the 8 waves (lin_mx stages them per wave). The group
 // partials, the block counters and the finish are lin_mx's (two blocks per workgroup).
-template <int K, int RT>
-constexpr uint32_t lin_mxw_stage() { return RT * 256 + 8 * kLinChunkKt * 64 * K; }
-template <int K, int RT>
-constexpr uint32_t lin_mxw_lds() { return 2 * lin_mxw_stage<K, RT>(); }
-template <int K, int RT>
-__global__ __launch_bounds__(512) void lin_mxw(LinMulti m) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-  __shared__ int flag;
+template <int K, int RT, int NW>
+constexpr uint32_t lin_mxw_stage() { return RT * 256 + NW * kLinChunkKt * 64 * K; }
+template <int K, int RT, int NW>
+constexpr uint32_t lin_mxw_lds() { return 2 * lin_mxw_stage<K, RT, NW>(); }
+template <int K, int RT, int NW>
+__global__ __launch_bounds__(64 * NW) void lin_mxw(LinMulti m) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];  // the only LDS (4 pairs, 16 rows, K8: 40 KB, 4
+                                                                  // workgroups per CU)
   const LinArgs a = m.l[0];  // one linear per launch
-  const int NP = (a.OT + 1) / 2, OTp = 2 * NP, R = a.R, IT = a.IT, NBP = (NP + 7) / 8;
+  const int NP = (a.OT + 1) / 2, OTp = 2 * NP, R = a.R, IT = a.IT, NBP = (NP + NW - 1) / NW;
   const int bp = (int)blockIdx.x % NBP, g = (int)blockIdx.x / NBP;
-  const int lane = threadIdx.x & 63, w = (int)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6), p = bp * 8 + w;
+  const int lane = threadIdx.x & 63, w = (int)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6), p = bp * NW + w;
   const bool live = p < NP;
   const int nck = min(kLinGroupKt / kLinChunkKt, (IT - g * kLinGroupKt + kLinChunkKt - 1) / kLinChunkKt);
   const uint8_t *tiles = (const uint8_t *)a.tiles + (uint64_t)min(p, NP - 1) * IT * 64 * K;
   // chunk c's requests into stage buffer c & 1: this wave's tiles, then the row quads 4 j .. 4 j + 3 with j = w mod 8
   auto stage = [&](int c) {
     const int kt0 = g * kLinGroupKt + c * kLinChunkKt, nkt = min(kLinChunkKt, IT - kt0);
-    uint8_t *sb = lds + (c & 1) * lin_mxw_stage<K, RT>();
+    uint8_t *sb = lds + (c & 1) * lin_mxw_stage<K, RT, NW>();
     uint8_t *tl = sb + RT * 256 + w * kLinChunkKt * 64 * K;
     int n = 0;
     if (live) {
@@ -880,7 +881,7 @@ __global__ __launch_bounds__(512) void lin_mxw(LinMulti m) {
           __builtin_amdgcn_global_load_lds((const void *)(tiles + (uint64_t)kt0 * 64 * K + o + lane * 16),
                                            (__attribute__((address_space(3))) void *)(tl + o), 16, 0, 0);
     }
-    for (int j = w; 4 * j < R; j += 8, n++) {
+    for (int j = w; 4 * j < R; j += NW, n++) {
       const int rr = 4 * j + (lane >> 4), q = lane & 15;
       if (rr < R && q * 16 < nkt * 32)
         __builtin_amdgcn_global_load_lds((const void *)(a.xh + (uint64_t)rr * a.in + kt0 * 16 + q * 8),
@@ -902,7 +903,7 @@ __global__ __launch_bounds__(512) void lin_mxw(LinMulti m) {
     __syncthreads();  // and every wave's (the rows)
     if (live) {
       const int kt0 = g * kLinGroupKt + c * kLinChunkKt, nkt = min(kLinChunkKt, IT - kt0);
-      const uint8_t *sb = lds + (c & 1) * lin_mxw_stage<K, RT>();
+      const uint8_t *sb = lds + (c & 1) * lin_mxw_stage<K, RT, NW>();
       const _Float16 *xa = (const _Float16 *)sb + min(lane & 31, R - 1) * 128 + 8 * (lane >> 5);
       f32x16 acc;
 #pragma unroll
@@ -920,17 +921,18 @@ __global__ __launch_bounds__(512) void lin_mxw(LinMulti m) {
     }
   if (!a.cnt) return;
   // each of the (one or two) blocks: its last arriving k group finishes it (waves 0-3 the first, 4-7 the second)
-  const int nb = min(2, (NP - 8 * bp + 3) / 4);
+  const int nb = min(NW / 4, (NP - NW * bp + 3) / 4);
   uint32_t last = 0;
   for (int b = 0; b < nb; b++) {
-    uint32_t *ctr = a.cnt + (uint64_t)(2 * bp + b) * kSyncStride;
-    if (block_signal(ctr, &flag) == (uint32_t)(a.S - 1)) {
+    uint32_t *ctr = a.cnt + (uint64_t)((NW / 4) * bp + b) * kSyncStride;
+    // the flag word in the stage buffers: block_signal's barrier comes after every wave's last chunk
+    if (block_signal(ctr, (int *)lds) == (uint32_t)(a.S - 1)) {
       last |= 1u << b;
       if (threadIdx.x == 0) st_cg(ctr, 0u);
     }
   }
   const int b = w >> 2;
-  if (last & (1u << b)) lin_finish_block(a, w & 3, 2 * bp + b);
+  if (last & (1u << b)) lin_finish_block(a, w & 3, (NW / 4) * bp + b);
 }
 
 // lin_finish: the finisher of the staged path, grid R x ceil(out/128) (one workgroup per row and output block)
@@ -1145,22 +1147,32 @@ static size_t lin_mxl_lds_any(int K, int RT, int G) {
   IJ_DISPATCH_K(K, n = lin_mxl_lds_fn<KK>(RT, G));
   return n;
 }
-template <int K>
+static const int kLinWideWaves = getenv("IJAH_LIN_WIDE8") ? 8 : 4;  // A/B switch: 4 or 8 tile pairs per workgroup
+template <int K, int NW>
 static const void *lin_mxw_fn(int RT) {
-  return RT <= 8 ? (const void *)&lin_mxw<K, 8> : RT <= 16 ? (const void *)&lin_mxw<K, 16> : (const void *)&lin_mxw<K, 32>;
+  return RT <= 8 ? (const void *)&lin_mxw<K, 8, NW> : RT <= 16 ? (const void *)&lin_mxw<K, 16, NW>
+                                                                 : (const void *)&lin_mxw<K, 32, NW>;
 }
-static const void *lin_mxw_any(int K, int RT) {
+static const void *lin_mxw_any(int K, int RT, int NW) {
   const void *f = nullptr;
-  IJ_DISPATCH_K(K, f = lin_mxw_fn<KK>(RT));
+  if (NW == 4) {
+    IJ_DISPATCH_K(K, f = (lin_mxw_fn<KK, 4>(RT)));
+  } else {
+    IJ_DISPATCH_K(K, f = (lin_mxw_fn<KK, 8>(RT)));
+  }
   return f;
 }
-template <int K>
+template <int K, int NW>
 static size_t lin_mxw_lds_fn(int RT) {
-  return RT <= 8 ? lin_mxw_lds<K, 8>() : RT <= 16 ? lin_mxw_lds<K, 16>() : lin_mxw_lds<K, 32>();
+  return RT <= 8 ? lin_mxw_lds<K, 8, NW>() : RT <= 16 ? lin_mxw_lds<K, 16, NW>() : lin_mxw_lds<K, 32, NW>();
 }
-static size_t lin_mxw_lds_any(int K, int RT) {
+static size_t lin_mxw_lds_any(int K, int RT, int NW) {
   size_t n = 0;
-  IJ_DISPATCH_K(K, n = lin_mxw_lds_fn<KK>(RT));
+  if (NW == 4) {
+    IJ_DISPATCH_K(K, n = (lin_mxw_lds_fn<KK, 4>(RT)));
+  } else {
+    IJ_DISPATCH_K(K, n = (lin_mxw_lds_fn<KK, 8>(RT)));
+  }
   return n;
 }
 template <int K>
@@ -1200,13 +1212,15 @@ void launch_lin_multi(const LinArgs *l, int n, hipStream_t s) {
     if (a.xh_in) hipLaunchKernelGGL(lin_prep, dim3(a.R * ((a.in + 127) / 128)), dim3(64), 0, s, a);
     m.l[i] = a;
     m.wg0[i] = wg;
-    wg += a.kloop == 2 ? ((a.OT + 1) / 2 + 7) / 8 * a.S : ((a.OT + 1) / 2) * (a.kloop ? 1 : a.S);
+    wg += a.kloop == 2 ? ((a.OT + 1) / 2 + kLinWideWaves - 1) / kLinWideWaves * a.S
+                       : ((a.OT + 1) / 2) * (a.kloop ? 1 : a.S);
   }
   m.wg0[n] = wg;
   const int RT = rows_tier(l[0].R);
   void *args[] = {&m};
   if (l[0].kloop == 2) {
-    IJ_HIP(hipLaunchKernel(lin_mxw_any(l[0].K, RT), dim3(wg), dim3(512), args, lin_mxw_lds_any(l[0].K, RT), s));
+    IJ_HIP(hipLaunchKernel(lin_mxw_any(l[0].K, RT, kLinWideWaves), dim3(wg), dim3(64 * kLinWideWaves), args,
+                           lin_mxw_lds_any(l[0].K, RT, kLinWideWaves), s));
   } else if (l[0].kloop) {
     int G = 0;
     for (int i = 0; i < n; i++) G = std::max(G, (l[i].IT + kLinGroupKt - 1) / kLinGroupKt);
@@ -1232,8 +1246,9 @@ void init_lin_attrs() {
                                  (int)std::min<size_t>(160 * 1024 - 256, lin_mxl_lds_any(K, RT, kLinLoopMaxGroups))));
   for (int K = 2; K <= 8; K++)
     for (int RT : {8, 16, 32})
-      IJ_HIP(hipFuncSetAttribute(lin_mxw_any(K, RT), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                 (int)lin_mxw_lds_any(K, RT)));
+      for (int NW : {4, 8})
+        IJ_HIP(hipFuncSetAttribute(lin_mxw_any(K, RT, NW), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                   (int)lin_mxw_lds_any(K, RT, NW)));
 }
 
 static const void *decode_fn(int K) {
