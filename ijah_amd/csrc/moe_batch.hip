@@ -253,15 +253,18 @@ __global__ __launch_bounds__(512, 2) void bat_router_rows(MoeArgs a, int ngroups
 // order, then the lanes' sums meet in an xor butterfly over lane distances 32, 16, .., 1 (reference
 // kernels/fn_moe.metal:50-67).
 constexpr int kRouterExactChunks = 16;  // hid <= 8192
+// NC: the chunk bound the registers are sized for (hid / 512 <= NC): 4 at hid 2048 keeps the wave at ~50 registers
+// (eight waves per SIMD to cover the loads' latency) instead of ~200 for the largest hidden size
+template <int NC>
 __global__ __launch_bounds__(256) void bat_router_exact(MoeArgs a) {
   const int lane = threadIdx.x & 63, col = blockIdx.x * 4 + (threadIdx.x >> 6), r = blockIdx.y, nc = a.hid / 512;
   if (col >= a.ne + a.has_sgate) return;
   const uint16_t *w = a.router + (uint64_t)col * a.hid + lane * 8;
   const float *x = a.x + (uint64_t)r * a.hid + lane * 8;
-  uint4 wv[kRouterExactChunks];
-  float4 x0[kRouterExactChunks], x1[kRouterExactChunks];
+  uint4 wv[NC];
+  float4 x0[NC], x1[NC];
 #pragma unroll
-  for (int j = 0; j < kRouterExactChunks; j++)
+  for (int j = 0; j < NC; j++)
     if (j < nc) {
       wv[j] = *(const uint4 *)(w + j * 512);
       x0[j] = *(const float4 *)(x + j * 512);
@@ -269,7 +272,7 @@ __global__ __launch_bounds__(256) void bat_router_exact(MoeArgs a) {
     }
   float acc = 0.f;
 #pragma unroll
-  for (int j = 0; j < kRouterExactChunks; j++)
+  for (int j = 0; j < NC; j++)
     if (j < nc) {
       acc = fmaf(x0[j].x, bf16_f32(wv[j].x & 0xFFFFu), acc);
       acc = fmaf(x0[j].y, bf16_f32(wv[j].x >> 16), acc);
@@ -1658,7 +1661,13 @@ void launch_moe_batch(const MoeArgs &a, const MoeBatchBufs &b, hipStream_t s) {
     hipLaunchKernelGGL(bat_router_rows, dim3((ng * ((ncol + 127) / 128) + 7) & ~7), dim3(512), 0, s, a, ng);
   } else if (moe_batch_exact(a)) {
     IJ_CHECK(a.hid / 512 <= kRouterExactChunks, "few-row router: hidden %d above %d", a.hid, 512 * kRouterExactChunks);
-    hipLaunchKernelGGL(bat_router_exact, dim3((ncol + 3) / 4, a.R), dim3(256), 0, s, a);
+    const int nc = a.hid / 512;
+    if (nc <= 4)
+      hipLaunchKernelGGL(bat_router_exact<4>, dim3((ncol + 3) / 4, a.R), dim3(256), 0, s, a);
+    else if (nc <= 8)
+      hipLaunchKernelGGL(bat_router_exact<8>, dim3((ncol + 3) / 4, a.R), dim3(256), 0, s, a);
+    else
+      hipLaunchKernelGGL(bat_router_exact<kRouterExactChunks>, dim3((ncol + 3) / 4, a.R), dim3(256), 0, s, a);
   } else {
     hipLaunchKernelGGL(bat_router<1>, dim3((a.R + 31) / 32, (ncol + 31) / 32), dim3(64 * kRouterWaves), 0, s, a);
   }
