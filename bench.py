@@ -302,25 +302,28 @@ def run_probes(eng, iters=4000):
     return out
 
 
-def measure_hc_read(eng, R, steps, seed, hid=2560, lr=320, K=6):
+def measure_hc_read(eng, R, steps, seed, hid=2560, lr=320, K=6, copies=96):
     """The hyper-connection read (ne_hc_read: prep, down linear + silu epilogue, up linear + output epilogue) at R rows on
-    synthetic EXL3 mixes of the reference shape. GPU time per call from HIP events around its three launches, averaged
-    over calls on the same weights (4.9 MB: they stay in the last-level cache between calls)."""
+    synthetic EXL3 mixes of the reference shape. GPU time per call from HIP events around its three launches (median
+    over calls). The mixes are 4.9 MB: each call reads its own device copy of them, out of `copies` (96 copies = 470
+    MB, beyond the 256 MB last-level cache), so the weights come from HBM as in a model's layer chain."""
     from ijah_amd import synth
     from ijah_amd.engine import hc_read
     rng = np.random.default_rng(seed)
-    ld, lu = eng.exl3_linear(*synth.linear(rng, 4 * hid, lr, K)), eng.exl3_linear(*synth.linear(rng, lr, 4 * hid, K))
+    dn, up = synth.linear(rng, 4 * hid, lr, K), synth.linear(rng, lr, 4 * hid, K)
+    mixes = [(eng.exl3_linear(*dn), eng.exl3_linear(*up)) for _ in range(copies)]
     h = eng.from_numpy(rng.standard_normal((R, 4, hid)).astype(np.float32))
     nw = eng.from_numpy(synth.bf16((1 + 0.1 * rng.standard_normal(4 * hid)).astype(np.float32)))
     iw = eng.from_numpy(synth.bf16((rng.standard_normal((4, 4 * hid)) / 100).astype(np.float32)))
     mix, inj, out = eng.alloc(R * lr * 4), eng.alloc(R * 32), eng.alloc(R * hid * 4)
-    for _ in range(3):
-        hc_read(ld, lu, R, h, nw, iw, mix, inj, out)
-    ms = [hc_read(ld, lu, R, h, nw, iw, mix, inj, out, timed=True) for _ in range(max(10, steps))]
+    for m in mixes:  # every copy once, untimed: its scratch sized for R rows (470 MB still cycle through the cache)
+        hc_read(*m, R, h, nw, iw, mix, inj, out)
+    ms = [hc_read(*mixes[i % copies], R, h, nw, iw, mix, inj, out, timed=True) for i in range(max(10, min(steps, copies)))]
     res = {"rows": R, "hid": hid, "mix_rows": lr, "K": K, "us": round(1e3 * float(np.median(ms)), 3),
-           "launches": 3}
-    ld.free()
-    lu.free()
+           "launches": 4, "weights": f"{copies} distinct copies"}
+    for ld, lu in mixes:
+        ld.free()
+        lu.free()
     print(f"hc read R={R}: {res}", file=sys.stderr, flush=True)
     return res
 
