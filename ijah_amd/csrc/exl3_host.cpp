@@ -212,8 +212,7 @@ struct LinScratch {
 static LinArgs lin_args(ne_exl3_lin *l, int R, const float *x, float *y, const LinEpi &epi = LinEpi(),
                         const LinScratch *sc = nullptr) {
   const bool kloop = l->one_launch && l->k_loop(R);
-  static const bool no_wide = getenv("IJAH_LIN_NO_WIDE") != nullptr;  // A/B switch: lin_mx instead
-  const bool wide = l->one_launch && epi.kind != 8 && l->k_wide(R) && !no_wide;
+  const bool wide = l->one_launch && epi.kind != 8 && l->k_wide(R);
   const int S = kloop ? 1 : l->groups();
   if (!sc && R > l->part_rows) {  // never while the stream is captured: a captured launch would keep the freed buffer
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;

@@ -3,7 +3,6 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
-#include <cstdlib>
 #include <cmath>
 #include <cstring>
 
@@ -1147,32 +1146,26 @@ static size_t lin_mxl_lds_any(int K, int RT, int G) {
   IJ_DISPATCH_K(K, n = lin_mxl_lds_fn<KK>(RT, G));
   return n;
 }
-static const int kLinWideWaves = getenv("IJAH_LIN_WIDE8") ? 8 : 4;  // A/B switch: 4 or 8 tile pairs per workgroup
-template <int K, int NW>
+constexpr int kLinWideWaves = 4;  // tile pairs (waves) per wide workgroup: one output block (8 measured slower)
+template <int K>
 static const void *lin_mxw_fn(int RT) {
-  return RT <= 8 ? (const void *)&lin_mxw<K, 8, NW> : RT <= 16 ? (const void *)&lin_mxw<K, 16, NW>
-                                                                 : (const void *)&lin_mxw<K, 32, NW>;
+  return RT <= 8 ? (const void *)&lin_mxw<K, 8, kLinWideWaves>
+                 : RT <= 16 ? (const void *)&lin_mxw<K, 16, kLinWideWaves> : (const void *)&lin_mxw<K, 32, kLinWideWaves>;
 }
-static const void *lin_mxw_any(int K, int RT, int NW) {
+static const void *lin_mxw_any(int K, int RT) {
   const void *f = nullptr;
-  if (NW == 4) {
-    IJ_DISPATCH_K(K, f = (lin_mxw_fn<KK, 4>(RT)));
-  } else {
-    IJ_DISPATCH_K(K, f = (lin_mxw_fn<KK, 8>(RT)));
-  }
+  IJ_DISPATCH_K(K, f = lin_mxw_fn<KK>(RT));
   return f;
 }
-template <int K, int NW>
+template <int K>
 static size_t lin_mxw_lds_fn(int RT) {
-  return RT <= 8 ? lin_mxw_lds<K, 8, NW>() : RT <= 16 ? lin_mxw_lds<K, 16, NW>() : lin_mxw_lds<K, 32, NW>();
+  return RT <= 8    ? lin_mxw_lds<K, 8, kLinWideWaves>()
+         : RT <= 16 ? lin_mxw_lds<K, 16, kLinWideWaves>()
+                    : lin_mxw_lds<K, 32, kLinWideWaves>();
 }
-static size_t lin_mxw_lds_any(int K, int RT, int NW) {
+static size_t lin_mxw_lds_any(int K, int RT) {
   size_t n = 0;
-  if (NW == 4) {
-    IJ_DISPATCH_K(K, n = (lin_mxw_lds_fn<KK, 4>(RT)));
-  } else {
-    IJ_DISPATCH_K(K, n = (lin_mxw_lds_fn<KK, 8>(RT)));
-  }
+  IJ_DISPATCH_K(K, n = lin_mxw_lds_fn<KK>(RT));
   return n;
 }
 template <int K>
@@ -1219,8 +1212,8 @@ void launch_lin_multi(const LinArgs *l, int n, hipStream_t s) {
   const int RT = rows_tier(l[0].R);
   void *args[] = {&m};
   if (l[0].kloop == 2) {
-    IJ_HIP(hipLaunchKernel(lin_mxw_any(l[0].K, RT, kLinWideWaves), dim3(wg), dim3(64 * kLinWideWaves), args,
-                           lin_mxw_lds_any(l[0].K, RT, kLinWideWaves), s));
+    IJ_HIP(hipLaunchKernel(lin_mxw_any(l[0].K, RT), dim3(wg), dim3(64 * kLinWideWaves), args,
+                           lin_mxw_lds_any(l[0].K, RT), s));
   } else if (l[0].kloop) {
     int G = 0;
     for (int i = 0; i < n; i++) G = std::max(G, (l[i].IT + kLinGroupKt - 1) / kLinGroupKt);
@@ -1246,9 +1239,8 @@ void init_lin_attrs() {
                                  (int)std::min<size_t>(160 * 1024 - 256, lin_mxl_lds_any(K, RT, kLinLoopMaxGroups))));
   for (int K = 2; K <= 8; K++)
     for (int RT : {8, 16, 32})
-      for (int NW : {4, 8})
-        IJ_HIP(hipFuncSetAttribute(lin_mxw_any(K, RT, NW), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                   (int)lin_mxw_lds_any(K, RT, NW)));
+      IJ_HIP(hipFuncSetAttribute(lin_mxw_any(K, RT), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                 (int)lin_mxw_lds_any(K, RT)));
 }
 
 static const void *decode_fn(int K) {
