@@ -532,20 +532,41 @@ __device__ __forceinline__ void lin_store(const LinArgs &a, int r, int c, float 
 }
 
 // The HC read's output step fused into the up linear's finisher (LinEpi kind 8; reference
-// kernels/trunk6/t6_epi.metal:80-97 for the arithmetic): row r (global), column cc of the hid outputs, from the four
-// streams' u (coherent loads: other workgroups stored them)
-__device__ __forceinline__ void hc_fin_col(const LinArgs &a, int r, int cc) {
+// kernels/trunk6/t6_epi.metal:80-97 for the arithmetic): for each of up to B output columns i0, i0 + stride, ..
+// below n (row r0 + i / 128, column cs * 128 + i % 128 of the hid outputs) the four streams' u (coherent loads: other
+// workgroups stored them) and the other operands are all requested first, then each column is finished: one round
+// trip for B columns instead of one per column.
+template <int B>
+__device__ __forceinline__ void hc_fin_cols(const LinArgs &a, int r0, int cs, int i0, int stride, int n) {
   const LinEpi &e = a.epi;
   const int hid = e.hid, q = e.refr;
-  float v[4];
+  float u[B][4], y[B][4], inv[B][4], w[B][4];
 #pragma unroll
-  for (int st = 0; st < 4; st++) {
-    const uint64_t row = (uint64_t)st * hid + cc;
-    const float u = ld_cg(e.e0 + (uint64_t)r * a.out + row), inv = e.e4[r * 8 + 4 + st];
-    const float sg = epi_rr(1.f / (1.f + expf(-epi_rr(u, q))), q);
-    v[st] = epi_rr(sg * epi_rr(e.e1[(uint64_t)r * a.out + row] * inv * epi_bf(e.w16[row]), q), q);
+  for (int b = 0; b < B; b++) {
+    const int i = min(i0 + b * stride, n - 1), r = r0 + i / 128, cc = cs * 128 + i % 128;
+#pragma unroll
+    for (int st = 0; st < 4; st++) {
+      const uint64_t row = (uint64_t)st * hid + cc;
+      u[b][st] = ld_cg(e.e0 + (uint64_t)r * a.out + row);
+      y[b][st] = e.e1[(uint64_t)r * a.out + row];
+      inv[b][st] = e.e4[r * 8 + 4 + st];
+      w[b][st] = epi_bf(e.w16[row]);
+    }
   }
-  e.e2[(uint64_t)r * hid + cc] = epi_rr(((v[0] + v[1]) + (v[2] + v[3])) * 0.25f, q);
+#pragma unroll
+  for (int b = 0; b < B; b++) {
+    const int i = i0 + b * stride;
+    if (i < n) {
+      const int r = r0 + i / 128, cc = cs * 128 + i % 128;
+      float v[4];
+#pragma unroll
+      for (int st = 0; st < 4; st++) {
+        const float sg = epi_rr(1.f / (1.f + expf(-epi_rr(u[b][st], q))), q);
+        v[st] = epi_rr(sg * epi_rr(y[b][st] * inv[b][st] * w[b][st], q), q);
+      }
+      e.e2[(uint64_t)r * hid + cc] = epi_rr(((v[0] + v[1]) + (v[2] + v[3])) * 0.25f, q);
+    }
+  }
 }
 // the row's four inject gates from the prep's partials, on one whole wave (lane = (chunk phase, stream, gate))
 __device__ __forceinline__ void hc_fin_gates(const LinArgs &a, int r, int lane) {
@@ -566,7 +587,8 @@ __device__ void hc_fin_block(const LinArgs &a, uint32_t *ctr, int r0, int r1, in
   const int nw = (int)(blockDim.x >> 6);
   if (block_signal(ctr, flag) != 3u) return;
   if (threadIdx.x == 0) st_cg(ctr, 0u);
-  for (int i = threadIdx.x; i < (r1 - r0) * 128; i += blockDim.x) hc_fin_col(a, r0 + i / 128, cs * 128 + i % 128);
+  const int n = (r1 - r0) * 128;
+  for (int i0 = threadIdx.x; i0 < n; i0 += 4 * (int)blockDim.x) hc_fin_cols<4>(a, r0, cs, i0, (int)blockDim.x, n);
   if (cs == 0)
     for (int r = r0 + wave; r < r1; r += nw) hc_fin_gates(a, r, lane);
 }
