@@ -234,7 +234,8 @@ def epi_case(eng, oracle, kind, inp, out, K, R, refr=True, ldy=0, yoff=0, seed=0
     (1, 48, 96, 8, 12, True, 0, 0), (1, 2048, 512, 6, 2, False, 0, 0),
     (5, 2048, 48, 6, 1, True, 96, 48), (5, 2048, 48, 6, 10, True, 96, 48),
     (6, 2048, 48, 6, 1, True, 96, 0), (6, 2048, 48, 6, 10, True, 96, 0), (6, 2048, 48, 6, 2, False, 96, 0),
-    (7, 2048, 640, 6, 1, True, 0, 0), (7, 2048, 640, 6, 16, True, 0, 0), (7, 48, 640, 5, 12, True, 0, 0)])
+    (7, 2048, 640, 6, 1, True, 0, 0), (7, 2048, 640, 6, 16, True, 0, 0), (7, 48, 640, 5, 12, True, 0, 0),
+    (3, 512, 65536, 4, 8, True, 0, 0), (2, 512, 65536, 4, 16, True, 0, 0)])  # the wide form (>= 2048 pairs)
 def test_linear_fused_epilogues(eng, oracle, kind, inp, out, K, R, refr, ldy, yoff):
     print(f"linear epilogue {kind} {inp}x{out} K{K} R{R} refr {refr} ldy {ldy} y_off {yoff}", flush=True)
     pairs, y, ref_full = epi_case(eng, oracle, kind, inp, out, K, R, refr, ldy, yoff)
