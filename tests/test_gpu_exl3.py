@@ -138,7 +138,8 @@ def test_lm_head_k8_column_blocks(eng, oracle):
         assert rel(y[:, cols], want) < 5e-5, blk
 
 
-@pytest.mark.parametrize("inp,out,K,R", [(576, 65536 + 96, 5, 16), (2048, 65536, 8, 9), (512, 65536 + 256, 4, 32)])
+@pytest.mark.parametrize("inp,out,K,R", [(576, 65536 + 96, 5, 16), (2048, 65536, 8, 9), (512, 65536 + 256, 4, 32),
+                                         (1024, 65536, 6, 5)])
 def test_wide_linear_rows_bit_identical(eng, oracle, inp, out, K, R):
     """Linears of >= 2048 tile pairs (vocabulary heads) at 5..32 rows take the wide form (8 tile pairs per
     workgroup, one k group each, a k chunk's rows staged once for the 8 waves): every row bit-identical to that row
