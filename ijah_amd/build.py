@@ -15,7 +15,7 @@ LIB = OUT / "libijah_exl3.so"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = os.environ.get("IJAH_ARCH", "gfx950")
 
-SOURCES = ["exl3_kernels.hip", "moe_fused.hip", "moe_batch.hip", "noalloc.hip", "probes.hip", "exl3_host.cpp", "capi.cpp", "json.cpp", "pack_align.cpp"]
+SOURCES = ["exl3_kernels.hip", "moe_fused.hip", "moe_batch.hip", "noalloc.hip", "moe_q8.hip", "probes.hip", "exl3_host.cpp", "capi.cpp", "json.cpp", "pack_align.cpp"]
 # -ffp-contract=off: the prepared input must round exactly as the reference's f32 arithmetic (no fused x*suh + y).
 # -packed-fp32-ops off: packed FP32 VALU forms are not used on this pool.
 COMMON = ["-O3", "-std=c++17", "-fPIC", "-ffp-contract=off", "-fvisibility=hidden", "-Wall", "-Wno-unused-function",

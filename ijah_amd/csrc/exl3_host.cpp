@@ -520,25 +520,26 @@ NE_API int ne_exl3_lin_decode(ne_exl3_lin *l, ne_buf *w, double *gpu_ms) {
 
 // ---------------------------------------------------------------------------------------------------- MoE layer
 // The few-row MoE kernels' partials and block counters, one pool per layer shape shared by every layer of that shape
-// (the layers run one after another on the library's stream; the counters are back at zero after each launch). It
-// only grows (counters zeroed), never while a stream is captured.
+// (the layers run one after another on the library's stream; the counters are back at zero after each launch). A
+// pool only grows (counters zeroed), never while a stream is captured. A grown pool's old arrays are kept until the
+// process ends: a graph captured earlier, or another layer, may still hold their addresses; every launch takes the
+// pool's current arrays (few_pool_now), which are at least as large as any layer's need.
+struct FewPool {
+  uint64_t *part = nullptr;
+  uint32_t *ep = nullptr;
+  int chunks = 0;
+};
+static std::mutex g_few_mu;
+static std::map<std::pair<int, int>, FewPool> g_few_pools;
+static std::vector<FewPool> g_few_retired;
 static void few_pool(int hid, int inter, int chunks, uint64_t **part, uint32_t **ep) {
-  struct Pool {
-    uint64_t *part = nullptr;
-    uint32_t *ep = nullptr;
-    int chunks = 0;
-  };
-  static std::mutex mu;
-  static std::map<std::pair<int, int>, Pool> pools;
-  std::lock_guard<std::mutex> g(mu);
-  Pool &p = pools[{hid, inter}];
+  std::lock_guard<std::mutex> g(g_few_mu);
+  FewPool &p = g_few_pools[{hid, inter}];
   if (chunks > p.chunks) {
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     IJ_HIP(hipStreamIsCapturing(stream(), &cs));
     IJ_CHECK(cs == hipStreamCaptureStatusNone, "MoE: few-row scratch must grow before a stream capture");
-    IJ_HIP(hipStreamSynchronize(stream()));  // no launch still uses the old pool
-    dev_free(p.part);
-    dev_free(p.ep);
+    if (p.part) g_few_retired.push_back(p);
     const size_t np = moe_batch_few_part(chunks, hid, inter), ne = moe_batch_few_epochs(chunks, inter);
     p.part = dev_alloc<uint64_t>(np);
     p.ep = dev_alloc<uint32_t>(ne);
@@ -549,11 +550,21 @@ static void few_pool(int hid, int inter, int chunks, uint64_t **part, uint32_t *
   *part = p.part;
   *ep = p.ep;
 }
+// the pool's current arrays (no growth): what a launch uses
+static void few_pool_now(int hid, int inter, uint64_t **part, uint32_t **ep, int *chunks) {
+  std::lock_guard<std::mutex> g(g_few_mu);
+  const FewPool &p = g_few_pools[{hid, inter}];
+  *part = p.part;
+  *ep = p.ep;
+  *chunks = p.chunks;
+}
 
 struct ne_moe {
   int hid = 0, inter = 0, ne = 0, topk = 0, K = 0, Ks = 0, has_shared = 0, has_sgate = 0, ksplit = 4;
   ExpertLayout lay, slay;
   uint8_t *experts = nullptr, *shared = nullptr;
+  uint8_t *q8 = nullptr;       // the 8-bit affine shared expert (q8_offsets), in place of an EXL3 shared slot
+  float *q8gu = nullptr, *q8o = nullptr;  // its per-row outputs (staged and batched paths)
   uint16_t *router = nullptr;  // [ne + has_sgate][hid]
   int Rcap = 0;
   float *logits = nullptr, *sgv = nullptr, *guo = nullptr, *dn = nullptr;
@@ -571,7 +582,8 @@ struct ne_moe {
   int last_R = 0;
   float *last_y = nullptr;
   ~ne_moe() {
-    for (void *p : std::initializer_list<void *>{experts, shared, router, logits, sgv, guo, dn, route, sync, trace, hprep, plan, part, fsync})
+    for (void *p : std::initializer_list<void *>{experts, shared, q8, q8gu, q8o, router, logits, sgv, guo, dn, route,
+                                                 sync, trace, hprep, plan, part, fsync})
       dev_free(p);
     free_batch();
   }
@@ -607,16 +619,21 @@ struct ne_moe {
   }
   void ensure_scratch(int R) {
     if (R <= Rcap) return;
-    for (void *p : std::initializer_list<void *>{logits, sgv, guo, dn, route, sync, hprep}) dev_free(p);
+    for (void *p : std::initializer_list<void *>{logits, sgv, guo, dn, route, sync, hprep, q8gu, q8o}) dev_free(p);
+    q8gu = q8o = nullptr;
     const size_t S = (size_t)R * nslot();
+    if (q8) {
+      q8gu = dev_alloc<float>((size_t)R * 2 * inter);
+      q8o = dev_alloc<float>((size_t)R * hid);
+    }
     logits = dev_alloc<float>(logit_floats(R));
     IJ_HIP(hipMemset(logits, 0, sizeof(float) * logit_floats(R)));  // the fused kernel's launch tags start at 1
     sgv = dev_alloc<float>(R);
     guo = dev_alloc<float>(S * 2 * ksplit * inter);
     dn = dev_alloc<float>(S * hid);
     hprep = dev_alloc<uint16_t>(S * inter);
-    if (!plan && fused && moe_fused_supported(K, has_shared ? Ks : K, 1, hid, inter, ne, topk)) {
-      const MoePlan pl = moe_fused_plan(hid, inter, topk, nslot(), moe_fused_grid());
+    if (!plan && fused && moe_fused_supported(K, has_shared ? Ks : K, 1, hid, inter, ne, topk, q8 != nullptr)) {
+      const MoePlan pl = moe_fused_plan(hid, inter, topk, nslot(), moe_fused_grid(), q8 != nullptr);
       if (pl.ok) {
         plan = dev_alloc<uint32_t>(pl.words.size());
         IJ_HIP(hipMemcpy(plan, pl.words.data(), pl.words.size() * 4, hipMemcpyHostToDevice));
@@ -674,6 +691,9 @@ struct ne_moe {
     a.units = plan;
     a.part = part;
     a.fsync = fsync;
+    a.q8 = q8;
+    a.q8gu = q8gu;
+    a.q8o = q8o;
     return a;
   }
   // a failed cross-workgroup wait leaves the error word set: report it and clear the counters
@@ -702,7 +722,15 @@ struct ne_moe {
       a.hc_out = hc->hc_out;
     }
     if (batch_ok(R) && R <= bat_R) {
-      launch_moe_batch(a, bat, s);
+      MoeBatchBufs b = bat;
+      if (b.vpart) {  // the shape's pool may have grown (for another layer) since this layer took its arrays
+        int pc = 0;
+        few_pool_now(hid, inter, &b.vpart, &b.vep, &pc);
+        IJ_CHECK(pc >= b.vmax_chunks, "MoE: few-row pool smaller than the layer's need");
+        b.vmax_chunks = pc;
+      }
+      if (q8) launch_moe_q8(a, s);  // independent of the route; the batch's combine reads its output
+      launch_moe_batch(a, b, s);
       return;
     }
     if (fused_ok(R)) {
@@ -710,6 +738,7 @@ struct ne_moe {
       return;
     }
     launch_moe_router(a, s);
+    if (q8) launch_moe_q8(a, s);
     launch_moe_gateup(a, s);
     launch_moe_down(a, s);
     launch_moe_combine(a, s);
@@ -744,9 +773,15 @@ ne_moe *moe_create(const ne_moe_desc &d) {
   IJ_CHECK(d.K >= 2 && d.K <= 8, "routed K %d (2..8)", d.K);
   IJ_CHECK(d.router && d.gt && d.ut && d.dt && d.gsu && d.gsv && d.usu && d.usv && d.dsu && d.dsv,
            "missing routed expert or router arrays");
-  const bool sh = d.sgt != nullptr;
+  const bool sh = d.sgt != nullptr, q8 = d.qgw != nullptr;
   IJ_CHECK(!sh || (d.sut && d.sdt && d.sgsu && d.sgsv && d.susu && d.susv && d.sdsu && d.sdsv),
            "shared expert arrays incomplete");
+  IJ_CHECK(!(sh && q8), "two shared experts (EXL3 and 8-bit): give one");
+  IJ_CHECK(!q8 || (d.quw && d.qdw && d.qgs && d.qgb && d.qus && d.qub && d.qds && d.qdb),
+           "8-bit shared expert arrays incomplete");
+  IJ_CHECK(!q8 || d.qgroup == kQ8Group, "8-bit shared expert: group %d (the MoE layer takes %d, as the reference's "
+           "fn_moe kernels)", d.qgroup, kQ8Group);
+  IJ_CHECK(!q8 || moe_q8_supported(d.hid, d.inter), "8-bit shared expert: %d x %d not supported", d.hid, d.inter);
   IJ_CHECK(!sh || (d.Ks >= 2 && d.Ks <= 8), "shared K %d (2..8)", d.Ks);
   ensure_device();
   auto m = std::make_unique<ne_moe>();
@@ -785,6 +820,20 @@ ne_moe *moe_create(const ne_moe_desc &d) {
     build_block(m->slay, d.hid, d.inter, tr, su, sv, sb.data());
     m->shared = dev_alloc<uint8_t>(m->slay.bytes);
     IJ_HIP(hipMemcpy(m->shared, sb.data(), sb.size(), hipMemcpyHostToDevice));
+  }
+  if (q8) {  // weight bytes as stored; each group's bf16 scale and bias joined into one word
+    const Q8Off o = q8_offsets(d.hid, d.inter);
+    std::vector<uint8_t> qb(q8_block_bytes(d.hid, d.inter));
+    const uint32_t *w[3] = {d.qgw, d.quw, d.qdw};
+    const uint16_t *sc[3] = {d.qgs, d.qus, d.qds}, *bi[3] = {d.qgb, d.qub, d.qdb};
+    const int rows[3] = {d.inter, d.inter, d.hid}, in[3] = {d.hid, d.hid, d.inter};
+    for (int p = 0; p < 3; p++) {
+      memcpy(qb.data() + o.w[p], w[p], (size_t)rows[p] * in[p]);
+      uint32_t *sb = (uint32_t *)(qb.data() + o.sb[p]);
+      for (size_t i = 0; i < (size_t)rows[p] * (in[p] / kQ8Group); i++) sb[i] = sc[p][i] | (uint32_t)bi[p][i] << 16;
+    }
+    m->q8 = dev_alloc<uint8_t>(qb.size());
+    IJ_HIP(hipMemcpy(m->q8, qb.data(), qb.size(), hipMemcpyHostToDevice));
   }
   const size_t rrows = (size_t)d.ne + m->has_sgate;
   m->router = dev_alloc<uint16_t>(rrows * d.hid);
@@ -846,7 +895,34 @@ NE_API ne_moe *ne_moe_load(const ne_pack *p, const char *prefix, int topk) {
     for (const char *n : {"gate_proj", "up_proj", "down_proj"})
       for (const char *s : {"suh", "svh"})
         IJ_CHECK(P.need(mp + "switch_mlp." + n + "." + s, -1, {}).dtype == NE_F16, "%s: suh/svh must be F16", n);
-    if (P.has(mp + "shared_expert.gate_proj.trellis")) {
+    const bool sh_exl3 = P.has(mp + "shared_expert.gate_proj.trellis"),
+               sh_q8 = P.has(mp + "shared_expert.gate_proj.weight");
+    if (!sh_exl3 && !sh_q8) {  // nothing else may be there: a shared expert in another form is refused, not dropped
+      for (const std::string &n : P.names())
+        IJ_CHECK(n.compare(0, mp.size() + 14, mp + "shared_expert.") != 0,
+                 "%s: shared expert in a form this layer does not take (EXL3 .trellis or 8-bit .weight/.scales/"
+                 ".biases)", n.c_str());
+      IJ_CHECK(!d.sgate, "%sshared_expert_gate.weight without a shared expert", mp.c_str());
+    }
+    if (sh_q8) {  // the reference's 8-bit affine shared expert (layer.mm:39-61 q8, :186-193)
+      const int rows[3] = {d.inter, d.inter, d.hid}, in[3] = {d.hid, d.hid, d.inter};
+      const char *nm[3] = {"shared_expert.gate_proj", "shared_expert.up_proj", "shared_expert.down_proj"};
+      const uint32_t **w[3] = {&d.qgw, &d.quw, &d.qdw};
+      const uint16_t **sc[3] = {&d.qgs, &d.qus, &d.qds}, **bi[3] = {&d.qgb, &d.qub, &d.qdb};
+      for (int p = 0; p < 3; p++) {
+        const std::string b = mp + nm[p];
+        *w[p] = (const uint32_t *)P.need(b + ".weight", NE_U32, {rows[p], in[p] / 4}).host;
+        const TensorInfo &s = P.need(b + ".scales", NE_BF16, {rows[p], -1});
+        IJ_CHECK(s.shape[1] > 0 && in[p] % s.shape[1] == 0, "%s.scales: shape [%lld, %lld]", b.c_str(),
+                 (long long)s.shape[0], (long long)s.shape[1]);
+        const int g = in[p] / (int)s.shape[1];
+        IJ_CHECK(g == kQ8Group, "%s: group %d; the MoE layer's 8-bit shared expert takes g%d (reference "
+                 "layer.mm:191-192)", b.c_str(), g, kQ8Group);
+        *sc[p] = (const uint16_t *)s.host;
+        *bi[p] = (const uint16_t *)P.need(b + ".biases", NE_BF16, {rows[p], s.shape[1]}).host;
+      }
+      d.qgroup = kQ8Group;
+    } else if (sh_exl3) {
       const TensorInfo &sg = P.need(mp + "shared_expert.gate_proj.trellis", NE_U16, {d.hid / 16, d.inter / 16, -1});
       d.Ks = (int)sg.shape[2] / 16;
       const int64_t ts = 16 * d.Ks;
@@ -877,8 +953,11 @@ NE_API ne_moe *ne_moe_synth(int hid, int inter, int ne, int topk, int K, int has
     m->ne = ne;
     m->topk = topk;
     m->K = K;
-    m->Ks = has_shared ? Ks : 0;
-    m->has_shared = has_shared != 0;
+    IJ_CHECK(has_shared >= 0 && has_shared <= 2, "has_shared %d (0 none, 1 EXL3, 2 8-bit)", has_shared);
+    IJ_CHECK(has_shared != 2 || moe_q8_supported(hid, inter), "8-bit shared expert: %d x %d not supported", hid,
+             inter);
+    m->Ks = has_shared == 1 ? Ks : 0;
+    m->has_shared = has_shared == 1;
     m->lay = expert_layout(hid, inter, K);
     hipStream_t s = stream();
     m->experts = dev_alloc<uint8_t>((size_t)ne * m->lay.bytes);
@@ -891,7 +970,15 @@ NE_API ne_moe *ne_moe_synth(int hid, int inter, int ne, int topk, int K, int has
       }
     };
     for (int e = 0; e < ne; e++) scales(m->experts + (size_t)e * m->lay.bytes, m->lay, seed * 100003 + e);
-    if (has_shared) {
+    if (has_shared == 2) {
+      const Q8Off o = q8_offsets(hid, inter);
+      m->q8 = dev_alloc<uint8_t>(q8_block_bytes(hid, inter));
+      launch_fill_u32((uint32_t *)m->q8, o.sb[0] / 4, seed * 7 + 3, s);
+      const int in[3] = {hid, hid, inter};
+      for (int p = 0; p < 3; p++)
+        launch_fill_q8_sb((uint32_t *)(m->q8 + o.sb[p]), (uint64_t)inter * hid / kQ8Group, in[p], seed * 13 + p, s);
+    }
+    if (has_shared == 1) {
       m->slay = expert_layout(hid, inter, Ks);
       m->shared = dev_alloc<uint8_t>(m->slay.bytes);
       launch_fill_u32((uint32_t *)m->shared, m->slay.bytes / 4, seed * 7 + 3, s);
@@ -998,6 +1085,18 @@ NE_API int ne_moe_read(ne_moe *m, const char *name, void *dst, uint64_t nbytes) 
       fetch(m->route, (size_t)R * 2 * m->topk * 4);
     } else if (n == "shared_gate") {
       fetch(m->sgv, (size_t)R * 4);
+    } else if (n == "shared_q8") {  // the 8-bit shared expert's rounded output o [R][hid]
+      IJ_CHECK(m->q8, "the layer has no 8-bit shared expert");
+      if (m->fused_ok(R)) {  // tagged u64 values: the f32 in the low word
+        std::vector<uint64_t> t((size_t)m->hid);
+        const uint64_t *src = (const uint64_t *)m->part + moe_fused_q8_index(m->hid, m->inter, m->nslot()) +
+                              2 * (size_t)m->inter;
+        IJ_HIP(hipMemcpy(t.data(), src, t.size() * 8, hipMemcpyDeviceToHost));
+        out.resize(t.size() * 4);
+        for (size_t i = 0; i < t.size(); i++) memcpy(out.data() + 4 * i, &t[i], 4);
+      } else {
+        fetch(m->q8o, (size_t)R * m->hid * 4);
+      }
     } else if ((n == "experts_gu" || n == "experts_dn") && m->batch_ok(R)) {
       IJ_CHECK(false, "\"%s\" is not kept by the batched path (R >= 2); IJAH_MOE_PATH=staged keeps it", name);
     } else if (n == "experts_gu" && m->fused_ok(R)) {  // the fused step stores the summed inner outputs
@@ -1058,6 +1157,7 @@ NE_API int ne_moe_bytes(const ne_moe *m, int R, uint64_t *bytes) {
     };
     uint64_t b = uniq.size() * per_expert(m->K);
     if (m->has_shared) b += per_expert(m->Ks);
+    if (m->q8) b += q8_block_bytes(m->hid, m->inter);  // weight bytes + bf16 scales and biases
     b += 2u * (uint64_t)(m->ne + m->has_sgate) * m->hid;
     *bytes = b;
   });

@@ -433,7 +433,9 @@ __device__ void combine_block(const MoeArgs &a, int r, int c, float (*vs)[128]) 
     const int i = c * 128 + threadIdx.x;
     float s = 0.f;
     for (int k = 0; k < a.topk; k++) s += vs[k][threadIdx.x];
-    const float t = a.nslot > a.topk ? vs[a.topk][threadIdx.x] : 0.f;
+    const float t = a.nslot > a.topk ? vs[a.topk][threadIdx.x]
+                    : a.q8 && i < a.hid ? ld_cg(a.sgv + r) * a.q8o[(uint64_t)r * a.hid + i]
+                                        : 0.f;
     if (i < a.hid) a.y[(uint64_t)r * a.hid + i] = moe_finish(a, r, i, s, t);
   }
   __syncthreads();
@@ -1082,6 +1084,15 @@ __global__ void fill_scale_f16(uint16_t *p, uint64_t n, uint64_t seed) {
     p[i] = f2h(neg ? -m : m);
   }
 }
+// 8-bit affine group words (scale bf16 low, bias bf16 high): scale = |N(1, 0.1)| / (74 sqrt(in)) (a uniform byte has
+// a standard deviation of ~74), bias = -127.5 scale, so that a row's weights have mean ~0 and variance ~1 / in
+__global__ void fill_q8_sb(uint32_t *p, uint64_t n, int in, uint64_t seed) {
+  for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x) {
+    const float sc = bf16_round(fabsf(1.0f + 0.1f * gauss(seed, i)) / (74.f * sqrtf((float)in)));
+    const float bi = bf16_round(-127.5f * sc);
+    p[i] = (__float_as_uint(sc) >> 16) | (__float_as_uint(bi) & 0xFFFF0000u);
+  }
+}
 __global__ void fill_normal_bf16(uint16_t *p, uint64_t n, uint64_t seed, float sd) {
   for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x) {
     const float v = sd * gauss(seed, i);
@@ -1099,6 +1110,9 @@ void launch_fill_u32(uint32_t *p, uint64_t n, uint64_t seed, hipStream_t s) {
 }
 void launch_fill_scale_f16(uint16_t *p, uint64_t n, uint64_t seed, hipStream_t s) {
   hipLaunchKernelGGL(fill_scale_f16, dim3(fill_grid(n)), dim3(256), 0, s, p, n, seed);
+}
+void launch_fill_q8_sb(uint32_t *p, uint64_t n, int in, uint64_t seed, hipStream_t s) {
+  hipLaunchKernelGGL(fill_q8_sb, dim3(fill_grid(n)), dim3(256), 0, s, p, n, in, seed);
 }
 void launch_fill_normal_bf16(uint16_t *p, uint64_t n, uint64_t seed, float sd, hipStream_t s) {
   hipLaunchKernelGGL(fill_normal_bf16, dim3(fill_grid(n)), dim3(256), 0, s, p, n, seed, sd);

@@ -63,7 +63,35 @@ struct MoeArgs {
   int hc = 0, refr = 1;
   const float *hc_h = nullptr, *hc_inj = nullptr;
   float *hc_out = nullptr;
+  // The shared expert in the reference's 8-bit affine form (q8_offsets), in place of an EXL3 shared
+  // slot (nslot == topk then): g = rr(gate . x), u = rr(up . x), h = rr(silu(g) u), o = rr(down . h) (rr: bf16 when
+  // refr); the combine adds the shared gate times o after the routed slots. Null: none.
+  const uint8_t *q8 = nullptr;
+  float *q8gu = nullptr;  // [R][2 inter] g, u (staged and batched paths)
+  float *q8o = nullptr;   // [R][hid] o
 };
+// Byte offsets inside the 8-bit shared expert's block: gate, up, down weight bytes, then their group words.
+constexpr int kQ8Group = 128;
+struct Q8Off {  // byte offsets inside the 8-bit block
+  uint64_t w[3], sb[3];
+};
+__host__ __device__ inline Q8Off q8_offsets(int hid, int inter) {
+  Q8Off o;
+  const uint64_t gu = (uint64_t)inter * hid;
+  o.w[0] = 0;
+  o.w[1] = gu;
+  o.w[2] = 2 * gu;
+  o.sb[0] = 3 * gu;
+  o.sb[1] = o.sb[0] + gu / kQ8Group * 4;
+  o.sb[2] = o.sb[1] + gu / kQ8Group * 4;
+  return o;
+}
+__host__ __device__ inline uint64_t q8_block_bytes(int hid, int inter) {
+  return 3 * (uint64_t)inter * hid + 3 * (uint64_t)inter * hid / kQ8Group * 4;
+}
+// the 8-bit shared expert's two launches for the staged and batched paths (moe_q8.hip): q8gu, then q8o
+void launch_moe_q8(const MoeArgs &a, hipStream_t s);
+bool moe_q8_supported(int hid, int inter);
 void launch_moe_router(const MoeArgs &a, hipStream_t s);
 void launch_moe_gateup(const MoeArgs &a, hipStream_t s);
 void launch_moe_down(const MoeArgs &a, hipStream_t s);
@@ -77,12 +105,15 @@ struct MoePlan {
   size_t part_floats = 0;
 };
 int moe_fused_grid();
-MoePlan moe_fused_plan(int hid, int inter, int topk, int nslot, int grid);
-bool moe_fused_supported(int K, int KS, int R, int hid, int inter, int ne, int topk);
+// q8: the 8-bit shared expert runs beside the routed work (its tagged hand-offs are added to the partials)
+MoePlan moe_fused_plan(int hid, int inter, int topk, int nslot, int grid, bool q8 = false);
+bool moe_fused_supported(int K, int KS, int R, int hid, int inter, int ne, int topk, bool q8 = false);
 inline size_t moe_fused_sync_words(int nslot, int hid, int inter) {
   return 64 * (1 + (size_t)nslot * (inter / 128) + hid / 128);
 }
 void launch_moe_fused(const MoeArgs &a, int grid, hipStream_t s);
+// u64 index in the fused step's partials of the 8-bit shared expert's tagged values: [2 inter] gate / up, [hid] down
+size_t moe_fused_q8_index(int hid, int inter, int nslot);
 const void *moe_fused_kernel(int K, int KS, int hid, int inter);  // nullptr if not instantiated
 // The batched layer (moe_batch.hip) for R >= 2 rows: device buffers sized by the host for R rows.
 struct MoeBatchBufs {
@@ -186,5 +217,6 @@ void launch_decode(const uint32_t *tiles, int IT, int OT, int K, uint16_t *w, hi
 void launch_fill_u32(uint32_t *p, uint64_t n, uint64_t seed, hipStream_t s);
 void launch_fill_scale_f16(uint16_t *p, uint64_t n, uint64_t seed, hipStream_t s);        // +-|N(1, 0.1)|
 void launch_fill_normal_bf16(uint16_t *p, uint64_t n, uint64_t seed, float stddev, hipStream_t s);
+void launch_fill_q8_sb(uint32_t *p, uint64_t n, int in, uint64_t seed, hipStream_t s);  // 8-bit group words
 
 }  // namespace ijah

@@ -1297,6 +1297,11 @@ __global__ __launch_bounds__(256) void bat_combine(MoeArgs a, const float *__res
         sh = make_float4(v[j][0], v[j][1], v[j][2], v[j][3]);
       }
   }
+  if (a.q8) {  // the 8-bit shared expert: its gate times its output
+    const float g = a.sgv[r];
+    const float4 o = *(const float4 *)(a.q8o + (uint64_t)r * a.hid + i);
+    sh = make_float4(g * o.x, g * o.y, g * o.z, g * o.w);
+  }
   *(float4 *)(a.y + (uint64_t)r * a.hid + i) =
       make_float4(moe_finish(a, r, i, y.x, sh.x), moe_finish(a, r, i + 1, y.y, sh.y), moe_finish(a, r, i + 2, y.z, sh.z),
                   moe_finish(a, r, i + 3, y.w, sh.w));

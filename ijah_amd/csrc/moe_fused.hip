@@ -336,6 +336,81 @@ __device__ __forceinline__ void prep_chunk(const float *x, int chunk, _Float16 *
   dst[kp(lane + 64)] = to_f16(v1);
 }
 
+// The 8-bit shared expert before the route (reference kernels/fn_moe.metal:40-46 and :264-290): wave kSpw + i takes
+// gate / up row b + G i (all waves of the grid together: the 2 inter rows) and stores it tagged (part_q8[row]); wave
+// kSpw then waits until all 2 inter are in, computes h = rr(silu(g) u) into LDS and sets s_q8; waves kSpw .. kSpw + 3
+// take the down rows b + G (i + 4 j) and store them tagged (part_q8[2 inter + row]), which the combine reads. The row
+// arithmetic is q8_dot (moe_device.h), as in the staged and batched paths.
+constexpr int kQ8GuWaves = 6, kQ8DnWaves = 4, kQ8DnPerWave = 4;
+template <int HID, int INTER>
+__device__ __forceinline__ void q8_shared(const MoeArgs &a, uint64_t *part_q8, uint32_t tag, float *hq, uint32_t *s_q8) {
+  constexpr int NQG = (HID + 1023) / 1024, NQD = (INTER + 1023) / 1024, NI = INTER / 64;
+  const int lane = threadIdx.x & 63, qi = (int)rfl(threadIdx.x >> 6) - kSpw, G = (int)gridDim.x, b = (int)blockIdx.x;
+  if (qi < 0 || qi >= kQ8GuWaves) return;
+  const Q8Off o = q8_offsets(HID, INTER);
+  const int grow = b + G * qi;
+  if (grow < 2 * INTER) {
+    const int proj = grow >= INTER ? 1 : 0, r = grow - proj * INTER;
+    Q8Row<NQG> w;
+    q8_load<NQG>(a.q8 + o.w[proj] + (uint64_t)r * HID, (const uint32_t *)(a.q8 + o.sb[proj]) + (uint64_t)r * (HID / kQ8Group),
+                 HID, w);
+    const float v = q8_dot<NQG>(w, a.x, HID);
+    if (lane == 0) st_tag(part_q8 + grow, moe_rr(v, a.refr), tag);
+  }
+  if (qi >= kQ8DnWaves) return;
+  Q8Row<NQD> dw[kQ8DnPerWave];  // this wave's down rows, requested before the wait for h
+#pragma unroll
+  for (int j = 0; j < kQ8DnPerWave; j++) {
+    const int row = b + G * (qi + kQ8DnWaves * j);
+    if (row < HID)
+      q8_load<NQD>(a.q8 + o.w[2] + (uint64_t)row * INTER,
+                   (const uint32_t *)(a.q8 + o.sb[2]) + (uint64_t)row * (INTER / kQ8Group), INTER, dw[j]);
+  }
+  if (qi == 0) {  // every gate / up row of the grid, then h into LDS
+    float gv[NI], uv[NI];
+    bool got = false;
+    for (uint32_t it = 0; it < kSpin; it++) {
+      bool all = true;
+#pragma unroll
+      for (int i = 0; i < NI; i++) {
+        const uint64_t tg = ld_cg(part_q8 + lane + 64 * i), tu = ld_cg(part_q8 + INTER + lane + 64 * i);
+        all = all && tag_ok(tg, tag) && tag_ok(tu, tag);
+        gv[i] = tag_val(tg);
+        uv[i] = tag_val(tu);
+      }
+      if (__all(all)) {
+        got = true;
+        break;
+      }
+      if ((it & 15u) == 15u && ld_relaxed(a.sync + kWordErr)) break;
+      __builtin_amdgcn_s_sleep(1);
+    }
+    if (!got && lane == 0) atomicOr(a.sync + kWordErr, 1u);
+#pragma unroll
+    for (int i = 0; i < NI; i++) hq[lane + 64 * i] = q8_act(gv[i], uv[i], a.refr);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    if (lane == 0) atomicOr(s_q8, 1u);
+  }
+  bool got = false;
+  for (uint32_t it = 0; it < kSpin; it++) {
+    if (__hip_atomic_load(s_q8, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) & 1u) {
+      got = true;
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+  if (!got && lane == 0) atomicOr(a.sync + kWordErr, 1u);
+  asm volatile("" ::: "memory");
+#pragma unroll
+  for (int j = 0; j < kQ8DnPerWave; j++) {
+    const int row = b + G * (qi + kQ8DnWaves * j);
+    if (row < HID) {
+      const float v = q8_dot<NQD>(dw[j], hq, INTER);
+      if (lane == 0) st_tag(part_q8 + 2 * INTER + row, moe_rr(v, a.refr), tag);
+    }
+  }
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------------------------------------------- the kernel
@@ -359,7 +434,8 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t csv[kMaxTopkV + 1][128]; // the combine's svh_d per slot
   __shared__ __attribute__((aligned(16))) float xl[HID];                    // the input row (staged at launch)
   __shared__ Route rt;
-  __shared__ uint32_t s_tag, s_ok;
+  __shared__ uint32_t s_tag, s_ok, s_q8;
+  __shared__ __attribute__((aligned(16))) float hq[INTER];                 // the 8-bit shared expert's h
   const int lane = threadIdx.x & 63, wave = (int)rfl(threadIdx.x >> 6);
   const int hs = a.nslot > a.topk ? 1 : 0;
   // ---- 0. every launch-time load at once, so that their latencies overlap rather than add: the router rows, the
@@ -407,6 +483,7 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
   if (threadIdx.x < kMaxGT) tcnt[threadIdx.x] = 0;
   if (threadIdx.x == 0) s_prep = 0;
   if (threadIdx.x == 0) s_hrdy = 0;
+  if (threadIdx.x == 0) s_q8 = 0;
   uint32_t ep_lo = (uint32_t)ep;
   asm volatile("" : "+v"(ep_lo));  // its first use here, after the plan words' request (not at the branch's end)
   if (wave == kCtl && lane == 0) s_tag = ep_lo + 1u;
@@ -435,6 +512,7 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
   };
   if (rrow) router_finish<HID>(a, rr, tag16);
   lds_barrier();  // this workgroup's logits are out: the router rows had HBM to themselves
+  if (a.q8) q8_shared<HID, INTER>(a, part_dn + (size_t)a.nslot * NBI * HID, tag, hq, &s_q8);
   const bool sprep_w = spk != kNone && wave >= kSpw && wave < kSpw + kGrp;
   if (sprep_w && lane < 16) {  // chunk c of the shared prep group's suh
     const int proj = (int)(spk / NKG), kc = (int)(spk % NKG) * kGrp + (wave - kSpw);
@@ -729,10 +807,17 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
     // thread: column o, slots g, g + 8, g + 16 (g = t / 128), all polled together
     const int g = threadIdx.x >> 7;
     const uint64_t *src = part_dn + c * 128 + o;
-    float sv[3] = {0.f, 0.f, 0.f};
+    const uint64_t *qsrc = part_dn + (size_t)a.nslot * NBI * HID + 2 * INTER + c * 128 + o;  // 8-bit shared o
+    const bool qpoll = a.q8 && g == 0;
+    float sv[3] = {0.f, 0.f, 0.f}, qv = 0.f;
     bool got = false;
     for (uint32_t it = 0; it < kSpin; it++) {
       bool all = true;
+      if (qpoll) {
+        const uint64_t t = ld_cg(qsrc);
+        all = tag_ok(t, tag);
+        qv = tag_val(t);
+      }
 #pragma unroll
       for (int q = 0; q < 3; q++) {
         const int ls = g + 8 * q;
@@ -772,7 +857,7 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
       const int i = c * 128 + wave * 64 + lane, oo = wave * 64 + lane;
       float yv = 0.f;
       for (int k = 0; k < a.topk; k++) yv += cv[(hs + k) * 128 + oo];
-      const float sh = hs ? cv[oo] : 0.f;
+      const float sh = hs ? cv[oo] : a.q8 ? rt.sg * qv : 0.f;
       a.y[i] = moe_finish(a, 0, i, yv, sh);
     }
   }
@@ -814,7 +899,7 @@ int moe_fused_grid() {
 
 // The work plan (see the kernel's header). Returns ok = false when the shape does not fit the kernel's per-wave
 // limits; the layer then runs the staged path.
-MoePlan moe_fused_plan(int hid, int inter, int topk, int nslot, int G) {
+MoePlan moe_fused_plan(int hid, int inter, int topk, int nslot, int G, bool q8) {
   MoePlan pl;
   const int NP = inter / 32, NG = NP / 4, NBI = inter / 128, NBLK = hid / 128, UPS = NBI * NBLK * 4;
   const int NKG = hid / (128 * kGrp), hs = nslot > topk ? 1 : 0, NCOL = nslot * 2 * NP;
@@ -901,14 +986,23 @@ MoePlan moe_fused_plan(int hid, int inter, int topk, int nslot, int G) {
   for (int c = 0; c < NBLK; c++) w[(size_t)(c * G / NBLK) * kPW + P_COMB] = (uint32_t)c;
   pl.words = w;
   // tagged partials (u64 = 2 floats): gate/up [column][NKG k groups][32], down [slot][cb][hid]
-  pl.part_floats = 2 * ((size_t)NCOL * NKG * 32 + (size_t)nslot * NBI * hid);
+  // and, with the 8-bit shared expert, its gate / up [2 inter] and down [hid] rows
+  pl.part_floats = 2 * ((size_t)NCOL * NKG * 32 + (size_t)nslot * NBI * hid + (q8 ? 2 * (size_t)inter + hid : 0));
   pl.grid = G;
   pl.ok = true;
   return pl;
 }
 
-bool moe_fused_supported(int K, int KS, int R, int hid, int inter, int ne, int topk) {
-  return R == 1 && step_fn(K, KS, hid, inter) != nullptr && ne <= kMaxExpertsV && topk <= kMaxTopkV;
+size_t moe_fused_q8_index(int hid, int inter, int nslot) {
+  const size_t NCOL = (size_t)nslot * 2 * (inter / 32), NKG = hid / (128 * kGrp), NBI = inter / 128;
+  return NCOL * NKG * 32 + (size_t)nslot * NBI * hid;
+}
+
+bool moe_fused_supported(int K, int KS, int R, int hid, int inter, int ne, int topk, bool q8) {
+  const int G = moe_fused_grid();
+  const bool q8ok = !q8 || (moe_q8_supported(hid, inter) && 2 * inter <= kQ8GuWaves * G &&
+                            hid <= kQ8DnWaves * kQ8DnPerWave * G);
+  return R == 1 && step_fn(K, KS, hid, inter) != nullptr && ne <= kMaxExpertsV && topk <= kMaxTopkV && q8ok;
 }
 
 void launch_moe_fused(const MoeArgs &a, int grid, hipStream_t s) {

@@ -8,6 +8,7 @@ activations bf16-representable N(0,1).
 Tensor names follow the reference pack (models/flash_next/layer.mm:180-196):
     <pre>gate.weight, <pre>shared_expert_gate.weight,
     <pre>switch_mlp.{gate,up,down}_proj.{trellis,suh,svh}, <pre>shared_expert.{gate,up,down}_proj.{trellis,suh,svh}
+    or, for the 8-bit affine shared expert, <pre>shared_expert.{gate,up,down}_proj.{weight,scales,biases}
 """
 import json
 import struct
@@ -38,18 +39,33 @@ def linear(rng, inp, out, K, lead=()):
     return t, scales(rng, *lead, inp), scales(rng, *lead, out)
 
 
+def q8_linear(rng, inp, out, group=128):
+    """8-bit affine (MLX layout, the reference's Q8): weight U32 [out, in/4] (uniform bytes, row-major), scales and
+    biases bf16 bits [out, in/group]: scale = |N(1, 0.1)| / (74 sqrt(in)) (a uniform byte's deviation is ~74), bias =
+    -127.5 scale, so the weights have mean ~0 and variance ~1/in"""
+    wb = rng.integers(0, 256, (out, inp), dtype=np.uint8)
+    sc = bf16(np.abs(rng.normal(1.0, 0.1, (out, inp // group))).astype(np.float32) / np.float32(74 * np.sqrt(inp)))
+    bi = bf16(np.float32(-127.5) * (sc.astype(np.uint32) << 16).view(np.float32))
+    return wb.view(np.uint32).reshape(out, inp // 4), sc, bi
+
+
 def moe_layer(seed, hid=2048, inter=512, ne=512, topk=10, K=5, shared=True, Ks=None, sgate=False):
-    """dict of numpy arrays for ne_moe_create / the oracle (keys as ijah_amd.engine.Engine.moe_create)."""
+    """dict of numpy arrays for ne_moe_create / the oracle (keys as ijah_amd.engine.Engine.moe_create).
+    shared: False, True (an EXL3 shared expert of Ks bits) or "q8" (the reference's 8-bit affine g128 one)."""
     rng = np.random.default_rng(seed)
     Ks = Ks or K
-    w = dict(hid=hid, inter=inter, ne=ne, topk=topk, K=K, Ks=Ks if shared else 0)
+    w = dict(hid=hid, inter=inter, ne=ne, topk=topk, K=K, Ks=Ks if shared is True else 0)
     w["router"] = bf16(rng.standard_normal((ne, hid)).astype(np.float32) / np.float32(np.sqrt(hid)))
     if sgate:
         w["sgate"] = bf16(rng.standard_normal(hid).astype(np.float32) / np.float32(np.sqrt(hid)))
     for p, (i, o) in (("gate", (hid, inter)), ("up", (hid, inter)), ("down", (inter, hid))):
         t, su, sv = linear(rng, i, o, K, (ne,))
         w[f"{p}.trellis"], w[f"{p}.suh"], w[f"{p}.svh"] = t, su, sv
-    if shared:
+    if shared == "q8":
+        for p, (i, o) in (("sq8_gate", (hid, inter)), ("sq8_up", (hid, inter)), ("sq8_down", (inter, hid))):
+            w[f"{p}.weight"], w[f"{p}.scales"], w[f"{p}.biases"] = q8_linear(rng, i, o)
+        w["qgroup"] = 128
+    elif shared:
         for p, (i, o) in (("sgate_proj", (hid, inter)), ("sup_proj", (hid, inter)), ("sdown_proj", (inter, hid))):
             t, su, sv = linear(rng, i, o, Ks)
             w[f"{p}.trellis"], w[f"{p}.suh"], w[f"{p}.svh"] = t, su, sv
@@ -58,7 +74,8 @@ def moe_layer(seed, hid=2048, inter=512, ne=512, topk=10, K=5, shared=True, Ks=N
 
 PACK_NAMES = {"gate": "switch_mlp.gate_proj", "up": "switch_mlp.up_proj", "down": "switch_mlp.down_proj",
               "sgate_proj": "shared_expert.gate_proj", "sup_proj": "shared_expert.up_proj",
-              "sdown_proj": "shared_expert.down_proj"}
+              "sdown_proj": "shared_expert.down_proj", "sq8_gate": "shared_expert.gate_proj",
+              "sq8_up": "shared_expert.up_proj", "sq8_down": "shared_expert.down_proj"}
 
 
 def moe_tensors(w, prefix):
@@ -105,7 +122,8 @@ def write_moe_pack(directory, w, layer=0, extra=None, shards=1):
     t = moe_tensors(w, prefix)
     if extra:
         t.update(extra)
-    bfn = {prefix + "gate.weight", prefix + "shared_expert_gate.weight"}
+    bfn = {prefix + "gate.weight", prefix + "shared_expert_gate.weight"} | \
+        {n for n in t if n.endswith(".scales") or n.endswith(".biases")}
     names = sorted(t)
     per = (len(names) + shards - 1) // shards
     for i in range(shards):

@@ -111,15 +111,22 @@ NE_API int ne_exl3_lin_decode(ne_exl3_lin *l, ne_buf *w, double *gpu_ms);
 
 /* ---- fused MoE layer (router + softmax/top-k + routed and shared EXL3 experts + weighted combine) ---- */
 typedef struct ne_moe ne_moe;
-/* Host arrays in the pack's layout (reference models/flash_next/layer.mm:180-196):
+/* Host arrays in the pack's layout (reference models/flash_next/layer.mm:180-196, MoeW of layer.h:37):
  *   router BF16 [ne][hid]; sgate BF16 [hid] or NULL (no shared_expert_gate: the shared expert is added with weight 1);
  *   routed gate/up/down: trellis U16 [ne][in/16][out/16][16K], suh F16 [ne][in], svh F16 [ne][out];
- *   shared gate/up/down (all NULL = no shared expert): trellis U16 [in/16][out/16][16 Ks], suh, svh. */
+ *   shared expert, at most one of two forms (all NULL = none):
+ *     EXL3: gate/up/down trellis U16 [in/16][out/16][16 Ks], suh, svh;
+ *     8-bit affine (the reference's Q8, layer.h:21; the form of its real packs): weight U32 [rows][in/4] (bytes
+ *     row-major), scales and biases BF16 [rows][in/qgroup], w = scale q + bias; qgroup 128; gate and up [inter][hid],
+ *     down [hid][inter]. Its outputs are rounded to bf16 as the reference's (kernels/fn_moe.metal:47,268,288). */
 typedef struct {
   int hid, inter, ne, topk, K, Ks;
   const uint16_t *router, *sgate;
   const uint16_t *gt, *ut, *dt, *gsu, *gsv, *usu, *usv, *dsu, *dsv;
   const uint16_t *sgt, *sut, *sdt, *sgsu, *sgsv, *susu, *susv, *sdsu, *sdsv;
+  int qgroup;
+  const uint32_t *qgw, *quw, *qdw;
+  const uint16_t *qgs, *qgb, *qus, *qub, *qds, *qdb;
 } ne_moe_desc;
 NE_API ne_moe *ne_moe_create(const ne_moe_desc *d);
 /* reference models/flash_next/layer.mm:180-196 (MoeW from "<prefix>gate.weight", "switch_mlp.*", "shared_expert.*",
@@ -127,7 +134,8 @@ NE_API ne_moe *ne_moe_create(const ne_moe_desc *d);
  * re-laid so each expert's trellis tiles, suh and svh are one contiguous 256-byte-aligned block in HBM. */
 NE_API ne_moe *ne_moe_load(const ne_pack *p, const char *prefix, int topk);
 /* Seeded synthetic layer generated on the device (no host copy): trellis uniform u16, suh / svh = +-|N(1, 0.1)|,
- * router BF16 N(0, 1/hid) (logits ~ N(0,1) for N(0,1) inputs). has_shared: 1 = a shared expert of Ks bits.
+ * router BF16 N(0, 1/hid) (logits ~ N(0,1) for N(0,1) inputs). has_shared: 1 = an EXL3 shared expert of Ks bits,
+ * 2 = an 8-bit affine one (g128: weight bytes uniform, scale = |N(1, 0.1)| / (74 sqrt(in)), bias = -127.5 scale).
  * No reference counterpart (the reference benchmarks real packs); it feeds the benchmark at full size. */
 NE_API ne_moe *ne_moe_synth(int hid, int inter, int ne, int topk, int K, int has_shared, int Ks, uint64_t seed);
 NE_API void ne_moe_free(ne_moe *m);
@@ -150,7 +158,8 @@ NE_API int ne_moe_run_hc(ne_moe *m, int R, const ne_buf *x, uint64_t x_off, ne_b
 /* reference models/flash_next/layer.h:258-262 (ne_fn_layer_read) for the MoE intermediates of the last run:
  * "logits" f32 [R][ne], "route" u32 [R][2 topk] (ids, f32 weight bits), "shared_gate" f32 [R],
  * "experts_gu" f32 [R][slots][2][inter] (gate / up inner outputs before H_out), "experts_dn" f32 [R][slots][hid]
- * (down inner outputs before H_out), "mlp_out" f32 [R][hid]. Copies at most nbytes; returns 0. */
+ * (down inner outputs before H_out), "mlp_out" f32 [R][hid], "shared_q8" f32 [R][hid] (the 8-bit shared expert's
+ * rounded output before its gate). Copies at most nbytes; returns 0. */
 NE_API int ne_moe_read(ne_moe *m, const char *name, void *dst, uint64_t nbytes);
 /* Expert e's projection proj (0 gate, 1 up, 2 down; e == ne: the shared expert) decoded from the re-laid HBM block:
  * fp16 bits [in][out] into w. */

@@ -447,6 +447,40 @@ static void expert_emul(const lin_view L[3], const float *x, float wk, float *v_
   free(xh);
 }
 
+void orc_q8_linear(const float *x, int R, const uint8_t *w, const uint16_t *s, const uint16_t *b, int in, int out,
+                   int group, float *y) {
+  const int ng = in / group;
+  for (int r = 0; r < R; r++)
+    for (int o = 0; o < out; o++) {
+      double acc = 0.0;
+      for (int g = 0; g < ng; g++) {
+        double qx = 0.0, sx = 0.0; /* dot16q: (sum q x, sum x) per chunk, here per group */
+        for (int i = g * group; i < (g + 1) * group; i++) {
+          const double xv = x[(size_t)r * in + i];
+          qx += (double)w[(size_t)o * in + i] * xv;
+          sx += xv;
+        }
+        acc += (double)orc_bf16_to_f32(s[(size_t)o * ng + g]) * qx + (double)orc_bf16_to_f32(b[(size_t)o * ng + g]) * sx;
+      }
+      y[(size_t)r * out + o] = (float)acc;
+    }
+}
+
+void orc_q8_shared(const orc_moe *m, const float *x, int refr, float *o) {
+  const int hid = m->hid, inter = m->inter;
+  float *g = (float *)malloc(sizeof(float) * (size_t)inter), *u = (float *)malloc(sizeof(float) * (size_t)inter);
+  orc_q8_linear(x, 1, m->qgw, m->qgs, m->qgb, hid, inter, m->qgroup, g);
+  orc_q8_linear(x, 1, m->quw, m->qus, m->qub, hid, inter, m->qgroup, u);
+  for (int j = 0; j < inter; j++) {
+    const float gv = rr_(g[j], refr), uv = rr_(u[j], refr);
+    g[j] = rr_(gv / (1.0f + expf(-gv)) * uv, refr); /* kernels/fn_moe.metal:267-268 */
+  }
+  orc_q8_linear(g, 1, m->qdw, m->qds, m->qdb, inter, hid, m->qgroup, o);
+  for (int c = 0; c < hid; c++) o[c] = rr_(o[c], refr); /* :288 rr(simd_sum) */
+  free(g);
+  free(u);
+}
+
 /* y[r] = sum over slots k in order (v_k) + sg * v_shared: the finisher's fixed slot order (kernels/fn_moe.metal:440-447,
  * kernels/prefill/pf_moe.metal:149-155); the shared expert's gate is sigmoid(logit) when the pack has
  * shared_expert_gate, else 1. */
@@ -469,6 +503,11 @@ int orc_moe_experts(const orc_moe *m, const float *x, int R, const uint32_t *rou
       lin_view L[3] = {shared(m, 0), shared(m, 1), shared(m, 2)};
       expert_emul(L, xr, sg ? sg[r] : 1.0f, v);
       for (int j = 0; j < hid; j++) yr[j] += v[j];
+    }
+    if (m->qgw) { /* the 8-bit shared expert, reference rounding on */
+      orc_q8_shared(m, xr, 1, v);
+      const float gk = sg ? sg[r] : 1.0f;
+      for (int j = 0; j < hid; j++) yr[j] += gk * v[j];
     }
   }
   free(v);
@@ -528,6 +567,12 @@ int orc_moe_experts_exact(const orc_moe *m, const float *x, int R, const uint32_
       lin_view L[3] = {shared(m, 0), shared(m, 1), shared(m, 2)};
       expert_exact(L, x + (size_t)r * hid, sg ? sg[r] : 1.0, v);
       for (int j = 0; j < hid; j++) yr[j] += v[j];
+    }
+    if (m->qgw) { /* no bf16 rounding points: the plain f64 shared expert */
+      float *o = (float *)malloc(sizeof(float) * (size_t)hid);
+      orc_q8_shared(m, x + (size_t)r * hid, 0, o);
+      for (int j = 0; j < hid; j++) yr[j] += (sg ? sg[r] : 1.0) * (double)o[j];
+      free(o);
     }
   }
   free(v);
@@ -654,6 +699,10 @@ int orc_moe_layer_hc(const orc_moe *m, const float *x, int R, int hc, int refr, 
     if (m->sgt) {
       lin_view L[3] = {shared(m, 0), shared(m, 1), shared(m, 2)};
       expert_emul(L, xr, sg, t);
+    }
+    if (m->qgw) {
+      orc_q8_shared(m, xr, refr, t);
+      for (int j = 0; j < hid; j++) t[j] *= sg;
     }
     orc_hc_write(s, t, 1, hid, hc, refr, h + (size_t)r * hc * hid, inj + (size_t)r * 8, y + (size_t)r * hid,
                  hout + (size_t)r * hc * hid);

@@ -87,7 +87,19 @@ typedef struct {
   /* shared expert (NULL = none): same per-projection layout without the expert dim; bits Ks */
   int Ks;
   const uint16_t *sgt, *sut, *sdt, *sgsu, *sgsv, *susu, *susv, *sdsu, *sdsv;
+  /* the shared expert in 8-bit affine form instead (NULL qgw = none; exclusive with sgt): weight bytes [rows][in]
+   * (gate/up [inter][hid], down [hid][inter]), scales / biases BF16 [rows][in / qgroup] */
+  int qgroup;
+  const uint8_t *qgw, *quw, *qdw;
+  const uint16_t *qgs, *qgb, *qus, *qub, *qds, *qdb;
 } orc_moe;
+/* 8-bit affine linear (kernels/ne_common.h:33-88 q8row_dev / dot16q, MLX layout): y[r][o] = sum over groups g of
+ * s[o][g] sum_{i in g} q[o][i] x[r][i] + b[o][g] sum_{i in g} x[r][i], summed in f64, returned in f32 */
+void orc_q8_linear(const float *x, int R, const uint8_t *w, const uint16_t *s, const uint16_t *b, int in, int out,
+                   int group, float *y);
+/* the layer's 8-bit shared expert on one row (kernels/fn_moe.metal:40-47, :264-290): g = rr(gate x), u = rr(up x),
+ * h = rr(silu(g) u), o = rr(down h); rr = bf16 when refr. o [hid]. */
+void orc_q8_shared(const orc_moe *m, const float *x, int refr, float *o);
 /* kernel arithmetic; y [R][hid] f32; logits [R][ne] (may be NULL); route [R][2 topk] u32 (ids, f32 weight bits,
  * may be NULL). Returns 0. */
 int orc_moe_layer(const orc_moe *m, const float *x, int R, float *y, float *logits, uint32_t *route);

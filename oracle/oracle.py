@@ -33,7 +33,8 @@ class _Moe(C.Structure):
                 ("dsv", C.c_void_p), ("Ks", C.c_int),
                 ("sgt", C.c_void_p), ("sut", C.c_void_p), ("sdt", C.c_void_p), ("sgsu", C.c_void_p),
                 ("sgsv", C.c_void_p), ("susu", C.c_void_p), ("susv", C.c_void_p), ("sdsu", C.c_void_p),
-                ("sdsv", C.c_void_p)]
+                ("sdsv", C.c_void_p), ("qgroup", C.c_int)] + \
+               [(n, C.c_void_p) for n in ("qgw", "quw", "qdw", "qgs", "qgb", "qus", "qub", "qds", "qdb")]
 
 
 _lib = None
@@ -80,6 +81,11 @@ def lib():
         L.orc_moe_experts.argtypes = [C.POINTER(_Moe), _f32p, C.c_int, _u32p, C.c_void_p, _f32p]
         L.orc_moe_experts_exact.restype = C.c_int
         L.orc_moe_experts_exact.argtypes = [C.POINTER(_Moe), _f32p, C.c_int, _u32p, C.c_void_p, _f64p]
+        L.orc_q8_linear.restype = None
+        L.orc_q8_linear.argtypes = [_f32p, C.c_int, np.ctypeslib.ndpointer(np.uint8, flags="C_CONTIGUOUS"), _u16p,
+                                    _u16p, C.c_int, C.c_int, C.c_int, _f32p]
+        L.orc_q8_shared.restype = None
+        L.orc_q8_shared.argtypes = [C.POINTER(_Moe), _f32p, C.c_int, _f32p]
         L.orc_moe_experts_fast.restype = C.c_int
         L.orc_moe_experts_fast.argtypes = [C.POINTER(_Moe), _f32p, C.c_int, _u32p, C.c_void_p, _f32p, C.c_int]
         _lib = L
@@ -203,7 +209,32 @@ class MoeWeights:
         m.sgsu, m.sgsv, m.susu, m.susv = (p("sgate_proj.suh"), p("sgate_proj.svh"), p("sup_proj.suh"),
                                           p("sup_proj.svh"))
         m.sdsu, m.sdsv = p("sdown_proj.suh"), p("sdown_proj.svh")
+        if g.get("sq8_gate.weight") is not None:  # the 8-bit affine shared expert (bytes of the U32 weights)
+            m.qgroup = g.get("qgroup", 128)
+            m.qgw, m.quw, m.qdw = p("sq8_gate.weight"), p("sq8_up.weight"), p("sq8_down.weight")
+            m.qgs, m.qgb, m.qus, m.qub = (p("sq8_gate.scales"), p("sq8_gate.biases"), p("sq8_up.scales"),
+                                          p("sq8_up.biases"))
+            m.qds, m.qdb = p("sq8_down.scales"), p("sq8_down.biases")
         self.m = m
+
+
+def q8_linear(x, w_u32, scales, biases, group=128):
+    """8-bit affine linear (kernels/ne_common.h:33-88): x f32 [R, in], weight U32 [out, in/4] (bytes), scales /
+    biases bf16 bits [out, in/group] -> y f32 [R, out]"""
+    x = _c(np.atleast_2d(x), np.float32)
+    w = _c(w_u32, np.uint32)
+    out, inp = w.shape[0], w.shape[1] * 4
+    y = np.zeros((x.shape[0], out), np.float32)
+    lib().orc_q8_linear(x, x.shape[0], w.view(np.uint8), _c(scales, np.uint16), _c(biases, np.uint16), inp, out,
+                        group, y)
+    return y
+
+
+def q8_shared(W, x, refr=True):
+    """the layer's 8-bit shared expert on one row x [hid] -> o [hid] (rr'd when refr)"""
+    o = np.zeros(W.m.hid, np.float32)
+    lib().orc_q8_shared(C.byref(W.m), _c(x, np.float32).reshape(-1), int(bool(refr)), o)
+    return o
 
 
 def moe_layer(W, x):

@@ -91,3 +91,28 @@ def test_moe_load_rejects_wrong_shapes(eng, tmp_path):
     p = eng.pack_open(tmp_path)
     assert eng.lib.ne_moe_load(p.ptr, prefix.encode(), 2) is None
     assert "up_proj.trellis has shape" in eng.last_error()
+
+
+@pytest.mark.parametrize("case", ["q8_group64", "bf16_dense", "unknown_part", "gate_without_expert"])
+def test_moe_load_refuses_unsupported_shared_expert(eng, tmp_path, case):
+    """A shared expert in a form the layer does not take is refused with a message, never silently dropped."""
+    kind = "q8" if case in ("q8_group64",) else False
+    w = synth.moe_layer(3, hid=256, inter=128, ne=4, topk=2, K=5, shared=kind, sgate=True)
+    pre = "language_model.model.layers.0.mlp."
+    extra = {}
+    if case == "q8_group64":  # scales / biases of 64-wide groups (the reference's fn_moe takes g128 only)
+        rng = np.random.default_rng(1)
+        for p, i, o in (("gate", 256, 128), ("up", 256, 128), ("down", 128, 256)):
+            wq, sc, bi = synth.q8_linear(rng, i, o, group=64)
+            w[f"sq8_{p}.weight"], w[f"sq8_{p}.scales"], w[f"sq8_{p}.biases"] = wq, sc, bi
+    elif case == "bf16_dense":
+        extra[pre + "shared_expert.gate_proj.weight"] = np.zeros((128, 256), np.uint16)
+    elif case == "unknown_part":
+        extra[pre + "shared_expert.gate_proj.qweight"] = np.zeros((128, 64), np.uint32)
+    prefix = synth.write_moe_pack(tmp_path, w, extra=extra)
+    assert prefix == pre
+    p = eng.pack_open(tmp_path)
+    assert eng.lib.ne_moe_load(p.ptr, prefix.encode(), 2) is None
+    msg = eng.last_error()
+    assert {"q8_group64": "group 64", "bf16_dense": "weight", "unknown_part": "shared expert in a form",
+            "gate_without_expert": "without a shared expert"}[case] in msg, msg

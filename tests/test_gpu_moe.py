@@ -405,3 +405,107 @@ def test_hc_read_then_moe_hc_write(eng, oracle):
     for g, wv in ((y, want_y), (hout, want_o)):
         assert (g == wv).mean() > 0.97 and rel(g, wv) < 3e-3
     assert np.all(np.abs(inj[:, :4]) <= 2) and np.all(inj[:, 4:] > 0)  # gates 2 sigmoid, 1/rms
+
+
+# ---------------------------------------------------------------------------------------------- 8-bit shared expert
+def check_q8_layer(eng, oracle, moe, W, x, sgate):
+    """The layer with the reference's 8-bit affine shared expert (kernels/fn_moe.metal:40-46, :264-290): the shared
+    output o = rr(down . rr(silu(rr g) rr u)) within one bf16 step of the oracle's (the GPU's f32 sums and the
+    oracle's f64 ones may round to neighbouring bf16 values), >= 95% of it bit-exact; the layer within rel-L2 1e-3 of
+    the oracle's kernel arithmetic on the GPU's route and within 1e-2 of the f64 layer."""
+    R = x.shape[0]
+    y = moe.run(x)
+    rt, sg = moe.read("route", R), moe.read("shared_gate", R)
+    o = moe.read("shared_q8", R)
+    for r in range(R):
+        want = oracle.q8_shared(W, x[r])
+        assert np.mean(o[r] == want) > 0.95, (r, np.mean(o[r] == want))
+        assert np.all(np.abs(o[r] - want) <= np.abs(want) * 2 ** -6 + 1e-6), r
+    sgv = sg if sgate else None
+    assert rel(y, oracle.moe_experts(W, x, rt, sg=sgv)) < 1e-3
+    assert rel(y, oracle.moe_experts(W, x, rt, sg=sgv, exact=True)) < 1e-2
+    return y
+
+
+@pytest.mark.parametrize("R", [1, 3, 16, 40])
+def test_moe_q8_shared_expert(eng, oracle, R):
+    """R = 1 runs the fused one-row step, 3 and 16 the few-row kernels, 40 the many-row ones; each with the 8-bit
+    shared expert and its gate."""
+    print(f"moe q8 shared R{R}", flush=True)
+    w = synth.moe_layer(150 + R, hid=2048, inter=512, ne=64, topk=10, K=5, shared="q8", sgate=True)
+    m = eng.moe_create(w)
+    x = synth.bf16_values(np.random.default_rng(151 + R), R, 2048)
+    y = check_q8_layer(eng, oracle, m, oracle.MoeWeights(w), x, True)
+    assert np.array_equal(y, m.run(x))
+
+
+@pytest.mark.parametrize("R", [1, 4])
+def test_moe_q8_reference_shape(eng, oracle, R):
+    """The reference's own shape (hidden 2560, inter 640; kernels/fn_moe.metal:16) with its 8-bit shared expert."""
+    print(f"moe q8 shared 2560x640 R{R}", flush=True)
+    w = synth.moe_layer(160 + R, hid=2560, inter=640, ne=32, topk=10, K=5, shared="q8", sgate=True)
+    m = eng.moe_create(w)
+    check_q8_layer(eng, oracle, m, oracle.MoeWeights(w), synth.bf16_values(np.random.default_rng(161), R, 2560), True)
+
+
+def test_moe_q8_verify_rows_bit_identical_to_one_row(eng):
+    """With the 8-bit shared expert, every row of a 16-row verify batch equals the fused one-row step on that row,
+    bit for bit (the shared rows' dot is the same function in both paths)."""
+    print("moe q8 verify rows vs one row", flush=True)
+    w = synth.moe_layer(170, hid=2048, inter=512, ne=64, topk=10, K=5, shared="q8", sgate=True)
+    m = eng.moe_create(w)
+    x = synth.bf16_values(np.random.default_rng(171), 16, 2048)
+    _rows_match_one_row(m, x, 16)
+    m.run(x)
+    o16 = m.read("shared_q8", 16)
+    for i in (0, 7, 15):
+        m.run(x[i:i + 1])
+        assert np.array_equal(m.read("shared_q8", 1)[0], o16[i]), i
+
+
+def test_moe_q8_pack_loader(eng, oracle, tmp_path):
+    """A pack whose shared expert is 8-bit (.weight U32 / .scales / .biases BF16, g128, the reference's real layout)
+    loads through ne_moe_load and gives the same output as the arrays."""
+    w = synth.moe_layer(180, hid=1024, inter=256, ne=16, topk=4, K=5, shared="q8", sgate=True)
+    prefix = synth.write_moe_pack(tmp_path, w, layer=2)
+    a, b = eng.moe_load(eng.pack_open(tmp_path), prefix, 4), eng.moe_create(w)
+    x = synth.bf16_values(np.random.default_rng(181), 2, 1024)
+    assert np.array_equal(a.run(x), b.run(x))
+    assert np.array_equal(a.run(x[:1]), b.run(x[:1]))
+    check_q8_layer(eng, oracle, a, oracle.MoeWeights(w), x, True)
+
+
+def test_moe_q8_hc_write(eng, oracle):
+    """The hyper-connection write with the 8-bit shared expert, rounding on: the branch and the streams against the
+    oracle layer with the write (rr(sigmoid) gate, rr(gate * o))."""
+    print("moe q8 hc write", flush=True)
+    w = synth.moe_layer(190, hid=2048, inter=512, ne=64, topk=10, K=5, shared="q8", sgate=True)
+    W = oracle.MoeWeights(w)
+    m = eng.moe_create(w)
+    rng = np.random.default_rng(191)
+    for R in (1, 4):
+        x = synth.bf16_values(rng, R, 2048)
+        h = rng.standard_normal((R, 4, 2048)).astype(np.float32)
+        inj = rng.standard_normal((R, 8)).astype(np.float32)
+        xb, yb, hb, ib, ob = (eng.from_numpy(x), eng.alloc(R * 2048 * 4), eng.from_numpy(h), eng.from_numpy(inj),
+                              eng.alloc(h.nbytes))
+        m.run_hc(R, xb, yb, hb, ib, ob, hc=4, refr=True)
+        y, hout = yb.download(np.float32, (R, 2048)), ob.download(np.float32, h.shape)
+        wy, whout = oracle.moe_layer_hc(W, x, h, inj, refr=True)
+        assert np.mean(y == wy) > 0.9 and rel(y, wy) < 3e-3, (R, np.mean(y == wy), rel(y, wy))
+        assert rel(hout, whout) < 3e-3
+
+
+def test_few_row_pool_shared_by_layers(eng):
+    """Two layers of one shape share the few-row kernels' scratch pool: layer A at 4 rows, then B at 32 rows (the
+    pool grows), then A at 4 rows again gives A's first output (A takes the pool's current arrays)."""
+    print("moe few-row pool shared by layers", flush=True)
+    a = eng.moe_synth(1024, 256, 64, 8, 5, True, 5, seed=21)
+    b = eng.moe_synth(1024, 256, 64, 8, 5, True, 5, seed=22)
+    rng = np.random.default_rng(23)
+    x4, x32 = synth.bf16_values(rng, 4, 1024), synth.bf16_values(rng, 32, 1024)
+    y4 = a.run(x4)
+    yb = b.run(x32)
+    assert np.array_equal(a.run(x4), y4)
+    assert np.array_equal(b.run(x32), yb)
+    assert np.array_equal(a.run(x4), y4)

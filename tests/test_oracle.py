@@ -498,3 +498,80 @@ def test_hc_read_vs_f64(oracle):
     assert np.linalg.norm(out - want_out) / np.linalg.norm(want_out) < 3e-3
     assert np.allclose(inj[:, :4], 2 / (1 + np.exp(-ip.sum(axis=1) / 4)), rtol=1e-5)
     assert np.allclose(inj[:, 4:], inv, rtol=1e-6)
+
+
+# ---------------------------------------------------------------------------------------------- 8-bit shared expert
+def _bf(u16):
+    return (np.asarray(u16, np.uint32) << 16).view(np.float32).astype(np.float64)
+
+
+def _dequant(w_u32, sc, bi, group=128):
+    """the explicit matrix W[o][i] = scale[o][i / group] q[o][i] + bias[o][i / group] (MLX affine, f64)"""
+    q = np.ascontiguousarray(w_u32).view(np.uint8).astype(np.float64)
+    return q * np.repeat(_bf(sc), group, axis=1) + np.repeat(_bf(bi), group, axis=1)
+
+
+def _rr(v):
+    """round f32 values to bf16 (RNE) and back"""
+    u = np.ascontiguousarray(v, np.float32).view(np.uint32)
+    return ((u + np.uint32(0x7FFF) + ((u >> 16) & np.uint32(1))) & np.uint32(0xFFFF0000)).view(np.float32)
+
+
+@pytest.mark.parametrize("inp,out", [(256, 64), (2048, 32), (640, 16)])
+def test_q8_linear_vs_dequantized_matrix(oracle, inp, out):
+    """orc_q8_linear against x @ W^T with W dequantized explicitly; a dropped bias or a scale on the wrong group fails"""
+    from ijah_amd import synth
+    rng = np.random.default_rng(inp + out)
+    w, sc, bi = synth.q8_linear(rng, inp, out)
+    x = rng.standard_normal((3, inp)).astype(np.float32)
+    W = _dequant(w, sc, bi)
+    want = x.astype(np.float64) @ W.T
+    got = oracle.q8_linear(x, w, sc, bi)
+    assert np.abs(got - want).max() <= 1e-5 * np.abs(want).max()
+    # mutations the check must catch: no bias; each group's scale and bias taken from the next group
+    assert np.abs(x.astype(np.float64) @ (W - np.repeat(_bf(bi), 128, axis=1)).T - got).max() > 1e-3 * np.abs(got).max()
+    if inp > 128:
+        Ws = _dequant(w, np.roll(sc, 1, axis=1), np.roll(bi, 1, axis=1))
+        assert np.abs(x.astype(np.float64) @ Ws.T - got).max() > 1e-3 * np.abs(got).max()
+
+
+def test_q8_shared_closed_form(oracle):
+    """the layer's 8-bit shared expert: g, u, h, o with the reference's bf16 rounding points (kernels/fn_moe.metal:47,
+    268, 288), against numpy on the dequantized matrices; with the rounding off it is the plain f64 SwiGLU"""
+    from ijah_amd import synth
+    w = synth.moe_layer(71, hid=1024, inter=256, ne=4, topk=2, K=5, shared="q8")
+    W = oracle.MoeWeights(w)
+    x = synth.bf16_values(np.random.default_rng(72), 1, 1024)[0]
+    Wg, Wu, Wd = (_dequant(w[f"sq8_{p}.weight"], w[f"sq8_{p}.scales"], w[f"sq8_{p}.biases"]) for p in
+                  ("gate", "up", "down"))
+    g, u = Wg @ x, Wu @ x
+    h = g / (1 + np.exp(-g)) * u
+    plain = Wd @ h
+    assert np.abs(oracle.q8_shared(W, x, refr=False) - plain).max() <= 1e-5 * np.abs(plain).max()
+    g, u = _rr(g), _rr(u)
+    h = _rr((g.astype(np.float64) / (1 + np.exp(-g.astype(np.float64))) * u).astype(np.float32))
+    o = _rr((Wd @ h).astype(np.float32))
+    got = oracle.q8_shared(W, x, refr=True)
+    assert np.mean(got == o) > 0.97 and np.all(np.abs(got - o) <= np.abs(o) * 2 ** -7 + 1e-7)
+    assert np.array_equal(got, _rr(got))  # bf16-valued
+    # the rounding points matter: without them the result differs
+    assert np.mean(oracle.q8_shared(W, x, refr=False) == got) < 0.5
+
+
+def test_moe_layer_q8_shared_term(oracle):
+    """the layer with an 8-bit shared expert = the routed slots in slot order + sg * o (o = the shared expert)"""
+    from ijah_amd import synth
+    w = synth.moe_layer(73, hid=512, inter=128, ne=8, topk=3, K=5, shared="q8", sgate=True)
+    W = oracle.MoeWeights(w)
+    routed = dict(w)
+    for k in [k for k in w if k.startswith("sq8_")]:
+        del routed[k]
+    Wr = oracle.MoeWeights(routed)
+    x = synth.bf16_values(np.random.default_rng(74), 2, 512)
+    y, lg, rt = oracle.moe_layer(W, x)
+    sg = np.array([1 / (1 + np.exp(-np.float32(oracle.router_logits(x[r], w["sgate"][None])[0]))) for r in range(2)],
+                  np.float32)
+    s = oracle.moe_experts(Wr, x, rt, sg=sg)
+    for r in range(2):
+        want = s[r] + sg[r] * oracle.q8_shared(W, x[r])
+        assert np.allclose(y[r], want, rtol=1e-6, atol=1e-7)
