@@ -62,7 +62,10 @@ def cpu_baseline(seconds=10.0):
     w = synth.moe_layer(99, hid=HID, inter=INTER, ne=NE, topk=TOPK, K=K, shared=True, Ks=K)
     W = O.MoeWeights(w)
     xs = synth.bf16_values(rng, 64, HID)
-    threads = min(os.cpu_count() or 1, 16)
+    # the host's cores, as many as this process may use: the GPU box grants each job a CPU share through
+    # OMP_NUM_THREADS (16 per GPU), whatever nproc reports
+    host = os.cpu_count() or 1
+    threads = min(host, int(os.environ.get("OMP_NUM_THREADS") or host))
     n, t0 = 0, time.perf_counter()
     while True:
         x = xs[n % len(xs)][None]
@@ -76,7 +79,8 @@ def cpu_baseline(seconds=10.0):
             break
     us = el / n * 1e6
     total = sum(kernel_bytes().values())
-    return {"value": round(total / (us * 1e-6) / 1e9, 3), "unit": "GB/s", "cores": int(used), "kind": "port",
+    return {"value": round(total / (us * 1e-6) / 1e9, 3), "unit": "GB/s", "cores": int(used), "host_cores": host,
+            "cpu_share": f"OMP_NUM_THREADS={os.environ.get('OMP_NUM_THREADS', 'unset')}", "kind": "port",
             "us_per_layer": round(us, 1),
             "sample": f"{n} M=1 layers over 64 input rows (router 512x2048 + top-10 + 11 K5 experts of 2048x512x3, "
                       f"all 512 experts resident in host memory) in {el:.1f}s"}
@@ -188,14 +192,53 @@ def run_trunk_eager(eng, steps, seed):
     return {"trunk_eager_runs": out}
 
 
+class Probes:
+    """The measurement probes' own library (ijah_amd/_lib/libijah_probes.so, kept out of the product library):
+    ijah_probe_run launches a probe kernel by name on device addresses of the engine's buffers."""
+
+    def __init__(self):
+        import ctypes as C
+        self.C = C
+        self.lib = C.CDLL(str(ROOT / "ijah_amd" / "_lib" / "libijah_probes.so"))
+        f = self.lib.ijah_probe_run
+        f.restype = C.c_int
+        f.argtypes = [C.c_char_p, C.c_int, C.c_int, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_uint, C.c_int,
+                      C.POINTER(C.c_double), C.c_char_p, C.c_int]
+
+    def run(self, name, args, grid, tg, K=-1, variant=-1, tg_mem=0, reps=1):
+        """args: Buf, (Buf, byte offset) or a numpy scalar; returns the GPU ms of `reps` launches"""
+        C = self.C
+        slots = []
+        for a in args:
+            if isinstance(a, tuple):
+                slots.append(a[0].gpu_address() + int(a[1]))
+            elif hasattr(a, "gpu_address"):
+                slots.append(a.gpu_address())
+            else:
+                slots.append(int(np.asarray(a).astype(np.int64)) & 0xFFFFFFFFFFFFFFFF)
+        arr = (C.c_uint64 * len(slots))(*slots)
+        ms, err = C.c_double(0), C.create_string_buffer(256)
+        rc = self.lib.ijah_probe_run(name.encode(), K, variant, arr, len(slots), (C.c_uint * 3)(*grid),
+                                     (C.c_uint * 3)(*tg), tg_mem, reps, C.byref(ms), err, 256)
+        if rc:
+            raise RuntimeError(f"probe {name}: {err.value.decode()}")
+        return ms.value
+
+
 def run_stream_probe(eng, total_mb=24, region_mb=2048):
     """probe_stream: 256 workgroups x 16 waves (the fused step's shape) stream total_mb of cold data (a different
     slice of a region_mb buffer each launch, beyond the 256 MB last-level cache), per wave total_mb / 4096, into LDS
     (mode 0) or registers (mode 1); and the same bytes over 1024 x 4 waves. us per launch (median of 8)."""
+    pl = Probes()
     region = eng.alloc(region_mb << 20)
     res = eng.alloc(4096 * 64 * 4)
     out = {}
     nb = total_mb << 20
+    # one pass over the whole region first: the first touch of its pages (address translation) would otherwise be
+    # charged to whichever shape runs first
+    for off in range(0, (region_mb << 20) - nb + 1, nb):
+        pl.run("probe_stream", [(region, off), np.uint32(nb // 4096 // 1024 * 1024), np.int32(1), res], (256, 1, 1),
+               (1024, 1, 1), tg_mem=16 * 4096)
     for shape in ((256, 1024), (512, 512), (1024, 256)):
         waves = shape[0] * shape[1] // 64
         per = nb // waves // 1024 * 1024
@@ -204,8 +247,8 @@ def run_stream_probe(eng, total_mb=24, region_mb=2048):
             for i in range(10):
                 if off + nb > (region_mb << 20):
                     off = 0
-                t = eng.run_kernel("probe_stream", [(region, off), np.uint32(per), np.int32(mode), res],
-                                   (shape[0], 1, 1), (shape[1], 1, 1), tg_mem=(shape[1] // 64) * 4096)
+                t = pl.run("probe_stream", [(region, off), np.uint32(per), np.int32(mode), res],
+                           (shape[0], 1, 1), (shape[1], 1, 1), tg_mem=(shape[1] // 64) * 4096)
                 off += nb
                 if i >= 2:
                     ts.append(t)
@@ -221,7 +264,8 @@ def run_probes(eng, iters=4000):
     """probe_mix (ijah_amd/csrc/probes.hip) on every CU at 1, 2, 4 and 8 waves per SIMD: mode 0 decode only, 1 MFMA
     only, 2 decode feeding each wave's MFMA chain, 3 even waves decode / odd waves MFMA (ms per launch). Decode: weights
     per second and SIMD cycles per weight at the measured shader clock; MFMA: dense f16 TFLOP/s."""
-    cus = eng.device_info().get("cus", 256) if hasattr(eng, "device_info") else 256
+    cus = 256
+    pl = Probes()
     out = {}
     for K in (5, 8):
         rng = np.random.default_rng(K)
@@ -231,10 +275,10 @@ def run_probes(eng, iters=4000):
             res = eng.alloc(grid * 4 * 64 * 4)
             t, cyc = {}, {}
             for mode in range(4):
-                eng.run_kernel("probe_mix", [tiles, np.int32(iters), np.int32(mode), res], (grid, 1, 1), (256, 1, 1),
-                               fconsts=[(10, "u32", K)], tg_mem=4 * 8 * 64 * K)  # warm
-                t[mode] = eng.run_kernel("probe_mix", [tiles, np.int32(iters), np.int32(mode), res], (grid, 1, 1),
-                                         (256, 1, 1), fconsts=[(10, "u32", K)], tg_mem=4 * 8 * 64 * K, reps=3) / 3
+                pl.run("probe_mix", [tiles, np.int32(iters), np.int32(mode), res], (grid, 1, 1), (256, 1, 1),
+                       K=K, tg_mem=4 * 8 * 64 * K)  # warm
+                t[mode] = pl.run("probe_mix", [tiles, np.int32(iters), np.int32(mode), res], (grid, 1, 1),
+                                 (256, 1, 1), K=K, tg_mem=4 * 8 * 64 * K, reps=3) / 3
                 w = res.download(np.uint32, (grid * 4, 64))
                 cyc[mode] = float(np.median(w[:, 1]))
                 if mode == 0:  # where the waves ran: distinct (XCC, SE, SH, CU) and waves per SIMD; the s_memtime rate
@@ -267,10 +311,10 @@ def run_probes(eng, iters=4000):
                 for ag in (0, 1):
                     tx = {}
                     for mode in (0, 1):
-                        kw = dict(fconsts=[(10, "u32", K), (16, "u32", ag)], tg_mem=4 * 8 * 64 * K)
+                        kw = dict(K=K, variant=ag, tg_mem=4 * 8 * 64 * K)
                         args = [tiles, np.int32(iters), np.int32(mode), res]
-                        eng.run_kernel("probe_x4", args, (grid, 1, 1), (256, 1, 1), **kw)
-                        tx[mode] = eng.run_kernel("probe_x4", args, (grid, 1, 1), (256, 1, 1), reps=3, **kw) / 3
+                        pl.run("probe_x4", args, (grid, 1, 1), (256, 1, 1), **kw)
+                        tx[mode] = pl.run("probe_x4", args, (grid, 1, 1), (256, 1, 1), reps=3, **kw) / 3
                     out[key][f"x4_{'agpr' if ag else 'vgpr'}"] = {
                         "ms_chains": round(tx[0], 4), "ms_decode_chains": round(tx[1], 4),
                         "vs_max": round(tx[1] / max(t[0], tx[0]), 3), "vs_sum": round(tx[1] / (t[0] + tx[0]), 3)}
@@ -282,9 +326,9 @@ def run_probes(eng, iters=4000):
             t = {}
             for mode in (0, 1, 2, 3):
                 args = [tiles, np.int32(iters), np.int32(mode), res]
-                kw = dict(fconsts=[(10, "u32", K)], tg_mem=65536 + nw * 8 * 64 * K)
-                eng.run_kernel("probe_lut", args, (cus, 1, 1), (nw * 64, 1, 1), **kw)
-                t[mode] = eng.run_kernel("probe_lut", args, (cus, 1, 1), (nw * 64, 1, 1), reps=3, **kw) / 3
+                kw = dict(K=K, tg_mem=65536 + nw * 8 * 64 * K)
+                pl.run("probe_lut", args, (cus, 1, 1), (nw * 64, 1, 1), **kw)
+                t[mode] = pl.run("probe_lut", args, (cus, 1, 1), (nw * 64, 1, 1), reps=3, **kw) / 3
             w = res.download(np.uint32, (cus * nw, 64))
             wts = cus * nw * iters * 8 * 512
             clk = float(np.median(w[:, 1] / np.maximum(w[:, 4], 1))) * 100e6
@@ -337,11 +381,12 @@ TRACE_FIELDS = {0: "start", 1: "pre-route work done", 2: "route known", 3: "requ
 
 
 def run_moe_trace(eng, layers, seed):
-    """The fused M=1 step's per-wave timeline (trace mode: IJAH_MOE_TRACE=1 before the layers exist; stamps kept in
+    """The fused M=1 step's per-wave timeline (trace mode: ne_moe_configure "trace"; stamps kept in
     LDS, written at the end of each launch): a `layers`-layer graph timed as bench does, then for the middle layer
     the stamp of each step in us from the launch's first wave start, p0 / p50 / p100 over the waves that reach it."""
     from ijah_amd import synth
-    lyr = [eng.moe_synth(2048, 512, 512, 10, 5, True, 5, seed=seed + 7919 * i) for i in range(layers)]
+    lyr = [eng.moe_synth(2048, 512, 512, 10, 5, True, 5, seed=seed + 7919 * i).configure("trace", 1)
+           for i in range(layers)]
     x = eng.from_numpy(synth.bf16_values(np.random.default_rng(seed), 1, 2048))
     us = eng.moe_time(lyr, 1, x, warmup=2, reps=5)
     out = np.zeros(8 * 65536, np.uint64)
@@ -393,14 +438,12 @@ def main():
         sys.exit(2)
 
     import ijah_amd
-    if a.moe_trace:
-        os.environ["IJAH_MOE_TRACE"] = "1"  # read when a layer is created
     eng = ijah_amd.load_engine()
     if a.copy_probe:
         n = a.copy_probe << 20
         src, dst = eng.alloc(n), eng.alloc(n)
         for _ in range(5):
-            eng.run_kernel("copy_u128", [src, dst, np.uint64(n // 16)], (2048, 1, 1), (256, 1, 1))
+            Probes().run("copy_u128", [src, dst, np.uint64(n // 16)], (2048, 1, 1), (256, 1, 1))
         print(json.dumps({"copy_probe_bytes": n, "launches": 5}), flush=True)
         return
     if a.moe_trace:

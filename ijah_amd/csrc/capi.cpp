@@ -53,7 +53,6 @@ void ensure_device() {
       init_batch_attrs();
       init_fused_attrs();
       init_lin_attrs();
-      init_probe_attrs();
       noalloc_scratch();  // the allocation-free linear's scratch address on this device
     } catch (const std::exception &e) {
       err = e.what();

@@ -114,8 +114,7 @@ static ne_exl3_lin *lin_create(const uint16_t *trellis, const uint16_t *suh, con
   const size_t nc = (size_t)((out + 127) / 128) * kSyncStride;
   l->cnt = dev_alloc<uint32_t>(nc);
   IJ_HIP(hipMemset(l->cnt, 0, nc * 4));
-  const char *path = getenv("IJAH_LIN_PATH");
-  l->one_launch = !(path && std::string(path) == "staged");
+  l->one_launch = true;
   return l.release();
 }
 
@@ -576,9 +575,9 @@ struct ne_moe {
   int plan_grid = 0;  // fused step: its grid (0: no plan, the staged path runs)
   MoeBatchBufs bat;   // batched path (R >= 2)
   int bat_R = 0;      // rows the batched buffers hold
-  bool batch = true;  // R >= 2 on the grouped matrix-core path (IJAH_MOE_PATH=staged: the staged kernels)
-  uint64_t *trace = nullptr;  // IJAH_MOE_TRACE=1: per-unit timestamps of the fused kernel (debug)
-  bool fused = true;  // one persistent launch per step (IJAH_MOE_PATH=staged: four launches)
+  bool batch = true;  // R >= 2 on the grouped matrix-core path (ne_moe_configure "staged": the staged kernels)
+  uint64_t *trace = nullptr;  // ne_moe_configure "trace": per-wave wall-clock stamps of the fused step
+  bool fused = true;  // one persistent launch per step (ne_moe_configure "staged": four launches)
   int last_R = 0;
   float *last_y = nullptr;
   ~ne_moe() {
@@ -648,11 +647,6 @@ struct ne_moe {
     route = dev_alloc<uint32_t>((size_t)R * 2 * topk);
     IJ_HIP(hipMemset(route, 0, sizeof(uint32_t) * R * 2 * topk));
     sync = dev_alloc<uint32_t>(sync_words(R, nslot(), hid, inter));
-    if (getenv("IJAH_MOE_TRACE")) {
-      dev_free(trace);
-      trace = dev_alloc<uint64_t>((size_t)8 * 65536);
-      IJ_HIP(hipMemset(trace, 0, 8 * 8 * 65536));
-    }
     IJ_HIP(hipMemset(sync, 0, 4 * sync_words(R, nslot(), hid, inter)));
     Rcap = R;
     ensure_batch(R);
@@ -685,8 +679,6 @@ struct ne_moe {
     a.dn = dn;
     a.sync = sync;
     a.trace = trace;
-    if (trace)
-      if (const char *e = getenv("IJAH_MOE_DBG")) a.dbg = atoi(e);
     a.hprep = hprep;
     a.units = plan;
     a.part = part;
@@ -839,8 +831,6 @@ ne_moe *moe_create(const ne_moe_desc &d) {
   m->router = dev_alloc<uint16_t>(rrows * d.hid);
   IJ_HIP(hipMemcpy(m->router, d.router, 2u * d.ne * d.hid, hipMemcpyHostToDevice));
   if (m->has_sgate) IJ_HIP(hipMemcpy(m->router + (size_t)d.ne * d.hid, d.sgate, 2u * d.hid, hipMemcpyHostToDevice));
-  if (const char *e = getenv("IJAH_MOE_PATH")) m->fused = m->batch = strcmp(e, "staged") != 0;
-  if (const char *e = getenv("IJAH_MOE_KSPLIT")) m->ksplit = std::max(1, atoi(e));
   IJ_CHECK((d.hid / 16) % m->ksplit == 0 && ((d.hid / 16) / m->ksplit) % 8 == 0, "ksplit %d does not divide hid %d",
            m->ksplit, d.hid);
   m->ensure_scratch(1);
@@ -986,8 +976,6 @@ NE_API ne_moe *ne_moe_synth(int hid, int inter, int ne, int topk, int K, int has
     }
     m->router = dev_alloc<uint16_t>((size_t)ne * hid);
     launch_fill_normal_bf16(m->router, (size_t)ne * hid, seed * 7 + 5, (float)(1.0 / std::sqrt((double)hid)), s);
-    if (const char *e = getenv("IJAH_MOE_PATH")) m->fused = m->batch = strcmp(e, "staged") != 0;
-    if (const char *e = getenv("IJAH_MOE_KSPLIT")) m->ksplit = std::max(1, atoi(e));
     IJ_CHECK((hid / 16) % m->ksplit == 0 && ((hid / 16) / m->ksplit) % 8 == 0, "ksplit %d does not divide hid %d",
              m->ksplit, hid);
     m->ensure_scratch(1);
@@ -1114,7 +1102,7 @@ NE_API int ne_moe_read(ne_moe *m, const char *name, void *dst, uint64_t nbytes) 
     } else if (n == "experts_dn") {
       fetch(m->dn, (size_t)S * m->hid * 4);
     } else if (n == "trace") {
-      IJ_CHECK(m->trace, "no trace (set IJAH_MOE_TRACE=1 before creating the layer)");
+      IJ_CHECK(m->trace, "no trace (ne_moe_configure(m, \"trace\", 1) before the run)");
       fetch(m->trace, (size_t)8 * 8 * 65536);
     } else if (n == "mlp_out") {
       fetch(m->last_y, (size_t)R * m->hid * 4);
@@ -1122,6 +1110,35 @@ NE_API int ne_moe_read(ne_moe *m, const char *name, void *dst, uint64_t nbytes) 
       throw Error(strfmt("unknown intermediate %s", name));
     }
     memcpy(dst, out.data(), std::min<uint64_t>(nbytes, out.size()));
+  });
+}
+
+NE_API int ne_moe_configure(ne_moe *m, const char *key, int value) {
+  return c_call([&] {
+    IJ_CHECK(m && key, "null argument");
+    const std::string k = key;
+    IJ_HIP(hipStreamSynchronize(stream()));
+    if (k == "staged") {
+      m->fused = m->batch = value == 0;
+    } else if (k == "trace") {
+      dev_free(m->trace);
+      m->trace = nullptr;
+      if (value) {
+        m->trace = dev_alloc<uint64_t>((size_t)8 * 65536);
+        IJ_HIP(hipMemset(m->trace, 0, 8 * 8 * 65536));
+      }
+    } else {
+      throw Error(strfmt("unknown option %s (staged, trace)", key));
+    }
+  });
+}
+
+NE_API int ne_exl3_lin_configure(ne_exl3_lin *l, const char *key, int value) {
+  return c_call([&] {
+    IJ_CHECK(l && key, "null argument");
+    IJ_CHECK(std::string(key) == "staged", "unknown option %s (staged)", key);
+    IJ_HIP(hipStreamSynchronize(stream()));
+    l->one_launch = value == 0;
   });
 }
 

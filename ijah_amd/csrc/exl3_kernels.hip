@@ -1071,12 +1071,6 @@ __global__ void fill_u32(uint32_t *p, uint64_t n, uint64_t seed) {
   for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x)
     p[i] = (uint32_t)splitmix64(seed * 0x100000001B3ull + i);
 }
-// Plain device copy of n16 16-byte words; the byte-count probe that scales HBM traffic counters (FETCH_SIZE,
-// WRITE_SIZE) to bytes.
-__global__ __launch_bounds__(256) void copy_u128(const uint4 *src, uint4 *dst, uint64_t n16) {
-  for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < n16; i += (uint64_t)gridDim.x * blockDim.x)
-    dst[i] = src[i];
-}
 __global__ void fill_scale_f16(uint16_t *p, uint64_t n, uint64_t seed) {
   for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x) {
     const float m = fabsf(1.0f + 0.1f * gauss(seed, i));
@@ -1311,8 +1305,6 @@ static std::vector<KernelEntry> build_registry() {
       if (const void *f = moe_fused_kernel(K, KS, 2048, 512))
         v.push_back({"moe_step_2048x512_ks" + std::to_string(KS), f, {(uint32_t)sizeof(MoeArgs)}, K, -1});
   v.push_back({"fill_u32", (const void *)&fill_u32, {P, 8, 8}, -1, -1});
-  v.push_back({"copy_u128", (const void *)&copy_u128, {P, P, 8}, -1, -1});
-  probe_kernels(v);
   return v;
 }
 

@@ -16,8 +16,6 @@ struct KernelEntry {
 };
 // name + optional function constants (index 10 = K, 16 = R) -> entry, or nullptr
 const KernelEntry *find_kernel(const char *name, const ne_fconst *fc, int nfc);
-void probe_kernels(std::vector<KernelEntry> &v);  // the measurement probes (probes.hip)
-size_t probe_lds(int K);
 
 // Byte offsets of one expert's (or one linear's) regions inside its HBM block. Tiles of a projection are re-laid as
 // [n-pair p][k-tile tk][2], so a workgroup working on output tiles (2p, 2p+1) streams one contiguous span.
@@ -51,7 +49,6 @@ struct MoeArgs {
   float *dn;                           // [R nslot][hid]
   uint32_t *sync;                      // counters: see sync_words(); zero between launches (kernels reset them)
   uint64_t *trace;                     // fused kernel: per-wave wall-clock stamps of its phases, or null
-  int dbg = 0;                         // fused kernel, with trace only: timing experiments (IJAH_MOE_DBG)
   uint16_t *hprep;                     // fused kernel: [R nslot][inter] fp16 down inputs (kp order)
   const uint32_t *units;               // fused kernel: the plan words (MoePlan::words) in device memory
   float *part;                         // fused kernel: column partial sums (MoePlan::part_floats)
@@ -209,7 +206,6 @@ void launch_hc_prep(const float *h, const uint16_t *nw, const uint16_t *iw, floa
 void init_batch_attrs();
 void init_fused_attrs();
 void init_lin_attrs();
-void init_probe_attrs();  // the probes' dynamic LDS limits (once per device)
 // W' fp16 bits [IT*16][OT*16] from re-laid tiles
 void launch_decode(const uint32_t *tiles, int IT, int OT, int K, uint16_t *w, hipStream_t s);
 

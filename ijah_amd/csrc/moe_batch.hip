@@ -837,13 +837,6 @@ __device__ void chunk_gemm(const uint16_t *A, int lda, int ahalf, int aidx, int 
                            int pair, uint8_t *lds, f32x16 (&acc)[NR / 32], uint64_t *dbg, int kt0, int nkt) {
   using Io = GemmIo<K, NA, NR>;
   constexpr int NRB = Io::NRB;
-#ifdef IJ_BATCH_TRACE  // debug builds only: shader-clock stamps of step 20 per (workgroup, wave)
-  uint64_t *drow = dbg ? dbg + ((uint64_t)8192 + blockIdx.x * 8 + (threadIdx.x >> 6)) * 8 : nullptr;
-#define IJ_STAMP(t_, f_) \
-  if (drow && (t_) && (threadIdx.x & 63) == 0) drow[f_] = __builtin_amdgcn_s_memtime();
-#else
-#define IJ_STAMP(t_, f_)
-#endif
   constexpr int DA = Io::DA, U = Io::RB;  // the k loop is unrolled by the B ring's length
   const int lane = threadIdx.x & 63, NS = nkt / 2;  // k tiles [kt0, kt0 + nkt) of IT (nkt even)
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -908,7 +901,6 @@ __device__ void chunk_gemm(const uint16_t *A, int lda, int ahalf, int aidx, int 
     for (int u = 0; u < U; u++) {
       const int t = t0 + u;
       if (t >= NS) break;
-      IJ_STAMP(t == 20, 0)
       const uint8_t *at = a_lane + (u % Io::RA) * Io::AB;
       const f16x8 b0 = bf[0], b1 = bf[1];
 #pragma unroll
@@ -940,10 +932,8 @@ __device__ void chunk_gemm(const uint16_t *A, int lda, int ahalf, int aidx, int 
           }
         }
       }
-      IJ_STAMP(t == 20, 1)
       // the matrix cores run while the next step's tiles decode
       if (t + 1 < NS) begin_step(t + 1, (u + 1) % U);
-      IJ_STAMP(t == 20, 2)
     }
   }
   if constexpr (FG > 0) {
@@ -954,8 +944,6 @@ __device__ void chunk_gemm(const uint16_t *A, int lda, int ahalf, int aidx, int 
 #pragma unroll
       for (int i = 0; i < 16; i++) acc[rb][i] = !closed ? grp[rb][i] : open ? tot[rb][i] + grp[rb][i] : tot[rb][i];
   }
-  IJ_STAMP(true, 5)
-#undef IJ_STAMP
 }
 
 // ---------------------------------------------------------------------------------------------------- Hadamard on

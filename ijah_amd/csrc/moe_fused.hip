@@ -218,8 +218,6 @@ __device__ bool route_wave(const MoeArgs &a, Route *rt, uint32_t tag16) {
   const uint32_t *lg = (const uint32_t *)a.logits + (blockIdx.x % kLogitReplicas) * moe_logit_stride(a.ne);
   uint32_t v[J + 1];
   bool ok = false;
-  if (a.trace && (a.dbg & 1))  // timing experiment: no polling traffic before ~4 us
-    for (int i = 0; i < 2; i++) __builtin_amdgcn_s_sleep(127);
   for (uint32_t it = 0; it < kSpin; it++) {
     bool mine = true;
 #pragma unroll

@@ -1,4 +1,5 @@
-// Measurement probes behind the kernels' design (registered by name for ne_run_kernel; bench.py --probe drives them):
+// Measurement probes behind the kernels' design, built into their own library (ijah_amd/_lib/libijah_probes.so,
+// never into the product library) and launched by name through ijah_probe_run (bench.py --probe, --copy-probe):
 //   probe_decode<K>  the trellis decode alone: every wave decodes the same 8 LDS-resident tile pairs into matrix-core
 //                    B operands over and over (the LDS reads included), so the time is the decode's VALU cost per
 //                    weight with no memory traffic;
@@ -6,13 +7,16 @@
 //                    real kernels: one dependent 32x32x16 f16 MFMA per decoded tile pair), 2 each wave decodes a tile
 //                    and feeds it to its MFMA chain (the fused loop of the GEMMs), 3 even waves decode and odd waves
 //                    run MFMA chains (specialised waves). Comparing the times says whether the two overlap.
-//   probe_stream     cold streams into LDS (global_load_lds) against plain 16-byte loads into registers.
+//   probe_stream     cold streams into LDS (global_load_lds) against plain 16-byte loads into registers;
+//   copy_u128        a plain device copy: the byte count that scales HBM traffic counters (FETCH_SIZE, WRITE_SIZE).
 // Per wave (64 words of out): lane 0 the results folded (so that nothing is optimised away), lane 1 the s_memtime
 // ticks of its loop, lanes 2-3 its HW_ID and XCC_ID (where it ran), lane 4 the loop in 100 MHz real-time ticks.
 #include <hip/hip_runtime.h>
 
+#include <cstring>
+#include <vector>
+
 #include "exl3_device.h"
-#include "kernels.h"
 
 namespace ijah {
 
@@ -255,27 +259,78 @@ __global__ __launch_bounds__(256) void probe_x4(const uint8_t *tiles, int iters,
 
 }  // namespace
 
-void init_probe_attrs() {
-  for (const void *f : {(const void *)&probe_lut<5>, (const void *)&probe_lut<8>})
-    IJ_HIP(hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 65536 + 16 * kProbeTiles * 64 * 8));
+struct ProbeEntry {
+  const char *name;
+  const void *fn;
+  std::vector<uint32_t> arg_sizes;
+  int K;  // -1: any
+  int v;  // variant (-1: any)
+};
+__global__ __launch_bounds__(256) void copy_u128(const uint4 *src, uint4 *dst, uint64_t n16) {
+  for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < n16; i += (uint64_t)gridDim.x * blockDim.x)
+    dst[i] = src[i];
 }
-
-size_t probe_lds(int K) { return (size_t)4 * kProbeTiles * 64 * K; }
-
-void probe_kernels(std::vector<KernelEntry> &v) {
+const std::vector<ProbeEntry> &probes() {
   const uint32_t P = sizeof(void *), I = sizeof(int);
-  v.push_back({"probe_mix", (const void *)&probe_mix<2>, {P, I, I, P}, 2, -1});
-  v.push_back({"probe_mix", (const void *)&probe_mix<3>, {P, I, I, P}, 3, -1});
-  v.push_back({"probe_mix", (const void *)&probe_mix<4>, {P, I, I, P}, 4, -1});
-  v.push_back({"probe_mix", (const void *)&probe_mix<5>, {P, I, I, P}, 5, -1});
-  v.push_back({"probe_mix", (const void *)&probe_mix<6>, {P, I, I, P}, 6, -1});
-  v.push_back({"probe_mix", (const void *)&probe_mix<7>, {P, I, I, P}, 7, -1});
-  v.push_back({"probe_mix", (const void *)&probe_mix<8>, {P, I, I, P}, 8, -1});
-  v.push_back({"probe_lut", (const void *)&probe_lut<5>, {P, I, I, P}, 5, -1});
-  v.push_back({"probe_lut", (const void *)&probe_lut<8>, {P, I, I, P}, 8, -1});
-  v.push_back({"probe_x4", (const void *)&probe_x4<5, false>, {P, I, I, P}, 5, 0});
-  v.push_back({"probe_x4", (const void *)&probe_x4<5, true>, {P, I, I, P}, 5, 1});
-  v.push_back({"probe_stream", (const void *)&probe_stream, {P, I, I, P}, -1, -1});
+  static const std::vector<ProbeEntry> v = {
+      {"probe_mix", (const void *)&probe_mix<2>, {P, I, I, P}, 2, -1},
+      {"probe_mix", (const void *)&probe_mix<3>, {P, I, I, P}, 3, -1},
+      {"probe_mix", (const void *)&probe_mix<4>, {P, I, I, P}, 4, -1},
+      {"probe_mix", (const void *)&probe_mix<5>, {P, I, I, P}, 5, -1},
+      {"probe_mix", (const void *)&probe_mix<6>, {P, I, I, P}, 6, -1},
+      {"probe_mix", (const void *)&probe_mix<7>, {P, I, I, P}, 7, -1},
+      {"probe_mix", (const void *)&probe_mix<8>, {P, I, I, P}, 8, -1},
+      {"probe_lut", (const void *)&probe_lut<5>, {P, I, I, P}, 5, -1},
+      {"probe_lut", (const void *)&probe_lut<8>, {P, I, I, P}, 8, -1},
+      {"probe_x4", (const void *)&probe_x4<5, false>, {P, I, I, P}, 5, 0},
+      {"probe_x4", (const void *)&probe_x4<5, true>, {P, I, I, P}, 5, 1},
+      {"probe_stream", (const void *)&probe_stream, {P, I, I, P}, -1, -1},
+      {"copy_u128", (const void *)&copy_u128, {P, P, 8}, -1, -1},
+  };
+  return v;
 }
 
 }  // namespace ijah
+
+// args: nargs slots of 8 bytes each (a device address or a value in the low bytes, as the kernel's argument sizes say);
+// runs reps launches and waits; *ms = their GPU time. Returns 0, or -1 with a message in err (errlen bytes).
+extern "C" __attribute__((visibility("default"))) int ijah_probe_run(const char *name, int K, int variant,
+                                                                   const uint64_t *args, int nargs,
+                                                                   const unsigned *grid, const unsigned *block,
+                                                                   unsigned lds, int reps, double *ms, char *err,
+                                                                   int errlen) {
+  using namespace ijah;
+  auto fail = [&](const char *m) {
+    snprintf(err, (size_t)errlen, "%s", m);
+    return -1;
+  };
+  static bool attrs = false;
+  if (!attrs) {
+    for (const void *f : {(const void *)&probe_lut<5>, (const void *)&probe_lut<8>})
+      if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 65536 + 16 * kProbeTiles * 64 * 8))
+        return fail("hipFuncSetAttribute failed");
+    attrs = true;
+  }
+  for (const ProbeEntry &e : probes()) {
+    if (strcmp(e.name, name) || (e.K >= 0 && e.K != K) || (e.v >= 0 && e.v != variant)) continue;
+    if ((int)e.arg_sizes.size() != nargs) return fail("argument count");
+    std::vector<void *> addr(nargs);
+    for (int i = 0; i < nargs; i++) addr[i] = const_cast<uint64_t *>(args + i);  // little-endian: low bytes first
+    hipEvent_t a, b;
+    if (hipEventCreate(&a) || hipEventCreate(&b)) return fail("hipEventCreate failed");
+    hipEventRecord(a, nullptr);
+    for (int r = 0; r < reps; r++)
+      if (hipLaunchKernel(e.fn, dim3(grid[0], grid[1], grid[2]), dim3(block[0], block[1], block[2]), addr.data(), lds,
+                          nullptr) != hipSuccess)
+        return fail("launch failed");
+    hipEventRecord(b, nullptr);
+    if (hipEventSynchronize(b) != hipSuccess) return fail("probe failed on the GPU");
+    float t = 0.f;
+    hipEventElapsedTime(&t, a, b);
+    *ms = t;
+    hipEventDestroy(a);
+    hipEventDestroy(b);
+    return 0;
+  }
+  return fail("no such probe");
+}

@@ -118,6 +118,7 @@ SIGNATURES = {
     "ne_moe_run": (_i, [_vp, _i, _vp, _u64, _vp, _u64, _dp]),
     "ne_moe_run_hc": (_i, [_vp, _i, _vp, _u64, _vp, _u64, _vp, _dp]),
     "ne_moe_read": (_i, [_vp, _s, _vp, _u64]), "ne_moe_decode": (_i, [_vp, _i, _i, _vp, _dp]),
+    "ne_moe_configure": (_i, [_vp, _s, _i]), "ne_exl3_lin_configure": (_i, [_vp, _s, _i]),
     "ne_moe_info": (_i, [_vp] + [_ip] * 6), "ne_moe_bytes": (_i, [_vp, _i, C.POINTER(_u64)]),
     "ne_moe_time": (_i, [C.POINTER(_vp), _i, _i, _vp, _i, _i, _dp]),
     "ne_moe_time_kernels": (_i, [C.POINTER(_vp), _i, _i, _vp, _i, _vp, _dp, _ip]),
@@ -308,6 +309,11 @@ class Exl3Linear(_Handle):
         self.run_bufs(x.shape[0], xb, yb)
         return yb.download(np.float32, (x.shape[0], self.out))
 
+    def configure(self, key, value):
+        """ne_exl3_lin_configure ("staged": 1 = three launches)"""
+        self._call("ne_exl3_lin_configure", key.encode(), int(value))
+        return self
+
     def decode(self):
         w = self.eng.alloc(self.inp * self.out * 2)
         self._call("ne_exl3_lin_decode", w.ptr, None)
@@ -363,6 +369,12 @@ class MoeLayer(_Handle):
         out = np.zeros(shape, dt)
         self._call("ne_moe_read", name.encode(), out.ctypes.data, out.nbytes)
         return out
+
+    def configure(self, key, value):
+        """ne_moe_configure ("staged": 1 = the four staged launches at every row count; "trace": 1 = per-wave stamps
+        of the fused step)"""
+        self._call("ne_moe_configure", key.encode(), int(value))
+        return self
 
     def decode(self, e, proj):
         inp, out = (self.inter, self.hid) if proj == 2 else (self.hid, self.inter)

@@ -161,6 +161,14 @@ NE_API int ne_moe_run_hc(ne_moe *m, int R, const ne_buf *x, uint64_t x_off, ne_b
  * (down inner outputs before H_out), "mlp_out" f32 [R][hid], "shared_q8" f32 [R][hid] (the 8-bit shared expert's
  * rounded output before its gate). Copies at most nbytes; returns 0. */
 NE_API int ne_moe_read(ne_moe *m, const char *name, void *dst, uint64_t nbytes);
+/* Layer options (no reference counterpart: the reference picks its dispatch forms by function constants at build):
+ *   "staged" 1: every row count on the four staged launches (router, gate/up, down, combine) instead of the fused
+ *               one-row step (R = 1) and the grouped matrix-core kernels (R >= 2); 0: the default choice;
+ *   "trace"  1: the fused step keeps per-wave wall-clock stamps of its phases (ne_moe_read "trace"); 0: off.
+ * Waits for queued work first. Returns 0, or -1 for an unknown key. */
+NE_API int ne_moe_configure(ne_moe *m, const char *key, int value);
+/* Linear options: "staged" 1 = three launches (prep, GEMM, finish) instead of one; 0: one launch (default). */
+NE_API int ne_exl3_lin_configure(ne_exl3_lin *l, const char *key, int value);
 /* Expert e's projection proj (0 gate, 1 up, 2 down; e == ne: the shared expert) decoded from the re-laid HBM block:
  * fp16 bits [in][out] into w. */
 NE_API int ne_moe_decode(ne_moe *m, int e, int proj, ne_buf *w, double *gpu_ms);

@@ -104,7 +104,7 @@ def test_linear_multi_launch_matches_single(eng, oracle, R):
 
 
 @pytest.mark.parametrize("inp,out,K,R", [(2048, 512, 5, 1), (2048, 4096, 6, 3), (320, 640, 7, 8), (96, 48, 4, 2)])
-def test_linear_one_launch_matches_staged(eng, oracle, inp, out, K, R, monkeypatch):
+def test_linear_one_launch_matches_staged(eng, oracle, inp, out, K, R):
     """The one-launch linear (in-workgroup prep, last-arriver finish) against the three-launch path (prep launch, GEMM,
     finish launch): bit-identical, over repeated runs (the block counters reset themselves)."""
     print(f"linear one-launch vs staged {inp}x{out} K{K} R{R}", flush=True)
@@ -112,8 +112,7 @@ def test_linear_one_launch_matches_staged(eng, oracle, inp, out, K, R, monkeypat
     t, su, sv = synth.linear(rng, inp, out, K)
     x = synth.bf16_values(rng, R, inp)
     one = eng.exl3_linear(t, su, sv)
-    monkeypatch.setenv("IJAH_LIN_PATH", "staged")
-    staged = eng.exl3_linear(t, su, sv)
+    staged = eng.exl3_linear(t, su, sv).configure("staged", 1)
     want = staged.run(x)
     for _ in range(3):
         assert np.array_equal(one.run(x), want)

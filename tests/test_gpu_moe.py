@@ -131,15 +131,13 @@ def test_moe_synth_full_properties(eng):
     assert m.bytes(1) == 11 * per_expert + 512 * 2048 * 2
 
 
-def test_moe_fused_and_staged_paths_agree(eng, oracle, monkeypatch):
+def test_moe_fused_and_staged_paths_agree(eng, oracle):
     """The persistent fused launch and the four staged launches compute the same layer (same decode, prep and combine
     arithmetic; the f32 k-accumulation order differs), and each is deterministic; the inner outputs agree too."""
     w = synth.moe_layer(61, hid=2048, inter=512, ne=64, topk=10, K=5, shared=True, Ks=6, sgate=True)
     x = synth.bf16_values(np.random.default_rng(62), 1, 2048)  # the fused step serves one row
-    monkeypatch.setenv("IJAH_MOE_PATH", "staged")
-    st = eng.moe_create(w)
+    st = eng.moe_create(w).configure("staged", 1)
     ys = st.run(x)
-    monkeypatch.setenv("IJAH_MOE_PATH", "fused")
     m = eng.moe_create(w)
     yf = m.run(x)
     assert rel(yf, ys) < 1e-5
@@ -151,7 +149,7 @@ def test_moe_fused_and_staged_paths_agree(eng, oracle, monkeypatch):
 
 
 @pytest.mark.parametrize("Ks", [4, 5, 6])
-def test_moe_m1_k4_mtp_head(eng, oracle, Ks, monkeypatch):
+def test_moe_m1_k4_mtp_head(eng, oracle, Ks):
     """The MTP head's MoE at M=1: K4 routed experts (reference core/main_test.mm:371, mtp_k = 4) at the config-2
     shape, with a K4 / K5 / K6 shared expert, on the fused single-row kernel (moe_step<4, Ks>); against the oracle
     and the staged kernels."""
@@ -162,8 +160,7 @@ def test_moe_m1_k4_mtp_head(eng, oracle, Ks, monkeypatch):
     x = synth.bf16_values(np.random.default_rng(111 + Ks), 1, 2048)
     y, _ = check_layer(eng, oracle, m, W, x)
     assert np.array_equal(m.run(x), y)
-    monkeypatch.setenv("IJAH_MOE_PATH", "staged")
-    assert rel(eng.moe_create(w).run(x), y) < 5e-5  # same arithmetic, other f32 accumulation orders
+    assert rel(eng.moe_create(w).configure("staged", 1).run(x), y) < 5e-5  # same arithmetic, other f32 accumulation orders
 
 
 @pytest.mark.parametrize("R", [1, 4])
@@ -207,13 +204,11 @@ def test_moe_batch_row_block_forms(eng, oracle, R):
     assert np.array_equal(m.run(x), y)
 
 
-def test_moe_batch_matches_staged(eng, oracle, monkeypatch):
+def test_moe_batch_matches_staged(eng, oracle):
     """The grouped path and the staged kernels compute the same layer for several rows."""
     w = synth.moe_layer(81, hid=2048, inter=512, ne=64, topk=10, K=5, shared=True, Ks=5, sgate=False)
     x = synth.bf16_values(np.random.default_rng(82), 5, 2048)
-    monkeypatch.setenv("IJAH_MOE_PATH", "staged")
-    ys = eng.moe_create(w).run(x)
-    monkeypatch.setenv("IJAH_MOE_PATH", "fused")
+    ys = eng.moe_create(w).configure("staged", 1).run(x)
     yb = eng.moe_create(w).run(x)
     assert rel(yb, ys) < 1e-4  # matrix-core vs lane accumulation order; fp16 rounding of h may flip
 
@@ -328,7 +323,7 @@ def test_moe_prefill_config5_rows_match_single_row(eng):
 @pytest.mark.parametrize("R,path,dims", [
     (1, "fused", (2048, 512, 64, 10)), (1, "staged", (2048, 512, 64, 10)), (3, "staged", (1024, 256, 16, 4)),
     (3, "batched", (1024, 256, 16, 4)), (16, "batched", (1024, 256, 16, 4)), (40, "batched", (1024, 256, 16, 4))])
-def test_moe_hc_write(eng, oracle, R, path, dims, monkeypatch):
+def test_moe_hc_write(eng, oracle, R, path, dims):
     """ne_moe_run_hc, the hyper-connection write fused into the combine (reference kernels/fn_moe.metal:437-448), on
     the fused single-row kernel, the staged kernels and the batched GEMM forms (16 rows: the one-row-block form, 40
     rows x 4 slots over 16 experts: the transposed form). Rounding off: the branch is the plain run's output bit for
@@ -336,11 +331,11 @@ def test_moe_hc_write(eng, oracle, R, path, dims, monkeypatch):
     where the GPU's and the oracle's f32 sums straddle a rounding boundary."""
     hid, inter, ne, topk = dims
     print(f"moe hc write R{R} {path} hid {hid} ne {ne}", flush=True)
-    if path == "staged":
-        monkeypatch.setenv("IJAH_MOE_PATH", "staged")
     w = synth.moe_layer(70 + R, hid=hid, inter=inter, ne=ne, topk=topk, K=5, shared=True, Ks=6, sgate=True)
     W = oracle.MoeWeights(w)
     moe = eng.moe_create(w)
+    if path == "staged":
+        moe.configure("staged", 1)
     rng = np.random.default_rng(80 + R)
     x = synth.bf16_values(rng, R, hid)
     hc = 4
