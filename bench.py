@@ -167,6 +167,32 @@ def measure_trunk(eng, R, steps, seed, min_bytes=300e6):
     return out
 
 
+# the reference's own trunk shapes with published M=1 timings on its hardware (docs/trunk6.md:93-100)
+TRUNK_REF = [("2560x10240_k6", 2560, 10240, 6, 39.4), ("2560x12288_k6", 2560, 12288, 6, 46.9),
+             ("2560x640_k6", 2560, 640, 6, 11.0), ("320x10240_k8", 320, 10240, 8, 9.0)]
+
+
+def measure_trunk_ref(eng, steps, seed, min_bytes=300e6):
+    """The reference's trunk shapes at M=1, timed as measure_trunk (graphs over distinct copies beyond the last-level
+    cache); the reference's published us on its M5 Max beside each (a different machine: context, not a target)."""
+    from ijah_amd import synth
+    out = {}
+    xb = eng.from_numpy(synth.bf16_values(np.random.default_rng(seed), 1, 2560))
+    for name, inp, o, K, ref_us in TRUNK_REF:
+        t, su, sv = synth.linear(np.random.default_rng(seed + inp + o), inp, o, K)
+        nbytes = t.nbytes + su.nbytes + sv.nbytes
+        copies = int(min(64, max(2, np.ceil(min_bytes / nbytes))))
+        lins = [eng.exl3_linear(t, su, sv) for _ in range(copies)]
+        us = eng.lin_time(lins, 1, xb, warmup=2, reps=max(3, steps))
+        for m in lins:
+            m.free()
+        gbs = nbytes / (us * 1e-6) / 1e9
+        out[name] = {"us": round(us, 3), "bytes": int(nbytes), "GBps": round(gbs, 1),
+                     "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2), "reference_m5max_us": ref_us}
+        print(f"trunk ref {name}: {out[name]}", file=sys.stderr, flush=True)
+    return out
+
+
 def run_trunk_eager(eng, steps, seed):
     """Config 3's trunk linears launched one by one (ne_exl3_lin_run, and q/k/v through ne_exl3_lin_run_multi), no
     graphs: a kernel trace of this run gives each shape's kernel time at 1 and 16 rows."""
@@ -403,6 +429,14 @@ def run_moe_trace(eng, layers, seed):
     rows.sort()
     for _, name, p0, p50, p100, n in rows:
         print(f"{name:26s} {p0:7.2f} {p50:7.2f} {p100:7.2f}  waves={n}", flush=True)
+    # where the skew sits: per workgroup the latest wave's stamp, by XCD (workgroup % 8) and the slowest workgroups
+    for f in (2, 13, 8, 9, 5, 6):
+        v = np.where(t[:, :, f] > 0, (t[:, :, f] - base) / 100.0, np.nan)
+        wg = np.nanmax(v, axis=1)
+        by_xcd = [round(float(np.nanmedian(wg[x::8])), 2) for x in range(8)]
+        slow = np.argsort(-np.nan_to_num(wg, nan=-1))[:6]
+        print(f"{TRACE_FIELDS[f]:26s} per-XCD median {by_xcd}  slowest wg {slow.tolist()} "
+              f"{[round(float(wg[i]), 2) for i in slow]}", flush=True)
     return {"us_per_layer_traced": round(us, 3), "layers": layers}
 
 
@@ -512,6 +546,9 @@ def main():
     if not a.no_batch:
         for m in layers:  # the M=1 layers' memory is no longer needed
             m.free()
+        for R in (2, 4, 8):  # the reference's draft sizes (docs/mtp.md:987-993)
+            extra[f"verify_r{R}"] = measure_batch(eng, R, 32, max(5, a.steps // 5), a.seed + R)
+            print(f"verify R={R}: {extra[f'verify_r{R}']}", file=sys.stderr, flush=True)
         extra["verify_r16"] = measure_batch(eng, 16, 32, max(5, a.steps // 5), a.seed + 16)
         print(f"verify R=16: {extra['verify_r16']}", file=sys.stderr, flush=True)
         extra["verify_r16_k4"] = measure_batch(eng, 16, 32, max(5, a.steps // 5), a.seed + 17, k=4)
@@ -521,6 +558,7 @@ def main():
     if not a.no_trunk:
         extra["trunk_m1"] = measure_trunk(eng, 1, max(5, a.steps // 5), a.seed + 3)
         extra["trunk_m16"] = measure_trunk(eng, 16, max(5, a.steps // 5), a.seed + 4)
+        extra["trunk_reference_shapes_m1"] = measure_trunk_ref(eng, max(5, a.steps // 5), a.seed + 7)
         extra["hc_read_m1"] = measure_hc_read(eng, 1, a.steps, a.seed + 5)
         extra["hc_read_m16"] = measure_hc_read(eng, 16, a.steps, a.seed + 6)
     cpu = None if a.no_cpu else cpu_baseline()

@@ -573,6 +573,7 @@ struct ne_moe {
   size_t part_floats = 0;
   uint32_t *fsync = nullptr;  // the fused step's launch epoch
   int plan_grid = 0;  // fused step: its grid (0: no plan, the staged path runs)
+  int plan_slots = 0; // fused step: the LDS slots its plan uses
   MoeBatchBufs bat;   // batched path (R >= 2)
   int bat_R = 0;      // rows the batched buffers hold
   bool batch = true;  // R >= 2 on the grouped matrix-core path (ne_moe_configure "staged": the staged kernels)
@@ -632,7 +633,8 @@ struct ne_moe {
     dn = dev_alloc<float>(S * hid);
     hprep = dev_alloc<uint16_t>(S * inter);
     if (!plan && fused && moe_fused_supported(K, has_shared ? Ks : K, 1, hid, inter, ne, topk, q8 != nullptr)) {
-      const MoePlan pl = moe_fused_plan(hid, inter, topk, nslot(), moe_fused_grid(), q8 != nullptr);
+      const MoePlan pl = moe_fused_plan(hid, inter, topk, nslot(), moe_fused_grid(), q8 != nullptr,
+                                        moe_fused_slots(K, has_shared ? Ks : K, hid, inter));
       if (pl.ok) {
         plan = dev_alloc<uint32_t>(pl.words.size());
         IJ_HIP(hipMemcpy(plan, pl.words.data(), pl.words.size() * 4, hipMemcpyHostToDevice));
@@ -642,6 +644,7 @@ struct ne_moe {
         fsync = dev_alloc<uint32_t>(moe_fused_sync_words(nslot(), hid, inter));
         IJ_HIP(hipMemset(fsync, 0, 4 * moe_fused_sync_words(nslot(), hid, inter)));
         plan_grid = pl.grid;
+        plan_slots = pl.slots;
       }
     }
     route = dev_alloc<uint32_t>((size_t)R * 2 * topk);
@@ -683,6 +686,7 @@ struct ne_moe {
     a.units = plan;
     a.part = part;
     a.fsync = fsync;
+    a.fused_slots = plan_slots;
     a.q8 = q8;
     a.q8gu = q8gu;
     a.q8o = q8o;

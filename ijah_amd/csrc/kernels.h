@@ -53,6 +53,7 @@ struct MoeArgs {
   const uint32_t *units;               // fused kernel: the plan words (MoePlan::words) in device memory
   float *part;                         // fused kernel: column partial sums (MoePlan::part_floats)
   uint32_t *fsync;                     // fused kernel: its counters (moe_fused_sync_words), zero when created
+  int fused_slots = 0;                 // fused kernel: LDS slots of its plan (MoePlan::slots)
   // The hyper-connection write fused into the combine (reference kernels/fn_moe.metal:7-10, 420-448), on when hc > 0
   // (rr = bf16 rounding when refr): the shared gate is rr(sigmoid), y = branch = rr(rr(routed sum) + rr(gated shared)),
   // hc_out[r][s][c] = rr(hc_h[r][s][c] + rr(branch hc_inj[r][s])) for s < hc; hc_h, hc_out f32 [R][hc][hid], hc_inj
@@ -98,12 +99,15 @@ void launch_moe_combine(const MoeArgs &a, hipStream_t s);
 struct MoePlan {
   bool ok = false;
   int grid = 0;
-  std::vector<uint32_t> words;  // per wave 4 segment words, then per-column segment counts and counter targets
+  std::vector<uint32_t> words;  // kPW words per workgroup: task ranges, prep keys, h blocks, per-wave unit words
   size_t part_floats = 0;
+  int slots = 0;                // LDS slots (8 k tile pairs each) the busiest workgroup uses
 };
 int moe_fused_grid();
 // q8: the 8-bit shared expert runs beside the routed work (its tagged hand-offs are added to the partials)
-MoePlan moe_fused_plan(int hid, int inter, int topk, int nslot, int grid, bool q8 = false);
+// slots: the LDS slots the instance has room for (moe_fused_slots)
+MoePlan moe_fused_plan(int hid, int inter, int topk, int nslot, int grid, bool q8, int slots);
+int moe_fused_slots(int K, int KS, int hid, int inter);  // 0: not instantiated
 bool moe_fused_supported(int K, int KS, int R, int hid, int inter, int ne, int topk, bool q8 = false);
 inline size_t moe_fused_sync_words(int nslot, int hid, int inter) {
   return 64 * (1 + (size_t)nslot * (inter / 128) + hid / 128);

@@ -29,6 +29,8 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <map>
+#include <mutex>
 #include <vector>
 
 #include "exl3_device.h"
@@ -45,16 +47,19 @@ constexpr int kWaves = 16;
 constexpr int kCtl = kWaves - 1;
 constexpr int kDnKt = 8;           // k tiles of a down unit (one 128-wide h block) and of a k chunk (LDS slot size)
 constexpr int kGrp = 4;            // k chunks per k group (a gate/up task: 32 k tiles of one tile pair)
-constexpr int kMaxSlots = 36;      // LDS slots (8 k tile pairs each) per workgroup
-constexpr int kUnitsPerWave = 3;
-constexpr int kMaxGT = 8;          // gate/up tasks per workgroup (shared and routed)
-constexpr int kMaxPrep = 8;        // routed prepared k chunks per workgroup (2 k groups)
+constexpr int kMaxSlots = 64;      // LDS slots (8 k tile pairs each) per workgroup: at most (6-bit slot field); the
+                                   // instance's LDS sets the real count (fused_slots)
+constexpr int kUnitsPerWave = 4;
+constexpr int kMaxGT = 10;         // gate/up tasks per workgroup (shared and routed)
+constexpr int kMaxPrep = 12;       // routed prepared k chunks per workgroup (3 k groups)
+constexpr int kMaxDn = 2;          // down units per wave
+constexpr uint32_t kDnReuse = 1u << 22;  // down unit word: its tiles go into a gate/up chunk's slot, after that chunk
 constexpr int kSpw = 8;            // the waves preparing the shared k group's chunks: kSpw .. kSpw + 3
-constexpr int kMaxH = 3;           // h blocks per workgroup (2 loader waves each)
+constexpr int kMaxH = 4;           // h blocks per workgroup (2 loader waves each)
 constexpr uint32_t kURouted = 1, kUShared = 2, kUDown = 3;  // unit word types (bits 31:30)
 constexpr int kMaxExpertsV = 1024;
 constexpr int kMaxTopkV = 16;      // the combine stages svh_d of every slot in LDS
-constexpr int kPW = 64;            // plan words per workgroup (one per lane)
+constexpr int kPW = 128;           // plan words per workgroup (two per lane)
 constexpr uint32_t kNone = ~0u;
 constexpr uint32_t kSpin = 1u << 22;  // bounded waits: far beyond any real wait
 enum { kWordErr = kSyncErrWord };
@@ -63,13 +68,13 @@ enum { kWordErr = kSyncErrWord };
 enum {
   P_RT0 = 0, P_NRT,                    // routed gate/up tasks [rt0, rt0 + nrt) (global task index)
   P_ST0, P_NST,                        // shared gate/up tasks
-  P_NRP, P_RP,                         // routed prep groups: count, then 2 keys (matrix * NKG + k group)
-  P_SPK = P_RP + 2,                    // the shared tasks' prep key (proj * NKG + k group), or kNone
+  P_NRP, P_RP,                         // routed prep groups: count, then 3 keys (matrix * NKG + k group)
+  P_SPK = P_RP + 3,                    // the shared tasks' prep key (proj * NKG + k group), or kNone
   P_COMB,                              // combine output block, or kNone
   P_NH, P_HB,                          // h blocks: count, then kMaxH ids (slot * NBI + cb); bit 31: store its g / u sums
   P_U = 16                             // per wave kUnitsPerWave unit words: type << 30 | LDS slot << 24 | payload
 };                                     // (a k chunk of a gate/up task: prep group << 8 | task - rt0 (or - st0) << 2 |
-                                       // chunk; down unit: h slot << 20 | unit), or kNone
+                                       // chunk; down unit: kDnReuse | h slot << 20 | unit), or kNone
 
 __device__ __forceinline__ uint32_t ld_relaxed(const uint32_t *p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -100,6 +105,11 @@ __device__ __forceinline__ void trace_out(const MoeArgs &a) {
   if (a.trace && lane < kTraceFields)
     a.trace[((uint64_t)blockIdx.x * kWaves + wave) * kTraceFields + lane] = trace_lds()[wave * kTraceFields + lane];
 }
+
+struct DnUnit {  // a down unit of a wave: global unit index (-1: none) and where its data sits
+  int unit = -1, slot = 0, hs = 0, end = 0, ls = 0, cb = 0, c = 0, p = 0;
+  bool reuse = false, shared = false;
+};
 
 struct Route {  // the workgroup's copy of the route of the row
   uint32_t id[kMaxTopkV];
@@ -426,7 +436,7 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
   __shared__ float hsum[kMaxH][2][128];
   __shared__ float csum[kMaxGT][kGrp][32];                                 // k chunk sums of the gate/up tasks
   __shared__ uint32_t tcnt[kMaxGT];                                        // chunk sums of each task in LDS
-  __shared__ uint32_t s_prep;                                              // prep chunks ready: routed bits 0-7, shared 8-11
+  __shared__ uint32_t s_prep;                                              // prep chunks ready: routed bits 0-11, shared 16-19
   __shared__ uint32_t s_hrdy;  // h sums loaded: bit 2 h slot + proj; h block ready: bit 8 + h slot
   __shared__ __attribute__((aligned(16))) uint16_t hvec[kMaxH][3][128];   // svh_g, svh_u, suh_d of each h block
   __shared__ __attribute__((aligned(16))) uint16_t csv[kMaxTopkV + 1][128]; // the combine's svh_d per slot
@@ -449,8 +459,10 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
     ep = ld_cg((const uint64_t *)a.fsync);  // every lane (one request; no branch whose end would wait for it)
     stream_tiles((const uint8_t *)a.x, 0, 0, 0, HID / 4, 8, (uint8_t *)xl);  // 4 HID bytes
   }
-  const uint32_t plw = a.units[(size_t)blockIdx.x * kPW + lane];
-  auto PL = [&](int i) { return (uint32_t)__builtin_amdgcn_readlane((int)plw, i); };
+  const uint32_t plw0 = a.units[(size_t)blockIdx.x * kPW + lane], plw1 = a.units[(size_t)blockIdx.x * kPW + 64 + lane];
+  auto PL = [&](int i) {
+    return (uint32_t)(i < 64 ? __builtin_amdgcn_readlane((int)plw0, i) : __builtin_amdgcn_readlane((int)plw1, i - 64));
+  };
   uint64_t *part_gu = (uint64_t *)a.part;                                   // [column][NKG groups][32]
   uint64_t *part_dn = part_gu + (size_t)a.nslot * 2 * NP * NKG * 32;        // [slot][cb][HID]
   const float sch = a.sc_hid, sci = a.sc_inter;
@@ -584,22 +596,33 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
   stamp_w(a, 5);
   lds_barrier();
   stamp_w(a, 6);
-  int dunit = -1, dslot = 0, dhs = 0, end_dn = 0;  // this wave's down unit, its LDS slot and h slot
+  // this wave's down units (at most kMaxDn, in plan order: a shared one comes first): the first one's tiles are
+  // requested now and decoded before its h block is ready; a unit whose tiles reuse a gate/up chunk's LDS slot
+  // (shapes whose units outnumber the slots) is requested once the wave's chunks are done; a second unit is decoded
+  // after the first one's product is stored
+  DnUnit D0, D1;
 #pragma unroll
   for (int k = 0; k < kUnitsPerWave; k++)
     if (uw[k] != kNone && (uw[k] >> 30) == kUDown) {
-      dunit = (int)(uw[k] & 0xFFFFFu);
-      dhs = (int)((uw[k] >> 20) & 3u);
-      dslot = (int)((uw[k] >> 24) & 0x3Fu);
+      DnUnit &D = D0.unit < 0 ? D0 : D1;
+      D.unit = (int)(uw[k] & 0xFFFFFu);
+      D.hs = (int)((uw[k] >> 20) & 3u);
+      D.slot = (int)((uw[k] >> 24) & 0x3Fu);
+      D.reuse = (uw[k] & kDnReuse) != 0;
+      D.ls = D.unit / UPS;
+      D.cb = (D.unit / (NBLK * 4)) % NBI;
+      D.c = (D.unit / 4) % NBLK;
+      D.p = D.unit % 4;
+      D.shared = hs && D.ls == 0;
     }
-  const int d_ls = dunit / UPS, d_cb = (dunit / (NBLK * 4)) % NBI, d_c = (dunit / 4) % NBLK, d_p = dunit % 4;
-  const bool dn_shared = dunit >= 0 && hs && d_ls == 0;
+  auto issue_dn = [&](DnUnit &D) {
+    nops += stream_tiles(slot_block(a, rt, D.ls) + tr_off(a, D.ls, 2), ITd, D.c * 4 + D.p, D.cb * kDnKt, kDnKt,
+                         32u * K, tiles + D.slot * SLOT);
+    D.end = nops;
+  };
   if (ok) {
-    if (dunit >= 0 && !dn_shared) {
-      nops += stream_tiles(slot_block(a, rt, d_ls) + tr_off(a, d_ls, 2), ITd, d_c * 4 + d_p, d_cb * kDnKt, kDnKt,
-                           32u * K, tiles + dslot * SLOT);
-      end_dn = nops;
-    }
+    if (D0.unit >= 0 && !D0.shared && !D0.reuse) issue_dn(D0);
+    if (D1.unit >= 0 && !D1.reuse) issue_dn(D1);
     // small vectors the later phases read, into LDS: the h prologue's svh_g, svh_u, suh_d of block `wave`; the
     // combine's svh_d of slot ls = wave (mod 16)
     if (wave < nh) {
@@ -651,7 +674,7 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
   auto prep_wait = [&](uint32_t bit) { flag_wait(&s_prep, bit); };
   if (sprep_w) {
     prep_chunk<HH>(xl, (int)(spk % NKG) * kGrp + (wave - kSpw), sprep[wave - kSpw], sch);
-    prep_ready(1u << (8 + wave - kSpw));
+    prep_ready(1u << (16 + wave - kSpw));
   }
   stamp_w(a, 7);
   // ---- 3. gate/up k chunks: the shared ones (tiles in since before the route) and the shared down unit's B
@@ -674,15 +697,15 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
       const uint32_t u = uw[k];
       if (u == kNone || (u >> 30) != kUShared) continue;
       const int c = (int)(u & 3u);
-      prep_wait(1u << (8 + c));
+      prep_wait(1u << (16 + c));
       f32x16 acc;
       zero16(acc);
       pair_mfma<KS, 8>(tiles + ((u >> 24) & 0x3Fu) * SLOT, &sprep[c][0], 0, 8, acc);
       task_done((int)((u >> 2) & 0xFu), true, c, acc[0]);
     }
-    if (dn_shared) {
+    if (D0.shared) {
 #pragma unroll
-      for (int kt = 0; kt < kDnKt; kt++) dw[kt] = decode_pair<KS>(tiles + dslot * SLOT, kt);
+      for (int kt = 0; kt < kDnKt; kt++) dw[kt] = decode_pair<KS>(tiles + D0.slot * SLOT, kt);
     }
   }
   if (ok) {
@@ -694,8 +717,8 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
       if (u == kNone || (u >> 30) != kURouted) continue;
       const uint8_t *tl = tiles + ((u >> 24) & 0x3Fu) * SLOT;
       const int c = (int)(u & 3u);
-      const _Float16 *xs = &prep[kGrp * ((u >> 8) & 1u) + c][0] + 8 * (lane >> 5);
-      prep_wait(1u << (kGrp * ((u >> 8) & 1u) + c));
+      const _Float16 *xs = &prep[kGrp * ((u >> 8) & 3u) + c][0] + 8 * (lane >> 5);
+      prep_wait(1u << (kGrp * ((u >> 8) & 3u) + c));
       const int first = end_u[k] - dma_ops(8 * pb);  // requests issued before this chunk's
       f32x16 acc;
       zero16(acc);
@@ -715,13 +738,17 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
   __builtin_amdgcn_s_setprio(0);
   stamp_w(a, 1);
   stamp(a, 4);
+  if (ok) {  // down tiles into the slots of gate/up chunks this wave has finished
+    if (D0.unit >= 0 && D0.reuse) issue_dn(D0);
+    if (D1.unit >= 0 && D1.reuse) issue_dn(D1);
+  }
 
-  // ---- 4. the routed down unit's tiles into B operands; the h blocks from the gate/up partials (the NKG k group
-  // sums of each column folded left in k order)
-  if (ok && dunit >= 0 && !dn_shared) {
-    wait_vm(nops - end_dn);
+  // ---- 4. the first routed down unit's tiles into B operands; the h blocks from the gate/up partials (the NKG k
+  // group sums of each column folded left in k order)
+  if (ok && D0.unit >= 0 && !D0.shared) {
+    wait_vm(nops - D0.end);
 #pragma unroll
-    for (int kt = 0; kt < kDnKt; kt++) dw[kt] = decode_pair<K>(tiles + dslot * SLOT, kt);
+    for (int kt = 0; kt < kDnKt; kt++) dw[kt] = decode_pair<K>(tiles + D0.slot * SLOT, kt);
   }
   stamp_w(a, 2);
   // h loaders: the first 2 nh waves, which the SIMDs serve first (oldest first); wave (h slot, proj), lane: columns
@@ -783,16 +810,22 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
   }
   __builtin_amdgcn_s_setprio(0);
   // ---- 5. down: 8 k tiles of h against the unit's decoded tiles; one tagged partial per unit
-  if (ok && dunit >= 0) {
-    flag_wait(&s_hrdy, 1u << (8 + dhs));  // its h block
+  auto down_unit = [&](const DnUnit &D) {
+    flag_wait(&s_hrdy, 1u << (8 + D.hs));  // its h block
     f32x16 d;
     zero16(d);
-    const _Float16 *ha = &hl[dhs][0] + 8 * (lane >> 5);
+    const _Float16 *ha = &hl[D.hs][0] + 8 * (lane >> 5);
 #pragma unroll
     for (int kt = 0; kt < kDnKt; kt++)
       d = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const f16x8 *)(ha + kt * 16), dw[kt], d, 0, 0, 0);
-    if (lane < 32)
-      st_tag(part_dn + ((size_t)d_ls * NBI + d_cb) * HID + d_c * 128 + d_p * 32 + lane, d[0], tag);
+    if (lane < 32) st_tag(part_dn + ((size_t)D.ls * NBI + D.cb) * HID + D.c * 128 + D.p * 32 + lane, d[0], tag);
+  };
+  if (ok && D0.unit >= 0) down_unit(D0);
+  if (ok && D1.unit >= 0) {  // a routed unit (the plan gives a wave at most one shared down unit, first)
+    wait_vm(nops - D1.end);
+#pragma unroll
+    for (int kt = 0; kt < kDnKt; kt++) dw[kt] = decode_pair<K>(tiles + D1.slot * SLOT, kt);
+    down_unit(D1);
   }
   stamp(a, 6);
 
@@ -878,11 +911,12 @@ StepFn step_for_k(int K, int KS) {
   return nullptr;
 }
 StepFn step_fn(int K, int KS, int hid, int inter) {
+  if (hid == 2560 && inter == 640) return step_for_k<2560, 640>(K, KS);  // the reference's own shape
   if (hid == 2048 && inter == 512) return step_for_k<2048, 512>(K, KS);
   if (hid == 1024 && inter == 256) return step_for_k<1024, 256>(K, KS);
   return nullptr;
 }
-size_t step_lds(int K, int KS) { return (size_t)kMaxSlots * kDnKt * 64 * std::max(K, KS); }
+uint32_t slot_bytes(int K, int KS) { return kDnKt * 64 * std::max(K, KS); }
 }  // namespace
 
 int moe_fused_grid() {
@@ -897,8 +931,9 @@ int moe_fused_grid() {
 
 // The work plan (see the kernel's header). Returns ok = false when the shape does not fit the kernel's per-wave
 // limits; the layer then runs the staged path.
-MoePlan moe_fused_plan(int hid, int inter, int topk, int nslot, int G, bool q8) {
+MoePlan moe_fused_plan(int hid, int inter, int topk, int nslot, int G, bool q8, int slots) {
   MoePlan pl;
+  slots = std::min(slots, kMaxSlots);
   const int NP = inter / 32, NG = NP / 4, NBI = inter / 128, NBLK = hid / 128, UPS = NBI * NBLK * 4;
   const int NKG = hid / (128 * kGrp), hs = nslot > topk ? 1 : 0, NCOL = nslot * 2 * NP;
   if (inter % 128 || hid % (128 * kGrp) || G < 1 || NBLK > G) return pl;
@@ -908,6 +943,7 @@ MoePlan moe_fused_plan(int hid, int inter, int topk, int nslot, int G, bool q8) 
   const long US = hs ? UPS : 0, UR = (long)topk * UPS;
   auto key_of = [&](long t) { return (uint32_t)((t / (4L * NKG * NG)) * NKG + (t / 4) % NKG); };  // matrix, k group
   std::vector<int> hb_first((size_t)nslot * NBI, -1);
+  int used = 0;  // LDS slots the busiest workgroup needs
   for (int b = 0; b < G; b++) {
     uint32_t *pw = &w[(size_t)b * kPW];
     const long t0 = TR * b / G, t1 = TR * (b + 1) / G, s0 = TS * b / G, s1 = TS * (b + 1) / G;
@@ -916,7 +952,7 @@ MoePlan moe_fused_plan(int hid, int inter, int topk, int nslot, int G, bool q8) 
     pw[P_NRT] = (uint32_t)(t1 - t0);
     pw[P_ST0] = (uint32_t)s0;
     pw[P_NST] = (uint32_t)(s1 - s0);
-    // prep groups: the distinct (matrix, k group) of the routed run (at most 2); one of the shared run
+    // prep groups: the distinct (matrix, k group) of the routed run (at most 3); one of the shared run
     std::vector<uint32_t> keys;
     for (long t = t0; t < t1; t++)
       if (std::find(keys.begin(), keys.end(), key_of(t)) == keys.end()) keys.push_back(key_of(t));
@@ -928,22 +964,41 @@ MoePlan moe_fused_plan(int hid, int inter, int topk, int nslot, int G, bool q8) 
     if (s1 > s0) pw[P_SPK] = key_of(s0);
     int slot = 0;
     std::vector<int> nu(kWaves, 0), simd(4, 0), ndn(kWaves, 0);
+    std::vector<std::vector<uint32_t>> rs(kWaves);  // per wave: LDS slots of its routed chunks, free for a down unit
     // every unit (a k chunk or a down unit: 8 k tile pairs to decode) goes to the wave whose SIMD has the least routed
     // work so far (then the wave with the fewest units): after the route the decode is the step's VALU bound, and a
     // SIMD's waves share it. The shared expert's units (requested before the route) go to waves kSpw .. kCtl - 1: not the control
-    // wave (it polls the logits meanwhile) and not the routed prep waves (their prep gates the routed chunks). A wave
-    // holds at most one down unit.
+    // wave (it polls the logits meanwhile) and not the routed prep waves (their prep gates the routed chunks). A down
+    // unit goes to a wave without one if any can take it (a wave holds at most kMaxDn, a shared one only as its
+    // first); once the LDS slots run out, a routed down unit takes a slot of one of its wave's routed chunks (its
+    // tiles are requested after that chunk is done).
     auto put = [&](bool pre_route, uint32_t word) {
-      const bool dn = (word >> 30) == kUDown;
+      const uint32_t type = word >> 30;
+      const bool dn = type == kUDown, reuse = dn && !pre_route && slot >= slots;
       int best = -1;
       for (int w = pre_route ? kSpw : 0; w < (pre_route ? kCtl : kWaves); w++) {
-        if (nu[w] >= kUnitsPerWave || (dn && ndn[w])) continue;
-        if (best < 0 || simd[w % 4] < simd[best % 4] || (simd[w % 4] == simd[best % 4] && nu[w] < nu[best])) best = w;
+        if (nu[w] >= kUnitsPerWave || (dn && ndn[w] >= (pre_route ? 1 : kMaxDn)) || (reuse && rs[w].empty())) continue;
+        const bool fewer_dn = dn && best >= 0 && ndn[w] < ndn[best];
+        const bool same_dn = !dn || best < 0 || ndn[w] == ndn[best];
+        if (best < 0 || fewer_dn ||
+            (same_dn && (simd[w % 4] < simd[best % 4] || (simd[w % 4] == simd[best % 4] && nu[w] < nu[best]))))
+          best = w;
       }
-      if (best < 0 || slot >= kMaxSlots) return -1;
-      pw[P_U + kUnitsPerWave * best + nu[best]++] = word | (uint32_t)slot++ << 24;
+      if (best < 0) return -1;
+      uint32_t sl;
+      if (reuse) {
+        sl = rs[best].front();
+        rs[best].erase(rs[best].begin());
+        word |= kDnReuse;
+      } else {
+        if (slot >= slots) return -1;
+        sl = (uint32_t)slot++;
+      }
+      pw[P_U + kUnitsPerWave * best + nu[best]++] = word | sl << 24;
+      if (type == kURouted) rs[best].push_back(sl);
       simd[best % 4] += pre_route ? 0 : 1;  // the shared units run while the routed tiles are on their way
       ndn[best] += dn ? 1 : 0;
+      used = std::max(used, slot);
       return best;
     };
     // gate/up tasks: the shared ones first (requested before the route), then the routed ones
@@ -987,6 +1042,7 @@ MoePlan moe_fused_plan(int hid, int inter, int topk, int nslot, int G, bool q8) 
   // and, with the 8-bit shared expert, its gate / up [2 inter] and down [hid] rows
   pl.part_floats = 2 * ((size_t)NCOL * NKG * 32 + (size_t)nslot * NBI * hid + (q8 ? 2 * (size_t)inter + hid : 0));
   pl.grid = G;
+  pl.slots = used;
   pl.ok = true;
   return pl;
 }
@@ -1011,20 +1067,41 @@ void launch_moe_fused(const MoeArgs &a, int grid, hipStream_t s) {
   if (grid <= 0) grid = moe_fused_grid();
   IJ_CHECK(grid * kWaves >= a.ne + a.has_sgate, "fused MoE: %d router rows on %d workgroups", a.ne + a.has_sgate, grid);
   IJ_CHECK(a.units && a.part && a.fsync, "fused MoE: no plan");
-  const size_t lds = step_lds(a.lay.K, KS);  // (the dynamic LDS limit is raised by init_fused_attrs)
+  IJ_CHECK(a.fused_slots > 0 && a.fused_slots <= moe_fused_slots(a.lay.K, KS, a.hid, a.inter),
+           "fused MoE: %d LDS slots planned", a.fused_slots);
+  const size_t lds = (size_t)a.fused_slots * slot_bytes(a.lay.K, KS);  // (limit raised by init_fused_attrs)
   void *args[] = {const_cast<MoeArgs *>(&a)};
   IJ_HIP(hipLaunchKernel(f, dim3(grid), dim3(64 * kWaves), args, lds, s));
 }
 
 const void *moe_fused_kernel(int K, int KS, int hid, int inter) { return step_fn(K, KS, hid, inter); }
 
+// The LDS slots an instance has room for: the CU's 160 KB less its static LDS, in slots of 8 k tile pairs (at most
+// kMaxSlots, the slot field's range).
+constexpr size_t kCuLds = 160 * 1024;
+int moe_fused_slots(int K, int KS, int hid, int inter) {
+  const StepFn f = step_fn(K, KS, hid, inter);
+  if (!f) return 0;
+  static std::mutex mu;
+  static std::map<const void *, int> cache;
+  std::lock_guard<std::mutex> g(mu);
+  auto it = cache.find(f);
+  if (it != cache.end()) return it->second;
+  hipFuncAttributes at;
+  IJ_HIP(hipFuncGetAttributes(&at, f));
+  const int n = (int)std::min<size_t>(kMaxSlots, (kCuLds - at.sharedSizeBytes) / slot_bytes(K, KS));
+  cache[f] = n;
+  return n;
+}
+
 // every instance's dynamic LDS limit, once at device set-up (never inside a stream capture)
 void init_fused_attrs() {
-  for (int hid : {1024, 2048})
+  for (int hid : {1024, 2048, 2560})
     for (int K = 4; K <= 6; K++)
       for (int KS = 4; KS <= 6; KS++)
         if (const StepFn f = step_fn(K, KS, hid, hid / 4))
-          IJ_HIP(hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)step_lds(K, KS)));
+          IJ_HIP(hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                     (int)(moe_fused_slots(K, KS, hid, hid / 4) * slot_bytes(K, KS))));
 }
 
 }  // namespace ijah

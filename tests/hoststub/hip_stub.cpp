@@ -377,7 +377,8 @@ ExpertLayout expert_layout(int hid, int inter, int K) {  // the same regions, pa
   return L;
 }
 int moe_fused_grid() { return 256; }
-MoePlan moe_fused_plan(int, int, int, int, int, bool) { return MoePlan(); }  // no fused plan: the staged path
+MoePlan moe_fused_plan(int, int, int, int, int, bool, int) { return MoePlan(); }  // no fused plan: the staged path
+int moe_fused_slots(int, int, int, int) { return 0; }
 size_t moe_fused_q8_index(int, int, int) { return 0; }
 bool moe_fused_supported(int, int, int, int, int, int, int, bool) { return false; }
 bool moe_q8_supported(int hid, int inter) { return hid % 128 == 0 && inter % 128 == 0 && inter <= 1024; }

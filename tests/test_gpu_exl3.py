@@ -62,6 +62,25 @@ def test_linear_trunk_shapes(eng, oracle, inp, out, K, R):
     assert rel(y, oracle.exl3_linear(x, t, su, sv, exact=True)) < 1e-2
 
 
+@pytest.mark.parametrize("inp,out,K,R", [(2560, 10240, 6, 1), (2560, 12288, 6, 1), (2560, 640, 6, 1), (320, 10240, 8, 1),
+                                         (2560, 12288, 6, 4), (2560, 640, 6, 16), (320, 10240, 8, 8)])
+def test_linear_reference_trunk_shapes(eng, oracle, inp, out, K, R):
+    """The reference's own trunk shapes, whose published timings BASELINE.md quotes (docs/trunk6.md:93-100): 2560 ->
+    10240 and 2560 -> 12288 at K6, 2560 -> 640 at K6, 320 -> 10240 at K8; against the oracle, and rows bit-identical
+    to the one-row run."""
+    print(f"linear reference shape {inp}x{out} K{K} R{R}", flush=True)
+    rng = np.random.default_rng(inp + out * 3 + K + R)
+    t, su, sv = synth.linear(rng, inp, out, K)
+    x = synth.bf16_values(rng, R, inp)
+    lin = eng.exl3_linear(t, su, sv)
+    y = lin.run(x)
+    assert rel(y, oracle.exl3_linear(x, t, su, sv)) < 5e-5
+    assert rel(y, oracle.exl3_linear(x, t, su, sv, exact=True)) < 1e-2
+    if R > 1:
+        for i in (0, R - 1):
+            assert np.array_equal(lin.run(x[i:i + 1])[0], y[i])
+
+
 @pytest.mark.parametrize("inp,out,K,R", [(2048, 512, 5, 9), (2048, 512, 5, 16), (2048, 512, 5, 32),
                                          (2048, 4096, 6, 16), (4096, 2048, 6, 16), (320, 640, 7, 12), (96, 48, 4, 12),
                                          (2048, 1024, 8, 16), (2048, 640, 3, 20), (2048, 512, 2, 10), (48, 96, 8, 12),

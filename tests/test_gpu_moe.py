@@ -504,3 +504,30 @@ def test_few_row_pool_shared_by_layers(eng):
     assert np.array_equal(a.run(x4), y4)
     assert np.array_equal(b.run(x32), yb)
     assert np.array_equal(a.run(x4), y4)
+
+
+@pytest.mark.parametrize("R", [2, 4, 6, 8])
+def test_moe_verify_draft_sizes_bit_identical(eng, R):
+    """The reference's draft sizes (grouped verify at R = 2 .. 8, docs/mtp.md:987-993), config 2's layer at full size
+    (512 experts, top-10 + shared, K5): every row equals the fused one-row step on that row, bit for bit."""
+    print(f"moe verify R{R} rows vs one row", flush=True)
+    m = eng.moe_synth(2048, 512, 512, 10, 5, True, 5, seed=50 + R)
+    _rows_match_one_row(m, synth.bf16_values(np.random.default_rng(51 + R), R, 2048), R)
+
+
+@pytest.mark.parametrize("shared,K,Ks", [(True, 5, 5), (True, 5, 6), (True, 4, 4), ("q8", 5, 5), ("q8", 6, 6)])
+def test_moe_fused_reference_shape(eng, oracle, shared, K, Ks):
+    """The fused one-row step at the reference's own shape (hidden 2560, inter 640: kernels/fn_moe.metal:16), where a
+    workgroup's units outnumber its LDS slots and some down units take a finished gate/up chunk's slot: the step is
+    the fused launch (its kernel timed by ne_moe_time_kernels), against the oracle, and bit-identical to itself."""
+    print(f"moe fused 2560x640 shared={shared} K{K}/{Ks}", flush=True)
+    w = synth.moe_layer(200 + K + Ks, hid=2560, inter=640, ne=64, topk=10, K=K, shared=shared, Ks=Ks, sgate=True)
+    W = oracle.MoeWeights(w)
+    m = eng.moe_create(w)
+    x = synth.bf16_values(np.random.default_rng(201 + K), 1, 2560)
+    assert "fused" in eng.moe_time_kernels([m], 1, eng.from_numpy(x), reps=1)
+    y = check_q8_layer(eng, oracle, m, W, x, True) if shared == "q8" else check_layer(eng, oracle, m, W, x)[0]
+    for _ in range(2):
+        assert np.array_equal(m.run(x), y)
+    if shared is True:  # the verify rows of this shape agree with the fused step, bit for bit
+        _rows_match_one_row(m, synth.bf16_values(np.random.default_rng(202), 4, 2560), 4)
