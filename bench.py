@@ -86,17 +86,41 @@ def cpu_baseline(seconds=10.0):
                       f"all 512 experts resident in host memory) in {el:.1f}s"}
 
 
+def measure_m1(eng, hid, inter, shared, n_layers, steps, seed, k=K):
+    """The one-row step (fused launch) of another layer form: the reference's own shape (hidden 2560, inter 640) and/or
+    its 8-bit affine shared expert ("q8", the form of its real packs) instead of an EXL3 one; a chain of n_layers
+    distinct synthetic layers in one graph, as the headline line. Returns a dict for the JSON line."""
+    from ijah_amd import synth
+    layers = [eng.moe_synth(hid, inter, NE, TOPK, k, shared, k, seed=seed + 7919 * i) for i in range(n_layers)]
+    xb = eng.from_numpy(synth.bf16_values(np.random.default_rng(seed), 1, hid))
+    yb = eng.alloc(hid * 4)
+    for m in layers:
+        m.run_bufs(1, xb, yb)
+    eng.sync()
+    byts = float(np.mean([m.bytes(1) for m in layers]))
+    us = eng.moe_time(layers, 1, xb, warmup=2, reps=steps)
+    kus = eng.moe_time_kernels(layers[:4], 1, xb, reps=2)
+    for m in layers:
+        m.free()
+    gbs = byts / (us * 1e-6) / 1e9
+    out = {"hidden": hid, "intermediate": inter, "shared": "8-bit affine g128" if shared == "q8" else f"EXL3 K{k}",
+           "fused": "fused" in kus, "us_per_layer": round(us, 2), "bytes_per_layer": int(byts),
+           "GBps": round(gbs, 1), "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2)}
+    print(f"m1 {hid}x{inter} shared={shared}: {out}", file=sys.stderr, flush=True)
+    return out
+
+
 def moe_flops(R, hid=HID, inter=INTER, topk=TOPK, shared=1):
     """Algorithmic flops of the layer's expert GEMMs at R rows (gate, up, down per slot; router excluded)."""
     return 2.0 * 3 * hid * inter * R * (topk + shared)
 
 
-def measure_batch(eng, R, n_layers, steps, seed, k=K):
+def measure_batch(eng, R, n_layers, steps, seed, k=K, shared=True):
     """The layer at R rows (BASELINE.json config 4 at R = 16, config 5 at R = 4096) on the grouped matrix-core path:
     a chain of n_layers distinct synthetic layers in one HIP graph, experts and shared expert at k bits. Returns a
     dict for the JSON line."""
     from ijah_amd import synth
-    layers = [eng.moe_synth(HID, INTER, NE, TOPK, k, True, k, seed=seed + 7919 * i) for i in range(n_layers)]
+    layers = [eng.moe_synth(HID, INTER, NE, TOPK, k, shared, k, seed=seed + 7919 * i) for i in range(n_layers)]
     x = synth.bf16_values(np.random.default_rng(seed), R, HID)
     xb = eng.from_numpy(x)
     yb = eng.alloc(R * HID * 4)
@@ -106,7 +130,8 @@ def measure_batch(eng, R, n_layers, steps, seed, k=K):
     byts = float(np.mean([m.bytes(R) for m in layers]))
     us = eng.moe_time(layers, R, xb, warmup=2, reps=steps)
     fl = moe_flops(R)
-    out = {"rows": R, "K": k, "layers_per_step": n_layers, "us_per_layer": round(us, 2),
+    out = {"rows": R, "K": k, "shared": "8-bit affine g128" if shared == "q8" else f"EXL3 K{k}",
+           "layers_per_step": n_layers, "us_per_layer": round(us, 2),
            "tokens_per_s_per_layer": round(R * 1e6 / us, 1),
            "weight_bytes_per_layer": int(byts), "weight_GBps": round(byts / (us * 1e-6) / 1e9, 1),
            "expert_gemm_TFLOPs": round(fl / (us * 1e-6) / 1e12, 2),
@@ -459,6 +484,7 @@ def main():
     ap.add_argument("--hc-only", action="store_true", help="only measure the hyper-connection read and exit")
     ap.add_argument("--batch-rows", type=int, default=0, metavar="R",
                     help="only measure the grouped matrix-core layer at R rows (a 4-layer graph) and exit")
+    ap.add_argument("--q8", action="store_true", help="with --batch-rows: the 8-bit affine shared expert")
     ap.add_argument("--moe-trace", action="store_true",
                     help="the fused M=1 step's per-wave timeline (trace mode), then exit")
     ap.add_argument("--probe", action="store_true",
@@ -501,7 +527,8 @@ def main():
               flush=True)
         return
     if a.batch_rows:
-        print(json.dumps(measure_batch(eng, a.batch_rows, 4, a.steps, a.seed + a.batch_rows)), flush=True)
+        print(json.dumps(measure_batch(eng, a.batch_rows, 4, a.steps, a.seed + a.batch_rows,
+                                       shared="q8" if a.q8 else True)), flush=True)
         return
     t_setup = time.perf_counter()
     layers = [eng.moe_synth(HID, INTER, NE, TOPK, K, True, K, seed=a.seed * 1000 + i) for i in range(a.layers)]
@@ -546,6 +573,10 @@ def main():
     if not a.no_batch:
         for m in layers:  # the M=1 layers' memory is no longer needed
             m.free()
+        layers = []
+        extra["m1_q8_shared"] = measure_m1(eng, HID, INTER, "q8", 16, a.steps, a.seed + 31)
+        extra["m1_2560x640"] = measure_m1(eng, 2560, 640, True, 16, a.steps, a.seed + 32)
+        extra["m1_2560x640_q8_shared"] = measure_m1(eng, 2560, 640, "q8", 16, a.steps, a.seed + 33)
         for R in (2, 4, 8):  # the reference's draft sizes (docs/mtp.md:987-993)
             extra[f"verify_r{R}"] = measure_batch(eng, R, 32, max(5, a.steps // 5), a.seed + R)
             print(f"verify R={R}: {extra[f'verify_r{R}']}", file=sys.stderr, flush=True)
@@ -555,6 +586,8 @@ def main():
         print(f"verify R=16 K4: {extra['verify_r16_k4']}", file=sys.stderr, flush=True)
         extra["prefill_r4096"] = measure_batch(eng, 4096, 4, 3, a.seed + 4096)
         print(f"prefill R=4096: {extra['prefill_r4096']}", file=sys.stderr, flush=True)
+        extra["prefill_r4096_q8_shared"] = measure_batch(eng, 4096, 4, 3, a.seed + 4097, shared="q8")
+        print(f"prefill R=4096 q8 shared: {extra['prefill_r4096_q8_shared']}", file=sys.stderr, flush=True)
     if not a.no_trunk:
         extra["trunk_m1"] = measure_trunk(eng, 1, max(5, a.steps // 5), a.seed + 3)
         extra["trunk_m16"] = measure_trunk(eng, 16, max(5, a.steps // 5), a.seed + 4)

@@ -564,6 +564,7 @@ struct ne_moe {
   uint8_t *experts = nullptr, *shared = nullptr;
   uint8_t *q8 = nullptr;       // the 8-bit affine shared expert (q8_offsets), in place of an EXL3 shared slot
   float *q8gu = nullptr, *q8o = nullptr;  // its per-row outputs (staged and batched paths)
+  uint16_t *q8bf = nullptr;               // its weight bytes as bf16 (the many-row matrix-core form)
   uint16_t *router = nullptr;  // [ne + has_sgate][hid]
   int Rcap = 0;
   float *logits = nullptr, *sgv = nullptr, *guo = nullptr, *dn = nullptr;
@@ -582,7 +583,7 @@ struct ne_moe {
   int last_R = 0;
   float *last_y = nullptr;
   ~ne_moe() {
-    for (void *p : std::initializer_list<void *>{experts, shared, q8, q8gu, q8o, router, logits, sgv, guo, dn, route,
+    for (void *p : std::initializer_list<void *>{experts, shared, q8, q8bf, q8gu, q8o, router, logits, sgv, guo, dn, route,
                                                  sync, trace, hprep, plan, part, fsync})
       dev_free(p);
     free_batch();
@@ -688,6 +689,7 @@ struct ne_moe {
     a.fsync = fsync;
     a.fused_slots = plan_slots;
     a.q8 = q8;
+    a.q8bf = q8bf;
     a.q8gu = q8gu;
     a.q8o = q8o;
     return a;
@@ -830,6 +832,9 @@ ne_moe *moe_create(const ne_moe_desc &d) {
     }
     m->q8 = dev_alloc<uint8_t>(qb.size());
     IJ_HIP(hipMemcpy(m->q8, qb.data(), qb.size(), hipMemcpyHostToDevice));
+    m->q8bf = dev_alloc<uint16_t>(3ull * d.hid * d.inter);
+    launch_q8_bf16(m->q8, m->q8bf, d.hid, d.inter, stream());
+    IJ_HIP(hipStreamSynchronize(stream()));
   }
   const size_t rrows = (size_t)d.ne + m->has_sgate;
   m->router = dev_alloc<uint16_t>(rrows * d.hid);
@@ -971,6 +976,8 @@ NE_API ne_moe *ne_moe_synth(int hid, int inter, int ne, int topk, int K, int has
       const int in[3] = {hid, hid, inter};
       for (int p = 0; p < 3; p++)
         launch_fill_q8_sb((uint32_t *)(m->q8 + o.sb[p]), (uint64_t)inter * hid / kQ8Group, in[p], seed * 13 + p, s);
+      m->q8bf = dev_alloc<uint16_t>(3ull * hid * inter);
+      launch_q8_bf16(m->q8, m->q8bf, hid, inter, s);
     }
     if (has_shared == 1) {
       m->slay = expert_layout(hid, inter, Ks);

@@ -65,6 +65,7 @@ struct MoeArgs {
   // slot (nslot == topk then): g = rr(gate . x), u = rr(up . x), h = rr(silu(g) u), o = rr(down . h) (rr: bf16 when
   // refr); the combine adds the shared gate times o after the routed slots. Null: none.
   const uint8_t *q8 = nullptr;
+  const uint16_t *q8bf = nullptr;  // its weight bytes as bf16 values [3 matrices], for the many-row form
   float *q8gu = nullptr;  // [R][2 inter] g, u (staged and batched paths)
   float *q8o = nullptr;   // [R][hid] o
 };
@@ -89,6 +90,7 @@ __host__ __device__ inline uint64_t q8_block_bytes(int hid, int inter) {
 }
 // the 8-bit shared expert's two launches for the staged and batched paths (moe_q8.hip): q8gu, then q8o
 void launch_moe_q8(const MoeArgs &a, hipStream_t s);
+void launch_q8_bf16(const uint8_t *q8, uint16_t *bf, int hid, int inter, hipStream_t s);  // weight bytes -> bf16
 bool moe_q8_supported(int hid, int inter);
 void launch_moe_router(const MoeArgs &a, hipStream_t s);
 void launch_moe_gateup(const MoeArgs &a, hipStream_t s);

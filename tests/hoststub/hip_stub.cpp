@@ -359,6 +359,10 @@ void launch_moe_down(const MoeArgs &a, hipStream_t) { use_moe(a, "moe_down"); }
 void launch_moe_combine(const MoeArgs &a, hipStream_t) { use_moe(a, "moe_combine"); }
 void launch_moe_fused(const MoeArgs &a, int, hipStream_t) { use_moe(a, "moe_fused"); }
 void launch_moe_q8(const MoeArgs &a, hipStream_t) { use_moe(a, "moe_q8"); }
+void launch_q8_bf16(const uint8_t *q, uint16_t *b, int, int, hipStream_t) {
+  use(q, "q8_bf16");
+  use(b, "q8_bf16");
+}
 void launch_moe_batch(const MoeArgs &a, const MoeBatchBufs &b, hipStream_t) {
   use_moe(a, "moe_batch");
   std::lock_guard<std::recursive_mutex> l(mu);

@@ -406,26 +406,35 @@ def test_hc_read_then_moe_hc_write(eng, oracle):
 def check_q8_layer(eng, oracle, moe, W, x, sgate):
     """The layer with the reference's 8-bit affine shared expert (kernels/fn_moe.metal:40-46, :264-290): the shared
     output o = rr(down . rr(silu(rr g) rr u)) within one bf16 step of the oracle's (the GPU's f32 sums and the
-    oracle's f64 ones may round to neighbouring bf16 values), >= 95% of it bit-exact; the layer within rel-L2 1e-3 of
+    oracle's f64 ones may round to neighbouring bf16 values; near zero, within 2^-12 of the row's rms), >= 95% of it
+    bit-exact; the layer within rel-L2 1e-3 of
     the oracle's kernel arithmetic on the GPU's route and within 1e-2 of the f64 layer."""
     R = x.shape[0]
     y = moe.run(x)
     rt, sg = moe.read("route", R), moe.read("shared_gate", R)
     o = moe.read("shared_q8", R)
+    y_all = y
+    if R > 40:  # many rows: sampled rows against the oracle (its layer costs ~1 s a row)
+        rows = [0, 1, R // 2, R - 1]
+        x, y, rt, sg, o = x[rows], y[rows], rt[rows], sg[rows], o[rows]
+        R = len(rows)
     for r in range(R):
         want = oracle.q8_shared(W, x[r])
         assert np.mean(o[r] == want) > 0.95, (r, np.mean(o[r] == want))
-        assert np.all(np.abs(o[r] - want) <= np.abs(want) * 2 ** -6 + 1e-6), r
+        # one bf16 step of the value, or (an output near zero, where the sums cancel) a small part of the row's scale
+        scale = float(np.sqrt(np.mean(want.astype(np.float64) ** 2)))
+        assert np.all(np.abs(o[r] - want) <= np.abs(want) * 2 ** -6 + scale * 2 ** -12), r
     sgv = sg if sgate else None
     assert rel(y, oracle.moe_experts(W, x, rt, sg=sgv)) < 1e-3
     assert rel(y, oracle.moe_experts(W, x, rt, sg=sgv, exact=True)) < 1e-2
-    return y
+    return y_all
 
 
-@pytest.mark.parametrize("R", [1, 3, 16, 40])
+@pytest.mark.parametrize("R", [1, 3, 16, 40, 200])
 def test_moe_q8_shared_expert(eng, oracle, R):
-    """R = 1 runs the fused one-row step, 3 and 16 the few-row kernels, 40 the many-row ones; each with the 8-bit
-    shared expert and its gate."""
+    """R = 1 runs the fused one-row step, 3 and 16 the few-row kernels, 40 and 200 the many-row ones (the shared
+    expert on the matrix cores: bf16 weights, x split into bf16 hi + lo); each with the 8-bit shared expert and its
+    gate."""
     print(f"moe q8 shared R{R}", flush=True)
     w = synth.moe_layer(150 + R, hid=2048, inter=512, ne=64, topk=10, K=5, shared="q8", sgate=True)
     m = eng.moe_create(w)
