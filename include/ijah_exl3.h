@@ -16,7 +16,8 @@ extern "C" {
 
 /* ---- buffers on a discrete GPU ---- */
 /* Writes the whole host mirror returned by ne_buf_contents back to the device now (changed bytes also go on their
- * own before the next library call that uses the buffer). No reference counterpart: the reference's buffers are
+ * own before the next library call that uses the buffer, unless that call is made while the library stream is
+ * being captured into a graph: flush before a capture). No reference counterpart: the reference's buffers are
  * unified memory (reference include/engine.h:6-7), where this is a no-op. */
 NE_API int ne_buf_flush(ne_buf *b);
 /* Waits for all queued GPU work of the library (the reference's Recorder::wait, core/recorder.h:76). */

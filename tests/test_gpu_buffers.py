@@ -35,21 +35,30 @@ def test_mirror_writes_reach_the_device_before_use(eng):
     assert np.array_equal(b.numpy(), want)
 
 
-def test_reference_pattern_numpy_write_then_run_kernel(eng):
+def test_reference_pattern_numpy_write_then_run_kernel(eng, oracle):
     """Buf.numpy() writes, then ne_run_kernel on the buffer (the reference's tools/engine.py usage), then the output
-    read back through numpy()."""
+    read back through numpy(): the trellis tiles written through the mirror are decoded by a kernel run by name."""
     print("buffers: numpy write then run_kernel", flush=True)
-    n = 1 << 16
-    src, dst = eng.alloc(n), eng.alloc(n)
-    s = src.numpy(np.uint8)
-    s[:] = np.arange(n, dtype=np.uint32).astype(np.uint8)
-    d0 = dst.numpy(np.uint8)  # a mirror of dst taken before the kernel writes it
-    assert not d0.any()
-    eng.run_kernel("copy_u128", [src, dst, np.uint64(n // 16)], (n // 16 // 256, 1, 1), (256, 1, 1))
-    assert np.array_equal(dst.numpy(np.uint8), s)
-    # the stale mirror d0 was not touched: using dst again does not put its old zeros back
-    eng.run_kernel("copy_u128", [dst, src, np.uint64(n // 16)], (n // 16 // 256, 1, 1), (256, 1, 1))
-    assert np.array_equal(src.download(np.uint8), s)
+    from ijah_amd import synth
+    K, inp, out = 5, 64, 96
+    t, _, _ = synth.linear(np.random.default_rng(12), inp, out, K)
+    IT, OT = inp // 16, out // 16
+    rel_t = np.zeros((OT // 2, IT, 2, 16 * K), np.uint16)  # the library's tile order: [out/32 pairs][in/16][2]
+    for tk in range(IT):
+        for tn in range(OT):
+            rel_t[tn // 2, tk, tn % 2] = t[tk, tn]
+    tiles, w = eng.alloc(rel_t.nbytes), eng.alloc(inp * out * 2)
+    tiles.numpy(np.uint16)[:] = rel_t.reshape(-1)
+    w0 = w.numpy(np.uint16)  # a mirror of w taken before the kernel writes it
+    assert not w0.any()
+    run = lambda: eng.run_kernel("exl3_decode", [tiles, np.int32(IT), np.int32(OT), w], grid=((IT * OT + 3) // 4, 1, 1),
+                                 tg=(256, 1, 1), fconsts=[(10, "u32", K)])
+    run()
+    want = oracle.decode(t).view(np.uint16).reshape(-1)
+    assert np.array_equal(w.numpy(np.uint16), want)
+    # the stale mirror w0 was not touched: using w again does not put its old zeros back
+    run()
+    assert np.array_equal(w.download(np.uint16), want)
 
 
 def test_reference_pattern_numpy_write_then_linear(eng, oracle):
