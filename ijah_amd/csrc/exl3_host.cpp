@@ -606,8 +606,8 @@ struct ne_moe {
     }
     const size_t S = (size_t)R * nslot();
     bat.max_chunks = std::max(moe_batch_max_chunks(R, ne, topk, has_shared), bat.vmax_chunks);
-    bat.bk = dev_alloc<uint32_t>(3 * (size_t)(ne + 1) + 1);
-    IJ_HIP(hipMemset(bat.bk, 0, sizeof(uint32_t) * (3 * (size_t)(ne + 1) + 1)));  // bat_hist adds into the counts
+    bat.bk = dev_alloc<uint32_t>(3 * (size_t)(ne + 1) + 2);
+    IJ_HIP(hipMemset(bat.bk, 0, sizeof(uint32_t) * (3 * (size_t)(ne + 1) + 2)));  // bat_hist adds into the counts
     bat.chunks = dev_alloc<uint32_t>(3 * (size_t)bat.max_chunks);
     bat.rows = dev_alloc<uint32_t>(S);
     bat.xh = dev_alloc<uint16_t>(S * 2 * hid);

@@ -120,7 +120,7 @@ size_t moe_fused_q8_index(int hid, int inter, int nslot);
 const void *moe_fused_kernel(int K, int KS, int hid, int inter);  // nullptr if not instantiated
 // The batched layer (moe_batch.hip) for R >= 2 rows: device buffers sized by the host for R rows.
 struct MoeBatchBufs {
-  uint32_t *bk = nullptr;      // [ne + 1] counts, [ne + 1] offsets, [ne + 1] cursors, 1 chunk count
+  uint32_t *bk = nullptr;      // [ne + 1] counts, [ne + 1] offsets, [ne + 1] cursors, 1 chunk count, 1 arrival count
   uint32_t *chunks = nullptr;  // [max_chunks][3] (expert, first sorted row, rows)
   uint32_t *rows = nullptr;    // [R nslot] sorted row -> slot r * nslot + k
   uint16_t *xh = nullptr;      // [R nslot][2][hid] prepared gate / up inputs, fp16, kp order

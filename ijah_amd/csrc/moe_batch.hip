@@ -329,9 +329,9 @@ __device__ void route_one(const MoeArgs &a, int r, uint32_t *lid = nullptr) {
   const float pk = lane < a.topk ? expf(key_value(mykey) - top) : 0.f;
   float sum = 0.f;
   for (int k = 0; k < a.topk; k++) sum += __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(pk), k));
-  if (lane < a.topk) {
-    a.route[(uint64_t)r * 2 * a.topk + lane] = id;
-    a.route[(uint64_t)r * 2 * a.topk + a.topk + lane] = __float_as_uint(pk / sum);
+  if (lane < a.topk) {  // device-coherent stores: bat_route_place's last workgroup reads other workgroups' routes
+    st_cg(a.route + (uint64_t)r * 2 * a.topk + lane, id);
+    st_cg(a.route + (uint64_t)r * 2 * a.topk + a.topk + lane, __float_as_uint(pk / sum));
     if (lid) lid[r * a.topk + lane] = id;  // the caller's LDS copy of the ids
   }
   if (lane == 0) a.sgv[r] = moe_shared_gate(a, sgl);
@@ -458,16 +458,31 @@ __global__ __launch_bounds__(1024) void bat_scan(MoeArgs a, uint32_t *bk, uint32
 // rows for the top-k (route_one: the one-row step's keys and weights); then the routed slots per expert are counted in
 // LDS, scanned into offsets and chunks of at most crows rows (the shared expert takes every row, last), and each slot
 // takes its row in its expert's list (rows[row] = r * nslot + k; the order inside an expert changes no result).
+// The route of 4 rows per workgroup (waves 0-3, one per SIMD: the top-k rounds are a serial chain on one wave), then
+// the workgroup that arrives last (a count in bk, reset by it) places every slot: per-expert counts, offsets and the
+// chunk list (as bat_scan, chunks of at most crows rows), and each slot's row in its expert's list.
+constexpr int kRouteRows = 4;
 __global__ __launch_bounds__(1024) void bat_route_place(MoeArgs a, uint32_t *bk, uint32_t *chunks, int max_chunks,
                                                         uint32_t crows, uint32_t *rows) {
   __shared__ uint32_t sc[1024], cc[1024], offl[1024], cur[1024], lid[1024];
+  __shared__ uint32_t s_last;
   const int tid = threadIdx.x, wave = tid >> 6, n = a.ne + (a.nslot > a.topk ? 1 : 0);
-  for (int r = wave; r < a.R; r += 16) {  // the route, its ids also kept in LDS for the counts and the placement
+  const int r = (int)blockIdx.x * kRouteRows + wave;
+  if (wave < kRouteRows && r < a.R) {
     if (a.ne <= 512)
-      route_one<8>(a, r, lid);
+      route_one<8>(a, r);
     else
-      route_one<16>(a, r, lid);
+      route_one<16>(a, r);
   }
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's route stores have completed
+  __syncthreads();
+  uint32_t *arrived = bk + 3 * (a.ne + 1) + 1;
+  if (tid == 0) s_last = atomicAdd(arrived, 1u) == gridDim.x - 1 ? 1u : 0u;
+  __syncthreads();
+  if (!s_last) return;
+  if (tid == 0) st_cg(arrived, 0u);  // for the next launch
+  for (int q = tid; q < a.R * a.topk; q += 1024)  // every row's ids, as stored
+    lid[q] = ld_cg(a.route + (uint64_t)(q / a.topk) * 2 * a.topk + q % a.topk);
   sc[tid] = 0u;
   cur[tid] = 0u;
   __syncthreads();
@@ -1669,7 +1684,8 @@ void launch_moe_batch(const MoeArgs &a, const MoeBatchBufs &b, hipStream_t s) {
   if (few) {  // route, chunks and placement in one workgroup
     IJ_CHECK(a.ne < 1024 && a.R * a.nslot <= 1024 * 32 && a.R * a.topk <= 1024, "few-row MoE: %d experts, %d slots",
              a.ne, a.R * a.topk);
-    hipLaunchKernelGGL(bat_route_place, dim3(1), dim3(1024), 0, s, a, b.bk, b.chunks, b.max_chunks,
+    hipLaunchKernelGGL(bat_route_place, dim3((a.R + kRouteRows - 1) / kRouteRows), dim3(1024), 0, s, a, b.bk, b.chunks,
+                       b.max_chunks,
                        (uint32_t)kFewChunkRows, b.rows);
   } else {
     hipLaunchKernelGGL(bat_route, dim3((a.R + 3) / 4), dim3(256), 0, s, a);
