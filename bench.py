@@ -477,6 +477,8 @@ def main():
     ap.add_argument("--eager-only", action="store_true",
                     help="run the layer chain eagerly --steps times and exit (for rocprofv3 --pmc passes)")
     ap.add_argument("--no-trunk", action="store_true", help="skip the trunk (config 3) lines")
+    ap.add_argument("--no-m1-forms", action="store_true",
+                    help="skip the one-row lines of the other layer forms (8-bit shared expert, hidden 2560)")
     ap.add_argument("--trunk-only", action="store_true", help="only measure the trunk linears (config 3) and exit")
     ap.add_argument("--trunk-eager", action="store_true",
                     help="only run the trunk linears (config 3, 1 and 16 rows, q/k/v also as one launch) eagerly "
@@ -570,13 +572,14 @@ def main():
                                                  for k, v in kus.items()), file=sys.stderr, flush=True)
 
     extra = {}
-    if not a.no_batch:
-        for m in layers:  # the M=1 layers' memory is no longer needed
-            m.free()
-        layers = []
+    for m in layers:  # the M=1 layers' memory is no longer needed
+        m.free()
+    layers = []
+    if not a.no_m1_forms:
         extra["m1_q8_shared"] = measure_m1(eng, HID, INTER, "q8", 16, a.steps, a.seed + 31)
         extra["m1_2560x640"] = measure_m1(eng, 2560, 640, True, 16, a.steps, a.seed + 32)
         extra["m1_2560x640_q8_shared"] = measure_m1(eng, 2560, 640, "q8", 16, a.steps, a.seed + 33)
+    if not a.no_batch:
         for R in (2, 4, 8):  # the reference's draft sizes (docs/mtp.md:987-993)
             extra[f"verify_r{R}"] = measure_batch(eng, R, 32, max(5, a.steps // 5), a.seed + R)
             print(f"verify R={R}: {extra[f'verify_r{R}']}", file=sys.stderr, flush=True)
