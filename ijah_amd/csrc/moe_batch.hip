@@ -580,7 +580,9 @@ __global__ __launch_bounds__(64 * kPrepWaves, 2) void bat_place_prep(MoeArgs a, 
   const int s = blockIdx.x * kPrepWaves + wave;  // wave-uniform, so the row's buffer descriptors are too
   if (s >= a.R * a.nslot) return;
   uint8_t *lx = lds + (size_t)wave * kPrepUnits * 16, *lsu = lx + 520 * 16;
-  const int r = s / a.nslot, k = s % a.nslot;
+  // routed slots first (row-major), then the shared expert's rows in order
+  const int nrs = a.R * a.topk;
+  const int r = s < nrs ? s / a.topk : s - nrs, k = s < nrs ? s % a.topk : a.topk;
   const int n = lane & 31, h = lane >> 5, proj = n >> 4, bl = n & 15, nb = a.hid / 128;
   const float *x = a.x + (uint64_t)r * a.hid;
   // load lanes: source byte offsets inside a run (x: two blocks of 512 B; su: four blocks of 256 B)
@@ -725,7 +727,7 @@ __global__ __launch_bounds__(64 * kPrepWaves, 2) void bat_place_prep(MoeArgs a, 
     }
     __builtin_amdgcn_wave_barrier();  // the next tile's loads into LDS come after these reads
   }
-  if (lane == 0) rows[(orow_p - xh) / (2 * a.hid)] = (uint32_t)s;
+  if (lane == 0) rows[(orow_p - xh) / (2 * a.hid)] = (uint32_t)(r * a.nslot + k);
 }
 
 // Few rows (speculative verify): the placement, then the one-row step's prepared input.
