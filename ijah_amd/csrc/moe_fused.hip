@@ -221,9 +221,11 @@ __device__ __forceinline__ void sort_desc(uint32_t (&k)[J]) {
 // carries this launch's tag (bounded), then top-k by logit with ties to the lower index, weights exp(l - l_max) / sum
 // over the top k in f32 summed in slot order, and the shared gate. Each lane sorts its J keys once; a round takes the
 // wave max of the lanes' heads and the winning lane shifts its list. A NaN logit ranks as -inf (weight 0).
-// Workgroup 0 also writes the route to the route / shared-gate buffers for the host.
+// Only the ids are published here (every wave's requests need them); the weights and the shared gate, which only the
+// combine reads, follow in route_weights from mykey (lane t < topk: the t-th largest key) and sgl (the shared gate's
+// logit), after the control wave has issued its own requests.
 template <int J>
-__device__ bool route_wave(const MoeArgs &a, Route *rt, uint32_t tag16) {
+__device__ bool route_wave(const MoeArgs &a, Route *rt, uint32_t tag16, uint32_t &mykey_out, float &sgl_out) {
   const int lane = threadIdx.x & 63, n = a.ne + a.has_sgate;
   const uint32_t *lg = (const uint32_t *)a.logits + (blockIdx.x % kLogitReplicas) * moe_logit_stride(a.ne);
   uint32_t v[J + 1];
@@ -275,7 +277,17 @@ __device__ bool route_wave(const MoeArgs &a, Route *rt, uint32_t tag16) {
     key[J - 1] = win ? 0u : key[J - 1];
   }
   const uint32_t id = 0xFFFFu - (mykey & 0xFFFFu);
+  if (lane < a.topk) rt->id[lane] = id;
+  mykey_out = mykey;
+  sgl_out = sgl;
   stamp_r(a, 2);
+  return true;
+}
+// the route's weights and shared gate (see route_wave); workgroup 0 also writes the route to the route / shared-gate
+// buffers for the host
+__device__ void route_weights(const MoeArgs &a, Route *rt, uint32_t mykey, float sgl) {
+  const int lane = threadIdx.x & 63;
+  const uint32_t id = 0xFFFFu - (mykey & 0xFFFFu);
   const float top = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(key_value(mykey)), 0));
   const float pk = lane < a.topk ? expf(key_value(mykey) - top) : 0.f;
   float sum = 0.f;
@@ -283,7 +295,6 @@ __device__ bool route_wave(const MoeArgs &a, Route *rt, uint32_t tag16) {
   const float wk = pk / sum;
   const float sg = moe_shared_gate(a, sgl);
   if (lane < a.topk) {
-    rt->id[lane] = id;
     rt->w[lane] = wk;
     if (blockIdx.x == 0) {
       st_cg(a.route + lane, id);
@@ -295,7 +306,6 @@ __device__ bool route_wave(const MoeArgs &a, Route *rt, uint32_t tag16) {
     if (blockIdx.x == 0) st_cg(a.sgv, sg);
   }
   stamp_r(a, 3);
-  return true;
 }
 
 // ---------------------------------------------------------------------------------------------------- tiles
@@ -548,8 +558,10 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
   f16x8 dw[kDnKt];
 
   // ---- 1. route (control wave), shared to every wave through LDS
+  uint32_t rkey = 0u;  // the control wave: its lane's route key and the shared gate's logit, for route_weights
+  float rsgl = 0.f;
   if (wave == kCtl) {
-    const bool ok = a.ne <= 512 ? route_wave<8>(a, &rt, tag16) : route_wave<16>(a, &rt, tag16);
+    const bool ok = a.ne <= 512 ? route_wave<8>(a, &rt, tag16, rkey, rsgl) : route_wave<16>(a, &rt, tag16, rkey, rsgl);
     if (!ok && lane == 0) s_ok = 0;
     __builtin_amdgcn_s_setprio(0);  // from here on a wave like the others (it takes routed units)
     stamp(a, 2);
@@ -647,6 +659,8 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
       }
     }
   }
+  // the route's weights, which only the combine reads (past later barriers), once this wave's requests are out
+  if (ok && wave == kCtl) route_weights(a, &rt, rkey, rsgl);
   stamp(a, 3);
   // the shared expert while the routed tiles are on their way (its requests went out before the route): its prep
   // chunks, its k chunks and its down unit's B operands; then the routed prep (suh chunk -> fp16(H(x suh)) in kp
