@@ -338,6 +338,11 @@ NE_API int ne_buf_flush(ne_buf *b) {
 NE_API int ne_sync(void) {
   return c_call([&] { IJ_HIP(hipStreamSynchronize(stream())); });
 }
+NE_API void *ne_stream(void) {
+  void *s = nullptr;
+  c_call([&] { s = (void *)stream(); });
+  return s;
+}
 
 NE_API ne_pack *ne_pack_open(const char *dir) {
   ne_pack *p = nullptr;

@@ -101,7 +101,7 @@ SIGNATURES = {
     "ne_kernel_exists": (_i, [_s]),
     "ne_run_kernel": (_i, [_s, C.POINTER(FConst), _i, C.POINTER(ArgC), _i, _U3, _U3, C.c_uint32, _i, _s, _dp]),
     # include/ijah_exl3.h
-    "ne_buf_flush": (_i, [_vp]), "ne_sync": (_i, []),
+    "ne_buf_flush": (_i, [_vp]), "ne_sync": (_i, []), "ne_stream": (_vp, []),
     "ne_pack_align": (_i, [_s, _s, _u64, _i, _vp]),
     "ne_exl3_lin_load": (_vp, [_vp, _s]), "ne_exl3_lin_create": (_vp, [_vp, _vp, _vp, _i, _i, _i]),
     "ne_exl3_lin_free": (None, [_vp]), "ne_exl3_lin_info": (_i, [_vp, _ip, _ip, _ip]),

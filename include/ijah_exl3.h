@@ -22,6 +22,11 @@ extern "C" {
 NE_API int ne_buf_flush(ne_buf *b);
 /* Waits for all queued GPU work of the library (the reference's Recorder::wait, core/recorder.h:76). */
 NE_API int ne_sync(void);
+/* The library's HIP stream (a hipStream_t; NULL with ne_last_error set if no device), so that a caller can capture
+ * library calls into its own HIP graph (hipStreamBeginCapture on it, the calls, hipStreamEndCapture) or order its own
+ * work against them. Calls that allocate refuse to grow scratch during a capture; ne_exl3_lin_run_noalloc allocates
+ * nothing. No reference counterpart: the reference records into its own command buffers (core/recorder.h). */
+NE_API void *ne_stream(void);
 
 /* ---- pack alignment ----
  * reference core/pack_align.h:1-25 (ne::align_pack, the engine-cli `align-pack` command): writes into dst_dir a copy of
