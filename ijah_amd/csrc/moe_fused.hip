@@ -958,6 +958,22 @@ MoePlan moe_fused_plan(int hid, int inter, int topk, int nslot, int G, bool q8, 
   auto key_of = [&](long t) { return (uint32_t)((t / (4L * NKG * NG)) * NKG + (t / 4) % NKG); };  // matrix, k group
   std::vector<int> hb_first((size_t)nslot * NBI, -1);
   int used = 0;  // LDS slots the busiest workgroup needs
+  // the combining workgroups (output block c on workgroup c G / NBLK, spread over the XCDs) take no routed down
+  // unit: the combine waits for the last down partial, so they poll from early on instead of storing some of the last
+  std::vector<char> comb_wg(G, 0);
+  if (G >= 2 * NBLK)
+    for (int c = 0; c < NBLK; c++) comb_wg[(size_t)c * G / NBLK] = 1;
+  std::vector<long> ur0(G + 1, 0);  // routed down units [ur0[b], ur0[b + 1]) of workgroup b
+  {
+    long nw = 0;
+    for (int b = 0; b < G; b++) nw += comb_wg[b] ? 0 : 1;
+    long k = 0;
+    for (int b = 0; b < G; b++) {
+      ur0[b] = UR * k / nw;
+      k += comb_wg[b] ? 0 : 1;
+    }
+    ur0[G] = UR;
+  }
   for (int b = 0; b < G; b++) {
     uint32_t *pw = &w[(size_t)b * kPW];
     const long t0 = TR * b / G, t1 = TR * (b + 1) / G, s0 = TS * b / G, s1 = TS * (b + 1) / G;
@@ -1028,7 +1044,7 @@ MoePlan moe_fused_plan(int hid, int inter, int topk, int nslot, int G, bool q8, 
     // down units (global unit index: the shared slot's first)
     std::vector<long> units;
     for (long u = US * b / G; u < US * (b + 1) / G; u++) units.push_back(u);
-    for (long u = UR * b / G; u < UR * (b + 1) / G; u++) units.push_back(US + u);
+    for (long u = ur0[b]; u < ur0[b + 1]; u++) units.push_back(US + u);
     std::vector<uint32_t> hbs;
     for (size_t i = 0; i < units.size(); i++) {
       const long u = units[i];
@@ -1049,7 +1065,6 @@ MoePlan moe_fused_plan(int hid, int inter, int topk, int nslot, int G, bool q8, 
       pw[P_HB + i] = v;
     }
   }
-  // combine: output block c on workgroup c G / NBLK (spread over the XCDs)
   for (int c = 0; c < NBLK; c++) w[(size_t)(c * G / NBLK) * kPW + P_COMB] = (uint32_t)c;
   pl.words = w;
   // tagged partials (u64 = 2 floats): gate/up [column][NKG k groups][32], down [slot][cb][hid]
