@@ -958,11 +958,15 @@ MoePlan moe_fused_plan(int hid, int inter, int topk, int nslot, int G, bool q8, 
   auto key_of = [&](long t) { return (uint32_t)((t / (4L * NKG * NG)) * NKG + (t / 4) % NKG); };  // matrix, k group
   std::vector<int> hb_first((size_t)nslot * NBI, -1);
   int used = 0;  // LDS slots the busiest workgroup needs
-  // the combining workgroups (output block c on workgroup c G / NBLK, spread over the XCDs) take no routed down
-  // unit: the combine waits for the last down partial, so they poll from early on instead of storing some of the last
+  // output block c combines on workgroup c G / NBLK + c % 8: spread over the grid and, as workgroups go to the 8
+  // XCDs in turn, over the XCDs (c G / NBLK alone is a multiple of 8 at G = 256, NBLK = 16: all on one XCD, whose
+  // link then carries every combine's polls)
+  auto comb_b = [&](int c) { return c * G / NBLK + (G >= 8 * NBLK ? c % 8 : 0); };
+  // the combining workgroups take no routed down unit: the combine waits for the last down partial, so they poll
+  // from early on instead of storing some of the last
   std::vector<char> comb_wg(G, 0);
   if (G >= 2 * NBLK)
-    for (int c = 0; c < NBLK; c++) comb_wg[(size_t)c * G / NBLK] = 1;
+    for (int c = 0; c < NBLK; c++) comb_wg[comb_b(c)] = 1;
   std::vector<long> ur0(G + 1, 0);  // routed down units [ur0[b], ur0[b + 1]) of workgroup b
   {
     long nw = 0;
@@ -1065,7 +1069,7 @@ MoePlan moe_fused_plan(int hid, int inter, int topk, int nslot, int G, bool q8, 
       pw[P_HB + i] = v;
     }
   }
-  for (int c = 0; c < NBLK; c++) w[(size_t)(c * G / NBLK) * kPW + P_COMB] = (uint32_t)c;
+  for (int c = 0; c < NBLK; c++) w[(size_t)comb_b(c) * kPW + P_COMB] = (uint32_t)c;
   pl.words = w;
   // tagged partials (u64 = 2 floats): gate/up [column][NKG k groups][32], down [slot][cb][hid]
   // and, with the 8-bit shared expert, its gate / up [2 inter] and down [hid] rows
