@@ -454,6 +454,10 @@ def run_moe_trace(eng, layers, seed):
     rows.sort()
     for _, name, p0, p50, p100, n in rows:
         print(f"{name:26s} {p0:7.2f} {p50:7.2f} {p100:7.2f}  waves={n}", flush=True)
+    xcc = t[:, 0, 31].astype(np.int64)  # the XCD each workgroup ran on
+    same = int(np.sum(xcc == np.arange(len(xcc)) % 8))
+    print(f"workgroups on XCD (workgroup % 8): {same} of {len(xcc)}; XCD of workgroups 0-15: {xcc[:16].tolist()}; "
+          f"XCDs of each class workgroup % 8: {[sorted(set(xcc[r::8].tolist())) for r in range(8)]}", flush=True)
     # where the skew sits: per workgroup the latest wave's stamp, by XCD (workgroup % 8) and the slowest workgroups
     for f in (2, 13, 8, 9, 5, 6):
         v = np.where(t[:, :, f] > 0, (t[:, :, f] - base) / 100.0, np.nan)

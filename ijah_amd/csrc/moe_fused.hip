@@ -87,7 +87,8 @@ __device__ __forceinline__ uint32_t rfl(uint32_t v) { return __builtin_amdgcn_re
 
 // Trace mode (a.trace set; a measurement aid): per-wave wall-clock stamps kept in LDS, so that they add nothing to the
 // wave's vector-memory counter (which the hand-counted waits rely on), and written out at the end of the launch:
-// trace[(workgroup * 16 + wave) * 32 + field]; fields 0-7 the phases, 8-15 and 16-23 finer steps, 24-27 the route's.
+// trace[(workgroup * 16 + wave) * 32 + field]; fields 0-7 the phases, 8-15 and 16-23 finer steps, 24-27 the route's,
+// 31 the XCD the workgroup ran on.
 constexpr int kTraceFields = 32;
 __device__ __forceinline__ uint64_t *trace_lds() {
   __shared__ uint64_t t[kWaves * kTraceFields];
@@ -497,6 +498,11 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
   int nops = 0;  // tile / vector requests (loads) this wave has issued: waits count the ones issued after
   if (a.trace && lane < kTraceFields) trace_lds()[wave * kTraceFields + lane] = 0;
   stamp(a, 0);
+  if (a.trace && (threadIdx.x & 63) == 0) {  // field 31: the XCD this workgroup runs on
+    uint32_t xcc;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    trace_lds()[(threadIdx.x >> 6) * kTraceFields + 31] = xcc & 0xFu;
+  }
 
   // the router logits, then the shared expert's units and its suh chunks once this workgroup's logits are out
   if (threadIdx.x == 0) s_ok = 1;
