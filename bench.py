@@ -106,6 +106,11 @@ def measure_m1(eng, hid, inter, shared, n_layers, steps, seed, k=K):
     out = {"hidden": hid, "intermediate": inter, "shared": "8-bit affine g128" if shared == "q8" else f"EXL3 K{k}",
            "fused": "fused" in kus, "us_per_layer": round(us, 2), "bytes_per_layer": int(byts),
            "GBps": round(gbs, 1), "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2)}
+    if (hid, inter, shared) == (2560, 640, "q8"):
+        # the reference's own layer form at M=1 on its hardware (Apple M5 Max): router + shared gate/up + top-10
+        # 14.1 us, gate/up 45.4 us, down + combine 31.8 us (27.5-29.4 after its load hoist) in context
+        # (docs/kernels.md:136-142, 167); another machine, quoted beside this one, not a vs_baseline
+        out["reference_m5max_us"] = [87.0, 91.3]
     print(f"m1 {hid}x{inter} shared={shared}: {out}", file=sys.stderr, flush=True)
     return out
 
