@@ -12,6 +12,8 @@
  *   and only the changed bytes, so the reference's write-then-run pattern works; ne_buf_flush() (ijah_exl3.h)
  *   writes the whole mirror at once. A caller that reads results must call ne_buf_contents() again after the run
  *   (the GPU's writes do not reach an existing mirror), and must not change bytes the GPU is still writing.
+ *   Exception: a call made while the library's stream is being captured into a graph pushes nothing (a copy would
+ *   be recorded into the graph): call ne_buf_flush() before the capture.
  * - Pack tensors are uploaded to HBM on first use; their ne_buf handles belong to the pack (do not ne_free them).
  */
 #ifndef NATIVE_ENGINE_H
