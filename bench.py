@@ -404,8 +404,8 @@ def run_probes(eng, iters=4000):
 
 def measure_hc_read(eng, R, steps, seed, hid=2560, lr=320, K=6, copies=96):
     """The hyper-connection read (ne_hc_read: prep, down linear + silu epilogue, up linear + output epilogue) at R rows on
-    synthetic EXL3 mixes of the reference shape. GPU time per call from HIP events around its three launches (median
-    over calls). The mixes are 4.9 MB: each call reads its own device copy of them, out of `copies` (96 copies = 470
+    synthetic EXL3 mixes of the reference shape. GPU time per call from HIP events around its launches (median over
+    calls). The mixes are 4.9 MB: each call reads its own device copy of them, out of `copies` (96 copies = 470
     MB, beyond the 256 MB last-level cache), so the weights come from HBM as in a model's layer chain."""
     from ijah_amd import synth
     from ijah_amd.engine import hc_read
@@ -420,7 +420,11 @@ def measure_hc_read(eng, R, steps, seed, hid=2560, lr=320, K=6, copies=96):
         hc_read(*m, R, h, nw, iw, mix, inj, out)
     ms = [hc_read(*mixes[i % copies], R, h, nw, iw, mix, inj, out, timed=True) for i in range(max(10, min(steps, copies)))]
     res = {"rows": R, "hid": hid, "mix_rows": lr, "K": K, "us": round(1e3 * float(np.median(ms)), 3),
-           "launches": 4, "weights": f"{copies} distinct copies"}
+           # hc_prep, the down linear, the up linear; and the up linear's input prepared by a launch of its own when
+           # its 320 tile pairs would repeat too much preparation (the library's rule: pairs R > 256 and pairs R in
+           # > 256 * 2048)
+           "launches": 3 + int(4 * hid // 32 * R > 256 and 4 * hid // 32 * R * lr > 256 * 2048),
+           "weights": f"{copies} distinct copies"}
     for ld, lu in mixes:
         ld.free()
         lu.free()

@@ -78,8 +78,10 @@ struct ne_exl3_lin {
   // the input preparation runs inside the GEMM (each tile pair's workgroups prepare their own k chunks) unless that
   // repeats too much work: many tile pairs times many rows take one prep launch instead (same results)
   // the rows prepared once by a launch of their own when many tile pairs would each prepare them again (measured:
-  // 16 rows of q / o 2048->4096 / 4096->2048, 128 pairs, take 15 us so against 16.6 us preparing in each workgroup)
-  bool prep_launch(int R) const { return (long)(OTp / 2) * R > 256; }
+  // 16 rows of q / o 2048->4096 / 4096->2048, 128 pairs, take 15 us so against 16.6 us preparing in each workgroup),
+  // unless the input is short enough that preparing it again in each workgroup costs less than a launch (the HC
+  // read's up linear, 320 -> 10240)
+  bool prep_launch(int R) const { return (long)(OTp / 2) * R > 256 && (long)(OTp / 2) * R * in > 256L * 2048; }
   // many tile pairs (a vocabulary head): one workgroup per pair loops over the k groups (same results)
   bool k_loop(int R) const { return OTp / 2 >= 2048 && groups() <= 16 && R <= 4 && prep_launch(R); }
   // the same linears at 5..32 rows: 8 tile pairs per workgroup share each k chunk's staged rows (same results)
