@@ -468,7 +468,7 @@ def run_moe_trace(eng, layers, seed):
     print(f"workgroups on XCD (workgroup % 8): {same} of {len(xcc)}; XCD of workgroups 0-15: {xcc[:16].tolist()}; "
           f"XCDs of each class workgroup % 8: {[sorted(set(xcc[r::8].tolist())) for r in range(8)]}", flush=True)
     # where the skew sits: per workgroup the latest wave's stamp, by XCD (workgroup % 8) and the slowest workgroups
-    for f in (2, 13, 8, 9, 5, 6):
+    for f in (1, 24, 2, 13, 8, 9, 5, 6):
         v = np.where(t[:, :, f] > 0, (t[:, :, f] - base) / 100.0, np.nan)
         wg = np.nanmax(v, axis=1)
         by_xcd = [round(float(np.nanmedian(wg[x::8])), 2) for x in range(8)]
