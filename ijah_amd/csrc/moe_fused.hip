@@ -970,8 +970,10 @@ MoePlan moe_fused_plan(int hid, int inter, int topk, int nslot, int G, bool q8, 
   auto comb_b = [&](int c) { return c * G / NBLK + (G >= 8 * NBLK ? c % 8 : 0); };
   // the combining workgroups take no routed down unit: the combine waits for the last down partial, so they poll
   // from early on instead of storing some of the last
+  // (only while that leaves every other wave at most one down unit: a second one is decoded after the first one's
+  // product is stored, on the step's tail)
   std::vector<char> comb_wg(G, 0);
-  if (G >= 2 * NBLK)
+  if (G >= 2 * NBLK && UR + US <= (long)(G - NBLK) * kWaves)
     for (int c = 0; c < NBLK; c++) comb_wg[comb_b(c)] = 1;
   std::vector<long> ur0(G + 1, 0);  // routed down units [ur0[b], ur0[b + 1]) of workgroup b
   {
