@@ -580,8 +580,9 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
 
   // ---- 2. requests, in the order they are consumed. A CU returns its waves' requests roughly in issue order, and a
   // wave issues all its requests before the next wave of its SIMD does: so every wave first requests the routed prep
-  // chunks' suh and its routed gate/up tasks' tiles, and only after a workgroup barrier its later needs (its routed
-  // down unit, small vectors), which would otherwise hold back the other waves' gate/up tiles.
+  // chunks' suh and its routed gate/up tasks' tiles, and only after a workgroup barrier its small vectors. Its
+  // routed down units' tiles go out once its gate/up chunks are done, so the gate/up tiles every h block waits for
+  // do not share the HBM queues with them.
   int end_u[kUnitsPerWave];  // per unit: requests issued up to and including its own
 #pragma unroll
   for (int k = 0; k < kUnitsPerWave; k++) end_u[k] = 0;
@@ -614,10 +615,10 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
   stamp_w(a, 5);
   lds_barrier();
   stamp_w(a, 6);
-  // this wave's down units (at most kMaxDn, in plan order: a shared one comes first): the first one's tiles are
-  // requested now and decoded before its h block is ready; a unit whose tiles reuse a gate/up chunk's LDS slot
-  // (shapes whose units outnumber the slots) is requested once the wave's chunks are done; a second unit is decoded
-  // after the first one's product is stored
+  // this wave's down units (at most kMaxDn, in plan order: a shared one comes first, its tiles requested at launch):
+  // the routed ones' tiles are requested once the wave's gate/up chunks are done (into their own LDS slots, or, for
+  // shapes whose units outnumber the slots, those of finished chunks); the first one is decoded before its h block
+  // is ready, a second one after the first one's product is stored
   DnUnit D0, D1;
 #pragma unroll
   for (int k = 0; k < kUnitsPerWave; k++)
@@ -639,8 +640,6 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
     D.end = nops;
   };
   if (ok) {
-    if (D0.unit >= 0 && !D0.shared && !D0.reuse) issue_dn(D0);
-    if (D1.unit >= 0 && !D1.reuse) issue_dn(D1);
     // small vectors the later phases read, into LDS: the h prologue's svh_g, svh_u, suh_d of block `wave`; the
     // combine's svh_d of slot ls = wave (mod 16)
     if (wave < nh) {
@@ -758,9 +757,9 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
   __builtin_amdgcn_s_setprio(0);
   stamp_w(a, 1);
   stamp(a, 4);
-  if (ok) {  // down tiles into the slots of gate/up chunks this wave has finished
-    if (D0.unit >= 0 && D0.reuse) issue_dn(D0);
-    if (D1.unit >= 0 && D1.reuse) issue_dn(D1);
+  if (ok) {  // the routed down units' tiles (into their own slots, or those of gate/up chunks this wave has finished)
+    if (D0.unit >= 0 && !D0.shared) issue_dn(D0);
+    if (D1.unit >= 0) issue_dn(D1);
   }
 
   // ---- 4. the first routed down unit's tiles into B operands; the h blocks from the gate/up partials (the NKG k
