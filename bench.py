@@ -435,7 +435,7 @@ def measure_hc_read(eng, R, steps, seed, hid=2560, lr=320, K=6, copies=96):
 TRACE_FIELDS = {0: "start", 1: "pre-route work done", 2: "route known", 3: "requests issued", 4: "gate/up chunks done",
                 5: "h blocks loaded", 6: "down partials stored", 7: "end", 8: "first routed tile in",
                 9: "last gate/up chunk done", 10: "down tiles decoded", 11: "prep suh requested", 12: "barrier 1",
-                13: "gate/up tiles requested", 14: "barrier 2", 15: "shared prep done", 16: "routed prep start",
+                13: "gate/up tiles requested", 15: "shared prep done", 16: "routed prep start",
                 18: "routed suh in", 24: "route: keys", 25: "route: sorted", 26: "route: top-k rounds",
                 27: "route: softmax"}
 

@@ -580,9 +580,9 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
 
   // ---- 2. requests, in the order they are consumed. A CU returns its waves' requests roughly in issue order, and a
   // wave issues all its requests before the next wave of its SIMD does: so every wave first requests the routed prep
-  // chunks' suh and its routed gate/up tasks' tiles, and only after a workgroup barrier its small vectors. Its
-  // routed down units' tiles go out once its gate/up chunks are done, so the gate/up tiles every h block waits for
-  // do not share the HBM queues with them.
+  // chunks' suh (a workgroup barrier: every wave's, ahead of any tile stream), then its routed gate/up tasks' tiles
+  // and its small vectors. Its routed down units' tiles go out once its gate/up chunks are done, so the gate/up tiles
+  // every h block waits for do not share the HBM queues with them.
   int end_u[kUnitsPerWave];  // per unit: requests issued up to and including its own
 #pragma unroll
   for (int k = 0; k < kUnitsPerWave; k++) end_u[k] = 0;
@@ -613,8 +613,6 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
     }
   }
   stamp_w(a, 5);
-  lds_barrier();
-  stamp_w(a, 6);
   // this wave's down units (at most kMaxDn, in plan order: a shared one comes first, its tiles requested at launch):
   // the routed ones' tiles are requested once the wave's gate/up chunks are done (into their own LDS slots, or, for
   // shapes whose units outnumber the slots, those of finished chunks); the first one is decoded before its h block
