@@ -580,9 +580,9 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
 
   // ---- 2. requests, in the order they are consumed. A CU returns its waves' requests roughly in issue order, and a
   // wave issues all its requests before the next wave of its SIMD does: so every wave first requests the routed prep
-  // chunks' suh (a workgroup barrier: every wave's, ahead of any tile stream), then its routed gate/up tasks' tiles
-  // and its small vectors. Its routed down units' tiles go out once its gate/up chunks are done, so the gate/up tiles
-  // every h block waits for do not share the HBM queues with them.
+  // chunks' suh (a workgroup barrier: every wave's, ahead of any tile stream), then its routed gate/up tasks' tiles.
+  // Its routed down units' tiles and the small vectors of the later phases go out once its gate/up chunks are done,
+  // so the gate/up tiles every h block waits for do not share the HBM queues with them.
   int end_u[kUnitsPerWave];  // per unit: requests issued up to and including its own
 #pragma unroll
   for (int k = 0; k < kUnitsPerWave; k++) end_u[k] = 0;
@@ -637,31 +637,6 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
                          32u * K, tiles + D.slot * SLOT);
     D.end = nops;
   };
-  if (ok) {
-    // small vectors the later phases read, into LDS: the h prologue's svh_g, svh_u, suh_d of block `wave`; the
-    // combine's svh_d of slot ls = wave (mod 16)
-    if (wave < nh) {
-      const uint32_t hb = PL(P_HB + wave) & 0x7FFFFFFFu;
-      const int ls = (int)(hb / NBI), cb = (int)(hb % NBI);
-      const uint8_t *blk = slot_block(a, rt, ls);
-      const uint64_t offs[3] = {sv_off(a, ls, 0), sv_off(a, ls, 1), su_off(a, ls, 2)};
-#pragma unroll
-      for (int v = 0; v < 3; v++)
-        if (lane < 16)
-          __builtin_amdgcn_global_load_lds((const void *)(blk + offs[v] + cb * 256 + lane * 16),
-                                           (__attribute__((address_space(3))) void *)(hvec[wave][v]), 16, 0, 0);
-      nops += 3;
-    }
-    if (comb != kNone) {
-      for (int ls = wave; ls < a.nslot; ls += kWaves) {
-        if (lane < 16)
-          __builtin_amdgcn_global_load_lds(
-              (const void *)(slot_block(a, rt, ls) + sv_off(a, ls, 2) + comb * 256 + lane * 16),
-              (__attribute__((address_space(3))) void *)(csv[ls]), 16, 0, 0);
-        nops++;
-      }
-    }
-  }
   // the route's weights, which only the combine reads (past later barriers), once this wave's requests are out
   if (ok && wave == kCtl) route_weights(a, &rt, rkey, rsgl);
   stamp(a, 3);
@@ -758,6 +733,31 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
   if (ok) {  // the routed down units' tiles (into their own slots, or those of gate/up chunks this wave has finished)
     if (D0.unit >= 0 && !D0.shared) issue_dn(D0);
     if (D1.unit >= 0) issue_dn(D1);
+  }
+  if (ok) {
+    // (after the gate/up chunks, as the down tiles) small vectors the later phases read, into LDS: the h prologue's svh_g, svh_u, suh_d of block `wave`; the
+    // combine's svh_d of slot ls = wave (mod 16)
+    if (wave < nh) {
+      const uint32_t hb = PL(P_HB + wave) & 0x7FFFFFFFu;
+      const int ls = (int)(hb / NBI), cb = (int)(hb % NBI);
+      const uint8_t *blk = slot_block(a, rt, ls);
+      const uint64_t offs[3] = {sv_off(a, ls, 0), sv_off(a, ls, 1), su_off(a, ls, 2)};
+#pragma unroll
+      for (int v = 0; v < 3; v++)
+        if (lane < 16)
+          __builtin_amdgcn_global_load_lds((const void *)(blk + offs[v] + cb * 256 + lane * 16),
+                                           (__attribute__((address_space(3))) void *)(hvec[wave][v]), 16, 0, 0);
+      nops += 3;
+    }
+    if (comb != kNone) {
+      for (int ls = wave; ls < a.nslot; ls += kWaves) {
+        if (lane < 16)
+          __builtin_amdgcn_global_load_lds(
+              (const void *)(slot_block(a, rt, ls) + sv_off(a, ls, 2) + comb * 256 + lane * 16),
+              (__attribute__((address_space(3))) void *)(csv[ls]), 16, 0, 0);
+        nops++;
+      }
+    }
   }
 
   // ---- 4. the first routed down unit's tiles into B operands; the h blocks from the gate/up partials (the NKG k
