@@ -8,7 +8,7 @@
 //
 // Wave64 mapping (this build's own): lane m of a wave owns slots 4m .. 4m+3 of a tile, i.e. rows 2q, 2q+1, 2q+8,
 // 2q+9 (q = (m >> 1) & 3) of column (m >> 3) + 8 (m & 1). Its four codewords span 15 + 3K ring bits starting at
-// (4m + 1) K - 15: one funnel shift (v_alignbit) of two words for K <= 5, two funnels of three words above. The input
+// (4m + 1) K - 15: funnel shifts (v_alignbit) of two words, except at K 7 (three words). The input
 // is staged in LDS as fp16 in the reference's k-permuted order (kp), so a lane's four rows are one 8-byte read, and the
 // four weights meet it in two v_dot2_f32_f16. Lanes sharing a column differ in lane bits 1-2: two xor-shuffles reduce.
 //
@@ -116,11 +116,13 @@ struct TileLane {
 // Lane m's window starts at ring bit S = (4m + 1) K - 15 (mod 256 K). Taking i0 = floor((S - 1) / 32) puts the
 // window's first bit at a' = S - 32 i0 in [1, 32] of words (i0, i0+1), so v_alignbit(w0, w1, 32 - a') yields the
 // window's first 32 bits with no special case for a' = 32.
+__host__ __device__ constexpr uint32_t group_sm1(int K, uint32_t m) {
+  return ((4u * m + 1u) * K + 256u * K - 16u) % (256u * K);  // S - 1
+}
 template <int K>
 __device__ __forceinline__ TileLane<K> tile_lane(uint32_t m) {
-  constexpr uint32_t NW = 8u * K, TOT = 256u * K;
-  const uint32_t S = ((4u * m + 1u) * K + TOT - 15u) % TOT;
-  const uint32_t Sm1 = (S + TOT - 1u) % TOT;
+  constexpr uint32_t NW = 8u * K;
+  const uint32_t Sm1 = group_sm1(K, m);
   TileLane<K> t;
   t.i0 = Sm1 >> 5;
   t.i1 = (t.i0 + 1u) % NW;
@@ -128,8 +130,25 @@ __device__ __forceinline__ TileLane<K> tile_lane(uint32_t m) {
   t.sh = 31u - (Sm1 & 31u);
   return t;
 }
+// A group's codewords span 15 + 3K bits from bit a' = 32 - sh of words (i0, i1, ...). For K 6 and 8 every group
+// start puts a' <= 49 - 3K (sh >= 3K - 17), so the window ends inside word i1 and no third word is read; only K 7
+// needs one.
 template <int K>
-constexpr bool kThreeWords = (15 + 3 * K > 32);
+constexpr bool two_word_windows() {
+  for (uint32_t m = 0; m < 64; m++)
+    if ((int)(31u - (group_sm1(K, m) & 31u)) < 3 * K - 17) return false;
+  return true;
+}
+template <int K>
+constexpr bool kThreeWords = (15 + 3 * K > 32) && !two_word_windows<K>();
+// sh when it is the same for every group (K 8: 7), else -1
+template <int K>
+constexpr int const_sh() {
+  const uint32_t s = 31u - (group_sm1(K, 0) & 31u);
+  for (uint32_t m = 1; m < 64; m++)
+    if (31u - (group_sm1(K, m) & 31u) != s) return -1;
+  return (int)s;
+}
 
 struct TileWords {
   uint32_t w0, w1, w2;
@@ -191,14 +210,19 @@ __device__ __forceinline__ f16x2 mcg_pair(uint32_t c0, uint32_t c1) {
   return __builtin_bit_cast(f16x2, d);
 }
 
-// The lane's four weights: a = rows (2q, 2q+1), b = rows (2q+8, 2q+9) of its column.
+// The group's four codewords (15 bits each, at window bits K i .. K i + 14) from its words and shift.
 template <int K>
-__device__ __forceinline__ void decode4(const TileWords &w, uint32_t sh, f16x2 &a, f16x2 &b) {
-  uint32_t c[4];
-  const uint32_t hi = __builtin_amdgcn_alignbit(w.w0, w.w1, sh);
+__device__ __forceinline__ void codewords4(const TileWords &w, uint32_t sh, uint32_t (&c)[4]) {
+  const uint32_t hi = __builtin_amdgcn_alignbit(w.w0, w.w1, sh);  // window bits 0 .. 31
   if constexpr (!kThreeWords<K>) {
 #pragma unroll
-    for (int i = 0; i < 4; i++) c[i] = (hi >> (17 - i * K)) & 0x7FFFu;
+    for (int i = 0; i < 4; i++) {
+      const int r = 17 - i * K;  // codeword i's lowest bit in hi; below 0: it ends -r bits past hi, still in w1
+      if (r >= 0)
+        c[i] = (hi >> r) & 0x7FFFu;
+      else
+        c[i] = (const_sh<K>() == -r ? w.w1 : __builtin_amdgcn_alignbit(w.w0, w.w1, sh - (uint32_t)(-r))) & 0x7FFFu;
+    }
   } else {
     const uint32_t lo = __builtin_amdgcn_alignbit(w.w1, w.w2, sh);
 #pragma unroll
@@ -207,6 +231,12 @@ __device__ __forceinline__ void decode4(const TileWords &w, uint32_t sh, f16x2 &
       c[i] = (s >= 32 ? (hi >> (s - 32)) : __builtin_amdgcn_alignbit(hi, lo, (uint32_t)s)) & 0x7FFFu;
     }
   }
+}
+// The lane's four weights: a = rows (2q, 2q+1), b = rows (2q+8, 2q+9) of its column.
+template <int K>
+__device__ __forceinline__ void decode4(const TileWords &w, uint32_t sh, f16x2 &a, f16x2 &b) {
+  uint32_t c[4];
+  codewords4<K>(w, sh, c);
   a = mcg_pair(c[0], c[1]);
   b = mcg_pair(c[2], c[3]);
 }

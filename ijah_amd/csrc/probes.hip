@@ -140,19 +140,10 @@ __device__ __forceinline__ f16x8 decode_pair_lut(const uint8_t *tl, int kt, cons
   f16x8 r;
 #pragma unroll
   for (int g = 0; g < 2; g++) {
-    const uint32_t hi = __builtin_amdgcn_alignbit(w[g].w0, w[g].w1, sh[g]);
-    const uint32_t lo = kThreeWords<K> ? __builtin_amdgcn_alignbit(w[g].w1, w[g].w2, sh[g]) : 0u;
+    uint32_t c[4];
+    codewords4<K>(w[g], sh[g], c);
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      uint32_t c;
-      if constexpr (!kThreeWords<K>) {
-        c = (hi >> (17 - i * K)) & 0x7FFFu;
-      } else {
-        const int s = 49 - i * K;
-        c = (s >= 32 ? (hi >> (s - 32)) : __builtin_amdgcn_alignbit(hi, lo, (uint32_t)s)) & 0x7FFFu;
-      }
-      r[4 * g + i] = lut[c];
-    }
+    for (int i = 0; i < 4; i++) r[4 * g + i] = lut[c[i]];
   }
   return r;
 }
