@@ -149,6 +149,8 @@ constexpr int const_sh() {
     if (31u - (group_sm1(K, m) & 31u) != s) return -1;
   return (int)s;
 }
+template <int K>
+constexpr int kConstSh = const_sh<K>();
 
 struct TileWords {
   uint32_t w0, w1, w2;
@@ -221,7 +223,7 @@ __device__ __forceinline__ void codewords4(const TileWords &w, uint32_t sh, uint
       if (r >= 0)
         c[i] = (hi >> r) & 0x7FFFu;
       else
-        c[i] = (const_sh<K>() == -r ? w.w1 : __builtin_amdgcn_alignbit(w.w0, w.w1, sh - (uint32_t)(-r))) & 0x7FFFu;
+        c[i] = (kConstSh<K> == -r ? w.w1 : __builtin_amdgcn_alignbit(w.w0, w.w1, sh - (uint32_t)(-r))) & 0x7FFFu;
     }
   } else {
     const uint32_t lo = __builtin_amdgcn_alignbit(w.w1, w.w2, sh);
