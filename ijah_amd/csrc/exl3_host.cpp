@@ -417,8 +417,19 @@ NE_API int ne_hc_read(ne_exl3_lin *down, ne_exl3_lin *up, int R, const ne_buf *h
     fin.ctr = ctr;
     timed(stream(), gpu_ms, [&] {
       hipStream_t s = stream();
-      launch_hc_prep(hp, nw, (const uint16_t *)ne_dev(inject), xn, ip, injp, R, hid, s);
-      lin_launch(down, R, xn, (float *)ne_dev(mix), s, act);
+      // one row: hc_prep's step runs inside the down linear's workgroups (one launch fewer, the same bits)
+      LinArgs da = lin_args(down, R, hp, (float *)ne_dev(mix), act);
+      if (R == 1 && !da.xh_in && !da.kloop && da.cnt && hid % 512 == 0 && hid <= 4096) {
+        da.hc.nw = nw;
+        da.hc.iw = (const uint16_t *)ne_dev(inject);
+        da.hc.ip = ip;
+        da.hc.inj = injp;
+        da.hc.hid = hid;
+        launch_lin(da, s);
+      } else {
+        launch_hc_prep(hp, nw, (const uint16_t *)ne_dev(inject), xn, ip, injp, R, hid, s);
+        lin_launch(down, R, xn, (float *)ne_dev(mix), s, act);
+      }
       lin_launch(up, R, (const float *)ne_dev(mix), u, s, fin);
     });
   });

@@ -723,6 +723,35 @@ __global__ __launch_bounds__(256) void lin_mx(LinMulti m) {
         xv1[r] = i1 < a.in ? a.x[(uint64_t)r * a.in + i1] : 0.f;
       }
   }
+  // (HC read, one row) hc_prep's loads, requested with x and suh: the stream's values for its sum of squares (thread
+  // t: columns t + 256 u of stream hs, hc_prep's batch of 16) and the norm weights of the wave's columns; the first
+  // tile pair's workgroups also the norm and inject weights of the group's two 256-column chunks (thread t: column
+  // t of each)
+  constexpr int kHcB = 16;
+  const bool hcin = RT == 1 && a.hc.nw != nullptr;
+  const int hhid = a.hc.hid, hs = hcin ? g * kLinGroupKt * 16 / hhid : 0;
+  float hq[kHcB], nw0 = 0.f, nw1 = 0.f, cx[2] = {0.f, 0.f}, cw[2][4] = {};
+  if constexpr (RT == 1) {
+    if (hcin) {
+      const float *hr = a.x + (uint64_t)hs * hhid;
+#pragma unroll
+      for (int u = 0; u < kHcB; u++) {
+        const int j = 256 * u + (int)threadIdx.x;
+        hq[u] = hr[j < hhid ? j : 0];
+      }
+      nw0 = epi_bf(a.hc.nw[i0]);
+      nw1 = epi_bf(a.hc.nw[i1]);
+      if (p == 0) {
+#pragma unroll
+        for (int q = 0; q < 2; q++) {
+          const int j = g * kLinGroupKt * 16 + q * 256 + (int)threadIdx.x;
+          cx[q] = a.x[j] * epi_bf(a.hc.nw[j]);
+#pragma unroll
+          for (int k = 0; k < 4; k++) cw[q][k] = epi_bf(a.hc.iw[(uint64_t)k * 4 * hhid + j]);
+        }
+      }
+    }
+  }
   int ndma = 0;
   if (nkt > 0) {
     const uint8_t *src = (const uint8_t *)a.tiles + ((uint64_t)p * a.IT + kt0) * 64 * K;
@@ -741,6 +770,38 @@ __global__ __launch_bounds__(256) void lin_mx(LinMulti m) {
     }
   }
   if (!a.xh_in && nkt > 0) wait_vm(ndma);  // x and suh are in (the tiles, requested after them, may not be)
+  if constexpr (RT == 1) {
+    if (hcin) {  // hc_prep's sums (same order: per thread, the wave's xor butterfly, the four waves left to right)
+      __shared__ float hred[4][9];
+      float t[9];
+      t[0] = 0.f;
+#pragma unroll
+      for (int u = 0; u < kHcB; u++)
+        if (256 * u + (int)threadIdx.x < hhid) t[0] += hq[u] * hq[u];
+#pragma unroll
+      for (int q = 0; q < 2; q++)
+#pragma unroll
+        for (int k = 0; k < 4; k++) t[1 + 4 * q + k] = cw[q][k] * cx[q];
+#pragma unroll
+      for (int k = 0; k < 9; k++)
+        for (int o = 32; o >= 1; o >>= 1) t[k] += __shfl_xor(t[k], o, 64);
+      if (lane == 0)
+#pragma unroll
+        for (int k = 0; k < 9; k++) hred[c][k] = t[k];
+      __syncthreads();
+#pragma unroll
+      for (int k = 0; k < 9; k++) t[k] = ((hred[0][k] + hred[1][k]) + hred[2][k]) + hred[3][k];
+      const float inv = 1.f / sqrtf(t[0] / (float)hhid + 1e-6f);
+      xv0[0] = (xv0[0] * nw0) * inv;
+      xv1[0] = (xv1[0] * nw1) * inv;
+      if (p == 0) {  // hc_prep's other outputs for this group's two chunks of stream hs
+        const int nch = (hhid + 255) / 256, ch0 = (g * kLinGroupKt * 16 - hs * hhid) / 256;
+        if (threadIdx.x < 8)
+          a.hc.ip[(hs * nch + ch0 + (int)threadIdx.x / 4) * 4 + threadIdx.x % 4] = t[1 + threadIdx.x] * inv;
+        if (threadIdx.x == 0 && ch0 == 0) a.hc.inj[kHcStreams + hs] = inv;
+      }
+    }
+  }
   f32x16 acc;
 #pragma unroll
   for (int i = 0; i < 16; i++) acc[i] = 0.f;
@@ -973,7 +1034,6 @@ __global__ __launch_bounds__(64) void lin_finish(LinArgs a) {
 // ------------------------------------------------------------------------------------------------ HC read
 // The hyper-connection read's elementwise steps around the down and up linears (reference
 // kernels/trunk6/t6_epi.metal:16-97). Four streams of hid columns per row; rr = bf16 rounding when refr.
-constexpr int kHcStreams = 4;
 
 // workgroup (row r, stream s, 256-column chunk ch), 256 threads (reference t6e_hc_prep, :16-50): every workgroup
 // sums the whole stream's squares (independent loads, hid floats from L2), then prepares its own chunk:
@@ -1229,6 +1289,9 @@ void launch_lin_multi(const LinArgs *l, int n, hipStream_t s) {
     IJ_CHECK(!a.kloop || (a.xh_in && G <= kLinLoopMaxGroups), "linear launch: the k-group loop needs the prep launch");
     IJ_CHECK(a.kloop != 2 || (n == 1 && a.R > 4 && a.R <= kLinMaxRows && a.cnt && a.epi.kind != 8),
              "linear launch: the wide form takes one linear of 5..32 rows with its counters and no HC epilogue");
+    IJ_CHECK(!a.hc.nw || (n == 1 && a.R == 1 && !a.kloop && !a.xh_in && a.cnt && a.hc.iw && a.hc.ip && a.hc.inj &&
+                          a.in == kHcStreams * a.hc.hid && a.hc.hid % 512 == 0 && a.hc.hid <= 4096),
+             "linear launch: the HC read's input step folds into a one-row, one-launch down linear only");
     IJ_CHECK(a.K == l[0].K && a.R == l[0].R && a.R >= 1 && a.R <= kLinMaxRows && (bool)a.cnt == (bool)l[0].cnt &&
                  a.kloop == l[0].kloop,
              "multi-linear launch: K, R and path must agree");

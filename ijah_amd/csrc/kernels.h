@@ -176,6 +176,15 @@ struct LinEpi {
   const uint16_t *w16 = nullptr;
   uint32_t *ctr = nullptr;  // kind 8: [hid / 128] (one-launch finisher), then [R][hid / 128], kSyncStride apart
 };
+// The HC read's input step folded into its down linear at one row (nw null: off). The linear's x is then the streams h
+// [4 hid] and its input x_i (nw_i) inv_s, inv_s = 1 / rms of stream s, summed in hc_prep's order so the bits are
+// hc_prep's; the workgroups of the first tile pair also store hc_prep's inject partials ip and inv_s (inj[4 + s]).
+constexpr int kHcStreams = 4;
+struct LinHcIn {
+  const uint16_t *nw = nullptr, *iw = nullptr;
+  float *ip = nullptr, *inj = nullptr;
+  int hid = 0;
+};
 struct LinArgs {
   const uint32_t *tiles;  // re-laid trellis
   const uint16_t *suh, *svh;
@@ -191,6 +200,7 @@ struct LinArgs {
   int xh_in;              // 1: xh holds this run's prepared rows (a prep launch ran); 0: the GEMM prepares its chunks
   int kloop;              // 1: one workgroup per tile pair loops over the k groups (S = 1: one total per pair)
   LinEpi epi;
+  LinHcIn hc;
 };
 constexpr int kLinMaxRows = 32;
 // The k order of every linear: k chunks of 8 k tiles (one MFMA chain from zero each), folded left in k groups of

@@ -335,6 +335,33 @@ def test_hc_read(eng, oracle, hid, lr, K, R):
     assert np.array_equal(ob.download(np.float32, (R, hid)), hc_read_again(ld, lu, R, hb, nb, ib, eng, lr, hid))
 
 
+@pytest.mark.parametrize("hid,lr,K", [(2560, 320, 6), (512, 64, 5)])
+def test_hc_read_one_row_matches_rows(eng, oracle, hid, lr, K):
+    """At one row the HC read's input step (1/rms, the normed input, the inject partials) runs inside the down
+    linear's workgroups instead of its own launch: each row read alone gives the bits of that row of a 4-row read,
+    which takes the separate step."""
+    print(f"hc read one row vs rows hid {hid} lr {lr} K{K}", flush=True)
+    rng = np.random.default_rng(hid + 7)
+    R = 4
+    h = (rng.standard_normal((R, 4, hid)) * np.array([0.5, 1, 2, 4])[None, :, None]).astype(np.float32)
+    nw = synth.bf16((1 + 0.1 * rng.standard_normal(4 * hid)).astype(np.float32))
+    iw = synth.bf16((rng.standard_normal((4, 4 * hid)) / np.sqrt(4 * hid)).astype(np.float32))
+    ld, lu = eng.exl3_linear(*synth.linear(rng, 4 * hid, lr, K)), eng.exl3_linear(*synth.linear(rng, lr, 4 * hid, K))
+    nb, ib = eng.from_numpy(nw), eng.from_numpy(iw)
+    from ijah_amd.engine import hc_read
+    for refr in (True, False):
+        mb, jb, ob = eng.alloc(R * lr * 4), eng.alloc(R * 32), eng.alloc(R * hid * 4)
+        hc_read(ld, lu, R, eng.from_numpy(h), nb, ib, mb, jb, ob, refr=refr)
+        mix, inj, out = mb.download(np.float32, (R, lr)), jb.download(np.float32, (R, 8)), ob.download(np.float32,
+                                                                                                     (R, hid))
+        for r in range(R):
+            m1, j1, o1 = eng.alloc(lr * 4), eng.alloc(32), eng.alloc(hid * 4)
+            hc_read(ld, lu, 1, eng.from_numpy(np.ascontiguousarray(h[r:r + 1])), nb, ib, m1, j1, o1, refr=refr)
+            assert np.array_equal(m1.download(np.float32, (1, lr))[0], mix[r])
+            assert np.array_equal(j1.download(np.float32, (1, 8))[0], inj[r])
+            assert np.array_equal(o1.download(np.float32, (1, hid))[0], out[r])
+
+
 def act_of_neighbour(got, v, act):
     """got == rr(act(c)) within one bf16 step, for c = rr(v) or a bf16 neighbour of it"""
     b = oracle_bf16(v)
