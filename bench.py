@@ -420,10 +420,11 @@ def measure_hc_read(eng, R, steps, seed, hid=2560, lr=320, K=6, copies=96):
         hc_read(*m, R, h, nw, iw, mix, inj, out)
     ms = [hc_read(*mixes[i % copies], R, h, nw, iw, mix, inj, out, timed=True) for i in range(max(10, min(steps, copies)))]
     res = {"rows": R, "hid": hid, "mix_rows": lr, "K": K, "us": round(1e3 * float(np.median(ms)), 3),
-           # hc_prep, the down linear, the up linear; and the up linear's input prepared by a launch of its own when
-           # its 320 tile pairs would repeat too much preparation (the library's rule: pairs R > 256 and pairs R in
-           # > 256 * 2048)
-           "launches": 3 + int(4 * hid // 32 * R > 256 and 4 * hid // 32 * R * lr > 256 * 2048),
+           # the down linear and the up linear; hc_prep as a launch of its own above one row (at one row the down
+           # linear's workgroups run it); and the up linear's input prepared by a launch of its own when its tile
+           # pairs would repeat too much preparation (the library's rule: pairs R > 256 and pairs R in > 256 * 2048)
+           "launches": 2 + int(R > 1 or hid % 512 != 0 or hid > 4096)
+                       + int(4 * hid // 32 * R > 256 and 4 * hid // 32 * R * lr > 256 * 2048),
            "weights": f"{copies} distinct copies"}
     for ld, lu in mixes:
         ld.free()
