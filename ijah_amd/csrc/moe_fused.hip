@@ -355,15 +355,18 @@ __device__ __forceinline__ void prep_chunk(const float *x, int chunk, _Float16 *
   dst[kp(lane + 64)] = to_f16(v1);
 }
 
-// The 8-bit shared expert before the route (reference kernels/fn_moe.metal:40-46 and :264-290): wave kSpw + i takes
-// gate / up row b + G i (all waves of the grid together: the 2 inter rows) and stores it tagged (part_q8[row]); wave
-// kSpw then waits until all 2 inter are in, computes h = rr(silu(g) u) into LDS and sets s_q8; waves kSpw .. kSpw + 3
-// take the down rows b + G (i + 4 j) and store them tagged (part_q8[2 inter + row]), which the combine reads. The row
+// The 8-bit shared expert (reference kernels/fn_moe.metal:40-46 and :264-290). Before the route is known, wave
+// kSpw + i takes gate / up row b + G i (all waves of the grid together: the 2 inter rows) and stores it tagged
+// (part_q8[row]), and waves kSpw .. kSpw + 3 request their down rows b + G (i + 4 j). Those rows wait in the registers
+// of the shared EXL3 down unit's operands (this form has no such unit) until the wave's gate/up chunks are done: then
+// wave kSpw polls every gate and up value, computes h = rr(silu(g) u) into LDS and sets s_q8, and the four waves store
+// their down rows tagged (part_q8[2 inter + row]), which the combine reads. So no wave holds the workgroup's route
+// barrier, and with it every wave's routed requests, while the grid's gate and up values are on their way. The row
 // arithmetic is q8_dot (moe_device.h), as in the staged and batched paths.
 constexpr int kQ8GuWaves = 6, kQ8DnWaves = 4, kQ8DnPerWave = 4;
 template <int HID, int INTER>
-__device__ __forceinline__ void q8_shared(const MoeArgs &a, uint64_t *part_q8, uint32_t tag, float *hq, uint32_t *s_q8) {
-  constexpr int NQG = (HID + 1023) / 1024, NQD = (INTER + 1023) / 1024, NI = INTER / 64;
+__device__ __forceinline__ void q8_gu(const MoeArgs &a, uint64_t *part_q8, uint32_t tag) {
+  constexpr int NQG = (HID + 1023) / 1024;
   const int lane = threadIdx.x & 63, qi = (int)rfl(threadIdx.x >> 6) - kSpw, G = (int)gridDim.x, b = (int)blockIdx.x;
   if (qi < 0 || qi >= kQ8GuWaves) return;
   const Q8Off o = q8_offsets(HID, INTER);
@@ -376,15 +379,33 @@ __device__ __forceinline__ void q8_shared(const MoeArgs &a, uint64_t *part_q8, u
     const float v = q8_dot<NQG>(w, a.x, HID);
     if (lane == 0) st_tag(part_q8 + grow, moe_rr(v, a.refr), tag);
   }
-  if (qi >= kQ8DnWaves) return;
-  Q8Row<NQD> dw[kQ8DnPerWave];  // this wave's down rows, requested before the wait for h
+}
+// the down rows of wave kSpw + qi (qi < kQ8DnWaves) into st: row j's 16-byte chunk in st[j], the group words in st[4]
+template <int HID, int INTER>
+__device__ __forceinline__ void q8_dn_load(const MoeArgs &a, int qi, f16x8 (&st)[kDnKt]) {
+  static_assert(INTER <= 1024 && kQ8DnPerWave <= 4 && kQ8DnPerWave + 1 <= kDnKt, "one chunk per row, in st");
+  const int G = (int)gridDim.x, b = (int)blockIdx.x;
+  const Q8Off o = q8_offsets(HID, INTER);
+  uint32_t sbw[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
   for (int j = 0; j < kQ8DnPerWave; j++) {
     const int row = b + G * (qi + kQ8DnWaves * j);
+    Q8Row<1> r;
+    r.w[0] = make_uint4(0, 0, 0, 0);
+    r.sb[0] = 0u;
     if (row < HID)
-      q8_load<NQD>(a.q8 + o.w[2] + (uint64_t)row * INTER,
-                   (const uint32_t *)(a.q8 + o.sb[2]) + (uint64_t)row * (INTER / kQ8Group), INTER, dw[j]);
+      q8_load<1>(a.q8 + o.w[2] + (uint64_t)row * INTER, (const uint32_t *)(a.q8 + o.sb[2]) + (uint64_t)row * (INTER / kQ8Group),
+                 INTER, r);
+    st[j] = __builtin_bit_cast(f16x8, r.w[0]);
+    sbw[j] = r.sb[0];
   }
+  st[kQ8DnPerWave] = __builtin_bit_cast(f16x8, make_uint4(sbw[0], sbw[1], sbw[2], sbw[3]));
+}
+template <int HID, int INTER>
+__device__ __forceinline__ void q8_dn_finish(const MoeArgs &a, int qi, uint64_t *part_q8, uint32_t tag, float *hq,
+                                             uint32_t *s_q8, const f16x8 (&st)[kDnKt]) {
+  constexpr int NI = INTER / 64;
+  const int lane = threadIdx.x & 63, G = (int)gridDim.x, b = (int)blockIdx.x;
   if (qi == 0) {  // every gate / up row of the grid, then h into LDS
     float gv[NI], uv[NI];
     bool got = false;
@@ -420,11 +441,16 @@ __device__ __forceinline__ void q8_shared(const MoeArgs &a, uint64_t *part_q8, u
   }
   if (!got && lane == 0) atomicOr(a.sync + kWordErr, 1u);
   asm volatile("" ::: "memory");
+  const uint4 sbw = __builtin_bit_cast(uint4, st[kQ8DnPerWave]);
+  const uint32_t sbs[4] = {sbw.x, sbw.y, sbw.z, sbw.w};
 #pragma unroll
   for (int j = 0; j < kQ8DnPerWave; j++) {
     const int row = b + G * (qi + kQ8DnWaves * j);
     if (row < HID) {
-      const float v = q8_dot<NQD>(dw[j], hq, INTER);
+      Q8Row<1> r;
+      r.w[0] = __builtin_bit_cast(uint4, st[j]);
+      r.sb[0] = sbs[j];
+      const float v = q8_dot<1>(r, hq, INTER);
       if (lane == 0) st_tag(part_q8 + 2 * INTER + row, moe_rr(v, a.refr), tag);
     }
   }
@@ -538,7 +564,12 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
   };
   if (rrow) router_finish<HID>(a, rr, tag16);
   lds_barrier();  // this workgroup's logits are out: the router rows had HBM to themselves
-  if (a.q8) q8_shared<HID, INTER>(a, part_dn + (size_t)a.nslot * NBI * HID, tag, hq, &s_q8);
+  uint64_t *const part_q8 = part_dn + (size_t)a.nslot * NBI * HID;
+  const int q8w = wave - kSpw;  // the 8-bit shared expert's down waves: 0 .. kQ8DnWaves - 1
+  const bool q8dn = a.q8 && q8w >= 0 && q8w < kQ8DnWaves;
+  f16x8 dw[kDnKt];  // the shared EXL3 down unit's B operands, or (8-bit shared expert) this wave's down rows
+  if (a.q8) q8_gu<HID, INTER>(a, part_q8, tag);
+  if (q8dn) q8_dn_load<HID, INTER>(a, q8w, dw);
   const bool sprep_w = spk != kNone && wave >= kSpw && wave < kSpw + kGrp;
   if (sprep_w && lane < 16) {  // chunk c of the shared prep group's suh
     const int proj = (int)(spk / NKG), kc = (int)(spk % NKG) * kGrp + (wave - kSpw);
@@ -561,7 +592,6 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
       stream_tiles(a.shared + a.slay.tr[2], ITd, c * 4 + p, cb * kDnKt, kDnKt, 32u * KS, tiles + slot * SLOT);
     }
   }
-  f16x8 dw[kDnKt];
 
   // ---- 1. route (control wave), shared to every wave through LDS
   uint32_t rkey = 0u;  // the control wave: its lane's route key and the shared gate's logit, for route_weights
@@ -759,6 +789,10 @@ __global__ __launch_bounds__(1024, 1) void moe_step(MoeArgs a) {
       }
     }
   }
+
+  // the 8-bit shared expert's down rows (their loads went out before the route), before dw takes this wave's first
+  // routed down unit
+  if (ok && q8dn) q8_dn_finish<HID, INTER>(a, q8w, part_q8, tag, hq, &s_q8, dw);
 
   // ---- 4. the first routed down unit's tiles into B operands; the h blocks from the gate/up partials (the NKG k
   // group sums of each column folded left in k order)
